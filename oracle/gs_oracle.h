@@ -1,0 +1,113 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- the CPU oracle (checker) for the HIP rasterizer.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it; the product library never does.
+ *
+ * A plain-C fp32 restatement of the reference's differentiable Gaussian
+ * rasterizer hot path (BlitzGS diff-gaussian-rasterization_f preprocess +
+ * diff-gaussian-rasterization_r binning/render), simple-knn's distCUDA2 and
+ * fused-ssim.  Each function cites the reference file:line it follows.
+ * All arrays are host memory, row-major, fp32 unless stated.
+ */
+#ifndef GS_ORACLE_H
+#define GS_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int W, H;              /* image width / height                          */
+    float tanfovx, tanfovy;
+    float scale_modifier;
+    int sh_degree;         /* D                                              */
+    float view[16];        /* viewmatrix, flat, as the reference tensors     */
+    float proj[16];        /* full projection matrix, flat                   */
+    float campos[3];
+} o_camera;
+
+/* Per-Gaussian preprocess forward (reference _f/cuda_rasterizer/forward.cu:164-284).
+ * sh is (P, K, 3), K >= (D+1)^2.  All outputs are fully written (zeros for
+ * culled Gaussians, except cov3D which is written once the near cull passes). */
+void o_preprocess_fwd(int P, int K, const o_camera* cam,
+                      const float* means3D, const float* scales, const float* rotations,
+                      const float* sh, const float* opacities,
+                      float* means2D, float* depths, int* radii, float* cov3D,
+                      float* conic_opacity, float* rgb, uint8_t* clamped);
+
+/* Per-Gaussian preprocess backward: computeCov2DCUDA + preprocessCUDA
+ * (reference _f/cuda_rasterizer/backward.cu:146-400).  dL_dmeans2D has row
+ * stride m2d_stride floats (2 or 3).  Outputs fully written. */
+void o_preprocess_bwd(int P, int K, const o_camera* cam,
+                      const float* means3D, const float* scales, const float* rotations,
+                      const float* sh, const int* radii, const float* cov3D,
+                      const uint8_t* clamped,
+                      const float* dL_dmeans2D, int m2d_stride,
+                      const float* dL_dconic_opacity, const float* dL_drgb,
+                      float* dL_dmeans3D, float* dL_dscales, float* dL_drotations,
+                      float* dL_dsh, float* dL_dopacity);
+
+/* Reference tile-count rule (_r rasterizer_impl.cu:258-282): returns R. */
+int64_t o_binning_count(int P, int W, int H, const float* means2D, const int* radii,
+                        const uint8_t* compute_locally, uint32_t* tiles_touched);
+
+/* Reference binning: inclusive scan, duplicateWithKeys, stable sort of the
+ * 64-bit keys, identifyTileRanges (_r rasterizer_impl.cu:74-138,556-660).
+ * keys/values: R entries; ranges: 2*T uint32 (start,end). */
+void o_binning(int P, int W, int H, const float* means2D, const float* depths,
+               const int* radii, const uint8_t* compute_locally,
+               const uint32_t* tiles_touched, int64_t R,
+               uint64_t* keys, uint32_t* values, uint32_t* ranges);
+
+/* getHigherMsb (_r rasterizer_impl.cu:39-54). */
+uint32_t o_higher_msb(uint32_t n);
+
+/* Render forward (_r/cuda_rasterizer/forward.cu:263-413) plus the per-tile
+ * statistics (_r rasterizer_impl.cu:213-256).  out_color (3,H,W) and the
+ * per-pixel state are written for local tiles; non-local tiles get zeros. */
+void o_render_fwd(int P, int W, int H, const float* bg,
+                  const float* means2D, const float* conic_opacity, const float* rgb,
+                  const uint8_t* compute_locally,
+                  const uint32_t* ranges, const uint32_t* point_list,
+                  float* out_color, float* final_T, uint32_t* n_contrib,
+                  uint32_t* n_contrib2loss, int32_t* out_observe,
+                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile);
+
+/* Render backward (_r/cuda_rasterizer/backward.cu:324-530).  dL_dmean2D and
+ * dL_dmean2D_abs are (P,3); dL_dconic is (P,4) in the reference's float4
+ * slot layout (.x=c00, .y=c01, .w=c11); dL_dopacity (P); dL_dcolors (P,3).
+ * Outputs are accumulated (caller zeroes them). */
+void o_render_bwd(int P, int W, int H, const float* bg,
+                  const float* means2D, const float* conic_opacity, const float* rgb,
+                  const uint8_t* compute_locally,
+                  const uint32_t* ranges, const uint32_t* point_list,
+                  const float* final_T, const uint32_t* n_contrib,
+                  const float* dL_dpixels,
+                  float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                  float* dL_dopacity, float* dL_dcolors);
+
+/* distCUDA2 (simple-knn simple_knn.cu:148-221): mean of the three smallest
+ * squared distances to other points.  Exact; O(P log P) grid search. */
+void o_knn_meandist3(int P, const float* points, float* out);
+
+/* fused-ssim forward / backward (fused-ssim ssim.cu:186-365).  img (B,C,H,W). */
+void o_ssim_fwd(int B, int C, int H, int W, float C1, float C2,
+                const float* img1, const float* img2, float* ssim_map,
+                float* dm_dmu1, float* dm_dsigma1_sq, float* dm_dsigma12);
+void o_ssim_bwd(int B, int C, int H, int W, float C1, float C2,
+                const float* img1, const float* img2, const float* dL_dmap,
+                const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
+                float* dL_dimg1);
+
+/* Scalar math used by the oracle, exported so tests can pin it. */
+void o_vec_expf(int n, const float* x, float* y);
+void o_vec_logf(int n, const float* x, float* y);
+
+int o_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,239 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- CPU oracle, never linked into the product.
+ *
+ * distCUDA2 (/root/reference/submodule/simple-knn/simple_knn.cu:120-221,
+ * spatial.cu:15-26): for every point, the mean of the squared distances to
+ * its three nearest other points (self excluded by index, duplicates count
+ * as distance 0).  The reference's Morton-box search is exact (both of its
+ * prunings are conservative), so its result is the exact 3-NN; this oracle
+ * computes the same exact 3-NN with a uniform grid and a conservative ring
+ * bound.  Distances use d = (dx*dx + dy*dy) + dz*dz with dx = other - self,
+ * no FMA, and the output is ((b0 + b1) + b2) / 3 with b0 <= b1 <= b2 -- the
+ * updateKBest / boxMeanDist order (simple_knn.cu:132-146,183).  For P < 4
+ * the missing neighbours stay FLT_MAX, as in the reference.
+ *
+ * fused-ssim (/root/reference/submodule/fused-ssim/ssim.cu:8-365): 11x11
+ * separable Gaussian window (sigma 1.5), zero padding, horizontal pass over
+ * the padded rows then vertical pass, taps accumulated from -5 to +5; SSIM
+ * map and the three partial derivatives (forward), and the three
+ * convolutions of the backward.
+ */
+#include "gs_oracle.h"
+#include "o_math.h"
+#include <stdlib.h>
+#include <float.h>
+
+/* ------------------------------------------------------------------ KNN */
+
+static inline float o_d2(const float* a, const float* b)
+{
+    const float dx = b[0] - a[0], dy = b[1] - a[1], dz = b[2] - a[2];
+    return (dx * dx + dy * dy) + dz * dz;
+}
+
+static inline void upd3(float* best, float d)
+{
+    for (int j = 0; j < 3; j++)
+        if (best[j] > d) { float t = best[j]; best[j] = d; d = t; }
+}
+
+void o_knn_meandist3(int P, const float* pts, float* out)
+{
+    if (P <= 0) return;
+    double mn[3] = { pts[0], pts[1], pts[2] }, mx[3] = { pts[0], pts[1], pts[2] };
+    for (int i = 1; i < P; i++)
+        for (int k = 0; k < 3; k++) {
+            const double v = pts[3 * i + k];
+            if (v < mn[k]) mn[k] = v;
+            if (v > mx[k]) mx[k] = v;
+        }
+    double ext[3], vol = 1.0;
+    for (int k = 0; k < 3; k++) { ext[k] = mx[k] - mn[k]; if (ext[k] < 1e-12) ext[k] = 1e-12; vol *= ext[k]; }
+    /* about two points per cell */
+    double h = cbrt(vol / ((double)P / 2.0 + 1.0));
+    int n[3];
+    for (int k = 0; k < 3; k++) {
+        double c = ceil(ext[k] / h);
+        if (c < 1) c = 1;
+        if (c > 1024) c = 1024;
+        n[k] = (int)c;
+    }
+    const size_t NC = (size_t)n[0] * n[1] * n[2];
+    double hk[3];
+    for (int k = 0; k < 3; k++) hk[k] = ext[k] / n[k];
+    int* cell = (int*)malloc(sizeof(int) * (size_t)P);
+    int* start = (int*)calloc(NC + 1, sizeof(int));
+    int* order = (int*)malloc(sizeof(int) * (size_t)P);
+    for (int i = 0; i < P; i++) {
+        int c[3];
+        for (int k = 0; k < 3; k++) {
+            int v = (int)floor(((double)pts[3 * i + k] - mn[k]) / hk[k]);
+            c[k] = v < 0 ? 0 : (v >= n[k] ? n[k] - 1 : v);
+        }
+        cell[i] = (c[2] * n[1] + c[1]) * n[0] + c[0];
+        start[cell[i] + 1]++;
+    }
+    for (size_t c = 0; c < NC; c++) start[c + 1] += start[c];
+    {
+        int* fill = (int*)malloc(sizeof(int) * NC);
+        memcpy(fill, start, sizeof(int) * NC);
+        for (int i = 0; i < P; i++) order[fill[cell[i]]++] = i;
+        free(fill);
+    }
+
+#pragma omp parallel for schedule(dynamic, 256)
+    for (int i = 0; i < P; i++) {
+        const float* q = pts + 3 * i;
+        int c[3];
+        const int cid = cell[i];
+        c[0] = cid % n[0]; c[1] = (cid / n[0]) % n[1]; c[2] = cid / (n[0] * n[1]);
+        float best[3] = { FLT_MAX, FLT_MAX, FLT_MAX };
+        const int rmax = n[0] > n[1] ? (n[0] > n[2] ? n[0] : n[2]) : (n[1] > n[2] ? n[1] : n[2]);
+        for (int r = 0; r <= rmax; r++) {
+            for (int z = c[2] - r; z <= c[2] + r; z++) {
+                if (z < 0 || z >= n[2]) continue;
+                for (int y = c[1] - r; y <= c[1] + r; y++) {
+                    if (y < 0 || y >= n[1]) continue;
+                    const int onshell_zy = (z == c[2] - r || z == c[2] + r || y == c[1] - r || y == c[1] + r);
+                    for (int x = c[0] - r; x <= c[0] + r; x++) {
+                        if (x < 0 || x >= n[0]) continue;
+                        if (!onshell_zy && x != c[0] - r && x != c[0] + r) continue;
+                        const size_t cc = ((size_t)z * n[1] + y) * n[0] + x;
+                        for (int k = start[cc]; k < start[cc + 1]; k++) {
+                            const int j = order[k];
+                            if (j == i) continue;
+                            upd3(best, o_d2(q, pts + 3 * j));
+                        }
+                    }
+                }
+            }
+            /* distance from q to the outside of the (2r+1)^3 block of cells */
+            double bound = DBL_MAX;
+            for (int k = 0; k < 3; k++) {
+                const double lo = mn[k] + (double)(c[k] - r) * hk[k];
+                const double hi = mn[k] + (double)(c[k] + r + 1) * hk[k];
+                if (c[k] - r > 0) { double d = (double)q[k] - lo; if (d < bound) bound = d; }
+                if (c[k] + r + 1 < n[k]) { double d = hi - (double)q[k]; if (d < bound) bound = d; }
+            }
+            if (bound == DBL_MAX) break;          /* whole grid covered */
+            if (bound < 0) bound = 0;
+            if ((double)best[2] < bound * bound * (1.0 - 1e-6)) break;
+        }
+        out[i] = ((best[0] + best[1]) + best[2]) / 3.0f;
+    }
+    free(cell); free(start); free(order);
+}
+
+/* ----------------------------------------------------------------- SSIM */
+
+static float g_win[11];
+static int g_win_init = 0;
+
+/* normalised 11-tap Gaussian, sigma 1.5, computed in double then rounded */
+static void ssim_window(void)
+{
+    if (g_win_init) return;
+    double w[11], s = 0;
+    for (int i = 0; i < 11; i++) { const double x = i - 5; w[i] = exp(-(x * x) / (2.0 * 1.5 * 1.5)); s += w[i]; }
+    for (int i = 0; i < 11; i++) g_win[i] = (float)(w[i] / s);
+    g_win_init = 1;
+}
+
+/* same-size zero-padded separable blur of one plane: horizontal pass on the
+ * padded rows, then vertical pass */
+static void blur_plane(int H, int W, const float* in, float* out, float* tmp /* (H+10)*W */)
+{
+    for (int yy = 0; yy < H + 10; yy++) {
+        const int y = yy - 5;
+        for (int x = 0; x < W; x++) {
+            float v = 0.0f;
+            if (y >= 0 && y < H)
+                for (int t = 0; t < 11; t++) {
+                    const int xs = x + t - 5;
+                    const float p = (xs >= 0 && xs < W) ? in[(size_t)y * W + xs] : 0.0f;
+                    v += g_win[t] * p;
+                }
+            else
+                for (int t = 0; t < 11; t++) v += g_win[t] * 0.0f;
+            tmp[(size_t)yy * W + x] = v;
+        }
+    }
+    for (int y = 0; y < H; y++)
+        for (int x = 0; x < W; x++) {
+            float v = 0.0f;
+            for (int t = 0; t < 11; t++) v += g_win[t] * tmp[(size_t)(y + t) * W + x];
+            out[(size_t)y * W + x] = v;
+        }
+}
+
+void o_ssim_fwd(int B, int C, int H, int W, float C1, float C2,
+                const float* img1, const float* img2, float* ssim_map,
+                float* dm_dmu1, float* dm_dsigma1_sq, float* dm_dsigma12)
+{
+    ssim_window();
+    const size_t N = (size_t)H * W;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int bc = 0; bc < B * C; bc++) {
+        const float* x = img1 + (size_t)bc * N;
+        const float* y = img2 + (size_t)bc * N;
+        float* buf = (float*)malloc(sizeof(float) * N * 9 + sizeof(float) * (size_t)(H + 10) * W);
+        float *xx = buf, *yy = buf + N, *xy = buf + 2 * N, *mu1 = buf + 3 * N, *mu2 = buf + 4 * N;
+        float *s11 = buf + 5 * N, *s22 = buf + 6 * N, *s12 = buf + 7 * N, *tmp = buf + 9 * N;
+        for (size_t i = 0; i < N; i++) { xx[i] = x[i] * x[i]; yy[i] = y[i] * y[i]; xy[i] = x[i] * y[i]; }
+        blur_plane(H, W, x, mu1, tmp);
+        blur_plane(H, W, y, mu2, tmp);
+        blur_plane(H, W, xx, s11, tmp);
+        blur_plane(H, W, yy, s22, tmp);
+        blur_plane(H, W, xy, s12, tmp);
+        for (size_t i = 0; i < N; i++) {
+            const float m1 = mu1[i], m2 = mu2[i];
+            const float sigma1_sq = s11[i] - m1 * m1;
+            const float sigma2_sq = s22[i] - m2 * m2;
+            const float sigma12 = s12[i] - m1 * m2;
+            const float mu1_sq = m1 * m1, mu2_sq = m2 * m2, mu1_mu2 = m1 * m2;
+            const float Cn = (2.0f * mu1_mu2 + C1);
+            const float Dn = (2.0f * sigma12 + C2);
+            const float A = (mu1_sq + mu2_sq + C1);
+            const float Bd = (sigma1_sq + sigma2_sq + C2);
+            const size_t o = (size_t)bc * N + i;
+            ssim_map[o] = (Cn * Dn) / (A * Bd);
+            if (dm_dmu1) {
+                dm_dmu1[o] = ((m2 * 2.0f * Dn) / (A * Bd) - (m2 * 2.0f * Cn) / (A * Bd) -
+                              (m1 * 2.0f * Cn * Dn) / (A * A * Bd) + (m1 * 2.0f * Cn * Dn) / (A * Bd * Bd));
+                dm_dsigma1_sq[o] = ((-Cn * Dn) / (A * Bd * Bd));
+                dm_dsigma12[o] = ((2 * Cn) / (A * Bd));
+            }
+        }
+        free(buf);
+    }
+}
+
+void o_ssim_bwd(int B, int C, int H, int W, float C1, float C2,
+                const float* img1, const float* img2, const float* dL_dmap,
+                const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
+                float* dL_dimg1)
+{
+    (void)C1; (void)C2;
+    ssim_window();
+    const size_t N = (size_t)H * W;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int bc = 0; bc < B * C; bc++) {
+        const size_t base = (size_t)bc * N;
+        float* buf = (float*)malloc(sizeof(float) * N * 4 + sizeof(float) * (size_t)(H + 10) * W);
+        float *p = buf, *q1 = buf + N, *q2 = buf + 2 * N, *q3 = buf + 3 * N, *tmp = buf + 4 * N;
+        for (size_t i = 0; i < N; i++) p[i] = dm_dmu1[base + i] * dL_dmap[base + i];
+        blur_plane(H, W, p, q1, tmp);
+        for (size_t i = 0; i < N; i++) p[i] = dm_dsigma1_sq[base + i] * dL_dmap[base + i];
+        blur_plane(H, W, p, q2, tmp);
+        for (size_t i = 0; i < N; i++) p[i] = dm_dsigma12[base + i] * dL_dmap[base + i];
+        blur_plane(H, W, p, q3, tmp);
+        for (size_t i = 0; i < N; i++) {
+            float d = 0.0f;
+            d += q1[i];
+            d += img1[base + i] * 2.0f * q2[i];
+            d += img2[base + i] * q3[i];
+            dL_dimg1[base + i] = d;
+        }
+        free(buf);
+    }
+}

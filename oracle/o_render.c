@@ -1,0 +1,323 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- CPU oracle, never linked into the product.
+ *
+ * fp32 restatement of the reference's binning and tile rendering
+ * (/root/reference/submodule/diff-gaussian-rasterization_r):
+ *   getHigherMsb              cuda_rasterizer/rasterizer_impl.cu:39-54
+ *   duplicateWithKeys         cuda_rasterizer/rasterizer_impl.cu:74-111
+ *   identifyTileRanges        cuda_rasterizer/rasterizer_impl.cu:116-138
+ *   get_n_render / reduce_data_per_block  rasterizer_impl.cu:213-256
+ *   updateTileTouched         cuda_rasterizer/rasterizer_impl.cu:258-282
+ *   renderForward sequence    cuda_rasterizer/rasterizer_impl.cu:556-723
+ *   getRect(float2,int)       cuda_rasterizer/auxiliary.h:66-76
+ *   renderCUDA (forward)      cuda_rasterizer/forward.cu:263-413
+ *   renderCUDA (backward)     cuda_rasterizer/backward.cu:324-530
+ * The reference sorts with a stable LSD radix sort on bits [0, 32+msb); here a
+ * stable merge sort on the full 64-bit key gives the same order (tile ids are
+ * below 2^msb, checked in the tests, and depth bits are the low word).
+ *
+ * Per-pixel arithmetic is written in the fixed order the device code uses:
+ *   d = mean - pixel;  power = fma(-0.5a*dx, dx, fma(-0.5c*dy, dy, (-b*dx)*dy))
+ *   G = o_expf(power); alpha = min(0.99, o*G);  C = fma(rgb, alpha*T, C)
+ * which is the reference's expression with its products grouped for FMA.
+ */
+#include "gs_oracle.h"
+#include "o_math.h"
+#include <stdlib.h>
+
+#define OT 16  /* BLOCK_X = BLOCK_Y = 16 (config.h) */
+
+uint32_t o_higher_msb(uint32_t n)
+{
+    uint32_t msb = sizeof(n) * 4;
+    uint32_t step = msb;
+    while (step > 1) {
+        step /= 2;
+        if (n >> msb) msb += step;
+        else msb -= step;
+    }
+    if (n >> msb) msb++;
+    return msb;
+}
+
+/* getRect with an integer radius: float arithmetic left to right, (int)
+ * truncation toward zero, clamped to [0, grid]. */
+static inline void rect_int(const float* p, int r, unsigned gx, unsigned gy,
+                            unsigned* x0, unsigned* y0, unsigned* x1, unsigned* y1)
+{
+    const float rf = (float)r;
+    int v;
+    v = o_f2i_sat((p[0] - rf) / 16.0f); v = v < 0 ? 0 : v; *x0 = (unsigned)v > gx ? gx : (unsigned)v;
+    v = o_f2i_sat((p[1] - rf) / 16.0f); v = v < 0 ? 0 : v; *y0 = (unsigned)v > gy ? gy : (unsigned)v;
+    v = o_f2i_sat(((p[0] + rf) + 16.0f - 1.0f) / 16.0f); v = v < 0 ? 0 : v; *x1 = (unsigned)v > gx ? gx : (unsigned)v;
+    v = o_f2i_sat(((p[1] + rf) + 16.0f - 1.0f) / 16.0f); v = v < 0 ? 0 : v; *y1 = (unsigned)v > gy ? gy : (unsigned)v;
+}
+
+int64_t o_binning_count(int P, int W, int H, const float* means2D, const int* radii,
+                        const uint8_t* compute_locally, uint32_t* tiles_touched)
+{
+    const unsigned gx = (unsigned)((W + OT - 1) / OT), gy = (unsigned)((H + OT - 1) / OT);
+    int64_t total = 0;
+#pragma omp parallel for schedule(static) reduction(+ : total)
+    for (int i = 0; i < P; i++) {
+        uint32_t cnt = 0;
+        if (radii[i] > 0) {
+            unsigned x0, y0, x1, y1;
+            rect_int(means2D + 2 * i, radii[i], gx, gy, &x0, &y0, &x1, &y1);
+            for (unsigned y = y0; y < y1; y++)
+                for (unsigned x = x0; x < x1; x++)
+                    if (compute_locally[y * gx + x]) cnt++;
+        }
+        tiles_touched[i] = cnt;
+        total += cnt;
+    }
+    return total;
+}
+
+void o_binning(int P, int W, int H, const float* means2D, const float* depths,
+               const int* radii, const uint8_t* compute_locally,
+               const uint32_t* tiles_touched, int64_t R,
+               uint64_t* keys, uint32_t* values, uint32_t* ranges)
+{
+    const unsigned gx = (unsigned)((W + OT - 1) / OT), gy = (unsigned)((H + OT - 1) / OT);
+    const unsigned T = gx * gy;
+    int64_t* off = (int64_t*)malloc(sizeof(int64_t) * (size_t)(P > 0 ? P : 1));
+    int64_t acc = 0;
+    for (int i = 0; i < P; i++) { off[i] = acc; acc += tiles_touched[i]; }
+
+    /* duplicateWithKeys: Gaussian order, then rows, then columns */
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < P; i++) {
+        if (!(radii[i] > 0)) continue;
+        int64_t o = off[i];
+        unsigned x0, y0, x1, y1;
+        rect_int(means2D + 2 * i, radii[i], gx, gy, &x0, &y0, &x1, &y1);
+        const uint32_t dbits = o_f2u(depths[i]);
+        for (unsigned y = y0; y < y1; y++)
+            for (unsigned x = x0; x < x1; x++)
+                if (compute_locally[y * gx + x]) {
+                    keys[o] = ((uint64_t)(y * gx + x) << 32) | dbits;
+                    values[o] = (uint32_t)i;
+                    o++;
+                }
+    }
+    free(off);
+
+    /* stable sort by key */
+    if (R > 1) {
+        uint64_t* tk = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)R);
+        uint32_t* tv = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)R);
+        uint64_t* a = keys; uint32_t* av = values;
+        uint64_t* b = tk; uint32_t* bv = tv;
+        for (int64_t width = 1; width < R; width *= 2) {
+#pragma omp parallel for schedule(dynamic, 1)
+            for (int64_t lo = 0; lo < R; lo += 2 * width) {
+                int64_t mid = lo + width < R ? lo + width : R;
+                int64_t hi = lo + 2 * width < R ? lo + 2 * width : R;
+                int64_t i = lo, j = mid, o = lo;
+                while (i < mid && j < hi) {
+                    if (a[j] < a[i]) { b[o] = a[j]; bv[o] = av[j]; j++; }
+                    else { b[o] = a[i]; bv[o] = av[i]; i++; }
+                    o++;
+                }
+                while (i < mid) { b[o] = a[i]; bv[o] = av[i]; i++; o++; }
+                while (j < hi) { b[o] = a[j]; bv[o] = av[j]; j++; o++; }
+            }
+            uint64_t* s = a; a = b; b = s;
+            uint32_t* sv = av; av = bv; bv = sv;
+        }
+        if (a != keys) {
+            memcpy(keys, a, sizeof(uint64_t) * (size_t)R);
+            memcpy(values, av, sizeof(uint32_t) * (size_t)R);
+        }
+        free(tk); free(tv);
+    }
+
+    /* identifyTileRanges (after the memset of rasterizer_impl.cu:655) */
+    memset(ranges, 0, sizeof(uint32_t) * 2 * (size_t)T);
+    for (int64_t idx = 0; idx < R; idx++) {
+        const uint32_t cur = (uint32_t)(keys[idx] >> 32);
+        if (idx == 0) ranges[2 * cur] = 0;
+        else {
+            const uint32_t prev = (uint32_t)(keys[idx - 1] >> 32);
+            if (cur != prev) { ranges[2 * prev + 1] = (uint32_t)idx; ranges[2 * cur] = (uint32_t)idx; }
+        }
+        if (idx == R - 1) ranges[2 * cur + 1] = (uint32_t)R;
+    }
+}
+
+/* the per-(pixel, Gaussian) Gaussian falloff exponent, in the device order */
+static inline float o_power(const float* xy, const float* co, float px, float py)
+{
+    const float dx = xy[0] - px, dy = xy[1] - py;
+    const float ha = -0.5f * co[0], hc = -0.5f * co[2], nb = -co[1];
+    return fmaf(ha * dx, dx, fmaf(hc * dy, dy, (nb * dx) * dy));
+}
+
+void o_render_fwd(int P, int W, int H, const float* bg,
+                  const float* means2D, const float* conic_opacity, const float* rgb,
+                  const uint8_t* compute_locally,
+                  const uint32_t* ranges, const uint32_t* point_list,
+                  float* out_color, float* final_T, uint32_t* n_contrib,
+                  uint32_t* n_contrib2loss, int32_t* out_observe,
+                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile)
+{
+    (void)P;
+    const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const int T = gx * gy;
+    const float alpha_min = 1.0f / 255.0f;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int t = 0; t < T; t++) {
+        const int tx = t % gx, ty = t / gx;
+        n_render[t] = (int32_t)(ranges[2 * t + 1] - ranges[2 * t]);
+        n_consider[t] = 0; n_contrib_tile[t] = 0;
+        const int x0 = tx * OT, y0 = ty * OT;
+        const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
+        if (!compute_locally[t]) {
+            for (int y = y0; y < y1; y++)
+                for (int x = x0; x < x1; x++) {
+                    const size_t pid = (size_t)y * W + x;
+                    for (int c = 0; c < 3; c++) out_color[(size_t)c * H * W + pid] = 0.f;
+                    final_T[pid] = 0.f; n_contrib[pid] = 0; n_contrib2loss[pid] = 0;
+                }
+            continue;
+        }
+        const uint32_t rs = ranges[2 * t], re = ranges[2 * t + 1];
+        int64_t s_consider = 0, s_contrib = 0;
+        for (int y = y0; y < y1; y++)
+            for (int x = x0; x < x1; x++) {
+                const float px = (float)x, py = (float)y;
+                float T_ = 1.0f, C[3] = { 0.f, 0.f, 0.f };
+                uint32_t contributor = 0, last = 0, n2l = 0;
+                for (uint32_t k = rs; k < re; k++) {
+                    contributor++;
+                    const uint32_t id = point_list[k];
+                    const float* co = conic_opacity + 4 * (size_t)id;
+                    const float power = o_power(means2D + 2 * (size_t)id, co, px, py);
+                    if (power > 0.0f) continue;
+                    const float alpha = o_fminf(0.99f, co[3] * o_expf(power));
+                    if (alpha < alpha_min) continue;
+                    const float test_T = T_ * (1.0f - alpha);
+                    if (test_T < 0.0001f) break;
+                    n2l++;
+                    const float wgt = alpha * T_;
+                    for (int c = 0; c < 3; c++) C[c] = fmaf(rgb[3 * (size_t)id + c], wgt, C[c]);
+                    if (T_ > 0.5f) {
+#pragma omp atomic
+                        out_observe[id]++;
+                    }
+                    T_ = test_T;
+                    last = contributor;
+                }
+                const size_t pid = (size_t)y * W + x;
+                final_T[pid] = T_;
+                n_contrib[pid] = last;
+                n_contrib2loss[pid] = n2l;
+                for (int c = 0; c < 3; c++) out_color[(size_t)c * H * W + pid] = fmaf(T_, bg[c], C[c]);
+                s_consider += last;
+                s_contrib += n2l;
+            }
+        n_consider[t] = (int32_t)s_consider;
+        n_contrib_tile[t] = (int32_t)s_contrib;
+    }
+}
+
+static inline void atomic_addf(float* p, float v)
+{
+#pragma omp atomic
+    *p += v;
+}
+
+void o_render_bwd(int P, int W, int H, const float* bg,
+                  const float* means2D, const float* conic_opacity, const float* rgb,
+                  const uint8_t* compute_locally,
+                  const uint32_t* ranges, const uint32_t* point_list,
+                  const float* final_T, const uint32_t* n_contrib,
+                  const float* dL_dpixels,
+                  float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                  float* dL_dopacity, float* dL_dcolors)
+{
+    (void)P;
+    const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const int T = gx * gy;
+    const float alpha_min = 1.0f / 255.0f;
+    const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int t = 0; t < T; t++) {
+        if (!compute_locally[t]) continue;
+        const int tx = t % gx, ty = t / gx;
+        const int x0 = tx * OT, y0 = ty * OT;
+        const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
+        const uint32_t rs = ranges[2 * t], re = ranges[2 * t + 1];
+        for (int y = y0; y < y1; y++)
+            for (int x = x0; x < x1; x++) {
+                const size_t pid = (size_t)y * W + x;
+                const float px = (float)x, py = (float)y;
+                const float T_final = final_T[pid];
+                float T_ = T_final;
+                const uint32_t last = n_contrib[pid];
+                float dpix[3], accum[3] = { 0, 0, 0 }, last_color[3] = { 0, 0, 0 };
+                for (int c = 0; c < 3; c++) dpix[c] = dL_dpixels[(size_t)c * H * W + pid];
+                float last_alpha = 0.f;
+                float bg_dot = 0.f;
+                for (int c = 0; c < 3; c++) bg_dot += bg[c] * dpix[c];
+                /* contributor index k-rs+1 runs from the back; skip >= last */
+                for (int64_t k = (int64_t)re - 1; k >= (int64_t)rs; k--) {
+                    const uint32_t contributor = (uint32_t)(k - rs);  /* after the decrement */
+                    if (contributor >= last) continue;
+                    const uint32_t id = point_list[k];
+                    const float* xy = means2D + 2 * (size_t)id;
+                    const float* co = conic_opacity + 4 * (size_t)id;
+                    const float dx = xy[0] - px, dy = xy[1] - py;
+                    const float power = o_power(xy, co, px, py);
+                    if (power > 0.0f) continue;
+                    const float G = o_expf(power);
+                    const float alpha = o_fminf(0.99f, co[3] * G);
+                    if (alpha < alpha_min) continue;
+                    T_ = T_ / (1.f - alpha);
+                    const float dchannel_dcolor = alpha * T_;
+                    float dL_dalpha = 0.0f;
+                    for (int c = 0; c < 3; c++) {
+                        const float col = rgb[3 * (size_t)id + c];
+                        accum[c] = last_alpha * last_color[c] + (1.f - last_alpha) * accum[c];
+                        last_color[c] = col;
+                        dL_dalpha += (col - accum[c]) * dpix[c];
+                        atomic_addf(&dL_dcolors[3 * (size_t)id + c], dchannel_dcolor * dpix[c]);
+                    }
+                    dL_dalpha *= T_;
+                    last_alpha = alpha;
+                    dL_dalpha += (-T_final / (1.f - alpha)) * bg_dot;
+                    const float dL_dG = co[3] * dL_dalpha;
+                    const float gdx = G * dx, gdy = G * dy;
+                    const float dG_ddelx = -gdx * co[0] - gdy * co[1];
+                    const float dG_ddely = -gdy * co[2] - gdx * co[1];
+                    const float gmx = dL_dG * dG_ddelx * ddelx_dx;
+                    const float gmy = dL_dG * dG_ddely * ddely_dy;
+                    atomic_addf(&dL_dmean2D[3 * (size_t)id + 0], gmx);
+                    atomic_addf(&dL_dmean2D[3 * (size_t)id + 1], gmy);
+                    atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 0], fabsf(gmx));
+                    atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 1], fabsf(gmy));
+                    atomic_addf(&dL_dconic[4 * (size_t)id + 0], -0.5f * gdx * dx * dL_dG);
+                    atomic_addf(&dL_dconic[4 * (size_t)id + 1], -0.5f * gdx * dy * dL_dG);
+                    atomic_addf(&dL_dconic[4 * (size_t)id + 3], -0.5f * gdy * dy * dL_dG);
+                    atomic_addf(&dL_dopacity[id], G * dL_dalpha);
+                }
+            }
+    }
+}
+
+void o_vec_expf(int n, const float* x, float* y)
+{
+    for (int i = 0; i < n; i++) y[i] = o_expf(x[i]);
+}
+void o_vec_logf(int n, const float* x, float* y)
+{
+    for (int i = 0; i < n; i++) y[i] = o_logf(x[i]);
+}
+
+#ifdef _OPENMP
+#include <omp.h>
+int o_num_threads(void) { return omp_get_max_threads(); }
+#else
+int o_num_threads(void) { return 1; }
+#endif

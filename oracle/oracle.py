@@ -1,0 +1,240 @@
+"""ctypes wrapper around the C oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker or the timed CPU baseline.  The product
+(blitzgs_amd) never imports it.
+
+All functions take and return numpy arrays (float32 / int32 / uint8 / ...).
+Camera dictionaries use the keys produced by blitzgs_amd.synth.make_camera:
+W, H, tanfovx, tanfovy, viewmatrix (4x4), projmatrix (4x4), campos (3),
+plus the preprocess settings scale_modifier and sh_degree.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import build as _build
+
+_lib = None
+
+
+class OCamera(C.Structure):
+    _fields_ = [("W", C.c_int), ("H", C.c_int), ("tanfovx", C.c_float), ("tanfovy", C.c_float),
+                ("scale_modifier", C.c_float), ("sh_degree", C.c_int),
+                ("view", C.c_float * 16), ("proj", C.c_float * 16), ("campos", C.c_float * 3)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = _build.build()
+        _lib = C.CDLL(path)
+        fp = C.c_void_p
+        _lib.o_binning_count.restype = C.c_int64
+        _lib.o_higher_msb.restype = C.c_uint32
+        _lib.o_higher_msb.argtypes = [C.c_uint32]
+        _lib.o_num_threads.restype = C.c_int
+        for name in ["o_preprocess_fwd", "o_preprocess_bwd", "o_binning", "o_render_fwd",
+                     "o_render_bwd", "o_knn_meandist3", "o_ssim_fwd", "o_ssim_bwd",
+                     "o_vec_expf", "o_vec_logf"]:
+            getattr(_lib, name).restype = None
+        del fp
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def camera_struct(cam, scale_modifier=1.0, sh_degree=3):
+    c = OCamera()
+    c.W = int(cam["W"])
+    c.H = int(cam["H"])
+    c.tanfovx = float(cam["tanfovx"])
+    c.tanfovy = float(cam["tanfovy"])
+    c.scale_modifier = float(scale_modifier)
+    c.sh_degree = int(sh_degree)
+    v = _f32(cam["viewmatrix"]).reshape(-1)
+    p = _f32(cam["projmatrix"]).reshape(-1)
+    cp = _f32(cam["campos"]).reshape(-1)
+    for i in range(16):
+        c.view[i] = float(v[i])
+        c.proj[i] = float(p[i])
+    for i in range(3):
+        c.campos[i] = float(cp[i])
+    return c
+
+
+def num_threads():
+    return lib().o_num_threads()
+
+
+def vec_expf(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().o_vec_expf(C.c_int(x.size), _p(x), _p(y))
+    return y
+
+
+def vec_logf(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().o_vec_logf(C.c_int(x.size), _p(x), _p(y))
+    return y
+
+
+def higher_msb(n):
+    return int(lib().o_higher_msb(C.c_uint32(n)))
+
+
+def preprocess_fwd(cam, means3D, scales, rotations, sh, opacities, scale_modifier=1.0, sh_degree=3):
+    means3D, scales, rotations, sh, opacities = map(_f32, (means3D, scales, rotations, sh, opacities))
+    P = means3D.shape[0]
+    K = sh.shape[1] if sh.ndim == 3 else 1
+    cs = camera_struct(cam, scale_modifier, sh_degree)
+    out = dict(
+        means2D=np.empty((P, 2), np.float32), depths=np.empty(P, np.float32),
+        radii=np.empty(P, np.int32), cov3D=np.empty((P, 6), np.float32),
+        conic_opacity=np.empty((P, 4), np.float32), rgb=np.empty((P, 3), np.float32),
+        clamped=np.empty((P, 3), np.uint8))
+    lib().o_preprocess_fwd(C.c_int(P), C.c_int(K), C.byref(cs), _p(means3D), _p(scales), _p(rotations),
+                           _p(sh), _p(opacities), _p(out["means2D"]), _p(out["depths"]), _p(out["radii"]),
+                           _p(out["cov3D"]), _p(out["conic_opacity"]), _p(out["rgb"]), _p(out["clamped"]))
+    return out
+
+
+def preprocess_bwd(cam, means3D, scales, rotations, sh, radii, cov3D, clamped,
+                   dL_dmeans2D, dL_dconic_opacity, dL_drgb, scale_modifier=1.0, sh_degree=3):
+    means3D, scales, rotations, sh, cov3D = map(_f32, (means3D, scales, rotations, sh, cov3D))
+    dL_dmeans2D, dL_dconic_opacity, dL_drgb = map(_f32, (dL_dmeans2D, dL_dconic_opacity, dL_drgb))
+    radii = np.ascontiguousarray(radii, dtype=np.int32)
+    clamped = np.ascontiguousarray(clamped, dtype=np.uint8)
+    P = means3D.shape[0]
+    K = sh.shape[1]
+    cs = camera_struct(cam, scale_modifier, sh_degree)
+    out = dict(dL_dmeans3D=np.empty((P, 3), np.float32), dL_dscales=np.empty((P, 3), np.float32),
+               dL_drotations=np.empty((P, 4), np.float32), dL_dsh=np.empty((P, K, 3), np.float32),
+               dL_dopacity=np.empty((P, 1), np.float32))
+    lib().o_preprocess_bwd(C.c_int(P), C.c_int(K), C.byref(cs), _p(means3D), _p(scales), _p(rotations),
+                           _p(sh), _p(radii), _p(cov3D), _p(clamped), _p(dL_dmeans2D),
+                           C.c_int(dL_dmeans2D.shape[1]), _p(dL_dconic_opacity), _p(dL_drgb),
+                           _p(out["dL_dmeans3D"]), _p(out["dL_dscales"]), _p(out["dL_drotations"]),
+                           _p(out["dL_dsh"]), _p(out["dL_dopacity"]))
+    return out
+
+
+def tile_grid(W, H):
+    return (W + 15) // 16, (H + 15) // 16
+
+
+def binning(W, H, means2D, depths, radii, compute_locally=None):
+    means2D, depths = _f32(means2D), _f32(depths)
+    radii = np.ascontiguousarray(radii, dtype=np.int32)
+    gx, gy = tile_grid(W, H)
+    if compute_locally is None:
+        compute_locally = np.ones(gx * gy, np.uint8)
+    cl = np.ascontiguousarray(compute_locally, dtype=np.uint8).reshape(-1)
+    P = means2D.shape[0]
+    tt = np.empty(P, np.uint32)
+    R = lib().o_binning_count(C.c_int(P), C.c_int(W), C.c_int(H), _p(means2D), _p(radii), _p(cl), _p(tt))
+    keys = np.empty(R, np.uint64)
+    vals = np.empty(R, np.uint32)
+    ranges = np.empty((gx * gy, 2), np.uint32)
+    lib().o_binning(C.c_int(P), C.c_int(W), C.c_int(H), _p(means2D), _p(depths), _p(radii), _p(cl),
+                    _p(tt), C.c_int64(R), _p(keys), _p(vals), _p(ranges))
+    return dict(R=int(R), tiles_touched=tt, keys=keys, point_list=vals, ranges=ranges)
+
+
+def render_fwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, compute_locally=None):
+    means2D, conic_opacity, rgb, bg = map(_f32, (means2D, conic_opacity, rgb, bg))
+    gx, gy = tile_grid(W, H)
+    if compute_locally is None:
+        compute_locally = np.ones(gx * gy, np.uint8)
+    cl = np.ascontiguousarray(compute_locally, dtype=np.uint8).reshape(-1)
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    P = means2D.shape[0]
+    T = gx * gy
+    out = dict(color=np.empty((3, H, W), np.float32), final_T=np.empty((H, W), np.float32),
+               n_contrib_px=np.empty((H, W), np.uint32), n_contrib2loss_px=np.empty((H, W), np.uint32),
+               out_observe=np.zeros(P, np.int32), n_render=np.empty(T, np.int32),
+               n_consider=np.empty(T, np.int32), n_contrib=np.empty(T, np.int32))
+    lib().o_render_fwd(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity), _p(rgb),
+                       _p(cl), _p(ranges), _p(point_list), _p(out["color"]), _p(out["final_T"]),
+                       _p(out["n_contrib_px"]), _p(out["n_contrib2loss_px"]), _p(out["out_observe"]),
+                       _p(out["n_render"]), _p(out["n_consider"]), _p(out["n_contrib"]))
+    return out
+
+
+def render_bwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, final_T, n_contrib_px,
+               dL_dpixels, compute_locally=None):
+    means2D, conic_opacity, rgb, bg, final_T, dL_dpixels = map(
+        _f32, (means2D, conic_opacity, rgb, bg, final_T, dL_dpixels))
+    gx, gy = tile_grid(W, H)
+    if compute_locally is None:
+        compute_locally = np.ones(gx * gy, np.uint8)
+    cl = np.ascontiguousarray(compute_locally, dtype=np.uint8).reshape(-1)
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    n_contrib_px = np.ascontiguousarray(n_contrib_px, dtype=np.uint32)
+    P = means2D.shape[0]
+    out = dict(dL_dmeans2D=np.zeros((P, 3), np.float32), dL_dmeans2D_abs=np.zeros((P, 3), np.float32),
+               dL_dconic=np.zeros((P, 4), np.float32), dL_dopacity=np.zeros(P, np.float32),
+               dL_dcolors=np.zeros((P, 3), np.float32))
+    lib().o_render_bwd(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity), _p(rgb),
+                       _p(cl), _p(ranges), _p(point_list), _p(final_T), _p(n_contrib_px), _p(dL_dpixels),
+                       _p(out["dL_dmeans2D"]), _p(out["dL_dmeans2D_abs"]), _p(out["dL_dconic"]),
+                       _p(out["dL_dopacity"]), _p(out["dL_dcolors"]))
+    dc = out["dL_dconic"]
+    # rasterize_points.cu:425-433: repack (P,2,2) slots into [c00, c01, c11, opacity]
+    out["dL_dconic_opacity"] = np.stack([dc[:, 0], dc[:, 1], dc[:, 3], out["dL_dopacity"]], axis=1)
+    return out
+
+
+def knn_meandist3(points):
+    points = _f32(points)
+    P = points.shape[0]
+    out = np.empty(P, np.float32)
+    lib().o_knn_meandist3(C.c_int(P), _p(points), _p(out))
+    return out
+
+
+def ssim_fwd(img1, img2, C1=0.01 ** 2, C2=0.03 ** 2, train=True):
+    img1, img2 = _f32(img1), _f32(img2)
+    B, Ch, H, W = img1.shape
+    m = np.empty_like(img1)
+    if train:
+        d1, d2, d3 = np.empty_like(img1), np.empty_like(img1), np.empty_like(img1)
+        lib().o_ssim_fwd(B, Ch, H, W, C.c_float(C1), C.c_float(C2), _p(img1), _p(img2), _p(m),
+                         _p(d1), _p(d2), _p(d3))
+        return m, d1, d2, d3
+    lib().o_ssim_fwd(B, Ch, H, W, C.c_float(C1), C.c_float(C2), _p(img1), _p(img2), _p(m),
+                     None, None, None)
+    return m, None, None, None
+
+
+def ssim_bwd(img1, img2, dL_dmap, d1, d2, d3, C1=0.01 ** 2, C2=0.03 ** 2):
+    img1, img2, dL_dmap, d1, d2, d3 = map(_f32, (img1, img2, dL_dmap, d1, d2, d3))
+    B, Ch, H, W = img1.shape
+    g = np.empty_like(img1)
+    lib().o_ssim_bwd(B, Ch, H, W, C.c_float(C1), C.c_float(C2), _p(img1), _p(img2), _p(dL_dmap),
+                     _p(d1), _p(d2), _p(d3), _p(g))
+    return g
+
+
+def full_forward(cam, scene, bg=None, compute_locally=None, scale_modifier=1.0, sh_degree=3):
+    """Preprocess + binning + render forward, the reference's training forward."""
+    pre = preprocess_fwd(cam, scene["means3D"], scene["scales"], scene["rotations"], scene["sh"],
+                         scene["opacities"], scale_modifier, sh_degree)
+    W, H = int(cam["W"]), int(cam["H"])
+    bn = binning(W, H, pre["means2D"], pre["depths"], pre["radii"], compute_locally)
+    if bg is None:
+        bg = np.zeros(3, np.float32)
+    rf = render_fwd(W, H, bg, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"],
+                    bn["point_list"], compute_locally)
+    return pre, bn, rf

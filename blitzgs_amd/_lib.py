@@ -1,0 +1,87 @@
+"""ctypes binding of libblitzgs_amd.so (the C ABI declared in include/blitzgs_amd.h).
+
+The library is built in-tree by blitzgs_amd.build (or __graft_entry__.build()).
+There is no fallback path: if the library or a HIP device is missing, every
+operator raises.
+"""
+import ctypes as C
+import os
+
+from . import build as _build
+
+_lib = None
+
+_c = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_i64 = C.c_int64
+_sz = C.c_size_t
+
+_SIGS = {
+    "gs_version": (_i, []),
+    "gs_last_error": (C.c_char_p, []),
+    "gs_preprocess_forward": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
+                                   _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_preprocess_backward": (_i, [_i, _i, _i, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
+                                    _c, _c, _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_geom_bytes": (_sz, [_i, _i, _i]),
+    "gs_render_binning_bytes": (_sz, [_i64]),
+    "gs_render_img_bytes": (_sz, [_i, _i]),
+    "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _c]),
+    "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
+                               _c, _c]),
+    "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
+    "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
+                                    C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
+    "gs_knn_workspace_bytes": (_sz, [_i]),
+    "gs_knn_meandist3": (_i, [_i, _c, _c, _c, _c]),
+    "gs_ssim_forward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_diag_math": (_i, [_i, _i, _c, _c, _c]),
+}
+
+
+def lib_path():
+    return _build.LIB
+
+
+def load():
+    """Load (once) and return the ctypes library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not os.path.exists(path):
+        raise RuntimeError(f"blitzgs_amd: {path} is not built; run blitzgs_amd.build.build() "
+                           "(or __graft_entry__.build()) first")
+    lib = C.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = load().gs_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return C.c_void_p(t.data_ptr())
+
+
+def stream_of(device=None):
+    import torch
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,46 @@
+// Host-side helpers for the C-ABI entry points: error reporting and launch
+// checks.  Every entry point returns 0 on success or a negative code, and
+// leaves a message for gs_last_error().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gs {
+void set_error(const char* fmt, ...);
+void clear_error();
+}  // namespace gs
+
+#define GS_OK 0
+#define GS_ERR_ARG -1
+#define GS_ERR_HIP -2
+#define GS_ERR_SIZE -3
+
+#define GS_HIP(expr)                                                                   \
+    do {                                                                               \
+        hipError_t gs_e_ = (expr);                                                     \
+        if (gs_e_ != hipSuccess) {                                                     \
+            gs::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(gs_e_),    \
+                          __FILE__, __LINE__);                                         \
+            return GS_ERR_HIP;                                                         \
+        }                                                                              \
+    } while (0)
+
+#define GS_LAUNCH_CHECK(name)                                                          \
+    do {                                                                               \
+        hipError_t gs_e_ = hipGetLastError();                                          \
+        if (gs_e_ != hipSuccess) {                                                     \
+            gs::set_error("launch of %s failed: %s", name, hipGetErrorString(gs_e_));  \
+            return GS_ERR_HIP;                                                         \
+        }                                                                              \
+    } while (0)
+
+#define GS_REQUIRE(cond, ...)                                                          \
+    do {                                                                               \
+        if (!(cond)) {                                                                 \
+            gs::set_error(__VA_ARGS__);                                                \
+            return GS_ERR_ARG;                                                         \
+        }                                                                              \
+    } while (0)
+
+static inline unsigned gs_div_up(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }

@@ -1,0 +1,609 @@
+// Per-Gaussian preprocess, forward and backward, for gfx950.
+//
+// Forward  (reference: BlitzGS submodule/diff-gaussian-rasterization_f,
+//           cuda_rasterizer/forward.cu:28-284, auxiliary.h:41-184, host side
+//           rasterizer_impl.cu:982-1067 and rasterize_points.cu:834-923):
+//   near cull, EWA projection with the 0.3 low-pass, conic, opacity-aware
+//   radius and float tile rect, SH (degree <= 3) colour with clamp flags.
+// Backward (reference: same package, cuda_rasterizer/backward.cu:20-400,
+//           rasterizer_impl.cu:1069-1129, rasterize_points.cu:926-1029):
+//   the reference's two kernels (computeCov2DCUDA, preprocessCUDA) fused into
+//   one pass that reads dL/dconic_opacity and dL/dmeans2D directly (no
+//   (P,2,2) repack, no (P,3) padding, no dc/rest split and no dL/dcov3D
+//   round trip through memory) and writes dL/dsh as (P,K,3) in place.
+//
+// One thread per Gaussian.  Every output element is written (zeros for culled
+// Gaussians), so callers need not clear the outputs.  The forward arithmetic
+// is the fixed-order fp32 sequence that oracle/o_preprocess.c restates on the
+// CPU; with -ffp-contract=off the two agree bit for bit.
+#include "gs_device.h"
+#include "gs_host.h"
+#include "../../include/blitzgs_amd.h"
+
+namespace {
+
+constexpr float SH_C0 = 0.28209479177387814f;
+constexpr float SH_C1 = 0.4886025119029199f;
+constexpr float SH_C2_0 = 1.0925484305920792f, SH_C2_1 = -1.0925484305920792f,
+                SH_C2_2 = 0.31539156525252005f, SH_C2_3 = -1.0925484305920792f,
+                SH_C2_4 = 0.5462742152960396f;
+constexpr float SH_C3_0 = -0.5900435899266435f, SH_C3_1 = 2.890611442640554f,
+                SH_C3_2 = -0.4570457994644658f, SH_C3_3 = 0.3731763325901154f,
+                SH_C3_4 = -0.4570457994644658f, SH_C3_5 = 1.445305721320277f,
+                SH_C3_6 = -0.5900435899266435f;
+
+struct Cam {
+    float v[16];
+    float p[16];
+    float c[3];
+};
+
+__device__ __forceinline__ void load_cam(Cam& cam, const float* __restrict__ view, const float* __restrict__ proj,
+                                         const float* __restrict__ campos)
+{
+#pragma unroll
+    for (int i = 0; i < 16; i++) { cam.v[i] = view[i]; cam.p[i] = proj[i]; }
+    cam.c[0] = campos[0]; cam.c[1] = campos[1]; cam.c[2] = campos[2];
+}
+
+__device__ __forceinline__ void xform3(const float* m, float x, float y, float z, float* o)
+{
+    o[0] = m[0] * x + m[4] * y + m[8] * z + m[12];
+    o[1] = m[1] * x + m[5] * y + m[9] * z + m[13];
+    o[2] = m[2] * x + m[6] * y + m[10] * z + m[14];
+}
+
+__device__ __forceinline__ float xform_w(const float* m, float x, float y, float z)
+{
+    return m[3] * x + m[7] * y + m[11] * z + m[15];
+}
+
+__device__ __forceinline__ float ndc2pix(float v, int S)
+{
+    return (float)((((double)v + 1.0) * (double)S - 1.0) * 0.5);
+}
+
+// Rm: glm rotation matrix of the reference read row-wise (un-normalised quat)
+__device__ __forceinline__ void quat_rows(float r, float x, float y, float z, float Rm[3][3])
+{
+    Rm[0][0] = 1.f - 2.f * (y * y + z * z); Rm[0][1] = 2.f * (x * y + r * z); Rm[0][2] = 2.f * (x * z - r * y);
+    Rm[1][0] = 2.f * (x * y - r * z); Rm[1][1] = 1.f - 2.f * (x * x + z * z); Rm[1][2] = 2.f * (y * z + r * x);
+    Rm[2][0] = 2.f * (x * z + r * y); Rm[2][1] = 2.f * (y * z - r * x); Rm[2][2] = 1.f - 2.f * (x * x + y * y);
+}
+
+struct Ewa {
+    float t0, t1, t2;
+    float u[3], w[3];
+    float xmask, ymask;
+};
+
+__device__ __forceinline__ void ewa_setup(const float* V, float mx, float my, float mz, float fx, float fy,
+                                          float tanfovx, float tanfovy, Ewa& e)
+{
+    float t[3];
+    xform3(V, mx, my, mz, t);
+    const float limx = 1.3f * tanfovx;
+    const float limy = 1.3f * tanfovy;
+    const float txtz = t[0] / t[2];
+    const float tytz = t[1] / t[2];
+    t[0] = __builtin_fminf(limx, __builtin_fmaxf(-limx, txtz)) * t[2];
+    t[1] = __builtin_fminf(limy, __builtin_fmaxf(-limy, tytz)) * t[2];
+    e.xmask = (txtz < -limx || txtz > limx) ? 0.f : 1.f;
+    e.ymask = (tytz < -limy || tytz > limy) ? 0.f : 1.f;
+    e.t0 = t[0]; e.t1 = t[1]; e.t2 = t[2];
+    const float tz2 = t[2] * t[2];
+    const float J00 = fx / t[2];
+    const float J11 = fy / t[2];
+    const float J20 = -(fx * t[0]) / tz2;
+    const float J21 = -(fy * t[1]) / tz2;
+#pragma unroll
+    for (int r = 0; r < 3; r++) {
+        e.u[r] = V[r * 4 + 0] * J00 + V[r * 4 + 2] * J20;
+        e.w[r] = V[r * 4 + 1] * J11 + V[r * 4 + 2] * J21;
+    }
+}
+
+__device__ __forceinline__ void symv(const float* c6, const float* v, float* o)
+{
+    o[0] = c6[0] * v[0] + c6[1] * v[1] + c6[2] * v[2];
+    o[1] = c6[1] * v[0] + c6[3] * v[1] + c6[4] * v[2];
+    o[2] = c6[2] * v[0] + c6[4] * v[1] + c6[5] * v[2];
+}
+
+// Load the first NC (= (DEG+1)^2) coefficients of one Gaussian's SH block.
+template <int NC>
+__device__ __forceinline__ void load_sh(const float* __restrict__ base, bool vec16, float* s)
+{
+    if (vec16) {
+        const float4* b4 = reinterpret_cast<const float4*>(base);
+#pragma unroll
+        for (int i = 0; i < (3 * NC + 3) / 4; i++) {
+            const float4 v = b4[i];
+            if (4 * i + 0 < 3 * NC) s[4 * i + 0] = v.x;
+            if (4 * i + 1 < 3 * NC) s[4 * i + 1] = v.y;
+            if (4 * i + 2 < 3 * NC) s[4 * i + 2] = v.z;
+            if (4 * i + 3 < 3 * NC) s[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 3 * NC; i++) s[i] = base[i];
+    }
+}
+
+template <int DEG>
+__device__ __forceinline__ void sh_color(float x, float y, float z, const float* s, float* out, bool* clamped)
+{
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        float r = SH_C0 * s[c];
+        if (DEG > 0) {
+            r = r - (SH_C1 * y) * s[3 + c] + (SH_C1 * z) * s[6 + c] - (SH_C1 * x) * s[9 + c];
+            if (DEG > 1) {
+                const float xx = x * x, yy = y * y, zz = z * z;
+                const float xy = x * y, yz = y * z, xz = x * z;
+                r = r + (SH_C2_0 * xy) * s[12 + c] + (SH_C2_1 * yz) * s[15 + c] +
+                    (SH_C2_2 * (2.0f * zz - xx - yy)) * s[18 + c] +
+                    (SH_C2_3 * xz) * s[21 + c] + (SH_C2_4 * (xx - yy)) * s[24 + c];
+                if (DEG > 2) {
+                    r = r + ((SH_C3_0 * y) * (3.0f * xx - yy)) * s[27 + c] +
+                        ((SH_C3_1 * xy) * z) * s[30 + c] +
+                        ((SH_C3_2 * y) * (4.0f * zz - xx - yy)) * s[33 + c] +
+                        ((SH_C3_3 * z) * (2.0f * zz - 3.0f * xx - 3.0f * yy)) * s[36 + c] +
+                        ((SH_C3_4 * x) * (4.0f * zz - xx - yy)) * s[39 + c] +
+                        ((SH_C3_5 * z) * (xx - yy)) * s[42 + c] +
+                        ((SH_C3_6 * x) * (xx - 3.0f * yy)) * s[45 + c];
+                }
+            }
+        }
+        r = r + 0.5f;
+        clamped[c] = r < 0.0f;
+        out[c] = __builtin_fmaxf(r, 0.0f);
+    }
+}
+
+template <int DEG>
+__global__ __launch_bounds__(256) void preprocess_fwd_kernel(
+    int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
+    const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
+    const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
+    const float* __restrict__ sh, int sh_vec16, const float* __restrict__ opacities,
+    float* __restrict__ means2D, float* __restrict__ depths, int* __restrict__ radii, float* __restrict__ cov3D,
+    float* __restrict__ conic_opacity, float* __restrict__ rgb, uint8_t* __restrict__ clamped)
+{
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= P) return;
+    Cam cam;
+    load_cam(cam, view, proj, campos);
+    const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
+
+    const float mx = means3D[3 * idx], my = means3D[3 * idx + 1], mz = means3D[3 * idx + 2];
+    float o_m2d[2] = {0.f, 0.f}, o_depth = 0.f, o_con[4] = {0.f, 0.f, 0.f, 0.f}, o_rgb[3] = {0.f, 0.f, 0.f};
+    float c6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int o_radius = 0;
+    bool o_clamp[3] = {false, false, false};
+
+    do {
+        float pv[3];
+        xform3(cam.v, mx, my, mz, pv);
+        if (pv[2] <= 0.2f) break;
+        float ph[3];
+        xform3(cam.p, mx, my, mz, ph);
+        const float pw = 1.0f / (xform_w(cam.p, mx, my, mz) + 0.0000001f);
+        const float pp0 = ph[0] * pw, pp1 = ph[1] * pw;
+
+        {
+            const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
+            float Rm[3][3];
+            quat_rows(q.x, q.y, q.z, q.w, Rm);
+            const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
+            float M[3][3];
+#pragma unroll
+            for (int i = 0; i < 3; i++)
+#pragma unroll
+                for (int j = 0; j < 3; j++) M[i][j] = s[i] * Rm[i][j];
+            c6[0] = M[0][0] * M[0][0] + M[1][0] * M[1][0] + M[2][0] * M[2][0];
+            c6[1] = M[0][0] * M[0][1] + M[1][0] * M[1][1] + M[2][0] * M[2][1];
+            c6[2] = M[0][0] * M[0][2] + M[1][0] * M[1][2] + M[2][0] * M[2][2];
+            c6[3] = M[0][1] * M[0][1] + M[1][1] * M[1][1] + M[2][1] * M[2][1];
+            c6[4] = M[0][1] * M[0][2] + M[1][1] * M[1][2] + M[2][1] * M[2][2];
+            c6[5] = M[0][2] * M[0][2] + M[1][2] * M[1][2] + M[2][2] * M[2][2];
+        }
+
+        Ewa e;
+        ewa_setup(cam.v, mx, my, mz, fx, fy, tanfovx, tanfovy, e);
+        float Su[3], Sw[3];
+        symv(c6, e.u, Su);
+        symv(c6, e.w, Sw);
+        float ca = e.u[0] * Su[0] + e.u[1] * Su[1] + e.u[2] * Su[2];
+        const float cb = e.u[0] * Sw[0] + e.u[1] * Sw[1] + e.u[2] * Sw[2];
+        float cc = e.w[0] * Sw[0] + e.w[1] * Sw[1] + e.w[2] * Sw[2];
+        ca = ca + 0.3f;
+        cc = cc + 0.3f;
+
+        const float det = ca * cc - cb * cb;
+        if (det == 0.0f) break;
+        const float det_inv = 1.f / det;
+
+        const float opacity = opacities[idx];
+        const float opt = gs::logf_full(opacity / (1.0f / 255.0f));
+        const float sq = __builtin_sqrtf(2.0f * opt);
+        const float extent = (sq != sq || (double)sq >= 3.33) ? (float)3.33 : sq;
+        const float mid = 0.5f * (ca + cc);
+        const float lambda = mid + __builtin_sqrtf(__builtin_fmaxf(0.01f, mid * mid - det));
+        const float my_radius = extent * __builtin_sqrtf(lambda);
+        if (my_radius <= 0.0f) break;
+
+        const float pix0 = ndc2pix(pp0, W), pix1 = ndc2pix(pp1, H);
+        const float ex = __builtin_fminf(extent * __builtin_sqrtf(ca), my_radius);
+        const float ey = __builtin_fminf(extent * __builtin_sqrtf(cc), my_radius);
+        const unsigned rminx = gs::clamp_tile(gs::f2i_sat(__builtin_floorf((pix0 - ex) / 16.0f)), gx);
+        const unsigned rminy = gs::clamp_tile(gs::f2i_sat(__builtin_floorf((pix1 - ey) / 16.0f)), gy);
+        const unsigned rmaxx = gs::clamp_tile(gs::f2i_sat(__builtin_ceilf((pix0 + ex) / 16.0f)), gx);
+        const unsigned rmaxy = gs::clamp_tile(gs::f2i_sat(__builtin_ceilf((pix1 + ey) / 16.0f)), gy);
+        if ((rmaxx - rminx) * (rmaxy - rminy) == 0) break;
+
+        // SH -> RGB (only Gaussians that survive every cull read their SH block)
+        {
+            constexpr int NC = (DEG + 1) * (DEG + 1);
+            float s[3 * NC];
+            load_sh<NC>(sh + (size_t)idx * K * 3, sh_vec16 != 0, s);
+            float dir0 = mx - cam.c[0], dir1 = my - cam.c[1], dir2 = mz - cam.c[2];
+            const float len = __builtin_sqrtf(dir0 * dir0 + dir1 * dir1 + dir2 * dir2);
+            dir0 = dir0 / len; dir1 = dir1 / len; dir2 = dir2 / len;
+            sh_color<DEG>(dir0, dir1, dir2, s, o_rgb, o_clamp);
+        }
+
+        o_depth = pv[2];
+        o_radius = gs::f2i_sat(__builtin_ceilf(my_radius));
+        o_m2d[0] = pix0; o_m2d[1] = pix1;
+        o_con[0] = cc * det_inv;
+        o_con[1] = -cb * det_inv;
+        o_con[2] = ca * det_inv;
+        o_con[3] = opacity;
+    } while (0);
+
+    reinterpret_cast<float2*>(means2D)[idx] = make_float2(o_m2d[0], o_m2d[1]);
+    depths[idx] = o_depth;
+    radii[idx] = o_radius;
+    float2* c2 = reinterpret_cast<float2*>(cov3D + 6 * (size_t)idx);
+    c2[0] = make_float2(c6[0], c6[1]);
+    c2[1] = make_float2(c6[2], c6[3]);
+    c2[2] = make_float2(c6[4], c6[5]);
+    reinterpret_cast<float4*>(conic_opacity)[idx] = make_float4(o_con[0], o_con[1], o_con[2], o_con[3]);
+    rgb[3 * idx + 0] = o_rgb[0];
+    rgb[3 * idx + 1] = o_rgb[1];
+    rgb[3 * idx + 2] = o_rgb[2];
+    clamped[3 * idx + 0] = o_clamp[0];
+    clamped[3 * idx + 1] = o_clamp[1];
+    clamped[3 * idx + 2] = o_clamp[2];
+}
+
+// dnormvdv (reference auxiliary.h:126-136)
+__device__ __forceinline__ void dnormvdv3(const float* v, const float* dv, float* o)
+{
+    const float sum2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+    const float invsum32 = 1.0f / __builtin_sqrtf(sum2 * sum2 * sum2);
+    o[0] = ((sum2 - v[0] * v[0]) * dv[0] - v[1] * v[0] * dv[1] - v[2] * v[0] * dv[2]) * invsum32;
+    o[1] = (-v[0] * v[1] * dv[0] + (sum2 - v[1] * v[1]) * dv[1] - v[2] * v[1] * dv[2]) * invsum32;
+    o[2] = (-v[0] * v[2] * dv[0] - v[1] * v[2] * dv[1] + (sum2 - v[2] * v[2]) * dv[2]) * invsum32;
+}
+
+template <int DEG>
+__device__ __forceinline__ void sh_backward(float x, float y, float z, const float* s, const float* g,
+                                            float* gsh, float* dx, float* dy, float* dz)
+{
+#pragma unroll
+    for (int c = 0; c < 3; c++) { gsh[c] = SH_C0 * g[c]; dx[c] = 0.f; dy[c] = 0.f; dz[c] = 0.f; }
+    if (DEG > 0) {
+        const float b1 = -SH_C1 * y, b2 = SH_C1 * z, b3 = -SH_C1 * x;
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            gsh[3 + c] = b1 * g[c]; gsh[6 + c] = b2 * g[c]; gsh[9 + c] = b3 * g[c];
+            dx[c] = -SH_C1 * s[9 + c];
+            dy[c] = -SH_C1 * s[3 + c];
+            dz[c] = SH_C1 * s[6 + c];
+        }
+        if (DEG > 1) {
+            const float xx = x * x, yy = y * y, zz = z * z;
+            const float xy = x * y, yz = y * z, xz = x * z;
+            const float b4 = SH_C2_0 * xy, b5 = SH_C2_1 * yz, b6 = SH_C2_2 * (2.f * zz - xx - yy);
+            const float b7 = SH_C2_3 * xz, b8 = SH_C2_4 * (xx - yy);
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                gsh[12 + c] = b4 * g[c]; gsh[15 + c] = b5 * g[c]; gsh[18 + c] = b6 * g[c];
+                gsh[21 + c] = b7 * g[c]; gsh[24 + c] = b8 * g[c];
+                dx[c] += SH_C2_0 * y * s[12 + c] + SH_C2_2 * 2.f * -x * s[18 + c] + SH_C2_3 * z * s[21 + c] + SH_C2_4 * 2.f * x * s[24 + c];
+                dy[c] += SH_C2_0 * x * s[12 + c] + SH_C2_1 * z * s[15 + c] + SH_C2_2 * 2.f * -y * s[18 + c] + SH_C2_4 * 2.f * -y * s[24 + c];
+                dz[c] += SH_C2_1 * y * s[15 + c] + SH_C2_2 * 2.f * 2.f * z * s[18 + c] + SH_C2_3 * x * s[21 + c];
+            }
+            if (DEG > 2) {
+                const float b9 = SH_C3_0 * y * (3.f * xx - yy);
+                const float b10 = SH_C3_1 * xy * z;
+                const float b11 = SH_C3_2 * y * (4.f * zz - xx - yy);
+                const float b12 = SH_C3_3 * z * (2.f * zz - 3.f * xx - 3.f * yy);
+                const float b13 = SH_C3_4 * x * (4.f * zz - xx - yy);
+                const float b14 = SH_C3_5 * z * (xx - yy);
+                const float b15 = SH_C3_6 * x * (xx - 3.f * yy);
+#pragma unroll
+                for (int c = 0; c < 3; c++) {
+                    gsh[27 + c] = b9 * g[c]; gsh[30 + c] = b10 * g[c]; gsh[33 + c] = b11 * g[c];
+                    gsh[36 + c] = b12 * g[c]; gsh[39 + c] = b13 * g[c]; gsh[42 + c] = b14 * g[c];
+                    gsh[45 + c] = b15 * g[c];
+                    dx[c] += (SH_C3_0 * s[27 + c] * 3.f * 2.f * xy + SH_C3_1 * s[30 + c] * yz +
+                              SH_C3_2 * s[33 + c] * -2.f * xy + SH_C3_3 * s[36 + c] * -3.f * 2.f * xz +
+                              SH_C3_4 * s[39 + c] * (-3.f * xx + 4.f * zz - yy) +
+                              SH_C3_5 * s[42 + c] * 2.f * xz + SH_C3_6 * s[45 + c] * 3.f * (xx - yy));
+                    dy[c] += (SH_C3_0 * s[27 + c] * 3.f * (xx - yy) + SH_C3_1 * s[30 + c] * xz +
+                              SH_C3_2 * s[33 + c] * (-3.f * yy + 4.f * zz - xx) +
+                              SH_C3_3 * s[36 + c] * -3.f * 2.f * yz + SH_C3_4 * s[39 + c] * -2.f * xy +
+                              SH_C3_5 * s[42 + c] * -2.f * yz + SH_C3_6 * s[45 + c] * -3.f * 2.f * xy);
+                    dz[c] += (SH_C3_1 * s[30 + c] * xy + SH_C3_2 * s[33 + c] * 4.f * 2.f * yz +
+                              SH_C3_3 * s[36 + c] * 3.f * (2.f * zz - xx - yy) +
+                              SH_C3_4 * s[39 + c] * 4.f * 2.f * xz + SH_C3_5 * s[42 + c] * (xx - yy));
+                }
+            }
+        }
+    }
+}
+
+template <int DEG>
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
+    int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
+    const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
+    const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
+    const float* __restrict__ sh, int sh_vec16, const int* __restrict__ radii, const float* __restrict__ cov3D,
+    const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
+    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
+    float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity)
+{
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= P) return;
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
+    dL_dopacity[idx] = gco.w;
+    float* gsh_out = dL_dsh + (size_t)idx * K * 3;
+    const bool vec16 = sh_vec16 != 0;
+
+    if (!(radii[idx] > 0)) {
+        reinterpret_cast<float*>(dL_dmeans3D)[3 * idx + 0] = 0.f;
+        dL_dmeans3D[3 * idx + 1] = 0.f;
+        dL_dmeans3D[3 * idx + 2] = 0.f;
+        dL_dscales[3 * idx + 0] = 0.f;
+        dL_dscales[3 * idx + 1] = 0.f;
+        dL_dscales[3 * idx + 2] = 0.f;
+        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (vec16) {
+            float4* o4 = reinterpret_cast<float4*>(gsh_out);
+            for (int i = 0; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            for (int i = 0; i < 3 * K; i++) gsh_out[i] = 0.f;
+        }
+        return;
+    }
+    Cam cam;
+    load_cam(cam, view, proj, campos);
+    (void)W; (void)H;
+    const float mx = means3D[3 * idx], my = means3D[3 * idx + 1], mz = means3D[3 * idx + 2];
+    const float* V = cam.v;
+    const float* PM = cam.p;
+    float c6[6];
+    {
+        const float2* c2 = reinterpret_cast<const float2*>(cov3D + 6 * (size_t)idx);
+        const float2 a = c2[0], b = c2[1], c = c2[2];
+        c6[0] = a.x; c6[1] = a.y; c6[2] = b.x; c6[3] = b.y; c6[4] = c.x; c6[5] = c.y;
+    }
+
+    // ---- conic -> 2D covariance -> 3D covariance and mean (cov2D backward)
+    Ewa e;
+    ewa_setup(V, mx, my, mz, fx, fy, tanfovx, tanfovy, e);
+    float Su[3], Sw[3];
+    symv(c6, e.u, Su);
+    symv(c6, e.w, Sw);
+    float a = e.u[0] * Su[0] + e.u[1] * Su[1] + e.u[2] * Su[2];
+    const float b = e.u[0] * Sw[0] + e.u[1] * Sw[1] + e.u[2] * Sw[2];
+    float c = e.w[0] * Sw[0] + e.w[1] * Sw[1] + e.w[2] * Sw[2];
+    a = a + 0.3f;
+    c = c + 0.3f;
+    const float g0 = gco.x, g1 = gco.y, g2 = gco.z;
+    const float denom = a * c - b * b;
+    const float denom2inv = 1.0f / ((denom * denom) + 0.0000001f);
+    float dL_da = 0, dL_db = 0, dL_dc = 0;
+    float dcov[6] = {0, 0, 0, 0, 0, 0};
+    if (denom2inv != 0) {
+        dL_da = denom2inv * (-c * c * g0 + 2 * b * c * g1 + (denom - a * c) * g2);
+        dL_dc = denom2inv * (-a * a * g2 + 2 * a * b * g1 + (denom - a * c) * g0);
+        dL_db = denom2inv * 2 * (b * c * g0 - (denom + 2 * b * b) * g1 + a * b * g2);
+        const float* u = e.u;
+        const float* w = e.w;
+        dcov[0] = u[0] * u[0] * dL_da + u[0] * w[0] * dL_db + w[0] * w[0] * dL_dc;
+        dcov[3] = u[1] * u[1] * dL_da + u[1] * w[1] * dL_db + w[1] * w[1] * dL_dc;
+        dcov[5] = u[2] * u[2] * dL_da + u[2] * w[2] * dL_db + w[2] * w[2] * dL_dc;
+        dcov[1] = 2 * u[0] * u[1] * dL_da + (u[0] * w[1] + u[1] * w[0]) * dL_db + 2 * w[0] * w[1] * dL_dc;
+        dcov[2] = 2 * u[0] * u[2] * dL_da + (u[0] * w[2] + u[2] * w[0]) * dL_db + 2 * w[0] * w[2] * dL_dc;
+        dcov[4] = 2 * u[2] * u[1] * dL_da + (u[1] * w[2] + u[2] * w[1]) * dL_db + 2 * w[1] * w[2] * dL_dc;
+    }
+    float du[3], dw[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        du[k] = 2 * Su[k] * dL_da + Sw[k] * dL_db;
+        dw[k] = 2 * Sw[k] * dL_dc + Su[k] * dL_db;
+    }
+    const float dJ00 = V[0] * du[0] + V[4] * du[1] + V[8] * du[2];
+    const float dJ20 = V[2] * du[0] + V[6] * du[1] + V[10] * du[2];
+    const float dJ11 = V[1] * dw[0] + V[5] * dw[1] + V[9] * dw[2];
+    const float dJ21 = V[2] * dw[0] + V[6] * dw[1] + V[10] * dw[2];
+    const float tz = 1.f / e.t2;
+    const float tz2 = tz * tz;
+    const float tz3 = tz2 * tz;
+    const float dtx = e.xmask * -fx * tz2 * dJ20;
+    const float dty = e.ymask * -fy * tz2 * dJ21;
+    const float dtz = -fx * tz2 * dJ00 - fy * tz2 * dJ11 + (2 * fx * e.t0) * tz3 * dJ20 + (2 * fy * e.t1) * tz3 * dJ21;
+    float gm[3];
+    gm[0] = V[0] * dtx + V[1] * dty + V[2] * dtz;
+    gm[1] = V[4] * dtx + V[5] * dty + V[6] * dtz;
+    gm[2] = V[8] * dtx + V[9] * dty + V[10] * dtz;
+
+    // ---- screen-space mean -> 3D mean
+    {
+        const float m_w = 1.0f / (xform_w(PM, mx, my, mz) + 0.0000001f);
+        const float mul1 = (PM[0] * mx + PM[4] * my + PM[8] * mz + PM[12]) * m_w * m_w;
+        const float mul2 = (PM[1] * mx + PM[5] * my + PM[9] * mz + PM[13]) * m_w * m_w;
+        const float gx = dL_dmeans2D[(size_t)idx * m2d_stride + 0];
+        const float gy = dL_dmeans2D[(size_t)idx * m2d_stride + 1];
+        gm[0] += (PM[0] * m_w - PM[3] * mul1) * gx + (PM[1] * m_w - PM[3] * mul2) * gy;
+        gm[1] += (PM[4] * m_w - PM[7] * mul1) * gx + (PM[5] * m_w - PM[7] * mul2) * gy;
+        gm[2] += (PM[8] * m_w - PM[11] * mul1) * gx + (PM[9] * m_w - PM[11] * mul2) * gy;
+    }
+
+    // ---- SH backward
+    {
+        float s[3 * NC];
+        load_sh<NC>(sh + (size_t)idx * K * 3, vec16, s);
+        const float dir_orig[3] = {mx - cam.c[0], my - cam.c[1], mz - cam.c[2]};
+        const float len = __builtin_sqrtf(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]);
+        const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
+        float g[3];
+#pragma unroll
+        for (int ch = 0; ch < 3; ch++) g[ch] = clamped[3 * idx + ch] ? 0.0f : dL_drgb[3 * idx + ch];
+        float gsh[3 * NC], dx[3], dy[3], dz[3];
+        sh_backward<DEG>(x, y, z, s, g, gsh, dx, dy, dz);
+        const float dL_ddir[3] = {dx[0] * g[0] + dx[1] * g[1] + dx[2] * g[2],
+                                  dy[0] * g[0] + dy[1] * g[1] + dy[2] * g[2],
+                                  dz[0] * g[0] + dz[1] * g[1] + dz[2] * g[2]};
+        float dm[3];
+        dnormvdv3(dir_orig, dL_ddir, dm);
+        gm[0] += dm[0]; gm[1] += dm[1]; gm[2] += dm[2];
+        // dL/dsh: the first NC coefficients, zeros after
+        if (vec16) {
+            float4* o4 = reinterpret_cast<float4*>(gsh_out);
+#pragma unroll
+            for (int i = 0; i < (3 * NC + 3) / 4; i++) {
+                float v[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[k] = (4 * i + k < 3 * NC) ? gsh[4 * i + k] : 0.f;
+                o4[i] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+            for (int i = (3 * NC + 3) / 4; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 3 * NC; i++) gsh_out[i] = gsh[i];
+            for (int i = 3 * NC; i < 3 * K; i++) gsh_out[i] = 0.f;
+        }
+    }
+    dL_dmeans3D[3 * idx + 0] = gm[0];
+    dL_dmeans3D[3 * idx + 1] = gm[1];
+    dL_dmeans3D[3 * idx + 2] = gm[2];
+
+    // ---- 3D covariance -> scale and (un-normalised) quaternion
+    {
+        const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
+        const float r = q.x, x = q.y, y = q.z, z = q.w;
+        float Rm[3][3];
+        quat_rows(r, x, y, z, Rm);
+        const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
+        float M[3][3];
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) M[i][j] = s[i] * Rm[i][j];
+        const float D[3][3] = {{dcov[0], 0.5f * dcov[1], 0.5f * dcov[2]},
+                               {0.5f * dcov[1], dcov[3], 0.5f * dcov[4]},
+                               {0.5f * dcov[2], 0.5f * dcov[4], dcov[5]}};
+        float G[3][3];
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+                G[i][j] = (2.0f * M[i][0]) * D[0][j] + (2.0f * M[i][1]) * D[1][j] + (2.0f * M[i][2]) * D[2][j];
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            dL_dscales[3 * idx + i] = Rm[i][0] * G[i][0] + Rm[i][1] * G[i][1] + Rm[i][2] * G[i][2];
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) G[i][j] = G[i][j] * s[i];
+        const float q0 = 2 * z * (G[0][1] - G[1][0]) + 2 * y * (G[2][0] - G[0][2]) + 2 * x * (G[1][2] - G[2][1]);
+        const float q1 = 2 * y * (G[1][0] + G[0][1]) + 2 * z * (G[2][0] + G[0][2]) + 2 * r * (G[1][2] - G[2][1]) - 4 * x * (G[2][2] + G[1][1]);
+        const float q2 = 2 * x * (G[1][0] + G[0][1]) + 2 * r * (G[2][0] - G[0][2]) + 2 * z * (G[1][2] + G[2][1]) - 4 * y * (G[2][2] + G[0][0]);
+        const float q3 = 2 * r * (G[0][1] - G[1][0]) + 2 * x * (G[2][0] + G[0][2]) + 2 * y * (G[1][2] + G[2][1]) - 4 * z * (G[1][1] + G[0][0]);
+        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(q0, q1, q2, q3);
+    }
+}
+
+}  // namespace
+
+extern "C" int gs_preprocess_forward(
+    int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
+    const float* sh, const float* opacities, float scale_modifier, const float* viewmatrix,
+    const float* projmatrix, const float* campos, float tanfovx, float tanfovy, int image_height,
+    int image_width, float* means2D, float* depths, int* radii, float* cov3D, float* conic_opacity,
+    float* rgb, uint8_t* clamped, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(D >= 0 && D <= 3, "sh_degree must be in [0, 3] (got %d)", D);
+    GS_REQUIRE(K >= (D + 1) * (D + 1), "sh must have at least (D+1)^2 = %d coefficients (got %d)",
+               (D + 1) * (D + 1), K);
+    GS_REQUIRE(image_width > 0 && image_height > 0, "image size must be positive");
+    GS_REQUIRE(((uintptr_t)rotations & 15) == 0 && ((uintptr_t)conic_opacity & 15) == 0,
+               "rotations and conic_opacity must be 16-byte aligned");
+    const int sh_vec16 = ((K & 3) == 0 && ((uintptr_t)sh & 15) == 0) ? 1 : 0;
+    const float fy = (float)image_height / (2.0f * tanfovy);
+    const float fx = (float)image_width / (2.0f * tanfovx);
+    const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+#define GS_PRE_FWD(DEG)                                                                             \
+    hipLaunchKernelGGL(preprocess_fwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,        \
+                       image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
+                       campos, means3D, scales, rotations, sh, sh_vec16, opacities, means2D, depths, radii, \
+                       cov3D, conic_opacity, rgb, clamped)
+    switch (D) {
+        case 0: GS_PRE_FWD(0); break;
+        case 1: GS_PRE_FWD(1); break;
+        case 2: GS_PRE_FWD(2); break;
+        default: GS_PRE_FWD(3); break;
+    }
+#undef GS_PRE_FWD
+    GS_LAUNCH_CHECK("preprocess_fwd_kernel");
+    return GS_OK;
+}
+
+extern "C" int gs_preprocess_backward(
+    int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
+    const float* sh, float scale_modifier, const float* viewmatrix, const float* projmatrix,
+    const float* campos, float tanfovx, float tanfovy, int image_height, int image_width,
+    const int* radii, const float* cov3D, const uint8_t* clamped, const float* dL_dmeans2D,
+    int dL_dmeans2D_stride, const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
+    float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(D >= 0 && D <= 3, "sh_degree must be in [0, 3] (got %d)", D);
+    GS_REQUIRE(K >= (D + 1) * (D + 1), "sh must have at least (D+1)^2 = %d coefficients (got %d)",
+               (D + 1) * (D + 1), K);
+    GS_REQUIRE(dL_dmeans2D_stride >= 2, "dL_dmeans2D row stride must be >= 2");
+    GS_REQUIRE(((uintptr_t)rotations & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
+               ((uintptr_t)dL_drotations & 15) == 0,
+               "rotations, dL_dconic_opacity and dL_drotations must be 16-byte aligned");
+    const int sh_vec16 = ((K & 3) == 0 && ((uintptr_t)sh & 15) == 0 && ((uintptr_t)dL_dsh & 15) == 0) ? 1 : 0;
+    const float fy = (float)image_height / (2.0f * tanfovy);
+    const float fx = (float)image_width / (2.0f * tanfovx);
+    const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+#define GS_PRE_BWD(DEG)                                                                                  \
+    hipLaunchKernelGGL(preprocess_bwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,             \
+                       image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
+                       campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
+                       dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
+                       dL_drotations, dL_dsh, dL_dopacity)
+    switch (D) {
+        case 0: GS_PRE_BWD(0); break;
+        case 1: GS_PRE_BWD(1); break;
+        case 2: GS_PRE_BWD(2); break;
+        default: GS_PRE_BWD(3); break;
+    }
+#undef GS_PRE_BWD
+    GS_LAUNCH_CHECK("preprocess_bwd_kernel");
+    return GS_OK;
+}

@@ -1,0 +1,342 @@
+"""Python operator layer of the rasterizer: the reference's split training API.
+
+Mirrors BlitzGS submodule/diff-gaussian-rasterization_f/diff_gaussian_rasterization_f/__init__.py
+(and the _r package it dispatches render ops to):
+  GaussianRasterizationSettings          _f __init__.py:647-659 (_r adds render_geo)
+  GaussianRasterizer.preprocess_gaussians _f __init__.py:677-689
+  GaussianRasterizer.render_gaussians     _f __init__.py:812-829
+  preprocess_gaussians / _PreprocessGaussians   _f __init__.py:55-173
+  render_gaussians / _RenderGaussians           _f __init__.py:177-318, _r __init__.py:178-289
+Same argument order, return tuples, dtypes, saved buffers and
+non-differentiable outputs; the work is done by libblitzgs_amd.so (HIP,
+gfx950) through its C ABI.  Differences that do not change results:
+  * the (P,3) padding of dL/dmeans2D before the preprocess backward and the
+    [:, :2] slice after the render backward are not materialised: the C ABI
+    takes a row stride;
+  * dL/dall_map (all zeros when render_geo is off) is returned only when the
+    all_map input requires a gradient.
+"""
+import ctypes as C
+from typing import NamedTuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from ._lib import check, ptr
+
+
+class GaussianRasterizationSettings(NamedTuple):
+    image_height: int
+    image_width: int
+    tanfovx: float
+    tanfovy: float
+    bg: torch.Tensor
+    scale_modifier: float
+    viewmatrix: torch.Tensor
+    projmatrix: torch.Tensor
+    sh_degree: int
+    campos: torch.Tensor
+    prefiltered: bool
+    debug: bool
+
+
+def _dev_f32(t, device):
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _aligned(t, nbytes=16):
+    t = t.contiguous()
+    if t.numel() and t.data_ptr() % nbytes != 0:
+        t = t.clone()
+    return t
+
+
+def _require_device(t, name):
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a HIP device tensor (blitzgs_amd has no CPU path)")
+
+
+def _stream(device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _want_timing(cuda_args):
+    return isinstance(cuda_args, dict) and isinstance(cuda_args.get("stats_collector"), dict)
+
+
+# --------------------------------------------------------------- preprocess
+
+def preprocess_gaussians(means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
+    return _PreprocessGaussians.apply(means3D, scales, rotations, sh, opacities, raster_settings, cuda_args)
+
+
+def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs):
+    """Direct call of the C ABI; returns the reference's 8-tuple
+    (num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped)."""
+    if means3D.ndimension() != 2 or means3D.size(1) != 3:
+        raise RuntimeError("means3D must have dimensions (num_points, 3)")
+    _require_device(means3D, "means3D")
+    dev = means3D.device
+    P = means3D.size(0)
+    if sh.size(0) != 0 and (sh.ndimension() != 3 or sh.size(2) != 3 or sh.size(1) < 1):
+        raise RuntimeError("sh must have dimensions (num_points, num_sh_coeffs, 3) with num_sh_coeffs >= 1")
+    f32 = dict(device=dev, dtype=torch.float32)
+    means2D = torch.empty((P, 2), **f32)
+    depths = torch.empty((P,), **f32)
+    radii = torch.empty((P,), device=dev, dtype=torch.int32)
+    cov3D = torch.empty((P, 6), **f32)
+    conic_opacity = torch.empty((P, 4), **f32)
+    rgb = torch.empty((P, 3), **f32)
+    clamped = torch.empty((P, 3), device=dev, dtype=torch.bool)
+    if P != 0:
+        if sh.size(0) == 0:
+            raise RuntimeError("sh must be provided (precomputed colours are not supported by the split path)")
+        means3D = _dev_f32(means3D, dev)
+        scales = _dev_f32(scales, dev)
+        rotations = _aligned(_dev_f32(rotations, dev))
+        sh = _aligned(_dev_f32(sh, dev))
+        opacities = _dev_f32(opacities, dev)
+        view = _dev_f32(rs.viewmatrix, dev)
+        proj = _dev_f32(rs.projmatrix, dev)
+        campos = _dev_f32(rs.campos, dev)
+        lib = _lib.load()
+        rc = lib.gs_preprocess_forward(
+            P, int(rs.sh_degree), sh.size(1), ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), ptr(opacities),
+            float(rs.scale_modifier), ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy),
+            int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii), ptr(cov3D),
+            ptr(conic_opacity), ptr(rgb), ptr(clamped), _stream(dev))
+        check(rc, "gs_preprocess_forward")
+    return 0, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped
+
+
+def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
+                             dL_dconic_opacity, dL_drgb):
+    dev = means3D.device
+    P = means3D.size(0)
+    K = sh.size(1) if sh.ndimension() == 3 else 1
+    f32 = dict(device=dev, dtype=torch.float32)
+    dL_dmeans3D = torch.empty((P, 3), **f32)
+    dL_dscales = torch.empty((P, 3), **f32)
+    dL_drotations = torch.empty((P, 4), **f32)
+    dL_dsh = torch.empty((P, K, 3), **f32)
+    dL_dopacity = torch.empty((P, 1), **f32)
+    if P != 0:
+        means3D = _dev_f32(means3D, dev)
+        scales = _dev_f32(scales, dev)
+        rotations = _aligned(_dev_f32(rotations, dev))
+        sh = _aligned(_dev_f32(sh, dev))
+        dL_dmeans2D = _dev_f32(dL_dmeans2D, dev)
+        dL_dconic_opacity = _aligned(_dev_f32(dL_dconic_opacity, dev))
+        dL_drgb = _dev_f32(dL_drgb, dev)
+        view = _dev_f32(rs.viewmatrix, dev)
+        proj = _dev_f32(rs.projmatrix, dev)
+        campos = _dev_f32(rs.campos, dev)
+        lib = _lib.load()
+        rc = lib.gs_preprocess_backward(
+            P, int(rs.sh_degree), K, ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), float(rs.scale_modifier),
+            ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height),
+            int(rs.image_width), ptr(radii.contiguous()), ptr(cov3D.contiguous()), ptr(clamped.contiguous()),
+            ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
+            ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
+        check(rc, "gs_preprocess_backward")
+    return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity
+
+
+class _PreprocessGaussians(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
+        num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = _preprocess_forward_raw(
+            means3D, scales, rotations, sh, opacities, raster_settings)
+        ctx.raster_settings = raster_settings
+        ctx.cuda_args = cuda_args
+        ctx.num_rendered = num_rendered
+        ctx.save_for_backward(means3D, scales, rotations, sh, means2D, depths, radii, cov3D, conic_opacity, rgb,
+                              clamped)
+        ctx.mark_non_differentiable(radii, depths)
+        return means2D, rgb, conic_opacity, radii, depths
+
+    @staticmethod
+    def backward(ctx, grad_means2D, grad_rgb, grad_conic_opacity, grad_radii, grad_depths):
+        rs = ctx.raster_settings
+        means3D, scales, rotations, sh, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = ctx.saved_tensors
+        if grad_means2D is None:
+            grad_means2D = torch.zeros_like(means2D)
+        if grad_rgb is None:
+            grad_rgb = torch.zeros_like(rgb)
+        if grad_conic_opacity is None:
+            grad_conic_opacity = torch.zeros_like(conic_opacity)
+        dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity = _preprocess_backward_raw(
+            radii, cov3D, clamped, means3D, scales, rotations, sh, rs, grad_means2D, grad_conic_opacity, grad_rgb)
+        return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity, None, None
+
+
+# ------------------------------------------------------------------- render
+
+def render_gaussians(means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, compute_locally,
+                     extended_compute_locally, raster_settings, cuda_args):
+    return _RenderGaussians.apply(means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii,
+                                  compute_locally, extended_compute_locally, raster_settings, cuda_args)
+
+
+def _tile_mask(cl, H, W, device):
+    gy, gx = (H + 15) // 16, (W + 15) // 16
+    if cl is None:
+        return torch.ones(gy * gx, dtype=torch.uint8, device=device)
+    cl = cl.to(device=device)
+    if cl.numel() != gy * gx:
+        raise RuntimeError(f"compute_locally must have {gy}x{gx} tile entries, got {tuple(cl.shape)}")
+    return cl.reshape(-1).to(torch.uint8).contiguous()
+
+
+def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False):
+    """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
+    geomBuffer, binningBuffer, imgBuffer, render_ms)."""
+    _require_device(means2D, "means2D")
+    dev = means2D.device
+    P = means2D.size(0)
+    lib = _lib.load()
+    T = ((H + 15) // 16) * ((W + 15) // 16)
+    i32 = dict(device=dev, dtype=torch.int32)
+    cl = _tile_mask(compute_locally, H, W, dev)
+    means2D = _aligned(_dev_f32(means2D, dev), 8)
+    depths = _dev_f32(depths, dev)
+    radii = radii.to(device=dev, dtype=torch.int32).contiguous()
+    conic_opacity = _aligned(_dev_f32(conic_opacity, dev))
+    rgb = _dev_f32(rgb, dev)
+    bg = _dev_f32(bg, dev)
+    stream = _stream(dev)
+    geom = torch.empty(lib.gs_render_geom_bytes(P, W, H), device=dev, dtype=torch.uint8)
+    img = torch.empty(lib.gs_render_img_bytes(W, H), device=dev, dtype=torch.uint8)
+    R = C.c_int64(0)
+    check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(R), stream),
+          "gs_render_forward_count")
+    R = int(R.value)
+    binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
+    color = torch.empty((3, H, W), device=dev, dtype=torch.float32)
+    n_render = torch.empty((T,), **i32)
+    n_consider = torch.empty((T,), **i32)
+    n_contrib = torch.empty((T,), **i32)
+    out_observe = torch.empty((P,), **i32)
+    if timing:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    check(lib.gs_render_forward(P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity),
+                                ptr(rgb), ptr(cl), ptr(geom), ptr(binning), ptr(img), ptr(color), ptr(n_render),
+                                ptr(n_consider), ptr(n_contrib), ptr(out_observe), stream), "gs_render_forward")
+    ms = None
+    if timing:
+        ev1.record()
+        ev1.synchronize()
+        ms = ev0.elapsed_time(ev1)
+    return R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms
+
+
+def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, binning, img, dL_dpixels,
+                         m2d_stride=2, timing=False):
+    dev = means2D.device
+    P = means2D.size(0)
+    lib = _lib.load()
+    f32 = dict(device=dev, dtype=torch.float32)
+    cl = _tile_mask(compute_locally, H, W, dev)
+    dL_dmeans2D = torch.empty((P, m2d_stride), **f32)
+    dL_dmeans2D_abs = torch.empty((P, 3), **f32)
+    dL_dconic_opacity = torch.empty((P, 4), **f32)
+    dL_dcolors = torch.empty((P, 3), **f32)
+    means2D = _aligned(_dev_f32(means2D, dev), 8)
+    conic_opacity = _aligned(_dev_f32(conic_opacity, dev))
+    rgb = _dev_f32(rgb, dev)
+    bg = _dev_f32(bg, dev)
+    dL_dpixels = _dev_f32(dL_dpixels, dev)
+    if timing:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    check(lib.gs_render_backward(P, R, W, H, ptr(bg), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
+                                 ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D), m2d_stride,
+                                 ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors), _stream(dev)),
+          "gs_render_backward")
+    ms = None
+    if timing:
+        ev1.record()
+        ev1.synchronize()
+        ms = ev0.elapsed_time(ev1)
+    return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms
+
+
+class _RenderGaussians(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means2D, means2D_abs, conic_opacity, rgb, all_maps, depths, radii, compute_locally,
+                extended_compute_locally, raster_settings, cuda_args):
+        rs = raster_settings
+        if getattr(rs, "render_geo", False):
+            raise NotImplementedError("render_geo=True (normal / plane-depth maps) is not supported")
+        use_ext = isinstance(cuda_args, dict) and bool(cuda_args.get("avoid_pixel_all2all", False))
+        cl = extended_compute_locally if use_ext else compute_locally
+        H, W = int(rs.image_height), int(rs.image_width)
+        timing = _want_timing(cuda_args)
+        (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
+         ms) = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing)
+        if timing:
+            cuda_args["stats_collector"]["forward_render_time"] = ms
+        dev = means2D.device
+        out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
+        out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
+        ctx.raster_settings = rs
+        ctx.cuda_args = cuda_args
+        ctx.num_rendered = R
+        ctx.save_for_backward(means2D, conic_opacity, rgb, all_maps, out_all_map, geom, binning, img,
+                              compute_locally, extended_compute_locally)
+        ctx.mark_non_differentiable(n_render, n_consider, n_contrib)
+        return color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth
+
+    @staticmethod
+    def backward(ctx, grad_color, grad_n_render, grad_n_consider, grad_n_contrib, grad_out_observe,
+                 grad_out_all_map, grad_out_plane_depth):
+        rs = ctx.raster_settings
+        (means2D, conic_opacity, rgb, all_maps, all_map_pixels, geom, binning, img, compute_locally,
+         extended_compute_locally) = ctx.saved_tensors
+        H, W = int(rs.image_height), int(rs.image_width)
+        if grad_color is None:
+            grad_color = torch.zeros((3, H, W), device=means2D.device, dtype=torch.float32)
+        timing = _want_timing(ctx.cuda_args)
+        dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
+            rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, binning, img,
+            grad_color.contiguous(), 2, timing)
+        if timing:
+            ctx.cuda_args["stats_collector"]["backward_render_time"] = ms
+        dL_dall_map = None
+        if ctx.needs_input_grad[4]:
+            dL_dall_map = torch.zeros_like(all_maps)
+        return (dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, dL_dall_map,
+                None, None, None, None, None, None)
+
+
+class GaussianRasterizer(nn.Module):
+    """The split-path rasterizer module (_f __init__.py:661-829)."""
+
+    def __init__(self, raster_settings):
+        super().__init__()
+        self.raster_settings = raster_settings
+
+    def preprocess_gaussians(self, means3D, scales, rotations, shs, opacities, cuda_args=None):
+        return preprocess_gaussians(means3D, scales, rotations, shs, opacities, self.raster_settings, cuda_args)
+
+    def render_gaussians(self, means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, compute_locally,
+                         extended_compute_locally, cuda_args=None):
+        return render_gaussians(means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, compute_locally,
+                                extended_compute_locally, self.raster_settings, cuda_args)
+
+    def markVisible(self, positions):
+        raise NotImplementedError("markVisible (full-image _f path) is not part of the split training path")
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError("the full-image _f rasterize path (render_imp) is not implemented; "
+                                  "use preprocess_gaussians + render_gaussians")
+
+    def render_simp(self, *args, **kwargs):
+        raise NotImplementedError("render_simp (importance accumulation) is not implemented")
+
+    def render_depth(self, *args, **kwargs):
+        raise NotImplementedError("render_depth is not implemented")

@@ -1,0 +1,169 @@
+/*
+ * blitzgs_amd -- C ABI of the MI355X (gfx950) differentiable Gaussian
+ * rasterizer, simple-knn distCUDA2 and fused-ssim replacements.
+ *
+ * Conventions
+ *   - Every pointer argument named after a tensor is a device pointer to a
+ *     contiguous row-major array on the current HIP device; fp32 unless the
+ *     type says otherwise.  bool tensors are uint8_t (0/1).
+ *   - Every entry point is asynchronous on `stream` (a hipStream_t; 0 is the
+ *     null stream) unless documented otherwise, returns 0 on success and a
+ *     negative code on error; gs_last_error() then returns a message
+ *     (thread-local, valid until the next call on this thread).
+ *   - Argument validation mirrors the reference's checks; error text is
+ *     returned, never printed.
+ *   - Outputs are fully written by the library (no caller-side zeroing) unless
+ *     stated.
+ *   - Workspaces are plain device byte buffers sized by the *_bytes queries and
+ *     owned by the caller (the Python layer allocates them as torch uint8
+ *     tensors, as the reference keeps its geom/binning/img buffers).
+ *
+ * Reference interfaces replaced (paths under /root/reference/submodule):
+ *   diff-gaussian-rasterization_f/rasterize_points.cu:834-923  PreprocessGaussiansCUDA
+ *   diff-gaussian-rasterization_f/rasterize_points.cu:926-1029 PreprocessGaussiansBackwardCUDA
+ *   diff-gaussian-rasterization_r/rasterize_points.cu:273-361  RenderGaussiansCUDA
+ *   diff-gaussian-rasterization_r/rasterize_points.cu:363-436  RenderGaussiansBackwardCUDA
+ *   simple-knn/spatial.cu:15-26                                distCUDA2
+ *   fused-ssim/ssim.cu:367-402                                 fusedssim
+ *   fused-ssim/ssim.cu:404-441                                 fusedssim_backward
+ */
+#ifndef BLITZGS_AMD_H
+#define BLITZGS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* gs_stream_t; /* == hipStream_t */
+
+/* Library version (major*10000 + minor*100 + patch) and last error text. */
+int gs_version(void);
+const char* gs_last_error(void);
+
+/* ------------------------------------------------------------------------ *
+ * Preprocess forward.  Replaces PreprocessGaussiansCUDA
+ * (diff-gaussian-rasterization_f/rasterize_points.cu:834-923; kernel
+ * cuda_rasterizer/forward.cu:164-284).
+ *   P Gaussians, SH degree D (0..3), K = sh.size(1) >= (D+1)^2 coefficients.
+ *   means3D (P,3), scales (P,3), rotations (P,4) quaternions (r,x,y,z),
+ *   sh (P,K,3), opacities (P,1).  viewmatrix/projmatrix (4,4) and campos (3)
+ *   are device tensors laid out as the reference's settings tensors.
+ *   Outputs: means2D (P,2), depths (P), radii int32 (P), cov3D (P,6),
+ *   conic_opacity (P,4), rgb (P,3), clamped uint8 (P,3).
+ *   rotations and conic_opacity must be 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+int gs_preprocess_forward(int P, int D, int K, const float* means3D, const float* scales,
+                          const float* rotations, const float* sh, const float* opacities,
+                          float scale_modifier, const float* viewmatrix, const float* projmatrix,
+                          const float* campos, float tanfovx, float tanfovy, int image_height,
+                          int image_width, float* means2D, float* depths, int* radii, float* cov3D,
+                          float* conic_opacity, float* rgb, uint8_t* clamped, gs_stream_t stream);
+
+/* Preprocess backward.  Replaces PreprocessGaussiansBackwardCUDA
+ * (diff-gaussian-rasterization_f/rasterize_points.cu:926-1029; kernels
+ * cuda_rasterizer/backward.cu:146-276 and 348-400).
+ *   dL_dmeans2D has row stride dL_dmeans2D_stride floats (2, or 3 for the
+ *   reference's padded (P,3) layout); dL_dconic_opacity (P,4); dL_drgb (P,3).
+ *   Outputs: dL_dmeans3D (P,3), dL_dscales (P,3), dL_drotations (P,4),
+ *   dL_dsh (P,K,3), dL_dopacity (P,1) = dL_dconic_opacity[:,3]. */
+int gs_preprocess_backward(int P, int D, int K, const float* means3D, const float* scales,
+                           const float* rotations, const float* sh, float scale_modifier,
+                           const float* viewmatrix, const float* projmatrix, const float* campos,
+                           float tanfovx, float tanfovy, int image_height, int image_width,
+                           const int* radii, const float* cov3D, const uint8_t* clamped,
+                           const float* dL_dmeans2D, int dL_dmeans2D_stride,
+                           const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
+                           float* dL_dscales, float* dL_drotations, float* dL_dsh,
+                           float* dL_dopacity, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Render forward, in two calls because the size of the instance buffers
+ * (R = number of Gaussian/tile instances) is known only after counting.
+ * Together they replace RenderGaussiansCUDA
+ * (diff-gaussian-rasterization_r/rasterize_points.cu:273-361;
+ * cuda_rasterizer/rasterizer_impl.cu:556-723, forward.cu:263-413).
+ *
+ *   geom    : gs_render_geom_bytes(P, W, H) bytes  (counts, offsets)
+ *   binning : gs_render_binning_bytes(R) bytes     (sorted keys and ids)
+ *   img     : gs_render_img_bytes(W, H) bytes      (tile ranges, per-pixel
+ *             final transmittance and contributor counts)
+ * compute_locally is a uint8 (ceil(H/16), ceil(W/16)) tile mask.
+ * ------------------------------------------------------------------------ */
+size_t gs_render_geom_bytes(int P, int image_width, int image_height);
+size_t gs_render_binning_bytes(int64_t R);
+size_t gs_render_img_bytes(int image_width, int image_height);
+
+/* Count the tile instances: per-tile counts and offsets go to `geom`; R is
+ * copied to *num_rendered.  Synchronises `stream` (the reference reads R back
+ * with cudaMemcpy at rasterizer_impl.cu:621). */
+int gs_render_forward_count(int P, int image_width, int image_height, const float* means2D,
+                            const int* radii, const uint8_t* compute_locally, void* geom,
+                            int64_t* num_rendered, gs_stream_t stream);
+
+/* Duplicate, sort, range and blend.  Outputs: out_color (3,H,W),
+ * n_render / n_consider / n_contrib int32 (tiles), out_observe int32 (P).
+ * The sorted tile|depth keys and Gaussian ids stay in `binning`, the ranges
+ * and per-pixel state in `img`, for gs_render_backward. */
+int gs_render_forward(int P, int64_t R, int image_width, int image_height, const float* bg,
+                      const float* means2D, const float* depths, const int* radii,
+                      const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
+                      void* geom, void* binning, void* img, float* out_color, int32_t* n_render,
+                      int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe,
+                      gs_stream_t stream);
+
+/* Render backward.  Replaces RenderGaussiansBackwardCUDA
+ * (diff-gaussian-rasterization_r/rasterize_points.cu:363-436; kernel
+ * cuda_rasterizer/backward.cu:324-530).
+ *   dL_dpixels (3,H,W).  Outputs: dL_dmeans2D (row stride dL_dmeans2D_stride,
+ *   2 or 3; the third column, when present, is zero), dL_dmeans2D_abs (P,3),
+ *   dL_dconic_opacity (P,4) = [c00, c01, c11, opacity], dL_dcolors (P,3). */
+int gs_render_backward(int P, int64_t R, int image_width, int image_height, const float* bg,
+                       const float* means2D, const float* conic_opacity, const float* rgb,
+                       const uint8_t* compute_locally, const void* binning, const void* img,
+                       const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
+                       float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
+                       gs_stream_t stream);
+
+/* Views into the opaque buffers, for tests and tools:
+ *   binning: point_list uint32 (R), point_list_keys uint64 (R)
+ *   img    : ranges uint32 (T,2), final_T float (H,W), n_contrib uint32 (H,W),
+ *            n_contrib2loss uint32 (H,W)                                    */
+int gs_render_buffer_views(int64_t R, int image_width, int image_height, void* binning, void* img,
+                           uint32_t** point_list, uint64_t** point_list_keys, uint32_t** ranges,
+                           float** final_T, uint32_t** n_contrib, uint32_t** n_contrib2loss);
+
+/* ------------------------------------------------------------------------ *
+ * distCUDA2 (simple-knn/spatial.cu:15-26, simple_knn.cu:186-221):
+ * out[i] = mean of the squared distances from points[i] to its 3 nearest
+ * other points.  points (P,3), out (P).  Synchronises `stream`.
+ * ------------------------------------------------------------------------ */
+size_t gs_knn_workspace_bytes(int P);
+int gs_knn_meandist3(int P, const float* points, float* out, void* workspace, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * fused-ssim (fused-ssim/ssim.cu:367-441).  Images (B,C,H,W).
+ * Forward writes ssim_map and, when the three dm_* pointers are non-null
+ * (train=True), the partial derivatives dm/dmu1, dm/dsigma1^2, dm/dsigma12.
+ * Backward writes dL_dimg1.
+ * ------------------------------------------------------------------------ */
+int gs_ssim_forward(int B, int C, int H, int W, float C1, float C2, const float* img1,
+                    const float* img2, float* ssim_map, float* dm_dmu1, float* dm_dsigma1_sq,
+                    float* dm_dsigma12, gs_stream_t stream);
+int gs_ssim_backward(int B, int C, int H, int W, float C1, float C2, const float* img1,
+                     const float* img2, const float* dL_dmap, const float* dm_dmu1,
+                     const float* dm_dsigma1_sq, const float* dm_dsigma12, float* dL_dimg1,
+                     gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Diagnostics: evaluate the device exp / log used by the kernels on n inputs
+ * (op 0 = exp, 1 = log), so tests can compare them bit for bit with the CPU.
+ * ------------------------------------------------------------------------ */
+int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,227 @@
+"""HIP path vs CPU oracle, through the C ABI, on seeded synthetic scenes.
+
+Bar: bit-exact for the per-Gaussian preprocess outputs, the tile instance
+lists (sorted ids, keys, ranges) and the forward blend; gradients within
+1e-3 relative L2 of the oracle (float atomics reorder the sums)."""
+import numpy as np
+import pytest
+import torch
+
+from blitzgs_amd import synth, _lib
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+from tests.gpu_helpers import (assert_bitexact, gpu_preprocess, gpu_render_forward, np_, rel_l2, settings_for,
+                               to_dev)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _dev(gpu):
+    _lib.load()
+    yield
+
+
+def _oracle_pre(scene, cam, deg=3):
+    return O.preprocess_fwd(cam, scene["means3D"], scene["scales"], scene["rotations"], scene["sh"],
+                            scene["opacities"], sh_degree=deg)
+
+
+def test_device_math_bitexact():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([np.linspace(-87.5, 0.0, 400_001), rng.uniform(-100, 90, 200_000),
+                        [0.0, -0.0, -87.0, -87.00001, 88.5, 89.0, np.nan, -np.inf]]).astype(np.float32)
+    xt = to_dev(x)
+    for op, ref in ((0, O.vec_expf(x)), (2, O.vec_expf(x))):
+        y = torch.empty_like(xt)
+        _lib.check(_lib.load().gs_diag_math(op, x.size, _lib.ptr(xt), _lib.ptr(y), None), "diag")
+        torch.cuda.synchronize()
+        assert_bitexact(np_(y), ref, f"exp op{op}")
+    xl = np.concatenate([rng.uniform(1.0, 256.0, 300_000), np.exp(rng.uniform(-80, 80, 100_000)),
+                         [0.0, 1.0, -1.0, np.inf, np.nan, 1e-40]]).astype(np.float32)
+    xt = to_dev(xl)
+    y = torch.empty_like(xt)
+    _lib.check(_lib.load().gs_diag_math(1, xl.size, _lib.ptr(xt), _lib.ptr(y), None), "diag")
+    torch.cuda.synchronize()
+    assert_bitexact(np_(y), O.vec_logf(xl), "log")
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_preprocess_forward_bitexact(deg):
+    scene, cam = synth.small_scene(20000, seed=31 + deg, W=320, H=200, extent=2.0, cam_dist=3.0)
+    rs = settings_for(cam, sh_degree=deg)
+    g = gpu_preprocess(scene, rs)
+    o = _oracle_pre(scene, cam, deg)
+    for k in ["means2D", "depths", "radii", "cov3D", "conic_opacity", "rgb"]:
+        assert_bitexact(np_(g[k]), o[k], k)
+    assert_bitexact(np_(g["clamped"]).astype(np.uint8), o["clamped"], "clamped")
+    vis = o["radii"] > 0
+    assert 0 < vis.sum() < len(vis)   # both culled and visible Gaussians covered
+
+
+def test_preprocess_forward_config0_and_edge_inputs():
+    scene, cam = synth.config0()
+    # edge inputs: behind the camera, zero / tiny / >1 opacity, degenerate scale, huge scale
+    scene["means3D"][:4] = [[0, 0, -5.0], [0, 0, -3.9], [0.1, 0.1, 0.0], [0.0, 0.0, 1.0]]
+    scene["opacities"][4:8, 0] = [0.0, 1e-4, 1.0 / 255.0, 1.5]
+    scene["scales"][8] = 0.0
+    scene["scales"][9] = 1e3
+    rs = settings_for(cam)
+    g = gpu_preprocess(scene, rs)
+    o = _oracle_pre(scene, cam)
+    for k in ["means2D", "depths", "radii", "cov3D", "conic_opacity", "rgb"]:
+        assert_bitexact(np_(g[k]), o[k], k)
+
+
+def _check_binning_and_render(cam, pre, bg, cl=None):
+    rs = settings_for(cam, bg=bg)
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    g = gpu_render_forward(rs, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"], cl)
+    ob = O.binning(cam["W"], cam["H"], pre["means2D"], pre["depths"], pre["radii"], cl)
+    assert g["R"] == ob["R"]
+    assert_bitexact(np_(g["point_list"]).view(np.uint32), ob["point_list"], "point_list")
+    assert_bitexact(np_(g["keys"]).view(np.uint64), ob["keys"], "point_list_keys")
+    assert_bitexact(np_(g["ranges"]).view(np.uint32), ob["ranges"], "ranges")
+    orf = O.render_fwd(cam["W"], cam["H"], np.asarray(bg, np.float32), pre["means2D"], pre["conic_opacity"],
+                       pre["rgb"], ob["ranges"], ob["point_list"], cl)
+    assert_bitexact(np_(g["color"]), orf["color"], "color")
+    assert_bitexact(np_(g["final_T"]), orf["final_T"], "final_T")
+    assert_bitexact(np_(g["n_contrib_px"]).view(np.uint32), orf["n_contrib_px"], "n_contrib (pixel)")
+    assert_bitexact(np_(g["n_contrib2loss_px"]).view(np.uint32), orf["n_contrib2loss_px"], "n_contrib2loss")
+    assert_bitexact(np_(g["out_observe"]), orf["out_observe"], "out_observe")
+    assert_bitexact(np_(g["n_render"]), orf["n_render"], "n_render")
+    assert_bitexact(np_(g["n_consider"]), orf["n_consider"], "n_consider")
+    assert_bitexact(np_(g["n_contrib"]), orf["n_contrib"], "n_contrib (tile)")
+    return g, ob, orf
+
+
+def test_binning_and_render_forward_bitexact_config0():
+    scene, cam = synth.config0()
+    pre = _oracle_pre(scene, cam)
+    _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
+
+
+def test_binning_render_ragged_masked_and_ties():
+    scene, cam = synth.small_scene(6000, seed=77, W=250, H=170, extent=1.8, log_mu=-2.0)
+    pre = _oracle_pre(scene, cam)
+    pre["depths"][100:160] = pre["depths"][100]          # depth ties -> ascending id order
+    gx, gy = (250 + 15) // 16, (170 + 15) // 16
+    rng = np.random.default_rng(5)
+    for cl in [None, (rng.random((gy, gx)) < 0.4).astype(np.uint8), np.zeros((gy, gx), np.uint8)]:
+        _check_binning_and_render(cam, pre, (0.2, 0.5, 0.9), cl)
+
+
+def test_binning_large_bucket_and_global_mode():
+    # one tile receiving > 4096 instances (the global-memory sort path) and an
+    # image with more than 16384 local tiles (the global-atomics count path)
+    rng = np.random.default_rng(9)
+    P = 9000
+    W, H = 2304, 2048   # 144 x 128 = 18432 tiles
+    means2D = np.stack([rng.uniform(0, W, P), rng.uniform(0, H, P)], 1).astype(np.float32)
+    means2D[:5000] = rng.uniform(30, 34, (5000, 2))
+    radii = rng.integers(1, 12, P).astype(np.int32)
+    radii[::97] = 0
+    depths = rng.uniform(0.5, 50, P).astype(np.float32)
+    depths[:300] = 2.0
+    conic = np.tile(np.array([[0.05, 0.0, 0.05, 0.5]], np.float32), (P, 1))
+    rgb = rng.random((P, 3)).astype(np.float32)
+    cam = dict(W=W, H=H, tanfovx=1.0, tanfovy=1.0, viewmatrix=np.eye(4, dtype=np.float32),
+               projmatrix=np.eye(4, dtype=np.float32), campos=np.zeros(3, np.float32))
+    pre = dict(means2D=means2D, depths=depths, radii=radii, conic_opacity=conic, rgb=rgb)
+    g, ob, _ = _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
+    assert (np.diff(ob["ranges"], axis=1) > 4096).any()
+
+
+def test_sub_image_share_matches_full_image():
+    # config-3 style: a contiguous tile-row block; its ranges equal the full
+    # render's ranges of those tiles shifted by a constant
+    scene, cam = synth.small_scene(12000, seed=3, W=512, H=400, extent=1.6)
+    pre = _oracle_pre(scene, cam)
+    gx, gy = 32, 25
+    rs = settings_for(cam)
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    full = gpu_render_forward(rs, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"])
+    lo, hi = synth.tile_row_block(gy, 4, 1)
+    cl = np.zeros((gy, gx), np.uint8)
+    cl[lo:hi] = 1
+    sub = gpu_render_forward(rs, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"], cl)
+    fr, sr = np_(full["ranges"]).astype(np.int64), np_(sub["ranges"]).astype(np.int64)
+    t0, t1 = lo * gx, hi * gx
+    off = fr[t0, 0]
+    assert (sr[t0:t1] == fr[t0:t1] - off).all()
+    assert not sr[:t0].any() and not sr[t1:].any()
+    fc, sc = np_(full["color"]), np_(sub["color"])
+    rows = slice(lo * 16, min(hi * 16, cam["H"]))
+    assert_bitexact(sc[:, rows], fc[:, rows], "sub-image colour")
+    assert not sc[:, :lo * 16].any() and not sc[:, hi * 16:].any()
+
+
+def _grad_chain(scene, cam, bg, dLd):
+    pre, bn, rf = O.full_forward(cam, scene, bg=np.asarray(bg, np.float32))
+    rb = O.render_bwd(cam["W"], cam["H"], np.asarray(bg, np.float32), pre["means2D"], pre["conic_opacity"],
+                      pre["rgb"], bn["ranges"], bn["point_list"], rf["final_T"], rf["n_contrib_px"], dLd)
+    pb = O.preprocess_bwd(cam, scene["means3D"], scene["scales"], scene["rotations"], scene["sh"], pre["radii"],
+                          pre["cov3D"], pre["clamped"], rb["dL_dmeans2D"], rb["dL_dconic_opacity"],
+                          rb["dL_dcolors"])
+    return pre, bn, rf, rb, pb
+
+
+@pytest.mark.parametrize("cfg", ["small", "config0"])
+def test_autograd_forward_backward_vs_oracle(cfg):
+    from blitzgs_amd import rasterizer as R
+    if cfg == "small":
+        scene, cam = synth.small_scene(3000, seed=12, W=200, H=150, extent=1.2)
+        bg = (0.3, 0.2, 0.1)
+    else:
+        scene, cam = synth.config0()
+        bg = (0.0, 0.0, 0.0)
+    dLd = scene["dL_dimage"]
+    pre, bn, rf, rb, pb = _grad_chain(scene, cam, bg, dLd)
+    rs = settings_for(cam, bg=bg)
+    params = {k: to_dev(scene[k]).requires_grad_(True) for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+    ras = R.GaussianRasterizer(rs)
+    cuda_args = {"avoid_pixel_all2all": False, "stats_collector": {}}
+    means2D, rgb, conic_opacity, radii, depths = ras.preprocess_gaussians(
+        params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], cuda_args)
+    means2D.retain_grad()
+    means2D_abs = torch.zeros((means2D.shape[0], 3), device="cuda", requires_grad=True) + 0
+    means2D_abs.retain_grad()
+    all_map = torch.zeros((means2D.shape[0], 5), device="cuda")
+    color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth = ras.render_gaussians(
+        means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, None, None, cuda_args)
+    assert_bitexact(np_(color), rf["color"], "color")
+    assert_bitexact(np_(out_observe), rf["out_observe"], "out_observe")
+    assert set(cuda_args["stats_collector"]) >= {"forward_render_time"}
+    (color * to_dev(dLd)).sum().backward()
+    assert "backward_render_time" in cuda_args["stats_collector"]
+    checks = [(means2D.grad, rb["dL_dmeans2D"][:, :2], "dL_dmeans2D"),
+              (means2D_abs.grad, rb["dL_dmeans2D_abs"], "dL_dmeans2D_abs"),
+              (params["means3D"].grad, pb["dL_dmeans3D"], "dL_dmeans3D"),
+              (params["scales"].grad, pb["dL_dscales"], "dL_dscales"),
+              (params["rotations"].grad, pb["dL_drotations"], "dL_drotations"),
+              (params["sh"].grad, pb["dL_dsh"], "dL_dsh"),
+              (params["opacities"].grad, pb["dL_dopacity"], "dL_dopacity")]
+    for got, ref, name in checks:
+        e = rel_l2(np_(got), ref)
+        assert e < 1e-3, (name, e)
+
+
+def test_render_backward_vs_oracle_with_background():
+    scene, cam = synth.small_scene(5000, seed=44, W=300, H=180, extent=1.5, log_mu=-2.2)
+    bg = (0.7, 0.1, 0.4)
+    dLd = scene["dL_dimage"]
+    pre, bn, rf, rb, pb = _grad_chain(scene, cam, bg, dLd)
+    rs = settings_for(cam, bg=bg)
+    from blitzgs_amd import rasterizer as R
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    out = R._render_forward_raw(rs.bg, cam["H"], cam["W"], dev["means2D"], dev["depths"], dev["radii"],
+                                dev["conic_opacity"], dev["rgb"], None)
+    Rn, color, *_rest, geom, binning, img, _ = out
+    g = R._render_backward_raw(rs.bg, Rn, cam["H"], cam["W"], dev["means2D"], dev["conic_opacity"], dev["rgb"],
+                               None, binning, img, to_dev(dLd), m2d_stride=3)
+    dm, dma, dco, dcol, _ = g
+    assert rel_l2(np_(dm), rb["dL_dmeans2D"]) < 1e-3
+    assert not np_(dm)[:, 2].any()
+    assert rel_l2(np_(dma), rb["dL_dmeans2D_abs"]) < 1e-3
+    assert rel_l2(np_(dco), rb["dL_dconic_opacity"]) < 1e-3
+    assert rel_l2(np_(dcol), rb["dL_dcolors"]) < 1e-3

@@ -38,6 +38,9 @@ _SIGS = {
     "gs_ssim_forward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c]),
     "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_diag_math": (_i, [_i, _i, _c, _c, _c]),
+    "gs_timing_enable": (_i, [_i]),
+    "gs_timing_reset": (_i, []),
+    "gs_timing_read": (_i, [_i, C.c_char_p, C.POINTER(C.c_double), C.POINTER(_i)]),
 }
 
 
@@ -85,3 +88,24 @@ def ptr(t):
 def stream_of(device=None):
     import torch
     return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def timing_enable(on=True):
+    load().gs_timing_enable(1 if on else 0)
+
+
+def timing_reset():
+    load().gs_timing_reset()
+
+
+def timing_read(max_entries=64):
+    """{kernel name: (total_ms, launches)} accumulated since the last reset."""
+    names = C.create_string_buffer(64 * max_entries)
+    tot = (C.c_double * max_entries)()
+    cnt = (C.c_int * max_entries)()
+    n = load().gs_timing_read(max_entries, names, tot, cnt)
+    out = {}
+    for i in range(min(n, max_entries)):
+        nm = names.raw[64 * i:64 * i + 64].split(b"\0", 1)[0].decode()
+        out[nm] = (tot[i], cnt[i])
+    return out

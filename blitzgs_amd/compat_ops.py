@@ -1,0 +1,83 @@
+"""The reference extensions' raw operator signatures (their pybind `_C` modules).
+
+diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
+(ext.cpp of each package; C++ signatures in rasterize_points.h):
+  preprocess_gaussians            _f/rasterize_points.cu:834-923
+  preprocess_gaussians_backward   _f/rasterize_points.cu:926-1029
+  render_gaussians                _r/rasterize_points.cu:273-361
+  render_gaussians_backward       _r/rasterize_points.cu:363-436
+Same positional arguments and return tuples; `args` is the reference's
+cuda_args dict (its "stats_collector" entry receives forward_render_time /
+backward_render_time in ms).  The routing helpers of the multi-GPU path
+(get_local2j_ids_bool*, image-tile utilities) are not implemented.
+"""
+import torch
+
+from . import rasterizer as _r
+
+
+class _RS:
+    """Minimal settings record for the raw calls."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def preprocess_gaussians(means3D, scales, rotations, sh, opacity, scale_modifier, viewmatrix, projmatrix, tan_fovx,
+                         tan_fovy, image_height, image_width, degree, campos, prefiltered, debug, args=None):
+    rs = _RS(scale_modifier=scale_modifier, viewmatrix=viewmatrix, projmatrix=projmatrix, tanfovx=tan_fovx,
+             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos)
+    return _r._preprocess_forward_raw(means3D, scales, rotations, sh, opacity, rs)
+
+
+def preprocess_gaussians_backward(radii, cov3D, clamped, means3D, scales, rotations, sh, scale_modifier, viewmatrix,
+                                  projmatrix, tan_fovx, tan_fovy, image_height, image_width, degree, campos,
+                                  dL_dmeans2D, dL_dconic_opacity, dL_dcolors, R, debug, args=None):
+    rs = _RS(scale_modifier=scale_modifier, viewmatrix=viewmatrix, projmatrix=projmatrix, tanfovx=tan_fovx,
+             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos)
+    return _r._preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
+                                       dL_dconic_opacity, dL_dcolors)
+
+
+def render_gaussians(background, image_height, image_width, means2D, depths, radii, conic_opacity, rgb,
+                     compute_locally, viewmatrix, campos, tan_fovx, tan_fovy, all_map, render_geo, debug, args=None):
+    if render_geo:
+        raise NotImplementedError("render_geo=True is not supported")
+    timing = _r._want_timing(args)
+    H, W = int(image_height), int(image_width)
+    (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
+     ms) = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing)
+    if timing:
+        args["stats_collector"]["forward_render_time"] = ms
+    dev = means2D.device
+    out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
+    out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
+    return R, color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth, geom, binning, img
+
+
+def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, all_maps, R, geomBuffer, binningBuffer,
+                              imageBuffer, compute_locally, dL_dout_color, dL_dout_all_map, dL_dout_plane_depth,
+                              means2D, conic_opacity, rgb, render_geo, debug, args=None):
+    if render_geo:
+        raise NotImplementedError("render_geo=True is not supported")
+    H, W = int(dL_dout_color.size(1)), int(dL_dout_color.size(2))
+    timing = _r._want_timing(args)
+    dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _r._render_backward_raw(
+        background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, binningBuffer, imageBuffer,
+        dL_dout_color.contiguous(), 3, timing)
+    if timing:
+        args["stats_collector"]["backward_render_time"] = ms
+    dL_dall_map = torch.zeros((means2D.size(0), 5), device=means2D.device, dtype=torch.float32)
+    return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, dL_dall_map
+
+
+def _not_here(name):
+    def f(*a, **k):
+        raise NotImplementedError(f"{name}: multi-GPU routing / image-tile utilities are not part of this build")
+    f.__name__ = name
+    return f
+
+
+get_local2j_ids_bool = _not_here("get_local2j_ids_bool")
+get_local2j_ids_bool_adjust_mode6 = _not_here("get_local2j_ids_bool_adjust_mode6")
+mark_visible = _not_here("mark_visible")

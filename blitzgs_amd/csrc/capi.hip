@@ -2,6 +2,11 @@
 // device-math diagnostic entry point.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
 
 #include "gs_device.h"
 #include "gs_host.h"
@@ -21,6 +26,109 @@ void set_error(const char* fmt, ...)
 }
 void clear_error() { g_err[0] = 0; }
 }  // namespace gs
+
+// ------------------------------------------------------------ kernel timing
+namespace {
+struct PendingMark {
+    std::string name;
+    hipEvent_t start, stop;
+};
+struct TimingState {
+    std::mutex mu;
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    std::vector<PendingMark> pending;
+    std::vector<std::string> names;
+    std::vector<double> total_ms;
+    std::vector<int> counts;
+};
+TimingState& timing()
+{
+    static TimingState* s = new TimingState();   // lives until process exit
+    return *s;
+}
+hipEvent_t take_event(TimingState& t)
+{
+    if (!t.pool.empty()) {
+        hipEvent_t e = t.pool.back();
+        t.pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+void drain(TimingState& t)
+{
+    for (auto& m : t.pending) {
+        float ms = 0.f;
+        if (m.start && m.stop && hipEventSynchronize(m.stop) == hipSuccess &&
+            hipEventElapsedTime(&ms, m.start, m.stop) == hipSuccess) {
+            size_t k = 0;
+            while (k < t.names.size() && t.names[k] != m.name) k++;
+            if (k == t.names.size()) { t.names.push_back(m.name); t.total_ms.push_back(0.0); t.counts.push_back(0); }
+            t.total_ms[k] += ms;
+            t.counts[k] += 1;
+        }
+        if (m.start) t.pool.push_back(m.start);
+        if (m.stop) t.pool.push_back(m.stop);
+    }
+    t.pending.clear();
+}
+}  // namespace
+
+namespace gs {
+bool timing_on() { return timing().on; }
+void timing_mark_begin(hipStream_t stream, const char* name)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    PendingMark m{name, take_event(t), nullptr};
+    if (m.start) (void)hipEventRecord(m.start, stream);
+    t.pending.push_back(m);
+}
+void timing_mark_end(hipStream_t stream)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    if (t.pending.empty()) return;
+    PendingMark& m = t.pending.back();
+    m.stop = take_event(t);
+    if (m.stop) (void)hipEventRecord(m.stop, stream);
+}
+}  // namespace gs
+
+extern "C" int gs_timing_enable(int on)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    t.on = on != 0;
+    return GS_OK;
+}
+
+extern "C" int gs_timing_reset(void)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    drain(t);
+    t.names.clear(); t.total_ms.clear(); t.counts.clear();
+    return GS_OK;
+}
+
+extern "C" int gs_timing_read(int max_entries, char* names, double* total_ms, int* counts)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    drain(t);
+    const int n = (int)t.names.size();
+    for (int i = 0; i < n && i < max_entries; i++) {
+        strncpy(names + 64 * i, t.names[i].c_str(), 63);
+        names[64 * i + 63] = 0;
+        total_ms[i] = t.total_ms[i];
+        counts[i] = t.counts[i];
+    }
+    return n;
+}
 
 extern "C" int gs_version(void) { return 100; }
 extern "C" const char* gs_last_error(void) { return g_err; }

@@ -9,7 +9,22 @@
 namespace gs {
 void set_error(const char* fmt, ...);
 void clear_error();
+
+// Optional per-kernel timing (gs_timing_enable): when on, every launch made
+// through GS_TIMED is bracketed by HIP events on its stream and the elapsed
+// times are accumulated per kernel name by gs_timing_read.
+bool timing_on();
+void timing_mark_begin(hipStream_t stream, const char* name);
+void timing_mark_end(hipStream_t stream);
 }  // namespace gs
+
+#define GS_TIMED(name, stream, launch)                                                 \
+    do {                                                                               \
+        const bool gs_t_ = gs::timing_on();                                            \
+        if (gs_t_) gs::timing_mark_begin(stream, name);                                \
+        launch;                                                                        \
+        if (gs_t_) gs::timing_mark_end(stream);                                        \
+    } while (0)
 
 #define GS_OK 0
 #define GS_ERR_ARG -1

@@ -554,10 +554,10 @@ extern "C" int gs_preprocess_forward(
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
 #define GS_PRE_FWD(DEG)                                                                             \
-    hipLaunchKernelGGL(preprocess_fwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,        \
+    GS_TIMED("preprocess_fwd_kernel", stream, hipLaunchKernelGGL(preprocess_fwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,        \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
                        campos, means3D, scales, rotations, sh, sh_vec16, opacities, means2D, depths, radii, \
-                       cov3D, conic_opacity, rgb, clamped)
+                       cov3D, conic_opacity, rgb, clamped))
     switch (D) {
         case 0: GS_PRE_FWD(0); break;
         case 1: GS_PRE_FWD(1); break;
@@ -592,11 +592,11 @@ extern "C" int gs_preprocess_backward(
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
 #define GS_PRE_BWD(DEG)                                                                                  \
-    hipLaunchKernelGGL(preprocess_bwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,             \
+    GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL(preprocess_bwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,             \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
                        campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
                        dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
-                       dL_drotations, dL_dsh, dL_dopacity)
+                       dL_drotations, dL_dsh, dL_dopacity))
     switch (D) {
         case 0: GS_PRE_BWD(0); break;
         case 1: GS_PRE_BWD(1); break;

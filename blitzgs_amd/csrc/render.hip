@@ -692,18 +692,18 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
     uint32_t* tile_start = at<uint32_t>(geom, g.tile_start);
     uint32_t* cursor = at<uint32_t>(geom, g.cursor);
 
-    hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, compute_locally, loc_map,
-                       tile_of_local, tile_count, meta);
+    GS_TIMED("localmap_kernel", stream, hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, compute_locally, loc_map,
+                       tile_of_local, tile_count, meta));
     GS_LAUNCH_CHECK("localmap_kernel");
     if (P > 0) {
-        hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
-                           reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count);
+        GS_TIMED("count_kernel", stream, hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
+                           reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count));
         GS_LAUNCH_CHECK("count_kernel");
-        hipLaunchKernelGGL(colscan_kernel, dim3(gs_div_up((size_t)(g.T < LDS_TILES ? g.T : LDS_TILES), 256)),
-                           dim3(256), 0, stream, g.NC, meta, hist, tile_count);
+        GS_TIMED("colscan_kernel", stream, hipLaunchKernelGGL(colscan_kernel, dim3(gs_div_up((size_t)(g.T < LDS_TILES ? g.T : LDS_TILES), 256)),
+                           dim3(256), 0, stream, g.NC, meta, hist, tile_count));
         GS_LAUNCH_CHECK("colscan_kernel");
     }
-    hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor);
+    GS_TIMED("tilescan_kernel", stream, hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor));
     GS_LAUNCH_CHECK("tilescan_kernel");
     uint32_t hR[2] = {0, 0};
     GS_HIP(hipMemcpyAsync(hR, meta + 2, sizeof(hR), hipMemcpyDeviceToHost, stream));
@@ -744,30 +744,30 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
     uint64_t* keys = at<uint64_t>(binning, bl.keys);
 
     const unsigned T = (unsigned)g.T;
-    hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
-                       tile_start, ranges, n_render, n_consider, n_contrib);
+    GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
+                       tile_start, ranges, n_render, n_consider, n_contrib));
     GS_LAUNCH_CHECK("ranges_kernel");
     if (P > 0) {
-        hipLaunchKernelGGL(zero_i32_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P, out_observe);
+        GS_TIMED("zero_i32_kernel", stream, hipLaunchKernelGGL(zero_i32_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P, out_observe));
         GS_LAUNCH_CHECK("zero_i32_kernel");
     }
     if (R > 0) {
-        hipLaunchKernelGGL(scatter_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
+        GS_TIMED("scatter_kernel", stream, hipLaunchKernelGGL(scatter_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
                            reinterpret_cast<const float2*>(means2D), depths, radii, loc_map, meta, hist,
-                           tile_start, cursor, sortkey);
+                           tile_start, cursor, sortkey));
         GS_LAUNCH_CHECK("scatter_kernel");
-        hipLaunchKernelGGL(tilesort_kernel, dim3(T), dim3(SORT_THREADS), 0, stream, meta, tile_of_local, tile_count,
-                           tile_start, sortkey, point_list, keys);
+        GS_TIMED("tilesort_kernel", stream, hipLaunchKernelGGL(tilesort_kernel, dim3(T), dim3(SORT_THREADS), 0, stream, meta, tile_of_local, tile_count,
+                           tile_start, sortkey, point_list, keys));
         GS_LAUNCH_CHECK("tilesort_kernel");
-        hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta, tile_of_local,
-                           tile_count, tile_start, sortkey, point_list, keys);
+        GS_TIMED("tilesort_big_kernel", stream, hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta, tile_of_local,
+                           tile_count, tile_start, sortkey, point_list, keys));
         GS_LAUNCH_CHECK("tilesort_big_kernel");
     }
     const unsigned nblk = ((T + 7u) / 8u) * 32u;
-    hipLaunchKernelGGL(render_fwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T, ranges, point_list,
+    GS_TIMED("render_fwd_kernel", stream, hipLaunchKernelGGL(render_fwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T, ranges, point_list,
                        reinterpret_cast<const float2*>(means2D), reinterpret_cast<const float4*>(conic_opacity), rgb,
                        compute_locally, bg, out_color, at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib),
-                       at<uint32_t>(img, il.n_contrib2loss), out_observe, n_consider, n_contrib);
+                       at<uint32_t>(img, il.n_contrib2loss), out_observe, n_consider, n_contrib));
     GS_LAUNCH_CHECK("render_fwd_kernel");
     (void)gy;
     return GS_OK;
@@ -790,17 +790,17 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
     const BinLayout bl = bin_layout(R);
     const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
     const unsigned T = gx * gy;
-    hipLaunchKernelGGL(zero_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
+    GS_TIMED("zero_grads_kernel", stream, hipLaunchKernelGGL(zero_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
                        dL_dmeans2D_stride, dL_dmeans2D, dL_dmeans2D_abs, reinterpret_cast<float4*>(dL_dconic_opacity),
-                       dL_dcolors);
+                       dL_dcolors));
     GS_LAUNCH_CHECK("zero_grads_kernel");
     if (R == 0) return GS_OK;
     const unsigned nblk = ((T + 7u) / 8u) * 32u;
-    hipLaunchKernelGGL(render_bwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T,
+    GS_TIMED("render_bwd_kernel", stream, hipLaunchKernelGGL(render_bwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T,
                        at<uint2>(img, il.ranges), at<uint32_t>(binning, bl.point_list),
                        reinterpret_cast<const float2*>(means2D), reinterpret_cast<const float4*>(conic_opacity), rgb,
                        compute_locally, bg, at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
-                       dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors);
+                       dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors));
     GS_LAUNCH_CHECK("render_bwd_kernel");
     return GS_OK;
 }

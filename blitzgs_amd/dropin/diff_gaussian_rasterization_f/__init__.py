@@ -1,0 +1,19 @@
+"""Drop-in for BlitzGS's diff_gaussian_rasterization_f split training API
+(submodule/diff-gaussian-rasterization_f/diff_gaussian_rasterization_f/__init__.py),
+backed by the gfx950 HIP library.  Render ops dispatch to the same library the
+_r drop-in uses (the reference routes them to _r, __init__.py:24-46)."""
+from blitzgs_amd import compat_ops as _C
+from blitzgs_amd.rasterizer import (GaussianRasterizationSettings, GaussianRasterizer, _PreprocessGaussians,
+                                    _RenderGaussians, preprocess_gaussians, render_gaussians)
+
+_SPLIT_C = _C
+
+
+def _get_split_op_backend(op_name):
+    if hasattr(_C, op_name):
+        return _C
+    raise AttributeError(f"No backend provides split op '{op_name}'")
+
+
+__all__ = ["GaussianRasterizationSettings", "GaussianRasterizer", "preprocess_gaussians", "render_gaussians",
+           "_get_split_op_backend", "_C"]

@@ -7,9 +7,11 @@ scene/cameras.py:111-133): ``viewmatrix`` is getWorld2View2(R, T) transposed,
 columns are the camera's x (right), y (down) and z (forward) axes in world
 coordinates, T = -R^T C.
 
-Scenes are drawn with numpy ``Generator(PCG64(seed))`` in float64 and cast to
-float32, in the fixed order: means -> log-scales -> quaternions -> opacity
-logits -> SH DC -> SH rest -> dL/dimage.  Parameters are returned already
+Scenes are drawn with numpy ``Generator(PCG64(seed))`` in the fixed order:
+means (float64) -> log-scales -> quaternions -> opacity logits (float64) ->
+SH (one (P,16,3) float32 standard-normal draw; coefficient 0 is scaled by the
+DC standard deviation, the other 15 by the higher-band one) -> dL/dimage
+(float32).  Parameters are returned already
 activated, as the reference's GaussianModel hands them to the rasterizer
 (scene/gaussian_model.py:53-58): scales = exp(log-scale), rotations =
 normalised quaternions (r, x, y, z), opacities = sigmoid(logit) with shape
@@ -91,12 +93,12 @@ def _finish(rng, means, log_mu, log_sd, op_mu, op_sd, P, dc_sd=0.5, rest_sd=0.05
     log_scales = rng.normal(log_mu, log_sd, size=(P, 3))
     quats = _quats(rng, P)
     op_logit = rng.normal(op_mu, op_sd, size=(P, 1))
-    dc = rng.normal(0.0, dc_sd, size=(P, 1, 3))
-    rest = rng.normal(0.0, rest_sd, size=(P, K - 1, 3))
-    sh = np.concatenate([dc, rest], axis=1)
+    sh = rng.standard_normal((P, K, 3), dtype=np.float32)
+    sh[:, 0, :] *= np.float32(dc_sd)
+    sh[:, 1:, :] *= np.float32(rest_sd)
     return dict(means3D=means.astype(np.float32), scales=np.exp(log_scales).astype(np.float32),
                 rotations=quats.astype(np.float32), opacities=_sigmoid(op_logit).astype(np.float32),
-                sh=sh.astype(np.float32))
+                sh=sh)
 
 
 def _ground_plane_means(rng, P):
@@ -158,7 +160,7 @@ def config2(P=6_000_000, W=1600, H=1066, seed=2):
     means = _ground_plane_means(rng, P)
     scene = _finish(rng, means, -1.5, 0.8, 0.5, 1.5, P)
     cam = aerial_camera(W, H)
-    scene["dL_dimage"] = rng.standard_normal((3, H, W)).astype(np.float32)
+    scene["dL_dimage"] = rng.standard_normal((3, H, W), dtype=np.float32)
     return scene, cam
 
 

@@ -163,6 +163,18 @@ int gs_ssim_backward(int B, int C, int H, int W, float C1, float C2, const float
  * ------------------------------------------------------------------------ */
 int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
 
+/* ------------------------------------------------------------------------ *
+ * Per-kernel timing (the counterpart of the reference's MyTimerOnGPU,
+ * diff-gaussian-rasterization_r/cuda_rasterizer/timers.cu:11-79): when
+ * enabled, every kernel launch is bracketed by HIP events on its stream.
+ * gs_timing_read synchronises on the recorded events and returns, per kernel
+ * name (64-byte slots in `names`), the summed milliseconds and launch count;
+ * the return value is the number of distinct kernels.
+ * ------------------------------------------------------------------------ */
+int gs_timing_enable(int on);
+int gs_timing_reset(void);
+int gs_timing_read(int max_entries, char* names, double* total_ms, int* counts);
+
 #ifdef __cplusplus
 }
 #endif

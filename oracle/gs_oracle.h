@@ -101,6 +101,8 @@ void o_ssim_bwd(int B, int C, int H, int W, float C1, float C2,
                 const float* dm_dmu1, const float* dm_dsigma1_sq, const float* dm_dsigma12,
                 float* dL_dimg1);
 
+void o_ssim_window(float* w);
+
 /* Scalar math used by the oracle, exported so tests can pin it. */
 void o_vec_expf(int n, const float* x, float* y);
 void o_vec_logf(int n, const float* x, float* y);

@@ -129,14 +129,21 @@ void o_knn_meandist3(int P, const float* pts, float* out)
 static float g_win[11];
 static int g_win_init = 0;
 
-/* normalised 11-tap Gaussian, sigma 1.5, computed in double then rounded */
+/* The normalised 11-tap Gaussian (sigma 1.5) with the reference's float
+ * values (ssim.cu:8-18); tests check each is within 1 ulp of
+ * exp(-x^2/4.5)/sum. */
 static void ssim_window(void)
 {
     if (g_win_init) return;
-    double w[11], s = 0;
-    for (int i = 0; i < 11; i++) { const double x = i - 5; w[i] = exp(-(x * x) / (2.0 * 1.5 * 1.5)); s += w[i]; }
-    for (int i = 0; i < 11; i++) g_win[i] = (float)(w[i] / s);
+    static const uint32_t h[6] = { 0x3a86cab6u, 0x3bf8ff01u, 0x3d13758cu, 0x3ddff87fu, 0x3e5a1e1fu, 0x3e8832b0u };
+    for (int i = 0; i < 6; i++) { g_win[i] = o_u2f(h[i]); g_win[10 - i] = o_u2f(h[i]); }
     g_win_init = 1;
+}
+
+void o_ssim_window(float* w)
+{
+    ssim_window();
+    for (int i = 0; i < 11; i++) w[i] = g_win[i];
 }
 
 /* same-size zero-padded separable blur of one plane: horizontal pass on the

@@ -37,8 +37,8 @@ def stage_bytes(P, P_vis, R, npx, T):
     }
 
 
-BINNING_KERNELS = ("localmap_kernel", "count_kernel", "colscan_kernel", "tilescan_kernel", "ranges_kernel",
-                   "scatter_kernel", "tilesort_kernel", "tilesort_big_kernel")
+BINNING_KERNELS = ("localmap_kernel", "count_kernel", "tilescan_kernel", "ranges_kernel", "scatter_kernel",
+                   "tilesort_kernel_s", "tilesort_kernel_m", "tilesort_kernel_l", "tilesort_big_kernel")
 
 
 def parse():

@@ -134,6 +134,17 @@ extern "C" int gs_version(void) { return 100; }
 extern "C" const char* gs_last_error(void) { return g_err; }
 
 namespace {
+// op 3: x holds 12 x 64 values ([value][lane]); y[k] = sum over lanes of value k
+__global__ void diag_sum12_kernel(const float* __restrict__ x, float* __restrict__ y)
+{
+    float v[12];
+#pragma unroll
+    for (int k = 0; k < 12; k++) v[k] = x[k * 64 + threadIdx.x];
+    const float t = gs::wave_sum12(v);
+    const int k = gs::wave_sum12_index((int)threadIdx.x);
+    if (k >= 0) y[k] = t;
+}
+
 __global__ void diag_math_kernel(int op, int n, const float* __restrict__ x, float* __restrict__ y)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -150,8 +161,14 @@ __global__ void diag_math_kernel(int op, int n, const float* __restrict__ x, flo
 extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t stream)
 {
     gs::clear_error();
-    GS_REQUIRE(op >= 0 && op <= 2, "op must be 0 (exp), 1 (log) or 2 (blend exp)");
+    GS_REQUIRE(op >= 0 && op <= 3, "op must be 0 (exp), 1 (log), 2 (blend exp) or 3 (wave sum of 12 values)");
     GS_REQUIRE(n >= 0, "n must be >= 0");
+    if (op == 3) {
+        GS_REQUIRE(n == 12 * 64, "op 3 takes 12 x 64 inputs");
+        hipLaunchKernelGGL(diag_sum12_kernel, dim3(1), dim3(64), 0, stream, x, y);
+        GS_LAUNCH_CHECK("diag_sum12_kernel");
+        return GS_OK;
+    }
     if (n == 0) return GS_OK;
     hipLaunchKernelGGL(diag_math_kernel, dim3(gs_div_up((size_t)n, 256)), dim3(256), 0, stream, op, n, x, y);
     GS_LAUNCH_CHECK("diag_math_kernel");

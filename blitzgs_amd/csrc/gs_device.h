@@ -115,11 +115,60 @@ __device__ __forceinline__ float power_of(float ha, float nb, float hc, float dx
     return __builtin_fmaf(ha * dx, dx, __builtin_fmaf(hc * dy, dy, (nb * dx) * dy));
 }
 
+// Conservative test: can a Gaussian (mean mx,my; conic a,b,c; opacity o)
+// reach alpha >= 1/255 at any pixel centre of the rectangle [x0,x1]x[y0,y1]?
+// The maximum of the concave falloff exponent over the rectangle is found in
+// double precision (the convex quadratic form's minimum lies at the clamped
+// stationary point of one of the four edges when the mean is outside); the
+// test keeps a margin of 1e-3 + 1e-6 * M, where M bounds the magnitude of the
+// fp32 terms of the per-pixel exponent, far above the fp32 rounding of that
+// exponent (a few ulp of M) and of exp.  A false answer therefore implies that
+// the exact per-pixel fp32 evaluation skips the Gaussian at every pixel of
+// the rectangle, so culling with it leaves the blend's results unchanged.
+// Non-finite inputs and non-positive-definite conics are always kept.
+__device__ __forceinline__ bool may_touch(float mx, float my, float ca, float cb, float cc, float o, float x0,
+                                          float y0, float x1, float y1)
+{
+    if (o != o) return true;
+    if (o < 1.0f / 255.0f) return false;           // alpha = min(.99, o*G) <= o with G <= 1
+    if (!(__builtin_isfinite(mx) && __builtin_isfinite(my) && __builtin_isfinite(o))) return true;
+    const double a = ca, b = cb, c = cc;
+    if (!(a > 0.0 && c > 0.0 && a * c - b * b > 0.0)) return true;
+    const double dxl = (double)mx - (double)x1, dxh = (double)mx - (double)x0;
+    const double dyl = (double)my - (double)y1, dyh = (double)my - (double)y0;
+    if (dxl <= 0.0 && dxh >= 0.0 && dyl <= 0.0 && dyh >= 0.0) return true;
+    double best = __builtin_huge_val();
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const double dx = e ? dxh : dxl;
+        const double dy = __builtin_fmin(__builtin_fmax(-b * dx / c, dyl), dyh);
+        best = __builtin_fmin(best, a * dx * dx + 2.0 * b * dx * dy + c * dy * dy);
+    }
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const double dy = e ? dyh : dyl;
+        const double dx = __builtin_fmin(__builtin_fmax(-b * dy / a, dxl), dxh);
+        best = __builtin_fmin(best, a * dx * dx + 2.0 * b * dx * dy + c * dy * dy);
+    }
+    const double DX = __builtin_fmax(__builtin_fabs(dxl), __builtin_fabs(dxh));
+    const double DY = __builtin_fmax(__builtin_fabs(dyl), __builtin_fabs(dyh));
+    const double M = 0.5 * (a * DX * DX + c * DY * DY) + __builtin_fabs(b) * DX * DY;
+    const double margin = 1e-3 + 1e-6 * M;
+    const double thresh = -::log(255.0 * (double)o);
+    return -0.5 * best + margin >= thresh;
+}
+
 // ---- wave64 helpers -------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// number of set bits of m below this lane
+__device__ __forceinline__ int rank_below(uint64_t m)
+{
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v)
@@ -145,6 +194,51 @@ __device__ __forceinline__ float bcast63(float v) { return __int_as_float(__buil
 // Sum over the 64 lanes, returned (uniform) in every lane.  Must be called
 // with all 64 lanes active.
 __device__ __forceinline__ float wave_sum(float v) { return bcast63(wave_sum_to_lane63(v)); }
+
+// Twelve per-lane values summed over the wave at once (gfx950 lane swaps):
+//   level 1  v_permlane32_swap pairs (v0,v1),...: one register holds 32-lane
+//            partials of v[2i] in lanes 0-31 and of v[2i+1] in lanes 32-63;
+//   level 2  v_permlane16_swap pairs of those: each 16-lane row of a register
+//            holds 16 partials of one value (rows map to values 0,2,1,3);
+//   level 3  DPP row_shr 1,2,4,8 inside each row: lane 15 of the row has the
+//            total; the second and third registers are shifted down one and
+//            two lanes (row_shl) so one register carries all twelve totals.
+// 34 VALU operations instead of 12 separate full-wave reductions.  Lane L
+// returns the total of value wave_sum12_index(L) (-1: nothing).  All lanes
+// must be active.
+__device__ __forceinline__ float wave_sum12(const float (&v)[12])
+{
+    float s[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * i]), __float_as_uint(v[2 * i + 1]),
+                                                        false, false);
+        s[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    float t[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[2 * j]), __float_as_uint(s[2 * j + 1]),
+                                                        false, false);
+        float x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        x = x + dpp_f<0x111>(x);      // row_shr:1
+        x = x + dpp_f<0x112>(x);      // row_shr:2
+        x = x + dpp_f<0x114>(x);      // row_shr:4
+        x = x + dpp_f<0x118>(x);      // row_shr:8
+        t[j] = x;
+    }
+    const float t1 = dpp_f<0x101>(t[1]);   // row_shl:1 -> lane 14 of each row
+    const float t2 = dpp_f<0x102>(t[2]);   // row_shl:2 -> lane 13
+    const int sl = lane_id() & 15;
+    return sl == 15 ? t[0] : (sl == 14 ? t1 : t2);
+}
+
+__device__ __forceinline__ int wave_sum12_index(int lane)
+{
+    const int q = lane >> 4, sl = lane & 15;
+    const int m = q == 0 ? 0 : (q == 1 ? 2 : (q == 2 ? 1 : 3));
+    return sl == 15 ? m : (sl == 14 ? 4 + m : (sl == 13 ? 8 + m : -1));
+}
 
 __device__ __forceinline__ int wave_sum_i(int v)
 {

@@ -346,44 +346,24 @@ __device__ __forceinline__ void sh_backward(float x, float y, float z, const flo
     }
 }
 
-template <int DEG>
-__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
-    int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
+template <int DEG, bool STAGED>
+__device__ __forceinline__ void preprocess_bwd_one(
+    int idx, int K, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
     const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
-    const float* __restrict__ sh, int sh_vec16, const int* __restrict__ radii, const float* __restrict__ cov3D,
+    const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
     const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
-    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity)
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row)
 {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= P) return;
     constexpr int NC = (DEG + 1) * (DEG + 1);
     const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
     dL_dopacity[idx] = gco.w;
     float* gsh_out = dL_dsh + (size_t)idx * K * 3;
     const bool vec16 = sh_vec16 != 0;
-
-    if (!(radii[idx] > 0)) {
-        reinterpret_cast<float*>(dL_dmeans3D)[3 * idx + 0] = 0.f;
-        dL_dmeans3D[3 * idx + 1] = 0.f;
-        dL_dmeans3D[3 * idx + 2] = 0.f;
-        dL_dscales[3 * idx + 0] = 0.f;
-        dL_dscales[3 * idx + 1] = 0.f;
-        dL_dscales[3 * idx + 2] = 0.f;
-        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (vec16) {
-            float4* o4 = reinterpret_cast<float4*>(gsh_out);
-            for (int i = 0; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-            for (int i = 0; i < 3 * K; i++) gsh_out[i] = 0.f;
-        }
-        return;
-    }
     Cam cam;
     load_cam(cam, view, proj, campos);
-    (void)W; (void)H;
     const float mx = means3D[3 * idx], my = means3D[3 * idx + 1], mz = means3D[3 * idx + 2];
     const float* V = cam.v;
     const float* PM = cam.p;
@@ -475,7 +455,10 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         dnormvdv3(dir_orig, dL_ddir, dm);
         gm[0] += dm[0]; gm[1] += dm[1]; gm[2] += dm[2];
         // dL/dsh: the first NC coefficients, zeros after
-        if (vec16) {
+        if (STAGED) {
+#pragma unroll
+            for (int i = 0; i < 48; i++) s_row[i] = i < 3 * NC ? gsh[i] : 0.f;
+        } else if (vec16) {
             float4* o4 = reinterpret_cast<float4*>(gsh_out);
 #pragma unroll
             for (int i = 0; i < (3 * NC + 3) / 4; i++) {
@@ -528,6 +511,68 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         const float q2 = 2 * x * (G[1][0] + G[0][1]) + 2 * r * (G[2][0] - G[0][2]) + 2 * z * (G[1][2] + G[2][1]) - 4 * y * (G[2][2] + G[0][0]);
         const float q3 = 2 * r * (G[0][1] - G[1][0]) + 2 * x * (G[2][0] + G[0][2]) + 2 * y * (G[1][2] + G[2][1]) - 4 * z * (G[1][1] + G[0][0]);
         reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(q0, q1, q2, q3);
+    }
+}
+
+// Rows of dL/dsh are staged in LDS (pitch 49 floats: conflict-free column
+// writes) and copied out with fully coalesced 16-byte stores when K == 16.
+constexpr int SH_PITCH = 49;
+
+template <int DEG, bool STAGED>
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
+    int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
+    const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
+    const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
+    const float* __restrict__ sh, int sh_vec16, const int* __restrict__ radii, const float* __restrict__ cov3D,
+    const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
+    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
+    float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity)
+{
+    __shared__ float s_sh[STAGED ? 256 * SH_PITCH : 1];
+    __shared__ uint8_t s_vis[256];
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool in = idx < P;
+    const bool vis = in && radii[idx] > 0;
+    if (STAGED) s_vis[threadIdx.x] = vis ? 1 : 0;
+    if (in && !vis) {
+        dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
+        dL_dmeans3D[3 * idx + 0] = 0.f;
+        dL_dmeans3D[3 * idx + 1] = 0.f;
+        dL_dmeans3D[3 * idx + 2] = 0.f;
+        dL_dscales[3 * idx + 0] = 0.f;
+        dL_dscales[3 * idx + 1] = 0.f;
+        dL_dscales[3 * idx + 2] = 0.f;
+        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!STAGED) {
+            float* gsh_out = dL_dsh + (size_t)idx * K * 3;
+            if (sh_vec16) {
+                float4* o4 = reinterpret_cast<float4*>(gsh_out);
+                for (int i = 0; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                for (int i = 0; i < 3 * K; i++) gsh_out[i] = 0.f;
+            }
+        }
+    }
+    if (vis) preprocess_bwd_one<DEG, STAGED>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, means3D,
+                                              scales, rotations, sh, sh_vec16, cov3D, clamped, dL_dmeans2D,
+                                              m2d_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,
+                                              dL_drotations, dL_dsh, dL_dopacity, s_sh + threadIdx.x * SH_PITCH);
+    if (STAGED) {
+        // coalesced copy-out of this block's rows [blockIdx*256, +nrows) x 48 floats
+        __syncthreads();
+        const int row0 = blockIdx.x * 256;
+        const int nrows = min(256, P - row0);
+        float4* dst = reinterpret_cast<float4*>(dL_dsh + (size_t)row0 * 48);
+        for (int c = threadIdx.x; c < nrows * 12; c += 256) {
+            const int r = c / 12, col = (c - r * 12) * 4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s_vis[r]) {
+                const float* src = s_sh + r * SH_PITCH + col;
+                v = make_float4(src[0], src[1], src[2], src[3]);
+            }
+            dst[c] = v;
+        }
     }
 }
 
@@ -588,11 +633,17 @@ extern "C" int gs_preprocess_backward(
                ((uintptr_t)dL_drotations & 15) == 0,
                "rotations, dL_dconic_opacity and dL_drotations must be 16-byte aligned");
     const int sh_vec16 = ((K & 3) == 0 && ((uintptr_t)sh & 15) == 0 && ((uintptr_t)dL_dsh & 15) == 0) ? 1 : 0;
+    const bool staged = K == 16 && ((uintptr_t)dL_dsh & 15) == 0;
     const float fy = (float)image_height / (2.0f * tanfovy);
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
 #define GS_PRE_BWD(DEG)                                                                                  \
-    GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL(preprocess_bwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,             \
+    if (staged) GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, true>), grid, block, 0, stream, P, K, image_width,             \
+                       image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
+                       campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
+                       dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
+                       dL_drotations, dL_dsh, dL_dopacity));                                               \
+    else GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false>), grid, block, 0, stream, P, K, image_width,             \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
                        campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
                        dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \

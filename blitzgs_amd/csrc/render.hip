@@ -15,17 +15,18 @@
 // a 64-bit (tile | depth) key in Gaussian order and radix-sorts all R pairs
 // globally (about six passes over 12 bytes per instance).  Here the tiles are
 // bucketed first and each bucket is sorted on chip:
-//   1. count   : each block takes a chunk of Gaussians and histograms their
-//                tile instances in LDS (one counter per local tile), then
-//                writes its histogram row.
-//   2. scan    : a column scan over the chunk rows gives each block a private
-//                write cursor per tile; a scan over tiles gives tile offsets
-//                (these are the reference's ranges).
+//   1. count   : each block takes a chunk of Gaussians, expands their tile
+//                instances wave-cooperatively (one instance per lane per
+//                round, whatever the rect sizes) and histograms them in LDS
+//                (one counter per local tile); it then reserves its slice of
+//                every tile bucket with one global atomic per non-empty tile.
+//   2. scan    : a scan over the tile totals gives the tile offsets (these
+//                are the reference's ranges) and R.
 //   3. scatter : each block re-walks its chunk and appends (depth bits, id)
-//                to its cursors (LDS atomics only).
+//                to its reserved slices (LDS cursors).
 //   4. sort    : one block per tile sorts its bucket by (depth bits, id) in
-//                LDS (bitonic) and writes the sorted ids and the
-//                (tile << 32 | depth bits) keys.
+//                LDS (bitonic, three size classes) and writes the sorted ids
+//                and the (tile << 32 | depth bits) keys.
 // Sorting each bucket by (depth bits, Gaussian id) yields exactly the order
 // of a stable sort of the reference's duplicated keys, so the sorted arrays
 // and the ranges are bit-identical to the reference algorithm's.
@@ -48,8 +49,9 @@ namespace {
 constexpr int LDS_TILES = 16384;     // local tiles histogrammed in LDS (64 KB)
 constexpr int BIN_THREADS = 512;
 constexpr int MAX_CHUNKS = 512;
-constexpr int SORT_CAP = 4096;       // bucket size sorted entirely in LDS
-constexpr int SORT_THREADS = 512;
+constexpr int SORT_CAP_S = 2048;     // bucket size classes sorted entirely in LDS
+constexpr int SORT_CAP_M = 4096;
+constexpr int SORT_CAP_L = 8192;
 constexpr int BIG_SORT_THREADS = 1024;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -174,6 +176,75 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, const uint8_t* __
 
 // ------------------------------------------------------------- counting
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(v, off, 64);
+        if (lane >= off) v += y;
+    }
+    return v;
+}
+
+// Wave-cooperative instance expansion.  Each lane holds one Gaussian with
+// `cnt` tile instances (its w-wide rect starting at (x0, y0)); the wave walks
+// the concatenated instance list 64 at a time, so every lane handles one
+// instance per round however unevenly the rect sizes are spread.
+struct Expansion {
+    int incl, total;
+};
+
+__device__ __forceinline__ Expansion expansion_begin(int cnt)
+{
+    Expansion e;
+    e.incl = wave_incl_scan(cnt);
+    e.total = __shfl(e.incl, 63, 64);
+    return e;
+}
+
+// Owner lane and tile of instance k.  All 64 lanes must call this (it
+// shuffles); the result is meaningful when k < total.
+__device__ __forceinline__ void expansion_at(const Expansion& e, int cnt, unsigned x0, unsigned y0, unsigned w, int k,
+                                             int& owner, unsigned& tx, unsigned& ty)
+{
+    int lo = 0;
+#pragma unroll
+    for (int step = 32; step > 0; step >>= 1) {
+        const int probe = __shfl(e.incl, lo + step - 1, 64);
+        if (probe <= k) lo += step;
+    }
+    owner = lo < 64 ? lo : 63;
+    const int o_excl = __shfl(e.incl - cnt, owner, 64);
+    const unsigned ox0 = (unsigned)__shfl((int)x0, owner, 64);
+    const unsigned oy0 = (unsigned)__shfl((int)y0, owner, 64);
+    const unsigned ow = (unsigned)__shfl((int)w, owner, 64);
+    const unsigned local = (unsigned)(k - o_excl);
+    const unsigned q = ow ? local / ow : 0u;
+    tx = ox0 + (local - q * ow);
+    ty = oy0 + q;
+}
+
+// tile rect of Gaussian i (binning rule); returns its tile count
+__device__ __forceinline__ int rect_of(int i, int i1, const float2* __restrict__ means2D, const int* __restrict__ radii,
+                                       unsigned gx, unsigned gy, unsigned& x0, unsigned& y0, unsigned& w)
+{
+    x0 = y0 = w = 0;
+    if (i >= i1) return 0;
+    const int r = radii[i];
+    if (r <= 0) return 0;
+    const float2 p = means2D[i];
+    unsigned x1, y1;
+    gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
+    w = x1 - x0;
+    return (int)(w * (y1 - y0));
+}
+
+// Per chunk of Gaussians: histogram of its tile instances in LDS; the chunk
+// then reserves its slice of every tile's bucket with one atomic per
+// non-empty tile and keeps the returned base in its histogram row.  With more
+// local tiles than LDS_TILES, instances are counted with global atomics.
 __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     int P, int CH, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const int* __restrict__ radii,
     const int* __restrict__ loc_map, const uint32_t* __restrict__ meta, uint32_t* __restrict__ hist,
@@ -182,51 +253,41 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     __shared__ uint32_t s_hist[LDS_TILES];
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
+    const bool all_local = TL == (int)(gx * gy);
     const int c = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lds) {
         for (int l = threadIdx.x; l < TL; l += BIN_THREADS) s_hist[l] = 0;
         __syncthreads();
     }
     const int i0 = c * CH;
     const int i1 = min(P, i0 + CH);
-    for (int i = i0 + threadIdx.x; i < i1; i += BIN_THREADS) {
-        const int r = radii[i];
-        if (r <= 0) continue;
-        const float2 p = means2D[i];
-        unsigned x0, y0, x1, y1;
-        gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
-        for (unsigned y = y0; y < y1; y++)
-            for (unsigned x = x0; x < x1; x++) {
-                const int l = loc_map[y * gx + x];
+    for (int wb = i0 + wave * 64; wb < i1; wb += BIN_THREADS) {
+        unsigned x0, y0, w;
+        const int cnt = rect_of(wb + lane, i1, means2D, radii, gx, gy, x0, y0, w);
+        const Expansion e = expansion_begin(cnt);
+        for (int k0 = 0; k0 < e.total; k0 += 64) {
+            int owner;
+            unsigned tx, ty;
+            expansion_at(e, cnt, x0, y0, w, k0 + lane, owner, tx, ty);
+            if (k0 + lane < e.total) {
+                const unsigned t = ty * gx + tx;
+                const int l = all_local ? (int)t : loc_map[t];
                 if (l >= 0) {
                     if (lds) atomicAdd(&s_hist[l], 1u);
                     else atomicAdd(&tile_count[l], 1u);
                 }
             }
+        }
     }
     if (lds) {
         __syncthreads();
         uint32_t* row = hist + (size_t)c * TL;
-        for (int l = threadIdx.x; l < TL; l += BIN_THREADS) row[l] = s_hist[l];
+        for (int l = threadIdx.x; l < TL; l += BIN_THREADS) {
+            const uint32_t v = s_hist[l];
+            row[l] = v ? atomicAdd(&tile_count[l], v) : 0u;
+        }
     }
-}
-
-// per local tile: exclusive prefix of the chunk histograms (in place) and total
-__global__ __launch_bounds__(256) void colscan_kernel(int NC, const uint32_t* __restrict__ meta,
-                                                      uint32_t* __restrict__ hist, uint32_t* __restrict__ tile_count)
-{
-    const int TL = (int)meta[0];
-    if (TL > LDS_TILES) return;
-    const int l = blockIdx.x * blockDim.x + threadIdx.x;
-    if (l >= TL) return;
-    uint32_t run = 0;
-    for (int c = 0; c < NC; c++) {
-        uint32_t* p = hist + (size_t)c * TL + l;
-        const uint32_t v = *p;
-        *p = run;
-        run += v;
-    }
-    tile_count[l] = run;
 }
 
 // exclusive scan over local tiles -> tile_start, R -> meta[2..3]
@@ -273,6 +334,8 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
 
 // ------------------------------------------------------------- scatter
 
+// Re-walks the chunk and appends (depth bits << 32 | Gaussian id) to the
+// chunk's reserved slice of each tile bucket (LDS cursors).
 __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     int P, int CH, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const float* __restrict__ depths,
     const int* __restrict__ radii, const int* __restrict__ loc_map, const uint32_t* __restrict__ meta,
@@ -282,7 +345,9 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     __shared__ uint32_t s_cur[LDS_TILES];
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
+    const bool all_local = TL == (int)(gx * gy);
     const int c = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lds) {
         const uint32_t* row = hist + (size_t)c * TL;
         for (int l = threadIdx.x; l < TL; l += BIN_THREADS) s_cur[l] = tile_start[l] + row[l];
@@ -290,21 +355,26 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     }
     const int i0 = c * CH;
     const int i1 = min(P, i0 + CH);
-    for (int i = i0 + threadIdx.x; i < i1; i += BIN_THREADS) {
-        const int r = radii[i];
-        if (r <= 0) continue;
-        const float2 p = means2D[i];
-        const uint64_t key = ((uint64_t)gs::f2u(depths[i]) << 32) | (uint32_t)i;
-        unsigned x0, y0, x1, y1;
-        gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
-        for (unsigned y = y0; y < y1; y++)
-            for (unsigned x = x0; x < x1; x++) {
-                const int l = loc_map[y * gx + x];
+    for (int wb = i0 + wave * 64; wb < i1; wb += BIN_THREADS) {
+        const int i = wb + lane;
+        unsigned x0, y0, w;
+        const int cnt = rect_of(i, i1, means2D, radii, gx, gy, x0, y0, w);
+        const uint32_t dbits = cnt ? gs::f2u(depths[i]) : 0u;
+        const Expansion e = expansion_begin(cnt);
+        for (int k0 = 0; k0 < e.total; k0 += 64) {
+            int owner;
+            unsigned tx, ty;
+            expansion_at(e, cnt, x0, y0, w, k0 + lane, owner, tx, ty);
+            const uint32_t odb = (uint32_t)__shfl((int)dbits, owner, 64);
+            if (k0 + lane < e.total) {
+                const unsigned t = ty * gx + tx;
+                const int l = all_local ? (int)t : loc_map[t];
                 if (l >= 0) {
                     const uint32_t pos = lds ? atomicAdd(&s_cur[l], 1u) : atomicAdd(&cursor[l], 1u);
-                    sortkey[pos] = key;
+                    sortkey[pos] = ((uint64_t)odb << 32) | (uint32_t)(wb + owner);
                 }
             }
+        }
     }
 }
 
@@ -316,23 +386,28 @@ __device__ __forceinline__ void cswap(uint64_t* a, uint64_t* b)
     if (y < x) { *a = y; *b = x; }
 }
 
-// Bitonic sort (all comparators put the minimum at the lower index, so a
-// virtual +inf tail beyond n needs no storage) of s[0..N), N = pow2 >= n.
+// Bitonic sort of s[0..N), N a power of two, n real keys (the rest are
+// treated as +inf): every comparator puts the minimum at the lower index
+// (the "flip" first stage of each merge), so keys past n never move and need
+// no storage; pairs touching them are skipped.
 template <int NT>
-__device__ __forceinline__ void bitonic_lds(uint64_t* s, int N)
+__device__ __forceinline__ void bitonic(uint64_t* s, int n, int N)
 {
     for (int k = 2; k <= N; k <<= 1) {
-        const int hk = k >> 1;
+        const int lh = __builtin_ctz((unsigned)k) - 1;            // log2(k/2)
         for (int p = threadIdx.x; p < (N >> 1); p += NT) {
-            const int blk = p / hk, off = p - blk * hk;
-            cswap(&s[blk * k + off], &s[blk * k + k - 1 - off]);
+            const int blk = p >> lh, off = p & ((1 << lh) - 1);
+            const int a = (blk << (lh + 1)) + off;
+            const int b = a + k - 1 - 2 * off;
+            if (b < n) cswap(&s[a], &s[b]);
         }
         __syncthreads();
         for (int j = k >> 2; j >= 1; j >>= 1) {
+            const int lj = __builtin_ctz((unsigned)j);
             for (int p = threadIdx.x; p < (N >> 1); p += NT) {
-                const int blk = p / j, off = p - blk * j;
-                const int a = blk * 2 * j + off;
-                cswap(&s[a], &s[a + j]);
+                const int blk = p >> lj, off = p & (j - 1);
+                const int a = (blk << (lj + 1)) + off;
+                if (a + j < n) cswap(&s[a], &s[a + j]);
             }
             __syncthreads();
         }
@@ -349,26 +424,31 @@ __device__ __forceinline__ void write_sorted(uint32_t tile, uint32_t start, int 
     }
 }
 
-__global__ __launch_bounds__(SORT_THREADS) void tilesort_kernel(
+// One block per local tile whose bucket size lies in (LO, CAP]: the bucket is
+// sorted by (depth bits, Gaussian id) in LDS.  Three size classes keep the
+// LDS footprint (and so the occupancy) matched to the bucket.
+template <int CAP, int NT, int LO>
+__global__ __launch_bounds__(NT) void tilesort_kernel(
     const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ tile_start, const uint64_t* __restrict__ sortkey, uint32_t* __restrict__ point_list,
     uint64_t* __restrict__ keys)
 {
-    __shared__ uint64_t s[SORT_CAP];
+    __shared__ uint64_t s[CAP];
     const int l = blockIdx.x;
     if (l >= (int)meta[0]) return;
     const int n = (int)tile_count[l];
-    if (n == 0 || n > SORT_CAP) return;
+    if (n <= LO || n > CAP) return;
     const uint32_t start = tile_start[l];
     int N = 1;
     while (N < n) N <<= 1;
-    for (int i = threadIdx.x; i < N; i += SORT_THREADS) s[i] = i < n ? sortkey[start + i] : ~(uint64_t)0;
+    for (int i = threadIdx.x; i < n; i += NT) s[i] = sortkey[start + i];
     __syncthreads();
-    bitonic_lds<SORT_THREADS>(s, N);
-    write_sorted((uint32_t)tile_of_local[l], start, n, s, point_list, keys, SORT_THREADS);
+    bitonic<NT>(s, n, N);
+    write_sorted((uint32_t)tile_of_local[l], start, n, s, point_list, keys, NT);
 }
 
-// Buckets larger than SORT_CAP: the same network in global memory (in place)
+// Buckets larger than the biggest LDS class: the same network in global
+// memory, in place.
 __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
     const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ point_list,
@@ -377,28 +457,12 @@ __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
     const int l = blockIdx.x;
     if (l >= (int)meta[0]) return;
     const int n = (int)tile_count[l];
-    if (n <= SORT_CAP) return;
+    if (n <= SORT_CAP_L) return;
     const uint32_t start = tile_start[l];
     uint64_t* s = sortkey + start;
     int N = 1;
     while (N < n) N <<= 1;
-    for (int k = 2; k <= N; k <<= 1) {
-        const int hk = k >> 1;
-        for (int p = threadIdx.x; p < (N >> 1); p += BIG_SORT_THREADS) {
-            const int blk = p / hk, off = p - blk * hk;
-            const int a = blk * k + off, b = blk * k + k - 1 - off;
-            if (b < n) cswap(&s[a], &s[b]);
-        }
-        __syncthreads();
-        for (int j = k >> 2; j >= 1; j >>= 1) {
-            for (int p = threadIdx.x; p < (N >> 1); p += BIG_SORT_THREADS) {
-                const int blk = p / j, off = p - blk * j;
-                const int a = blk * 2 * j + off;
-                if (a + j < n) cswap(&s[a], &s[a + j]);
-            }
-            __syncthreads();
-        }
-    }
+    bitonic<BIG_SORT_THREADS>(s, n, N);
     write_sorted((uint32_t)tile_of_local[l], start, n, s, point_list, keys, BIG_SORT_THREADS);
 }
 
@@ -439,36 +503,49 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     __shared__ float4 s_a[64];   // x, y, -a/2, -b
     __shared__ float4 s_b[64];   // -c/2, opacity, r, g
     __shared__ float2 s_c[64];   // blue, id bits
+    __shared__ int s_pos[64];    // position in the tile's list
 
     const uint2 range = ranges[tile];
     const int n = (int)(range.y - range.x);
     const float pxf = (float)px, pyf = (float)py;
+    const float qx0 = (float)((int)(tile % gx) * 16 + (int)(quad & 1u) * 8);
+    const float qy0 = (float)((int)(tile / gx) * 16 + (int)(quad >> 1) * 8);
     const float alpha_min = 1.0f / 255.0f;
     float T_ = 1.0f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
-    uint32_t contributor = 0, last = 0, n2l = 0;
+    uint32_t last = 0, n2l = 0;
     bool done = !inside;
 
     for (int base = 0; base < n; base += 64) {
         if (gs::ballot(!done) == 0) break;
+        // stage the batch, keeping only Gaussians that can reach this quadrant
         const int k = base + lane;
+        bool keep = false;
+        uint32_t id = 0;
+        float2 xy = make_float2(0.f, 0.f);
+        float4 co = make_float4(0.f, 0.f, 0.f, 0.f);
         if (k < n) {
-            const uint32_t id = point_list[range.x + k];
-            const float2 xy = means2D[id];
-            const float4 co = conic_opacity[id];
-            s_a[lane] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
-            s_b[lane] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
-            s_c[lane] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
+            id = point_list[range.x + k];
+            xy = means2D[id];
+            co = conic_opacity[id];
+            keep = gs::may_touch(xy.x, xy.y, co.x, co.y, co.z, co.w, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
+        }
+        const uint64_t km = gs::ballot(keep);
+        if (keep) {
+            const int slot = gs::rank_below(km);
+            s_a[slot] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
+            s_b[slot] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
+            s_c[slot] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
+            s_pos[slot] = k;
         }
         __syncthreads();
-        const int cnt = min(64, n - base);
+        const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
             if (gs::ballot(!done) == 0) break;
             const float4 A = s_a[j];
             const float4 B = s_b[j];
             const float2 Cc = s_c[j];
-            bool blend = false, observe = false;
+            bool observe = false;
             if (!done) {
-                contributor++;
                 const float dx = A.x - pxf, dy = A.y - pyf;
                 const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
                 const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
@@ -477,7 +554,6 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
                     if (test_T < 0.0001f) {
                         done = true;
                     } else {
-                        blend = true;
                         observe = T_ > 0.5f;
                         n2l++;
                         const float wgt = alpha * T_;
@@ -485,11 +561,10 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
                         C1 = __builtin_fmaf(B.w, wgt, C1);
                         C2 = __builtin_fmaf(Cc.x, wgt, C2);
                         T_ = test_T;
-                        last = contributor;
+                        last = (uint32_t)s_pos[j] + 1u;
                     }
                 }
             }
-            (void)blend;
             const uint64_t m = gs::ballot(observe);
             if (m != 0 && lane == (int)__builtin_ctzll(m))
                 atomicAdd(&out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
@@ -558,30 +633,63 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     __shared__ float4 s_a[64];   // x, y, -a/2, -b
     __shared__ float4 s_b[64];   // -c/2, opacity, r, g
     __shared__ float2 s_c[64];   // blue, id bits
+    __shared__ int s_pos[64];    // position in the tile's list
 
     const uint2 range = ranges[tile];
     const float pxf = (float)px, pyf = (float)py;
+    const float qx0 = (float)((int)(tile % gx) * 16 + (int)(quad & 1u) * 8);
+    const float qy0 = (float)((int)(tile / gx) * 16 + (int)(quad >> 1) * 8);
     const float alpha_min = 1.0f / 255.0f;
     const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
     const float bg_dot = bg[0] * dp0 + bg[1] * dp1 + bg[2] * dp2;
+    // after the wave reduction this lane holds the total of one gradient term:
+    // its array, row stride and offset
+    float* my_dst = nullptr;
+    int my_stride = 0;
+    switch (gs::wave_sum12_index(lane)) {
+        case 0: my_dst = g_m2d; my_stride = m2d_stride; break;
+        case 1: my_dst = g_m2d + 1; my_stride = m2d_stride; break;
+        case 2: my_dst = g_m2d_abs; my_stride = 3; break;
+        case 3: my_dst = g_m2d_abs + 1; my_stride = 3; break;
+        case 4: my_dst = g_con; my_stride = 4; break;
+        case 5: my_dst = g_con + 1; my_stride = 4; break;
+        case 6: my_dst = g_con + 2; my_stride = 4; break;
+        case 7: my_dst = g_con + 3; my_stride = 4; break;
+        case 8: my_dst = g_col; my_stride = 3; break;
+        case 9: my_dst = g_col + 1; my_stride = 3; break;
+        case 10: my_dst = g_col + 2; my_stride = 3; break;
+        default: break;
+    }
     float T_ = T_final;
     float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
     float lc0 = 0.f, lc1 = 0.f, lc2 = 0.f, last_alpha = 0.f;
 
     // walk positions maxlast-1 .. 0 of the tile's list, back to front
     for (int top = maxlast; top > 0; top -= 64) {
-        const int cnt = min(64, top);
-        if (lane < cnt) {
-            const uint32_t id = point_list[range.x + top - 1 - lane];
-            const float2 xy = means2D[id];
-            const float4 co = conic_opacity[id];
-            s_a[lane] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
-            s_b[lane] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
-            s_c[lane] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
+        // stage positions top-1, top-2, ... keeping only Gaussians that can reach this quadrant
+        const int k = top - 1 - lane;
+        bool keep = false;
+        uint32_t id = 0;
+        float2 xy = make_float2(0.f, 0.f);
+        float4 co = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k >= 0) {
+            id = point_list[range.x + k];
+            xy = means2D[id];
+            co = conic_opacity[id];
+            keep = gs::may_touch(xy.x, xy.y, co.x, co.y, co.z, co.w, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
+        }
+        const uint64_t km = gs::ballot(keep);
+        if (keep) {
+            const int slot = gs::rank_below(km);
+            s_a[slot] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
+            s_b[slot] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
+            s_c[slot] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
+            s_pos[slot] = k;
         }
         __syncthreads();
+        const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
-            const int ci = top - 1 - j;   // position in the tile's list
+            const int ci = s_pos[j];   // position in the tile's list
             const float4 A = s_a[j];
             const float4 B = s_b[j];
             const float2 Cc = s_c[j];
@@ -596,7 +704,8 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
                 if (!(power > 0.0f) && !(alpha < alpha_min)) {
                     valid = true;
                     const float one_m = 1.f - alpha;
-                    T_ = T_ / one_m;
+                    const float inv_one_m = __builtin_amdgcn_rcpf(one_m);   // 1 ulp; gradients only
+                    T_ = T_ * inv_one_m;
                     const float dchannel_dcolor = alpha * T_;
                     acc0 = last_alpha * lc0 + (1.f - last_alpha) * acc0;
                     acc1 = last_alpha * lc1 + (1.f - last_alpha) * acc1;
@@ -608,7 +717,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
                     gc2 = dchannel_dcolor * dp2;
                     dL_dalpha *= T_;
                     last_alpha = alpha;
-                    dL_dalpha += (-T_final / one_m) * bg_dot;
+                    dL_dalpha += (-T_final * inv_one_m) * bg_dot;
                     const float a = -2.0f * A.z, b = -A.w, c = -2.0f * B.x;
                     const float dL_dG = B.y * dL_dalpha;
                     const float gdx = G * dx, gdy = G * dy;
@@ -622,31 +731,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
                     gop = G * dL_dalpha;
                 }
             }
-            if (gs::ballot(valid) == 0) continue;
-            const float s_mx = gs::wave_sum(gmx), s_my = gs::wave_sum(gmy);
-            const float s_ax = gs::wave_sum(__builtin_fabsf(gmx)), s_ay = gs::wave_sum(__builtin_fabsf(gmy));
-            const float s_ca = gs::wave_sum(gca), s_cb = gs::wave_sum(gcb), s_cc = gs::wave_sum(gcc);
-            const float s_op = gs::wave_sum(gop);
-            const float s_c0 = gs::wave_sum(gc0), s_c1 = gs::wave_sum(gc1), s_c2 = gs::wave_sum(gc2);
-            // eleven atomics, one lane each, in one instruction
+            const uint64_t vm = gs::ballot(valid);
+            if (vm == 0) continue;
             const uint32_t id = __float_as_uint(Cc.y);
-            float v = 0.f;
-            float* dst = nullptr;
-            switch (lane) {
-                case 0: v = s_mx; dst = g_m2d + (size_t)id * m2d_stride; break;
-                case 1: v = s_my; dst = g_m2d + (size_t)id * m2d_stride + 1; break;
-                case 2: v = s_ax; dst = g_m2d_abs + 3 * (size_t)id; break;
-                case 3: v = s_ay; dst = g_m2d_abs + 3 * (size_t)id + 1; break;
-                case 4: v = s_ca; dst = g_con + 4 * (size_t)id; break;
-                case 5: v = s_cb; dst = g_con + 4 * (size_t)id + 1; break;
-                case 6: v = s_cc; dst = g_con + 4 * (size_t)id + 2; break;
-                case 7: v = s_op; dst = g_con + 4 * (size_t)id + 3; break;
-                case 8: v = s_c0; dst = g_col + 3 * (size_t)id; break;
-                case 9: v = s_c1; dst = g_col + 3 * (size_t)id + 1; break;
-                case 10: v = s_c2; dst = g_col + 3 * (size_t)id + 2; break;
-                default: break;
-            }
-            if (dst != nullptr && v != 0.f) atomicAdd(dst, v);
+            const float vals[12] = {gmx, gmy, __builtin_fabsf(gmx), __builtin_fabsf(gmy), gca, gcb, gcc, gop,
+                                    gc0, gc1, gc2, 0.f};
+            const float tot = gs::wave_sum12(vals);
+            if (my_dst != nullptr && tot != 0.f) unsafeAtomicAdd(my_dst + (size_t)id * my_stride, tot);
         }
         __syncthreads();
     }
@@ -699,9 +790,6 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
         GS_TIMED("count_kernel", stream, hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
                            reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count));
         GS_LAUNCH_CHECK("count_kernel");
-        GS_TIMED("colscan_kernel", stream, hipLaunchKernelGGL(colscan_kernel, dim3(gs_div_up((size_t)(g.T < LDS_TILES ? g.T : LDS_TILES), 256)),
-                           dim3(256), 0, stream, g.NC, meta, hist, tile_count));
-        GS_LAUNCH_CHECK("colscan_kernel");
     }
     GS_TIMED("tilescan_kernel", stream, hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor));
     GS_LAUNCH_CHECK("tilescan_kernel");
@@ -756,11 +844,21 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
                            reinterpret_cast<const float2*>(means2D), depths, radii, loc_map, meta, hist,
                            tile_start, cursor, sortkey));
         GS_LAUNCH_CHECK("scatter_kernel");
-        GS_TIMED("tilesort_kernel", stream, hipLaunchKernelGGL(tilesort_kernel, dim3(T), dim3(SORT_THREADS), 0, stream, meta, tile_of_local, tile_count,
-                           tile_start, sortkey, point_list, keys));
-        GS_LAUNCH_CHECK("tilesort_kernel");
-        GS_TIMED("tilesort_big_kernel", stream, hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta, tile_of_local,
-                           tile_count, tile_start, sortkey, point_list, keys));
+        GS_TIMED("tilesort_kernel_s", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_S, 256, 0>), dim3(T), dim3(256), 0, stream, meta,
+                                    tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+        GS_LAUNCH_CHECK("tilesort_kernel<S>");
+        GS_TIMED("tilesort_kernel_m", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_M, 512, SORT_CAP_S>), dim3(T), dim3(512), 0, stream,
+                                    meta, tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+        GS_LAUNCH_CHECK("tilesort_kernel<M>");
+        GS_TIMED("tilesort_kernel_l", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_L, 1024, SORT_CAP_M>), dim3(T), dim3(1024), 0, stream,
+                                    meta, tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+        GS_LAUNCH_CHECK("tilesort_kernel<L>");
+        GS_TIMED("tilesort_big_kernel", stream,
+                 hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta,
+                                    tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
         GS_LAUNCH_CHECK("tilesort_big_kernel");
     }
     const unsigned nblk = ((T + 7u) / 8u) * 32u;

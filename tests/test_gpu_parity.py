@@ -225,3 +225,65 @@ def test_render_backward_vs_oracle_with_background():
     assert rel_l2(np_(dma), rb["dL_dmeans2D_abs"]) < 1e-3
     assert rel_l2(np_(dco), rb["dL_dconic_opacity"]) < 1e-3
     assert rel_l2(np_(dcol), rb["dL_dcolors"]) < 1e-3
+
+
+def test_quadrant_cull_keeps_results_exact_on_hard_cases():
+    # needle-like and huge Gaussians, opacities around 1/255, means exactly on
+    # pixel centres and tile borders: the blend kernels cull Gaussians that
+    # cannot reach alpha >= 1/255 in a quadrant; the image, transmittance and
+    # contributor counts must still equal the unculled CPU evaluation bit for bit
+    rng = np.random.default_rng(123)
+    P, W, H = 6000, 160, 128
+    means2D = np.stack([rng.uniform(-40, W + 40, P), rng.uniform(-40, H + 40, P)], 1).astype(np.float32)
+    means2D[:500] = np.round(means2D[:500])
+    means2D[500:800, 0] = 16.0 * rng.integers(0, 10, 300) - 0.5
+    ang = rng.uniform(0, np.pi, P)
+    s_long = np.exp(rng.uniform(0, 5, P))
+    s_short = np.exp(rng.uniform(-1, 1.5, P))
+    ca, sa = np.cos(ang), np.sin(ang)
+    cxx = ca * ca * s_long ** 2 + sa * sa * s_short ** 2 + 0.3
+    cyy = sa * sa * s_long ** 2 + ca * ca * s_short ** 2 + 0.3
+    cxy = ca * sa * (s_long ** 2 - s_short ** 2)
+    det = cxx * cyy - cxy * cxy
+    conic = np.stack([cyy / det, -cxy / det, cxx / det], 1)
+    op = rng.uniform(0, 1, P)
+    op[:1500] = rng.choice([1 / 255.0, 0.0039, 0.0040, 0.004, 0.99, 1.0], 1500)
+    co = np.concatenate([conic, op[:, None]], 1).astype(np.float32)
+    radii = np.ceil(3.33 * np.sqrt(np.maximum(cxx, cyy))).astype(np.int32)
+    depths = rng.uniform(1, 100, P).astype(np.float32)
+    rgb = rng.random((P, 3)).astype(np.float32)
+    cam = dict(W=W, H=H, tanfovx=1.0, tanfovy=1.0, viewmatrix=np.eye(4, dtype=np.float32),
+               projmatrix=np.eye(4, dtype=np.float32), campos=np.zeros(3, np.float32))
+    pre = dict(means2D=means2D, depths=depths, radii=radii, conic_opacity=co, rgb=rgb)
+    _check_binning_and_render(cam, pre, (0.1, 0.2, 0.3))
+    # and the backward over the same lists
+    dLd = rng.standard_normal((3, H, W)).astype(np.float32)
+    bn = O.binning(W, H, means2D, depths, radii)
+    rf = O.render_fwd(W, H, np.array([0.1, 0.2, 0.3], np.float32), means2D, co, rgb, bn["ranges"], bn["point_list"])
+    rb = O.render_bwd(W, H, np.array([0.1, 0.2, 0.3], np.float32), means2D, co, rgb, bn["ranges"], bn["point_list"],
+                      rf["final_T"], rf["n_contrib_px"], dLd)
+    from blitzgs_amd import rasterizer as R
+    rs = settings_for(cam, bg=(0.1, 0.2, 0.3))
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    out = R._render_forward_raw(rs.bg, H, W, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"],
+                                dev["rgb"], None)
+    Rn, *_rest, geom, binning, img, _ = out
+    dm, dma, dco, dcol, _ = R._render_backward_raw(rs.bg, Rn, H, W, dev["means2D"], dev["conic_opacity"],
+                                                   dev["rgb"], None, binning, img, to_dev(dLd), m2d_stride=3)
+    for g, r, nm in ((dm, rb["dL_dmeans2D"], "dmean2D"), (dma, rb["dL_dmeans2D_abs"], "abs"),
+                     (dco, rb["dL_dconic_opacity"], "conic_opacity"), (dcol, rb["dL_dcolors"], "colors")):
+        assert rel_l2(np_(g), r) < 1e-3, nm
+
+
+def test_wave_sum12_lane_layout():
+    # the backward's 12-value wave reduction (permlane32/16 swaps + DPP row
+    # scans) against a plain sum, with values that make any mis-routed lane visible
+    rng = np.random.default_rng(0)
+    x = rng.integers(-1000, 1000, (12, 64)).astype(np.float32)
+    x[7] = 1.0
+    x[3, 5] = 1e6
+    xt = to_dev(x.reshape(-1))
+    y = torch.zeros(12, device="cuda")
+    _lib.check(_lib.load().gs_diag_math(3, 12 * 64, _lib.ptr(xt), _lib.ptr(y), None), "diag sum12")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np_(y), x.astype(np.float64).sum(1).astype(np.float32))

@@ -51,7 +51,26 @@ def parse():
     ap.add_argument("--cpu-sample", type=float, default=1.0,
                     help="fraction of the Gaussians the CPU baseline runs on")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run the library's plain copy kernel on MIB MiB (5 launches): the known-size "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
     return ap.parse_args()
+
+
+def calibrate_copy(mib):
+    import torch
+    from blitzgs_amd import _lib
+    lib = _lib.load()
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda:0")
+    y = torch.empty_like(x)
+    stream = _lib.stream_of(x.device)
+    for _ in range(5):
+        _lib.check(lib.gs_diag_math(4, n, _lib.ptr(x), _lib.ptr(y), stream), "gs_diag_math copy")
+    torch.cuda.synchronize()
+    assert bool((y == 1).all())
+    print(json.dumps({"copy_kernel": "diag_copy_kernel", "bytes_read": 4 * n, "bytes_written": 4 * n,
+                      "launches": 5}), flush=True)
 
 
 def log(*a):
@@ -64,6 +83,9 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding of this path is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     import torch
     from blitzgs_amd import _lib, synth
     from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer

@@ -1,9 +1,11 @@
 // Library-wide C-ABI pieces: version, thread-local error text, and the
 // device-math diagnostic entry point.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -156,12 +158,21 @@ __global__ void diag_math_kernel(int op, int n, const float* __restrict__ x, flo
     else r = (v <= 0.0f || v != v) ? gs::expf_nonpos(v) : gs::expf_full(v);
     y[i] = r;
 }
+
+// op 4: plain copy of n floats (n % 4 == 0), 16-byte loads and stores; the
+// known-size reference against which HBM byte counters are calibrated
+__global__ void diag_copy_kernel(size_t n4, const float4* __restrict__ x, float4* __restrict__ y)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) y[i] = x[i];
+}
 }  // namespace
 
 extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t stream)
 {
     gs::clear_error();
-    GS_REQUIRE(op >= 0 && op <= 3, "op must be 0 (exp), 1 (log), 2 (blend exp) or 3 (wave sum of 12 values)");
+    GS_REQUIRE(op >= 0 && op <= 4,
+               "op must be 0 (exp), 1 (log), 2 (blend exp), 3 (wave sum of 12 values) or 4 (copy)");
     GS_REQUIRE(n >= 0, "n must be >= 0");
     if (op == 3) {
         GS_REQUIRE(n == 12 * 64, "op 3 takes 12 x 64 inputs");
@@ -170,6 +181,17 @@ extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t
         return GS_OK;
     }
     if (n == 0) return GS_OK;
+    if (op == 4) {
+        GS_REQUIRE(n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0,
+                   "op 4 copies whole 16-byte groups from 16-byte aligned buffers");
+        const size_t n4 = (size_t)n / 4;
+        const unsigned blocks = (unsigned)std::min<size_t>(gs_div_up(n4, 256), 8192);
+        GS_TIMED("diag_copy_kernel", stream,
+                 hipLaunchKernelGGL(diag_copy_kernel, dim3(blocks), dim3(256), 0, stream, n4,
+                                    (const float4*)x, (float4*)y));
+        GS_LAUNCH_CHECK("diag_copy_kernel");
+        return GS_OK;
+    }
     hipLaunchKernelGGL(diag_math_kernel, dim3(gs_div_up((size_t)n, 256)), dim3(256), 0, stream, op, n, x, y);
     GS_LAUNCH_CHECK("diag_math_kernel");
     return GS_OK;

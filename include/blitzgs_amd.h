@@ -158,8 +158,11 @@ int gs_ssim_backward(int B, int C, int H, int W, float C1, float C2, const float
                      gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
- * Diagnostics: evaluate the device exp / log used by the kernels on n inputs
- * (op 0 = exp, 1 = log), so tests can compare them bit for bit with the CPU.
+ * Diagnostics (no counterpart in the reference): evaluate the device exp / log
+ * used by the kernels on n inputs (op 0 = exp, 1 = log, 2 = the blend's exp,
+ * 3 = the 12-value wave reduction on 12 x 64 inputs), so tests can compare them
+ * bit for bit with the CPU; op 4 copies n floats (n % 4 == 0, 16-byte aligned),
+ * the known-size kernel that HBM byte counters are calibrated against.
  * ------------------------------------------------------------------------ */
 int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
 

@@ -34,6 +34,8 @@ def stage_bytes(P, P_vis, R, npx, T):
         "binning": 16 * P + 44 * R,
         "render_fwd_kernel": 40 * R + 24 * npx,
         "render_bwd_kernel": 40 * R + 32 * npx,
+        # out_observe clear (4P) and the gradient unpack (1P flag + 48 P_vis read + 48 P_vis clear + 48 P written)
+        "other": 4 * P + P + 96 * P_vis + 48 * P,
     }
 
 
@@ -159,6 +161,7 @@ def main():
     stages = {k: per_kernel.get(k, 0.0) for k in ("preprocess_fwd_kernel", "render_fwd_kernel",
                                                   "render_bwd_kernel", "preprocess_bwd_kernel")}
     stages["binning"] = sum(per_kernel.get(k, 0.0) for k in BINNING_KERNELS)
+    stages["other"] = sum(v for k, v in per_kernel.items() if k not in stages and k not in BINNING_KERNELS)
     sb = stage_bytes(P, P_vis, R, W * H, T)
     stage_rows = {}
     for k, ms in stages.items():

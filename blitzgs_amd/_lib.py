@@ -30,7 +30,7 @@ _SIGS = {
     "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _c]),
     "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
                                _c, _c]),
-    "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
+    "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
     "gs_knn_workspace_bytes": (_sz, [_i]),
@@ -45,7 +45,9 @@ _SIGS = {
 
 
 def lib_path():
-    return _build.LIB
+    """The in-tree library, or the file named by BLITZGS_AMD_LIB (another build
+    of the same sources, e.g. for side-by-side benchmarking)."""
+    return os.environ.get("BLITZGS_AMD_LIB") or _build.LIB
 
 
 def load():

@@ -63,7 +63,7 @@ def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, al
     H, W = int(dL_dout_color.size(1)), int(dL_dout_color.size(2))
     timing = _r._want_timing(args)
     dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _r._render_backward_raw(
-        background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, binningBuffer, imageBuffer,
+        background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, geomBuffer, binningBuffer, imageBuffer,
         dL_dout_color.contiguous(), 3, timing)
     if timing:
         args["stats_collector"]["backward_render_time"] = ms

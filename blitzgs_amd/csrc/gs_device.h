@@ -122,18 +122,44 @@ __device__ __forceinline__ float power_of(float ha, float nb, float hc, float dx
 // stationary point of one of the four edges when the mean is outside); the
 // test keeps a margin of 1e-3 + 1e-6 * M, where M bounds the magnitude of the
 // fp32 terms of the per-pixel exponent, far above the fp32 rounding of that
-// exponent (a few ulp of M) and of exp.  A false answer therefore implies that
-// the exact per-pixel fp32 evaluation skips the Gaussian at every pixel of
-// the rectangle, so culling with it leaves the blend's results unchanged.
-// Non-finite inputs and non-positive-definite conics are always kept.
-__device__ __forceinline__ bool may_touch(float mx, float my, float ca, float cb, float cc, float o, float x0,
-                                          float y0, float x1, float y1)
+// exponent (a few ulp of M) and of exp, and far above the double rounding of
+// the stationary point (which moves the edge minimum only quadratically).  A
+// false answer therefore implies that the exact per-pixel fp32 evaluation
+// skips the Gaussian at every pixel of the rectangle, so culling with it
+// leaves the blend's results unchanged.  Non-finite inputs and
+// non-positive-definite conics are always kept.
+//
+// The per-Gaussian part is computed once per Gaussian by cull_prepare, in
+// fp32: the threshold -log(255 o) (relative error ~1e-7 of a value <= 5.6,
+// far inside the margin) and the edge slopes -b/c, -b/a (an error in the
+// stationary point moves the edge minimum only quadratically).  A NaN
+// threshold means "always keep", +inf "never" (opacity below 1/255).
+// may_touch_prepared is the per-rectangle part.
+struct CullPrep {
+    float thresh, nbc, nba;
+};
+
+__device__ __forceinline__ CullPrep cull_prepare(float mx, float my, float ca, float cb, float cc, float o)
 {
-    if (o != o) return true;
-    if (o < 1.0f / 255.0f) return false;           // alpha = min(.99, o*G) <= o with G <= 1
-    if (!(__builtin_isfinite(mx) && __builtin_isfinite(my) && __builtin_isfinite(o))) return true;
+    const float qnan = __builtin_nanf("");
+    CullPrep r{qnan, 0.f, 0.f};
+    if (o != o) return r;
+    if (o < 1.0f / 255.0f) { r.thresh = __builtin_huge_valf(); return r; }   // alpha <= o with G <= 1
+    if (!(__builtin_isfinite(mx) && __builtin_isfinite(my) && __builtin_isfinite(o))) return r;
     const double a = ca, b = cb, c = cc;
-    if (!(a > 0.0 && c > 0.0 && a * c - b * b > 0.0)) return true;
+    if (!(a > 0.0 && c > 0.0 && a * c - b * b > 0.0)) return r;
+    r.thresh = -logf_full(255.0f * o);
+    r.nbc = -cb * __builtin_amdgcn_rcpf(cc);
+    r.nba = -cb * __builtin_amdgcn_rcpf(ca);
+    return r;
+}
+
+__device__ __forceinline__ bool may_touch_prepared(float thresh, float nbc, float nba, float mx, float my, float ca,
+                                                   float cb, float cc, float x0, float y0, float x1, float y1)
+{
+    if (thresh != thresh) return true;
+    if (thresh == __builtin_huge_valf()) return false;
+    const double a = ca, b = cb, c = cc;
     const double dxl = (double)mx - (double)x1, dxh = (double)mx - (double)x0;
     const double dyl = (double)my - (double)y1, dyh = (double)my - (double)y0;
     if (dxl <= 0.0 && dxh >= 0.0 && dyl <= 0.0 && dyh >= 0.0) return true;
@@ -141,21 +167,20 @@ __device__ __forceinline__ bool may_touch(float mx, float my, float ca, float cb
 #pragma unroll
     for (int e = 0; e < 2; e++) {
         const double dx = e ? dxh : dxl;
-        const double dy = __builtin_fmin(__builtin_fmax(-b * dx / c, dyl), dyh);
+        const double dy = __builtin_fmin(__builtin_fmax((double)nbc * dx, dyl), dyh);
         best = __builtin_fmin(best, a * dx * dx + 2.0 * b * dx * dy + c * dy * dy);
     }
 #pragma unroll
     for (int e = 0; e < 2; e++) {
         const double dy = e ? dyh : dyl;
-        const double dx = __builtin_fmin(__builtin_fmax(-b * dy / a, dxl), dxh);
+        const double dx = __builtin_fmin(__builtin_fmax((double)nba * dy, dxl), dxh);
         best = __builtin_fmin(best, a * dx * dx + 2.0 * b * dx * dy + c * dy * dy);
     }
     const double DX = __builtin_fmax(__builtin_fabs(dxl), __builtin_fabs(dxh));
     const double DY = __builtin_fmax(__builtin_fabs(dyl), __builtin_fabs(dyh));
     const double M = 0.5 * (a * DX * DX + c * DY * DY) + __builtin_fabs(b) * DX * DY;
     const double margin = 1e-3 + 1e-6 * M;
-    const double thresh = -::log(255.0 * (double)o);
-    return -0.5 * best + margin >= thresh;
+    return -0.5 * best + margin >= (double)thresh;
 }
 
 // ---- wave64 helpers -------------------------------------------------------

@@ -15,31 +15,40 @@
 // a 64-bit (tile | depth) key in Gaussian order and radix-sorts all R pairs
 // globally (about six passes over 12 bytes per instance).  Here the tiles are
 // bucketed first and each bucket is sorted on chip:
-//   1. count   : each block takes a chunk of Gaussians, expands their tile
-//                instances wave-cooperatively (one instance per lane per
-//                round, whatever the rect sizes) and histograms them in LDS
-//                (one counter per local tile); it then reserves its slice of
-//                every tile bucket with one global atomic per non-empty tile.
+//   1. count   : each block takes a chunk of Gaussians (each wave a
+//                contiguous run of it), expands their tile instances
+//                wave-cooperatively (one instance per lane per round, whatever
+//                the rect sizes) and histograms them in LDS (one counter per
+//                local tile); it then reserves its slice of every tile bucket
+//                with one global atomic per non-empty tile.  Each wave also
+//                counts its listed Gaussians (non-empty rect).
 //   2. scan    : a scan over the tile totals gives the tile offsets (these
-//                are the reference's ranges) and R.
-//   3. scatter : each block re-walks its chunk and appends (depth bits, id)
-//                to its reserved slices (LDS cursors).
-//   4. sort    : one block per tile sorts its bucket by (depth bits, id) in
-//                LDS (bitonic, three size classes) and writes the sorted ids
-//                and the (tile << 32 | depth bits) keys.
-// Sorting each bucket by (depth bits, Gaussian id) yields exactly the order
-// of a stable sort of the reference's duplicated keys, so the sorted arrays
-// and the ranges are bit-identical to the reference algorithm's.
-// When more than LDS_TILES tiles are local, steps 1 and 3 use global atomics
-// instead of the LDS histogram (same result after step 4).
+//                are the reference's ranges) and R; a scan over the per-wave
+//                listed counts numbers the listed Gaussians densely in id
+//                order (compact index).
+//   3. scatter : each block re-walks its chunk, appends (depth bits, compact
+//                index) to its reserved slices (LDS cursors) and writes each
+//                listed Gaussian's 64-byte blend record at its compact index.
+//   4. sort    : one block per tile sorts its bucket by (depth bits, compact
+//                index) in LDS (bitonic, three size classes) and writes the
+//                sorted Gaussian ids, the (tile << 32 | depth bits) keys and
+//                the compact list the blend walks.
+// The compact index is increasing in Gaussian id, so each sorted bucket is
+// exactly the order of a stable sort of the reference's duplicated keys, and
+// the sorted arrays and the ranges are bit-identical to the reference
+// algorithm's.  When more than LDS_TILES tiles are local, steps 1 and 3 use
+// global atomics instead of the LDS histogram (same result after step 4).
 //
 // Blend design.  One wave64 per 8x8 quadrant of a tile, one pixel per lane,
-// no block-wide barriers: a wave stages batches of 64 Gaussians in its own
-// LDS slots and stops as soon as all of its 64 pixels are saturated.  The
-// backward walks each quadrant's list back to front from the largest last
-// contributor of its pixels, reduces every Gaussian's eleven gradient terms
-// across the wave with DPP row shifts / row broadcasts, and issues one set of
-// global atomics per (wave, Gaussian) instead of one per (pixel, Gaussian).
+// no block-wide barriers: a wave stages batches of 64 list entries (their
+// records gathered while the previous batch blends) in its own LDS slots,
+// dropping those that provably cannot reach the quadrant, and stops as soon as
+// all of its 64 pixels are saturated.  The backward walks each quadrant's
+// list back to front from the largest last contributor of its pixels, reduces
+// every Gaussian's eleven gradient terms across the wave and adds them into
+// the Gaussian's 64-byte accumulator with one atomic instruction per (wave,
+// Gaussian) instead of eleven atomics per (pixel, Gaussian); a final pass
+// writes the reference's gradient arrays from the accumulators.
 #include "gs_device.h"
 #include "gs_host.h"
 #include "../../include/blitzgs_amd.h"
@@ -48,17 +57,31 @@ namespace {
 
 constexpr int LDS_TILES = 16384;     // local tiles histogrammed in LDS (64 KB)
 constexpr int BIN_THREADS = 512;
+constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_S = 2048;     // bucket size classes sorted entirely in LDS
 constexpr int SORT_CAP_M = 4096;
 constexpr int SORT_CAP_L = 8192;
 constexpr int BIG_SORT_THREADS = 1024;
+// Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
+// order ("compact index").  Per listed Gaussian the scatter writes a blend
+// record of 4 x float4 at its compact index:
+//   [0] mean x, mean y, conic a, conic b
+//   [1] conic c, opacity, red, green
+//   [2] blue, cull threshold, cull slopes -b/c and -b/a
+//   [3] Gaussian id bits, 0, 0, 0
+// so the blend gathers one aligned 64-byte segment per list entry.
+constexpr size_t REC_BYTES = 64;
+// Per-Gaussian gradient accumulator of the backward (16 floats, 11 used):
+//   dmean x, dmean y, |dmean x|, |dmean y|, dconic a, b, c, dopacity, drgb x 3
+constexpr size_t GACC_BYTES = 64;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct GeomLayout {
-    int T, NC, CH;
-    size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, total;
+    int T, NC, CH, WS;
+    size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, wcount, cidx_of, cid2id, rec, gacc,
+        total;
 };
 
 GeomLayout geom_layout(int P, int W, int H)
@@ -71,6 +94,8 @@ GeomLayout geom_layout(int P, int W, int H)
     if (nc > MAX_CHUNKS) nc = MAX_CHUNKS;
     g.NC = (int)nc;
     g.CH = (int)(((long)P + g.NC - 1) / g.NC);
+    // each of a block's waves takes a contiguous run of WS Gaussians (whole groups of 64)
+    g.WS = (int)((((long)g.CH + WAVES_PER_BIN - 1) / WAVES_PER_BIN + 63) / 64 * 64);
     size_t o = 0;
     g.loc_map = o; o = align256(o + sizeof(int) * (size_t)g.T);
     g.tile_of_local = o; o = align256(o + sizeof(int) * (size_t)g.T);
@@ -79,6 +104,11 @@ GeomLayout geom_layout(int P, int W, int H)
     g.tile_count = o; o = align256(o + sizeof(uint32_t) * (size_t)g.T);
     g.tile_start = o; o = align256(o + sizeof(uint32_t) * (size_t)g.T);
     g.cursor = o; o = align256(o + sizeof(uint32_t) * (size_t)g.T);
+    g.wcount = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NC * WAVES_PER_BIN);
+    g.cidx_of = o; o = align256(o + sizeof(int) * (size_t)P);
+    g.cid2id = o; o = align256(o + sizeof(uint32_t) * (size_t)P);
+    g.rec = o; o = align256(o + REC_BYTES * (size_t)P);
+    g.gacc = o; o = align256(o + GACC_BYTES * (size_t)P);
     g.total = o;
     return g;
 }
@@ -102,7 +132,7 @@ ImgLayout img_layout(int W, int H)
 }
 
 struct BinLayout {
-    size_t sortkey, point_list, keys, total;
+    size_t sortkey, point_list, keys, clist, total;
 };
 
 BinLayout bin_layout(int64_t R)
@@ -112,6 +142,7 @@ BinLayout bin_layout(int64_t R)
     b.sortkey = o; o = align256(o + sizeof(uint64_t) * (size_t)R);
     b.point_list = o; o = align256(o + sizeof(uint32_t) * (size_t)R);
     b.keys = o; o = align256(o + sizeof(uint64_t) * (size_t)R);
+    b.clist = o; o = align256(o + sizeof(uint32_t) * (size_t)R);
     b.total = o < 256 ? 256 : o;
     return b;
 }
@@ -226,31 +257,46 @@ __device__ __forceinline__ void expansion_at(const Expansion& e, int cnt, unsign
     ty = oy0 + q;
 }
 
-// tile rect of Gaussian i (binning rule); returns its tile count
-__device__ __forceinline__ int rect_of(int i, int i1, const float2* __restrict__ means2D, const int* __restrict__ radii,
-                                       unsigned gx, unsigned gy, unsigned& x0, unsigned& y0, unsigned& w)
+// tile rect of a Gaussian with radius r and mean p (binning rule); returns
+// its tile count
+__device__ __forceinline__ int rect_from(int r, float2 p, unsigned gx, unsigned gy, unsigned& x0, unsigned& y0,
+                                         unsigned& w)
 {
     x0 = y0 = w = 0;
-    if (i >= i1) return 0;
-    const int r = radii[i];
     if (r <= 0) return 0;
-    const float2 p = means2D[i];
     unsigned x1, y1;
     gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
     w = x1 - x0;
     return (int)(w * (y1 - y0));
 }
 
+// radius and mean of Gaussian i of a wave's run ending at i1 (radius 0 past it)
+__device__ __forceinline__ void load_rm(int i, int i1, const int* __restrict__ radii,
+                                        const float2* __restrict__ means2D, int& r, float2& m)
+{
+    r = 0;
+    m = make_float2(0.f, 0.f);
+    if (i < i1) {
+        r = radii[i];
+        m = means2D[i];
+    }
+}
+
 // Per chunk of Gaussians: histogram of its tile instances in LDS; the chunk
 // then reserves its slice of every tile's bucket with one atomic per
 // non-empty tile and keeps the returned base in its histogram row.  With more
 // local tiles than LDS_TILES, instances are counted with global atomics.
+//
+// Each wave takes a contiguous run of WS Gaussians of the chunk and also
+// counts its listed Gaussians (wcount), from which the scan derives the
+// compact indices.
 __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
-    int P, int CH, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const int* __restrict__ radii,
+    int P, int CH, int WS, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const int* __restrict__ radii,
     const int* __restrict__ loc_map, const uint32_t* __restrict__ meta, uint32_t* __restrict__ hist,
-    uint32_t* __restrict__ tile_count)
+    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ wcount)
 {
-    __shared__ uint32_t s_hist[LDS_TILES];
+    extern __shared__ uint4 s_dyn[];   // min(T, LDS_TILES) tile counters
+    uint32_t* s_hist = reinterpret_cast<uint32_t*>(s_dyn);
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
     const bool all_local = TL == (int)(gx * gy);
@@ -260,11 +306,21 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
         for (int l = threadIdx.x; l < TL; l += BIN_THREADS) s_hist[l] = 0;
         __syncthreads();
     }
-    const int i0 = c * CH;
-    const int i1 = min(P, i0 + CH);
-    for (int wb = i0 + wave * 64; wb < i1; wb += BIN_THREADS) {
+    const int i1c = min(P, c * CH + CH);
+    const int ws = min(i1c, c * CH + wave * WS);
+    const int i1 = min(i1c, ws + WS);
+    uint32_t listed = 0;
+    // the next group's radii and means are loaded while this group expands
+    int r_n;
+    float2 m_n;
+    load_rm(ws + lane, i1, radii, means2D, r_n, m_n);
+    for (int wb = ws; wb < i1; wb += 64) {
+        const int r = r_n;
+        const float2 m = m_n;
+        load_rm(wb + 64 + lane, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_of(wb + lane, i1, means2D, radii, gx, gy, x0, y0, w);
+        const int cnt = rect_from(r, m, gx, gy, x0, y0, w);
+        listed += (uint32_t)__builtin_popcountll(gs::ballot(cnt > 0));
         const Expansion e = expansion_begin(cnt);
         for (int k0 = 0; k0 < e.total; k0 += 64) {
             int owner;
@@ -280,6 +336,7 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
             }
         }
     }
+    if (lane == 0) wcount[(size_t)c * WAVES_PER_BIN + wave] = listed;
     if (lds) {
         __syncthreads();
         uint32_t* row = hist + (size_t)c * TL;
@@ -290,12 +347,26 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     }
 }
 
-// exclusive scan over local tiles -> tile_start, R -> meta[2..3]
+// exclusive scans: over local tiles -> tile_start, R -> meta[2..3]; over the
+// per-wave listed counts (in place) -> compact index bases, L -> meta[4]
 __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ meta, const uint32_t* __restrict__ tile_count,
-                                                        uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor)
+                                                        uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
+                                                        uint32_t* __restrict__ wcount, int NW)
 {
     __shared__ uint32_t s_wave[32];
     const int TL = (int)meta[0];
+    {
+        uint32_t base = 0;
+        for (int w0 = 0; w0 < NW; w0 += 1024) {
+            const int wi = w0 + threadIdx.x;
+            const uint32_t v = wi < NW ? wcount[wi] : 0u;
+            uint32_t tot;
+            const uint32_t pre = block_excl_scan_1024(v, s_wave, &tot);
+            if (wi < NW) wcount[wi] = base + pre;
+            base += tot;
+        }
+        if (threadIdx.x == 0) meta[4] = base;
+    }
     uint64_t base = 0;
     for (int t0 = 0; t0 < TL; t0 += 1024) {
         const int l = t0 + threadIdx.x;
@@ -334,46 +405,115 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
 
 // ------------------------------------------------------------- scatter
 
-// Re-walks the chunk and appends (depth bits << 32 | Gaussian id) to the
-// chunk's reserved slice of each tile bucket (LDS cursors).
+// Re-walks the chunk (each wave its run, as in the count) and appends
+// (depth bits << 32 | compact index) to the chunk's reserved slice of each
+// tile bucket (LDS cursors).  Compact indices follow Gaussian id order, so
+// sorting by them breaks depth ties exactly as sorting by id does.  Every
+// Gaussian gets its compact index or -1 (cidx_of); listed ones also get their
+// blend record, id (cid2id) and a zeroed gradient accumulator.
 __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
-    int P, int CH, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const float* __restrict__ depths,
-    const int* __restrict__ radii, const int* __restrict__ loc_map, const uint32_t* __restrict__ meta,
+    int P, int CH, int WS, unsigned gx, unsigned gy, const float2* __restrict__ means2D,
+    const float* __restrict__ depths, const int* __restrict__ radii, const float4* __restrict__ conic_opacity,
+    const float* __restrict__ rgb, const int* __restrict__ loc_map, const uint32_t* __restrict__ meta,
     const uint32_t* __restrict__ hist, const uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
-    uint64_t* __restrict__ sortkey)
+    const uint32_t* __restrict__ wbase, uint64_t* __restrict__ sortkey, int* __restrict__ cidx_of,
+    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, float4* __restrict__ gacc)
 {
-    __shared__ uint32_t s_cur[LDS_TILES];
+    // dynamic LDS: per wave 64 staged records, then min(T, LDS_TILES) cursors
+    extern __shared__ uint4 s_dyn[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float4* stage = reinterpret_cast<float4*>(s_dyn) + wave * 256;
+    uint32_t* s_cur = reinterpret_cast<uint32_t*>(s_dyn + WAVES_PER_BIN * 256);
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
     const bool all_local = TL == (int)(gx * gy);
     const int c = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lds) {
         const uint32_t* row = hist + (size_t)c * TL;
         for (int l = threadIdx.x; l < TL; l += BIN_THREADS) s_cur[l] = tile_start[l] + row[l];
         __syncthreads();
     }
-    const int i0 = c * CH;
-    const int i1 = min(P, i0 + CH);
-    for (int wb = i0 + wave * 64; wb < i1; wb += BIN_THREADS) {
+    const int i1c = min(P, c * CH + CH);
+    const int ws = min(i1c, c * CH + wave * WS);
+    const int i1 = min(i1c, ws + WS);
+    uint32_t next = wbase[(size_t)c * WAVES_PER_BIN + wave];
+    // software pipeline: the next group's radii and means are loaded while
+    // this group expands, and its depth / conic / colour once its radii are in
+    int r_n;
+    float2 m_n;
+    load_rm(ws + lane, i1, radii, means2D, r_n, m_n);
+    float d_n = 0.f;
+    float4 co_n = make_float4(0.f, 0.f, 0.f, 0.f);
+    float3 c_n = make_float3(0.f, 0.f, 0.f);
+    if (r_n > 0) {
+        const int i = ws + lane;
+        d_n = depths[i];
+        co_n = conic_opacity[i];
+        c_n = make_float3(rgb[3 * (size_t)i], rgb[3 * (size_t)i + 1], rgb[3 * (size_t)i + 2]);
+    }
+    for (int wb = ws; wb < i1; wb += 64) {
         const int i = wb + lane;
+        const int r = r_n;
+        const float2 xy = m_n;
+        const float dep = d_n;
+        const float4 co = co_n;
+        const float3 col = c_n;
+        load_rm(i + 64, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_of(i, i1, means2D, radii, gx, gy, x0, y0, w);
-        const uint32_t dbits = cnt ? gs::f2u(depths[i]) : 0u;
+        const int cnt = rect_from(r, xy, gx, gy, x0, y0, w);
+        const uint64_t lm = gs::ballot(cnt > 0);
+        const int nl = (int)__builtin_popcountll(lm);
+        const int rank = gs::rank_below(lm);
+        const uint32_t first = next;
+        const uint32_t cidx = first + (uint32_t)rank;
+        next += (uint32_t)nl;
+        uint32_t dbits = 0;
+        if (i < i1) cidx_of[i] = cnt > 0 ? (int)cidx : -1;
+        if (cnt > 0) {
+            dbits = gs::f2u(dep);
+            const gs::CullPrep cp = gs::cull_prepare(xy.x, xy.y, co.x, co.y, co.z, co.w);
+            float4* sp = stage + 4 * rank;
+            sp[0] = make_float4(xy.x, xy.y, co.x, co.y);
+            sp[1] = make_float4(co.z, co.w, col.x, col.y);
+            sp[2] = make_float4(col.z, cp.thresh, cp.nbc, cp.nba);
+            sp[3] = make_float4(__uint_as_float((uint32_t)i), 0.f, 0.f, 0.f);
+            cid2id[cidx] = (uint32_t)i;
+        }
+        // the group's records and zeroed accumulators are one contiguous run:
+        // write them with consecutive 16-byte stores (wave-private staging, so
+        // a wave-level barrier suffices)
+        __builtin_amdgcn_wave_barrier();
+        {
+            float4* rdst = rec + 4 * (size_t)first;
+            float4* gdst = gacc + 4 * (size_t)first;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int j = lane; j < 4 * nl; j += 64) {
+                rdst[j] = stage[j];
+                gdst[j] = z;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
         const Expansion e = expansion_begin(cnt);
         for (int k0 = 0; k0 < e.total; k0 += 64) {
             int owner;
             unsigned tx, ty;
             expansion_at(e, cnt, x0, y0, w, k0 + lane, owner, tx, ty);
             const uint32_t odb = (uint32_t)__shfl((int)dbits, owner, 64);
+            const uint32_t ocx = (uint32_t)__shfl((int)cidx, owner, 64);
             if (k0 + lane < e.total) {
                 const unsigned t = ty * gx + tx;
                 const int l = all_local ? (int)t : loc_map[t];
                 if (l >= 0) {
                     const uint32_t pos = lds ? atomicAdd(&s_cur[l], 1u) : atomicAdd(&cursor[l], 1u);
-                    sortkey[pos] = ((uint64_t)odb << 32) | (uint32_t)(wb + owner);
+                    sortkey[pos] = ((uint64_t)odb << 32) | ocx;
                 }
             }
+        }
+        if (r_n > 0) {
+            const int in = i + 64;
+            d_n = depths[in];
+            co_n = conic_opacity[in];
+            c_n = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
         }
     }
 }
@@ -414,24 +554,33 @@ __device__ __forceinline__ void bitonic(uint64_t* s, int n, int N)
     }
 }
 
+// sorted bucket -> Gaussian ids, tile|depth keys and the blend's compact list
+struct SortOut {
+    const uint32_t* cid2id;
+    uint32_t* point_list;
+    uint64_t* keys;
+    uint32_t* clist;
+};
+
 __device__ __forceinline__ void write_sorted(uint32_t tile, uint32_t start, int n, const uint64_t* src,
-                                             uint32_t* __restrict__ point_list, uint64_t* __restrict__ keys, int nt)
+                                             const SortOut& o, int nt)
 {
     for (int i = threadIdx.x; i < n; i += nt) {
         const uint64_t k = src[i];
-        point_list[start + i] = (uint32_t)k;
-        keys[start + i] = ((uint64_t)tile << 32) | (k >> 32);
+        const uint32_t cx = (uint32_t)k;
+        o.clist[start + i] = cx;
+        o.point_list[start + i] = o.cid2id[cx];
+        o.keys[start + i] = ((uint64_t)tile << 32) | (k >> 32);
     }
 }
 
 // One block per local tile whose bucket size lies in (LO, CAP]: the bucket is
-// sorted by (depth bits, Gaussian id) in LDS.  Three size classes keep the
+// sorted by (depth bits, compact index) in LDS.  Three size classes keep the
 // LDS footprint (and so the occupancy) matched to the bucket.
 template <int CAP, int NT, int LO>
 __global__ __launch_bounds__(NT) void tilesort_kernel(
     const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
-    const uint32_t* __restrict__ tile_start, const uint64_t* __restrict__ sortkey, uint32_t* __restrict__ point_list,
-    uint64_t* __restrict__ keys)
+    const uint32_t* __restrict__ tile_start, const uint64_t* __restrict__ sortkey, SortOut out)
 {
     __shared__ uint64_t s[CAP];
     const int l = blockIdx.x;
@@ -444,15 +593,14 @@ __global__ __launch_bounds__(NT) void tilesort_kernel(
     for (int i = threadIdx.x; i < n; i += NT) s[i] = sortkey[start + i];
     __syncthreads();
     bitonic<NT>(s, n, N);
-    write_sorted((uint32_t)tile_of_local[l], start, n, s, point_list, keys, NT);
+    write_sorted((uint32_t)tile_of_local[l], start, n, s, out, NT);
 }
 
 // Buckets larger than the biggest LDS class: the same network in global
 // memory, in place.
 __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
     const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
-    const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ point_list,
-    uint64_t* __restrict__ keys)
+    const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, SortOut out)
 {
     const int l = blockIdx.x;
     if (l >= (int)meta[0]) return;
@@ -463,33 +611,85 @@ __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
     int N = 1;
     while (N < n) N <<= 1;
     bitonic<BIG_SORT_THREADS>(s, n, N);
-    write_sorted((uint32_t)tile_of_local[l], start, n, s, point_list, keys, BIG_SORT_THREADS);
+    write_sorted((uint32_t)tile_of_local[l], start, n, s, out, BIG_SORT_THREADS);
 }
 
 // ------------------------------------------------------------- blend
 
-// block b -> (tile, quadrant): the four quadrant waves of a tile land on the
-// same XCD (workgroups are dispatched to the 8 XCDs round-robin)
-__device__ __forceinline__ void block_to_tile(unsigned b, unsigned& tile, unsigned& quad)
+// Blend blocks -> (tile, quadrant).  Workgroups are dispatched to the 8 XCDs
+// round-robin (block b runs on XCD b % 8) and each XCD has its own L2.  Tiles
+// are grouped into 8x8-tile supertiles; supertile s belongs to XCD s % 8, and
+// an XCD's blocks walk its supertiles in order, four quadrant waves per tile,
+// so the waves resident on one XCD cover a compact patch of the image and
+// share the records of the Gaussians overlapping it in that XCD's L2.
+constexpr unsigned SUPER = 8;
+constexpr unsigned BLOCKS_PER_SUPER = SUPER * SUPER * 4;
+
+__device__ __forceinline__ bool block_to_tile(unsigned b, unsigned gx, unsigned gy, unsigned sgx, unsigned NS,
+                                              unsigned& tile, unsigned& quad, unsigned& tx, unsigned& ty)
 {
     const unsigned xcd = b & 7u, slot = b >> 3;
-    quad = slot & 3u;
-    tile = (slot >> 2) * 8u + xcd;
+    const unsigned st = (slot / BLOCKS_PER_SUPER) * 8u + xcd;
+    if (st >= NS) return false;
+    const unsigned loc = slot % BLOCKS_PER_SUPER;
+    quad = loc & 3u;
+    const unsigned t = loc >> 2;
+    tx = (st % sgx) * SUPER + (t % SUPER);
+    ty = (st / sgx) * SUPER + (t / SUPER);
+    if (tx >= gx || ty >= gy) return false;
+    tile = ty * gx + tx;
+    return true;
+}
+
+struct Rec {
+    float4 q0, q1, q2;
+    uint32_t gid;   // Gaussian id (loaded only WITH_ID)
+};
+
+template <bool WITH_ID>
+__device__ __forceinline__ Rec load_rec(const float4* __restrict__ rec, uint32_t cx)
+{
+    const float4* r = rec + 4 * (size_t)cx;
+    Rec o{r[0], r[1], r[2], 0u};
+    if (WITH_ID) o.gid = __float_as_uint(r[3].x);
+    return o;
+}
+
+__device__ __forceinline__ bool rec_may_touch(const Rec& r, float x0, float y0, float x1, float y1)
+{
+    return gs::may_touch_prepared(r.q2.y, r.q2.z, r.q2.w, r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, x0, y0, x1, y1);
+}
+
+// wave-private staging slots of one batch of 64 list entries
+struct Stage {
+    float4 a[64];   // x, y, -a/2, -b
+    float4 b[64];   // -c/2, opacity, r, g
+    float2 c[64];   // blue, tag bits
+    int pos[64];    // position in the tile's list
+};
+
+// stages entry k of the list; `tag` (Gaussian id in the forward, compact
+// index in the backward) rides along in the blue slot's partner
+__device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uint32_t tag, int k)
+{
+    st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
+    st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
+    st.c[slot] = make_float2(r.q2.x, __uint_as_float(tag));
+    st.pos[slot] = k;
 }
 
 __global__ __launch_bounds__(64) void render_fwd_kernel(
-    int W, int H, unsigned gx, unsigned T, const uint2* __restrict__ ranges, const uint32_t* __restrict__ point_list,
-    const float2* __restrict__ means2D, const float4* __restrict__ conic_opacity, const float* __restrict__ rgb,
-    const uint8_t* __restrict__ cl, const float* __restrict__ bg, float* __restrict__ out_color,
-    float* __restrict__ final_T, uint32_t* __restrict__ n_contrib_px, uint32_t* __restrict__ n_contrib2loss_px,
-    int32_t* __restrict__ out_observe, int32_t* __restrict__ n_consider, int32_t* __restrict__ n_contrib_tile)
+    int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
+    const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
+    const float* __restrict__ bg, float* __restrict__ out_color, float* __restrict__ final_T,
+    uint32_t* __restrict__ n_contrib_px, uint32_t* __restrict__ n_contrib2loss_px, int32_t* __restrict__ out_observe,
+    int32_t* __restrict__ n_consider, int32_t* __restrict__ n_contrib_tile)
 {
-    unsigned tile, quad;
-    block_to_tile(blockIdx.x, tile, quad);
-    if (tile >= T) return;
+    unsigned tile, quad, tx, ty;
+    if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
     const int lane = threadIdx.x;
-    const int px = (int)(tile % gx) * 16 + (int)(quad & 1u) * 8 + (lane & 7);
-    const int py = (int)(tile / gx) * 16 + (int)(quad >> 1) * 8 + (lane >> 3);
+    const int qx = (int)tx * 16 + (int)(quad & 1u) * 8, qy = (int)ty * 16 + (int)(quad >> 1) * 8;
+    const int px = qx + (lane & 7), py = qy + (lane >> 3);
     const bool inside = px < W && py < H;
     const size_t pid = (size_t)py * W + px;
     const size_t HW = (size_t)H * W;
@@ -500,50 +700,43 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         }
         return;
     }
-    __shared__ float4 s_a[64];   // x, y, -a/2, -b
-    __shared__ float4 s_b[64];   // -c/2, opacity, r, g
-    __shared__ float2 s_c[64];   // blue, id bits
-    __shared__ int s_pos[64];    // position in the tile's list
+    __shared__ Stage st;
 
     const uint2 range = ranges[tile];
     const int n = (int)(range.y - range.x);
+    const uint32_t* list = clist + range.x;
     const float pxf = (float)px, pyf = (float)py;
-    const float qx0 = (float)((int)(tile % gx) * 16 + (int)(quad & 1u) * 8);
-    const float qy0 = (float)((int)(tile / gx) * 16 + (int)(quad >> 1) * 8);
+    const float qx0 = (float)qx, qy0 = (float)qy;
     const float alpha_min = 1.0f / 255.0f;
     float T_ = 1.0f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     uint32_t last = 0, n2l = 0;
     bool done = !inside;
 
+    // software pipeline: while a batch blends, the next batch's records and
+    // the list entries of the batch after it are in flight
+    uint32_t id_cur = lane < n ? list[lane] : 0u;
+    uint32_t id_nxt = 64 + lane < n ? list[64 + lane] : 0u;
+    Rec r_cur{};
+    if (lane < n) r_cur = load_rec<true>(rec, id_cur);
+
     for (int base = 0; base < n; base += 64) {
         if (gs::ballot(!done) == 0) break;
-        // stage the batch, keeping only Gaussians that can reach this quadrant
         const int k = base + lane;
-        bool keep = false;
-        uint32_t id = 0;
-        float2 xy = make_float2(0.f, 0.f);
-        float4 co = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k < n) {
-            id = point_list[range.x + k];
-            xy = means2D[id];
-            co = conic_opacity[id];
-            keep = gs::may_touch(xy.x, xy.y, co.x, co.y, co.z, co.w, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
-        }
+        Rec r_nxt{};
+        uint32_t id_nn = 0;
+        if (k + 64 < n) r_nxt = load_rec<true>(rec, id_nxt);
+        if (k + 128 < n) id_nn = list[k + 128];
+        // stage the batch, keeping only Gaussians that can reach this quadrant
+        const bool keep = k < n && rec_may_touch(r_cur, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
         const uint64_t km = gs::ballot(keep);
-        if (keep) {
-            const int slot = gs::rank_below(km);
-            s_a[slot] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
-            s_b[slot] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
-            s_c[slot] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
-            s_pos[slot] = k;
-        }
+        if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
             if (gs::ballot(!done) == 0) break;
-            const float4 A = s_a[j];
-            const float4 B = s_b[j];
-            const float2 Cc = s_c[j];
+            const float4 A = st.a[j];
+            const float4 B = st.b[j];
+            const float2 Cc = st.c[j];
             bool observe = false;
             if (!done) {
                 const float dx = A.x - pxf, dy = A.y - pyf;
@@ -561,7 +754,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
                         C1 = __builtin_fmaf(B.w, wgt, C1);
                         C2 = __builtin_fmaf(Cc.x, wgt, C2);
                         T_ = test_T;
-                        last = (uint32_t)s_pos[j] + 1u;
+                        last = (uint32_t)st.pos[j] + 1u;
                     }
                 }
             }
@@ -570,6 +763,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
                 atomicAdd(&out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
         }
         __syncthreads();
+        r_cur = r_nxt;
+        id_cur = id_nxt;
+        id_nxt = id_nn;
     }
 
     if (inside) {
@@ -594,31 +790,45 @@ __global__ __launch_bounds__(256) void zero_i32_kernel(int n, int32_t* __restric
     if (i < n) p[i] = 0;
 }
 
-__global__ __launch_bounds__(256) void zero_grads_kernel(int P, int m2d_stride, float* __restrict__ g_m2d,
-                                                         float* __restrict__ g_m2d_abs, float4* __restrict__ g_con,
-                                                         float* __restrict__ g_col)
+// Writes the render backward's outputs for every Gaussian from its
+// accumulator (listed Gaussians, whose accumulator is then cleared for the
+// next backward) or zeros; one thread per Gaussian.
+__global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __restrict__ cidx_of,
+                                                           float4* __restrict__ gacc, int m2d_stride,
+                                                           float* __restrict__ g_m2d, float* __restrict__ g_m2d_abs,
+                                                           float4* __restrict__ g_con, float* __restrict__ g_col)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= P) return;
-    for (int k = 0; k < m2d_stride; k++) g_m2d[(size_t)i * m2d_stride + k] = 0.f;
-    g_m2d_abs[3 * (size_t)i] = 0.f; g_m2d_abs[3 * (size_t)i + 1] = 0.f; g_m2d_abs[3 * (size_t)i + 2] = 0.f;
-    g_con[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    g_col[3 * (size_t)i] = 0.f; g_col[3 * (size_t)i + 1] = 0.f; g_col[3 * (size_t)i + 2] = 0.f;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a = z, b = z, c = z;
+    const int cx = cidx_of != nullptr ? cidx_of[i] : -1;
+    if (cx >= 0) {
+        float4* g = gacc + 4 * (size_t)cx;
+        a = g[0]; b = g[1]; c = g[2];
+        g[0] = z; g[1] = z; g[2] = z; g[3] = z;
+    }
+    float* m = g_m2d + (size_t)i * m2d_stride;
+    m[0] = a.x;
+    m[1] = a.y;
+    for (int k = 2; k < m2d_stride; k++) m[k] = 0.f;
+    g_m2d_abs[3 * (size_t)i] = a.z; g_m2d_abs[3 * (size_t)i + 1] = a.w; g_m2d_abs[3 * (size_t)i + 2] = 0.f;
+    g_con[i] = b;
+    g_col[3 * (size_t)i] = c.x; g_col[3 * (size_t)i + 1] = c.y; g_col[3 * (size_t)i + 2] = c.z;
 }
 
 __global__ __launch_bounds__(64) void render_bwd_kernel(
-    int W, int H, unsigned gx, unsigned T, const uint2* __restrict__ ranges, const uint32_t* __restrict__ point_list,
-    const float2* __restrict__ means2D, const float4* __restrict__ conic_opacity, const float* __restrict__ rgb,
-    const uint8_t* __restrict__ cl, const float* __restrict__ bg, const float* __restrict__ final_T,
-    const uint32_t* __restrict__ n_contrib_px, const float* __restrict__ dL_dpixels, float* __restrict__ g_m2d,
-    int m2d_stride, float* __restrict__ g_m2d_abs, float* __restrict__ g_con, float* __restrict__ g_col)
+    int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
+    const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
+    const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
+    const float* __restrict__ dL_dpixels, float* __restrict__ gacc)
 {
-    unsigned tile, quad;
-    block_to_tile(blockIdx.x, tile, quad);
-    if (tile >= T || !cl[tile]) return;
+    unsigned tile, quad, tx, ty;
+    if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
+    if (!cl[tile]) return;
     const int lane = threadIdx.x;
-    const int px = (int)(tile % gx) * 16 + (int)(quad & 1u) * 8 + (lane & 7);
-    const int py = (int)(tile / gx) * 16 + (int)(quad >> 1) * 8 + (lane >> 3);
+    const int qx = (int)tx * 16 + (int)(quad & 1u) * 8, qy = (int)ty * 16 + (int)(quad >> 1) * 8;
+    const int px = qx + (lane & 7), py = qy + (lane >> 3);
     const bool inside = px < W && py < H;
     const size_t pid = (size_t)py * W + px;
     const size_t HW = (size_t)H * W;
@@ -630,69 +840,45 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     const int maxlast = gs::wave_max_i(last);
     if (maxlast == 0) return;
 
-    __shared__ float4 s_a[64];   // x, y, -a/2, -b
-    __shared__ float4 s_b[64];   // -c/2, opacity, r, g
-    __shared__ float2 s_c[64];   // blue, id bits
-    __shared__ int s_pos[64];    // position in the tile's list
+    __shared__ Stage st;
 
-    const uint2 range = ranges[tile];
+    const uint32_t* list = clist + ranges[tile].x;
     const float pxf = (float)px, pyf = (float)py;
-    const float qx0 = (float)((int)(tile % gx) * 16 + (int)(quad & 1u) * 8);
-    const float qy0 = (float)((int)(tile / gx) * 16 + (int)(quad >> 1) * 8);
+    const float qx0 = (float)qx, qy0 = (float)qy;
     const float alpha_min = 1.0f / 255.0f;
     const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
     const float bg_dot = bg[0] * dp0 + bg[1] * dp1 + bg[2] * dp2;
-    // after the wave reduction this lane holds the total of one gradient term:
-    // its array, row stride and offset
-    float* my_dst = nullptr;
-    int my_stride = 0;
-    switch (gs::wave_sum12_index(lane)) {
-        case 0: my_dst = g_m2d; my_stride = m2d_stride; break;
-        case 1: my_dst = g_m2d + 1; my_stride = m2d_stride; break;
-        case 2: my_dst = g_m2d_abs; my_stride = 3; break;
-        case 3: my_dst = g_m2d_abs + 1; my_stride = 3; break;
-        case 4: my_dst = g_con; my_stride = 4; break;
-        case 5: my_dst = g_con + 1; my_stride = 4; break;
-        case 6: my_dst = g_con + 2; my_stride = 4; break;
-        case 7: my_dst = g_con + 3; my_stride = 4; break;
-        case 8: my_dst = g_col; my_stride = 3; break;
-        case 9: my_dst = g_col + 1; my_stride = 3; break;
-        case 10: my_dst = g_col + 2; my_stride = 3; break;
-        default: break;
-    }
+    // after the wave reduction this lane holds the total of gradient term
+    // my_k (accumulator slot), or nothing (my_k < 0)
+    const int my_k = gs::wave_sum12_index(lane);
     float T_ = T_final;
     float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
     float lc0 = 0.f, lc1 = 0.f, lc2 = 0.f, last_alpha = 0.f;
 
-    // walk positions maxlast-1 .. 0 of the tile's list, back to front
+    // walk positions maxlast-1 .. 0 of the tile's list, back to front, with
+    // the same software pipeline as the forward
+    uint32_t id_cur = maxlast - 1 - lane >= 0 ? list[maxlast - 1 - lane] : 0u;
+    uint32_t id_nxt = maxlast - 65 - lane >= 0 ? list[maxlast - 65 - lane] : 0u;
+    Rec r_cur{};
+    if (maxlast - 1 - lane >= 0) r_cur = load_rec<false>(rec, id_cur);
+
     for (int top = maxlast; top > 0; top -= 64) {
-        // stage positions top-1, top-2, ... keeping only Gaussians that can reach this quadrant
         const int k = top - 1 - lane;
-        bool keep = false;
-        uint32_t id = 0;
-        float2 xy = make_float2(0.f, 0.f);
-        float4 co = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k >= 0) {
-            id = point_list[range.x + k];
-            xy = means2D[id];
-            co = conic_opacity[id];
-            keep = gs::may_touch(xy.x, xy.y, co.x, co.y, co.z, co.w, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
-        }
+        Rec r_nxt{};
+        uint32_t id_nn = 0;
+        if (k - 64 >= 0) r_nxt = load_rec<false>(rec, id_nxt);
+        if (k - 128 >= 0) id_nn = list[k - 128];
+        // stage positions top-1, top-2, ... keeping only Gaussians that can reach this quadrant
+        const bool keep = k >= 0 && rec_may_touch(r_cur, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
         const uint64_t km = gs::ballot(keep);
-        if (keep) {
-            const int slot = gs::rank_below(km);
-            s_a[slot] = make_float4(xy.x, xy.y, -0.5f * co.x, -co.y);
-            s_b[slot] = make_float4(-0.5f * co.z, co.w, rgb[3 * id], rgb[3 * id + 1]);
-            s_c[slot] = make_float2(rgb[3 * id + 2], __uint_as_float(id));
-            s_pos[slot] = k;
-        }
+        if (keep) stage_put(st, gs::rank_below(km), r_cur, id_cur, k);
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
-            const int ci = s_pos[j];   // position in the tile's list
-            const float4 A = s_a[j];
-            const float4 B = s_b[j];
-            const float2 Cc = s_c[j];
+            const int ci = st.pos[j];   // position in the tile's list
+            const float4 A = st.a[j];
+            const float4 B = st.b[j];
+            const float2 Cc = st.c[j];
             float gmx = 0.f, gmy = 0.f, gca = 0.f, gcb = 0.f, gcc = 0.f, gop = 0.f;
             float gc0 = 0.f, gc1 = 0.f, gc2 = 0.f;
             bool valid = false;
@@ -733,19 +919,36 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             }
             const uint64_t vm = gs::ballot(valid);
             if (vm == 0) continue;
-            const uint32_t id = __float_as_uint(Cc.y);
+            const uint32_t cx = __float_as_uint(Cc.y);
             const float vals[12] = {gmx, gmy, __builtin_fabsf(gmx), __builtin_fabsf(gmy), gca, gcb, gcc, gop,
                                     gc0, gc1, gc2, 0.f};
             const float tot = gs::wave_sum12(vals);
-            if (my_dst != nullptr && tot != 0.f) unsafeAtomicAdd(my_dst + (size_t)id * my_stride, tot);
+            // the eleven totals of one Gaussian land in one 64-byte accumulator
+            if (my_k >= 0 && my_k < 11 && tot != 0.f) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
         }
         __syncthreads();
+        r_cur = r_nxt;
+        id_cur = id_nxt;
+        id_nxt = id_nn;
     }
 }
 
 }  // namespace
 
 // ====================================================================== C ABI
+
+namespace {
+size_t count_lds_bytes(int T) { return sizeof(uint32_t) * (size_t)(T < LDS_TILES ? T : LDS_TILES); }
+size_t scatter_lds_bytes(int T) { return sizeof(float4) * 256 * WAVES_PER_BIN + count_lds_bytes(T); }
+
+// grid of the blend kernels: whole supertiles per XCD
+unsigned blend_grid(unsigned gx, unsigned gy, unsigned& sgx, unsigned& NS)
+{
+    sgx = (gx + SUPER - 1) / SUPER;
+    NS = sgx * ((gy + SUPER - 1) / SUPER);
+    return ((NS + 7u) / 8u) * 8u * BLOCKS_PER_SUPER;
+}
+}  // namespace
 
 extern "C" size_t gs_render_geom_bytes(int P, int W, int H) { return geom_layout(P, W, H).total; }
 extern "C" size_t gs_render_binning_bytes(int64_t R) { return bin_layout(R).total; }
@@ -787,11 +990,16 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
                        tile_of_local, tile_count, meta));
     GS_LAUNCH_CHECK("localmap_kernel");
     if (P > 0) {
-        GS_TIMED("count_kernel", stream, hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
-                           reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count));
+        GS_TIMED("count_kernel", stream,
+                 hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream, P,
+                                    g.CH, g.WS, gx, gy,
+                                    reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count,
+                                    at<uint32_t>(geom, g.wcount)));
         GS_LAUNCH_CHECK("count_kernel");
     }
-    GS_TIMED("tilescan_kernel", stream, hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor));
+    GS_TIMED("tilescan_kernel", stream,
+             hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
+                                at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0));
     GS_LAUNCH_CHECK("tilescan_kernel");
     uint32_t hR[2] = {0, 0};
     GS_HIP(hipMemcpyAsync(hR, meta + 2, sizeof(hR), hipMemcpyDeviceToHost, stream));
@@ -840,42 +1048,50 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
         GS_LAUNCH_CHECK("zero_i32_kernel");
     }
     if (R > 0) {
-        GS_TIMED("scatter_kernel", stream, hipLaunchKernelGGL(scatter_kernel, dim3(g.NC), dim3(BIN_THREADS), 0, stream, P, g.CH, gx, gy,
-                           reinterpret_cast<const float2*>(means2D), depths, radii, loc_map, meta, hist,
-                           tile_start, cursor, sortkey));
+        GS_TIMED("scatter_kernel", stream,
+                 hipLaunchKernelGGL(scatter_kernel, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T), stream, P,
+                                    g.CH, g.WS, gx, gy,
+                                    reinterpret_cast<const float2*>(means2D), depths, radii,
+                                    reinterpret_cast<const float4*>(conic_opacity), rgb, loc_map, meta, hist,
+                                    tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
+                                    at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec),
+                                    at<float4>(geom, g.gacc)));
         GS_LAUNCH_CHECK("scatter_kernel");
+        const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};
         GS_TIMED("tilesort_kernel_s", stream,
                  hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_S, 256, 0>), dim3(T), dim3(256), 0, stream, meta,
-                                    tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+                                    tile_of_local, tile_count, tile_start, sortkey, sout));
         GS_LAUNCH_CHECK("tilesort_kernel<S>");
         GS_TIMED("tilesort_kernel_m", stream,
                  hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_M, 512, SORT_CAP_S>), dim3(T), dim3(512), 0, stream,
-                                    meta, tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+                                    meta, tile_of_local, tile_count, tile_start, sortkey, sout));
         GS_LAUNCH_CHECK("tilesort_kernel<M>");
         GS_TIMED("tilesort_kernel_l", stream,
                  hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_L, 1024, SORT_CAP_M>), dim3(T), dim3(1024), 0, stream,
-                                    meta, tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+                                    meta, tile_of_local, tile_count, tile_start, sortkey, sout));
         GS_LAUNCH_CHECK("tilesort_kernel<L>");
         GS_TIMED("tilesort_big_kernel", stream,
                  hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta,
-                                    tile_of_local, tile_count, tile_start, sortkey, point_list, keys));
+                                    tile_of_local, tile_count, tile_start, sortkey, sout));
         GS_LAUNCH_CHECK("tilesort_big_kernel");
     }
-    const unsigned nblk = ((T + 7u) / 8u) * 32u;
-    GS_TIMED("render_fwd_kernel", stream, hipLaunchKernelGGL(render_fwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T, ranges, point_list,
-                       reinterpret_cast<const float2*>(means2D), reinterpret_cast<const float4*>(conic_opacity), rgb,
-                       compute_locally, bg, out_color, at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib),
-                       at<uint32_t>(img, il.n_contrib2loss), out_observe, n_consider, n_contrib));
+    unsigned sgx, NS;
+    const unsigned nblk = blend_grid(gx, gy, sgx, NS);
+    GS_TIMED("render_fwd_kernel", stream,
+             hipLaunchKernelGGL(render_fwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS, ranges,
+                                at<const uint32_t>(binning, bl.clist), at<const float4>(geom, g.rec),
+                                compute_locally, bg, out_color,
+                                at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib),
+                                at<uint32_t>(img, il.n_contrib2loss), out_observe, n_consider, n_contrib));
     GS_LAUNCH_CHECK("render_fwd_kernel");
-    (void)gy;
     return GS_OK;
 }
 
 extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                                   const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
-                                  const void* binning, const void* img, const float* dL_dpixels, float* dL_dmeans2D,
-                                  int dL_dmeans2D_stride, float* dL_dmeans2D_abs, float* dL_dconic_opacity,
-                                  float* dL_dcolors, hipStream_t stream)
+                                  void* geom, const void* binning, const void* img, const float* dL_dpixels,
+                                  float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
+                                  float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
@@ -883,22 +1099,30 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
                ((uintptr_t)means2D & 7) == 0,
                "conic_opacity / dL_dconic_opacity must be 16-byte and means2D 8-byte aligned");
+    GS_REQUIRE(geom != nullptr, "geom must be the forward's geometry workspace");
+    (void)rgb;
     if (P == 0) return GS_OK;
+    const GeomLayout g = geom_layout(P, W, H);
     const ImgLayout il = img_layout(W, H);
     const BinLayout bl = bin_layout(R);
     const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
-    const unsigned T = gx * gy;
-    GS_TIMED("zero_grads_kernel", stream, hipLaunchKernelGGL(zero_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
-                       dL_dmeans2D_stride, dL_dmeans2D, dL_dmeans2D_abs, reinterpret_cast<float4*>(dL_dconic_opacity),
-                       dL_dcolors));
-    GS_LAUNCH_CHECK("zero_grads_kernel");
-    if (R == 0) return GS_OK;
-    const unsigned nblk = ((T + 7u) / 8u) * 32u;
-    GS_TIMED("render_bwd_kernel", stream, hipLaunchKernelGGL(render_bwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, T,
-                       at<uint2>(img, il.ranges), at<uint32_t>(binning, bl.point_list),
-                       reinterpret_cast<const float2*>(means2D), reinterpret_cast<const float4*>(conic_opacity), rgb,
-                       compute_locally, bg, at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
-                       dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors));
-    GS_LAUNCH_CHECK("render_bwd_kernel");
+    float4* gacc = at<float4>(geom, g.gacc);
+    if (R > 0) {
+        unsigned sgx, NS;
+        const unsigned nblk = blend_grid(gx, gy, sgx, NS);
+        GS_TIMED("render_bwd_kernel", stream,
+                 hipLaunchKernelGGL(render_bwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS,
+                                    at<uint2>(img, il.ranges), at<const uint32_t>(binning, bl.clist),
+                                    at<const float4>(geom, g.rec), compute_locally, bg, at<float>(img, il.final_T),
+                                    at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+        GS_LAUNCH_CHECK("render_bwd_kernel");
+    }
+    // without instances the forward wrote no flags: every output is zero
+    GS_TIMED("unpack_grads_kernel", stream,
+             hipLaunchKernelGGL(unpack_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
+                                R > 0 ? at<const int>(geom, g.cidx_of) : nullptr, gacc, dL_dmeans2D_stride,
+                                dL_dmeans2D, dL_dmeans2D_abs, reinterpret_cast<float4*>(dL_dconic_opacity),
+                                dL_dcolors));
+    GS_LAUNCH_CHECK("unpack_grads_kernel");
     return GS_OK;
 }

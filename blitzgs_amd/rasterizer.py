@@ -234,7 +234,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     return R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms
 
 
-def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, binning, img, dL_dpixels,
+def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img, dL_dpixels,
                          m2d_stride=2, timing=False):
     dev = means2D.device
     P = means2D.size(0)
@@ -254,7 +254,7 @@ def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_local
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
     check(lib.gs_render_backward(P, R, W, H, ptr(bg), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
-                                 ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D), m2d_stride,
+                                 ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D), m2d_stride,
                                  ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors), _stream(dev)),
           "gs_render_backward")
     ms = None
@@ -302,7 +302,7 @@ class _RenderGaussians(torch.autograd.Function):
             grad_color = torch.zeros((3, H, W), device=means2D.device, dtype=torch.float32)
         timing = _want_timing(ctx.cuda_args)
         dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
-            rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, binning, img,
+            rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
             grad_color.contiguous(), 2, timing)
         if timing:
             ctx.cuda_args["stats_collector"]["backward_render_time"] = ms

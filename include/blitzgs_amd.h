@@ -106,7 +106,8 @@ int gs_render_forward_count(int P, int image_width, int image_height, const floa
 /* Duplicate, sort, range and blend.  Outputs: out_color (3,H,W),
  * n_render / n_consider / n_contrib int32 (tiles), out_observe int32 (P).
  * The sorted tile|depth keys and Gaussian ids stay in `binning`, the ranges
- * and per-pixel state in `img`, for gs_render_backward. */
+ * and per-pixel state in `img`, and a packed 64-byte copy of each listed
+ * Gaussian's means2D / conic_opacity / rgb in `geom`, for gs_render_backward. */
 int gs_render_forward(int P, int64_t R, int image_width, int image_height, const float* bg,
                       const float* means2D, const float* depths, const int* radii,
                       const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
@@ -117,12 +118,16 @@ int gs_render_forward(int P, int64_t R, int image_width, int image_height, const
 /* Render backward.  Replaces RenderGaussiansBackwardCUDA
  * (diff-gaussian-rasterization_r/rasterize_points.cu:363-436; kernel
  * cuda_rasterizer/backward.cu:324-530).
+ *   geom / binning / img: the forward's workspaces (geom also holds the
+ *   gradient accumulators, cleared again on exit, so calls sharing one geom
+ *   must not overlap).  means2D / conic_opacity / rgb: the forward's inputs
+ *   (the kernels read the forward's packed copy of them in geom).
  *   dL_dpixels (3,H,W).  Outputs: dL_dmeans2D (row stride dL_dmeans2D_stride,
  *   2 or 3; the third column, when present, is zero), dL_dmeans2D_abs (P,3),
  *   dL_dconic_opacity (P,4) = [c00, c01, c11, opacity], dL_dcolors (P,3). */
 int gs_render_backward(int P, int64_t R, int image_width, int image_height, const float* bg,
                        const float* means2D, const float* conic_opacity, const float* rgb,
-                       const uint8_t* compute_locally, const void* binning, const void* img,
+                       const uint8_t* compute_locally, void* geom, const void* binning, const void* img,
                        const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
                        float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
                        gs_stream_t stream);

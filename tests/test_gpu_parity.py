@@ -218,7 +218,7 @@ def test_render_backward_vs_oracle_with_background():
                                 dev["conic_opacity"], dev["rgb"], None)
     Rn, color, *_rest, geom, binning, img, _ = out
     g = R._render_backward_raw(rs.bg, Rn, cam["H"], cam["W"], dev["means2D"], dev["conic_opacity"], dev["rgb"],
-                               None, binning, img, to_dev(dLd), m2d_stride=3)
+                               None, geom, binning, img, to_dev(dLd), m2d_stride=3)
     dm, dma, dco, dcol, _ = g
     assert rel_l2(np_(dm), rb["dL_dmeans2D"]) < 1e-3
     assert not np_(dm)[:, 2].any()
@@ -269,7 +269,7 @@ def test_quadrant_cull_keeps_results_exact_on_hard_cases():
                                 dev["rgb"], None)
     Rn, *_rest, geom, binning, img, _ = out
     dm, dma, dco, dcol, _ = R._render_backward_raw(rs.bg, Rn, H, W, dev["means2D"], dev["conic_opacity"],
-                                                   dev["rgb"], None, binning, img, to_dev(dLd), m2d_stride=3)
+                                                   dev["rgb"], None, geom, binning, img, to_dev(dLd), m2d_stride=3)
     for g, r, nm in ((dm, rb["dL_dmeans2D"], "dmean2D"), (dma, rb["dL_dmeans2D_abs"], "abs"),
                      (dco, rb["dL_dconic_opacity"], "conic_opacity"), (dcol, rb["dL_dcolors"], "colors")):
         assert rel_l2(np_(g), r) < 1e-3, nm

@@ -664,8 +664,7 @@ __device__ __forceinline__ bool rec_may_touch(const Rec& r, float x0, float y0, 
 struct Stage {
     float4 a[64];   // x, y, -a/2, -b
     float4 b[64];   // -c/2, opacity, r, g
-    float2 c[64];   // blue, tag bits
-    int pos[64];    // position in the tile's list
+    float4 c[64];   // blue, tag bits, position in the tile's list (bits), 0
 };
 
 // stages entry k of the list; `tag` (Gaussian id in the forward, compact
@@ -674,8 +673,7 @@ __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uin
 {
     st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
     st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
-    st.c[slot] = make_float2(r.q2.x, __uint_as_float(tag));
-    st.pos[slot] = k;
+    st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k), 0.f);
 }
 
 __global__ __launch_bounds__(64) void render_fwd_kernel(
@@ -732,35 +730,42 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
-        for (int j = 0; j < cnt; j++) {
-            if (gs::ballot(!done) == 0) break;
-            const float4 A = st.a[j];
-            const float4 B = st.b[j];
-            const float2 Cc = st.c[j];
-            bool observe = false;
-            if (!done) {
-                const float dx = A.x - pxf, dy = A.y - pyf;
-                const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-                const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
-                if (!(power > 0.0f) && !(alpha < alpha_min)) {
-                    const float test_T = T_ * (1.0f - alpha);
-                    if (test_T < 0.0001f) {
-                        done = true;
-                    } else {
-                        observe = T_ > 0.5f;
-                        n2l++;
-                        const float wgt = alpha * T_;
-                        C0 = __builtin_fmaf(B.z, wgt, C0);
-                        C1 = __builtin_fmaf(B.w, wgt, C1);
-                        C2 = __builtin_fmaf(Cc.x, wgt, C2);
-                        T_ = test_T;
-                        last = (uint32_t)st.pos[j] + 1u;
-                    }
-                }
-            }
+        // Branch-free blend of one staged entry: every lane evaluates it and
+        // the state changes are selects, so no exec-mask bookkeeping.
+        auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
+            const float dx = A.x - pxf, dy = A.y - pyf;
+            const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
+            const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
+            const float test_T = T_ * (1.0f - alpha);
+            const bool use = !done && !(power > 0.0f) && !(alpha < alpha_min);
+            const bool fin = use && test_T < 0.0001f;
+            const bool upd = use && !fin;
+            const bool observe = upd && T_ > 0.5f;
+            const float wgt = alpha * T_;
+            C0 = upd ? __builtin_fmaf(B.z, wgt, C0) : C0;
+            C1 = upd ? __builtin_fmaf(B.w, wgt, C1) : C1;
+            C2 = upd ? __builtin_fmaf(Cc.x, wgt, C2) : C2;
+            T_ = upd ? test_T : T_;
+            n2l += upd ? 1u : 0u;
+            last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : last;
+            done = done || fin;
             const uint64_t m = gs::ballot(observe);
-            if (m != 0 && lane == (int)__builtin_ctzll(m))
-                atomicAdd(&out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
+            if (m != 0) {
+                const int first = (int)__builtin_ctzll(m);
+                if (lane == first) atomicAdd(&out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
+            }
+        };
+        // two register sets in turn: the next entry's LDS reads are issued
+        // before this entry's arithmetic
+        float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
+        float4 A1, B1, D1;
+        for (int j = 0; j < cnt; j += 2) {
+            if (gs::ballot(!done) == 0) break;
+            A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
+            blend(A0, B0, D0);
+            if (j + 1 >= cnt || gs::ballot(!done) == 0) break;
+            A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
+            blend(A1, B1, D1);
         }
         __syncthreads();
         r_cur = r_nxt;
@@ -848,6 +853,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     const float alpha_min = 1.0f / 255.0f;
     const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
     const float bg_dot = bg[0] * dp0 + bg[1] * dp1 + bg[2] * dp2;
+    const float nT_bg = -T_final * bg_dot;   // the background term of dL/dalpha, before 1/(1-alpha)
     // after the wave reduction this lane holds the total of gradient term
     // my_k (accumulator slot), or nothing (my_k < 0)
     const int my_k = gs::wave_sum12_index(lane);
@@ -875,10 +881,10 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
-            const int ci = st.pos[j];   // position in the tile's list
             const float4 A = st.a[j];
             const float4 B = st.b[j];
-            const float2 Cc = st.c[j];
+            const float4 Cc = st.c[j];
+            const int ci = __float_as_int(Cc.z);   // position in the tile's list
             float gmx = 0.f, gmy = 0.f, gca = 0.f, gcb = 0.f, gcc = 0.f, gop = 0.f;
             float gc0 = 0.f, gc1 = 0.f, gc2 = 0.f;
             bool valid = false;
@@ -893,32 +899,37 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
                     const float inv_one_m = __builtin_amdgcn_rcpf(one_m);   // 1 ulp; gradients only
                     T_ = T_ * inv_one_m;
                     const float dchannel_dcolor = alpha * T_;
-                    acc0 = last_alpha * lc0 + (1.f - last_alpha) * acc0;
-                    acc1 = last_alpha * lc1 + (1.f - last_alpha) * acc1;
-                    acc2 = last_alpha * lc2 + (1.f - last_alpha) * acc2;
+                    // the reference's expressions, regrouped into fused multiply-adds
+                    // (gradients carry a tolerance, not bit-exactness):
+                    //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
+                    //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
+                    //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms)
+                    acc0 = __builtin_fmaf(last_alpha, lc0 - acc0, acc0);
+                    acc1 = __builtin_fmaf(last_alpha, lc1 - acc1, acc1);
+                    acc2 = __builtin_fmaf(last_alpha, lc2 - acc2, acc2);
                     lc0 = B.z; lc1 = B.w; lc2 = Cc.x;
-                    float dL_dalpha = (B.z - acc0) * dp0 + (B.w - acc1) * dp1 + (Cc.x - acc2) * dp2;
+                    float dL_dalpha = __builtin_fmaf(B.z - acc0, dp0,
+                                                     __builtin_fmaf(B.w - acc1, dp1, (Cc.x - acc2) * dp2));
                     gc0 = dchannel_dcolor * dp0;
                     gc1 = dchannel_dcolor * dp1;
                     gc2 = dchannel_dcolor * dp2;
-                    dL_dalpha *= T_;
+                    dL_dalpha = __builtin_fmaf(dL_dalpha, T_, inv_one_m * nT_bg);
                     last_alpha = alpha;
-                    dL_dalpha += (-T_final * inv_one_m) * bg_dot;
-                    const float a = -2.0f * A.z, b = -A.w, c = -2.0f * B.x;
                     const float dL_dG = B.y * dL_dalpha;
                     const float gdx = G * dx, gdy = G * dy;
-                    const float dG_ddelx = -gdx * a - gdy * b;
-                    const float dG_ddely = -gdy * c - gdx * b;
-                    gmx = dL_dG * dG_ddelx * ddelx_dx;
-                    gmy = dL_dG * dG_ddely * ddely_dy;
-                    gca = -0.5f * gdx * dx * dL_dG;
-                    gcb = -0.5f * gdx * dy * dL_dG;
-                    gcc = -0.5f * gdy * dy * dL_dG;
+                    const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
+                    const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
+                    gmx = (dL_dG * ddelx_dx) * dG_ddelx;
+                    gmy = (dL_dG * ddely_dy) * dG_ddely;
+                    const float h = -0.5f * dL_dG;
+                    const float hgdx = h * gdx;
+                    gca = hgdx * dx;
+                    gcb = hgdx * dy;
+                    gcc = (h * gdy) * dy;
                     gop = G * dL_dalpha;
                 }
             }
-            const uint64_t vm = gs::ballot(valid);
-            if (vm == 0) continue;
+            if (gs::ballot(valid) == 0) continue;
             const uint32_t cx = __float_as_uint(Cc.y);
             const float vals[12] = {gmx, gmy, __builtin_fabsf(gmx), __builtin_fabsf(gmy), gca, gcb, gcc, gop,
                                     gc0, gc1, gc2, 0.f};

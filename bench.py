@@ -1,20 +1,26 @@
 """Benchmark of the rasterizer hot path on one MI355X.
 
-One step = one training forward+backward of the reference's split rasterizer
-path on config 2 of BASELINE.json (6,000,000 SH-degree-3 Gaussians, city-scale
-aerial scene, 1600x1066 camera): preprocess forward -> binning + render forward
--> render backward (dL/dimage ~ N(0,1)) -> preprocess backward, driven through
-the drop-in autograd API exactly as gaussian_renderer does.  Inputs are
+Default (`--workload step --config 2`): one step = one training forward+backward
+of the reference's split rasterizer path on config 2 of BASELINE.json
+(6,000,000 SH-degree-3 Gaussians, city-scale aerial scene, 1600x1066 camera):
+preprocess forward -> binning + render forward -> render backward
+(dL/dimage ~ N(0,1)) -> preprocess backward, driven through the drop-in
+autograd API exactly as gaussian_renderer does.  Config 1 adds the reference's
+training loss 0.8 * L1 + 0.2 * (1 - fused_ssim) against a seeded target; config
+3 renders one rank's share (tile rows [43, 86) of 4096x2730).  Inputs are
 generated once (seeded, synthetic) and stay resident in HBM.
 
-Prints ONE JSON line (rank 0).  `value` is Gaussians/s = P / step time.
-`roofline` describes the dominant kernel, timed live with HIP events inside the
-timed region; `cpu_baseline` times the CPU oracle (oracle/, fp32 C with OpenMP)
-on a bounded sample of the same workload on this host.
+`--workload knn`: distCUDA2 over config 4's 10M points.  `--workload ssim`:
+fused_ssim forward+backward on config 4's 8 x 3 x 1080 x 1920 image pair.
+
+Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
+`roofline` describes the dominant kernel, timed live with HIP events on the
+launch stream inside the timed region; `cpu_baseline` times the CPU oracle
+(oracle/, fp32 C with OpenMP) on a bounded sample of the same workload on this
+host.
 """
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -25,9 +31,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+STEP_METRIC = "rasterizer fwd+bwd ms/iter & Gaussians/s at 6M SH3 1600x1066; % HBM roofline"
 
-# algorithmic bytes per unit of work, per stage
-def stage_bytes(P, P_vis, R, npx, T):
+
+# algorithmic bytes per unit of work, per stage (the scope table's per-unit figures)
+def stage_bytes(P, P_vis, R, npx):
     return {
         "preprocess_fwd_kernel": 115 * P + 192 * P_vis,
         "preprocess_bwd_kernel": 240 * P + 295 * P_vis,
@@ -41,6 +49,7 @@ def stage_bytes(P, P_vis, R, npx, T):
 
 BINNING_KERNELS = ("localmap_kernel", "count_kernel", "tilescan_kernel", "ranges_kernel", "scatter_kernel",
                    "tilesort_kernel_s", "tilesort_kernel_m", "tilesort_kernel_l", "tilesort_big_kernel")
+STEP_STAGES = ("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel")
 
 
 def parse():
@@ -48,15 +57,42 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["step", "knn", "ssim"], default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
-                    help="fraction of the Gaussians the CPU baseline runs on")
+                    help="fraction of the Gaussians (step) or points (knn) the CPU baseline runs on")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the library's plain copy kernel on MIB MiB (5 launches): the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
     return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def copy_peak(mib=1024, reps=5):
+    """Measured stream-copy bandwidth (read + write bytes / time) of the library's copy kernel."""
+    import torch
+    from blitzgs_amd import _lib
+    lib = _lib.load()
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, device="cuda:0")
+    y = torch.empty_like(x)
+    stream = _lib.stream_of(x.device)
+    _lib.check(lib.gs_diag_math(4, n, _lib.ptr(x), _lib.ptr(y), stream), "gs_diag_math copy")
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        _lib.check(lib.gs_diag_math(4, n, _lib.ptr(x), _lib.ptr(y), stream), "gs_diag_math copy")
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / reps
+    assert bool((y == 1).all())
+    del x, y
+    return 2 * 4 * n / (ms * 1e-3) / 1e9
 
 
 def calibrate_copy(mib):
@@ -75,28 +111,50 @@ def calibrate_copy(mib):
                       "launches": 5}), flush=True)
 
 
-def log(*a):
-    print(*a, file=sys.stderr, flush=True)
-
-
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding of this path is described in DESIGN.md", file=sys.stderr)
-        sys.exit(2)
-    if args.calibrate_copy:
-        calibrate_copy(args.calibrate_copy)
-        return
+def timed(fn, steps, warmup):
+    """Run fn warmup times, then time `steps` calls bracketed by synchronisation;
+    the library's per-kernel HIP-event timer records every launch inside."""
     import torch
-    from blitzgs_amd import _lib, synth
-    from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
+    from blitzgs_amd import _lib
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(steps):
+        fn()
+    ev1.record()
+    torch.cuda.synchronize()
+    _lib.timing_enable(False)
+    kt = _lib.timing_read()
+    return ev0.elapsed_time(ev1) / steps, kt
 
-    if not torch.cuda.is_available():
-        print("bench.py: no HIP device", file=sys.stderr)
-        sys.exit(1)
-    _lib.load()
+
+def roofline_of(name, alg_bytes, avg_ms, traffic=None):
+    achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
+    return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_launch_ms": round(avg_ms, 4),
+            "alg_bytes_per_launch": int(alg_bytes)}
+
+
+def header(args, metric, value, unit, ms, dtype, workload, extra_cfg):
+    return {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded PCG64)",
+            "config": dict({"workload": workload, "parallelism": "single-gpu"}, **extra_cfg)}
+
+
+# ------------------------------------------------------------------ step
+
+def run_step(args):
+    import torch
+    from blitzgs_amd import synth
+    from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
     dev = torch.device("cuda:0")
+    peak_copy = copy_peak()
 
     t0 = time.time()
     gen = {0: synth.config0, 1: synth.config1, 2: synth.config2, 3: synth.config3}[args.config]
@@ -118,6 +176,12 @@ def main():
     all_map = torch.zeros((P, 5), device=dev)
     cuda_args = {"avoid_pixel_all2all": False}
     info = {}
+    loss_desc = "dL/dimage ~ N(0,1)"
+    target = None
+    if args.config == 1:
+        from blitzgs_amd.ssim import fused_ssim
+        target = tt(np.random.Generator(np.random.PCG64(101)).random((3, H, W), dtype=np.float32))
+        loss_desc = "0.8 * L1 + 0.2 * (1 - fused_ssim) vs a seeded U[0,1] target (reference training loss)"
 
     def step():
         for p in params.values():
@@ -127,42 +191,27 @@ def main():
             params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], cuda_args)
         color, n_render, n_consider, n_contrib, out_observe, _, _ = ras.render_gaussians(
             means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, cl, cl, cuda_args)
-        torch.autograd.backward([color], [dL_dimage])
+        if target is None:
+            torch.autograd.backward([color], [dL_dimage])
+        else:
+            loss = 0.8 * (color - target).abs().mean() + 0.2 * (1.0 - fused_ssim(color[None], target[None]))
+            loss.backward()
         info["radii"] = radii
         info["n_render"] = n_render
+        info["n_consider"] = n_consider
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    ms_per_step, kt = timed(step, args.steps, args.warmup)
     P_vis = int((info["radii"] > 0).sum().item())
     R = int(info["n_render"].sum().item())
+    E = int(info["n_consider"].sum().item())
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step")
 
-    # timed region: K steps bracketed by synchronisation; per-kernel HIP events on
-    # the launch stream accumulate each kernel's launch durations
-    _lib.timing_reset()
-    _lib.timing_enable(True)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    _lib.timing_enable(False)
-    kt = _lib.timing_read()
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
-    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step (wall {1e3 * wall / args.steps:.3f} ms)")
-
-    # per-stage durations (ms per step) and algorithmic bandwidth
     per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
     avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
-    stages = {k: per_kernel.get(k, 0.0) for k in ("preprocess_fwd_kernel", "render_fwd_kernel",
-                                                  "render_bwd_kernel", "preprocess_bwd_kernel")}
+    stages = {k: per_kernel.get(k, 0.0) for k in STEP_STAGES}
     stages["binning"] = sum(per_kernel.get(k, 0.0) for k in BINNING_KERNELS)
     stages["other"] = sum(v for k, v in per_kernel.items() if k not in stages and k not in BINNING_KERNELS)
-    sb = stage_bytes(P, P_vis, R, W * H, T)
+    sb = stage_bytes(P, P_vis, R, W * H)
     stage_rows = {}
     for k, ms in stages.items():
         gbs = sb[k] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
@@ -171,41 +220,36 @@ def main():
     if args.verbose:
         for k, v in sorted(per_kernel.items(), key=lambda x: -x[1]):
             log(f"[bench]   {k:28s} {v:8.4f} ms/step  ({kt[k][1] // max(1, args.steps)} launches)")
-    dom = max(("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel"),
-              key=lambda k: per_kernel.get(k, 0.0))
-    dom_ms = avg_launch.get(dom, float("nan"))
-    dom_bytes = sb[dom]
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "avg_launch_ms": round(dom_ms, 4), "alg_bytes_per_launch": int(dom_bytes)}
-    traffic = os.path.join(ROOT, "profiles", "traffic_config2.json")
-    if os.path.exists(traffic):
+    dom = max(STEP_STAGES, key=lambda k: per_kernel.get(k, 0.0))
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"traffic_config{args.config}.json")
+    if os.path.exists(tf):
         try:
-            roofline["traffic"] = json.load(open(traffic)).get(dom)
-        except Exception:
-            pass
+            traffic = json.load(open(tf)).get(dom)
+        except (OSError, ValueError):
+            traffic = None
+    roofline = roofline_of(dom, sb[dom], avg_launch.get(dom, float("nan")), traffic)
+    roofline["note"] = ("the blend kernels are VALU-bound (per-pixel exp and gradient arithmetic plus a 64-lane "
+                        "reduction per Gaussian); their HBM fraction is low by nature")
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(scene, cam, args.cpu_sample, cl)
+        cpu = cpu_baseline_step(scene, cam, args.cpu_sample, cl)
 
-    gs_per_s = P / (ms_per_step * 1e-3)
-    out = {
-        "metric": "rasterizer fwd+bwd ms/iter & Gaussians/s at 6M SH3 1600x1066; % HBM roofline",
-        "value": round(gs_per_s, 1), "unit": "Gaussians/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded PCG64 scene)",
-        "config": {"workload": f"config{args.config}: {P} Gaussians SH3, {W}x{H}, fwd+bwd", "gaussians": P,
-                   "visible": P_vis, "instances": R, "image": [W, H], "tiles": T, "parallelism": "single-gpu"},
-        "stages_ms": stage_rows,
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
+    metric = STEP_METRIC if args.config == 2 else f"rasterizer fwd+bwd ms/iter & Gaussians/s, config {args.config}"
+    out = header(args, metric, P / (ms_per_step * 1e-3), "Gaussians/s", ms_per_step, "f32",
+                 f"config{args.config}: {P} Gaussians SH3, {W}x{H}, fwd+bwd",
+                 {"gaussians": P, "visible": P_vis, "instances": R, "image": [W, H], "tiles": T,
+                  "local_tiles": int(cl.sum().item()) if cl is not None else T, "loss": loss_desc})
+    out["stages_ms"] = stage_rows
+    out["render_fwd_evaluations"] = E
+    out["hbm_copy_GBs"] = round(peak_copy, 1)
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(scene, cam, frac, cl):
+def cpu_baseline_step(scene, cam, frac, cl):
     """The CPU oracle's full fwd+bwd chain on (a sample of) the same scene."""
     from oracle import oracle as O
     P = scene["means3D"].shape[0]
@@ -228,6 +272,111 @@ def cpu_baseline(scene, cam, frac, cl):
     return {"value": round(n / dt, 1), "unit": "Gaussians/s", "cores": O.num_threads(), "kind": "port",
             "sample": f"one fwd+bwd iteration of the CPU oracle on the first {n} of {P} Gaussians, "
                       f"same camera ({W}x{H}); {dt * 1e3:.0f} ms"}
+
+
+# ------------------------------------------------------------------- knn
+
+def run_knn(args):
+    import torch
+    from blitzgs_amd import synth
+    from blitzgs_amd.knn import distCUDA2
+    t0 = time.time()
+    pts_np = synth.config4_points()
+    log(f"[bench] config 4 points generated in {time.time() - t0:.1f}s")
+    P = pts_np.shape[0]
+    pts = torch.as_tensor(pts_np, device="cuda:0")
+    ms, kt = timed(lambda: distCUDA2(pts), args.steps, args.warmup)
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
+    if args.verbose:
+        for k, v in sorted(per_kernel.items(), key=lambda x: -x[1]):
+            log(f"[bench]   {k:28s} {v:8.4f} ms/call")
+    # compulsory traffic 12 P (points) + 4 P (output); the whole pipeline is the unit
+    roofline = roofline_of("distCUDA2 (all kernels)", 16 * P, ms)
+    roofline["query_kernel_ms"] = round(avg_launch.get("knn_query_kernel", float("nan")), 4)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        n = max(4, int(P * min(args.cpu_sample, 0.1)))
+        sub = np.ascontiguousarray(pts_np[:n])
+        t1 = time.perf_counter()
+        O.knn_meandist3(sub)
+        dt = time.perf_counter() - t1
+        cpu = {"value": round(n / dt, 1), "unit": "points/s", "cores": O.num_threads(), "kind": "port",
+               "sample": f"CPU oracle exact 3-NN (grid) on the first {n} of the {P} points; {dt * 1e3:.0f} ms"}
+    out = header(args, "distCUDA2 points/s (exact 3-NN mean squared distance)", P / (ms * 1e-3), "points/s", ms,
+                 "f32", f"config4: distCUDA2 over {P} points", {"points": P})
+    out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
+# ------------------------------------------------------------------ ssim
+
+def run_ssim(args):
+    import torch
+    from blitzgs_amd import synth
+    from blitzgs_amd.ssim import fused_ssim
+    a, b = synth.config4_images()
+    B, C, H, W = a.shape
+    img1 = torch.as_tensor(a, device="cuda:0").requires_grad_(True)
+    img2 = torch.as_tensor(b, device="cuda:0")
+
+    def step():
+        img1.grad = None
+        loss = 1.0 - fused_ssim(img1, img2)
+        loss.backward()
+
+    ms, kt = timed(step, args.steps, args.warmup)
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
+    N = B * C * H * W
+    fwd_bytes = 2 * 4 * N + 4 * 4 * N
+    bwd_bytes = 5 * 4 * N + 4 * N
+    rows = {}
+    for k, nb in (("ssim_fwd_kernel", fwd_bytes), ("ssim_bwd_kernel", bwd_bytes)):
+        t = per_kernel.get(k, 0.0)
+        gbs = nb / (t * 1e-3) / 1e9 if t > 0 else 0.0
+        rows[k] = {"ms": round(t, 4), "alg_GB": round(nb / 1e9, 4), "GB_per_s": round(gbs, 1),
+                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = max(rows, key=lambda k: rows[k]["ms"])
+    roofline = roofline_of(dom, fwd_bytes if dom == "ssim_fwd_kernel" else bwd_bytes,
+                           avg_launch.get(dom, float("nan")))
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        x, y = np.ascontiguousarray(a[:1]), np.ascontiguousarray(b[:1])
+        t1 = time.perf_counter()
+        m, d1, d2, d3 = O.ssim_fwd(x, y)
+        O.ssim_bwd(x, y, np.full(x.shape, -1.0 / N, np.float32), d1, d2, d3)
+        dt = time.perf_counter() - t1
+        cpu = {"value": round(x.size / dt, 1), "unit": "pixels/s", "cores": O.num_threads(), "kind": "port",
+               "sample": f"CPU oracle SSIM fwd+bwd on image 1 of {B} (3x{H}x{W}); {dt * 1e3:.0f} ms"}
+    out = header(args, "fused_ssim fwd+bwd pixels/s", N / (ms * 1e-3), "pixels/s", ms, "f32",
+                 f"config4: fused_ssim fwd+bwd, {B}x{C}x{H}x{W}", {"shape": [B, C, H, W]})
+    out["stages_ms"] = rows
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding of this path is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
+    import torch
+    from blitzgs_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    {"step": run_step, "knn": run_knn, "ssim": run_ssim}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -185,61 +185,134 @@ __global__ __launch_bounds__(256) void cell_scatter_kernel(int P, const float* _
     sorted[pos] = make_float4(pts[3 * (size_t)i], pts[3 * (size_t)i + 1], pts[3 * (size_t)i + 2], __uint_as_float((uint32_t)i));
 }
 
+// insertion of d into the ascending triple b0 <= b1 <= b2 (updateKBest,
+// simple_knn.cu:132-146): min / median-of-three are exact, so
+//   b0' = min(b0, d), b1' = med3(b0, b1, d), b2' = med3(b1, b2, d)
+// is the same triple the reference's swap chain produces (inputs are finite or +inf)
 __device__ __forceinline__ void upd3(float& b0, float& b1, float& b2, float d)
 {
-    // insertion into the ascending triple (updateKBest, simple_knn.cu:132-146)
-    if (b0 > d) { const float t = b0; b0 = d; d = t; }
-    if (b1 > d) { const float t = b1; b1 = d; d = t; }
-    if (b2 > d) { b2 = d; }
+    const float n2 = __builtin_amdgcn_fmed3f(b1, b2, d);
+    const float n1 = __builtin_amdgcn_fmed3f(b0, b1, d);
+    b0 = __builtin_fminf(b0, d);
+    b1 = n1;
+    b2 = n2;
 }
 
+// candidates sorted[lo, hi) against the query at sorted position `self`; four
+// loads in flight
+__device__ __forceinline__ void scan_segment(uint32_t lo, uint32_t hi, const float4* __restrict__ sorted, float4 q,
+                                             uint32_t self, float& b0, float& b1, float& b2)
+{
+    uint32_t k = lo;
+    for (; k + 4 <= hi; k += 4) {
+        float4 o[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) o[u] = sorted[k + u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float dx = o[u].x - q.x, dy = o[u].y - q.y, dz = o[u].z - q.z;
+            const float d = (dx * dx + dy * dy) + dz * dz;
+            upd3(b0, b1, b2, k + u == self ? __builtin_huge_valf() : d);
+        }
+    }
+    for (; k < hi; k++) {
+        const float4 o = sorted[k];
+        const float dx = o.x - q.x, dy = o.y - q.y, dz = o.z - q.z;
+        const float d = (dx * dx + dy * dy) + dz * dz;
+        upd3(b0, b1, b2, k == self ? __builtin_huge_valf() : d);
+    }
+}
+
+// distance from the query to the outside of the cell box c +- r (grid borders
+// excluded); DBL_MAX when the box covers the whole grid
+__device__ __forceinline__ double box_bound(const Grid& g, const int (&c)[3], const float (&qv)[3], int r)
+{
+    double bound = DBL_MAX;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const double lo = g.mn[k] + (double)(c[k] - r) * g.hk[k];
+        const double hi = g.mn[k] + (double)(c[k] + r + 1) * g.hk[k];
+        if (c[k] - r > 0) bound = fmin(bound, (double)qv[k] - lo);
+        if (c[k] + r + 1 < g.n[k]) bound = fmin(bound, hi - (double)qv[k]);
+    }
+    return bound;
+}
+
+// true when the third-best squared distance is provably below every point
+// outside the box (the bound is padded by a relative margin)
+__device__ __forceinline__ bool box_done(double bound, float b2)
+{
+    if (bound == DBL_MAX) return true;
+    if (bound < 0) bound = 0;
+    return (double)b2 < bound * bound * (1.0 - 1e-6);
+}
+
+// Queries run in cell order (one thread per sorted point), so a wave's
+// queries sit in neighbouring cells.  The 3x3x3 cells around the query are 9
+// runs of x-consecutive cells, i.e. 9 contiguous ranges of the cell-sorted
+// points; they are scanned first.  Only if the third-best distance is not yet
+// provably final are further shells visited cell by cell.
 __global__ __launch_bounds__(256) void knn_query_kernel(int P, Grid g, const uint32_t* __restrict__ start,
                                                         const float4* __restrict__ sorted, float* __restrict__ out)
 {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= P) return;
     const float4 q = sorted[s];
-    const uint32_t self = __float_as_uint(q.w);
+    const uint32_t self = (uint32_t)s;   // the query's own position in the sorted points
     const float qv[3] = {q.x, q.y, q.z};
     int c[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) c[k] = cell_coord(qv[k], g.mn[k], g.hk[k], g.n[k]);
     float b0 = FLT_MAX, b1 = FLT_MAX, b2 = FLT_MAX;
+
+    // r <= 1: nine row segments
+    {
+        const int x0 = max(0, c[0] - 1), x1 = min(g.n[0] - 1, c[0] + 1);
+        uint32_t lo[9], hi[9];
+#pragma unroll
+        for (int j = 0; j < 9; j++) {
+            const int z = c[2] + j / 3 - 1, y = c[1] + j % 3 - 1;
+            lo[j] = hi[j] = 0;
+            if (z >= 0 && z < g.n[2] && y >= 0 && y < g.n[1]) {
+                const uint32_t row = (uint32_t)((z * g.n[1] + y) * g.n[0]);
+                lo[j] = start[row + (uint32_t)x0];
+                hi[j] = start[row + (uint32_t)x1 + 1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 9; j++) scan_segment(lo[j], hi[j], sorted, q, self, b0, b1, b2);
+    }
     const int rmax = max(g.n[0], max(g.n[1], g.n[2]));
-    for (int r = 0; r <= rmax; r++) {
-        const int z0 = max(0, c[2] - r), z1 = min(g.n[2] - 1, c[2] + r);
-        const int y0 = max(0, c[1] - r), y1 = min(g.n[1] - 1, c[1] + r);
-        for (int z = z0; z <= z1; z++) {
-            for (int y = y0; y <= y1; y++) {
-                // rows inside the shell in (z, y) only visit the two x ends
-                const bool shell_zy = (z == c[2] - r || z == c[2] + r || y == c[1] - r || y == c[1] + r);
-                const int xstep = shell_zy ? 1 : max(1, 2 * r);
-                for (int x = c[0] - r; x <= c[0] + r; x += xstep) {
-                    if (x < 0 || x >= g.n[0]) continue;
-                    const uint32_t cc = (uint32_t)((z * g.n[1] + y) * g.n[0] + x);
-                    const uint32_t e = start[cc + 1];
-                    for (uint32_t k = start[cc]; k < e; k++) {
-                        const float4 o = sorted[k];
-                        if (__float_as_uint(o.w) == self) continue;
-                        const float dx = o.x - q.x, dy = o.y - q.y, dz = o.z - q.z;
-                        upd3(b0, b1, b2, (dx * dx + dy * dy) + dz * dz);
+    if (!box_done(box_bound(g, c, qv, 1), b2)) {
+        for (int r = 2; r <= rmax; r++) {
+            const int z0 = max(0, c[2] - r), z1 = min(g.n[2] - 1, c[2] + r);
+            const int y0 = max(0, c[1] - r), y1 = min(g.n[1] - 1, c[1] + r);
+            for (int z = z0; z <= z1; z++) {
+                for (int y = y0; y <= y1; y++) {
+                    const uint32_t row = (uint32_t)((z * g.n[1] + y) * g.n[0]);
+                    const bool shell_zy = (z == c[2] - r || z == c[2] + r || y == c[1] - r || y == c[1] + r);
+                    if (shell_zy) {
+                        // the whole x run of this shell row is new: one segment
+                        const int xa = max(0, c[0] - r), xb = min(g.n[0] - 1, c[0] + r);
+                        scan_segment(start[row + (uint32_t)xa], start[row + (uint32_t)xb + 1], sorted, q, self, b0,
+                                     b1, b2);
+                    } else {
+                        // interior rows: only the two x ends are new
+                        if (c[0] - r >= 0) {
+                            const uint32_t cc = row + (uint32_t)(c[0] - r);
+                            scan_segment(start[cc], start[cc + 1], sorted, q, self, b0, b1, b2);
+                        }
+                        if (c[0] + r < g.n[0]) {
+                            const uint32_t cc = row + (uint32_t)(c[0] + r);
+                            scan_segment(start[cc], start[cc + 1], sorted, q, self, b0, b1, b2);
+                        }
                     }
                 }
             }
+            if (box_done(box_bound(g, c, qv, r), b2)) break;
         }
-        double bound = DBL_MAX;
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const double lo = g.mn[k] + (double)(c[k] - r) * g.hk[k];
-            const double hi = g.mn[k] + (double)(c[k] + r + 1) * g.hk[k];
-            if (c[k] - r > 0) bound = fmin(bound, (double)qv[k] - lo);
-            if (c[k] + r + 1 < g.n[k]) bound = fmin(bound, hi - (double)qv[k]);
-        }
-        if (bound == DBL_MAX) break;
-        if (bound < 0) bound = 0;
-        if ((double)b2 < bound * bound * (1.0 - 1e-6)) break;
     }
-    out[self] = ((b0 + b1) + b2) / 3.0f;
+    out[__float_as_uint(q.w)] = ((b0 + b1) + b2) / 3.0f;
 }
 
 }  // namespace

@@ -48,7 +48,8 @@ def stage_bytes(P, P_vis, R, npx):
 
 
 BINNING_KERNELS = ("localmap_kernel", "count_kernel", "tilescan_kernel", "ranges_kernel", "scatter_kernel",
-                   "tilesort_kernel_s", "tilesort_kernel_m", "tilesort_kernel_l", "tilesort_big_kernel")
+                   "tilesort_kernel_512", "tilesort_kernel_1k", "tilesort_kernel_2k", "tilesort_kernel_4k",
+                   "tilesort_kernel_8k", "tilesort_big_kernel")
 STEP_STAGES = ("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel")
 
 

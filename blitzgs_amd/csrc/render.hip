@@ -30,7 +30,7 @@
 //                index) to its reserved slices (LDS cursors) and writes each
 //                listed Gaussian's 64-byte blend record at its compact index.
 //   4. sort    : one block per tile sorts its bucket by (depth bits, compact
-//                index) in LDS (bitonic, three size classes) and writes the
+//                index) in registers (bitonic, five size classes) and writes the
 //                sorted Gaussian ids, the (tile << 32 | depth bits) keys and
 //                the compact list the blend walks.
 // The compact index is increasing in Gaussian id, so each sorted bucket is
@@ -59,9 +59,7 @@ constexpr int LDS_TILES = 16384;     // local tiles histogrammed in LDS (64 KB)
 constexpr int BIN_THREADS = 512;
 constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
-constexpr int SORT_CAP_S = 2048;     // bucket size classes sorted entirely in LDS
-constexpr int SORT_CAP_M = 4096;
-constexpr int SORT_CAP_L = 8192;
+constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
 constexpr int BIG_SORT_THREADS = 1024;
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
@@ -574,26 +572,143 @@ __device__ __forceinline__ void write_sorted(uint32_t tile, uint32_t start, int 
     }
 }
 
-// One block per local tile whose bucket size lies in (LO, CAP]: the bucket is
-// sorted by (depth bits, compact index) in LDS.  Three size classes keep the
-// LDS footprint (and so the occupancy) matched to the bucket.
-template <int CAP, int NT, int LO>
+// ---- register-resident bitonic sort: each thread holds 8 consecutive keys
+// (position i = 8 t + r), so a compare-exchange between positions i and i ^ M
+// is in-thread for M < 8, between lanes of a wave for M < 512 (ds_swizzle /
+// permlane32 exchanges, no barrier) and through LDS only beyond that.
+
+// value of v held by lane (lane ^ D) of this wave, 0 < D < 64 (all lanes active)
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v)
+{
+    if constexpr ((D & 32) != 0) {
+        // permlane32_swap(v, v): first result = (v[0..31], v[0..31]), second = (v[32..63], v[32..63])
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = (threadIdx.x & 32u) ? r[0] : r[1];
+    }
+    if constexpr ((D & 31) != 0) v = (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, ((D & 31) << 10) | 0x1f);
+    return v;
+}
+
+template <int D>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v)
+{
+    return ((uint64_t)lane_xor<D>((uint32_t)(v >> 32)) << 32) | (uint64_t)lane_xor<D>((uint32_t)v);
+}
+
+template <int X>
+struct TopBit {
+    static constexpr int value = X <= 1 ? 0 : 1 + TopBit<X / 2>::value;
+};
+template <>
+struct TopBit<0> {
+    static constexpr int value = 0;
+};
+
+// padded LDS slot of position i (one spare slot per 8 keys: conflict-free rows)
+__device__ __forceinline__ int sort_slot(int i) { return (i >> 3) * 9 + (i & 7); }
+
+// compare-exchanges (i, i ^ M), M < 8, inside each thread
+template <int M>
+__device__ __forceinline__ void sort_stage_in(uint64_t (&k)[8])
+{
+    constexpr int HB = 1 << TopBit<M>::value;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        if ((r & HB) == 0) {
+            const uint64_t x = k[r], y = k[r ^ M];
+            k[r] = x < y ? x : y;
+            k[r ^ M] = x < y ? y : x;
+        }
+    }
+}
+
+// compare-exchanges (i, i ^ M), M >= 8: the partner is register r ^ (M & 7) of
+// thread t ^ (M >> 3); the lower position keeps the minimum
+template <int NT, int M>
+__device__ __forceinline__ void sort_stage_cross(uint64_t (&k)[8], uint64_t* lds)
+{
+    constexpr int DT = M >> 3, RX = M & 7;
+    const bool lower = ((threadIdx.x >> TopBit<DT>::value) & 1u) == 0;
+    uint64_t p[8];
+    if constexpr (DT < 64) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) p[r] = lane_xor64<DT>(k[r ^ RX]);
+    } else {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 8; r++) lds[threadIdx.x * 9 + r] = k[r];
+        __syncthreads();
+        const int pt = (int)threadIdx.x ^ DT;
+#pragma unroll
+        for (int r = 0; r < 8; r++) p[r] = lds[pt * 9 + (r ^ RX)];
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const uint64_t x = k[r], y = p[r];
+        k[r] = lower ? (x < y ? x : y) : (x < y ? y : x);
+    }
+}
+
+// half-cleaners j = J, J/2, ..., 1
+template <int NT, int J>
+__device__ __forceinline__ void sort_cleaners(uint64_t (&k)[8], uint64_t* lds)
+{
+    if constexpr (J >= 8) {
+        sort_stage_cross<NT, J>(k, lds);
+        sort_cleaners<NT, J / 2>(k, lds);
+    } else if constexpr (J >= 1) {
+        sort_stage_in<J>(k);
+        sort_cleaners<NT, J / 2>(k, lds);
+    }
+}
+
+// merges of size K2, 2 K2, ..., 8 NT: a flip (i, i ^ (K2 - 1)) then the half-cleaners
+template <int NT, int K2>
+__device__ __forceinline__ void sort_merges(uint64_t (&k)[8], uint64_t* lds)
+{
+    if constexpr (K2 <= 8 * NT) {
+        if constexpr (K2 <= 8) sort_stage_in<K2 - 1>(k);
+        else sort_stage_cross<NT, K2 - 1>(k, lds);
+        sort_cleaners<NT, K2 / 4>(k, lds);
+        sort_merges<NT, K2 * 2>(k, lds);
+    }
+}
+
+// One block of NT threads per local tile whose bucket size lies in
+// (8 NT / 2, 8 NT] (any size up to 512 for one wave): the bucket, padded with
+// all-ones keys, is sorted by (depth bits, compact index) in registers.
+template <int NT, int LO>
 __global__ __launch_bounds__(NT) void tilesort_kernel(
     const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
     const uint32_t* __restrict__ tile_start, const uint64_t* __restrict__ sortkey, SortOut out)
 {
-    __shared__ uint64_t s[CAP];
+    constexpr int CAP = 8 * NT;
+    __shared__ uint64_t lds[NT * 9];
     const int l = blockIdx.x;
     if (l >= (int)meta[0]) return;
     const int n = (int)tile_count[l];
     if (n <= LO || n > CAP) return;
     const uint32_t start = tile_start[l];
-    int N = 1;
-    while (N < n) N <<= 1;
-    for (int i = threadIdx.x; i < n; i += NT) s[i] = sortkey[start + i];
+    const int t = threadIdx.x;
+    for (int i = t; i < CAP; i += NT) lds[sort_slot(i)] = i < n ? sortkey[start + i] : ~0ull;
     __syncthreads();
-    bitonic<NT>(s, n, N);
-    write_sorted((uint32_t)tile_of_local[l], start, n, s, out, NT);
+    uint64_t k[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) k[r] = lds[t * 9 + r];
+    sort_merges<NT, 2>(k, lds);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 8; r++) lds[t * 9 + r] = k[r];
+    __syncthreads();
+    const uint32_t tile = (uint32_t)tile_of_local[l];
+    for (int i = t; i < n; i += NT) {
+        const uint64_t key = lds[sort_slot(i)];
+        const uint32_t cx = (uint32_t)key;
+        out.clist[start + i] = cx;
+        out.point_list[start + i] = out.cid2id[cx];
+        out.keys[start + i] = ((uint64_t)tile << 32) | (key >> 32);
+    }
 }
 
 // Buckets larger than the biggest LDS class: the same network in global
@@ -605,7 +720,7 @@ __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
     const int l = blockIdx.x;
     if (l >= (int)meta[0]) return;
     const int n = (int)tile_count[l];
-    if (n <= SORT_CAP_L) return;
+    if (n <= SORT_CAP_MAX) return;
     const uint32_t start = tile_start[l];
     uint64_t* s = sortkey + start;
     int N = 1;
@@ -1069,18 +1184,26 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
                                     at<float4>(geom, g.gacc)));
         GS_LAUNCH_CHECK("scatter_kernel");
         const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};
-        GS_TIMED("tilesort_kernel_s", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_S, 256, 0>), dim3(T), dim3(256), 0, stream, meta,
+        GS_TIMED("tilesort_kernel_512", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<64, 0>), dim3(T), dim3(64), 0, stream, meta, tile_of_local,
+                                    tile_count, tile_start, sortkey, sout));
+        GS_LAUNCH_CHECK("tilesort_kernel<64>");
+        GS_TIMED("tilesort_kernel_1k", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<128, 512>), dim3(T), dim3(128), 0, stream, meta, tile_of_local,
+                                    tile_count, tile_start, sortkey, sout));
+        GS_LAUNCH_CHECK("tilesort_kernel<128>");
+        GS_TIMED("tilesort_kernel_2k", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<256, 1024>), dim3(T), dim3(256), 0, stream, meta, tile_of_local,
+                                    tile_count, tile_start, sortkey, sout));
+        GS_LAUNCH_CHECK("tilesort_kernel<256>");
+        GS_TIMED("tilesort_kernel_4k", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<512, 2048>), dim3(T), dim3(512), 0, stream, meta, tile_of_local,
+                                    tile_count, tile_start, sortkey, sout));
+        GS_LAUNCH_CHECK("tilesort_kernel<512>");
+        GS_TIMED("tilesort_kernel_8k", stream,
+                 hipLaunchKernelGGL((tilesort_kernel<1024, 4096>), dim3(T), dim3(1024), 0, stream, meta,
                                     tile_of_local, tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<S>");
-        GS_TIMED("tilesort_kernel_m", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_M, 512, SORT_CAP_S>), dim3(T), dim3(512), 0, stream,
-                                    meta, tile_of_local, tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<M>");
-        GS_TIMED("tilesort_kernel_l", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<SORT_CAP_L, 1024, SORT_CAP_M>), dim3(T), dim3(1024), 0, stream,
-                                    meta, tile_of_local, tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<L>");
+        GS_LAUNCH_CHECK("tilesort_kernel<1024>");
         GS_TIMED("tilesort_big_kernel", stream,
                  hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta,
                                     tile_of_local, tile_count, tile_start, sortkey, sout));

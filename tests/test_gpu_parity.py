@@ -111,9 +111,40 @@ def test_binning_render_ragged_masked_and_ties():
         _check_binning_and_render(cam, pre, (0.2, 0.5, 0.9), cl)
 
 
+def test_binning_every_sort_size_class():
+    # A Gaussian of radius 1 at a tile centre lands in exactly that tile, so the
+    # bucket sizes below are exact: they straddle every boundary of the on-chip
+    # sort classes (512 / 1024 / 2048 / 4096 / 8192 keys) and exceed the largest
+    # (the global-memory path).  Depths are drawn from a small set (many ties ->
+    # ascending id order) plus a continuous range.
+    sizes = [1, 2, 63, 64, 65, 511, 512, 513, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097,
+             8191, 8192, 8193, 10000]
+    gx = 8
+    W, H = gx * 16, ((len(sizes) + gx - 1) // gx) * 16
+    rng = np.random.default_rng(21)
+    xs, ys = [], []
+    for t, n in enumerate(sizes):
+        xs.append(np.full(n, (t % gx) * 16 + 8.0))
+        ys.append(np.full(n, (t // gx) * 16 + 8.0))
+    P = sum(sizes)
+    order = rng.permutation(P)          # interleave the tiles' Gaussians in id order
+    means2D = np.stack([np.concatenate(xs)[order], np.concatenate(ys)[order]], 1).astype(np.float32)
+    radii = np.ones(P, np.int32)
+    depths = np.where(rng.random(P) < 0.5, rng.integers(1, 6, P).astype(np.float32),
+                      rng.uniform(0.3, 40.0, P)).astype(np.float32)
+    conic = np.tile(np.array([[0.3, 0.0, 0.3, 0.02]], np.float32), (P, 1))
+    rgb = rng.random((P, 3)).astype(np.float32)
+    cam = dict(W=W, H=H, tanfovx=1.0, tanfovy=1.0, viewmatrix=np.eye(4, dtype=np.float32),
+               projmatrix=np.eye(4, dtype=np.float32), campos=np.zeros(3, np.float32))
+    pre = dict(means2D=means2D, depths=depths, radii=radii, conic_opacity=conic, rgb=rgb)
+    g, ob, _ = _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
+    counts = np.diff(ob["ranges"].reshape(-1, 2), axis=1).ravel()
+    assert sorted(counts[counts > 0].tolist()) == sorted(sizes)
+
+
 def test_binning_large_bucket_and_global_mode():
-    # one tile receiving > 4096 instances (the global-memory sort path) and an
-    # image with more than 16384 local tiles (the global-atomics count path)
+    # one tile receiving > 4096 instances and an image with more than 16384
+    # local tiles (the global-atomics count path)
     rng = np.random.default_rng(9)
     P = 9000
     W, H = 2304, 2048   # 144 x 128 = 18432 tiles

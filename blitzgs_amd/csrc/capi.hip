@@ -185,7 +185,7 @@ extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t
         GS_REQUIRE(n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0,
                    "op 4 copies whole 16-byte groups from 16-byte aligned buffers");
         const size_t n4 = (size_t)n / 4;
-        const unsigned blocks = (unsigned)std::min<size_t>(gs_div_up(n4, 256), 8192);
+        const unsigned blocks = (unsigned)std::min<size_t>(gs_div_up(n4, 256), 32768);
         GS_TIMED("diag_copy_kernel", stream,
                  hipLaunchKernelGGL(diag_copy_kernel, dim3(blocks), dim3(256), 0, stream, n4,
                                     (const float4*)x, (float4*)y));

@@ -210,16 +210,18 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     stream = _stream(dev)
     geom = torch.empty(lib.gs_render_geom_bytes(P, W, H), device=dev, dtype=torch.uint8)
     img = torch.empty(lib.gs_render_img_bytes(W, H), device=dev, dtype=torch.uint8)
-    R = C.c_int64(0)
-    check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(R), stream),
-          "gs_render_forward_count")
-    R = int(R.value)
-    binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
+    # everything that does not depend on R is allocated before the count call,
+    # whose R readback synchronises the stream
     color = torch.empty((3, H, W), device=dev, dtype=torch.float32)
     n_render = torch.empty((T,), **i32)
     n_consider = torch.empty((T,), **i32)
     n_contrib = torch.empty((T,), **i32)
     out_observe = torch.empty((P,), **i32)
+    R = C.c_int64(0)
+    check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(R), stream),
+          "gs_render_forward_count")
+    R = int(R.value)
+    binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
     if timing:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()

@@ -182,11 +182,18 @@ __device__ __forceinline__ uint32_t block_excl_scan_1024(uint32_t v, uint32_t* s
 }
 
 // compute_locally -> local tile numbering; clears the per-tile counters
-__global__ __launch_bounds__(1024) void localmap_kernel(int T, const uint8_t* __restrict__ cl,
+// compute_locally -> local tile numbering and the bounding box of the local
+// tiles (meta[5..8] = x0, y0, x1, y1, exclusive ends; empty box if none);
+// clears the per-tile counters
+__global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, const uint8_t* __restrict__ cl,
                                                         int* __restrict__ loc_map, int* __restrict__ tile_of_local,
                                                         uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta)
 {
     __shared__ uint32_t s_wave[32];
+    __shared__ uint32_t s_box[4];
+    if (threadIdx.x == 0) { s_box[0] = 0xffffffffu; s_box[1] = 0xffffffffu; s_box[2] = 0u; s_box[3] = 0u; }
+    __syncthreads();
+    uint32_t bx0 = 0xffffffffu, by0 = 0xffffffffu, bx1 = 0u, by1 = 0u;
     uint32_t base = 0;
     for (int t0 = 0; t0 < T; t0 += 1024) {
         const int t = t0 + threadIdx.x;
@@ -195,12 +202,25 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, const uint8_t* __
         const uint32_t pre = block_excl_scan_1024(f, s_wave, &tot);
         if (t < T) {
             loc_map[t] = f ? (int)(base + pre) : -1;
-            if (f) tile_of_local[base + pre] = t;
+            if (f) {
+                tile_of_local[base + pre] = t;
+                const uint32_t tx = (uint32_t)t % gx, ty = (uint32_t)t / gx;
+                bx0 = min(bx0, tx); by0 = min(by0, ty);
+                bx1 = max(bx1, tx + 1); by1 = max(by1, ty + 1);
+            }
             tile_count[t] = 0;
         }
         base += tot;
     }
-    if (threadIdx.x == 0) meta[0] = base;
+    atomicMin(&s_box[0], bx0); atomicMin(&s_box[1], by0);
+    atomicMax(&s_box[2], bx1); atomicMax(&s_box[3], by1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        meta[0] = base;
+        const bool any = base > 0;
+        meta[5] = any ? s_box[0] : 0u; meta[6] = any ? s_box[1] : 0u;
+        meta[7] = any ? s_box[2] : 0u; meta[8] = any ? s_box[3] : 0u;
+    }
 }
 
 // ------------------------------------------------------------- counting
@@ -255,15 +275,29 @@ __device__ __forceinline__ void expansion_at(const Expansion& e, int cnt, unsign
     ty = oy0 + q;
 }
 
-// tile rect of a Gaussian with radius r and mean p (binning rule); returns
-// its tile count
-__device__ __forceinline__ int rect_from(int r, float2 p, unsigned gx, unsigned gy, unsigned& x0, unsigned& y0,
-                                         unsigned& w)
+// Local-tile bounding box: tiles outside it are never local, so rects are
+// clipped to it before their instances are expanded.
+struct TileBox {
+    unsigned x0, y0, x1, y1;
+};
+
+__device__ __forceinline__ TileBox tile_box(const uint32_t* __restrict__ meta)
+{
+    return TileBox{meta[5], meta[6], meta[7], meta[8]};
+}
+
+// tile rect of a Gaussian with radius r and mean p (binning rule), clipped to
+// the local-tile box; returns its tile count there
+__device__ __forceinline__ int rect_from(int r, float2 p, unsigned gx, unsigned gy, const TileBox& box, unsigned& x0,
+                                         unsigned& y0, unsigned& w)
 {
     x0 = y0 = w = 0;
     if (r <= 0) return 0;
     unsigned x1, y1;
     gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
+    x0 = max(x0, box.x0); y0 = max(y0, box.y0);
+    x1 = min(x1, box.x1); y1 = min(y1, box.y1);
+    if (x1 <= x0 || y1 <= y0) { x0 = y0 = 0; return 0; }
     w = x1 - x0;
     return (int)(w * (y1 - y0));
 }
@@ -298,6 +332,7 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
     const bool all_local = TL == (int)(gx * gy);
+    const TileBox box = tile_box(meta);
     const int c = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lds) {
@@ -317,7 +352,7 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
         const float2 m = m_n;
         load_rm(wb + 64 + lane, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_from(r, m, gx, gy, x0, y0, w);
+        const int cnt = rect_from(r, m, gx, gy, box, x0, y0, w);
         listed += (uint32_t)__builtin_popcountll(gs::ballot(cnt > 0));
         const Expansion e = expansion_begin(cnt);
         for (int k0 = 0; k0 < e.total; k0 += 64) {
@@ -425,6 +460,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     const int TL = (int)meta[0];
     const bool lds = TL <= LDS_TILES;
     const bool all_local = TL == (int)(gx * gy);
+    const TileBox box = tile_box(meta);
     const int c = blockIdx.x;
     if (lds) {
         const uint32_t* row = hist + (size_t)c * TL;
@@ -458,7 +494,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
         const float3 col = c_n;
         load_rm(i + 64, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_from(r, xy, gx, gy, x0, y0, w);
+        const int cnt = rect_from(r, xy, gx, gy, box, x0, y0, w);
         const uint64_t lm = gs::ballot(cnt > 0);
         const int nl = (int)__builtin_popcountll(lm);
         const int rank = gs::rank_below(lm);
@@ -1112,7 +1148,7 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
     uint32_t* tile_start = at<uint32_t>(geom, g.tile_start);
     uint32_t* cursor = at<uint32_t>(geom, g.cursor);
 
-    GS_TIMED("localmap_kernel", stream, hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, compute_locally, loc_map,
+    GS_TIMED("localmap_kernel", stream, hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, gx, compute_locally, loc_map,
                        tile_of_local, tile_count, meta));
     GS_LAUNCH_CHECK("localmap_kernel");
     if (P > 0) {

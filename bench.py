@@ -12,6 +12,7 @@ generated once (seeded, synthetic) and stay resident in HBM.
 
 `--workload knn`: distCUDA2 over config 4's 10M points.  `--workload ssim`:
 fused_ssim forward+backward on config 4's 8 x 3 x 1080 x 1920 image pair.
+`--workload adam`: the SparseGaussianAdam step over config 2's 6M Gaussians.
 
 Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
 `roofline` describes the dominant kernel, timed live with HIP events on the
@@ -58,7 +59,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["step", "knn", "ssim"], default="step")
+    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam"], default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
@@ -372,6 +373,54 @@ def run_ssim(args):
     print(json.dumps(out), flush=True)
 
 
+# ------------------------------------------------------------------ adam
+
+ADAM_GROUPS = {"xyz": 3, "f_dc": 3, "f_rest": 45, "opacity": 1, "scaling": 3, "rotation": 4}
+
+
+def run_adam(args):
+    """SparseGaussianAdam.step over config 2's 6M Gaussians (59 floats each, the
+    reference's six parameter groups) with 18.8 % of them visible (config 2's
+    visible fraction; a seeded random subset)."""
+    import torch
+    from blitzgs_amd.adam import SparseGaussianAdam
+    N = 6_000_000
+    rng = np.random.Generator(np.random.PCG64(5))
+    vis = torch.as_tensor(rng.random(N) < 0.1877, device="cuda:0")
+    params = {k: torch.zeros((N, m), device="cuda:0", requires_grad=True) for k, m in ADAM_GROUPS.items()}
+    for k, p in params.items():
+        p.grad = torch.randn_like(p)
+    opt = SparseGaussianAdam([{"params": [params[k]], "lr": 1e-3, "name": k} for k in ADAM_GROUPS], lr=0.0,
+                             eps=1e-15)
+    ms, kt, _ = timed(lambda: opt.step(vis, N), args.steps, args.warmup)
+    n_vis = int(vis.sum().item())
+    floats = sum(ADAM_GROUPS.values())
+    alg = n_vis * floats * 28 + N      # read param, grad, m, v and write param, m, v per visible element
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
+    roofline = roofline_of("adam_kernel", alg, avg_launch.get("adam_kernel", float("nan")))
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        n = 1_000_000
+        vis_np = vis[:n].cpu().numpy().astype(np.uint8)
+        arrs = {k: [np.zeros((n, m), np.float32) for _ in range(3)] + [rng.normal(0, 1, (n, m)).astype(np.float32)]
+                for k, m in ADAM_GROUPS.items()}
+        t1 = time.perf_counter()
+        for k, (p, m, v, g) in arrs.items():
+            O.adam_update(p, g, m, v, vis_np, 1e-3, 0.9, 0.999, 1e-15)
+        dt = time.perf_counter() - t1
+        cpu = {"value": round(n / dt, 1), "unit": "Gaussians/s", "cores": O.num_threads(), "kind": "port",
+               "sample": f"CPU oracle sparse Adam, six groups, first {n} of {N} Gaussians; {dt * 1e3:.0f} ms"}
+    out = header(args, "SparseGaussianAdam step Gaussians/s (59 floats per Gaussian)", N / (ms * 1e-3),
+                 "Gaussians/s", ms, "f32", f"config2-size optimiser step: {N} Gaussians, {n_vis} visible",
+                 {"gaussians": N, "visible": n_vis, "floats_per_gaussian": floats})
+    out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -387,7 +436,7 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     _lib.load()
-    {"step": run_step, "knn": run_knn, "ssim": run_ssim}[args.workload](args)
+    {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -17,6 +17,13 @@ _f = C.c_float
 _i64 = C.c_int64
 _sz = C.c_size_t
 
+
+class AdamGroup(C.Structure):
+    """gs_adam_group (include/blitzgs_amd.h)."""
+    _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("exp_avg", C.c_void_p), ("exp_avg_sq", C.c_void_p),
+                ("M", C.c_int64), ("lr", C.c_float), ("eps", C.c_float)]
+
+
 _SIGS = {
     "gs_version": (_i, []),
     "gs_last_error": (C.c_char_p, []),
@@ -37,6 +44,8 @@ _SIGS = {
     "gs_knn_meandist3": (_i, [_i, _c, _c, _c, _c]),
     "gs_ssim_forward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c]),
     "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_adam_update": (_i, [_c, _c, _c, _c, _c, _f, _f, _f, _f, _i64, _i64, _c]),
+    "gs_adam_update_groups": (_i, [_i, C.POINTER(AdamGroup), _i64, _c, _f, _f, _c]),
     "gs_diag_math": (_i, [_i, _i, _c, _c, _c]),
     "gs_timing_enable": (_i, [_i]),
     "gs_timing_reset": (_i, []),

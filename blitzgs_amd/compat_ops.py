@@ -14,6 +14,7 @@ backward_render_time in ms).  The routing helpers of the multi-GPU path
 import torch
 
 from . import rasterizer as _r
+from .adam import adamUpdate  # noqa: F401  (the reference's _C.adamUpdate)
 
 
 class _RS:

@@ -3,6 +3,7 @@
 backed by the gfx950 HIP library.  Render ops dispatch to the same library the
 _r drop-in uses (the reference routes them to _r, __init__.py:24-46)."""
 from blitzgs_amd import compat_ops as _C
+from blitzgs_amd.adam import SparseGaussianAdam
 from blitzgs_amd.rasterizer import (GaussianRasterizationSettings, GaussianRasterizer, _PreprocessGaussians,
                                     _RenderGaussians, preprocess_gaussians, render_gaussians)
 
@@ -16,4 +17,4 @@ def _get_split_op_backend(op_name):
 
 
 __all__ = ["GaussianRasterizationSettings", "GaussianRasterizer", "preprocess_gaussians", "render_gaussians",
-           "_get_split_op_backend", "_C"]
+           "_get_split_op_backend", "_C", "SparseGaussianAdam"]

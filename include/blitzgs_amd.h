@@ -163,6 +163,33 @@ int gs_ssim_backward(int B, int C, int H, int W, float C1, float C2, const float
                      gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Sparse Adam step.  gs_adam_update replaces the reference's adamUpdate
+ * (diff-gaussian-rasterization_f/rasterize_points.cu:807-832, kernel
+ * cuda_rasterizer/adam.cu:9-67): for every element p of a (N, M) parameter
+ * whose Gaussian p / M has visible != 0,
+ *   m = b1 m + (1 - b1) g,  v = b2 v + (1 - b2) g g,  param += -lr m / (sqrt(v) + eps);
+ * other elements are left unchanged.  gs_adam_update_groups applies the step
+ * to up to 8 parameter groups (SparseGaussianAdam.step's loop over
+ * param_groups, diff_gaussian_rasterization_f/__init__.py:836-863) in one
+ * launch.  All arrays are contiguous fp32; visible is one byte per Gaussian.
+ * ------------------------------------------------------------------------ */
+typedef struct gs_adam_group {
+    float* param;
+    const float* grad;
+    float* exp_avg;
+    float* exp_avg_sq;
+    int64_t M;   /* elements per Gaussian */
+    float lr;
+    float eps;
+} gs_adam_group;
+
+int gs_adam_update(float* param, const float* param_grad, float* exp_avg, float* exp_avg_sq,
+                   const uint8_t* visible, float lr, float b1, float b2, float eps, int64_t N,
+                   int64_t M, gs_stream_t stream);
+int gs_adam_update_groups(int n_groups, const gs_adam_group* groups, int64_t N,
+                          const uint8_t* visible, float b1, float b2, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Diagnostics (no counterpart in the reference): evaluate the device exp / log
  * used by the kernels on n inputs (op 0 = exp, 1 = log, 2 = the blend's exp,
  * 3 = the 12-value wave reduction on 12 x 64 inputs), so tests can compare them

@@ -104,6 +104,10 @@ void o_ssim_bwd(int B, int C, int H, int W, float C1, float C2,
 void o_ssim_window(float* w);
 
 /* Scalar math used by the oracle, exported so tests can pin it. */
+/* sparse Adam step over a (N, M) parameter (adam.cu:9-38) */
+void o_adam_update(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, const uint8_t* visible,
+                   float lr, float b1, float b2, float eps, int64_t N, int64_t M);
+
 void o_vec_expf(int n, const float* x, float* y);
 void o_vec_logf(int n, const float* x, float* y);
 

@@ -204,6 +204,17 @@ def knn_meandist3(points):
     return out
 
 
+def adam_update(param, grad, exp_avg, exp_avg_sq, visible, lr, b1, b2, eps):
+    """In-place sparse Adam step on (N, M) float32 arrays (adam.cu:9-38)."""
+    for a in (param, grad, exp_avg, exp_avg_sq):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    N = param.shape[0]
+    M = param.size // max(N, 1)
+    vis = np.ascontiguousarray(visible, dtype=np.uint8)
+    lib().o_adam_update(_p(param), _p(grad), _p(exp_avg), _p(exp_avg_sq), _p(vis), C.c_float(lr), C.c_float(b1),
+                        C.c_float(b2), C.c_float(eps), C.c_int64(N), C.c_int64(M))
+
+
 def ssim_fwd(img1, img2, C1=0.01 ** 2, C2=0.03 ** 2, train=True):
     img1, img2 = _f32(img1), _f32(img2)
     B, Ch, H, W = img1.shape

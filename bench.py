@@ -13,6 +13,8 @@ generated once (seeded, synthetic) and stay resident in HBM.
 `--workload knn`: distCUDA2 over config 4's 10M points.  `--workload ssim`:
 fused_ssim forward+backward on config 4's 8 x 3 x 1080 x 1920 image pair.
 `--workload adam`: the SparseGaussianAdam step over config 2's 6M Gaussians.
+`--workload route`: one rank's routing + pack/unpack around the screen-space
+all-to-all, config 3's 8M Gaussians split over four tile-row ranks.
 
 Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
 `roofline` describes the dominant kernel, timed live with HIP events on the
@@ -59,7 +61,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam"], default="step")
+    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route"], default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
@@ -421,6 +423,96 @@ def run_adam(args):
     print(json.dumps(out), flush=True)
 
 
+def run_route(args):
+    """One rank's side of the screen-space exchange at config 3's shape: config
+    3's 8M Gaussians (4096x2730) preprocessed once, then per step routed to
+    the four tile-row ranks of the image (rows [0, 43), [43, 86), [86, 129),
+    [129, 171): division_pos * TILE_X), every rank's send ids from one count
+    and one write pass, the send rows of all four ranks packed (means2D 2, rgb
+    3, conic_opacity 4, radii 1, depth 1, means3D 3, scales 3, rotation 4 =
+    21 values per row) and one received buffer of rank 1's size unpacked into
+    contiguous fields."""
+    import torch
+    from blitzgs_amd import rasterizer, routing, synth
+    scene, cam = synth.config3()
+    dev = torch.device("cuda:0")
+    tt = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)
+    rs = rasterizer.GaussianRasterizationSettings(
+        image_height=int(cam["H"]), image_width=int(cam["W"]), tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"],
+        bg=torch.zeros(3, device=dev), scale_modifier=1.0, viewmatrix=tt(cam["viewmatrix"]),
+        projmatrix=tt(cam["projmatrix"]), sh_degree=3, campos=tt(cam["campos"]), prefiltered=False, debug=False)
+    r = rasterizer._preprocess_forward_raw(tt(scene["means3D"]), tt(scene["scales"]), tt(scene["rotations"]),
+                                           tt(scene["sh"]), tt(scene["opacities"]), rs)
+    _, m2d, depths, radii, _, con, rgb, _ = r
+    m3d, sc, rot = tt(scene["means3D"]), tt(scene["scales"]), tt(scene["rotations"])
+    del scene["sh"]
+    H, W = int(cam["H"]), int(cam["W"])
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    rows = [0, 43, 86, 129, gy]
+    st = torch.tensor([v * gx for v in rows], dtype=torch.int32, device=dev)
+    P = int(m2d.size(0))
+    fields = [m2d, rgb, con, radii, depths, m3d, sc, rot]
+    widths = [2, 3, 4, 1, 1, 3, 3, 4]
+    types = [torch.float32] * 3 + [torch.int32] + [torch.float32] * 4
+    info = {}
+
+    def step():
+        ids, cnt, _ = routing.local2j_ids_concat(m2d, radii, H, W, st, 4)
+        buf = routing.pack_rows(ids, fields)
+        s1 = cnt[0]
+        routing.unpack_rows(buf[s1:s1 + cnt[1]], widths, types)
+        info["cnt"] = cnt
+
+    ms, kt, _ = timed(step, args.steps, args.warmup)
+    cnt = info["cnt"]
+    n_send = sum(cnt)
+    row_bytes = 4 * sum(widths)
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    # algorithmic bytes: pack reads an id and a row and writes a row per sent
+    # row; unpack reads and writes a row per received row
+    pack_b = n_send * (8 + 2 * row_bytes)
+    unpack_b = cnt[1] * 2 * row_bytes
+    tot_ms, launches = kt.get("move_rows_kernel", (float("nan"), 1))
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_route_config3.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("move_rows_kernel")
+        except (OSError, ValueError):
+            traffic = None
+    roofline = roofline_of("move_rows_kernel", (pack_b + unpack_b) / 2, tot_ms / max(1, launches), traffic)
+    roofline["note"] = ("two launches per step (pack of every send row, unpack of one rank's rows); achieved = "
+                        "their algorithmic bytes over their time, per launch on average.  The pack gathers sparse "
+                        "rows (20% of 8M) once per destination rank, so its HBM traffic is several times the "
+                        "algorithmic bytes (traffic)")
+    route_b = P * 12 * 2 + n_send * 8   # means2D + radii read by count and write passes; ids written
+    rt_ms = sum(kt.get(k, (0.0, 1))[0] for k in ("route_count_kernel", "route_scan_kernel", "route_write_kernel"))
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        hm, hr = m2d.cpu().numpy(), radii.cpu().numpy()
+        hf = [f.cpu().numpy().reshape(P, -1) for f in fields]
+        t1 = time.perf_counter()
+        b = O.local2j_ids_bool(H, W, hm, hr, st.cpu().numpy())
+        hids = np.concatenate([np.flatnonzero(b[:, k]) for k in range(4)])
+        hbuf = np.concatenate([f[hids].astype(np.float32) for f in hf], axis=1)
+        dt = time.perf_counter() - t1
+        assert hbuf.shape == (n_send, sum(widths))
+        cpu = {"value": round(P / dt, 1), "unit": "Gaussians/s", "cores": O.num_threads(), "kind": "port",
+               "sample": f"CPU oracle routing of all {P} Gaussians + numpy nonzero and row gather of the send "
+                         f"rows (no unpack); {dt * 1e3:.0f} ms"}
+    out = header(args, "exchange-side routing + pack/unpack Gaussians/s (one rank, 4 tile-row ranks)",
+                 P / (ms * 1e-3), "Gaussians/s", ms, "f32/int32",
+                 f"config3-shape routing: {P} Gaussians, 4096x2730, 4 ranks by tile rows",
+                 {"gaussians": P, "ranks": 4, "rows_sent": n_send, "rows_per_rank": cnt,
+                  "values_per_row": sum(widths)})
+    out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
+    out["routing_GBs"] = round(route_b / (rt_ms / max(1, args.steps) * 1e-3) / 1e9, 1) if rt_ms else None
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -436,7 +528,7 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     _lib.load()
-    {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam}[args.workload](args)
+    {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam, "route": run_route}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -18,6 +18,12 @@ _i64 = C.c_int64
 _sz = C.c_size_t
 
 
+class RowField(C.Structure):
+    """gs_row_field (include/blitzgs_amd.h)."""
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("src_stride", C.c_int64), ("dst_stride", C.c_int64),
+                ("width", C.c_int32), ("src_type", C.c_int32), ("dst_type", C.c_int32)]
+
+
 class AdamGroup(C.Structure):
     """gs_adam_group (include/blitzgs_amd.h)."""
     _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("exp_avg", C.c_void_p), ("exp_avg_sq", C.c_void_p),
@@ -46,6 +52,11 @@ _SIGS = {
     "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_adam_update": (_i, [_c, _c, _c, _c, _c, _f, _f, _f, _f, _i64, _i64, _c]),
     "gs_adam_update_groups": (_i, [_i, C.POINTER(AdamGroup), _i64, _c, _f, _f, _c]),
+    "gs_local2j_ids_bool": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c]),
+    "gs_local2j_workspace_bytes": (_sz, [_i, _i]),
+    "gs_local2j_count": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c, _c, _c]),
+    "gs_local2j_write": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c, _i64, _c]),
+    "gs_move_rows": (_i, [_i64, _c, _i64, _c, _i64, _i, C.POINTER(RowField), _i, _c]),
     "gs_diag_math": (_i, [_i, _i, _c, _c, _c]),
     "gs_timing_enable": (_i, [_i]),
     "gs_timing_reset": (_i, []),

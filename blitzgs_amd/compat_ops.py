@@ -6,15 +6,19 @@ diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
   preprocess_gaussians_backward   _f/rasterize_points.cu:926-1029
   render_gaussians                _r/rasterize_points.cu:273-361
   render_gaussians_backward       _r/rasterize_points.cu:363-436
+  get_local2j_ids_bool            _f/rasterize_points.cu:258-289
+  get_local2j_ids_bool_adjust_mode6  _f/rasterize_points.cu:337-367
+  adamUpdate                      _f/rasterize_points.cu:807-832
 Same positional arguments and return tuples; `args` is the reference's
 cuda_args dict (its "stats_collector" entry receives forward_render_time /
-backward_render_time in ms).  The routing helpers of the multi-GPU path
-(get_local2j_ids_bool*, image-tile utilities) are not implemented.
+backward_render_time in ms).  mark_visible and the image-tile utilities of the
+multi-GPU path are not implemented.
 """
 import torch
 
 from . import rasterizer as _r
 from .adam import adamUpdate  # noqa: F401  (the reference's _C.adamUpdate)
+from .routing import get_local2j_ids_bool, get_local2j_ids_bool_adjust_mode6  # noqa: F401
 
 
 class _RS:
@@ -79,6 +83,4 @@ def _not_here(name):
     return f
 
 
-get_local2j_ids_bool = _not_here("get_local2j_ids_bool")
-get_local2j_ids_bool_adjust_mode6 = _not_here("get_local2j_ids_bool_adjust_mode6")
 mark_visible = _not_here("mark_visible")

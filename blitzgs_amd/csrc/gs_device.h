@@ -195,6 +195,35 @@ __device__ __forceinline__ int rank_below(uint64_t m)
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Exclusive scan of one value per thread over a 1024-thread block; returns
+// the prefix and writes the block total to *total (all threads).
+__device__ __forceinline__ uint32_t block_excl_scan_1024(uint32_t v, uint32_t* s_wave, uint32_t* total)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wave[wid] = x;
+    __syncthreads();
+    if (wid == 0) {
+        uint32_t w = lane < 16 ? s_wave[lane] : 0;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const uint32_t y = __shfl_up(w, off, 64);
+            if (lane >= off) w += y;
+        }
+        if (lane < 16) s_wave[16 + lane] = w;
+    }
+    __syncthreads();
+    const uint32_t wbase = wid == 0 ? 0 : s_wave[16 + wid - 1];
+    *total = s_wave[31];
+    __syncthreads();
+    return wbase + x - v;
+}
+
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v)
 {

@@ -152,35 +152,6 @@ const T* at(const void* base, size_t off) { return reinterpret_cast<const T*>(st
 
 // ---------------------------------------------------------------- scans
 
-// Exclusive scan of one value per thread over a 1024-thread block; returns
-// the prefix and writes the block total to *total (all threads).
-__device__ __forceinline__ uint32_t block_excl_scan_1024(uint32_t v, uint32_t* s_wave, uint32_t* total)
-{
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
-    if (lane == 63) s_wave[wid] = x;
-    __syncthreads();
-    if (wid == 0) {
-        uint32_t w = lane < 16 ? s_wave[lane] : 0;
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-            const uint32_t y = __shfl_up(w, off, 64);
-            if (lane >= off) w += y;
-        }
-        if (lane < 16) s_wave[16 + lane] = w;
-    }
-    __syncthreads();
-    const uint32_t wbase = wid == 0 ? 0 : s_wave[16 + wid - 1];
-    *total = s_wave[31];
-    __syncthreads();
-    return wbase + x - v;
-}
-
 // compute_locally -> local tile numbering; clears the per-tile counters
 // compute_locally -> local tile numbering and the bounding box of the local
 // tiles (meta[5..8] = x0, y0, x1, y1, exclusive ends; empty box if none);
@@ -199,7 +170,7 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
         const int t = t0 + threadIdx.x;
         const uint32_t f = (t < T && cl[t]) ? 1u : 0u;
         uint32_t tot;
-        const uint32_t pre = block_excl_scan_1024(f, s_wave, &tot);
+        const uint32_t pre = gs::block_excl_scan_1024(f, s_wave, &tot);
         if (t < T) {
             loc_map[t] = f ? (int)(base + pre) : -1;
             if (f) {
@@ -394,7 +365,7 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
             const int wi = w0 + threadIdx.x;
             const uint32_t v = wi < NW ? wcount[wi] : 0u;
             uint32_t tot;
-            const uint32_t pre = block_excl_scan_1024(v, s_wave, &tot);
+            const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
             if (wi < NW) wcount[wi] = base + pre;
             base += tot;
         }
@@ -405,7 +376,7 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
         const int l = t0 + threadIdx.x;
         const uint32_t v = l < TL ? tile_count[l] : 0u;
         uint32_t tot;
-        const uint32_t pre = block_excl_scan_1024(v, s_wave, &tot);
+        const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
         if (l < TL) {
             tile_start[l] = (uint32_t)(base + pre);
             cursor[l] = (uint32_t)(base + pre);

@@ -26,6 +26,9 @@
  *   simple-knn/spatial.cu:15-26                                distCUDA2
  *   fused-ssim/ssim.cu:367-402                                 fusedssim
  *   fused-ssim/ssim.cu:404-441                                 fusedssim_backward
+ *   diff-gaussian-rasterization_f/rasterize_points.cu:258-289  GetLocal2jIdsBoolCUDA
+ *   diff-gaussian-rasterization_f/rasterize_points.cu:337-367  GetLocal2jIdsBoolAdjustMode6CUDA
+ *   diff-gaussian-rasterization_f/rasterize_points.cu:807-832  adamUpdate
  */
 #ifndef BLITZGS_AMD_H
 #define BLITZGS_AMD_H
@@ -188,6 +191,75 @@ int gs_adam_update(float* param, const float* param_grad, float* exp_avg, float*
                    int64_t M, gs_stream_t stream);
 int gs_adam_update_groups(int n_groups, const gs_adam_group* groups, int64_t N,
                           const uint8_t* visible, float b1, float b2, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Gaussian -> rank routing of the image-distributed step.
+ *
+ * gs_local2j_ids_bool replaces GetLocal2jIdsBoolCUDA (mode GS_ROUTE_INTERVAL,
+ * diff-gaussian-rasterization_f/rasterize_points.cu:258-289, kernel :212-256)
+ * and GetLocal2jIdsBoolAdjustMode6CUDA (mode GS_ROUTE_RECT, :337-367, kernel
+ * :291-335).  It writes every byte of the (P, world_size) bool matrix `out`
+ * (1 = rank rk's tiles meet Gaussian i's rect).  table: GS_ROUTE_INTERVAL ->
+ * world_size + 1 ascending tile indices (dist_global_strategy);
+ * GS_ROUTE_RECT -> world_size rows of (y_l, y_r, x_l, x_r) tile bounds.
+ * means2D (P, 2) fp32, radii (P) int32, table int32, all device memory.
+ * Any world_size >= 1.
+ *
+ * gs_local2j_count + gs_local2j_write replace the bool matrix followed by one
+ * nonzero() per rank (gaussian_renderer/workload_division.py:698-704, also
+ * :161-167 and :460-468): count writes counts[rk] (int64 device array of
+ * world_size + 1; counts[world_size] = total) and, if out_bool is non-null, the
+ * bool matrix; after the caller has read the counts, write stores every rank's
+ * ids (int64, ascending) into `ids`, concatenated rank after rank (rank rk's
+ * list starts at counts[0] + ... + counts[rk-1]); n_ids = counts[world_size],
+ * the size of `ids` (no id is stored at or past it).  world_size <= 64 and
+ * P * world_size < 2^32.  workspace: gs_local2j_workspace_bytes(P, world_size)
+ * bytes of device memory, passed unchanged from count to write.
+ * ------------------------------------------------------------------------ */
+#define GS_ROUTE_INTERVAL 0
+#define GS_ROUTE_RECT 1
+
+int gs_local2j_ids_bool(int mode, int P, int H, int W, int world_size, const float* means2D,
+                        const int* radii, const int* table, int avoid_pixel_all2all, uint8_t* out,
+                        gs_stream_t stream);
+size_t gs_local2j_workspace_bytes(int P, int world_size);
+int gs_local2j_count(int mode, int P, int H, int W, int world_size, const float* means2D,
+                     const int* radii, const int* table, int avoid_pixel_all2all, uint8_t* out_bool,
+                     int64_t* counts, void* workspace, gs_stream_t stream);
+int gs_local2j_write(int mode, int P, int H, int W, int world_size, const float* means2D,
+                     const int* radii, const int* table, int avoid_pixel_all2all,
+                     const void* workspace, int64_t* ids, int64_t n_ids, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * Row mover for the screen-space exchange: replaces, in one launch each, the
+ * torch.cat(fields, 1)[ids] pack per destination rank, the split + cat +
+ * .contiguous() + radii .float()/.int() unpack of what was received
+ * (gaussian_renderer/__init__.py:64-189) and the autograd backward of the
+ * pack (index_put of gradient rows into zero-filled per-field gradients).
+ * Output row r takes source row src_rows[r] (r if NULL; an entry outside
+ * [0, n_src_rows) reads as zeros) and stores into destination row dst_rows[r]
+ * (r if NULL; an entry outside [0, n_dst_rows) is skipped), for each
+ * field: `width` elements at src + row*src_stride -> dst + row*dst_stride
+ * (strides in elements).  Types convert as torch's .float() / .int() do.
+ * accumulate != 0 adds into the destination (equal types only).  Up to 8
+ * fields and 32 columns in all; rows named twice in dst_rows race.
+ * ------------------------------------------------------------------------ */
+#define GS_ROW_F32 0
+#define GS_ROW_I32 1
+
+typedef struct gs_row_field {
+    const void* src;
+    void* dst;
+    int64_t src_stride;
+    int64_t dst_stride;
+    int32_t width;
+    int32_t src_type;   /* GS_ROW_F32 or GS_ROW_I32 */
+    int32_t dst_type;
+} gs_row_field;
+
+int gs_move_rows(int64_t n_rows, const int64_t* src_rows, int64_t n_src_rows, const int64_t* dst_rows,
+                 int64_t n_dst_rows, int n_fields, const gs_row_field* fields, int accumulate,
+                 gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Diagnostics (no counterpart in the reference): evaluate the device exp / log

@@ -16,7 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "liboracle_gs.so")
-SOURCES = ["o_preprocess.c", "o_render.c", "o_knn_ssim.c", "o_adam.c"]
+SOURCES = ["o_preprocess.c", "o_render.c", "o_knn_ssim.c", "o_adam.c", "o_route.c"]
 HEADERS = ["o_math.h", "gs_oracle.h"]
 CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
           "-mfma", "-fno-math-errno", "-Wall", "-Wno-unused-function"]

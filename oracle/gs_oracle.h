@@ -108,6 +108,15 @@ void o_ssim_window(float* w);
 void o_adam_update(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, const uint8_t* visible,
                    float lr, float b1, float b2, float eps, int64_t N, int64_t M);
 
+/* Gaussian -> rank routing, (P, world) bool rows (rasterize_points.cu:212-289):
+ * rank rk gets Gaussian i when the linear tile-index span of its rect meets
+ * [strategy[rk], strategy[rk+1]) (widened by one tile row + 1 when avoid). */
+void o_local2j_ids_bool(int P, int H, int W, int world, const float* means2D, const int* radii,
+                        const int* strategy, int avoid, uint8_t* out);
+/* Same with one tile rectangle (y_l, y_r, x_l, x_r) per rank (rasterize_points.cu:291-367). */
+void o_local2j_ids_bool_rect(int P, int H, int W, int world, const float* means2D, const int* radii,
+                             const int* rectangles, int avoid, uint8_t* out);
+
 void o_vec_expf(int n, const float* x, float* y);
 void o_vec_logf(int n, const float* x, float* y);
 

@@ -37,7 +37,7 @@ def lib():
         _lib.o_num_threads.restype = C.c_int
         for name in ["o_preprocess_fwd", "o_preprocess_bwd", "o_binning", "o_render_fwd",
                      "o_render_bwd", "o_knn_meandist3", "o_ssim_fwd", "o_ssim_bwd",
-                     "o_vec_expf", "o_vec_logf"]:
+                     "o_vec_expf", "o_vec_logf", "o_local2j_ids_bool", "o_local2j_ids_bool_rect"]:
             getattr(_lib, name).restype = None
         del fp
     return _lib
@@ -213,6 +213,30 @@ def adam_update(param, grad, exp_avg, exp_avg_sq, visible, lr, b1, b2, eps):
     vis = np.ascontiguousarray(visible, dtype=np.uint8)
     lib().o_adam_update(_p(param), _p(grad), _p(exp_avg), _p(exp_avg_sq), _p(vis), C.c_float(lr), C.c_float(b1),
                         C.c_float(b2), C.c_float(eps), C.c_int64(N), C.c_int64(M))
+
+
+def local2j_ids_bool(H, W, means2D, radii, strategy, avoid=False):
+    """(P, world) bool routing matrix, interval mode (rasterize_points.cu:212-289).
+    strategy holds world + 1 tile indices."""
+    m2d = _f32(means2D).reshape(-1, 2)
+    r = np.ascontiguousarray(radii, dtype=np.int32)
+    st = np.ascontiguousarray(strategy, dtype=np.int32)
+    P, world = m2d.shape[0], st.size - 1
+    out = np.empty((P, world), np.uint8)
+    lib().o_local2j_ids_bool(P, H, W, world, _p(m2d), _p(r), _p(st), int(bool(avoid)), _p(out))
+    return out.astype(bool)
+
+
+def local2j_ids_bool_rect(H, W, means2D, radii, rectangles, avoid=False):
+    """(P, world) bool routing matrix, one tile rectangle (y_l, y_r, x_l, x_r)
+    per rank (rasterize_points.cu:291-367)."""
+    m2d = _f32(means2D).reshape(-1, 2)
+    r = np.ascontiguousarray(radii, dtype=np.int32)
+    rc = np.ascontiguousarray(rectangles, dtype=np.int32).reshape(-1, 4)
+    P, world = m2d.shape[0], rc.shape[0]
+    out = np.empty((P, world), np.uint8)
+    lib().o_local2j_ids_bool_rect(P, H, W, world, _p(m2d), _p(r), _p(rc), int(bool(avoid)), _p(out))
+    return out.astype(bool)
 
 
 def ssim_fwd(img1, img2, C1=0.01 ** 2, C2=0.03 ** 2, train=True):

@@ -53,3 +53,28 @@ def test_argument_errors_without_device(lib):
     assert rc != 0 and b"coefficients" in lib.gs_last_error()
     rc = lib.gs_diag_math(7, 1, None, None, None)
     assert rc != 0 and b"op" in lib.gs_last_error()
+
+
+def test_routing_argument_errors_without_device(lib):
+    # all of these fail in argument checks, before any HIP call
+    rc = lib.gs_local2j_ids_bool(7, 10, 64, 64, 2, None, None, None, 0, None, None)
+    assert rc != 0 and b"mode" in lib.gs_last_error()
+    rc = lib.gs_local2j_ids_bool(0, 10, 64, 64, 0, None, None, None, 0, None, None)
+    assert rc != 0 and b"world_size" in lib.gs_last_error()
+    rc = lib.gs_local2j_count(0, 10, 64, 64, 65, C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), 0, None,
+                              C.c_void_p(16), C.c_void_p(16), None)
+    assert rc != 0 and b"exceeds 64" in lib.gs_last_error()
+    assert lib.gs_local2j_workspace_bytes(6_000_000, 4) >= 4 * 4
+    assert lib.gs_local2j_workspace_bytes(-1, 4) == 0
+    f = (_lib.RowField * 1)(_lib.RowField(src=16, dst=16, src_stride=40, dst_stride=40, width=40, src_type=0,
+                                          dst_type=0))
+    rc = lib.gs_move_rows(10, None, 10, None, 10, 1, f, 0, None)
+    assert rc != 0 and b"columns" in lib.gs_last_error()
+    f = (_lib.RowField * 1)(_lib.RowField(src=16, dst=16, src_stride=1, dst_stride=1, width=1, src_type=0,
+                                          dst_type=1))
+    rc = lib.gs_move_rows(10, None, 10, None, 10, 1, f, 1, None)
+    assert rc != 0 and b"accumulate" in lib.gs_last_error()
+    rc = lib.gs_move_rows(10, None, 10, None, 10, 9, f, 0, None)
+    assert rc != 0 and b"n_fields" in lib.gs_last_error()
+    rc = lib.gs_move_rows(11, None, 10, None, 11, 1, f, 0, None)
+    assert rc != 0 and b"source rows" in lib.gs_last_error()

@@ -88,6 +88,65 @@ void o_render_bwd(int P, int W, int H, const float* bg,
                   float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
                   float* dL_dopacity, float* dL_dcolors);
 
+/* ---- full-image path (_f GaussianRasterizer.forward / render_simp) ---- */
+
+/* preprocessCUDA with the full path's arguments (_f forward.cu:165-284,
+ * rasterizer_impl.cu:396-424): culling mask (nonzero = skip), precomputed
+ * colours / 3D covariances (NULL = compute), SH as dc (P,1,3) + rest
+ * (P,M,3); also writes the float tile-rect extents rects (P,2) and the rect
+ * tile counts tiles_touched (P). */
+void o_preprocess_fwd_full(int P, int M, const o_camera* cam,
+                           const float* means3D, const float* scales, const float* rotations,
+                           const float* dc, const float* rest, const float* opacities,
+                           const float* colors_precomp, const float* cov3D_precomp, const uint8_t* culling,
+                           float* means2D, float* depths, int* radii, float* cov3D,
+                           float* conic_opacity, float* rgb, uint8_t* clamped,
+                           float* rects, uint32_t* tiles_touched);
+
+/* BACKWARD::preprocess with the full path's arguments (_f backward.cu:759-827,
+ * rasterizer_impl.cu:931-954).  dL_dmeans2D (P,3), dL_dconic (P,4) float4
+ * slots (.x=c00, .y=c01, .w=c11), dL_dcolors (P,3).  Outputs fully written. */
+void o_preprocess_bwd_full(int P, int M, const o_camera* cam,
+                           const float* means3D, const float* scales, const float* rotations,
+                           const float* dc, const float* rest, const float* colors_precomp,
+                           const float* cov3D_precomp, const int* radii, const float* cov3D,
+                           const uint8_t* clamped, const float* dL_dmeans2D, const float* dL_dconic,
+                           const float* dL_dcolors,
+                           float* dL_dmeans3D, float* dL_dcov3D, float* dL_ddc, float* dL_drest,
+                           float* dL_dscales, float* dL_drotations);
+
+/* The tile-culling test of the full path's duplicateWithKeys
+ * (rasterizer_impl.cu:56-95,144-167); 1 = keep tile (tx, ty). */
+int o_full_tile_keep(const float* xy, const float* co, unsigned tx, unsigned ty);
+
+/* Binning of the full path (rasterizer_impl.cu:119-210,440-480).  R = sum of
+ * tiles_touched; keys/values hold R entries (culled slots padded with the
+ * invalid key, sorted last).  Returns the valid instances; *num_buckets =
+ * sum of ceil(tile length / 32). */
+int64_t o_binning_full(int P, int W, int H, const float* means2D, const float* depths, const int* radii,
+                       const float* rects, const float* conic_opacity, const uint32_t* tiles_touched,
+                       int64_t R, uint64_t* keys, uint32_t* values, uint32_t* ranges, int64_t* num_buckets);
+
+/* renderCUDA / render_simpCUDA of the full path (forward.cu:291-607).
+ * accum_weights / accum_weights_count NULL for renderCUDA.  Accumulators
+ * are added to (caller zeroes them). */
+void o_render_fwd_full(int P, int W, int H, const float* bg, const float* means2D, const float* conic_opacity,
+                       const float* colors, const uint32_t* ranges, const uint32_t* point_list, int flag_max_count,
+                       float* out_color, float* final_T, uint32_t* n_contrib, uint32_t* max_contrib,
+                       float* accum_max_count, float* accum_weights, int32_t* accum_weights_count);
+
+/* Render backward of the full path: the split path's per-pixel gradients
+ * with PerGaussianRenderCUDA's rule (_f backward.cu:403-588): no
+ * |dL/dmean2D|, no conic / opacity gradient where opacity * G > 0.99.
+ * dL_dmean2D (P,3), dL_dconic (P,4) float4 slots, dL_dopacity (P),
+ * dL_dcolors (P,3); accumulated (caller zeroes them). */
+void o_render_bwd_full(int P, int W, int H, const float* bg,
+                       const float* means2D, const float* conic_opacity, const float* colors,
+                       const uint32_t* ranges, const uint32_t* point_list,
+                       const float* final_T, const uint32_t* n_contrib,
+                       const float* dL_dpixels,
+                       float* dL_dmean2D, float* dL_dconic, float* dL_dopacity, float* dL_dcolors);
+
 /* distCUDA2 (simple-knn simple_knn.cu:148-221): mean of the three smallest
  * squared distances to other points.  Exact; O(P log P) grid search. */
 void o_knn_meandist3(int P, const float* points, float* out);

@@ -156,11 +156,26 @@ static void sh_fwd(int deg, const float* pos, const float* campos, const float* 
     }
 }
 
-void o_preprocess_fwd(int P, int K, const o_camera* cam,
-                      const float* means3D, const float* scales, const float* rotations,
-                      const float* sh, const float* opacities,
-                      float* means2D, float* depths, int* radii, float* cov3D,
-                      float* conic_opacity, float* rgb, uint8_t* clamped)
+/* Options of the full-image path's preprocess (forward.cu:165-284 with the
+ * arguments rasterizer_impl.cu:396-424 passes): a culling mask, precomputed
+ * colours or 3D covariances, the SH DC term and the rest in separate arrays,
+ * and the float tile rect + tile count outputs.  The split path uses none. */
+typedef struct {
+    const uint8_t* culling;          /* P, nonzero = skip              */
+    const float* colors_precomp;     /* P x 3 or NULL                  */
+    const float* cov3D_precomp;      /* P x 6 or NULL                  */
+    const float* dc;                 /* P x 3 (with rest) or NULL      */
+    const float* rest;               /* P x M x 3                      */
+    int M;
+    float* rects;                    /* P x 2 or NULL                  */
+    uint32_t* tiles_touched;         /* P or NULL                      */
+} pre_opts;
+
+static void pre_fwd(int P, int K, const o_camera* cam,
+                    const float* means3D, const float* scales, const float* rotations,
+                    const float* sh, const float* opacities, const pre_opts* o,
+                    float* means2D, float* depths, int* radii, float* cov3D,
+                    float* conic_opacity, float* rgb, uint8_t* clamped)
 {
     const int W = cam->W, H = cam->H;
     const float fy = (float)H / (2.0f * cam->tanfovy);   /* rasterizer_impl.cu:1008-1009 */
@@ -176,6 +191,9 @@ void o_preprocess_fwd(int P, int K, const o_camera* cam,
         for (int k = 0; k < 6; k++) cov3D[6 * idx + k] = 0.f;
         for (int k = 0; k < 4; k++) conic_opacity[4 * idx + k] = 0.f;
         for (int k = 0; k < 3; k++) { rgb[3 * idx + k] = 0.f; clamped[3 * idx + k] = 0; }
+        if (o->rects) { o->rects[2 * idx] = 0.f; o->rects[2 * idx + 1] = 0.f; }
+        if (o->tiles_touched) o->tiles_touched[idx] = 0;
+        if (o->culling && o->culling[idx]) continue;    /* forward.cu:199-200 */
 
         const float* m = means3D + 3 * idx;
         /* in_frustum (auxiliary.h:158-184): near cull on view-space z */
@@ -189,8 +207,12 @@ void o_preprocess_fwd(int P, int K, const o_camera* cam,
         const float pp0 = ph[0] * pw, pp1 = ph[1] * pw;
 
         float c6[6];
-        cov3d_fwd(scales + 3 * idx, cam->scale_modifier, rotations + 4 * idx, c6);
-        for (int k = 0; k < 6; k++) cov3D[6 * idx + k] = c6[k];
+        if (o->cov3D_precomp) {
+            for (int k = 0; k < 6; k++) c6[k] = o->cov3D_precomp[6 * idx + k];
+        } else {
+            cov3d_fwd(scales + 3 * idx, cam->scale_modifier, rotations + 4 * idx, c6);
+            for (int k = 0; k < 6; k++) cov3D[6 * idx + k] = c6[k];
+        }
 
         o_ewa e;
         ewa_setup(m, fx, fy, cam->tanfovx, cam->tanfovy, V, &e);
@@ -230,11 +252,23 @@ void o_preprocess_fwd(int P, int K, const o_camera* cam,
         v = o_f2i_sat(floorf((pix1 - ey) / 16.0f)); unsigned rminy = (unsigned)(v < 0 ? 0 : v); if (rminy > gy) rminy = gy;
         v = o_f2i_sat(ceilf((pix0 + ex) / 16.0f));  unsigned rmaxx = (unsigned)(v < 0 ? 0 : v); if (rmaxx > gx) rmaxx = gx;
         v = o_f2i_sat(ceilf((pix1 + ey) / 16.0f));  unsigned rmaxy = (unsigned)(v < 0 ? 0 : v); if (rmaxy > gy) rmaxy = gy;
-        if ((rmaxx - rminx) * (rmaxy - rminy) == 0) continue;
+        const unsigned tiles = (rmaxx - rminx) * (rmaxy - rminy);
+        if (tiles == 0) continue;
 
-        float col[3];
-        sh_fwd(cam->sh_degree, m, cam->campos, sh + (size_t)idx * K * 3, col, clamped + 3 * idx);
-        rgb[3 * idx] = col[0]; rgb[3 * idx + 1] = col[1]; rgb[3 * idx + 2] = col[2];
+        /* forward.cu:268-275: SH colour unless colours are precomputed */
+        if (!o->colors_precomp) {
+            float col[3];
+            if (o->dc) {
+                float s48[48];
+                for (int c = 0; c < 3; c++) s48[c] = o->dc[3 * idx + c];
+                const int need = (cam->sh_degree + 1) * (cam->sh_degree + 1) - 1;
+                for (int k = 0; k < 3 * need; k++) s48[3 + k] = o->rest[(size_t)idx * o->M * 3 + k];
+                sh_fwd(cam->sh_degree, m, cam->campos, s48, col, clamped + 3 * idx);
+            } else {
+                sh_fwd(cam->sh_degree, m, cam->campos, sh + (size_t)idx * K * 3, col, clamped + 3 * idx);
+            }
+            rgb[3 * idx] = col[0]; rgb[3 * idx + 1] = col[1]; rgb[3 * idx + 2] = col[2];
+        }
 
         depths[idx] = pv[2];
         radii[idx] = o_f2i_sat(ceilf(my_radius));
@@ -243,7 +277,33 @@ void o_preprocess_fwd(int P, int K, const o_camera* cam,
         conic_opacity[4 * idx + 1] = con1;
         conic_opacity[4 * idx + 2] = con2;
         conic_opacity[4 * idx + 3] = opacity;
+        if (o->rects) { o->rects[2 * idx] = ex; o->rects[2 * idx + 1] = ey; }
+        if (o->tiles_touched) o->tiles_touched[idx] = tiles;
     }
+}
+
+void o_preprocess_fwd(int P, int K, const o_camera* cam,
+                      const float* means3D, const float* scales, const float* rotations,
+                      const float* sh, const float* opacities,
+                      float* means2D, float* depths, int* radii, float* cov3D,
+                      float* conic_opacity, float* rgb, uint8_t* clamped)
+{
+    const pre_opts o = { 0 };
+    pre_fwd(P, K, cam, means3D, scales, rotations, sh, opacities, &o, means2D, depths, radii, cov3D,
+            conic_opacity, rgb, clamped);
+}
+
+void o_preprocess_fwd_full(int P, int M, const o_camera* cam,
+                           const float* means3D, const float* scales, const float* rotations,
+                           const float* dc, const float* rest, const float* opacities,
+                           const float* colors_precomp, const float* cov3D_precomp, const uint8_t* culling,
+                           float* means2D, float* depths, int* radii, float* cov3D,
+                           float* conic_opacity, float* rgb, uint8_t* clamped,
+                           float* rects, uint32_t* tiles_touched)
+{
+    const pre_opts o = { culling, colors_precomp, cov3D_precomp, dc, rest, M, rects, tiles_touched };
+    pre_fwd(P, 0, cam, means3D, scales, rotations, NULL, opacities, &o, means2D, depths, radii, cov3D,
+            conic_opacity, rgb, clamped);
 }
 
 /* dnormvdv (auxiliary.h:126-136) */
@@ -359,35 +419,52 @@ static void cov3d_bwd(const float* scale, float mod, const float* q, const float
     dL_drot[3] = 2 * r * (G[0][1] - G[1][0]) + 2 * x * (G[2][0] + G[0][2]) + 2 * y * (G[1][2] + G[2][1]) - 4 * z * (G[1][1] + G[0][0]);
 }
 
-void o_preprocess_bwd(int P, int K, const o_camera* cam,
-                      const float* means3D, const float* scales, const float* rotations,
-                      const float* sh, const int* radii, const float* cov3D,
-                      const uint8_t* clamped,
-                      const float* dL_dmeans2D, int m2d_stride,
-                      const float* dL_dconic_opacity, const float* dL_drgb,
-                      float* dL_dmeans3D, float* dL_dscales, float* dL_drotations,
-                      float* dL_dsh, float* dL_dopacity)
+/* Options of the full-image path's backward (backward.cu:759-827 with the
+ * arguments rasterizer_impl.cu:931-954 passes). */
+typedef struct {
+    int c11_slot;                    /* float4 slot of dL/dconic c11: 2 (split path) or 3 (full path) */
+    const float* cov3D_precomp;      /* P x 6 or NULL: no scale/rotation gradients */
+    int colors_precomp;              /* nonzero: no SH gradients */
+    const float* dc;                 /* split SH: DC term, rest (P x M x 3) */
+    const float* rest;
+    int M;
+    float* dL_ddc;                   /* P x 3 */
+    float* dL_drest;                 /* P x M x 3 */
+    float* dL_dcov3D;                /* P x 6 or NULL */
+} pre_bwd_opts;
+
+static void pre_bwd(int P, int K, const o_camera* cam,
+                    const float* means3D, const float* scales, const float* rotations,
+                    const float* sh, const int* radii, const float* cov3D,
+                    const uint8_t* clamped,
+                    const float* dL_dmeans2D, int m2d_stride,
+                    const float* dL_dconic_opacity, const float* dL_drgb, const pre_bwd_opts* o,
+                    float* dL_dmeans3D, float* dL_dscales, float* dL_drotations,
+                    float* dL_dsh, float* dL_dopacity)
 {
     const int W = cam->W, H = cam->H;
     const float fy = (float)H / (2.0f * cam->tanfovy);   /* rasterizer_impl.cu:1102-1103 */
     const float fx = (float)W / (2.0f * cam->tanfovx);
     const float* V = cam->view;
     const float* PM = cam->proj;
+    const int full = o->dL_ddc != NULL || o->colors_precomp;
 
 #pragma omp parallel for schedule(static)
     for (int idx = 0; idx < P; idx++) {
         /* rasterize_points.cu:977-982: opacity gradient is column 3 for every Gaussian */
-        dL_dopacity[idx] = dL_dconic_opacity[4 * idx + 3];
+        if (dL_dopacity) dL_dopacity[idx] = dL_dconic_opacity[4 * idx + 3];
         float* gm = dL_dmeans3D + 3 * idx;
-        float* gsh = dL_dsh + (size_t)idx * K * 3;
         gm[0] = gm[1] = gm[2] = 0.f;
         for (int k = 0; k < 3; k++) dL_dscales[3 * idx + k] = 0.f;
         for (int k = 0; k < 4; k++) dL_drotations[4 * idx + k] = 0.f;
-        for (int k = 0; k < 3 * K; k++) gsh[k] = 0.f;
+        if (dL_dsh) for (int k = 0; k < 3 * K; k++) dL_dsh[(size_t)idx * K * 3 + k] = 0.f;
+        if (o->dL_ddc) for (int k = 0; k < 3; k++) o->dL_ddc[3 * idx + k] = 0.f;
+        if (o->dL_drest) for (int k = 0; k < 3 * o->M; k++) o->dL_drest[(size_t)idx * o->M * 3 + k] = 0.f;
+        if (o->dL_dcov3D) for (int k = 0; k < 6; k++) o->dL_dcov3D[6 * idx + k] = 0.f;
         if (!(radii[idx] > 0)) continue;
 
         const float* m = means3D + 3 * idx;
-        const float* c6 = cov3D + 6 * idx;
+        const float* c6 = o->cov3D_precomp ? o->cov3D_precomp + 6 * idx : cov3D + 6 * idx;
         /* ---- computeCov2DCUDA (backward.cu:146-276) ---- */
         o_ewa e;
         ewa_setup(m, fx, fy, cam->tanfovx, cam->tanfovy, V, &e);
@@ -401,7 +478,7 @@ void o_preprocess_bwd(int P, int K, const o_camera* cam,
         c = c + 0.3f;
         const float g0 = dL_dconic_opacity[4 * idx + 0];
         const float g1 = dL_dconic_opacity[4 * idx + 1];
-        const float g2 = dL_dconic_opacity[4 * idx + 2];
+        const float g2 = dL_dconic_opacity[4 * idx + o->c11_slot];
         const float denom = a * c - b * b;
         const float denom2inv = 1.0f / ((denom * denom) + 0.0000001f);
         float dL_da = 0, dL_db = 0, dL_dc = 0;
@@ -418,6 +495,7 @@ void o_preprocess_bwd(int P, int K, const o_camera* cam,
             dcov[2] = 2 * u[0] * u[2] * dL_da + (u[0] * w[2] + u[2] * w[0]) * dL_db + 2 * w[0] * w[2] * dL_dc;
             dcov[4] = 2 * u[2] * u[1] * dL_da + (u[1] * w[2] + u[2] * w[1]) * dL_db + 2 * w[1] * w[2] * dL_dc;
         }
+        if (o->dL_dcov3D) for (int k = 0; k < 6; k++) o->dL_dcov3D[6 * idx + k] = dcov[k];
         /* dL/du = 2 S u dL_da + S w dL_db ; dL/dw = 2 S w dL_dc + S u dL_db */
         float du[3], dw[3];
         for (int k = 0; k < 3; k++) {
@@ -451,9 +529,60 @@ void o_preprocess_bwd(int P, int K, const o_camera* cam,
         gm[1] += (PM[4] * m_w - PM[7] * mul1) * gx + (PM[5] * m_w - PM[7] * mul2) * gy;
         gm[2] += (PM[8] * m_w - PM[11] * mul1) * gx + (PM[9] * m_w - PM[11] * mul2) * gy;
 
-        sh_bwd(cam->sh_degree, m, cam->campos, sh + (size_t)idx * K * 3, clamped + 3 * idx,
-               dL_drgb + 3 * idx, gsh, gm);
-        cov3d_bwd(scales + 3 * idx, cam->scale_modifier, rotations + 4 * idx, dcov,
-                  dL_dscales + 3 * idx, dL_drotations + 4 * idx);
+        if (!full) {
+            sh_bwd(cam->sh_degree, m, cam->campos, sh + (size_t)idx * K * 3, clamped + 3 * idx,
+                   dL_drgb + 3 * idx, dL_dsh + (size_t)idx * K * 3, gm);
+        } else if (!o->colors_precomp && o->rest && o->M > 0) {
+            /* backward.cu:392-393: SH gradients only when the rest array exists */
+            const int need = (cam->sh_degree + 1) * (cam->sh_degree + 1);
+            float s48[48], g48[48];
+            for (int k = 0; k < 48; k++) { s48[k] = 0.f; g48[k] = 0.f; }
+            for (int ch = 0; ch < 3; ch++) s48[ch] = o->dc[3 * idx + ch];
+            for (int k = 0; k < 3 * (need - 1); k++) s48[3 + k] = o->rest[(size_t)idx * o->M * 3 + k];
+            sh_bwd(cam->sh_degree, m, cam->campos, s48, clamped + 3 * idx, dL_drgb + 3 * idx, g48, gm);
+            for (int ch = 0; ch < 3; ch++) o->dL_ddc[3 * idx + ch] = g48[ch];
+            for (int k = 0; k < 3 * (need - 1); k++) o->dL_drest[(size_t)idx * o->M * 3 + k] = g48[3 + k];
+        }
+        if (!o->cov3D_precomp)
+            cov3d_bwd(scales + 3 * idx, cam->scale_modifier, rotations + 4 * idx, dcov,
+                      dL_dscales + 3 * idx, dL_drotations + 4 * idx);
     }
+}
+
+void o_preprocess_bwd(int P, int K, const o_camera* cam,
+                      const float* means3D, const float* scales, const float* rotations,
+                      const float* sh, const int* radii, const float* cov3D,
+                      const uint8_t* clamped,
+                      const float* dL_dmeans2D, int m2d_stride,
+                      const float* dL_dconic_opacity, const float* dL_drgb,
+                      float* dL_dmeans3D, float* dL_dscales, float* dL_drotations,
+                      float* dL_dsh, float* dL_dopacity)
+{
+    pre_bwd_opts o = { 0 };
+    o.c11_slot = 2;
+    pre_bwd(P, K, cam, means3D, scales, rotations, sh, radii, cov3D, clamped, dL_dmeans2D, m2d_stride,
+            dL_dconic_opacity, dL_drgb, &o, dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity);
+}
+
+void o_preprocess_bwd_full(int P, int M, const o_camera* cam,
+                           const float* means3D, const float* scales, const float* rotations,
+                           const float* dc, const float* rest, const float* colors_precomp,
+                           const float* cov3D_precomp, const int* radii, const float* cov3D,
+                           const uint8_t* clamped, const float* dL_dmeans2D, const float* dL_dconic,
+                           const float* dL_dcolors,
+                           float* dL_dmeans3D, float* dL_dcov3D, float* dL_ddc, float* dL_drest,
+                           float* dL_dscales, float* dL_drotations)
+{
+    pre_bwd_opts o;
+    o.c11_slot = 3;
+    o.cov3D_precomp = cov3D_precomp;
+    o.colors_precomp = colors_precomp != NULL;
+    o.dc = dc;
+    o.rest = rest;
+    o.M = M;
+    o.dL_ddc = dL_ddc;
+    o.dL_drest = dL_drest;
+    o.dL_dcov3D = dL_dcov3D;
+    pre_bwd(P, 0, cam, means3D, scales, rotations, NULL, radii, cov3D, clamped, dL_dmeans2D, 3, dL_dconic,
+            dL_dcolors, &o, dL_dmeans3D, dL_dscales, dL_drotations, NULL, NULL);
 }

@@ -228,23 +228,25 @@ static inline void atomic_addf(float* p, float v)
     *p += v;
 }
 
-void o_render_bwd(int P, int W, int H, const float* bg,
-                  const float* means2D, const float* conic_opacity, const float* rgb,
-                  const uint8_t* compute_locally,
-                  const uint32_t* ranges, const uint32_t* point_list,
-                  const float* final_T, const uint32_t* n_contrib,
-                  const float* dL_dpixels,
-                  float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
-                  float* dL_dopacity, float* dL_dcolors)
+/* full != 0: the full-image path's rule (_f backward.cu:560-566): no
+ * |dL/dmean2D| output, and no conic / opacity gradient where the alpha clamp
+ * at 0.99 is active (opacity * G > 0.99). */
+static void render_bwd_impl(int full, int W, int H, const float* bg,
+                            const float* means2D, const float* conic_opacity, const float* rgb,
+                            const uint8_t* compute_locally,
+                            const uint32_t* ranges, const uint32_t* point_list,
+                            const float* final_T, const uint32_t* n_contrib,
+                            const float* dL_dpixels,
+                            float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                            float* dL_dopacity, float* dL_dcolors)
 {
-    (void)P;
     const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
     const int T = gx * gy;
     const float alpha_min = 1.0f / 255.0f;
     const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
 #pragma omp parallel for schedule(dynamic, 1)
     for (int t = 0; t < T; t++) {
-        if (!compute_locally[t]) continue;
+        if (compute_locally && !compute_locally[t]) continue;
         const int tx = t % gx, ty = t / gx;
         const int x0 = tx * OT, y0 = ty * OT;
         const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
@@ -295,14 +297,243 @@ void o_render_bwd(int P, int W, int H, const float* bg,
                     const float gmy = dL_dG * dG_ddely * ddely_dy;
                     atomic_addf(&dL_dmean2D[3 * (size_t)id + 0], gmx);
                     atomic_addf(&dL_dmean2D[3 * (size_t)id + 1], gmy);
-                    atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 0], fabsf(gmx));
-                    atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 1], fabsf(gmy));
+                    if (!full) {
+                        atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 0], fabsf(gmx));
+                        atomic_addf(&dL_dmean2D_abs[3 * (size_t)id + 1], fabsf(gmy));
+                    } else if (co[3] * G > 0.99f) {
+                        continue;
+                    }
                     atomic_addf(&dL_dconic[4 * (size_t)id + 0], -0.5f * gdx * dx * dL_dG);
                     atomic_addf(&dL_dconic[4 * (size_t)id + 1], -0.5f * gdx * dy * dL_dG);
                     atomic_addf(&dL_dconic[4 * (size_t)id + 3], -0.5f * gdy * dy * dL_dG);
                     atomic_addf(&dL_dopacity[id], G * dL_dalpha);
                 }
             }
+    }
+}
+
+void o_render_bwd(int P, int W, int H, const float* bg,
+                  const float* means2D, const float* conic_opacity, const float* rgb,
+                  const uint8_t* compute_locally,
+                  const uint32_t* ranges, const uint32_t* point_list,
+                  const float* final_T, const uint32_t* n_contrib,
+                  const float* dL_dpixels,
+                  float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                  float* dL_dopacity, float* dL_dcolors)
+{
+    (void)P;
+    render_bwd_impl(0, W, H, bg, means2D, conic_opacity, rgb, compute_locally, ranges, point_list, final_T,
+                    n_contrib, dL_dpixels, dL_dmean2D, dL_dmean2D_abs, dL_dconic, dL_dopacity, dL_dcolors);
+}
+
+void o_render_bwd_full(int P, int W, int H, const float* bg,
+                       const float* means2D, const float* conic_opacity, const float* colors,
+                       const uint32_t* ranges, const uint32_t* point_list,
+                       const float* final_T, const uint32_t* n_contrib,
+                       const float* dL_dpixels,
+                       float* dL_dmean2D, float* dL_dconic, float* dL_dopacity, float* dL_dcolors)
+{
+    (void)P;
+    render_bwd_impl(1, W, H, bg, means2D, conic_opacity, colors, NULL, ranges, point_list, final_T, n_contrib,
+                    dL_dpixels, dL_dmean2D, NULL, dL_dconic, dL_dopacity, dL_dcolors);
+}
+
+/* ---------------------------------------------------------------- full-image path
+ * (_f/cuda_rasterizer/rasterizer_impl.cu:52-210,336-486, forward.cu:291-614) */
+
+/* max_contrib_power_rect_gaussian_float<15,15> + the keep test of
+ * duplicateWithKeys (rasterizer_impl.cu:56-95,144-167): the smallest value of
+ * the falloff exponent 0.5 (a dx^2 + c dy^2) + b dx dy over the tile's pixel
+ * rect [16x, 16x+15] x [16y, 16y+15] (evaluated at the closest point along the
+ * rect edge nearest the mean), against log(opacity * 255).  Operations are
+ * left to right, no contraction; 1/(225 a) is a correctly rounded division
+ * (__frcp_rn); saturate maps NaN to 0. */
+static inline float sat01(float v) { return v > 0.0f ? (v < 1.0f ? v : 1.0f) : 0.0f; }
+
+int o_full_tile_keep(const float* xy, const float* co, unsigned tx, unsigned ty)
+{
+    const float rminx = (float)(tx * 16u), rminy = (float)(ty * 16u);
+    const float rmaxx = (float)((tx + 1u) * 16u - 1u), rmaxy = (float)((ty + 1u) * 16u - 1u);
+    const float mx = xy[0], my = xy[1];
+    const float a = co[0], b = co[1], c = co[2], o = co[3];
+    const float x_min_diff = rminx - mx;
+    const float x_left = x_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_x = x_left + (mx > rmaxx ? 1.0f : 0.0f);
+    const float y_min_diff = rminy - my;
+    const float y_above = y_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_y = y_above + (my > rmaxy ? 1.0f : 0.0f);
+    float power = 0.0f;
+    if ((not_in_y + not_in_x) > 0.0f) {
+        const float px = x_left * rminx + (1.0f - x_left) * rmaxx;
+        const float py = y_above * rminy + (1.0f - y_above) * rmaxy;
+        const float dx = copysignf(15.0f, x_min_diff);
+        const float dy = copysignf(15.0f, y_min_diff);
+        const float diffx = mx - px, diffy = my - py;
+        const float rcp_x = 1.0f / (225.0f * a);
+        const float rcp_y = 1.0f / (225.0f * c);
+        const float tx_ = not_in_y * sat01((dx * a * diffx + dx * b * diffy) * rcp_x);
+        const float ty_ = not_in_x * sat01((dy * b * diffx + dy * c * diffy) * rcp_y);
+        const float qx = px + tx_ * dx, qy = py + ty_ * dy;
+        const float ex = mx - qx, ey = my - qy;
+        power = 0.5f * (a * ex * ex + c * ey * ey) + b * ex * ey;
+    }
+    const float thr = o_logf(o / (1.0f / 255.0f));
+    return power <= thr;
+}
+
+/* Binning of the full-image path: every Gaussian with radius > 0 reserves
+ * tiles_touched slots (the area of its float-extent rect, getRect(float2,
+ * float2), auxiliary.h:63-73), fills them with the kept tiles in row-major
+ * order and pads the rest with the invalid key (tile 0xFFFFFFFF, depth
+ * FLT_MAX) and value 0xFFFFFFFF; stable sort; ranges of the valid tiles.
+ * Returns the number of valid instances; *num_buckets = sum over tiles of
+ * ceil(len / 32) (perTileBucketCount, rasterizer_impl.cu:244-253). */
+int64_t o_binning_full(int P, int W, int H, const float* means2D, const float* depths, const int* radii,
+                       const float* rects, const float* conic_opacity, const uint32_t* tiles_touched,
+                       int64_t R, uint64_t* keys, uint32_t* values, uint32_t* ranges, int64_t* num_buckets)
+{
+    const unsigned gx = (unsigned)((W + OT - 1) / OT), gy = (unsigned)((H + OT - 1) / OT);
+    const unsigned T = gx * gy;
+    int64_t* off = (int64_t*)malloc(sizeof(int64_t) * (size_t)(P > 0 ? P : 1));
+    int64_t acc = 0;
+    for (int i = 0; i < P; i++) { off[i] = acc; acc += tiles_touched[i]; }
+    const uint32_t flt_max_bits = 0x7f7fffffu;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < P; i++) {
+        if (!(radii[i] > 0)) continue;
+        int64_t o = off[i];
+        const int64_t end = o + tiles_touched[i];
+        const float* p = means2D + 2 * (size_t)i;
+        const float* ex = rects + 2 * (size_t)i;
+        int v;
+        v = o_f2i_sat(floorf((p[0] - ex[0]) / 16.0f)); unsigned x0 = (unsigned)(v < 0 ? 0 : v); if (x0 > gx) x0 = gx;
+        v = o_f2i_sat(floorf((p[1] - ex[1]) / 16.0f)); unsigned y0 = (unsigned)(v < 0 ? 0 : v); if (y0 > gy) y0 = gy;
+        v = o_f2i_sat(ceilf((p[0] + ex[0]) / 16.0f));  unsigned x1 = (unsigned)(v < 0 ? 0 : v); if (x1 > gx) x1 = gx;
+        v = o_f2i_sat(ceilf((p[1] + ex[1]) / 16.0f));  unsigned y1 = (unsigned)(v < 0 ? 0 : v); if (y1 > gy) y1 = gy;
+        const uint32_t dbits = o_f2u(depths[i]);
+        const float* co = conic_opacity + 4 * (size_t)i;
+        for (unsigned y = y0; y < y1; y++)
+            for (unsigned x = x0; x < x1; x++)
+                if (o_full_tile_keep(p, co, x, y)) {
+                    keys[o] = ((uint64_t)(y * gx + x) << 32) | dbits;
+                    values[o] = (uint32_t)i;
+                    o++;
+                }
+        for (; o < end; o++) {
+            keys[o] = ((uint64_t)0xffffffffu << 32) | flt_max_bits;
+            values[o] = 0xffffffffu;
+        }
+    }
+    free(off);
+    if (R > 1) {
+        uint64_t* tk = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)R);
+        uint32_t* tv = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)R);
+        uint64_t* a = keys; uint32_t* av = values;
+        uint64_t* b = tk; uint32_t* bv = tv;
+        for (int64_t width = 1; width < R; width *= 2) {
+#pragma omp parallel for schedule(dynamic, 1)
+            for (int64_t lo = 0; lo < R; lo += 2 * width) {
+                int64_t mid = lo + width < R ? lo + width : R;
+                int64_t hi = lo + 2 * width < R ? lo + 2 * width : R;
+                int64_t i = lo, j = mid, o = lo;
+                while (i < mid && j < hi) {
+                    if (a[j] < a[i]) { b[o] = a[j]; bv[o] = av[j]; j++; }
+                    else { b[o] = a[i]; bv[o] = av[i]; i++; }
+                    o++;
+                }
+                while (i < mid) { b[o] = a[i]; bv[o] = av[i]; i++; o++; }
+                while (j < hi) { b[o] = a[j]; bv[o] = av[j]; j++; o++; }
+            }
+            uint64_t* sw = a; a = b; b = sw;
+            uint32_t* sv = av; av = bv; bv = sv;
+        }
+        if (a != keys) {
+            memcpy(keys, a, sizeof(uint64_t) * (size_t)R);
+            memcpy(values, av, sizeof(uint32_t) * (size_t)R);
+        }
+        free(tk); free(tv);
+    }
+    /* identifyTileRanges with the invalid tile skipped (rasterizer_impl.cu:194-219) */
+    memset(ranges, 0, sizeof(uint32_t) * 2 * (size_t)T);
+    int64_t valid = 0;
+    for (int64_t idx = 0; idx < R; idx++) {
+        const uint32_t cur = (uint32_t)(keys[idx] >> 32);
+        const int ok = cur != 0xffffffffu;
+        if (ok) valid++;
+        if (idx == 0) { if (ok) ranges[2 * cur] = 0; }
+        else {
+            const uint32_t prev = (uint32_t)(keys[idx - 1] >> 32);
+            if (cur != prev) {
+                if (prev != 0xffffffffu) ranges[2 * prev + 1] = (uint32_t)idx;
+                if (ok) ranges[2 * cur] = (uint32_t)idx;
+            }
+        }
+        if (idx == R - 1 && ok) ranges[2 * cur + 1] = (uint32_t)R;
+    }
+    int64_t nb = 0;
+    for (unsigned t = 0; t < T; t++) nb += (ranges[2 * t + 1] - ranges[2 * t] + 31) / 32;
+    *num_buckets = nb;
+    return valid;
+}
+
+/* renderCUDA / render_simpCUDA of the full-image path (forward.cu:291-465,
+ * 466-607): the blend of the split path plus, per pixel, the Gaussian of the
+ * largest blend weight alpha * T (first one on ties), which gets one count in
+ * accum_max_count (when flag_max_count; render_simp always), and for
+ * render_simp every contribution's alpha * T added to accum_weights and 1 to
+ * accum_weights_count.  max_contrib[t] = the tile's largest last contributor.
+ * The accumulations run in tile, row, column, list order. */
+void o_render_fwd_full(int P, int W, int H, const float* bg, const float* means2D, const float* conic_opacity,
+                       const float* colors, const uint32_t* ranges, const uint32_t* point_list, int flag_max_count,
+                       float* out_color, float* final_T, uint32_t* n_contrib, uint32_t* max_contrib,
+                       float* accum_max_count, float* accum_weights, int32_t* accum_weights_count)
+{
+    (void)P;
+    const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const int T = gx * gy;
+    const float alpha_min = 1.0f / 255.0f;
+    for (int t = 0; t < T; t++) {
+        const int tx = t % gx, ty = t / gx;
+        const int x0 = tx * OT, y0 = ty * OT;
+        const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
+        const uint32_t rs = ranges[2 * t], re = ranges[2 * t + 1];
+        uint32_t mc = 0;
+        for (int y = y0; y < y1; y++)
+            for (int x = x0; x < x1; x++) {
+                const float px = (float)x, py = (float)y;
+                float T_ = 1.0f, C[3] = { 0.f, 0.f, 0.f };
+                uint32_t contributor = 0, last = 0;
+                float wmax = 0.0f;
+                uint32_t imax = 0;
+                int upd = 0;
+                for (uint32_t k = rs; k < re; k++) {
+                    contributor++;
+                    const uint32_t id = point_list[k];
+                    const float* co = conic_opacity + 4 * (size_t)id;
+                    const float power = o_power(means2D + 2 * (size_t)id, co, px, py);
+                    if (power > 0.0f) continue;
+                    const float alpha = o_fminf(0.99f, co[3] * o_expf(power));
+                    if (alpha < alpha_min) continue;
+                    const float test_T = T_ * (1.0f - alpha);
+                    if (test_T < 0.0001f) break;
+                    const float wgt = alpha * T_;
+                    for (int c = 0; c < 3; c++) C[c] = fmaf(colors[3 * (size_t)id + c], wgt, C[c]);
+                    if (wmax < wgt) { wmax = wgt; imax = id; upd = 1; }
+                    if (accum_weights) {
+                        accum_weights[id] += wgt;
+                        accum_weights_count[id] += 1;
+                    }
+                    T_ = test_T;
+                    last = contributor;
+                }
+                if (upd && (flag_max_count || accum_weights)) accum_max_count[imax] += 1.0f;
+                const size_t pid = (size_t)y * W + x;
+                final_T[pid] = T_;
+                n_contrib[pid] = last;
+                for (int c = 0; c < 3; c++) out_color[(size_t)c * H * W + pid] = fmaf(T_, bg[c], C[c]);
+                if (last > mc) mc = last;
+            }
+        if (max_contrib) max_contrib[t] = mc;
     }
 }
 

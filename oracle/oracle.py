@@ -273,3 +273,147 @@ def full_forward(cam, scene, bg=None, compute_locally=None, scale_modifier=1.0, 
     rf = render_fwd(W, H, bg, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"],
                     bn["point_list"], compute_locally)
     return pre, bn, rf
+
+
+# ---------------------------------------------------------------- full-image path
+
+def _opt_f32(a):
+    return None if a is None else _f32(a)
+
+
+def preprocess_fwd_full(cam, means3D, scales, rotations, dc, rest, opacities, colors_precomp=None,
+                        cov3D_precomp=None, culling=None, scale_modifier=1.0, sh_degree=3):
+    """preprocessCUDA with the full path's arguments (_f forward.cu:165-284)."""
+    means3D, scales, rotations, opacities = map(_f32, (means3D, scales, rotations, opacities))
+    P = means3D.shape[0]
+    dc = _f32(dc).reshape(P, 3) if dc is not None else np.zeros((P, 3), np.float32)
+    rest = _f32(rest).reshape(P, -1, 3) if rest is not None else np.zeros((P, 0, 3), np.float32)
+    M = rest.shape[1]
+    cp, c3 = _opt_f32(colors_precomp), _opt_f32(cov3D_precomp)
+    cull = np.zeros(P, np.uint8) if culling is None else np.ascontiguousarray(culling, dtype=np.uint8)
+    cs = camera_struct(cam, scale_modifier, sh_degree)
+    out = dict(
+        means2D=np.empty((P, 2), np.float32), depths=np.empty(P, np.float32),
+        radii=np.empty(P, np.int32), cov3D=np.empty((P, 6), np.float32),
+        conic_opacity=np.empty((P, 4), np.float32), rgb=np.empty((P, 3), np.float32),
+        clamped=np.empty((P, 3), np.uint8), rects=np.empty((P, 2), np.float32),
+        tiles_touched=np.empty(P, np.uint32))
+    lib().o_preprocess_fwd_full(C.c_int(P), C.c_int(M), C.byref(cs), _p(means3D), _p(scales), _p(rotations),
+                                _p(dc), _p(rest), _p(opacities), None if cp is None else _p(cp),
+                                None if c3 is None else _p(c3), _p(cull), _p(out["means2D"]), _p(out["depths"]),
+                                _p(out["radii"]), _p(out["cov3D"]), _p(out["conic_opacity"]), _p(out["rgb"]),
+                                _p(out["clamped"]), _p(out["rects"]), _p(out["tiles_touched"]))
+    return out
+
+
+def preprocess_bwd_full(cam, means3D, scales, rotations, dc, rest, radii, cov3D, clamped, dL_dmeans2D,
+                        dL_dconic, dL_dcolors, colors_precomp=None, cov3D_precomp=None, scale_modifier=1.0,
+                        sh_degree=3):
+    """BACKWARD::preprocess with the full path's arguments (_f backward.cu:759-827).
+    dL_dconic: (P,4) float4 slots (.x=c00, .y=c01, .w=c11)."""
+    means3D, scales, rotations, cov3D = map(_f32, (means3D, scales, rotations, cov3D))
+    P = means3D.shape[0]
+    dc = _f32(dc).reshape(P, 3) if dc is not None else np.zeros((P, 3), np.float32)
+    rest = _f32(rest).reshape(P, -1, 3) if rest is not None else np.zeros((P, 0, 3), np.float32)
+    M = rest.shape[1]
+    dL_dmeans2D = _f32(dL_dmeans2D).reshape(P, 3)
+    dL_dconic, dL_dcolors = _f32(dL_dconic).reshape(P, 4), _f32(dL_dcolors).reshape(P, 3)
+    radii = np.ascontiguousarray(radii, dtype=np.int32)
+    clamped = np.ascontiguousarray(clamped, dtype=np.uint8)
+    cp, c3 = _opt_f32(colors_precomp), _opt_f32(cov3D_precomp)
+    cs = camera_struct(cam, scale_modifier, sh_degree)
+    out = dict(dL_dmeans3D=np.empty((P, 3), np.float32), dL_dcov3D=np.empty((P, 6), np.float32),
+               dL_ddc=np.empty((P, 1, 3), np.float32), dL_dsh=np.empty((P, M, 3), np.float32),
+               dL_dscales=np.empty((P, 3), np.float32), dL_drotations=np.empty((P, 4), np.float32))
+    lib().o_preprocess_bwd_full(C.c_int(P), C.c_int(M), C.byref(cs), _p(means3D), _p(scales), _p(rotations),
+                                _p(dc), _p(rest) if M > 0 else None, None if cp is None else _p(cp),
+                                None if c3 is None else _p(c3), _p(radii), _p(cov3D), _p(clamped),
+                                _p(dL_dmeans2D), _p(dL_dconic), _p(dL_dcolors), _p(out["dL_dmeans3D"]),
+                                _p(out["dL_dcov3D"]), _p(out["dL_ddc"]), _p(out["dL_dsh"]),
+                                _p(out["dL_dscales"]), _p(out["dL_drotations"]))
+    return out
+
+
+def full_tile_keep(xy, co, tx, ty):
+    xy, co = _f32(xy), _f32(co)
+    return bool(lib().o_full_tile_keep(_p(xy), _p(co), C.c_uint(tx), C.c_uint(ty)))
+
+
+def binning_full(W, H, means2D, depths, radii, rects, conic_opacity, tiles_touched):
+    """Binning of the full path (rasterizer_impl.cu:119-210,440-480): R = sum of
+    tiles_touched entries, culled slots padded and sorted last."""
+    means2D, depths, rects, conic_opacity = map(_f32, (means2D, depths, rects, conic_opacity))
+    radii = np.ascontiguousarray(radii, dtype=np.int32)
+    tt = np.ascontiguousarray(tiles_touched, dtype=np.uint32)
+    gx, gy = tile_grid(W, H)
+    P = means2D.shape[0]
+    R = int(tt.astype(np.int64).sum())
+    keys = np.empty(R, np.uint64)
+    vals = np.empty(R, np.uint32)
+    ranges = np.empty((gx * gy, 2), np.uint32)
+    nb = C.c_int64(0)
+    lib().o_binning_full.restype = C.c_int64
+    valid = lib().o_binning_full(C.c_int(P), C.c_int(W), C.c_int(H), _p(means2D), _p(depths), _p(radii),
+                                 _p(rects), _p(conic_opacity), _p(tt), C.c_int64(R), _p(keys), _p(vals),
+                                 _p(ranges), C.byref(nb))
+    return dict(R=R, valid=int(valid), keys=keys, point_list=vals, ranges=ranges, num_buckets=int(nb.value))
+
+
+def render_fwd_full(W, H, bg, means2D, conic_opacity, colors, ranges, point_list, flag_max_count=True,
+                    simp=False):
+    """renderCUDA / render_simpCUDA of the full path (forward.cu:291-607)."""
+    means2D, conic_opacity, colors, bg = map(_f32, (means2D, conic_opacity, colors, bg))
+    gx, gy = tile_grid(W, H)
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    P = means2D.shape[0]
+    out = dict(color=np.empty((3, H, W), np.float32), final_T=np.empty((H, W), np.float32),
+               n_contrib_px=np.empty((H, W), np.uint32), max_contrib=np.empty(gx * gy, np.uint32),
+               accum_max_count=np.zeros(P, np.float32))
+    if simp:
+        out["accum_weights"] = np.zeros(P, np.float32)
+        out["accum_weights_count"] = np.zeros(P, np.int32)
+    lib().o_render_fwd_full(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity),
+                            _p(colors), _p(ranges), _p(point_list), C.c_int(int(bool(flag_max_count))),
+                            _p(out["color"]), _p(out["final_T"]), _p(out["n_contrib_px"]), _p(out["max_contrib"]),
+                            _p(out["accum_max_count"]), _p(out["accum_weights"]) if simp else None,
+                            _p(out["accum_weights_count"]) if simp else None)
+    return out
+
+
+def render_bwd_full(W, H, bg, means2D, conic_opacity, colors, ranges, point_list, final_T, n_contrib_px,
+                    dL_dpixels):
+    """Render backward of the full path (per-pixel gradients with the clamp rule of
+    PerGaussianRenderCUDA, _f backward.cu:403-588)."""
+    means2D, conic_opacity, colors, bg, final_T, dL_dpixels = map(
+        _f32, (means2D, conic_opacity, colors, bg, final_T, dL_dpixels))
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    n_contrib_px = np.ascontiguousarray(n_contrib_px, dtype=np.uint32)
+    P = means2D.shape[0]
+    out = dict(dL_dmeans2D=np.zeros((P, 3), np.float32), dL_dconic=np.zeros((P, 4), np.float32),
+               dL_dopacity=np.zeros(P, np.float32), dL_dcolors=np.zeros((P, 3), np.float32))
+    lib().o_render_bwd_full(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity),
+                            _p(colors), _p(ranges), _p(point_list), _p(final_T), _p(n_contrib_px),
+                            _p(dL_dpixels), _p(out["dL_dmeans2D"]), _p(out["dL_dconic"]), _p(out["dL_dopacity"]),
+                            _p(out["dL_dcolors"]))
+    return out
+
+
+def full_path_forward(cam, scene, bg=None, culling=None, colors_precomp=None, cov3D_precomp=None,
+                      flag_max_count=True, simp=False, scale_modifier=1.0, sh_degree=3):
+    """GaussianRasterizer.forward / render_simp of the full path
+    (rasterizer_impl.cu:336-486): preprocess, binning, render."""
+    sh = _f32(scene["sh"])
+    pre = preprocess_fwd_full(cam, scene["means3D"], scene["scales"], scene["rotations"], sh[:, :1], sh[:, 1:],
+                              scene["opacities"], colors_precomp, cov3D_precomp, culling, scale_modifier,
+                              sh_degree)
+    W, H = int(cam["W"]), int(cam["H"])
+    bn = binning_full(W, H, pre["means2D"], pre["depths"], pre["radii"], pre["rects"], pre["conic_opacity"],
+                      pre["tiles_touched"])
+    if bg is None:
+        bg = np.zeros(3, np.float32)
+    colors = pre["rgb"] if colors_precomp is None else colors_precomp
+    rf = render_fwd_full(W, H, bg, pre["means2D"], pre["conic_opacity"], colors, bn["ranges"],
+                         bn["point_list"], flag_max_count, simp)
+    return pre, bn, rf

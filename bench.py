@@ -15,6 +15,8 @@ fused_ssim forward+backward on config 4's 8 x 3 x 1080 x 1920 image pair.
 `--workload adam`: the SparseGaussianAdam step over config 2's 6M Gaussians.
 `--workload route`: one rank's routing + pack/unpack around the screen-space
 all-to-all, config 3's 8M Gaussians split over four tile-row ranks.
+`--workload full`: the full-image path (GaussianRasterizer.forward + backward,
+and render_simp) on a config's scene.
 
 Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
 `roofline` describes the dominant kernel, timed live with HIP events on the
@@ -61,7 +63,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route"], default="step")
+    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route", "full"], default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
@@ -423,6 +425,101 @@ def run_adam(args):
     print(json.dumps(out), flush=True)
 
 
+def run_full(args):
+    """The full-image path (GaussianRasterizer.forward, the render_imp / eval
+    rasterizer of diff-gaussian-rasterization_f) forward + backward through
+    autograd on a scene config (default config 2): preprocess with SH, the
+    tile-culled binning, the blend with accum_max_count, then dL/dimage ~ N(0,1)
+    through the render and preprocess backward; plus one render_simp per step
+    reported separately (the pruning steps' importance pass)."""
+    import torch
+    from blitzgs_amd import synth
+    from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
+    dev = torch.device("cuda:0")
+    gen = {0: synth.config0, 1: synth.config1, 2: synth.config2, 3: synth.config3}[args.config]
+    scene, cam = gen()
+    P = scene["means3D"].shape[0]
+    W, H = cam["W"], cam["H"]
+    tt = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)
+    sh = np.asarray(scene["sh"], np.float32)
+    params = {"means3D": tt(scene["means3D"]), "scales": tt(scene["scales"]), "rotations": tt(scene["rotations"]),
+              "opacities": tt(scene["opacities"]), "dc": tt(sh[:, :1]), "rest": tt(sh[:, 1:])}
+    for v in params.values():
+        v.requires_grad_(True)
+    means2D = torch.zeros((P, 3), device=dev, requires_grad=True)
+    culling = torch.zeros(P, dtype=torch.bool, device=dev)
+    dL = tt(scene.get("dL_dimage", np.random.default_rng(0).standard_normal((3, H, W)).astype(np.float32)))
+    rs = GaussianRasterizationSettings(
+        image_height=H, image_width=W, tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"],
+        bg=torch.zeros(3, device=dev), scale_modifier=1.0, viewmatrix=tt(cam["viewmatrix"]),
+        projmatrix=tt(cam["projmatrix"]), sh_degree=3, campos=tt(cam["campos"]), prefiltered=False, debug=False)
+    ras = GaussianRasterizer(rs)
+    info = {}
+
+    def step():
+        for v in list(params.values()) + [means2D]:
+            v.grad = None
+        color, radii, amc = ras(means3D=params["means3D"], means2D=means2D, opacities=params["opacities"],
+                                culling=culling, dc=params["dc"], shs=params["rest"], scales=params["scales"],
+                                rotations=params["rotations"], flag_max_count=True)
+        torch.autograd.backward([color], [dL])
+        info["radii"] = radii
+
+    ms, kt, _ = timed(step, args.steps, args.warmup)
+
+    def simp():
+        with torch.no_grad():
+            ras.render_simp(means3D=params["means3D"], means2D=means2D, opacities=params["opacities"],
+                            culling=culling, dc=params["dc"], shs=params["rest"], scales=params["scales"],
+                            rotations=params["rotations"])
+
+    ms_simp, kt_simp, _ = timed(simp, args.steps, args.warmup)
+    P_vis = int((info["radii"] > 0).sum().item())
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
+    # instances after the tile test, from one direct forward (outside the timed regions)
+    from blitzgs_amd import fullpath
+    x = fullpath._inputs(rs, params["means3D"].detach(), params["dc"].detach(), params["rest"].detach(), None,
+                         params["opacities"].detach(), params["scales"].detach(), params["rotations"].detach(), None)
+    R = fullpath._forward(rs, x, culling, True, False)[-1]
+    sb = stage_bytes(P, P_vis, R, W * H)
+    sb["preprocess_fwd_full_kernel"] = sb["preprocess_fwd_kernel"]
+    sb["preprocess_bwd_full_kernel"] = sb["preprocess_bwd_kernel"]
+    dom = max((k for k in sb if k in per_kernel), key=lambda k: per_kernel[k])
+    roofline = roofline_of(dom, sb[dom], avg_launch[dom])
+    roofline["note"] = ("the blend kernels are VALU-bound (per-pixel exp and gradient arithmetic plus a 64-lane "
+                        "reduction per Gaussian); their HBM fraction is low by nature")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        n = max(1, int(round(P * args.cpu_sample)))
+        sub = {k: scene[k][:n] for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+        t1 = time.perf_counter()
+        pre, bn, rf = O.full_path_forward(cam, sub)
+        rb = O.render_bwd_full(W, H, np.zeros(3, np.float32), pre["means2D"], pre["conic_opacity"], pre["rgb"],
+                               bn["ranges"], bn["point_list"], rf["final_T"], rf["n_contrib_px"], np.asarray(
+                                   scene.get("dL_dimage", np.zeros((3, H, W), np.float32)), np.float32))
+        shn = np.asarray(sub["sh"], np.float32)
+        O.preprocess_bwd_full(cam, sub["means3D"], sub["scales"], sub["rotations"], shn[:, :1], shn[:, 1:],
+                              pre["radii"], pre["cov3D"], pre["clamped"], rb["dL_dmeans2D"], rb["dL_dconic"],
+                              rb["dL_dcolors"])
+        dt = time.perf_counter() - t1
+        cpu = {"value": round(n / dt, 1), "unit": "Gaussians/s", "cores": O.num_threads(), "kind": "port",
+               "sample": f"one full-path fwd+bwd of the CPU oracle on the first {n} of {P} Gaussians; "
+                         f"{dt * 1e3:.0f} ms"}
+    out = header(args, f"full-image path (GaussianRasterizer.forward) fwd+bwd Gaussians/s, config {args.config}",
+                 P / (ms * 1e-3), "Gaussians/s", ms, "f32",
+                 f"config{args.config} full-image path: {P} Gaussians SH3, {W}x{H}, fwd+bwd",
+                 {"gaussians": P, "visible": P_vis, "image": [W, H]})
+    out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
+    out["render_simp_ms"] = round(ms_simp, 4)
+    out["render_simp_stages_ms"] = {k: round(v[0] / max(1, args.steps), 4) for k, v in kt_simp.items()}
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    out["config"]["instances"] = R
+    print(json.dumps(out), flush=True)
+
+
 def run_route(args):
     """One rank's side of the screen-space exchange at config 3's shape: config
     3's 8M Gaussians (4096x2730) preprocessed once, then per step routed to
@@ -528,7 +625,8 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     _lib.load()
-    {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam, "route": run_route}[args.workload](args)
+    {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam, "route": run_route,
+     "full": run_full}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -52,6 +52,14 @@ _SIGS = {
     "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_adam_update": (_i, [_c, _c, _c, _c, _c, _f, _f, _f, _f, _i64, _i64, _c]),
     "gs_adam_update_groups": (_i, [_i, C.POINTER(AdamGroup), _i64, _c, _f, _f, _c]),
+    "gs_preprocess_forward_full": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i,
+                                        _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_full_count": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, C.POINTER(_i64), _c]),
+    "gs_render_full_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_full_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_preprocess_backward_full": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i, _c,
+                                         _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_mark_visible": (_i, [_i, _c, _c, _c, _c, _c]),
     "gs_local2j_ids_bool": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c]),
     "gs_local2j_workspace_bytes": (_sz, [_i, _i]),
     "gs_local2j_count": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c, _c, _c]),

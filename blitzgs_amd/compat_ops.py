@@ -6,13 +6,17 @@ diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
   preprocess_gaussians_backward   _f/rasterize_points.cu:926-1029
   render_gaussians                _r/rasterize_points.cu:273-361
   render_gaussians_backward       _r/rasterize_points.cu:363-436
+  rasterize_gaussians             _f/rasterize_points.cu:370-475
+  rasterize_gaussians_simp        _f/rasterize_points.cu:477-583
+  rasterize_gaussians_backward    _f/rasterize_points.cu:697-783
+  mark_visible                    _f/rasterize_points.cu:785-805
   get_local2j_ids_bool            _f/rasterize_points.cu:258-289
   get_local2j_ids_bool_adjust_mode6  _f/rasterize_points.cu:337-367
   adamUpdate                      _f/rasterize_points.cu:807-832
 Same positional arguments and return tuples; `args` is the reference's
 cuda_args dict (its "stats_collector" entry receives forward_render_time /
-backward_render_time in ms).  mark_visible and the image-tile utilities of the
-multi-GPU path are not implemented.
+backward_render_time in ms).  rasterize_gaussians_depth (no caller in BlitzGS)
+and the image-tile utilities of the multi-GPU path are not implemented.
 """
 import torch
 
@@ -78,9 +82,14 @@ def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, al
 
 def _not_here(name):
     def f(*a, **k):
-        raise NotImplementedError(f"{name}: multi-GPU routing / image-tile utilities are not part of this build")
+        raise NotImplementedError(f"{name} is not part of this build")
     f.__name__ = name
     return f
 
 
-mark_visible = _not_here("mark_visible")
+from .fullpath import C_rasterize_gaussians as rasterize_gaussians  # noqa: E402,F401
+from .fullpath import C_rasterize_gaussians_backward as rasterize_gaussians_backward  # noqa: E402,F401
+from .fullpath import C_rasterize_gaussians_simp as rasterize_gaussians_simp  # noqa: E402,F401
+from .fullpath import mark_visible  # noqa: E402,F401
+
+rasterize_gaussians_depth = _not_here("rasterize_gaussians_depth")

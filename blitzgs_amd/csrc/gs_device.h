@@ -183,6 +183,56 @@ __device__ __forceinline__ bool may_touch_prepared(float thresh, float nbc, floa
     return -0.5 * best + margin >= (double)thresh;
 }
 
+// Tile test of the full-image path's duplicateWithKeys (reference
+// diff-gaussian-rasterization_f/cuda_rasterizer/rasterizer_impl.cu:56-95,
+// 144-167, max_contrib_power_rect_gaussian_float<15,15>): the falloff exponent
+// 0.5 (a dx^2 + c dy^2) + b dx dy at the point of the tile's pixel rect
+// [16 tx, 16 tx + 15] x [16 ty, 16 ty + 15] the reference picks (the mean if
+// inside; else along the nearest edge), kept when <= thr = log(opacity * 255).
+// Left-to-right fp32, no contraction; 1/(225 a) a correctly rounded division;
+// saturate maps NaN to 0.
+__device__ __forceinline__ float sat01(float v) { return v > 0.0f ? (v < 1.0f ? v : 1.0f) : 0.0f; }
+
+__device__ __forceinline__ bool full_tile_keep(float mx, float my, float a, float b, float c, float thr, unsigned tx,
+                                               unsigned ty)
+{
+    const float rminx = (float)(tx * 16u), rminy = (float)(ty * 16u);
+    const float rmaxx = (float)((tx + 1u) * 16u - 1u), rmaxy = (float)((ty + 1u) * 16u - 1u);
+    const float x_min_diff = rminx - mx;
+    const float x_left = x_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_x = x_left + (mx > rmaxx ? 1.0f : 0.0f);
+    const float y_min_diff = rminy - my;
+    const float y_above = y_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_y = y_above + (my > rmaxy ? 1.0f : 0.0f);
+    float power = 0.0f;
+    if ((not_in_y + not_in_x) > 0.0f) {
+        const float px = x_left * rminx + (1.0f - x_left) * rmaxx;
+        const float py = y_above * rminy + (1.0f - y_above) * rmaxy;
+        const float dx = __builtin_copysignf(15.0f, x_min_diff);
+        const float dy = __builtin_copysignf(15.0f, y_min_diff);
+        const float diffx = mx - px, diffy = my - py;
+        const float rcp_x = 1.0f / (225.0f * a);
+        const float rcp_y = 1.0f / (225.0f * c);
+        const float tx_ = not_in_y * sat01((dx * a * diffx + dx * b * diffy) * rcp_x);
+        const float ty_ = not_in_x * sat01((dy * b * diffx + dy * c * diffy) * rcp_y);
+        const float qx = px + tx_ * dx, qy = py + ty_ * dy;
+        const float ex = mx - qx, ey = my - qy;
+        power = 0.5f * (a * ex * ex + c * ey * ey) + b * ex * ey;
+    }
+    return power <= thr;
+}
+
+// Float-extent tile rect of the full-image path (getRect(float2, float2),
+// reference auxiliary.h:63-73): floor / ceil of (mean -+ extent) / 16, clamped.
+__device__ __forceinline__ void rect_float(float px, float py, float ex, float ey, unsigned gx, unsigned gy,
+                                           unsigned& x0, unsigned& y0, unsigned& x1, unsigned& y1)
+{
+    x0 = clamp_tile(f2i_sat(__builtin_floorf((px - ex) / 16.0f)), gx);
+    y0 = clamp_tile(f2i_sat(__builtin_floorf((py - ey) / 16.0f)), gy);
+    x1 = clamp_tile(f2i_sat(__builtin_ceilf((px + ex) / 16.0f)), gx);
+    y1 = clamp_tile(f2i_sat(__builtin_ceilf((py + ey) / 16.0f)), gy);
+}
+
 // ---- wave64 helpers -------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

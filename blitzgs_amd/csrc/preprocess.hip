@@ -12,6 +12,14 @@
 //   (P,2,2) repack, no (P,3) padding, no dc/rest split and no dL/dcov3D
 //   round trip through memory) and writes dL/dsh as (P,K,3) in place.
 //
+// The full-image path (GaussianRasterizer.forward / render_simp; reference
+// forward.cu:165-284 and backward.cu:759-827 with the arguments
+// rasterizer_impl.cu:396-424 and 931-954 pass) runs the same kernels with
+// FULL = true: a culling mask, precomputed colours or 3D covariances, the SH
+// DC term and the remaining coefficients in separate arrays, the float tile
+// rect extents and tile counts as extra outputs, and dL/dcov3D, dL/ddc,
+// dL/drest as separate gradients.
+//
 // One thread per Gaussian.  Every output element is written (zeros for culled
 // Gaussians), so callers need not clear the outputs.  The forward arithmetic
 // is the fixed-order fp32 sequence that oracle/o_preprocess.c restates on the
@@ -161,14 +169,35 @@ __device__ __forceinline__ void sh_color(float x, float y, float z, const float*
     }
 }
 
-template <int DEG>
+// Extra inputs and outputs of the full-image path's preprocess.
+struct FullPre {
+    const uint8_t* culling;          // P, nonzero = skip
+    const float* colors_precomp;     // P x 3 or null (null: SH colour)
+    const float* cov3D_precomp;      // P x 6 or null (null: from scale and rotation)
+    const float* dc;                 // P x 3
+    const float* rest;               // P x M x 3
+    int M;
+    float* rects;                    // P x 2 float tile-rect extents
+    uint32_t* tiles_touched;         // P
+};
+
+// SH coefficients of one Gaussian from the DC array and the rest array.
+template <int NC>
+__device__ __forceinline__ void load_sh_split(const float* __restrict__ dc, const float* __restrict__ rest, float* s)
+{
+    s[0] = dc[0]; s[1] = dc[1]; s[2] = dc[2];
+#pragma unroll
+    for (int i = 0; i < 3 * (NC - 1); i++) s[3 + i] = rest[i];
+}
+
+template <int DEG, bool FULL>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
     const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
     const float* __restrict__ sh, int sh_vec16, const float* __restrict__ opacities,
     float* __restrict__ means2D, float* __restrict__ depths, int* __restrict__ radii, float* __restrict__ cov3D,
-    float* __restrict__ conic_opacity, float* __restrict__ rgb, uint8_t* __restrict__ clamped)
+    float* __restrict__ conic_opacity, float* __restrict__ rgb, uint8_t* __restrict__ clamped, FullPre F)
 {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= P) return;
@@ -181,8 +210,11 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     float c6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int o_radius = 0;
     bool o_clamp[3] = {false, false, false};
+    float o_ex = 0.f, o_ey = 0.f;
+    uint32_t o_tiles = 0;
 
     do {
+        if (FULL && F.culling[idx]) break;
         float pv[3];
         xform3(cam.v, mx, my, mz, pv);
         if (pv[2] <= 0.2f) break;
@@ -191,7 +223,10 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
         const float pw = 1.0f / (xform_w(cam.p, mx, my, mz) + 0.0000001f);
         const float pp0 = ph[0] * pw, pp1 = ph[1] * pw;
 
-        {
+        if (FULL && F.cov3D_precomp != nullptr) {
+#pragma unroll
+            for (int k = 0; k < 6; k++) c6[k] = F.cov3D_precomp[6 * (size_t)idx + k];
+        } else {
             const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
             float Rm[3][3];
             quat_rows(q.x, q.y, q.z, q.w, Rm);
@@ -240,13 +275,17 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
         const unsigned rminy = gs::clamp_tile(gs::f2i_sat(__builtin_floorf((pix1 - ey) / 16.0f)), gy);
         const unsigned rmaxx = gs::clamp_tile(gs::f2i_sat(__builtin_ceilf((pix0 + ex) / 16.0f)), gx);
         const unsigned rmaxy = gs::clamp_tile(gs::f2i_sat(__builtin_ceilf((pix1 + ey) / 16.0f)), gy);
-        if ((rmaxx - rminx) * (rmaxy - rminy) == 0) break;
+        const uint32_t tiles = (rmaxx - rminx) * (rmaxy - rminy);
+        if (tiles == 0) break;
 
         // SH -> RGB (only Gaussians that survive every cull read their SH block)
-        {
+        if (!FULL || F.colors_precomp == nullptr) {
             constexpr int NC = (DEG + 1) * (DEG + 1);
             float s[3 * NC];
-            load_sh<NC>(sh + (size_t)idx * K * 3, sh_vec16 != 0, s);
+            if (FULL)
+                load_sh_split<NC>(F.dc + 3 * (size_t)idx, F.rest + (size_t)idx * F.M * 3, s);
+            else
+                load_sh<NC>(sh + (size_t)idx * K * 3, sh_vec16 != 0, s);
             float dir0 = mx - cam.c[0], dir1 = my - cam.c[1], dir2 = mz - cam.c[2];
             const float len = __builtin_sqrtf(dir0 * dir0 + dir1 * dir1 + dir2 * dir2);
             dir0 = dir0 / len; dir1 = dir1 / len; dir2 = dir2 / len;
@@ -260,7 +299,15 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
         o_con[1] = -cb * det_inv;
         o_con[2] = ca * det_inv;
         o_con[3] = opacity;
+        o_ex = ex;
+        o_ey = ey;
+        o_tiles = tiles;
     } while (0);
+
+    if (FULL) {
+        reinterpret_cast<float2*>(F.rects)[idx] = make_float2(o_ex, o_ey);
+        F.tiles_touched[idx] = o_tiles;
+    }
 
     reinterpret_cast<float2*>(means2D)[idx] = make_float2(o_m2d[0], o_m2d[1]);
     depths[idx] = o_depth;
@@ -346,7 +393,19 @@ __device__ __forceinline__ void sh_backward(float x, float y, float z, const flo
     }
 }
 
-template <int DEG, bool STAGED>
+// Extra inputs and outputs of the full-image path's preprocess backward.
+struct FullPreBwd {
+    const float* cov3D_precomp;      // null: covariance from scale and rotation (and their gradients)
+    int colors_precomp;              // nonzero: colours were given, no SH gradients
+    const float* dc;                 // P x 3
+    const float* rest;               // P x M x 3, null when M == 0 (then no SH gradients, as the reference)
+    int M;
+    float* dL_ddc;                   // P x 3
+    float* dL_drest;                 // P x M x 3
+    float* dL_dcov3D;                // P x 6
+};
+
+template <int DEG, bool STAGED, bool FULL>
 __device__ __forceinline__ void preprocess_bwd_one(
     int idx, int K, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
@@ -355,12 +414,12 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
-    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row)
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row, const FullPreBwd& F)
 {
     constexpr int NC = (DEG + 1) * (DEG + 1);
     const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
     dL_dopacity[idx] = gco.w;
-    float* gsh_out = dL_dsh + (size_t)idx * K * 3;
+    float* gsh_out = FULL ? nullptr : dL_dsh + (size_t)idx * K * 3;
     const bool vec16 = sh_vec16 != 0;
     Cam cam;
     load_cam(cam, view, proj, campos);
@@ -368,7 +427,10 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const float* V = cam.v;
     const float* PM = cam.p;
     float c6[6];
-    {
+    if (FULL && F.cov3D_precomp != nullptr) {
+#pragma unroll
+        for (int k = 0; k < 6; k++) c6[k] = F.cov3D_precomp[6 * (size_t)idx + k];
+    } else {
         const float2* c2 = reinterpret_cast<const float2*>(cov3D + 6 * (size_t)idx);
         const float2 a = c2[0], b = c2[1], c = c2[2];
         c6[0] = a.x; c6[1] = a.y; c6[2] = b.x; c6[3] = b.y; c6[4] = c.x; c6[5] = c.y;
@@ -403,6 +465,12 @@ __device__ __forceinline__ void preprocess_bwd_one(
         dcov[2] = 2 * u[0] * u[2] * dL_da + (u[0] * w[2] + u[2] * w[0]) * dL_db + 2 * w[0] * w[2] * dL_dc;
         dcov[4] = 2 * u[2] * u[1] * dL_da + (u[1] * w[2] + u[2] * w[1]) * dL_db + 2 * w[1] * w[2] * dL_dc;
     }
+    if (FULL) {
+        float2* o2 = reinterpret_cast<float2*>(F.dL_dcov3D + 6 * (size_t)idx);
+        o2[0] = make_float2(dcov[0], dcov[1]);
+        o2[1] = make_float2(dcov[2], dcov[3]);
+        o2[2] = make_float2(dcov[4], dcov[5]);
+    }
     float du[3], dw[3];
 #pragma unroll
     for (int k = 0; k < 3; k++) {
@@ -436,10 +504,13 @@ __device__ __forceinline__ void preprocess_bwd_one(
         gm[2] += (PM[8] * m_w - PM[11] * mul1) * gx + (PM[9] * m_w - PM[11] * mul2) * gy;
     }
 
-    // ---- SH backward
-    {
+    // ---- SH backward (the full path: only with SH colours and a rest array)
+    if (!FULL || (!F.colors_precomp && F.rest != nullptr)) {
         float s[3 * NC];
-        load_sh<NC>(sh + (size_t)idx * K * 3, vec16, s);
+        if (FULL)
+            load_sh_split<NC>(F.dc + 3 * (size_t)idx, F.rest + (size_t)idx * F.M * 3, s);
+        else
+            load_sh<NC>(sh + (size_t)idx * K * 3, vec16, s);
         const float dir_orig[3] = {mx - cam.c[0], my - cam.c[1], mz - cam.c[2]};
         const float len = __builtin_sqrtf(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]);
         const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
@@ -455,7 +526,15 @@ __device__ __forceinline__ void preprocess_bwd_one(
         dnormvdv3(dir_orig, dL_ddir, dm);
         gm[0] += dm[0]; gm[1] += dm[1]; gm[2] += dm[2];
         // dL/dsh: the first NC coefficients, zeros after
-        if (STAGED) {
+        if (FULL && !STAGED) {
+            F.dL_ddc[3 * (size_t)idx + 0] = gsh[0];
+            F.dL_ddc[3 * (size_t)idx + 1] = gsh[1];
+            F.dL_ddc[3 * (size_t)idx + 2] = gsh[2];
+            float* o = F.dL_drest + (size_t)idx * F.M * 3;
+#pragma unroll
+            for (int i = 0; i < 3 * (NC - 1); i++) o[i] = gsh[3 + i];
+            for (int i = 3 * (NC - 1); i < 3 * F.M; i++) o[i] = 0.f;
+        } else if (STAGED) {
 #pragma unroll
             for (int i = 0; i < 48; i++) s_row[i] = i < 3 * NC ? gsh[i] : 0.f;
         } else if (vec16) {
@@ -479,7 +558,12 @@ __device__ __forceinline__ void preprocess_bwd_one(
     dL_dmeans3D[3 * idx + 2] = gm[2];
 
     // ---- 3D covariance -> scale and (un-normalised) quaternion
-    {
+    if (FULL && F.cov3D_precomp != nullptr) {
+        dL_dscales[3 * idx + 0] = 0.f;
+        dL_dscales[3 * idx + 1] = 0.f;
+        dL_dscales[3 * idx + 2] = 0.f;
+        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
         const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
         const float r = q.x, x = q.y, y = q.z, z = q.w;
         float Rm[3][3];
@@ -515,10 +599,12 @@ __device__ __forceinline__ void preprocess_bwd_one(
 }
 
 // Rows of dL/dsh are staged in LDS (pitch 49 floats: conflict-free column
-// writes) and copied out with fully coalesced 16-byte stores when K == 16.
+// writes) and copied out with fully coalesced stores: as (P,16,3) rows of 16
+// bytes in the split path (K == 16), as the (P,1,3) DC and (P,M,3) rest
+// arrays in the full path (M <= 15).
 constexpr int SH_PITCH = 49;
 
-template <int DEG, bool STAGED>
+template <int DEG, bool STAGED, bool FULL>
 __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
@@ -527,14 +613,17 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
-    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity)
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, FullPreBwd F)
 {
     __shared__ float s_sh[STAGED ? 256 * SH_PITCH : 1];
     __shared__ uint8_t s_vis[256];
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     const bool in = idx < P;
     const bool vis = in && radii[idx] > 0;
-    if (STAGED) s_vis[threadIdx.x] = vis ? 1 : 0;
+    // staged rows hold SH gradients (the full path has none with precomputed
+    // colours or without a rest array)
+    const bool sh_rows = !FULL || (!F.colors_precomp && F.rest != nullptr);
+    if (STAGED) s_vis[threadIdx.x] = (vis && sh_rows) ? 1 : 0;
     if (in && !vis) {
         dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
         dL_dmeans3D[3 * idx + 0] = 0.f;
@@ -544,7 +633,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         dL_dscales[3 * idx + 1] = 0.f;
         dL_dscales[3 * idx + 2] = 0.f;
         reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!STAGED) {
+        if (FULL) {
+            for (int k = 0; k < 6; k++) F.dL_dcov3D[6 * (size_t)idx + k] = 0.f;
+        } else if (!STAGED) {
             float* gsh_out = dL_dsh + (size_t)idx * K * 3;
             if (sh_vec16) {
                 float4* o4 = reinterpret_cast<float4*>(gsh_out);
@@ -554,11 +645,36 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
             }
         }
     }
-    if (vis) preprocess_bwd_one<DEG, STAGED>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, means3D,
-                                              scales, rotations, sh, sh_vec16, cov3D, clamped, dL_dmeans2D,
-                                              m2d_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,
-                                              dL_drotations, dL_dsh, dL_dopacity, s_sh + threadIdx.x * SH_PITCH);
-    if (STAGED) {
+    if (FULL && !STAGED && in) {
+        // SH gradients are zero unless written below (culled, precomputed colours, no rest array)
+        F.dL_ddc[3 * (size_t)idx + 0] = 0.f;
+        F.dL_ddc[3 * (size_t)idx + 1] = 0.f;
+        F.dL_ddc[3 * (size_t)idx + 2] = 0.f;
+        float* o = F.dL_drest + (size_t)idx * F.M * 3;
+        for (int i = 0; i < 3 * F.M; i++) o[i] = 0.f;
+    }
+    if (vis) preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
+                                                    means3D, scales, rotations, sh, sh_vec16, cov3D, clamped,
+                                                    dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb,
+                                                    dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity,
+                                                    s_sh + threadIdx.x * SH_PITCH, F);
+    if (STAGED && FULL) {
+        // coalesced copy-out of this block's rows [blockIdx*256, +nrows): 3 DC floats, then 3M rest floats
+        __syncthreads();
+        const int row0 = blockIdx.x * 256;
+        const int nrows = min(256, P - row0);
+        float* ddc = F.dL_ddc + (size_t)row0 * 3;
+        for (int c = threadIdx.x; c < nrows * 3; c += 256) {
+            const int r = c / 3;
+            ddc[c] = s_vis[r] ? s_sh[r * SH_PITCH + (c - 3 * r)] : 0.f;
+        }
+        const int rw = 3 * F.M;
+        float* drest = F.dL_drest + (size_t)row0 * rw;
+        for (int c = threadIdx.x; c < nrows * rw; c += 256) {
+            const int r = c / rw;
+            drest[c] = s_vis[r] ? s_sh[r * SH_PITCH + 3 + (c - rw * r)] : 0.f;
+        }
+    } else if (STAGED) {
         // coalesced copy-out of this block's rows [blockIdx*256, +nrows) x 48 floats
         __syncthreads();
         const int row0 = blockIdx.x * 256;
@@ -599,10 +715,10 @@ extern "C" int gs_preprocess_forward(
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
 #define GS_PRE_FWD(DEG)                                                                             \
-    GS_TIMED("preprocess_fwd_kernel", stream, hipLaunchKernelGGL(preprocess_fwd_kernel<DEG>, grid, block, 0, stream, P, K, image_width,        \
+    GS_TIMED("preprocess_fwd_kernel", stream, hipLaunchKernelGGL((preprocess_fwd_kernel<DEG, false>), grid, block, 0, stream, P, K, image_width,        \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
                        campos, means3D, scales, rotations, sh, sh_vec16, opacities, means2D, depths, radii, \
-                       cov3D, conic_opacity, rgb, clamped))
+                       cov3D, conic_opacity, rgb, clamped, FullPre{}))
     switch (D) {
         case 0: GS_PRE_FWD(0); break;
         case 1: GS_PRE_FWD(1); break;
@@ -638,16 +754,16 @@ extern "C" int gs_preprocess_backward(
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
 #define GS_PRE_BWD(DEG)                                                                                  \
-    if (staged) GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, true>), grid, block, 0, stream, P, K, image_width,             \
+    if (staged) GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, true, false>), grid, block, 0, stream, P, K, image_width,             \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
                        campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
                        dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
-                       dL_drotations, dL_dsh, dL_dopacity));                                               \
-    else GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false>), grid, block, 0, stream, P, K, image_width,             \
+                       dL_drotations, dL_dsh, dL_dopacity, FullPreBwd{}));                                 \
+    else GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false, false>), grid, block, 0, stream, P, K, image_width,             \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
                        campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
                        dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
-                       dL_drotations, dL_dsh, dL_dopacity))
+                       dL_drotations, dL_dsh, dL_dopacity, FullPreBwd{}))
     switch (D) {
         case 0: GS_PRE_BWD(0); break;
         case 1: GS_PRE_BWD(1); break;
@@ -656,5 +772,138 @@ extern "C" int gs_preprocess_backward(
     }
 #undef GS_PRE_BWD
     GS_LAUNCH_CHECK("preprocess_bwd_kernel");
+    return GS_OK;
+}
+
+extern "C" int gs_preprocess_forward_full(
+    int P, int D, int M, const float* means3D, const float* scales, const float* rotations, const float* dc,
+    const float* rest, const float* opacities, const float* colors_precomp, const float* cov3D_precomp,
+    const uint8_t* culling, float scale_modifier, const float* viewmatrix, const float* projmatrix,
+    const float* campos, float tanfovx, float tanfovy, int image_height, int image_width, float* means2D,
+    float* depths, int* radii, float* cov3D, float* conic_opacity, float* rgb, uint8_t* clamped, float* rects,
+    uint32_t* tiles_touched, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(D >= 0 && D <= 3, "sh_degree must be in [0, 3] (got %d)", D);
+    GS_REQUIRE(M >= 0, "M must be >= 0");
+    GS_REQUIRE(colors_precomp != nullptr || (dc != nullptr && (D == 0 || (rest != nullptr && M >= (D + 1) * (D + 1) - 1))),
+               "SH colours need dc and at least (D+1)^2 - 1 = %d further coefficients (got %d)",
+               (D + 1) * (D + 1) - 1, M);
+    GS_REQUIRE(cov3D_precomp != nullptr || (scales != nullptr && rotations != nullptr),
+               "either cov3D_precomp or scales and rotations are needed");
+    GS_REQUIRE(culling && means3D && opacities, "null input");
+    GS_REQUIRE(image_width > 0 && image_height > 0, "image size must be positive");
+    GS_REQUIRE(((uintptr_t)rotations & 15) == 0 && ((uintptr_t)conic_opacity & 15) == 0,
+               "rotations and conic_opacity must be 16-byte aligned");
+    GS_REQUIRE(((uintptr_t)rects & 7) == 0 && ((uintptr_t)cov3D & 7) == 0, "rects and cov3D must be 8-byte aligned");
+    const FullPre F{culling, colors_precomp, cov3D_precomp, dc, rest, M, rects, tiles_touched};
+    const float fy = (float)image_height / (2.0f * tanfovy);
+    const float fx = (float)image_width / (2.0f * tanfovx);
+    const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+#define GS_PRE_FWD_FULL(DEG)                                                                                   \
+    GS_TIMED("preprocess_fwd_full_kernel", stream,                                                             \
+             hipLaunchKernelGGL((preprocess_fwd_kernel<DEG, true>), grid, block, 0, stream, P, 0, image_width, \
+                                image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
+                                campos, means3D, scales, rotations, nullptr, 0, opacities, means2D, depths,     \
+                                radii, cov3D, conic_opacity, rgb, clamped, F))
+    switch (D) {
+        case 0: GS_PRE_FWD_FULL(0); break;
+        case 1: GS_PRE_FWD_FULL(1); break;
+        case 2: GS_PRE_FWD_FULL(2); break;
+        default: GS_PRE_FWD_FULL(3); break;
+    }
+#undef GS_PRE_FWD_FULL
+    GS_LAUNCH_CHECK("preprocess_fwd_full_kernel");
+    return GS_OK;
+}
+
+extern "C" int gs_preprocess_backward_full(
+    int P, int D, int M, const float* means3D, const float* scales, const float* rotations, const float* dc,
+    const float* rest, const float* colors_precomp, const float* cov3D_precomp, float scale_modifier,
+    const float* viewmatrix, const float* projmatrix, const float* campos, float tanfovx, float tanfovy,
+    int image_height, int image_width, const int* radii, const float* cov3D, const uint8_t* clamped,
+    const float* dL_dmeans2D, const float* dL_dconic_opacity, const float* dL_dcolors, float* dL_dmeans3D,
+    float* dL_dcov3D, float* dL_ddc, float* dL_drest, float* dL_dscales, float* dL_drotations,
+    float* dL_dopacity, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(D >= 0 && D <= 3, "sh_degree must be in [0, 3] (got %d)", D);
+    GS_REQUIRE(M >= 0, "M must be >= 0");
+    const bool sh_grads = colors_precomp == nullptr && rest != nullptr && M > 0;
+    GS_REQUIRE(!sh_grads || (dc != nullptr && M >= (D + 1) * (D + 1) - 1),
+               "SH gradients need dc and at least (D+1)^2 - 1 = %d further coefficients (got %d)",
+               (D + 1) * (D + 1) - 1, M);
+    GS_REQUIRE(cov3D_precomp != nullptr || (scales != nullptr && rotations != nullptr),
+               "either cov3D_precomp or scales and rotations are needed");
+    GS_REQUIRE(((uintptr_t)rotations & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
+               ((uintptr_t)dL_drotations & 15) == 0,
+               "rotations, dL_dconic_opacity and dL_drotations must be 16-byte aligned");
+    GS_REQUIRE(((uintptr_t)dL_dcov3D & 7) == 0 && ((uintptr_t)cov3D & 7) == 0,
+               "dL_dcov3D and cov3D must be 8-byte aligned");
+    const FullPreBwd F{cov3D_precomp, colors_precomp != nullptr, dc, sh_grads ? rest : nullptr, M, dL_ddc,
+                       dL_drest, dL_dcov3D};
+    const bool staged = M <= 15;
+    const float fy = (float)image_height / (2.0f * tanfovy);
+    const float fx = (float)image_width / (2.0f * tanfovx);
+    const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+#define GS_PRE_BWD_FULL(DEG)                                                                                     \
+    if (staged)                                                                                                  \
+        GS_TIMED("preprocess_bwd_full_kernel", stream,                                                           \
+                 hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, true, true>), grid, block, 0, stream, P, 0,        \
+                                    image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
+                                    viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
+                                    cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F));                         \
+    else                                                                                                         \
+        GS_TIMED("preprocess_bwd_full_kernel", stream,                                                           \
+                 hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false, true>), grid, block, 0, stream, P, 0,       \
+                                    image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
+                                    viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
+                                    cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F))
+    switch (D) {
+        case 0: GS_PRE_BWD_FULL(0); break;
+        case 1: GS_PRE_BWD_FULL(1); break;
+        case 2: GS_PRE_BWD_FULL(2); break;
+        default: GS_PRE_BWD_FULL(3); break;
+    }
+#undef GS_PRE_BWD_FULL
+    GS_LAUNCH_CHECK("preprocess_bwd_full_kernel");
+    return GS_OK;
+}
+
+namespace {
+
+// checkFrustum (reference rasterizer_impl.cu:103-116 with in_frustum,
+// auxiliary.h:158-184, prefiltered = false): visible = view-space z > 0.2.
+__global__ __launch_bounds__(256) void mark_visible_kernel(int P, const float* __restrict__ means3D,
+                                                           const float* __restrict__ view,
+                                                           uint8_t* __restrict__ present)
+{
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= P) return;
+    const float x = means3D[3 * idx], y = means3D[3 * idx + 1], z = means3D[3 * idx + 2];
+    const float vz = view[2] * x + view[6] * y + view[10] * z + view[14];
+    present[idx] = vz <= 0.2f ? 0 : 1;
+}
+
+}  // namespace
+
+extern "C" int gs_mark_visible(int P, const float* means3D, const float* viewmatrix, const float* projmatrix,
+                               uint8_t* present, hipStream_t stream)
+{
+    gs::clear_error();
+    (void)projmatrix;
+    GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(means3D && viewmatrix && present, "null argument");
+    GS_TIMED("mark_visible_kernel", stream,
+             hipLaunchKernelGGL(mark_visible_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
+                                means3D, viewmatrix, present));
+    GS_LAUNCH_CHECK("mark_visible_kernel");
     return GS_OK;
 }

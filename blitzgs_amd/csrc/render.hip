@@ -152,10 +152,9 @@ const T* at(const void* base, size_t off) { return reinterpret_cast<const T*>(st
 
 // ---------------------------------------------------------------- scans
 
-// compute_locally -> local tile numbering; clears the per-tile counters
-// compute_locally -> local tile numbering and the bounding box of the local
-// tiles (meta[5..8] = x0, y0, x1, y1, exclusive ends; empty box if none);
-// clears the per-tile counters
+// compute_locally (null: every tile) -> local tile numbering and the
+// bounding box of the local tiles (meta[5..8] = x0, y0, x1, y1, exclusive
+// ends; empty box if none); clears the per-tile counters
 __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, const uint8_t* __restrict__ cl,
                                                         int* __restrict__ loc_map, int* __restrict__ tile_of_local,
                                                         uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta)
@@ -168,7 +167,7 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
     uint32_t base = 0;
     for (int t0 = 0; t0 < T; t0 += 1024) {
         const int t = t0 + threadIdx.x;
-        const uint32_t f = (t < T && cl[t]) ? 1u : 0u;
+        const uint32_t f = (t < T && (cl == nullptr || cl[t])) ? 1u : 0u;
         uint32_t tot;
         const uint32_t pre = gs::block_excl_scan_1024(f, s_wave, &tot);
         if (t < T) {
@@ -273,6 +272,42 @@ __device__ __forceinline__ int rect_from(int r, float2 p, unsigned gx, unsigned 
     return (int)(w * (y1 - y0));
 }
 
+// float-extent rect of the full-image path (ext = the preprocess's rect
+// extents), clipped to the local-tile box; returns its tile count there
+__device__ __forceinline__ int rect_from_ext(int r, float2 p, float2 ext, unsigned gx, unsigned gy,
+                                             const TileBox& box, unsigned& x0, unsigned& y0, unsigned& w)
+{
+    x0 = y0 = w = 0;
+    if (r <= 0) return 0;
+    unsigned x1, y1;
+    gs::rect_float(p.x, p.y, ext.x, ext.y, gx, gy, x0, y0, x1, y1);
+    x0 = max(x0, box.x0); y0 = max(y0, box.y0);
+    x1 = min(x1, box.x1); y1 = min(y1, box.y1);
+    if (x1 <= x0 || y1 <= y0) { x0 = y0 = 0; return 0; }
+    w = x1 - x0;
+    return (int)(w * (y1 - y0));
+}
+
+// Per-Gaussian constants of the full path's tile test, carried by the lane
+// that holds the Gaussian and shuffled to the lanes expanding its tiles.
+struct KeepTest {
+    float mx, my, a, b, c, thr;
+};
+
+__device__ __forceinline__ KeepTest keep_test_of(float2 m, float4 co)
+{
+    return KeepTest{m.x, m.y, co.x, co.y, co.z, gs::logf_full(co.w / (1.0f / 255.0f))};
+}
+
+// does instance (owner's Gaussian, tile tx, ty) survive the tile test
+__device__ __forceinline__ bool keep_instance(const KeepTest& k, int owner, unsigned tx, unsigned ty)
+{
+    const float mx = __shfl(k.mx, owner, 64), my = __shfl(k.my, owner, 64);
+    const float a = __shfl(k.a, owner, 64), b = __shfl(k.b, owner, 64), c = __shfl(k.c, owner, 64);
+    const float thr = __shfl(k.thr, owner, 64);
+    return gs::full_tile_keep(mx, my, a, b, c, thr, tx, ty);
+}
+
 // radius and mean of Gaussian i of a wave's run ending at i1 (radius 0 past it)
 __device__ __forceinline__ void load_rm(int i, int i1, const int* __restrict__ radii,
                                         const float2* __restrict__ means2D, int& r, float2& m)
@@ -293,10 +328,15 @@ __device__ __forceinline__ void load_rm(int i, int i1, const int* __restrict__ r
 // Each wave takes a contiguous run of WS Gaussians of the chunk and also
 // counts its listed Gaussians (wcount), from which the scan derives the
 // compact indices.
+//
+// FULL (the full-image path): rects come from the preprocess's float extents
+// and an instance counts only if it passes the tile test (full_tile_keep).
+template <bool FULL>
 __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     int P, int CH, int WS, unsigned gx, unsigned gy, const float2* __restrict__ means2D, const int* __restrict__ radii,
     const int* __restrict__ loc_map, const uint32_t* __restrict__ meta, uint32_t* __restrict__ hist,
-    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ wcount)
+    uint32_t* __restrict__ tile_count, uint32_t* __restrict__ wcount, const float2* __restrict__ rects,
+    const float4* __restrict__ conic_opacity)
 {
     extern __shared__ uint4 s_dyn[];   // min(T, LDS_TILES) tile counters
     uint32_t* s_hist = reinterpret_cast<uint32_t*>(s_dyn);
@@ -323,14 +363,23 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
         const float2 m = m_n;
         load_rm(wb + 64 + lane, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_from(r, m, gx, gy, box, x0, y0, w);
+        int cnt;
+        KeepTest kt{};
+        if (FULL) {
+            const int i = wb + lane;
+            cnt = rect_from_ext(r, m, r > 0 ? rects[i] : make_float2(0.f, 0.f), gx, gy, box, x0, y0, w);
+            if (cnt > 0) kt = keep_test_of(m, conic_opacity[i]);
+        } else {
+            cnt = rect_from(r, m, gx, gy, box, x0, y0, w);
+        }
         listed += (uint32_t)__builtin_popcountll(gs::ballot(cnt > 0));
         const Expansion e = expansion_begin(cnt);
         for (int k0 = 0; k0 < e.total; k0 += 64) {
             int owner;
             unsigned tx, ty;
             expansion_at(e, cnt, x0, y0, w, k0 + lane, owner, tx, ty);
-            if (k0 + lane < e.total) {
+            const bool kept = !FULL || keep_instance(kt, owner, tx, ty);
+            if (k0 + lane < e.total && kept) {
                 const unsigned t = ty * gx + tx;
                 const int l = all_local ? (int)t : loc_map[t];
                 if (l >= 0) {
@@ -402,9 +451,11 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
     uint32_t cnt = 0, s = 0;
     if (l >= 0) { cnt = tile_count[l]; s = tile_start[l]; }
     ranges[t] = cnt ? make_uint2(s, s + cnt) : make_uint2(0u, 0u);
-    n_render[t] = (int32_t)cnt;
-    n_consider[t] = 0;
-    n_contrib[t] = 0;
+    if (n_render != nullptr) {   // the split path's per-tile statistics
+        n_render[t] = (int32_t)cnt;
+        n_consider[t] = 0;
+        n_contrib[t] = 0;
+    }
 }
 
 // ------------------------------------------------------------- scatter
@@ -415,13 +466,15 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
 // sorting by them breaks depth ties exactly as sorting by id does.  Every
 // Gaussian gets its compact index or -1 (cidx_of); listed ones also get their
 // blend record, id (cid2id) and a zeroed gradient accumulator.
+template <bool FULL>
 __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     int P, int CH, int WS, unsigned gx, unsigned gy, const float2* __restrict__ means2D,
     const float* __restrict__ depths, const int* __restrict__ radii, const float4* __restrict__ conic_opacity,
     const float* __restrict__ rgb, const int* __restrict__ loc_map, const uint32_t* __restrict__ meta,
     const uint32_t* __restrict__ hist, const uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
     const uint32_t* __restrict__ wbase, uint64_t* __restrict__ sortkey, int* __restrict__ cidx_of,
-    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, float4* __restrict__ gacc)
+    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, float4* __restrict__ gacc,
+    const float2* __restrict__ rects)
 {
     // dynamic LDS: per wave 64 staged records, then min(T, LDS_TILES) cursors
     extern __shared__ uint4 s_dyn[];
@@ -465,7 +518,14 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
         const float3 col = c_n;
         load_rm(i + 64, i1, radii, means2D, r_n, m_n);
         unsigned x0, y0, w;
-        const int cnt = rect_from(r, xy, gx, gy, box, x0, y0, w);
+        int cnt;
+        KeepTest kt{};
+        if (FULL) {
+            cnt = rect_from_ext(r, xy, r > 0 ? rects[i] : make_float2(0.f, 0.f), gx, gy, box, x0, y0, w);
+            if (cnt > 0) kt = keep_test_of(xy, co);
+        } else {
+            cnt = rect_from(r, xy, gx, gy, box, x0, y0, w);
+        }
         const uint64_t lm = gs::ballot(cnt > 0);
         const int nl = (int)__builtin_popcountll(lm);
         const int rank = gs::rank_below(lm);
@@ -505,7 +565,8 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
             expansion_at(e, cnt, x0, y0, w, k0 + lane, owner, tx, ty);
             const uint32_t odb = (uint32_t)__shfl((int)dbits, owner, 64);
             const uint32_t ocx = (uint32_t)__shfl((int)cidx, owner, 64);
-            if (k0 + lane < e.total) {
+            const bool kept = !FULL || keep_instance(kt, owner, tx, ty);
+            if (k0 + lane < e.total && kept) {
                 const unsigned t = ty * gx + tx;
                 const int l = all_local ? (int)t : loc_map[t];
                 if (l >= 0) {
@@ -798,12 +859,32 @@ __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uin
     st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k), 0.f);
 }
 
+// Blend modes: the split path's render (observation counts and per-tile
+// statistics), the full-image path's render (per pixel, the Gaussian of the
+// largest blend weight alpha * T gets one count in accum_max_count, when that
+// pointer is set) and its render_simp (the same plus every contribution's
+// alpha * T and a count added to the Gaussian's accumulators, one atomic per
+// wave and Gaussian).
+constexpr int BLEND_SPLIT = 0, BLEND_FULL = 1, BLEND_SIMP = 2;
+
+struct FwdOut {
+    float* out_color;
+    float* final_T;
+    uint32_t* n_contrib_px;
+    uint32_t* n_contrib2loss_px;   // split
+    int32_t* out_observe;          // split
+    int32_t* n_consider;           // split
+    int32_t* n_contrib_tile;       // split
+    float* accum_max_count;        // full (null: flag_max_count off), simp
+    float* accum_weights;          // simp
+    int32_t* accum_weights_count;  // simp
+};
+
+template <int MODE>
 __global__ __launch_bounds__(64) void render_fwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
-    const float* __restrict__ bg, float* __restrict__ out_color, float* __restrict__ final_T,
-    uint32_t* __restrict__ n_contrib_px, uint32_t* __restrict__ n_contrib2loss_px, int32_t* __restrict__ out_observe,
-    int32_t* __restrict__ n_consider, int32_t* __restrict__ n_contrib_tile)
+    const float* __restrict__ bg, FwdOut O)
 {
     unsigned tile, quad, tx, ty;
     if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
@@ -813,10 +894,12 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     const bool inside = px < W && py < H;
     const size_t pid = (size_t)py * W + px;
     const size_t HW = (size_t)H * W;
-    if (!cl[tile]) {
+    float* __restrict__ out_color = O.out_color;
+    if (cl != nullptr && !cl[tile]) {
         if (inside) {
             out_color[pid] = 0.f; out_color[HW + pid] = 0.f; out_color[2 * HW + pid] = 0.f;
-            final_T[pid] = 0.f; n_contrib_px[pid] = 0; n_contrib2loss_px[pid] = 0;
+            O.final_T[pid] = 0.f; O.n_contrib_px[pid] = 0;
+            if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = 0;
         }
         return;
     }
@@ -830,6 +913,8 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     const float alpha_min = 1.0f / 255.0f;
     float T_ = 1.0f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
     uint32_t last = 0, n2l = 0;
+    float wmax = 0.f;      // largest blend weight so far, and its Gaussian (full / simp)
+    uint32_t imax = 0u;
     bool done = !inside;
 
     // software pipeline: while a batch blends, the next batch's records and
@@ -871,10 +956,26 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
             n2l += upd ? 1u : 0u;
             last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : last;
             done = done || fin;
-            const uint64_t m = gs::ballot(observe);
-            if (m != 0) {
-                const int first = (int)__builtin_ctzll(m);
-                if (lane == first) atomicAdd(&out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
+            if (MODE == BLEND_SPLIT) {
+                const uint64_t m = gs::ballot(observe);
+                if (m != 0) {
+                    const int first = (int)__builtin_ctzll(m);
+                    if (lane == first) atomicAdd(&O.out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
+                }
+            } else {
+                const bool better = upd && wmax < wgt;
+                wmax = better ? wgt : wmax;
+                imax = better ? __float_as_uint(Cc.y) : imax;
+                if (MODE == BLEND_SIMP) {
+                    const uint64_t um = gs::ballot(upd);
+                    if (um != 0) {
+                        const float ws = gs::wave_sum(upd ? wgt : 0.f);
+                        if (lane == (int)__builtin_ctzll(um)) {
+                            atomicAdd(&O.accum_weights[__float_as_uint(Cc.y)], ws);
+                            atomicAdd(&O.accum_weights_count[__float_as_uint(Cc.y)], (int)__builtin_popcountll(um));
+                        }
+                    }
+                }
             }
         };
         // two register sets in turn: the next entry's LDS reads are issued
@@ -896,18 +997,22 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     }
 
     if (inside) {
-        final_T[pid] = T_;
-        n_contrib_px[pid] = last;
-        n_contrib2loss_px[pid] = n2l;
+        O.final_T[pid] = T_;
+        O.n_contrib_px[pid] = last;
+        if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = n2l;
         out_color[pid] = __builtin_fmaf(T_, bg[0], C0);
         out_color[HW + pid] = __builtin_fmaf(T_, bg[1], C1);
         out_color[2 * HW + pid] = __builtin_fmaf(T_, bg[2], C2);
     }
-    const int s_last = gs::wave_sum_i(inside ? (int)last : 0);
-    const int s_n2l = gs::wave_sum_i(inside ? (int)n2l : 0);
-    if (lane == 0) {
-        if (s_last) atomicAdd(&n_consider[tile], s_last);
-        if (s_n2l) atomicAdd(&n_contrib_tile[tile], s_n2l);
+    if (MODE == BLEND_SPLIT) {
+        const int s_last = gs::wave_sum_i(inside ? (int)last : 0);
+        const int s_n2l = gs::wave_sum_i(inside ? (int)n2l : 0);
+        if (lane == 0) {
+            if (s_last) atomicAdd(&O.n_consider[tile], s_last);
+            if (s_n2l) atomicAdd(&O.n_contrib_tile[tile], s_n2l);
+        }
+    } else if (O.accum_max_count != nullptr && inside && last > 0) {
+        atomicAdd(&O.accum_max_count[imax], 1.0f);
     }
 }
 
@@ -939,11 +1044,17 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
     m[0] = a.x;
     m[1] = a.y;
     for (int k = 2; k < m2d_stride; k++) m[k] = 0.f;
-    g_m2d_abs[3 * (size_t)i] = a.z; g_m2d_abs[3 * (size_t)i + 1] = a.w; g_m2d_abs[3 * (size_t)i + 2] = 0.f;
+    if (g_m2d_abs != nullptr) {
+        g_m2d_abs[3 * (size_t)i] = a.z; g_m2d_abs[3 * (size_t)i + 1] = a.w; g_m2d_abs[3 * (size_t)i + 2] = 0.f;
+    }
     g_con[i] = b;
     g_col[3 * (size_t)i] = c.x; g_col[3 * (size_t)i + 1] = c.y; g_col[3 * (size_t)i + 2] = c.z;
 }
 
+// FULL: the full-image path's rule (reference _f backward.cu:560-566): no
+// conic or opacity gradient from a pixel where opacity * G > 0.99 (the alpha
+// clamp is active); |dL/dmean2D| is accumulated but not written out.
+template <bool FULL>
 __global__ __launch_bounds__(64) void render_bwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
@@ -952,7 +1063,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
 {
     unsigned tile, quad, tx, ty;
     if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
-    if (!cl[tile]) return;
+    if (cl != nullptr && !cl[tile]) return;
     const int lane = threadIdx.x;
     const int qx = (int)tx * 16 + (int)(quad & 1u) * 8, qy = (int)ty * 16 + (int)(quad >> 1) * 8;
     const int px = qx + (lane & 7), py = qy + (lane >> 3);
@@ -1045,10 +1156,11 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
                     gmy = (dL_dG * ddely_dy) * dG_ddely;
                     const float h = -0.5f * dL_dG;
                     const float hgdx = h * gdx;
-                    gca = hgdx * dx;
-                    gcb = hgdx * dy;
-                    gcc = (h * gdy) * dy;
-                    gop = G * dL_dalpha;
+                    const bool clamped = FULL && B.y * G > 0.99f;
+                    gca = clamped ? 0.f : hgdx * dx;
+                    gcb = clamped ? 0.f : hgdx * dy;
+                    gcc = clamped ? 0.f : (h * gdy) * dy;
+                    gop = clamped ? 0.f : G * dL_dalpha;
                 }
             }
             if (gs::ballot(valid) == 0) continue;
@@ -1102,13 +1214,19 @@ extern "C" int gs_render_buffer_views(int64_t R, int W, int H, void* binning, vo
     return GS_OK;
 }
 
-extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D, const int* radii,
-                                       const uint8_t* compute_locally, void* geom, int64_t* num_rendered,
-                                       hipStream_t stream)
+namespace {
+
+// count + scan + R readback, shared by the split and the full-image path
+int render_count_impl(bool full, int P, int W, int H, const float* means2D, const int* radii,
+                      const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
+                      int64_t* num_rendered, hipStream_t stream)
 {
-    gs::clear_error();
     GS_REQUIRE(P >= 0 && W > 0 && H > 0, "invalid sizes P=%d W=%d H=%d", P, W, H);
     GS_REQUIRE(geom != nullptr && num_rendered != nullptr, "geom and num_rendered must be non-null");
+    GS_REQUIRE(!full || P == 0 || (rects != nullptr && conic_opacity != nullptr),
+               "the full path needs rects and conic_opacity");
+    GS_REQUIRE(((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0 && ((uintptr_t)conic_opacity & 15) == 0,
+               "means2D / rects must be 8-byte and conic_opacity 16-byte aligned");
     const GeomLayout g = geom_layout(P, W, H);
     const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
     int* loc_map = at<int>(geom, g.loc_map);
@@ -1123,11 +1241,19 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
                        tile_of_local, tile_count, meta));
     GS_LAUNCH_CHECK("localmap_kernel");
     if (P > 0) {
-        GS_TIMED("count_kernel", stream,
-                 hipLaunchKernelGGL(count_kernel, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream, P,
-                                    g.CH, g.WS, gx, gy,
-                                    reinterpret_cast<const float2*>(means2D), radii, loc_map, meta, hist, tile_count,
-                                    at<uint32_t>(geom, g.wcount)));
+        const float2* m2 = reinterpret_cast<const float2*>(means2D);
+        if (full) {
+            GS_TIMED("count_kernel", stream,
+                     hipLaunchKernelGGL(count_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream,
+                                        P, g.CH, g.WS, gx, gy, m2, radii, loc_map, meta, hist, tile_count,
+                                        at<uint32_t>(geom, g.wcount), reinterpret_cast<const float2*>(rects),
+                                        reinterpret_cast<const float4*>(conic_opacity)));
+        } else {
+            GS_TIMED("count_kernel", stream,
+                     hipLaunchKernelGGL(count_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream,
+                                        P, g.CH, g.WS, gx, gy, m2, radii, loc_map, meta, hist, tile_count,
+                                        at<uint32_t>(geom, g.wcount), nullptr, nullptr));
+        }
         GS_LAUNCH_CHECK("count_kernel");
     }
     GS_TIMED("tilescan_kernel", stream,
@@ -1146,16 +1272,17 @@ extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D
     return GS_OK;
 }
 
-extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
-                                 const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
-                                 const uint8_t* compute_locally, void* geom, void* binning, void* img,
-                                 float* out_color, int32_t* n_render, int32_t* n_consider, int32_t* n_contrib,
-                                 int32_t* out_observe, hipStream_t stream)
+// duplicate + sort + ranges + blend, shared by the split and the full-image path
+int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                        const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
+                        const uint8_t* compute_locally, const float* rects, void* geom, void* binning, void* img,
+                        FwdOut O, int32_t* n_render, hipStream_t stream)
 {
-    gs::clear_error();
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
-    GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)means2D & 7) == 0,
-               "conic_opacity must be 16-byte and means2D 8-byte aligned");
+    GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0,
+               "conic_opacity must be 16-byte and means2D / rects 8-byte aligned");
+    const bool full = mode != BLEND_SPLIT;
+    GS_REQUIRE(!full || P == 0 || rects != nullptr, "the full path needs rects");
     const GeomLayout g = geom_layout(P, W, H);
     const ImgLayout il = img_layout(W, H);
     const BinLayout bl = bin_layout(R);
@@ -1174,21 +1301,45 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
 
     const unsigned T = (unsigned)g.T;
     GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
-                       tile_start, ranges, n_render, n_consider, n_contrib));
+                       tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
     GS_LAUNCH_CHECK("ranges_kernel");
     if (P > 0) {
-        GS_TIMED("zero_i32_kernel", stream, hipLaunchKernelGGL(zero_i32_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P, out_observe));
-        GS_LAUNCH_CHECK("zero_i32_kernel");
+        // per-Gaussian accumulators start at zero
+        const dim3 zg(gs_div_up((size_t)P, 256));
+        int32_t* zero_these[3] = {mode == BLEND_SPLIT ? O.out_observe : nullptr,
+                                  reinterpret_cast<int32_t*>(O.accum_max_count),
+                                  mode == BLEND_SIMP ? reinterpret_cast<int32_t*>(O.accum_weights) : nullptr};
+        for (int32_t* z : zero_these) {
+            if (z == nullptr) continue; {
+                GS_TIMED("zero_i32_kernel", stream, hipLaunchKernelGGL(zero_i32_kernel, zg, dim3(256), 0, stream, P, z));
+            }
+            GS_LAUNCH_CHECK("zero_i32_kernel");
+        }
+        if (mode == BLEND_SIMP) {
+            GS_TIMED("zero_i32_kernel", stream,
+                     hipLaunchKernelGGL(zero_i32_kernel, zg, dim3(256), 0, stream, P, O.accum_weights_count));
+            GS_LAUNCH_CHECK("zero_i32_kernel");
+        }
     }
     if (R > 0) {
-        GS_TIMED("scatter_kernel", stream,
-                 hipLaunchKernelGGL(scatter_kernel, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T), stream, P,
-                                    g.CH, g.WS, gx, gy,
-                                    reinterpret_cast<const float2*>(means2D), depths, radii,
-                                    reinterpret_cast<const float4*>(conic_opacity), rgb, loc_map, meta, hist,
-                                    tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
-                                    at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec),
-                                    at<float4>(geom, g.gacc)));
+        const float2* m2 = reinterpret_cast<const float2*>(means2D);
+        const float4* co = reinterpret_cast<const float4*>(conic_opacity);
+        if (full) {
+            GS_TIMED("scatter_kernel", stream,
+                     hipLaunchKernelGGL(scatter_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
+                                        stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
+                                        hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
+                                        at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
+                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc),
+                                        reinterpret_cast<const float2*>(rects)));
+        } else {
+            GS_TIMED("scatter_kernel", stream,
+                     hipLaunchKernelGGL(scatter_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
+                                        stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
+                                        hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
+                                        at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
+                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc), nullptr));
+        }
         GS_LAUNCH_CHECK("scatter_kernel");
         const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};
         GS_TIMED("tilesort_kernel_512", stream,
@@ -1218,30 +1369,39 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
     }
     unsigned sgx, NS;
     const unsigned nblk = blend_grid(gx, gy, sgx, NS);
-    GS_TIMED("render_fwd_kernel", stream,
-             hipLaunchKernelGGL(render_fwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS, ranges,
-                                at<const uint32_t>(binning, bl.clist), at<const float4>(geom, g.rec),
-                                compute_locally, bg, out_color,
-                                at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib),
-                                at<uint32_t>(img, il.n_contrib2loss), out_observe, n_consider, n_contrib));
+    O.final_T = at<float>(img, il.final_T);
+    O.n_contrib_px = at<uint32_t>(img, il.n_contrib);
+    O.n_contrib2loss_px = at<uint32_t>(img, il.n_contrib2loss);
+    const uint32_t* clist = at<const uint32_t>(binning, bl.clist);
+    const float4* recs = at<const float4>(geom, g.rec);
+    if (mode == BLEND_SPLIT) {
+        GS_TIMED("render_fwd_kernel", stream,
+                 hipLaunchKernelGGL(render_fwd_kernel<BLEND_SPLIT>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
+                                    NS, ranges, clist, recs, compute_locally, bg, O));
+    } else if (mode == BLEND_FULL) {
+        GS_TIMED("render_fwd_kernel", stream,
+                 hipLaunchKernelGGL(render_fwd_kernel<BLEND_FULL>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
+                                    NS, ranges, clist, recs, compute_locally, bg, O));
+    } else {
+        GS_TIMED("render_fwd_kernel", stream,
+                 hipLaunchKernelGGL(render_fwd_kernel<BLEND_SIMP>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
+                                    NS, ranges, clist, recs, compute_locally, bg, O));
+    }
     GS_LAUNCH_CHECK("render_fwd_kernel");
     return GS_OK;
 }
 
-extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
-                                  const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
-                                  void* geom, const void* binning, const void* img, const float* dL_dpixels,
-                                  float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
-                                  float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
+int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                         const float* conic_opacity, const uint8_t* compute_locally, void* geom, const void* binning,
+                         const void* img, const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
+                         float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
 {
-    gs::clear_error();
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
     GS_REQUIRE(dL_dmeans2D_stride >= 2, "dL_dmeans2D row stride must be >= 2");
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
                ((uintptr_t)means2D & 7) == 0,
                "conic_opacity / dL_dconic_opacity must be 16-byte and means2D 8-byte aligned");
     GS_REQUIRE(geom != nullptr, "geom must be the forward's geometry workspace");
-    (void)rgb;
     if (P == 0) return GS_OK;
     const GeomLayout g = geom_layout(P, W, H);
     const ImgLayout il = img_layout(W, H);
@@ -1251,11 +1411,20 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
     if (R > 0) {
         unsigned sgx, NS;
         const unsigned nblk = blend_grid(gx, gy, sgx, NS);
-        GS_TIMED("render_bwd_kernel", stream,
-                 hipLaunchKernelGGL(render_bwd_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS,
-                                    at<uint2>(img, il.ranges), at<const uint32_t>(binning, bl.clist),
-                                    at<const float4>(geom, g.rec), compute_locally, bg, at<float>(img, il.final_T),
-                                    at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+        const uint2* rng = at<uint2>(img, il.ranges);
+        const uint32_t* clist = at<const uint32_t>(binning, bl.clist);
+        const float4* recs = at<const float4>(geom, g.rec);
+        if (full) {
+            GS_TIMED("render_bwd_kernel", stream,
+                     hipLaunchKernelGGL(render_bwd_kernel<true>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
+                                        NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
+                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+        } else {
+            GS_TIMED("render_bwd_kernel", stream,
+                     hipLaunchKernelGGL(render_bwd_kernel<false>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
+                                        NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
+                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+        }
         GS_LAUNCH_CHECK("render_bwd_kernel");
     }
     // without instances the forward wrote no flags: every output is zero
@@ -1266,4 +1435,84 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
                                 dL_dcolors));
     GS_LAUNCH_CHECK("unpack_grads_kernel");
     return GS_OK;
+}
+
+}  // namespace
+
+extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D, const int* radii,
+                                       const uint8_t* compute_locally, void* geom, int64_t* num_rendered,
+                                       hipStream_t stream)
+{
+    gs::clear_error();
+    return render_count_impl(false, P, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom, num_rendered,
+                             stream);
+}
+
+extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                 const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
+                                 const uint8_t* compute_locally, void* geom, void* binning, void* img,
+                                 float* out_color, int32_t* n_render, int32_t* n_consider, int32_t* n_contrib,
+                                 int32_t* out_observe, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.out_observe = out_observe;
+    O.n_consider = n_consider;
+    O.n_contrib_tile = n_contrib;
+    return render_forward_impl(BLEND_SPLIT, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
+                               compute_locally, nullptr, geom, binning, img, O, n_render, stream);
+}
+
+extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                  const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
+                                  void* geom, const void* binning, const void* img, const float* dL_dpixels,
+                                  float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
+                                  float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
+{
+    gs::clear_error();
+    (void)rgb;
+    GS_REQUIRE(dL_dmeans2D_abs != nullptr, "dL_dmeans2D_abs must be non-null");
+    return render_backward_impl(false, P, R, W, H, bg, means2D, conic_opacity, compute_locally, geom, binning, img,
+                                dL_dpixels, dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity,
+                                dL_dcolors, stream);
+}
+
+extern "C" int gs_render_full_count(int P, int W, int H, const float* means2D, const int* radii, const float* rects,
+                                    const float* conic_opacity, void* geom, int64_t* num_rendered, hipStream_t stream)
+{
+    gs::clear_error();
+    return render_count_impl(true, P, W, H, means2D, radii, nullptr, rects, conic_opacity, geom, num_rendered,
+                             stream);
+}
+
+extern "C" int gs_render_full_forward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                      const float* depths, const int* radii, const float* rects,
+                                      const float* conic_opacity, const float* colors, void* geom, void* binning,
+                                      void* img, float* out_color, float* accum_max_count, float* accum_weights,
+                                      int32_t* accum_weights_count, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(out_color != nullptr, "out_color must be non-null");
+    GS_REQUIRE((accum_weights == nullptr) == (accum_weights_count == nullptr),
+               "accum_weights and accum_weights_count go together");
+    GS_REQUIRE(accum_weights == nullptr || accum_max_count != nullptr, "render_simp needs accum_max_count");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.accum_max_count = accum_max_count;
+    O.accum_weights = accum_weights;
+    O.accum_weights_count = accum_weights_count;
+    return render_forward_impl(accum_weights != nullptr ? BLEND_SIMP : BLEND_FULL, P, R, W, H, bg, means2D, depths,
+                               radii, conic_opacity, colors, nullptr, rects, geom, binning, img, O, nullptr, stream);
+}
+
+extern "C" int gs_render_full_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                       const float* conic_opacity, void* geom, const void* binning, const void* img,
+                                       const float* dL_dpixels, float* dL_dmeans2D, float* dL_dconic_opacity,
+                                       float* dL_dcolors, hipStream_t stream)
+{
+    gs::clear_error();
+    return render_backward_impl(true, P, R, W, H, bg, means2D, conic_opacity, nullptr, geom, binning, img, dL_dpixels,
+                                dL_dmeans2D, 3, nullptr, dL_dconic_opacity, dL_dcolors, stream);
 }

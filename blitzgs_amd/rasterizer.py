@@ -316,7 +316,9 @@ class _RenderGaussians(torch.autograd.Function):
 
 
 class GaussianRasterizer(nn.Module):
-    """The split-path rasterizer module (_f __init__.py:661-829)."""
+    """The rasterizer module (_f __init__.py:661-829): the split training path
+    (preprocess_gaussians, render_gaussians) and the full-image path (forward,
+    render_simp, markVisible; blitzgs_amd.fullpath)."""
 
     def __init__(self, raster_settings):
         super().__init__()
@@ -331,14 +333,35 @@ class GaussianRasterizer(nn.Module):
                                 extended_compute_locally, self.raster_settings, cuda_args)
 
     def markVisible(self, positions):
-        raise NotImplementedError("markVisible (full-image _f path) is not part of the split training path")
+        """_f __init__.py:665-674."""
+        from .fullpath import mark_visible
+        rs = self.raster_settings
+        return mark_visible(positions, rs.viewmatrix, rs.projmatrix)
 
-    def forward(self, *args, **kwargs):
-        raise NotImplementedError("the full-image _f rasterize path (render_imp) is not implemented; "
-                                  "use preprocess_gaussians + render_gaussians")
+    @staticmethod
+    def _check_inputs(shs, colors_precomp, scales, rotations, cov3D_precomp):
+        # the reference's argument rules (_f __init__.py:695-700)
+        if (shs is None and colors_precomp is None) or (shs is not None and colors_precomp is not None):
+            raise Exception('Please provide excatly one of either SHs or precomputed colors!')
+        if ((scales is None or rotations is None) and cov3D_precomp is None) or \
+                ((scales is not None or rotations is not None) and cov3D_precomp is not None):
+            raise Exception('Please provide exactly one of either scale/rotation pair or precomputed 3D covariance!')
 
-    def render_simp(self, *args, **kwargs):
-        raise NotImplementedError("render_simp (importance accumulation) is not implemented")
+    def forward(self, means3D, means2D, opacities, culling, dc=None, shs=None, colors_precomp=None, scales=None,
+                rotations=None, cov3D_precomp=None, flag_max_count=False):
+        """The full-image path (_f __init__.py:691-730): (color, radii, accum_max_count)."""
+        from .fullpath import rasterize_gaussians
+        self._check_inputs(shs, colors_precomp, scales, rotations, cov3D_precomp)
+        return rasterize_gaussians(means3D, means2D, dc, shs, colors_precomp, opacities, scales, rotations,
+                                   cov3D_precomp, flag_max_count, culling, self.raster_settings)
+
+    def render_simp(self, means3D, means2D, opacities, culling, dc=None, shs=None, colors_precomp=None, scales=None,
+                    rotations=None, cov3D_precomp=None):
+        """_f __init__.py:733-770: (color, radii, accum_weights, accum_weights_count, accum_max_count)."""
+        from .fullpath import rasterize_gaussians_simp
+        self._check_inputs(shs, colors_precomp, scales, rotations, cov3D_precomp)
+        return rasterize_gaussians_simp(means3D, means2D, dc, shs, colors_precomp, opacities, scales, rotations,
+                                        cov3D_precomp, culling, self.raster_settings)
 
     def render_depth(self, *args, **kwargs):
-        raise NotImplementedError("render_depth is not implemented")
+        raise NotImplementedError("render_depth (no caller in BlitzGS) is not provided")

@@ -193,6 +193,77 @@ int gs_adam_update_groups(int n_groups, const gs_adam_group* groups, int64_t N,
                           const uint8_t* visible, float b1, float b2, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
+ * Full-image path (GaussianRasterizer.forward / render_simp / markVisible of
+ * diff-gaussian-rasterization_f).  Together these replace
+ * RasterizeGaussiansCUDA (_f/rasterize_points.cu:370-475),
+ * RasterizeGaussiansSimpCUDA (:477-583), RasterizeGaussiansBackwardCUDA
+ * (:697-783) and markVisible (:785-805), i.e. Rasterizer::forward /
+ * forward_simp / backward (_f/cuda_rasterizer/rasterizer_impl.cu:336-660,
+ * 850-955) and their kernels (forward.cu:165-614, backward.cu:146-596,
+ * rasterizer_impl.cu:56-253).
+ *
+ * gs_preprocess_forward_full: preprocessCUDA with the full path's inputs --
+ *   culling (P) uint8 (nonzero = skip), colors_precomp (P,3) or NULL,
+ *   cov3D_precomp (P,6) or NULL (then scales / rotations are used), SH as dc
+ *   (P,1,3) + rest (P,M,3), M >= (D+1)^2 - 1 unless colours are given.
+ *   Outputs as gs_preprocess_forward plus rects (P,2) float tile-rect extents
+ *   and tiles_touched (P) uint32 rect tile counts (their sum is the reference's
+ *   num_rendered).  prefiltered is not an input: near-culled points are
+ *   skipped (the reference traps on them when prefiltered is set).
+ * gs_render_full_count / gs_render_full_forward: binning with the float
+ *   rects and the per-tile culling test of duplicateWithKeys, then the blend;
+ *   *num_rendered is the number of instances that pass the test (the sizes of
+ *   the workspaces; not the reference's num_rendered).  colors: the preprocess
+ *   rgb or colors_precomp.  accum_max_count (P) float: per pixel, the Gaussian
+ *   of the largest alpha * T gets +1 (NULL: flag_max_count off).  render_simp:
+ *   accum_weights (P) float (sum of alpha * T) and accum_weights_count (P)
+ *   int32 non-NULL.  All accumulators are zeroed by the call.
+ * gs_render_full_backward: dL_dmeans2D (P,3), dL_dconic_opacity (P,4) =
+ *   [c00, c01, c11, opacity] (16-byte aligned), dL_dcolors (P,3); conic and
+ *   opacity gradients skip pixels where the alpha clamp is active.
+ * gs_preprocess_backward_full: from those gradients, dL_dmeans3D (P,3),
+ *   dL_dcov3D (P,6), dL_ddc (P,1,3), dL_drest (P,M,3), dL_dscales (P,3),
+ *   dL_drotations (P,4), dL_dopacity (P,1); SH gradients only with SH colours
+ *   and M > 0, scale / rotation gradients only without cov3D_precomp.
+ * gs_mark_visible: present (P) uint8 = view-space z > 0.2.
+ * ------------------------------------------------------------------------ */
+int gs_preprocess_forward_full(int P, int D, int M, const float* means3D, const float* scales,
+                               const float* rotations, const float* dc, const float* rest,
+                               const float* opacities, const float* colors_precomp,
+                               const float* cov3D_precomp, const uint8_t* culling, float scale_modifier,
+                               const float* viewmatrix, const float* projmatrix, const float* campos,
+                               float tanfovx, float tanfovy, int image_height, int image_width,
+                               float* means2D, float* depths, int* radii, float* cov3D,
+                               float* conic_opacity, float* rgb, uint8_t* clamped, float* rects,
+                               uint32_t* tiles_touched, gs_stream_t stream);
+int gs_render_full_count(int P, int image_width, int image_height, const float* means2D, const int* radii,
+                         const float* rects, const float* conic_opacity, void* geom,
+                         int64_t* num_rendered, gs_stream_t stream);
+int gs_render_full_forward(int P, int64_t R, int image_width, int image_height, const float* bg,
+                           const float* means2D, const float* depths, const int* radii, const float* rects,
+                           const float* conic_opacity, const float* colors, void* geom, void* binning,
+                           void* img, float* out_color, float* accum_max_count, float* accum_weights,
+                           int32_t* accum_weights_count, gs_stream_t stream);
+int gs_render_full_backward(int P, int64_t R, int image_width, int image_height, const float* bg,
+                            const float* means2D, const float* conic_opacity, void* geom,
+                            const void* binning, const void* img, const float* dL_dpixels,
+                            float* dL_dmeans2D, float* dL_dconic_opacity, float* dL_dcolors,
+                            gs_stream_t stream);
+int gs_preprocess_backward_full(int P, int D, int M, const float* means3D, const float* scales,
+                                const float* rotations, const float* dc, const float* rest,
+                                const float* colors_precomp, const float* cov3D_precomp,
+                                float scale_modifier, const float* viewmatrix, const float* projmatrix,
+                                const float* campos, float tanfovx, float tanfovy, int image_height,
+                                int image_width, const int* radii, const float* cov3D,
+                                const uint8_t* clamped, const float* dL_dmeans2D,
+                                const float* dL_dconic_opacity, const float* dL_dcolors,
+                                float* dL_dmeans3D, float* dL_dcov3D, float* dL_ddc, float* dL_drest,
+                                float* dL_dscales, float* dL_drotations, float* dL_dopacity,
+                                gs_stream_t stream);
+int gs_mark_visible(int P, const float* means3D, const float* viewmatrix, const float* projmatrix,
+                    uint8_t* present, gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
  * Gaussian -> rank routing of the image-distributed step.
  *
  * gs_local2j_ids_bool replaces GetLocal2jIdsBoolCUDA (mode GS_ROUTE_INTERVAL,

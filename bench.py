@@ -16,7 +16,9 @@ fused_ssim forward+backward on config 4's 8 x 3 x 1080 x 1920 image pair.
 `--workload route`: one rank's routing + pack/unpack around the screen-space
 all-to-all, config 3's 8M Gaussians split over four tile-row ranks.
 `--workload full`: the full-image path (GaussianRasterizer.forward + backward,
-and render_simp) on a config's scene.
+and render_simp) on a config's scene.  `--workload ply`: the trained-scene PLY
+layer (records <-> parameter tensors) at config 2's size, plus one file
+save + load timed end to end.
 
 Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
 `roofline` describes the dominant kernel, timed live with HIP events on the
@@ -63,7 +65,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route", "full"], default="step")
+    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route", "full", "ply"], default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
@@ -610,6 +612,102 @@ def run_route(args):
     print(json.dumps(out), flush=True)
 
 
+def _ply_file_round_trip(plyio, t_, dev):
+    import tempfile
+    import torch
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "point_cloud.ply")
+        t0 = time.perf_counter()
+        plyio.save_ply(path, *t_)
+        t1 = time.perf_counter()
+        got = plyio.load_ply(path, 3, device=dev)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        ok = all(bool(torch.equal(a, b)) for a, b in zip(got[:6], t_))
+        size = os.path.getsize(path)
+        file_e2e = {"save_s": round(t1 - t0, 3), "load_s": round(t2 - t1, 3), "file_bytes": size,
+                    "save_GBs": round(size / (t1 - t0) / 1e9, 2), "load_GBs": round(size / (t2 - t1) / 1e9, 2),
+                    "round_trip_exact": ok}
+        del got
+    return file_e2e
+
+
+def run_ply(args):
+    """The trained-scene PLY layer at config 2's size (6M SH-3 Gaussians, 62
+    float32 properties per vertex record): one step = gs_ply_unpack of the
+    records resident in HBM into the six parameter tensors (load_ply's device
+    part) + gs_ply_pack of the tensors back into records (save_ply's device
+    part).  Outside the timed region one save_ply + load_ply through a file
+    under the temp directory is timed end to end (file system and PCIe
+    included)."""
+    import tempfile
+    import torch
+    from blitzgs_amd import plyio
+    P, n = 6_000_000, 62
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    rec = torch.randn((P, n), device=dev, generator=g)
+    names = plyio.construct_list_of_attributes(torch.empty(0, 1, 3), torch.empty(0, 15, 3), torch.empty(0, 3),
+                                               torch.empty(0, 4))
+    idx = {nm: i for i, nm in enumerate(names)}
+    cm = [[0, 1, 2], [6, 7, 8], [idx["f_rest_{}".format(c * 15 + k)] for k in range(15) for c in range(3)], [54],
+          [55, 56, 57], [58, 59, 60, 61]]
+    shapes = [(3,), (1, 3), (15, 3), (1,), (3,), (4,)]
+    state = {}
+
+    def step():
+        t = plyio.unpack_records(rec, cm, shapes)
+        state["rec"], _ = plyio.pack_records(*t)
+
+    ms, kt, _ = timed(step, args.steps, args.warmup)
+    per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+    avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
+    # algorithmic bytes per launch: all 62 record columns one way, the 59
+    # parameter columns (no normals) the other way
+    alg = P * (n + 59) * 4
+    dom = max(("ply_unpack_kernel", "ply_pack_kernel"), key=lambda k: avg_launch.get(k, 0.0))
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_ply_config2.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get(dom)
+        except (OSError, ValueError):
+            traffic = None
+    roofline = roofline_of(dom, alg, avg_launch.get(dom, float("nan")), traffic)
+    roofline["note"] = "per launch: {} B read + {} B written ({} Gaussians)".format(
+        *((P * n * 4, P * 59 * 4) if dom == "ply_unpack_kernel" else (P * 59 * 4, P * n * 4)), P)
+    t_ = plyio.unpack_records(rec, cm, shapes)
+    torch.cuda.synchronize()
+    file_e2e = {}
+    try:
+        file_e2e = _ply_file_round_trip(plyio, t_, dev)
+    except OSError as e:      # no room for the 1.5 GB file: report, keep the kernel line
+        file_e2e = {"error": str(e)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import o_ply
+        m = 1_000_000
+        h = [a[:m].cpu().numpy() for a in t_]
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "cpu.ply")
+            t0 = time.perf_counter()
+            o_ply.save_ply(path, *h)
+            o_ply.load_ply(path, 3)
+            dt = time.perf_counter() - t0
+        cpu = {"value": round(m / dt, 1), "unit": "Gaussians/s", "cores": 1, "kind": "port",
+               "sample": "numpy restatement of the reference's save_ply + load_ply (file I/O included) on the "
+                         "first {} of {} Gaussians; {:.0f} ms; compare with file_e2e".format(m, P, dt * 1e3)}
+    out = header(args, "PLY record <-> parameter tensors Gaussians/s (unpack + pack, 6M SH3 in HBM)",
+                 P / (ms * 1e-3), "Gaussians/s", ms, "f32",
+                 "config2-size PLY layer: {} Gaussians x {} properties".format(P, n),
+                 {"gaussians": P, "properties": n})
+    out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
+    out["file_e2e"] = file_e2e
+    out["roofline"] = roofline
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -626,7 +724,7 @@ def main():
         sys.exit(1)
     _lib.load()
     {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam, "route": run_route,
-     "full": run_full}[args.workload](args)
+     "full": run_full, "ply": run_ply}[args.workload](args)
 
 
 if __name__ == "__main__":

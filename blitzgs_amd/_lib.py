@@ -24,6 +24,11 @@ class RowField(C.Structure):
                 ("width", C.c_int32), ("src_type", C.c_int32), ("dst_type", C.c_int32)]
 
 
+class PlyTensor(C.Structure):
+    """gs_ply_tensor (include/blitzgs_amd.h)."""
+    _fields_ = [("ptr", C.c_void_p), ("width", C.c_int32), ("type", C.c_int32)]
+
+
 class AdamGroup(C.Structure):
     """gs_adam_group (include/blitzgs_amd.h)."""
     _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("exp_avg", C.c_void_p), ("exp_avg_sq", C.c_void_p),
@@ -65,6 +70,8 @@ _SIGS = {
     "gs_local2j_count": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c, _c, _c]),
     "gs_local2j_write": (_i, [_i, _i, _i, _i, _i, _c, _c, _c, _i, _c, _c, _i64, _c]),
     "gs_move_rows": (_i, [_i64, _c, _i64, _c, _i64, _i, C.POINTER(RowField), _i, _c]),
+    "gs_ply_unpack": (_i, [_i64, _c, C.c_int32, C.c_int32, C.POINTER(PlyTensor), C.POINTER(C.c_int32), _c]),
+    "gs_ply_pack": (_i, [_i64, C.c_int32, C.POINTER(PlyTensor), C.POINTER(C.c_int32), C.c_int32, _c, _c]),
     "gs_diag_math": (_i, [_i, _i, _c, _c, _c]),
     "gs_timing_enable": (_i, [_i]),
     "gs_timing_reset": (_i, []),

@@ -18,7 +18,8 @@
  *     owned by the caller (the Python layer allocates them as torch uint8
  *     tensors, as the reference keeps its geom/binning/img buffers).
  *
- * Reference interfaces replaced (paths under /root/reference/submodule):
+ * Reference interfaces replaced (paths under /root/reference/submodule, except
+ *   the scene/ one, which is under /root/reference):
  *   diff-gaussian-rasterization_f/rasterize_points.cu:834-923  PreprocessGaussiansCUDA
  *   diff-gaussian-rasterization_f/rasterize_points.cu:926-1029 PreprocessGaussiansBackwardCUDA
  *   diff-gaussian-rasterization_r/rasterize_points.cu:273-361  RenderGaussiansCUDA
@@ -29,6 +30,7 @@
  *   diff-gaussian-rasterization_f/rasterize_points.cu:258-289  GetLocal2jIdsBoolCUDA
  *   diff-gaussian-rasterization_f/rasterize_points.cu:337-367  GetLocal2jIdsBoolAdjustMode6CUDA
  *   diff-gaussian-rasterization_f/rasterize_points.cu:807-832  adamUpdate
+ *   scene/gaussian_model.py:434-575 (save_ply / load_ply record layout)  gs_ply_pack / gs_ply_unpack
  */
 #ifndef BLITZGS_AMD_H
 #define BLITZGS_AMD_H
@@ -331,6 +333,38 @@ typedef struct gs_row_field {
 int gs_move_rows(int64_t n_rows, const int64_t* src_rows, int64_t n_src_rows, const int64_t* dst_rows,
                  int64_t n_dst_rows, int n_fields, const gs_row_field* fields, int accumulate,
                  gs_stream_t stream);
+
+/* ------------------------------------------------------------------------ *
+ * PLY vertex records <-> Gaussian parameter tensors.  Replaces the record
+ * assembly of save_ply and the per-property reads of load_ply
+ * (scene/gaussian_model.py:434-446 construct_list_of_attributes, :447-520
+ * save_ply, :522-575 load_ply); the file bytes themselves are read and
+ * written by the host (binary little-endian 'vertex' element).
+ *   records: (P, rec_cols) float32 device array, one PLY vertex per row,
+ *     16-byte aligned for the vectorised path.
+ *   tensors: up to 8 row-major (P, width) device tensors, float32 or int8.
+ *   colmap: HOST array, one entry per tensor column (tensors concatenated in
+ *     the order given): the record column that tensor column is read from
+ *     (unpack) or written to (pack).
+ * gs_ply_unpack fills the tensors (int8 tensors take numpy's astype(int8)
+ * of the float: truncation, low byte).  gs_ply_pack writes every record
+ * column: the mapped ones from their tensor column (int8 as float), the
+ * others as 0 (the zero normals); two tensor columns may not map to one
+ * record column.  rec_cols <= 120, at most 120 tensor columns.
+ * ------------------------------------------------------------------------ */
+#define GS_PLY_F32 0
+#define GS_PLY_I8 1
+
+typedef struct gs_ply_tensor {
+    void* ptr;
+    int32_t width;
+    int32_t type;   /* GS_PLY_F32 or GS_PLY_I8 */
+} gs_ply_tensor;
+
+int gs_ply_unpack(int64_t P, const float* records, int32_t rec_cols, int32_t n_tensors,
+                  const gs_ply_tensor* tensors, const int32_t* colmap, gs_stream_t stream);
+int gs_ply_pack(int64_t P, int32_t n_tensors, const gs_ply_tensor* tensors, const int32_t* colmap,
+                int32_t rec_cols, float* records, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Diagnostics (no counterpart in the reference): evaluate the device exp / log

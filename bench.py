@@ -432,8 +432,8 @@ def run_full(args):
     rasterizer of diff-gaussian-rasterization_f) forward + backward through
     autograd on a scene config (default config 2): preprocess with SH, the
     tile-culled binning, the blend with accum_max_count, then dL/dimage ~ N(0,1)
-    through the render and preprocess backward; plus one render_simp per step
-    reported separately (the pruning steps' importance pass)."""
+    through the render and preprocess backward; plus render_simp (the pruning
+    steps' importance pass) and render_depth timed separately."""
     import torch
     from blitzgs_amd import synth
     from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
@@ -476,6 +476,13 @@ def run_full(args):
                             rotations=params["rotations"])
 
     ms_simp, kt_simp, _ = timed(simp, args.steps, args.warmup)
+
+    def depth():
+        ras.render_depth(means3D=params["means3D"], means2D=means2D, opacities=params["opacities"],
+                         culling=culling, dc=params["dc"], shs=params["rest"], scales=params["scales"],
+                         rotations=params["rotations"])
+
+    ms_depth, kt_depth, _ = timed(depth, args.steps, args.warmup)
     P_vis = int((info["radii"] > 0).sum().item())
     per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
     avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
@@ -516,6 +523,8 @@ def run_full(args):
     out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
     out["render_simp_ms"] = round(ms_simp, 4)
     out["render_simp_stages_ms"] = {k: round(v[0] / max(1, args.steps), 4) for k, v in kt_simp.items()}
+    out["render_depth_ms"] = round(ms_depth, 4)
+    out["render_depth_stages_ms"] = {k: round(v[0] / max(1, args.steps), 4) for k, v in kt_depth.items()}
     out["roofline"] = roofline
     out["cpu_baseline"] = cpu
     out["config"]["instances"] = R

@@ -61,6 +61,7 @@ _SIGS = {
                                         _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_render_full_count": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, C.POINTER(_i64), _c]),
     "gs_render_full_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_full_depth": (_i, [_i, _i64, _i, _i] + [_c] * 20 + [_c]),
     "gs_render_full_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward_full": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i, _c,
                                          _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),

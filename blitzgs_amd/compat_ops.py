@@ -8,6 +8,7 @@ diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
   render_gaussians_backward       _r/rasterize_points.cu:363-436
   rasterize_gaussians             _f/rasterize_points.cu:370-475
   rasterize_gaussians_simp        _f/rasterize_points.cu:477-583
+  rasterize_gaussians_depth       _f/rasterize_points.cu:588-690
   rasterize_gaussians_backward    _f/rasterize_points.cu:697-783
   mark_visible                    _f/rasterize_points.cu:785-805
   get_local2j_ids_bool            _f/rasterize_points.cu:258-289
@@ -15,8 +16,8 @@ diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
   adamUpdate                      _f/rasterize_points.cu:807-832
 Same positional arguments and return tuples; `args` is the reference's
 cuda_args dict (its "stats_collector" entry receives forward_render_time /
-backward_render_time in ms).  rasterize_gaussians_depth (no caller in BlitzGS)
-and the image-tile utilities of the multi-GPU path are not implemented.
+backward_render_time in ms).  The image-tile utilities of the multi-GPU path
+are not implemented.
 """
 import torch
 
@@ -92,4 +93,4 @@ from .fullpath import C_rasterize_gaussians_backward as rasterize_gaussians_back
 from .fullpath import C_rasterize_gaussians_simp as rasterize_gaussians_simp  # noqa: E402,F401
 from .fullpath import mark_visible  # noqa: E402,F401
 
-rasterize_gaussians_depth = _not_here("rasterize_gaussians_depth")
+from .fullpath import C_rasterize_gaussians_depth as rasterize_gaussians_depth  # noqa: E402,F401

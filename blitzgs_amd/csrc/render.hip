@@ -1022,6 +1022,230 @@ __global__ __launch_bounds__(256) void zero_i32_kernel(int n, int32_t* __restric
     if (i < n) p[i] = 0;
 }
 
+// ---------------------------------------------------------------- depth render
+//
+// render_depth of the full-image path (reference: _f/cuda_rasterizer/forward.cu:616-835,
+// host rasterizer_impl.cu:671-847): the forward blend plus, per pixel, the
+// intersection of the camera ray with each blended Gaussian's 3-sigma
+// ellipsoid; the Gaussian of the largest blend weight alpha * T gives the
+// pixel's depth, ray discriminant, hit point and id.  The reference's rules,
+// kept as they are:
+//   * the pixel ray runs from campos to inv(projmatrix) * (ndc.x * 1.0000001,
+//     ndc.y * 1.0000001, z_far, 1) taken WITHOUT the division by w;
+//   * the quaternion is used unnormalised; the ellipsoid radii are 3 * scale;
+//   * a Gaussian whose ray parameter gives depth < 0 still adds its colour but
+//     leaves T (and the depth state) unchanged;
+//   * the per-pixel contributor count stays 0.
+// Everything a Gaussian contributes independently of the pixel (rotation,
+// ray origin in its frame, the constant term of the quadratic) is computed
+// once when it is staged; the inverse projection is computed in double by
+// every wave (64 lanes, ~200 double operations) from the device matrix.
+constexpr int BLEND_DEPTH = 3;
+
+struct DepthIO {
+    const float* means3D;
+    const float* scales;
+    const float* rotations;
+    const float* projmatrix;   // (4,4) as the settings tensor: column-major for the kernels
+    const float* campos;
+    float* out_pts;            // (3,H,W)
+    float* out_depth;          // (1,H,W)
+    float* accum_alpha;        // (1,H,W): final T
+    int32_t* gidx;             // (1,H,W)
+    float* discriminants;      // (1,H,W)
+};
+
+// Inverse of the 4x4 matrix whose element (r, c) is m[4c + r], by the
+// expansion in complementary 2x2 minors, in double; written the same way.
+__device__ void inv4_colmajor(const float* __restrict__ mf, float* __restrict__ out)
+{
+    double a[4][4];
+    for (int c = 0; c < 4; c++)
+        for (int r = 0; r < 4; r++) a[r][c] = (double)mf[4 * c + r];
+    const double s0 = a[0][0] * a[1][1] - a[1][0] * a[0][1];
+    const double s1 = a[0][0] * a[1][2] - a[1][0] * a[0][2];
+    const double s2 = a[0][0] * a[1][3] - a[1][0] * a[0][3];
+    const double s3 = a[0][1] * a[1][2] - a[1][1] * a[0][2];
+    const double s4 = a[0][1] * a[1][3] - a[1][1] * a[0][3];
+    const double s5 = a[0][2] * a[1][3] - a[1][2] * a[0][3];
+    const double c5 = a[2][2] * a[3][3] - a[3][2] * a[2][3];
+    const double c4 = a[2][1] * a[3][3] - a[3][1] * a[2][3];
+    const double c3 = a[2][1] * a[3][2] - a[3][1] * a[2][2];
+    const double c2 = a[2][0] * a[3][3] - a[3][0] * a[2][3];
+    const double c1 = a[2][0] * a[3][2] - a[3][0] * a[2][2];
+    const double c0 = a[2][0] * a[3][1] - a[3][0] * a[2][1];
+    const double det = s0 * c5 - s1 * c4 + s2 * c3 + s3 * c2 - s4 * c1 + s5 * c0;
+    const double id = 1.0 / det;
+    double b[4][4];
+    b[0][0] = (a[1][1] * c5 - a[1][2] * c4 + a[1][3] * c3) * id;
+    b[0][1] = (-a[0][1] * c5 + a[0][2] * c4 - a[0][3] * c3) * id;
+    b[0][2] = (a[3][1] * s5 - a[3][2] * s4 + a[3][3] * s3) * id;
+    b[0][3] = (-a[2][1] * s5 + a[2][2] * s4 - a[2][3] * s3) * id;
+    b[1][0] = (-a[1][0] * c5 + a[1][2] * c2 - a[1][3] * c1) * id;
+    b[1][1] = (a[0][0] * c5 - a[0][2] * c2 + a[0][3] * c1) * id;
+    b[1][2] = (-a[3][0] * s5 + a[3][2] * s2 - a[3][3] * s1) * id;
+    b[1][3] = (a[2][0] * s5 - a[2][2] * s2 + a[2][3] * s1) * id;
+    b[2][0] = (a[1][0] * c4 - a[1][1] * c2 + a[1][3] * c0) * id;
+    b[2][1] = (-a[0][0] * c4 + a[0][1] * c2 - a[0][3] * c0) * id;
+    b[2][2] = (a[3][0] * s4 - a[3][1] * s2 + a[3][3] * s0) * id;
+    b[2][3] = (-a[2][0] * s4 + a[2][1] * s2 - a[2][3] * s0) * id;
+    b[3][0] = (-a[1][0] * c3 + a[1][1] * c1 - a[1][2] * c0) * id;
+    b[3][1] = (a[0][0] * c3 - a[0][1] * c1 + a[0][2] * c0) * id;
+    b[3][2] = (-a[3][0] * s3 + a[3][1] * s1 - a[3][2] * s0) * id;
+    b[3][3] = (a[2][0] * s3 - a[2][1] * s1 + a[2][2] * s0) * id;
+    for (int c = 0; c < 4; c++)
+        for (int r = 0; r < 4; r++) out[4 * c + r] = (float)b[r][c];
+}
+
+// staging slots of one batch for the depth render
+struct DepthStage {
+    float4 a[64];    // x, y, -a/2, -b
+    float4 b[64];    // -c/2, opacity, r, g
+    float4 c[64];    // blue, Gaussian id (bits), 0, 0
+    float4 r0[64];   // rotation entries m0..m3 (glm column order)
+    float4 r1[64];   // m4..m7
+    float4 r2[64];   // m8, ray origin in the Gaussian's frame
+    float4 s[64];    // 3 * scale, constant term of the quadratic
+};
+
+// glm::mat3(m0..m8) * v: m0..m2 is the first column
+__device__ __forceinline__ float3 rot_apply(const float4& r0, const float4& r1, const float4& r2, float x, float y,
+                                            float z)
+{
+    return make_float3(r0.x * x + r0.w * y + r1.z * z, r0.y * x + r1.x * y + r1.w * z, r0.z * x + r1.y * y + r2.x * z);
+}
+
+__global__ __launch_bounds__(64) void render_depth_kernel(int W, int H, unsigned gx, unsigned gy, unsigned sgx,
+                                                          unsigned NS, const uint2* __restrict__ ranges,
+                                                          const uint32_t* __restrict__ clist,
+                                                          const float4* __restrict__ rec, const float* __restrict__ bg,
+                                                          FwdOut O, DepthIO D)
+{
+    unsigned tile, quad, tx, ty;
+    if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
+    const int lane = threadIdx.x;
+    const int qx = (int)tx * 16 + (int)(quad & 1u) * 8, qy = (int)ty * 16 + (int)(quad >> 1) * 8;
+    const int px = qx + (lane & 7), py = qy + (lane >> 3);
+    const bool inside = px < W && py < H;
+    const size_t pid = (size_t)py * W + px;
+    const size_t HW = (size_t)H * W;
+    __shared__ DepthStage st;
+
+    // the pixel's ray
+    float inv[16];
+    inv4_colmajor(D.projmatrix, inv);
+    const float cx = D.campos[0], cy = D.campos[1], cz = D.campos[2];
+    const float pxf = (float)px, pyf = (float)py;
+    const float ndx = (2.0f * pxf + 1.0f) / (float)W - 1.0f;
+    const float ndy = (2.0f * pyf + 1.0f) / (float)H - 1.0f;
+    const float hx = (float)((double)ndx * 1.0000001), hy = (float)((double)ndy * 1.0000001);
+    const float hz = (float)((100.0 - 100.0 * 0.01) / (100.0 - 0.01));
+    const float ox = inv[0] * hx + inv[4] * hy + inv[8] * hz + inv[12];
+    const float oy = inv[1] * hx + inv[5] * hy + inv[9] * hz + inv[13];
+    const float oz = inv[2] * hx + inv[6] * hy + inv[10] * hz + inv[14];
+    const float rdx = ox - cx, rdy = oy - cy, rdz = oz - cz;
+    const float len = sqrtf(rdx * rdx + rdy * rdy + rdz * rdz);
+    const float il = 1.0f / len;
+    const float nx = rdx * il, ny = rdy * il, nz = rdz * il;
+
+    const uint2 range = ranges[tile];
+    const int n = (int)(range.y - range.x);
+    const uint32_t* list = clist + range.x;
+    const float qx0 = (float)qx, qy0 = (float)qy;
+    const float alpha_min = 1.0f / 255.0f;
+    float T_ = 1.0f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
+    float wmax = 0.f, dmax = 0.f, discmax = 0.f, prx = 0.f, pry = 0.f, prz = 0.f;
+    uint32_t imax = 0u;
+    bool done = !inside;
+
+    for (int base = 0; base < n; base += 64) {
+        if (gs::ballot(!done) == 0) break;
+        const int k = base + lane;
+        Rec r{};
+        if (k < n) r = load_rec<true>(rec, list[k]);
+        const bool keep = k < n && rec_may_touch(r, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
+        const uint64_t km = gs::ballot(keep);
+        if (keep) {
+            const int slot = gs::rank_below(km);
+            st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
+            st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
+            st.c[slot] = make_float4(r.q2.x, __uint_as_float(r.gid), 0.f, 0.f);
+            const uint32_t g = r.gid;
+            const float4 q = reinterpret_cast<const float4*>(D.rotations)[g];
+            const float qr = q.x, qxx = q.y, qy_ = q.z, qz = q.w;
+            const float m0 = 1.f - 2.f * (qy_ * qy_ + qz * qz), m1 = 2.f * (qxx * qy_ - qr * qz);
+            const float m2 = 2.f * (qxx * qz + qr * qy_), m3 = 2.f * (qxx * qy_ + qr * qz);
+            const float m4 = 1.f - 2.f * (qxx * qxx + qz * qz), m5 = 2.f * (qy_ * qz - qr * qxx);
+            const float m6 = 2.f * (qxx * qz - qr * qy_), m7 = 2.f * (qy_ * qz + qr * qxx);
+            const float m8 = 1.f - 2.f * (qxx * qxx + qy_ * qy_);
+            const float4 R0 = make_float4(m0, m1, m2, m3), R1 = make_float4(m4, m5, m6, m7);
+            const float tx_ = cx - D.means3D[3 * (size_t)g], ty_ = cy - D.means3D[3 * (size_t)g + 1],
+                        tz_ = cz - D.means3D[3 * (size_t)g + 2];
+            const float4 R2p = make_float4(m8, 0.f, 0.f, 0.f);
+            const float3 ro = rot_apply(R0, R1, R2p, tx_, ty_, tz_);
+            const float sx = D.scales[3 * (size_t)g] * 3.0f, sy = D.scales[3 * (size_t)g + 1] * 3.0f,
+                        sz = D.scales[3 * (size_t)g + 2] * 3.0f;
+            const float cc = ro.x / sx * ro.x / sx + ro.y / sy * ro.y / sy + ro.z / sz * ro.z / sz - 1.0f;
+            st.r0[slot] = R0;
+            st.r1[slot] = R1;
+            st.r2[slot] = make_float4(m8, ro.x, ro.y, ro.z);
+            st.s[slot] = make_float4(sx, sy, sz, cc);
+        }
+        __syncthreads();
+        const int cnt = (int)__builtin_popcountll(km);
+        for (int j = 0; j < cnt; j++) {
+            if (gs::ballot(!done) == 0) break;
+            if (done) continue;
+            const float4 A = st.a[j], B = st.b[j], Cc = st.c[j];
+            const float dx = A.x - pxf, dy = A.y - pyf;
+            const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
+            if (power > 0.0f) continue;
+            const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
+            if (alpha < alpha_min) continue;
+            const float test_T = T_ * (1.0f - alpha);
+            if (test_T < 0.0001f) { done = true; continue; }
+            C0 = __builtin_fmaf(B.z * alpha, T_, C0);
+            C1 = __builtin_fmaf(B.w * alpha, T_, C1);
+            C2 = __builtin_fmaf(Cc.x * alpha, T_, C2);
+            const float4 R0 = st.r0[j], R1 = st.r1[j], R2 = st.r2[j], S = st.s[j];
+            const float3 rd = rot_apply(R0, R1, R2, nx, ny, nz);
+            const float a = rd.x / S.x * rd.x / S.x + rd.y / S.y * rd.y / S.y + rd.z / S.z * rd.z / S.z;
+            const float b = 2.0f * (rd.x / S.x * R2.y / S.x + rd.y / S.y * R2.z / S.y + rd.z / S.z * R2.w / S.z);
+            const float disc = b * b - 4.0f * a * S.w;
+            const float tpar = -b / 2.0f / a;
+            const float depth = tpar / len;
+            if (depth < 0.0f) continue;
+            const float wgt = alpha * T_;
+            if (wmax < wgt) {
+                wmax = wgt;
+                dmax = depth;
+                discmax = disc;
+                imax = __float_as_uint(Cc.y);
+                prx = cx + tpar * nx;
+                pry = cy + tpar * ny;
+                prz = cz + tpar * nz;
+            }
+            T_ = test_T;
+        }
+        __syncthreads();
+    }
+
+    if (inside) {
+        O.final_T[pid] = T_;
+        O.n_contrib_px[pid] = 0u;
+        O.out_color[pid] = __builtin_fmaf(T_, bg[0], C0);
+        O.out_color[HW + pid] = __builtin_fmaf(T_, bg[1], C1);
+        O.out_color[2 * HW + pid] = __builtin_fmaf(T_, bg[2], C2);
+        D.out_pts[pid] = prx;
+        D.out_pts[HW + pid] = pry;
+        D.out_pts[2 * HW + pid] = prz;
+        D.out_depth[pid] = dmax;
+        D.accum_alpha[pid] = T_;
+        D.discriminants[pid] = discmax;
+        D.gidx[pid] = (int32_t)imax;
+    }
+}
+
 // Writes the render backward's outputs for every Gaussian from its
 // accumulator (listed Gaussians, whose accumulator is then cleared for the
 // next backward) or zeros; one thread per Gaussian.
@@ -1276,7 +1500,7 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
 int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                         const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
                         const uint8_t* compute_locally, const float* rects, void* geom, void* binning, void* img,
-                        FwdOut O, int32_t* n_render, hipStream_t stream)
+                        FwdOut O, int32_t* n_render, hipStream_t stream, const DepthIO* depth_io = nullptr)
 {
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0,
@@ -1382,10 +1606,17 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         GS_TIMED("render_fwd_kernel", stream,
                  hipLaunchKernelGGL(render_fwd_kernel<BLEND_FULL>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                     NS, ranges, clist, recs, compute_locally, bg, O));
-    } else {
+    } else if (mode == BLEND_SIMP) {
         GS_TIMED("render_fwd_kernel", stream,
                  hipLaunchKernelGGL(render_fwd_kernel<BLEND_SIMP>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                     NS, ranges, clist, recs, compute_locally, bg, O));
+    } else {
+        GS_REQUIRE(mode == BLEND_DEPTH && depth_io != nullptr, "bad blend mode %d", mode);
+        GS_TIMED("render_depth_kernel", stream,
+                 hipLaunchKernelGGL(render_depth_kernel, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS,
+                                    ranges, clist, recs, bg, O, *depth_io));
+        GS_LAUNCH_CHECK("render_depth_kernel");
+        return GS_OK;
     }
     GS_LAUNCH_CHECK("render_fwd_kernel");
     return GS_OK;
@@ -1505,6 +1736,27 @@ extern "C" int gs_render_full_forward(int P, int64_t R, int W, int H, const floa
     O.accum_weights_count = accum_weights_count;
     return render_forward_impl(accum_weights != nullptr ? BLEND_SIMP : BLEND_FULL, P, R, W, H, bg, means2D, depths,
                                radii, conic_opacity, colors, nullptr, rects, geom, binning, img, O, nullptr, stream);
+}
+
+extern "C" int gs_render_full_depth(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                    const float* depths, const int* radii, const float* rects,
+                                    const float* conic_opacity, const float* colors, const float* means3D,
+                                    const float* scales, const float* rotations, const float* projmatrix,
+                                    const float* campos, void* geom, void* binning, void* img, float* out_color,
+                                    float* out_pts, float* out_depth, float* accum_alpha, int32_t* gidx,
+                                    float* discriminants, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(out_color && out_pts && out_depth && accum_alpha && gidx && discriminants,
+               "every output must be non-null");
+    GS_REQUIRE(projmatrix && campos, "projmatrix and campos must be non-null");
+    GS_REQUIRE(P == 0 || (means3D && scales && rotations), "means3D, scales and rotations must be non-null");
+    GS_REQUIRE(((uintptr_t)rotations & 15) == 0, "rotations must be 16-byte aligned");
+    FwdOut O{};
+    O.out_color = out_color;
+    DepthIO D{means3D, scales, rotations, projmatrix, campos, out_pts, out_depth, accum_alpha, gidx, discriminants};
+    return render_forward_impl(BLEND_DEPTH, P, R, W, H, bg, means2D, depths, radii, conic_opacity, colors, nullptr,
+                               rects, geom, binning, img, O, nullptr, stream, &D);
 }
 
 extern "C" int gs_render_full_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,

@@ -12,7 +12,8 @@ Mirrors BlitzGS submodule/diff-gaussian-rasterization_f:
                                 RasterizeGaussiansBackwardCUDA, markVisible
 Same arguments, return tuples and gradient order.  The work is done by
 libblitzgs_amd.so: gs_preprocess_forward_full, gs_render_full_count /
-gs_render_full_forward (tile-culled binning + blend), gs_render_full_backward,
+gs_render_full_forward (tile-culled binning + blend), gs_render_full_depth,
+gs_render_full_backward,
 gs_preprocess_backward_full, gs_mark_visible.
 
 The reference keeps its intermediate state in four byte buffers
@@ -21,7 +22,8 @@ outputs followed by the render's geometry workspace and a 256-byte header
 (the instance count), binningBuffer and imgBuffer are the render's
 workspaces, and sampleBuffer is empty: the backward replays the blend per
 pixel from the final transmittance instead of from per-bucket samples.
-render_depth (no caller in BlitzGS) is not provided.
+render_depth (no caller in BlitzGS, no backward) runs the same preprocess and
+binning and gs_render_full_depth's blend.
 """
 import torch
 
@@ -106,9 +108,10 @@ def _inputs(rs, means3D, dc, sh, colors_precomp, opacities, scales, rotations, c
                 bg=_f32(rs.bg, dev))
 
 
-def _forward(rs, x, culling, flag_max_count, simp):
+def _forward(rs, x, culling, flag_max_count, simp, depth=False):
     """Preprocess + binning + blend.  Returns (color, radii, accum_max_count,
-    accum_weights, accum_weights_count, geom, binning, img, R)."""
+    accum_weights, accum_weights_count, geom, binning, img, R); with depth the
+    third item is the dict of render_depth's per-pixel outputs."""
     dev, P = x["dev"], x["P"]
     H, W = int(rs.image_height), int(rs.image_width)
     lib = _lib.load()
@@ -144,6 +147,19 @@ def _forward(rs, x, culling, flag_max_count, simp):
     binning = torch.empty(int(lib.gs_render_binning_bytes(R)), dtype=torch.uint8, device=dev)
     img = torch.empty(int(lib.gs_render_img_bytes(W, H)), dtype=torch.uint8, device=dev)
     colors = x["colors_precomp"] if x["colors_precomp"] is not None else g["rgb"]
+    if depth:
+        d = dict(out_pts=torch.empty((3, H, W), dtype=torch.float32, device=dev),
+                 depth=torch.empty((1, H, W), dtype=torch.float32, device=dev),
+                 accum_alpha=torch.empty((1, H, W), dtype=torch.float32, device=dev),
+                 gidx=torch.empty((1, H, W), dtype=torch.int32, device=dev),
+                 discriminants=torch.empty((1, H, W), dtype=torch.float32, device=dev))
+        check(lib.gs_render_full_depth(P, R, W, H, ptr(x["bg"]), ptr(g["means2D"]), ptr(g["depths"]), ptr(radii),
+                                       ptr(g["rects"]), ptr(g["conic"]), ptr(colors), ptr(x["means3D"]),
+                                       ptr(x["scales"]), ptr(x["rotations"]), ptr(x["proj"]), ptr(x["campos"]),
+                                       ptr(rws), ptr(binning), ptr(img), ptr(color), ptr(d["out_pts"]),
+                                       ptr(d["depth"]), ptr(d["accum_alpha"]), ptr(d["gidx"]),
+                                       ptr(d["discriminants"]), s), "gs_render_full_depth")
+        return color, radii, d, None, None, geom, binning, img, R
     check(lib.gs_render_full_forward(P, R, W, H, ptr(x["bg"]), ptr(g["means2D"]), ptr(g["depths"]), ptr(radii),
                                      ptr(g["rects"]), ptr(g["conic"]), ptr(colors), ptr(rws), ptr(binning), ptr(img),
                                      ptr(color), ptr(amc) if (flag_max_count or simp) else None, ptr(aw), ptr(awc),
@@ -232,6 +248,21 @@ class _RasterizeGaussians(torch.autograd.Function):
                 g_cov if x["cov3D_precomp"] is not None else None, None, None, None)
 
 
+    @staticmethod
+    def render_simp(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, culling,
+                    raster_settings):
+        """_f __init__.py:476-511."""
+        return rasterize_gaussians_simp(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations,
+                                        cov3Ds_precomp, culling, raster_settings)
+
+    @staticmethod
+    def render_depth(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, culling,
+                     raster_settings):
+        """_f __init__.py:525-577."""
+        return rasterize_gaussians_depth(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations,
+                                         cov3Ds_precomp, culling, raster_settings)
+
+
 def rasterize_gaussians(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp,
                         flag_max_count, culling, raster_settings):
     return _RasterizeGaussians.apply(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations,
@@ -248,8 +279,25 @@ def rasterize_gaussians_simp(means3D, means2D, dc, sh, colors_precomp, opacities
     return color, radii, aw, awc, amc
 
 
-def rasterize_gaussians_depth(*args, **kwargs):
-    raise NotImplementedError("render_depth (no caller in BlitzGS) is not provided")
+def _depth_inputs(raster_settings, means3D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp):
+    x = _inputs(raster_settings, means3D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp)
+    if x["scales"] is None or x["rotations"] is None:
+        # the depth kernel reads every blended Gaussian's scale and rotation
+        raise RuntimeError("render_depth needs scales and rotations (it intersects the camera ray with each "
+                           "Gaussian's ellipsoid)")
+    return x
+
+
+@torch.no_grad()
+def rasterize_gaussians_depth(means3D, means2D, dc, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp,
+                              culling, raster_settings):
+    """_RasterizeGaussians.render_depth (_f __init__.py:525-577): returns the
+    dict {render, out_pts, rendered_depth, discriminants, gidx, accum_alpha}."""
+    x = _depth_inputs(raster_settings, means3D, dc, sh, colors_precomp, opacities, scales, rotations,
+                      cov3Ds_precomp)
+    color, _, d, _, _, _, _, _, _ = _forward(raster_settings, x, culling, False, False, depth=True)
+    return {"render": color, "out_pts": d["out_pts"], "rendered_depth": d["depth"],
+            "discriminants": d["discriminants"], "gidx": d["gidx"], "accum_alpha": d["accum_alpha"]}
 
 
 @torch.no_grad()
@@ -309,6 +357,22 @@ def C_rasterize_gaussians_backward(background, means3D, radii, colors, scales, r
                 rotations, cov3D_precomp)
     R_ours = int(geomBuffer[:8].view(torch.int64).item())
     return _backward(rs, x, radii, geomBuffer, R_ours, binningBuffer, imageBuffer, dL_dout_color)
+
+
+def C_rasterize_gaussians_depth(background, means3D, colors, opacity, scales, rotations, scale_modifier,
+                                cov3D_precomp, viewmatrix, projmatrix, tan_fovx, tan_fovy, image_height, image_width,
+                                dc, sh, degree, campos, prefiltered, culling, debug):
+    """_C.rasterize_gaussians_depth (rasterize_points.cu:588-690): returns
+    (num_rendered, color, out_pts, depth, accum_alpha, gidx, discriminants,
+    radii, geomBuffer, binningBuffer, imgBuffer)."""
+    rs = _settings(background, scale_modifier, viewmatrix, projmatrix, tan_fovx, tan_fovy, image_height,
+                   image_width, degree, campos, prefiltered, debug)
+    x = _depth_inputs(rs, means3D, dc, sh, colors, opacity, scales, rotations, cov3D_precomp)
+    color, radii, d, _, _, geom, binning, img, R = _forward(rs, x, culling, False, False, depth=True)
+    g = _Geom(x["P"], int(image_width), int(image_height)).views(geom)
+    num_rendered = int(g["tiles"].to(torch.int64).sum().item()) if x["P"] else 0
+    return (num_rendered, color, d["out_pts"], d["depth"], d["accum_alpha"], d["gidx"], d["discriminants"], radii,
+            geom, binning, img)
 
 
 def C_rasterize_gaussians_simp(background, means3D, colors, opacity, scales, rotations, scale_modifier,

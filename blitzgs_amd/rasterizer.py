@@ -363,5 +363,11 @@ class GaussianRasterizer(nn.Module):
         return rasterize_gaussians_simp(means3D, means2D, dc, shs, colors_precomp, opacities, scales, rotations,
                                         cov3D_precomp, culling, self.raster_settings)
 
-    def render_depth(self, *args, **kwargs):
-        raise NotImplementedError("render_depth (no caller in BlitzGS) is not provided")
+    def render_depth(self, means3D, means2D, opacities, culling, dc=None, shs=None, colors_precomp=None, scales=None,
+                     rotations=None, cov3D_precomp=None):
+        """_f __init__.py:773-810: dict of render, out_pts, rendered_depth,
+        discriminants, gidx, accum_alpha (no gradients)."""
+        from .fullpath import rasterize_gaussians_depth
+        self._check_inputs(shs, colors_precomp, scales, rotations, cov3D_precomp)
+        return rasterize_gaussians_depth(means3D, means2D, dc, shs, colors_precomp, opacities, scales, rotations,
+                                         cov3D_precomp, culling, self.raster_settings)

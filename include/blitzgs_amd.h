@@ -227,6 +227,17 @@ int gs_adam_update_groups(int n_groups, const gs_adam_group* groups, int64_t N,
  *   dL_dcov3D (P,6), dL_ddc (P,1,3), dL_drest (P,M,3), dL_dscales (P,3),
  *   dL_drotations (P,4), dL_dopacity (P,1); SH gradients only with SH colours
  *   and M > 0, scale / rotation gradients only without cov3D_precomp.
+ * gs_render_full_depth: render_depth (RasterizeGaussiansDepthCUDA,
+ *   _f/rasterize_points.cu:588-690; Rasterizer::forward_depth,
+ *   rasterizer_impl.cu:671-847; render_depthCUDA, forward.cu:616-835): the
+ *   same binning as gs_render_full_forward, then the blend with, per pixel,
+ *   the camera ray's intersection with each blended Gaussian's 3-sigma
+ *   ellipsoid (means3D (P,3), scales (P,3) activated, rotations (P,4)
+ *   unnormalised, 16-byte aligned; projmatrix (4,4) and campos (3) device
+ *   tensors as in the settings).  Outputs: out_color (3,H,W), out_pts (3,H,W)
+ *   hit point, out_depth (1,H,W), accum_alpha (1,H,W) final T, gidx (1,H,W)
+ *   int32 Gaussian id and discriminants (1,H,W), each from the Gaussian of
+ *   the largest alpha * T (0 where none).  No backward.
  * gs_mark_visible: present (P) uint8 = view-space z > 0.2.
  * ------------------------------------------------------------------------ */
 int gs_preprocess_forward_full(int P, int D, int M, const float* means3D, const float* scales,
@@ -246,6 +257,13 @@ int gs_render_full_forward(int P, int64_t R, int image_width, int image_height, 
                            const float* conic_opacity, const float* colors, void* geom, void* binning,
                            void* img, float* out_color, float* accum_max_count, float* accum_weights,
                            int32_t* accum_weights_count, gs_stream_t stream);
+int gs_render_full_depth(int P, int64_t R, int image_width, int image_height, const float* bg,
+                         const float* means2D, const float* depths, const int* radii, const float* rects,
+                         const float* conic_opacity, const float* colors, const float* means3D,
+                         const float* scales, const float* rotations, const float* projmatrix,
+                         const float* campos, void* geom, void* binning, void* img, float* out_color,
+                         float* out_pts, float* out_depth, float* accum_alpha, int32_t* gidx,
+                         float* discriminants, gs_stream_t stream);
 int gs_render_full_backward(int P, int64_t R, int image_width, int image_height, const float* bg,
                             const float* means2D, const float* conic_opacity, void* geom,
                             const void* binning, const void* img, const float* dL_dpixels,

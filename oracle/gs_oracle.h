@@ -130,6 +130,12 @@ int64_t o_binning_full(int P, int W, int H, const float* means2D, const float* d
 /* renderCUDA / render_simpCUDA of the full path (forward.cu:291-607).
  * accum_weights / accum_weights_count NULL for renderCUDA.  Accumulators
  * are added to (caller zeroes them). */
+void o_inv4_colmajor(const float* m, float* out);
+void o_render_depth_full(int W, int H, const float* bg, const float* means2D, const float* conic_opacity,
+                         const float* colors, const uint32_t* ranges, const uint32_t* point_list,
+                         const float* means3D, const float* scales, const float* rotations, const float* projmatrix,
+                         const float* campos, float* out_color, float* out_pts, float* out_depth, float* accum_alpha,
+                         int32_t* gidx, float* discriminants);
 void o_render_fwd_full(int P, int W, int H, const float* bg, const float* means2D, const float* conic_opacity,
                        const float* colors, const uint32_t* ranges, const uint32_t* point_list, int flag_max_count,
                        float* out_color, float* final_T, uint32_t* n_contrib, uint32_t* max_contrib,

@@ -537,6 +537,160 @@ void o_render_fwd_full(int P, int W, int H, const float* bg, const float* means2
     }
 }
 
+/* Inverse of the 4x4 matrix whose element (r, c) is m[4c + r] (the layout
+ * glm::make_mat4x4 reads), by the expansion in complementary 2x2 minors, in
+ * double, rounded to float in the same layout.  Stands for glm::inverse in
+ * _f/cuda_rasterizer/forward.cu:686-688 (which inverts in float). */
+void o_inv4_colmajor(const float* mf, float* out)
+{
+    double a[4][4], b[4][4];
+    for (int c = 0; c < 4; c++)
+        for (int r = 0; r < 4; r++) a[r][c] = (double)mf[4 * c + r];
+    const double s0 = a[0][0] * a[1][1] - a[1][0] * a[0][1];
+    const double s1 = a[0][0] * a[1][2] - a[1][0] * a[0][2];
+    const double s2 = a[0][0] * a[1][3] - a[1][0] * a[0][3];
+    const double s3 = a[0][1] * a[1][2] - a[1][1] * a[0][2];
+    const double s4 = a[0][1] * a[1][3] - a[1][1] * a[0][3];
+    const double s5 = a[0][2] * a[1][3] - a[1][2] * a[0][3];
+    const double c5 = a[2][2] * a[3][3] - a[3][2] * a[2][3];
+    const double c4 = a[2][1] * a[3][3] - a[3][1] * a[2][3];
+    const double c3 = a[2][1] * a[3][2] - a[3][1] * a[2][2];
+    const double c2 = a[2][0] * a[3][3] - a[3][0] * a[2][3];
+    const double c1 = a[2][0] * a[3][2] - a[3][0] * a[2][2];
+    const double c0 = a[2][0] * a[3][1] - a[3][0] * a[2][1];
+    const double det = s0 * c5 - s1 * c4 + s2 * c3 + s3 * c2 - s4 * c1 + s5 * c0;
+    const double id = 1.0 / det;
+    b[0][0] = (a[1][1] * c5 - a[1][2] * c4 + a[1][3] * c3) * id;
+    b[0][1] = (-a[0][1] * c5 + a[0][2] * c4 - a[0][3] * c3) * id;
+    b[0][2] = (a[3][1] * s5 - a[3][2] * s4 + a[3][3] * s3) * id;
+    b[0][3] = (-a[2][1] * s5 + a[2][2] * s4 - a[2][3] * s3) * id;
+    b[1][0] = (-a[1][0] * c5 + a[1][2] * c2 - a[1][3] * c1) * id;
+    b[1][1] = (a[0][0] * c5 - a[0][2] * c2 + a[0][3] * c1) * id;
+    b[1][2] = (-a[3][0] * s5 + a[3][2] * s2 - a[3][3] * s1) * id;
+    b[1][3] = (a[2][0] * s5 - a[2][2] * s2 + a[2][3] * s1) * id;
+    b[2][0] = (a[1][0] * c4 - a[1][1] * c2 + a[1][3] * c0) * id;
+    b[2][1] = (-a[0][0] * c4 + a[0][1] * c2 - a[0][3] * c0) * id;
+    b[2][2] = (a[3][0] * s4 - a[3][1] * s2 + a[3][3] * s0) * id;
+    b[2][3] = (-a[2][0] * s4 + a[2][1] * s2 - a[2][3] * s0) * id;
+    b[3][0] = (-a[1][0] * c3 + a[1][1] * c1 - a[1][2] * c0) * id;
+    b[3][1] = (a[0][0] * c3 - a[0][1] * c1 + a[0][2] * c0) * id;
+    b[3][2] = (-a[3][0] * s3 + a[3][1] * s1 - a[3][2] * s0) * id;
+    b[3][3] = (a[2][0] * s3 - a[2][1] * s1 + a[2][2] * s0) * id;
+    for (int c = 0; c < 4; c++)
+        for (int r = 0; r < 4; r++) out[4 * c + r] = (float)b[r][c];
+}
+
+/* render_depthCUDA (_f/cuda_rasterizer/forward.cu:616-835): the full-image
+ * blend of the tile-culled list plus, per pixel, the camera ray's
+ * intersection with every blended Gaussian's 3-sigma ellipsoid.
+ *   ray: Pix2ndc (auxiliary.h:46-49), x / y times 1.0000001 in double, z =
+ *        (100 - 100*0.01) / (100 - 0.01); inv(projmatrix) applied as
+ *        transformPoint4x4 (no division by w); direction = that point - campos,
+ *        normalised as glm::normalize (v * (1 / sqrt(dot))) (:686-719)
+ *   per Gaussian: glm::mat3 of the unnormalised quaternion (columns m0..m2,
+ *        m3..m5, m6..m8); ray origin and direction in its frame; s = 3 scale;
+ *        a, b, c of the quadric, discriminant b*b - 4*a*c, t = -b/2/a,
+ *        depth = t / |direction| (:764-801)
+ *   rules: colour is added before the depth test; depth < 0 skips the rest
+ *        (T unchanged); the largest alpha * T picks depth, discriminant, id
+ *        and hit point campos + t * direction; n_contrib stays 0 (:767-823).
+ * Operation order: plain float operations left to right, except the colour
+ * sum fmaf(f * alpha, T, C) and the final colour fmaf(T, bg, C). */
+void o_render_depth_full(int W, int H, const float* bg, const float* means2D, const float* conic_opacity,
+                         const float* colors, const uint32_t* ranges, const uint32_t* point_list,
+                         const float* means3D, const float* scales, const float* rotations, const float* projmatrix,
+                         const float* campos, float* out_color, float* out_pts, float* out_depth, float* accum_alpha,
+                         int32_t* gidx, float* discriminants)
+{
+    const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const int T = gx * gy;
+    const float alpha_min = 1.0f / 255.0f;
+    const size_t HW = (size_t)H * W;
+    float inv[16];
+    o_inv4_colmajor(projmatrix, inv);
+    const float cx = campos[0], cy = campos[1], cz = campos[2];
+    const float hz = (float)((100.0 - 100.0 * 0.01) / (100.0 - 0.01));
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int t = 0; t < T; t++) {
+        const int tx = t % gx, ty = t / gx;
+        const int x0 = tx * OT, y0 = ty * OT;
+        const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
+        const uint32_t rs = ranges[2 * t], re = ranges[2 * t + 1];
+        for (int y = y0; y < y1; y++)
+            for (int x = x0; x < x1; x++) {
+                const float px = (float)x, py = (float)y;
+                const float ndx = (2.0f * px + 1.0f) / (float)W - 1.0f;
+                const float ndy = (2.0f * py + 1.0f) / (float)H - 1.0f;
+                const float hx = (float)((double)ndx * 1.0000001), hy = (float)((double)ndy * 1.0000001);
+                const float ox = inv[0] * hx + inv[4] * hy + inv[8] * hz + inv[12];
+                const float oy = inv[1] * hx + inv[5] * hy + inv[9] * hz + inv[13];
+                const float oz = inv[2] * hx + inv[6] * hy + inv[10] * hz + inv[14];
+                const float rdx = ox - cx, rdy = oy - cy, rdz = oz - cz;
+                const float len = sqrtf(rdx * rdx + rdy * rdy + rdz * rdz);
+                const float il = 1.0f / len;
+                const float nx = rdx * il, ny = rdy * il, nz = rdz * il;
+                float T_ = 1.0f, C[3] = { 0.f, 0.f, 0.f };
+                float wmax = 0.f, dmax = 0.f, discmax = 0.f, pr[3] = { 0.f, 0.f, 0.f };
+                int32_t imax = 0;
+                for (uint32_t k = rs; k < re; k++) {
+                    const uint32_t id = point_list[k];
+                    const float* co = conic_opacity + 4 * (size_t)id;
+                    const float power = o_power(means2D + 2 * (size_t)id, co, px, py);
+                    if (power > 0.0f) continue;
+                    const float alpha = o_fminf(0.99f, co[3] * o_expf(power));
+                    if (alpha < alpha_min) continue;
+                    const float test_T = T_ * (1.0f - alpha);
+                    if (test_T < 0.0001f) break;
+                    for (int c = 0; c < 3; c++) C[c] = fmaf(colors[3 * (size_t)id + c] * alpha, T_, C[c]);
+                    const float* q = rotations + 4 * (size_t)id;
+                    const float qr = q[0], qx = q[1], qy = q[2], qz = q[3];
+                    const float m0 = 1.f - 2.f * (qy * qy + qz * qz), m1 = 2.f * (qx * qy - qr * qz);
+                    const float m2 = 2.f * (qx * qz + qr * qy), m3 = 2.f * (qx * qy + qr * qz);
+                    const float m4 = 1.f - 2.f * (qx * qx + qz * qz), m5 = 2.f * (qy * qz - qr * qx);
+                    const float m6 = 2.f * (qx * qz - qr * qy), m7 = 2.f * (qy * qz + qr * qx);
+                    const float m8 = 1.f - 2.f * (qx * qx + qy * qy);
+                    const float* mu = means3D + 3 * (size_t)id;
+                    const float ex = cx - mu[0], ey = cy - mu[1], ez = cz - mu[2];
+                    const float rox = m0 * ex + m3 * ey + m6 * ez;
+                    const float roy = m1 * ex + m4 * ey + m7 * ez;
+                    const float roz = m2 * ex + m5 * ey + m8 * ez;
+                    const float rdx2 = m0 * nx + m3 * ny + m6 * nz;
+                    const float rdy2 = m1 * nx + m4 * ny + m7 * nz;
+                    const float rdz2 = m2 * nx + m5 * ny + m8 * nz;
+                    const float* sc = scales + 3 * (size_t)id;
+                    const float sx = sc[0] * 3.0f, sy = sc[1] * 3.0f, sz = sc[2] * 3.0f;
+                    const float a = rdx2 / sx * rdx2 / sx + rdy2 / sy * rdy2 / sy + rdz2 / sz * rdz2 / sz;
+                    const float b = 2.0f * (rdx2 / sx * rox / sx + rdy2 / sy * roy / sy + rdz2 / sz * roz / sz);
+                    const float cc = rox / sx * rox / sx + roy / sy * roy / sy + roz / sz * roz / sz - 1.0f;
+                    const float disc = b * b - 4.0f * a * cc;
+                    const float tpar = -b / 2.0f / a;
+                    const float depth = tpar / len;
+                    if (depth < 0.0f) continue;
+                    const float wgt = alpha * T_;
+                    if (wmax < wgt) {
+                        wmax = wgt;
+                        dmax = depth;
+                        discmax = disc;
+                        imax = (int32_t)id;
+                        pr[0] = cx + tpar * nx;
+                        pr[1] = cy + tpar * ny;
+                        pr[2] = cz + tpar * nz;
+                    }
+                    T_ = test_T;
+                }
+                const size_t pid = (size_t)y * W + x;
+                for (int c = 0; c < 3; c++) {
+                    out_color[(size_t)c * HW + pid] = fmaf(T_, bg[c], C[c]);
+                    out_pts[(size_t)c * HW + pid] = pr[c];
+                }
+                out_depth[pid] = dmax;
+                accum_alpha[pid] = T_;
+                discriminants[pid] = discmax;
+                gidx[pid] = imax;
+            }
+    }
+}
+
 void o_vec_expf(int n, const float* x, float* y)
 {
     for (int i = 0; i < n; i++) y[i] = o_expf(x[i]);

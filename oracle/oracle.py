@@ -381,6 +381,51 @@ def render_fwd_full(W, H, bg, means2D, conic_opacity, colors, ranges, point_list
     return out
 
 
+def inv4_colmajor(m):
+    """Inverse of the 4x4 matrix stored column-major in m (16 floats), as the depth render uses it."""
+    m = _f32(np.asarray(m).reshape(-1))
+    out = np.empty(16, np.float32)
+    lib().o_inv4_colmajor(_p(m), _p(out))
+    return out
+
+
+def render_depth_full(W, H, bg, means2D, conic_opacity, colors, ranges, point_list, means3D, scales, rotations,
+                      projmatrix, campos):
+    """render_depthCUDA of the full path (_f forward.cu:616-835)."""
+    means2D, conic_opacity, colors, bg, means3D, scales, rotations = map(
+        _f32, (means2D, conic_opacity, colors, bg, means3D, scales, rotations))
+    projmatrix, campos = _f32(np.asarray(projmatrix).reshape(-1)), _f32(np.asarray(campos).reshape(-1))
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    out = dict(color=np.empty((3, H, W), np.float32), out_pts=np.empty((3, H, W), np.float32),
+               depth=np.empty((1, H, W), np.float32), accum_alpha=np.empty((1, H, W), np.float32),
+               gidx=np.empty((1, H, W), np.int32), discriminants=np.empty((1, H, W), np.float32))
+    lib().o_render_depth_full(C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity), _p(colors),
+                              _p(ranges), _p(point_list), _p(means3D), _p(scales), _p(rotations), _p(projmatrix),
+                              _p(campos), _p(out["color"]), _p(out["out_pts"]), _p(out["depth"]),
+                              _p(out["accum_alpha"]), _p(out["gidx"]), _p(out["discriminants"]))
+    return out
+
+
+def full_path_depth(cam, scene, bg=None, culling=None, colors_precomp=None, cov3D_precomp=None, scale_modifier=1.0,
+                    sh_degree=3):
+    """render_depth of the full path (rasterizer_impl.cu:671-847): preprocess,
+    binning as the forward, the depth blend."""
+    sh = _f32(scene["sh"])
+    pre = preprocess_fwd_full(cam, scene["means3D"], scene["scales"], scene["rotations"], sh[:, :1], sh[:, 1:],
+                              scene["opacities"], colors_precomp, cov3D_precomp, culling, scale_modifier,
+                              sh_degree)
+    W, H = int(cam["W"]), int(cam["H"])
+    bn = binning_full(W, H, pre["means2D"], pre["depths"], pre["radii"], pre["rects"], pre["conic_opacity"],
+                      pre["tiles_touched"])
+    if bg is None:
+        bg = np.zeros(3, np.float32)
+    colors = pre["rgb"] if colors_precomp is None else colors_precomp
+    rd = render_depth_full(W, H, bg, pre["means2D"], pre["conic_opacity"], colors, bn["ranges"], bn["point_list"],
+                           scene["means3D"], scene["scales"], scene["rotations"], cam["projmatrix"], cam["campos"])
+    return pre, bn, rd
+
+
 def render_bwd_full(W, H, bg, means2D, conic_opacity, colors, ranges, point_list, final_T, n_contrib_px,
                     dL_dpixels):
     """Render backward of the full path (per-pixel gradients with the clamp rule of

@@ -229,3 +229,91 @@ def test_config1_full_path_forward_bitexact(gpu):
     got = _run(scene, cam)
     pre, bn, rf = _oracle(scene, cam)
     _check_forward(got, pre, bn, rf)
+
+
+# ------------------------------------------------------------------ render_depth
+
+def _depth_gpu(scene, cam, bg=(0.0, 0.0, 0.0), culling=None, colors_precomp=None, deg=3):
+    rs = settings_for(cam, bg=bg, sh_degree=deg)
+    dc, rest = _split_sh(scene)
+    ras = GaussianRasterizer(rs)
+    cull = torch.zeros(len(scene["means3D"]), dtype=torch.bool, device="cuda") if culling is None \
+        else to_dev(culling.astype(bool))
+    return ras.render_depth(means3D=to_dev(scene["means3D"]), means2D=None, opacities=to_dev(scene["opacities"]),
+                            culling=cull, dc=None if colors_precomp is not None else to_dev(dc),
+                            shs=None if colors_precomp is not None else to_dev(rest),
+                            colors_precomp=None if colors_precomp is None else to_dev(colors_precomp),
+                            scales=to_dev(scene["scales"]), rotations=to_dev(scene["rotations"]))
+
+
+def _check_depth(res, rd):
+    assert_bitexact(np_(res["render"]), rd["color"], "depth render colour")
+    assert_bitexact(np_(res["out_pts"]), rd["out_pts"], "out_pts")
+    assert_bitexact(np_(res["rendered_depth"]), rd["depth"], "rendered_depth")
+    assert_bitexact(np_(res["accum_alpha"]), rd["accum_alpha"], "accum_alpha")
+    assert_bitexact(np_(res["discriminants"]), rd["discriminants"], "discriminants")
+    assert_bitexact(np_(res["gidx"]), rd["gidx"], "gidx")
+
+
+@pytest.mark.parametrize("case", ["config0", "culling_colors", "negative_depth", "anisotropic"])
+def test_render_depth_bitexact(gpu, case):
+    print(f"render_depth {case}", flush=True)
+    bg = (0.1, 0.2, 0.3)
+    culling = colors = None
+    if case == "config0":
+        scene, cam = synth.config0()
+    elif case == "culling_colors":
+        scene, cam = synth.small_scene(3000, seed=21, W=96, H=80, log_mu=-2.0)
+        rng = np.random.default_rng(1)
+        culling = rng.random(3000) < 0.3
+        colors = rng.random((3000, 3)).astype(np.float32)
+    else:
+        scene, cam = synth.small_scene(1, seed=9, W=48, H=40)
+        if case == "negative_depth":
+            mu, q, s = [-3.0, 0.0, -3.5], [1, 0, 0, 0], [2.0, 2.0, 2.0]
+        else:
+            mu, q, s = [0.1, -0.05, 0.5], [0.8, 0.3, -0.4, 0.2], [1.2, 0.5, 0.3]
+        scene["means3D"] = np.array([mu], np.float32)
+        scene["rotations"] = np.array([q], np.float32)
+        scene["scales"] = np.array([s], np.float32)
+        scene["opacities"] = np.array([[0.9]], np.float32)
+    res = _depth_gpu(scene, cam, bg=bg, culling=culling, colors_precomp=colors)
+    pre, bn, rd = O.full_path_depth(cam, scene, bg=np.asarray(bg, np.float32), culling=culling,
+                                    colors_precomp=colors)
+    _check_depth(res, rd)
+    assert (np_(res["accum_alpha"]) < 1).any()
+
+
+def test_render_depth_raw_op_and_config1(gpu):
+    """The raw _C.rasterize_gaussians_depth tuple, and config 1's 1M Gaussians
+    at 1920x1080 bit-exact against the oracle."""
+    from blitzgs_amd import compat_ops as _C
+    scene, cam = synth.config1()
+    print("render_depth config1", flush=True)
+    rs = settings_for(cam)
+    dc, rest = _split_sh(scene)
+    e = torch.Tensor([])
+    out = _C.rasterize_gaussians_depth(rs.bg, to_dev(scene["means3D"]), e, to_dev(scene["opacities"]),
+                                       to_dev(scene["scales"]), to_dev(scene["rotations"]), 1.0, e, rs.viewmatrix,
+                                       rs.projmatrix, rs.tanfovx, rs.tanfovy, rs.image_height, rs.image_width,
+                                       to_dev(dc), to_dev(rest), 3, rs.campos, False,
+                                       torch.zeros(len(scene["means3D"]), dtype=torch.bool, device="cuda"), False)
+    assert len(out) == 11
+    num_rendered, color, out_pts, depth, accum_alpha, gidx, disc, radii = out[:8]
+    pre, bn, rd = O.full_path_depth(cam, scene)
+    assert num_rendered == bn["R"]
+    assert_bitexact(np_(radii), pre["radii"], "radii")
+    _check_depth(dict(render=color, out_pts=out_pts, rendered_depth=depth, accum_alpha=accum_alpha, gidx=gidx,
+                      discriminants=disc), rd)
+
+
+def test_render_depth_needs_scales_and_rotations(gpu):
+    scene, cam = synth.small_scene(10, seed=1)
+    rs = settings_for(cam)
+    ras = GaussianRasterizer(rs)
+    dc, rest = _split_sh(scene)
+    cov = torch.zeros((10, 6), device="cuda")
+    with pytest.raises(RuntimeError, match="scales and rotations"):
+        ras.render_depth(means3D=to_dev(scene["means3D"]), means2D=None, opacities=to_dev(scene["opacities"]),
+                         culling=torch.zeros(10, dtype=torch.bool, device="cuda"), dc=to_dev(dc), shs=to_dev(rest),
+                         cov3D_precomp=cov)

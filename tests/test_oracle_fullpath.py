@@ -328,3 +328,119 @@ def test_dL_dcov3D_consistent_with_scale_gradient():
             J[:, k] = [dcov[a, b] for a, b in iu]
         expect = J.T @ pb["dL_dcov3D"][i].astype(np.float64)
         np.testing.assert_allclose(pb["dL_dscales"][i], expect, rtol=2e-3, atol=1e-6)
+
+
+# ------------------------------------------------------------------ render_depth
+
+def _proj_colmajor(cam):
+    """The matrix the kernels see: element (r, c) is projmatrix's flat entry 4c + r."""
+    return np.asarray(cam["projmatrix"], np.float64).reshape(4, 4).T
+
+
+def test_inverse_projection_matches_numpy():
+    for cam in (synth.small_scene(1, seed=0)[1], synth.config0()[1], synth.aerial_camera(1600, 1066)):
+        got = O.inv4_colmajor(cam["projmatrix"]).astype(np.float64).reshape(4, 4).T
+        ref = np.linalg.inv(_proj_colmajor(cam))
+        np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-6 * np.abs(ref).max())
+
+
+def _rays64(cam):
+    """Per-pixel rays in float64: the point inv(M) (ndc.x, ndc.y, z, 1) (no
+    division by w) minus the camera centre.  For znear 0.01 / zfar 100 the
+    reference's z constant is the NDC depth of view depth 1, where w = 1."""
+    W, H = int(cam["W"]), int(cam["H"])
+    Minv = np.linalg.inv(_proj_colmajor(cam))
+    ys, xs = np.mgrid[0:H, 0:W].astype(np.float64)
+    ndx = (2 * xs + 1) / W - 1
+    ndy = (2 * ys + 1) / H - 1
+    h = np.stack([ndx * 1.0000001, ndy * 1.0000001, np.full_like(ndx, 99.0 / 99.99), np.ones_like(ndx)], -1)
+    p = h @ Minv.T
+    np.testing.assert_allclose(p[..., 3], 1.0, atol=1e-5)
+    return p[..., :3] - np.asarray(cam["campos"], np.float64)
+
+
+def _ellipsoid_hit64(cam, mu, q, s):
+    """Closest approach of every pixel ray to the Gaussian's 3-sigma ellipsoid,
+    from the quadric x^T A x = 1 with A = R diag(1/(3 s)^2) R^T (R the
+    textbook rotation of q): t = -b / 2a along the unit ray, depth = t / |ray|,
+    discriminant b^2 - 4ac, hit point c + t n."""
+    d = _rays64(cam)
+    L = np.linalg.norm(d, axis=-1)
+    n = d / L[..., None]
+    R = ref64.quat_to_rot(np.asarray(q, np.float64))
+    A = R @ np.diag(1.0 / (3.0 * np.asarray(s, np.float64)) ** 2) @ R.T
+    o = np.asarray(cam["campos"], np.float64) - np.asarray(mu, np.float64)
+    a = np.einsum("hwi,ij,hwj->hw", n, A, n)
+    b = 2 * np.einsum("hwi,ij,j->hw", n, A, o)
+    c = o @ A @ o - 1
+    t = -b / (2 * a)
+    return t / L, b * b - 4 * a * c, np.asarray(cam["campos"], np.float64) + t[..., None] * n, b * b + abs(4 * a * c)
+
+
+def _one_gaussian(mu, q, s, opacity, W=32, H=24):
+    scene, cam = synth.small_scene(1, seed=9, W=W, H=H)
+    scene["means3D"] = np.array([mu], np.float32)
+    scene["rotations"] = np.array([q], np.float32)
+    scene["scales"] = np.array([s], np.float32)
+    scene["opacities"] = np.array([[opacity]], np.float32)
+    return scene, cam
+
+
+def test_depth_single_anisotropic_gaussian_closed_form():
+    q = np.array([0.8, 0.3, -0.4, 0.2])                    # unnormalised on purpose
+    s = [1.2, 0.5, 0.3]
+    scene, cam = _one_gaussian([0.1, -0.05, 0.5], q, s, 0.9)
+    pre, bn, rd = O.full_path_depth(cam, scene)
+    hit = rd["accum_alpha"][0] < 1.0
+    assert hit.sum() > 100
+    depth, disc, pts, scale = _ellipsoid_hit64(cam, scene["means3D"][0], scene["rotations"][0].astype(np.float64),
+                                               s)
+    # The ray's float construction cancels terms of size ~1/znear = 100 (the
+    # inverse projection applied at NDC depth 0.990099 to give w = 1), so a
+    # float32 ray carries relative errors of a few 1e-5 against this float64
+    # one -- as the reference's float glm::inverse does.  A formula mistake
+    # (transposed rotation, missing factor 3, wrong ray normalisation) moves
+    # the depths by far more (checked below for the rotation).
+    np.testing.assert_allclose(rd["depth"][0][hit], depth[hit], rtol=1e-4)
+    np.testing.assert_allclose(rd["out_pts"][:, hit].T, pts[hit], rtol=1e-4, atol=1e-4)
+    assert np.all(np.abs(rd["discriminants"][0][hit] - disc[hit]) <= 1e-3 * scale[hit])
+    assert np.all(rd["gidx"][0] == 0)
+    assert np.all(rd["depth"][0][~hit] == 0) and np.all(rd["out_pts"][:, ~hit] == 0)
+    # a wrongly transposed rotation gives another ellipsoid
+    bad, _, _, _ = _ellipsoid_hit64(cam, scene["means3D"][0], q * np.array([1, -1, -1, -1]), s)
+    assert np.abs(bad[hit] - depth[hit]).max() > 1e-2
+
+
+def test_depth_negative_ray_parameter_keeps_transmittance():
+    """A large Gaussian off to the side: on the right of the image the ray's
+    closest approach lies behind the camera (depth < 0).  There its colour is
+    added but T, depth, id and hit point stay untouched."""
+    scene, cam = _one_gaussian([-3.0, 0.0, -3.5], [1, 0, 0, 0], [2.0, 2.0, 2.0], 0.9)
+    pre, bn, rd = O.full_path_depth(cam, scene)
+    rf = O.full_path_forward(cam, scene)[2]
+    depth, _, _, _ = _ellipsoid_hit64(cam, scene["means3D"][0], [1, 0, 0, 0], [2.0, 2.0, 2.0])
+    contributed = rf["n_contrib_px"] > 0
+    neg = contributed & (depth < -1e-4)
+    pos = contributed & (depth > 1e-4)
+    assert neg.sum() > 50 and pos.sum() > 50
+    assert np.all(rd["accum_alpha"][0][neg] == 1.0) and np.all(rd["depth"][0][neg] == 0)
+    assert np.all(rd["out_pts"][:, neg] == 0)
+    # colour = rgb * alpha with T = 1: the forward's colour there (one contribution, T = 1 before it)
+    np.testing.assert_allclose(rd["color"][:, neg], rf["color"][:, neg], rtol=1e-6, atol=1e-7)
+    assert np.all(rd["accum_alpha"][0][pos] == rf["final_T"][pos]) and np.all(rd["depth"][0][pos] > 0)
+
+
+def test_depth_render_agrees_with_forward_on_a_scene():
+    """On a scene in front of the camera (every depth positive) the depth
+    render's T equals the forward's final T bit for bit, its colour to
+    rounding, and counting each covered pixel's gidx reproduces the forward's
+    accum_max_count (the same arg-max of alpha * T)."""
+    scene, cam = synth.small_scene(400, seed=4, W=64, H=48, extent=0.8, log_mu=-2.2)
+    pre, bn, rd = O.full_path_depth(cam, scene)
+    rf = O.full_path_forward(cam, scene, flag_max_count=True)[2]
+    assert np.array_equal(rd["accum_alpha"][0], rf["final_T"])
+    np.testing.assert_allclose(rd["color"], rf["color"], rtol=1e-5, atol=1e-6)
+    covered = rf["n_contrib_px"] > 0
+    counts = np.bincount(rd["gidx"][0][covered], minlength=400).astype(np.float32)
+    assert np.array_equal(counts, rf["accum_max_count"])
+    assert np.all(rd["depth"][0][covered] > 0)

@@ -49,6 +49,8 @@
 // the Gaussian's 64-byte accumulator with one atomic instruction per (wave,
 // Gaussian) instead of eleven atomics per (pixel, Gaussian); a final pass
 // writes the reference's gradient arrays from the accumulators.
+#include <mutex>
+
 #include "gs_device.h"
 #include "gs_host.h"
 #include "../../include/blitzgs_amd.h"
@@ -60,6 +62,7 @@ constexpr int BIN_THREADS = 512;
 constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
+constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
 constexpr int BIG_SORT_THREADS = 1024;
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
@@ -78,6 +81,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct GeomLayout {
     int T, NC, CH, WS;
+    size_t cls_count, cls_list;   // per size class: number of local tiles, their local indices (T per class)
     size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, wcount, cidx_of, cid2id, rec, gacc,
         total;
 };
@@ -103,6 +107,8 @@ GeomLayout geom_layout(int P, int W, int H)
     g.tile_start = o; o = align256(o + sizeof(uint32_t) * (size_t)g.T);
     g.cursor = o; o = align256(o + sizeof(uint32_t) * (size_t)g.T);
     g.wcount = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NC * WAVES_PER_BIN);
+    g.cls_count = o; o = align256(o + sizeof(uint32_t) * SORT_CLASSES);
+    g.cls_list = o; o = align256(o + sizeof(int) * (size_t)SORT_CLASSES * (size_t)g.T);
     g.cidx_of = o; o = align256(o + sizeof(int) * (size_t)P);
     g.cid2id = o; o = align256(o + sizeof(uint32_t) * (size_t)P);
     g.rec = o; o = align256(o + REC_BYTES * (size_t)P);
@@ -402,11 +408,19 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
 
 // exclusive scans: over local tiles -> tile_start, R -> meta[2..3]; over the
 // per-wave listed counts (in place) -> compact index bases, L -> meta[4]
+__device__ __forceinline__ int sort_class(uint32_t n)
+{
+    return n <= 512u ? 0 : n <= 1024u ? 1 : n <= 2048u ? 2 : n <= 4096u ? 3 : n <= (uint32_t)SORT_CAP_MAX ? 4 : 5;
+}
+
 __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ meta, const uint32_t* __restrict__ tile_count,
                                                         uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
-                                                        uint32_t* __restrict__ wcount, int NW)
+                                                        uint32_t* __restrict__ wcount, int NW, int T,
+                                                        uint32_t* __restrict__ cls_count, int* __restrict__ cls_list)
 {
     __shared__ uint32_t s_wave[32];
+    __shared__ uint32_t s_cls[SORT_CLASSES];
+    if (threadIdx.x < SORT_CLASSES) s_cls[threadIdx.x] = 0u;
     const int TL = (int)meta[0];
     {
         uint32_t base = 0;
@@ -429,9 +443,16 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
         if (l < TL) {
             tile_start[l] = (uint32_t)(base + pre);
             cursor[l] = (uint32_t)(base + pre);
+            // the sort launches walk per-class lists of non-empty buckets
+            if (v > 0u) {
+                const int c = sort_class(v);
+                cls_list[(size_t)c * T + atomicAdd(&s_cls[c], 1u)] = l;
+            }
         }
         base += tot;
     }
+    __syncthreads();
+    if (threadIdx.x < SORT_CLASSES) cls_count[threadIdx.x] = s_cls[threadIdx.x];
     if (threadIdx.x == 0) {
         meta[2] = (uint32_t)(base & 0xffffffffu);
         meta[3] = (uint32_t)(base >> 32);
@@ -743,20 +764,17 @@ __device__ __forceinline__ void sort_merges(uint64_t (&k)[8], uint64_t* lds)
     }
 }
 
-// One block of NT threads per local tile whose bucket size lies in
-// (8 NT / 2, 8 NT] (any size up to 512 for one wave): the bucket, padded with
-// all-ones keys, is sorted by (depth bits, compact index) in registers.
-template <int NT, int LO>
-__global__ __launch_bounds__(NT) void tilesort_kernel(
-    const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
-    const uint32_t* __restrict__ tile_start, const uint64_t* __restrict__ sortkey, SortOut out)
+// A bucket whose size lies in (8 NT / 2, 8 NT] (any size up to 512 for one
+// wave) is sorted by one block of NT threads: padded with all-ones keys, by
+// (depth bits, compact index) in registers.
+template <int NT, int LO, int CAP>
+__device__ __forceinline__ void tilesort_one(int l, const int* __restrict__ tile_of_local,
+                                             const uint32_t* __restrict__ tile_count,
+                                             const uint32_t* __restrict__ tile_start,
+                                             const uint64_t* __restrict__ sortkey, const SortOut& out,
+                                             uint64_t* lds)
 {
-    constexpr int CAP = 8 * NT;
-    __shared__ uint64_t lds[NT * 9];
-    const int l = blockIdx.x;
-    if (l >= (int)meta[0]) return;
     const int n = (int)tile_count[l];
-    if (n <= LO || n > CAP) return;
     const uint32_t start = tile_start[l];
     const int t = threadIdx.x;
     for (int i = t; i < CAP; i += NT) lds[sort_slot(i)] = i < n ? sortkey[start + i] : ~0ull;
@@ -779,22 +797,42 @@ __global__ __launch_bounds__(NT) void tilesort_kernel(
     }
 }
 
+// One launch per size class; its blocks walk the class's list of buckets
+// (block b takes entries b, b + gridDim.x, ...).
+template <int NT, int LO>
+__global__ __launch_bounds__(NT) void tilesort_kernel(
+    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const int* __restrict__ tile_of_local,
+    const uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
+    const uint64_t* __restrict__ sortkey, SortOut out)
+{
+    constexpr int CAP = 8 * NT;
+    __shared__ uint64_t lds[NT * 9];
+    const int nl = (int)*cls_count;
+    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
+        if (e != (int)blockIdx.x) __syncthreads();   // the previous bucket's reads of lds are done
+        tilesort_one<NT, LO, CAP>(cls_list[e], tile_of_local, tile_count, tile_start, sortkey, out, lds);
+    }
+}
+
 // Buckets larger than the biggest LDS class: the same network in global
 // memory, in place.
 __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
-    const uint32_t* __restrict__ meta, const int* __restrict__ tile_of_local, const uint32_t* __restrict__ tile_count,
-    const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, SortOut out)
+    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const int* __restrict__ tile_of_local,
+    const uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey,
+    SortOut out)
 {
-    const int l = blockIdx.x;
-    if (l >= (int)meta[0]) return;
-    const int n = (int)tile_count[l];
-    if (n <= SORT_CAP_MAX) return;
-    const uint32_t start = tile_start[l];
-    uint64_t* s = sortkey + start;
-    int N = 1;
-    while (N < n) N <<= 1;
-    bitonic<BIG_SORT_THREADS>(s, n, N);
-    write_sorted((uint32_t)tile_of_local[l], start, n, s, out, BIG_SORT_THREADS);
+    const int nl = (int)*cls_count;
+    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
+        if (e != (int)blockIdx.x) __syncthreads();
+        const int l = cls_list[e];
+        const int n = (int)tile_count[l];
+        const uint32_t start = tile_start[l];
+        uint64_t* s = sortkey + start;
+        int N = 1;
+        while (N < n) N <<= 1;
+        bitonic<BIG_SORT_THREADS>(s, n, N);
+        write_sorted((uint32_t)tile_of_local[l], start, n, s, out, BIG_SORT_THREADS);
+    }
 }
 
 // ------------------------------------------------------------- blend
@@ -1440,6 +1478,42 @@ extern "C" int gs_render_buffer_views(int64_t R, int W, int H, void* binning, vo
 
 namespace {
 
+// Side streams for the bucket sort: the size classes sort disjoint buckets,
+// and the largest classes are a few single blocks whose bitonic networks are
+// latency-bound, so the classes run side by side (forked from and joined back
+// to the caller's stream with events).  Created once per device, at the
+// default priority, never destroyed.
+struct SideStreams {
+    std::mutex mu;
+    bool ready = false;
+    hipStream_t s[SORT_CLASSES];
+    hipEvent_t fork, join[SORT_CLASSES];
+};
+constexpr int MAX_DEVICES = 64;
+SideStreams g_side[MAX_DEVICES];
+
+// the side streams of the stream's device (null if it is not the current device)
+int side_streams_for(hipStream_t stream, SideStreams*& out)
+{
+    out = nullptr;
+    int cur = 0, sdev = -1;
+    GS_HIP(hipGetDevice(&cur));
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != cur || cur < 0 || cur >= MAX_DEVICES) {
+        (void)hipGetLastError();
+        return GS_OK;
+    }
+    SideStreams& ss = g_side[cur];
+    std::lock_guard<std::mutex> lk(ss.mu);
+    if (!ss.ready) {
+        for (int c = 0; c < SORT_CLASSES; c++) GS_HIP(hipStreamCreateWithFlags(&ss.s[c], hipStreamNonBlocking));
+        GS_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
+        for (int c = 0; c < SORT_CLASSES; c++) GS_HIP(hipEventCreateWithFlags(&ss.join[c], hipEventDisableTiming));
+        ss.ready = true;
+    }
+    out = &ss;
+    return GS_OK;
+}
+
 // count + scan + R readback, shared by the split and the full-image path
 int render_count_impl(bool full, int P, int W, int H, const float* means2D, const int* radii,
                       const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
@@ -1482,7 +1556,8 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     }
     GS_TIMED("tilescan_kernel", stream,
              hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
-                                at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0));
+                                at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
+                                at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list)));
     GS_LAUNCH_CHECK("tilescan_kernel");
     uint32_t hR[2] = {0, 0};
     GS_HIP(hipMemcpyAsync(hR, meta + 2, sizeof(hR), hipMemcpyDeviceToHost, stream));
@@ -1566,30 +1641,72 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         }
         GS_LAUNCH_CHECK("scatter_kernel");
         const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};
-        GS_TIMED("tilesort_kernel_512", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<64, 0>), dim3(T), dim3(64), 0, stream, meta, tile_of_local,
-                                    tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<64>");
-        GS_TIMED("tilesort_kernel_1k", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<128, 512>), dim3(T), dim3(128), 0, stream, meta, tile_of_local,
-                                    tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<128>");
-        GS_TIMED("tilesort_kernel_2k", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<256, 1024>), dim3(T), dim3(256), 0, stream, meta, tile_of_local,
-                                    tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<256>");
-        GS_TIMED("tilesort_kernel_4k", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<512, 2048>), dim3(T), dim3(512), 0, stream, meta, tile_of_local,
-                                    tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<512>");
-        GS_TIMED("tilesort_kernel_8k", stream,
-                 hipLaunchKernelGGL((tilesort_kernel<1024, 4096>), dim3(T), dim3(1024), 0, stream, meta,
-                                    tile_of_local, tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_kernel<1024>");
-        GS_TIMED("tilesort_big_kernel", stream,
-                 hipLaunchKernelGGL(tilesort_big_kernel, dim3(T), dim3(BIG_SORT_THREADS), 0, stream, meta,
-                                    tile_of_local, tile_count, tile_start, sortkey, sout));
-        GS_LAUNCH_CHECK("tilesort_big_kernel");
+        // one launch per size class over that class's bucket list; the grid is
+        // bounded by how many buckets of the class R instances can fill and
+        // by what fits on the chip at once
+        const uint32_t* cc = at<const uint32_t>(geom, g.cls_count);
+        const int* cls = at<const int>(geom, g.cls_list);
+        auto grid_of = [&](int lo, int cap) {
+            const int64_t fit = R / (int64_t)(lo + 1);
+            return (unsigned)std::min<int64_t>(std::min<int64_t>((int64_t)T, fit), (int64_t)cap);
+        };
+        const unsigned gcs[SORT_CLASSES] = {grid_of(0, 8192), grid_of(512, 4096), grid_of(1024, 2048),
+                                            grid_of(2048, 1024), grid_of(4096, 512), grid_of(SORT_CAP_MAX, 256)};
+        SideStreams* ss = nullptr;
+        if (int rc = side_streams_for(stream, ss); rc != GS_OK) return rc;
+        std::unique_lock<std::mutex> lk;
+        if (ss != nullptr) {
+            lk = std::unique_lock<std::mutex>(ss->mu);
+            GS_HIP(hipEventRecord(ss->fork, stream));
+        }
+        for (int c = SORT_CLASSES - 1; c >= 0; c--) {
+            const unsigned gc = gcs[c];
+            if (gc == 0) continue;
+            hipStream_t cs = stream;
+            if (ss != nullptr) {
+                cs = ss->s[c];
+                GS_HIP(hipStreamWaitEvent(cs, ss->fork, 0));
+            }
+            const uint32_t* ccc = cc + c;
+            const int* cl = cls + (size_t)c * T;
+            switch (c) {
+            case 0:
+                GS_TIMED("tilesort_kernel_512", cs,
+                         hipLaunchKernelGGL((tilesort_kernel<64, 0>), dim3(gc), dim3(64), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            case 1:
+                GS_TIMED("tilesort_kernel_1k", cs,
+                         hipLaunchKernelGGL((tilesort_kernel<128, 512>), dim3(gc), dim3(128), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            case 2:
+                GS_TIMED("tilesort_kernel_2k", cs,
+                         hipLaunchKernelGGL((tilesort_kernel<256, 1024>), dim3(gc), dim3(256), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            case 3:
+                GS_TIMED("tilesort_kernel_4k", cs,
+                         hipLaunchKernelGGL((tilesort_kernel<512, 2048>), dim3(gc), dim3(512), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            case 4:
+                GS_TIMED("tilesort_kernel_8k", cs,
+                         hipLaunchKernelGGL((tilesort_kernel<1024, 4096>), dim3(gc), dim3(1024), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            default:
+                GS_TIMED("tilesort_big_kernel", cs,
+                         hipLaunchKernelGGL(tilesort_big_kernel, dim3(gc), dim3(BIG_SORT_THREADS), 0, cs, ccc, cl,
+                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                break;
+            }
+            GS_LAUNCH_CHECK("tilesort_kernel");
+            if (ss != nullptr) {
+                GS_HIP(hipEventRecord(ss->join[c], cs));
+                GS_HIP(hipStreamWaitEvent(stream, ss->join[c], 0));
+            }
+        }
     }
     unsigned sgx, NS;
     const unsigned nblk = blend_grid(gx, gy, sgx, NS);

@@ -1380,51 +1380,51 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             const float4 B = st.b[j];
             const float4 Cc = st.c[j];
             const int ci = __float_as_int(Cc.z);   // position in the tile's list
-            float gmx = 0.f, gmy = 0.f, gca = 0.f, gcb = 0.f, gcc = 0.f, gop = 0.f;
-            float gc0 = 0.f, gc1 = 0.f, gc2 = 0.f;
-            bool valid = false;
-            if (ci < last) {
-                const float dx = A.x - pxf, dy = A.y - pyf;
-                const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-                const float G = gs::expf_nonpos(power);
-                const float alpha = __builtin_fminf(0.99f, B.y * G);
-                if (!(power > 0.0f) && !(alpha < alpha_min)) {
-                    valid = true;
-                    const float one_m = 1.f - alpha;
-                    const float inv_one_m = __builtin_amdgcn_rcpf(one_m);   // 1 ulp; gradients only
-                    T_ = T_ * inv_one_m;
-                    const float dchannel_dcolor = alpha * T_;
-                    // the reference's expressions, regrouped into fused multiply-adds
-                    // (gradients carry a tolerance, not bit-exactness):
-                    //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
-                    //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
-                    //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms)
-                    acc0 = __builtin_fmaf(last_alpha, lc0 - acc0, acc0);
-                    acc1 = __builtin_fmaf(last_alpha, lc1 - acc1, acc1);
-                    acc2 = __builtin_fmaf(last_alpha, lc2 - acc2, acc2);
-                    lc0 = B.z; lc1 = B.w; lc2 = Cc.x;
-                    float dL_dalpha = __builtin_fmaf(B.z - acc0, dp0,
-                                                     __builtin_fmaf(B.w - acc1, dp1, (Cc.x - acc2) * dp2));
-                    gc0 = dchannel_dcolor * dp0;
-                    gc1 = dchannel_dcolor * dp1;
-                    gc2 = dchannel_dcolor * dp2;
-                    dL_dalpha = __builtin_fmaf(dL_dalpha, T_, inv_one_m * nT_bg);
-                    last_alpha = alpha;
-                    const float dL_dG = B.y * dL_dalpha;
-                    const float gdx = G * dx, gdy = G * dy;
-                    const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
-                    const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
-                    gmx = (dL_dG * ddelx_dx) * dG_ddelx;
-                    gmy = (dL_dG * ddely_dy) * dG_ddely;
-                    const float h = -0.5f * dL_dG;
-                    const float hgdx = h * gdx;
-                    const bool clamped = FULL && B.y * G > 0.99f;
-                    gca = clamped ? 0.f : hgdx * dx;
-                    gcb = clamped ? 0.f : hgdx * dy;
-                    gcc = clamped ? 0.f : (h * gdy) * dy;
-                    gop = clamped ? 0.f : G * dL_dalpha;
-                }
-            }
+            // Branch-free: every lane evaluates the entry; a lane whose pixel
+            // does not blend it (past its last contributor, power > 0, alpha <
+            // 1/255) gets zero gradient factors and unchanged state, through
+            // selects on three factors instead of per-value zeroing.
+            const float dx = A.x - pxf, dy = A.y - pyf;
+            const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
+            const float G0 = gs::expf_nonpos(power);
+            const float alpha = __builtin_fminf(0.99f, B.y * G0);
+            const bool valid = ci < last && !(power > 0.0f) && !(alpha < alpha_min);
+            const float G = valid ? G0 : 0.f;
+            const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
+            T_ = T_ * inv_one_m;
+            const float dchannel_dcolor = valid ? alpha * T_ : 0.f;
+            // the reference's expressions, regrouped into fused multiply-adds
+            // (gradients carry a tolerance, not bit-exactness):
+            //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
+            //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
+            //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms);
+            // a lane that does not blend the entry updates acc with factor 0
+            const float la = valid ? last_alpha : 0.f;
+            acc0 = __builtin_fmaf(la, lc0 - acc0, acc0);
+            acc1 = __builtin_fmaf(la, lc1 - acc1, acc1);
+            acc2 = __builtin_fmaf(la, lc2 - acc2, acc2);
+            lc0 = valid ? B.z : lc0;
+            lc1 = valid ? B.w : lc1;
+            lc2 = valid ? Cc.x : lc2;
+            last_alpha = valid ? alpha : last_alpha;
+            float dL_dalpha = __builtin_fmaf(B.z - acc0, dp0, __builtin_fmaf(B.w - acc1, dp1, (Cc.x - acc2) * dp2));
+            const float gc0 = dchannel_dcolor * dp0;
+            const float gc1 = dchannel_dcolor * dp1;
+            const float gc2 = dchannel_dcolor * dp2;
+            dL_dalpha = valid ? __builtin_fmaf(dL_dalpha, T_, inv_one_m * nT_bg) : 0.f;
+            const float dL_dG = B.y * dL_dalpha;
+            const float gdx = G * dx, gdy = G * dy;
+            const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
+            const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
+            const float gmx = (dL_dG * ddelx_dx) * dG_ddelx;
+            const float gmy = (dL_dG * ddely_dy) * dG_ddely;
+            const float h = -0.5f * dL_dG;
+            const float hgdx = h * gdx;
+            const bool clamped = FULL && B.y * G > 0.99f;
+            const float gca = clamped ? 0.f : hgdx * dx;
+            const float gcb = clamped ? 0.f : hgdx * dy;
+            const float gcc = clamped ? 0.f : (h * gdy) * dy;
+            const float gop = clamped ? 0.f : G * dL_dalpha;
             if (gs::ballot(valid) == 0) continue;
             const uint32_t cx = __float_as_uint(Cc.y);
             const float vals[12] = {gmx, gmy, __builtin_fabsf(gmx), __builtin_fabsf(gmy), gca, gcb, gcc, gop,

@@ -975,6 +975,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
+        // T only decreases, so a batch that starts with no live pixel above
+        // T = 0.5 cannot observe (split path): its entries skip the ballot
+        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(!done && T_ > 0.5f) != 0;
         // Branch-free blend of one staged entry: every lane evaluates it and
         // the state changes are selects, so no exec-mask bookkeeping.
         auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
@@ -995,6 +998,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
             last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : last;
             done = done || fin;
             if (MODE == BLEND_SPLIT) {
+                if (!obs_batch) return;
                 const uint64_t m = gs::ballot(observe);
                 if (m != 0) {
                     const int first = (int)__builtin_ctzll(m);

@@ -516,20 +516,24 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     const int ws = min(i1c, c * CH + wave * WS);
     const int i1 = min(i1c, ws + WS);
     uint32_t next = wbase[(size_t)c * WAVES_PER_BIN + wave];
-    // software pipeline: the next group's radii and means are loaded while
-    // this group expands, and its depth / conic / colour once its radii are in
+    // software pipeline: all of the next group's inputs (radii, means, depth,
+    // conic, colour) are loaded while this group expands -- unconditionally,
+    // so that no load waits for the radius (the culled Gaussians' lines are
+    // mostly fetched anyway: a line holds several Gaussians)
     int r_n;
     float2 m_n;
-    load_rm(ws + lane, i1, radii, means2D, r_n, m_n);
     float d_n = 0.f;
     float4 co_n = make_float4(0.f, 0.f, 0.f, 0.f);
     float3 c_n = make_float3(0.f, 0.f, 0.f);
-    if (r_n > 0) {
-        const int i = ws + lane;
-        d_n = depths[i];
-        co_n = conic_opacity[i];
-        c_n = make_float3(rgb[3 * (size_t)i], rgb[3 * (size_t)i + 1], rgb[3 * (size_t)i + 2]);
-    }
+    auto load_next = [&](int in) {
+        load_rm(in, i1, radii, means2D, r_n, m_n);
+        if (in < i1) {
+            d_n = depths[in];
+            co_n = conic_opacity[in];
+            c_n = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
+        }
+    };
+    load_next(ws + lane);
     for (int wb = ws; wb < i1; wb += 64) {
         const int i = wb + lane;
         const int r = r_n;
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
         const float dep = d_n;
         const float4 co = co_n;
         const float3 col = c_n;
-        load_rm(i + 64, i1, radii, means2D, r_n, m_n);
+        load_next(i + 64);
         unsigned x0, y0, w;
         int cnt;
         KeepTest kt{};
@@ -595,12 +599,6 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
                     sortkey[pos] = ((uint64_t)odb << 32) | ocx;
                 }
             }
-        }
-        if (r_n > 0) {
-            const int in = i + 64;
-            d_n = depths[in];
-            co_n = conic_opacity[in];
-            c_n = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
         }
     }
 }

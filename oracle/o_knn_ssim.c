@@ -147,7 +147,8 @@ void o_ssim_window(float* w)
 }
 
 /* same-size zero-padded separable blur of one plane: horizontal pass on the
- * padded rows, then vertical pass */
+ * padded rows, then vertical pass; one fused multiply-add per tap, taps in
+ * order -5 .. +5 (nvcc contracts the reference's multiply-add the same way) */
 static void blur_plane(int H, int W, const float* in, float* out, float* tmp /* (H+10)*W */)
 {
     for (int yy = 0; yy < H + 10; yy++) {
@@ -158,17 +159,17 @@ static void blur_plane(int H, int W, const float* in, float* out, float* tmp /* 
                 for (int t = 0; t < 11; t++) {
                     const int xs = x + t - 5;
                     const float p = (xs >= 0 && xs < W) ? in[(size_t)y * W + xs] : 0.0f;
-                    v += g_win[t] * p;
+                    v = fmaf(g_win[t], p, v);
                 }
             else
-                for (int t = 0; t < 11; t++) v += g_win[t] * 0.0f;
+                for (int t = 0; t < 11; t++) v = fmaf(g_win[t], 0.0f, v);
             tmp[(size_t)yy * W + x] = v;
         }
     }
     for (int y = 0; y < H; y++)
         for (int x = 0; x < W; x++) {
             float v = 0.0f;
-            for (int t = 0; t < 11; t++) v += g_win[t] * tmp[(size_t)(y + t) * W + x];
+            for (int t = 0; t < 11; t++) v = fmaf(g_win[t], tmp[(size_t)(y + t) * W + x], v);
             out[(size_t)y * W + x] = v;
         }
 }

@@ -1747,7 +1747,7 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                          float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
 {
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
-    GS_REQUIRE(dL_dmeans2D_stride >= 2, "dL_dmeans2D row stride must be >= 2");
+    GS_REQUIRE(dL_dmeans2D_stride == 2 || dL_dmeans2D_stride == 3, "dL_dmeans2D row stride must be 2 or 3");
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
                ((uintptr_t)means2D & 7) == 0,
                "conic_opacity / dL_dconic_opacity must be 16-byte and means2D 8-byte aligned");

@@ -259,6 +259,8 @@ def run_step(args):
                  {"gaussians": P, "visible": P_vis, "instances": R, "image": [W, H], "tiles": T,
                   "local_tiles": int(cl.sum().item()) if cl is not None else T, "loss": loss_desc})
     out["stages_ms"] = stage_rows
+    out["stages_note"] = ("per-kernel HIP-event times; the bucket-sort size classes run concurrently on side "
+                          "streams (R >= 2^21), so the binning stage sums overlapping times")
     out["ms_per_step_with_kernel_events"] = round(ms_instr, 4)
     out["render_fwd_evaluations"] = E
     out["hbm_copy_GBs"] = round(peak_copy, 1)

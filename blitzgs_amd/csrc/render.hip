@@ -63,6 +63,7 @@ constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
 constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
+constexpr int64_t SIDE_STREAM_MIN_R = 1 << 21;   // instances from which the size classes sort concurrently
 constexpr int BIG_SORT_THREADS = 1024;
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
@@ -1654,8 +1655,12 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         };
         const unsigned gcs[SORT_CLASSES] = {grid_of(0, 8192), grid_of(512, 4096), grid_of(1024, 2048),
                                             grid_of(2048, 1024), grid_of(4096, 512), grid_of(SORT_CAP_MAX, 256)};
+        // side streams pay off once the sorts are long enough to hide the
+        // fork / join (small scenes sort on the caller's stream)
         SideStreams* ss = nullptr;
-        if (int rc = side_streams_for(stream, ss); rc != GS_OK) return rc;
+        if (R >= SIDE_STREAM_MIN_R) {
+            if (int rc = side_streams_for(stream, ss); rc != GS_OK) return rc;
+        }
         std::unique_lock<std::mutex> lk;
         if (ss != nullptr) {
             lk = std::unique_lock<std::mutex>(ss->mu);

@@ -30,9 +30,11 @@
 //                index) to its reserved slices (LDS cursors) and writes each
 //                listed Gaussian's 64-byte blend record at its compact index.
 //   4. sort    : one block per tile sorts its bucket by (depth bits, compact
-//                index) in registers (bitonic, five size classes) and writes the
-//                sorted Gaussian ids, the (tile << 32 | depth bits) keys and
-//                the compact list the blend walks.
+//                index) in registers (bitonic, five size classes, each class
+//                walking its own list of buckets, the classes side by side on
+//                side streams for large R) and writes the sorted Gaussian ids,
+//                the (tile << 32 | depth bits) keys and the compact list the
+//                blend walks.
 // The compact index is increasing in Gaussian id, so each sorted bucket is
 // exactly the order of a stable sort of the reference's duplicated keys, and
 // the sorted arrays and the ranges are bit-identical to the reference

@@ -64,11 +64,17 @@ __global__ __launch_bounds__(ADAM_THREADS) void adam_kernel(AdamBatch B, const u
     const uint64_t e0 = item * 4;
     if (e0 >= G.cnt) return;
     const uint32_t n_el = (uint32_t)min((uint64_t)4, G.cnt - e0);
+    // the Gaussian of element e0 + k: one division per item (32-bit when the
+    // group fits), the other three rows follow by comparison (k < 4, M >= 1)
+    const uint64_t row0 = G.cnt <= 0xffffffffull ? (uint64_t)((uint32_t)e0 / G.M) : e0 / G.M;
+    const uint32_t rem = (uint32_t)(e0 - row0 * G.M);
     bool vis[4];
     bool any = false;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        vis[k] = (uint32_t)k < n_el && visible[(e0 + (uint64_t)k) / G.M] != 0;
+        const uint32_t t = rem + (uint32_t)k;
+        const uint64_t row = row0 + (uint64_t)((t >= G.M) + (t >= 2 * G.M) + (t >= 3 * G.M));
+        vis[k] = (uint32_t)k < n_el && visible[row] != 0;
         any = any || vis[k];
     }
     if (!any) return;

@@ -182,9 +182,11 @@ def render_gaussians(means2D, means2D_abs, conic_opacity, rgb, all_map, depths, 
 
 
 def _tile_mask(cl, H, W, device):
+    """compute_locally as the library's uint8 tile mask; None (every tile is
+    local) is passed on as a null mask."""
     gy, gx = (H + 15) // 16, (W + 15) // 16
     if cl is None:
-        return torch.ones(gy * gx, dtype=torch.uint8, device=device)
+        return None
     cl = cl.to(device=device)
     if cl.numel() != gy * gx:
         raise RuntimeError(f"compute_locally must have {gy}x{gx} tile entries, got {tuple(cl.shape)}")
@@ -274,6 +276,8 @@ class _RenderGaussians(torch.autograd.Function):
         rs = raster_settings
         if getattr(rs, "render_geo", False):
             raise NotImplementedError("render_geo=True (normal / plane-depth maps) is not supported")
+        # the backward reads only dL/dcolor: unused outputs need no zero-filled gradients
+        ctx.set_materialize_grads(False)
         use_ext = isinstance(cuda_args, dict) and bool(cuda_args.get("avoid_pixel_all2all", False))
         cl = extended_compute_locally if use_ext else compute_locally
         H, W = int(rs.image_height), int(rs.image_width)

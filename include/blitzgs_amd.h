@@ -95,7 +95,8 @@ int gs_preprocess_backward(int P, int D, int K, const float* means3D, const floa
  *   binning : gs_render_binning_bytes(R) bytes     (sorted keys and ids)
  *   img     : gs_render_img_bytes(W, H) bytes      (tile ranges, per-pixel
  *             final transmittance and contributor counts)
- * compute_locally is a uint8 (ceil(H/16), ceil(W/16)) tile mask.
+ * compute_locally is a uint8 (ceil(H/16), ceil(W/16)) tile mask, or NULL
+ * when every tile is local.
  * ------------------------------------------------------------------------ */
 size_t gs_render_geom_bytes(int P, int image_width, int image_height);
 size_t gs_render_binning_bytes(int64_t R);

@@ -16,8 +16,10 @@ diff_gaussian_rasterization_f._C / diff_gaussian_rasterization_r._C expose
   adamUpdate                      _f/rasterize_points.cu:807-832
 Same positional arguments and return tuples; `args` is the reference's
 cuda_args dict (its "stats_collector" entry receives forward_render_time /
-backward_render_time in ms).  The image-tile utilities of the multi-GPU path
-are not implemented.
+backward_render_time in ms).  Not provided: the image-tile utilities of the
+multi-GPU path (_r ext.cpp:20-34) and _f's own older fusedssim /
+fusedssim_backward pair (_f ext.cpp:23-24, conv.cu:390-470; nothing in BlitzGS
+calls it -- the training loss uses the fused_ssim package, blitzgs_amd.ssim).
 """
 import torch
 
@@ -79,13 +81,6 @@ def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, al
         args["stats_collector"]["backward_render_time"] = ms
     dL_dall_map = torch.zeros((means2D.size(0), 5), device=means2D.device, dtype=torch.float32)
     return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, dL_dall_map
-
-
-def _not_here(name):
-    def f(*a, **k):
-        raise NotImplementedError(f"{name} is not part of this build")
-    f.__name__ = name
-    return f
 
 
 from .fullpath import C_rasterize_gaussians as rasterize_gaussians  # noqa: E402,F401

@@ -150,6 +150,43 @@ def timed(fn, steps, warmup):
     return ms, kt, ev0.elapsed_time(ev1) / steps
 
 
+def valu_peak(iters=2000, reps=5):
+    """Measured VALU issue rate in G wave-instructions/s: the library's FMA
+    probe (8192 blocks x 4 waves x 32 * iters independent-chain fp32 FMAs),
+    best of `reps` launches."""
+    import torch
+    from blitzgs_amd import _lib
+    lib = _lib.load()
+    y = torch.zeros(1, device="cuda:0")
+    stream = _lib.stream_of(y.device)
+    _lib.check(lib.gs_diag_math(5, 10, None, _lib.ptr(y), stream), "gs_diag_math valu")
+    best = float("inf")
+    for _ in range(reps):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        _lib.check(lib.gs_diag_math(5, iters, None, _lib.ptr(y), stream), "gs_diag_math valu")
+        ev1.record()
+        torch.cuda.synchronize()
+        best = min(best, ev0.elapsed_time(ev1))
+    return 8192 * 4 * 32 * iters / (best * 1e-3) / 1e9
+
+
+def valu_of(name, avg_ms, config):
+    """VALU issue rate of kernel `name` per launch: SQ_INSTS_VALU per launch
+    (profiles/valu_config<N>.json, rocprofv3 --pmc) over its live launch time,
+    against the measured FMA issue rate."""
+    f = os.path.join(ROOT, "profiles", f"valu_config{config}.json")
+    try:
+        insts = json.load(open(f))[name]["SQ_INSTS_VALU"]
+    except (OSError, ValueError, KeyError):
+        return None
+    peak = valu_peak()
+    achieved = insts / (avg_ms * 1e-3) / 1e9
+    return {"unit": "G wave-instructions/s", "insts_per_launch": int(insts), "achieved": round(achieved, 1),
+            "peak": round(peak, 1), "frac": round(achieved / peak, 4),
+            "peak_is": "measured fp32 FMA issue rate (gs_diag_math op 5)"}
+
+
 def roofline_of(name, alg_bytes, avg_ms, traffic=None):
     achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
     return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -247,7 +284,9 @@ def run_step(args):
             traffic = None
     roofline = roofline_of(dom, sb[dom], avg_launch.get(dom, float("nan")), traffic)
     roofline["note"] = ("the blend kernels are VALU-bound (per-pixel exp and gradient arithmetic plus a 64-lane "
-                        "reduction per Gaussian); their HBM fraction is low by nature")
+                        "reduction per Gaussian); their HBM fraction is low by nature: `valu` compares their VALU "
+                        "instruction issue rate with the measured peak")
+    roofline["valu"] = valu_of(dom, avg_launch.get(dom, float("nan")), args.config)
 
     cpu = None
     if not args.no_cpu_baseline:

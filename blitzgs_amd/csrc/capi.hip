@@ -166,14 +166,45 @@ __global__ void diag_copy_kernel(size_t n4, const float4* __restrict__ x, float4
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) y[i] = x[i];
 }
+
+// op 5: VALU issue-rate reference.  Every wave runs `iters` rounds of 32
+// independent-chain fp32 FMAs (8 chains, 4 deep), i.e. 32 * iters VALU
+// instructions; the result is stored only in the (never met) case that it
+// equals a sentinel, so nothing is optimised away and nothing is written.
+constexpr int DIAG_VALU_BLOCKS = 8192;
+__global__ __launch_bounds__(256) void diag_valu_kernel(int iters, float a, float b, float* __restrict__ y)
+{
+    float x0 = threadIdx.x * 1e-3f, x1 = x0 + 1e-4f, x2 = x0 + 2e-4f, x3 = x0 + 3e-4f;
+    float x4 = x0 + 4e-4f, x5 = x0 + 5e-4f, x6 = x0 + 6e-4f, x7 = x0 + 7e-4f;
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            x0 = __builtin_fmaf(x0, a, b); x1 = __builtin_fmaf(x1, a, b);
+            x2 = __builtin_fmaf(x2, a, b); x3 = __builtin_fmaf(x3, a, b);
+            x4 = __builtin_fmaf(x4, a, b); x5 = __builtin_fmaf(x5, a, b);
+            x6 = __builtin_fmaf(x6, a, b); x7 = __builtin_fmaf(x7, a, b);
+        }
+    }
+    const float s = ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7));
+    if (s == 12345.0f) y[0] = s;
+}
 }  // namespace
 
 extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t stream)
 {
     gs::clear_error();
-    GS_REQUIRE(op >= 0 && op <= 4,
-               "op must be 0 (exp), 1 (log), 2 (blend exp), 3 (wave sum of 12 values) or 4 (copy)");
+    GS_REQUIRE(op >= 0 && op <= 5,
+               "op must be 0 (exp), 1 (log), 2 (blend exp), 3 (wave sum of 12 values), 4 (copy) or 5 (VALU rate)");
     GS_REQUIRE(n >= 0, "n must be >= 0");
+    if (op == 5) {
+        GS_REQUIRE(y != nullptr, "op 5 needs y (one float)");
+        if (n == 0) return GS_OK;
+        GS_TIMED("diag_valu_kernel", stream,
+                 hipLaunchKernelGGL(diag_valu_kernel, dim3(DIAG_VALU_BLOCKS), dim3(256), 0, stream, n, 0.999f, 1e-3f,
+                                    y));
+        GS_LAUNCH_CHECK("diag_valu_kernel");
+        return GS_OK;
+    }
     if (op == 3) {
         GS_REQUIRE(n == 12 * 64, "op 3 takes 12 x 64 inputs");
         hipLaunchKernelGGL(diag_sum12_kernel, dim3(1), dim3(64), 0, stream, x, y);

@@ -390,7 +390,9 @@ int gs_ply_pack(int64_t P, int32_t n_tensors, const gs_ply_tensor* tensors, cons
  * used by the kernels on n inputs (op 0 = exp, 1 = log, 2 = the blend's exp,
  * 3 = the 12-value wave reduction on 12 x 64 inputs), so tests can compare them
  * bit for bit with the CPU; op 4 copies n floats (n % 4 == 0, 16-byte aligned),
- * the known-size kernel that HBM byte counters are calibrated against.
+ * the known-size kernel that HBM byte counters are calibrated against; op 5
+ * runs 8192 blocks of 256 threads, each wave issuing 32 * n fp32 FMAs (x unused,
+ * y one float that is never written), the reference for the VALU issue rate.
  * ------------------------------------------------------------------------ */
 int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
 

@@ -318,3 +318,13 @@ def test_wave_sum12_lane_layout():
     _lib.check(_lib.load().gs_diag_math(3, 12 * 64, _lib.ptr(xt), _lib.ptr(y), None), "diag sum12")
     torch.cuda.synchronize()
     np.testing.assert_array_equal(np_(y), x.astype(np.float64).sum(1).astype(np.float32))
+
+
+def test_valu_rate_probe_runs_and_writes_nothing():
+    # the VALU issue-rate reference bench.py times: it runs, and its sentinel
+    # store is never taken
+    y = torch.full((1,), -7.0, device="cuda")
+    _lib.check(_lib.load().gs_diag_math(5, 20, None, _lib.ptr(y), None), "diag valu")
+    torch.cuda.synchronize()
+    assert float(y.item()) == -7.0
+    assert _lib.load().gs_diag_math(5, 1, None, None, None) != 0

@@ -25,6 +25,21 @@ namespace gs {
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 
+// Streaming (non-temporal) stores for large write-once outputs: the hint keeps
+// the written lines from displacing cached lines that later kernels re-read.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_stream(int* p, int v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_stream(float2* p, float2 v)
+{
+    __builtin_nontemporal_store(f32x2_t{v.x, v.y}, reinterpret_cast<f32x2_t*>(p));
+}
+__device__ __forceinline__ void st_stream(float4* p, float4 v)
+{
+    __builtin_nontemporal_store(f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4_t*>(p));
+}
+
 // exp of the core range, x finite in [-87, 88.5]
 __device__ __forceinline__ float expf_core(float x)
 {

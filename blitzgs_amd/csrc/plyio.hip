@@ -83,13 +83,14 @@ __device__ __forceinline__ void span_to_lds(const float* __restrict__ src, float
     }
 }
 
+// whole 16-byte groups leave as streaming stores (written once, not re-read)
 __device__ __forceinline__ void lds_to_span(const float* __restrict__ s, float* __restrict__ dst, int n, bool vec)
 {
     const int tid = (int)threadIdx.x;
     if (vec) {
         const int n4 = n >> 2;
         for (int q = tid; q < n4; q += PLY_THREADS)
-            reinterpret_cast<float4*>(dst)[q] = reinterpret_cast<const float4*>(s)[q];
+            gs::st_stream(&reinterpret_cast<float4*>(dst)[q], reinterpret_cast<const float4*>(s)[q]);
         for (int k = (n4 << 2) + tid; k < n; k += PLY_THREADS) dst[k] = s[k];
     } else {
         for (int k = tid; k < n; k += PLY_THREADS) dst[k] = s[k];
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(PLY_THREADS) void ply_unpack_kernel(int64_t P, cons
                 v[e] = s_rec[row * rc + cm[col]];
                 if (++col == w) { col = 0; row++; }
             }
-            reinterpret_cast<float4*>(dst)[q] = make_float4(v[0], v[1], v[2], v[3]);
+            gs::st_stream(&reinterpret_cast<float4*>(dst)[q], make_float4(v[0], v[1], v[2], v[3]));
         }
         for (int k = (n4 << 2) + tid; k < n; k += PLY_THREADS) {
             const int row = div_w(k, T.magic);

@@ -599,9 +599,10 @@ __device__ __forceinline__ void preprocess_bwd_one(
 }
 
 // Rows of dL/dsh are staged in LDS (pitch 49 floats: conflict-free column
-// writes) and copied out with fully coalesced stores: as (P,16,3) rows of 16
-// bytes in the split path (K == 16), as the (P,1,3) DC and (P,M,3) rest
-// arrays in the full path (M <= 15).
+// writes) and copied out with fully coalesced streaming stores: as (P,16,3)
+// rows of 16 bytes in the split path (K == 16), as the (P,1,3) DC and (P,M,3)
+// rest arrays in the full path (M <= 15).  (Streaming stores pay off only for
+// such whole-line writes: the 12-byte per-Gaussian rows are stored normally.)
 constexpr int SH_PITCH = 49;
 
 template <int DEG, bool STAGED, bool FULL>
@@ -666,13 +667,13 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         float* ddc = F.dL_ddc + (size_t)row0 * 3;
         for (int c = threadIdx.x; c < nrows * 3; c += 256) {
             const int r = c / 3;
-            ddc[c] = s_vis[r] ? s_sh[r * SH_PITCH + (c - 3 * r)] : 0.f;
+            gs::st_stream(&ddc[c], s_vis[r] ? s_sh[r * SH_PITCH + (c - 3 * r)] : 0.f);
         }
         const int rw = 3 * F.M;
         float* drest = F.dL_drest + (size_t)row0 * rw;
         for (int c = threadIdx.x; c < nrows * rw; c += 256) {
             const int r = c / rw;
-            drest[c] = s_vis[r] ? s_sh[r * SH_PITCH + 3 + (c - rw * r)] : 0.f;
+            gs::st_stream(&drest[c], s_vis[r] ? s_sh[r * SH_PITCH + 3 + (c - rw * r)] : 0.f);
         }
     } else if (STAGED) {
         // coalesced copy-out of this block's rows [blockIdx*256, +nrows) x 48 floats
@@ -687,7 +688,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
                 const float* src = s_sh + r * SH_PITCH + col;
                 v = make_float4(src[0], src[1], src[2], src[3]);
             }
-            dst[c] = v;
+            gs::st_stream(&dst[c], v);
         }
     }
 }

@@ -1307,15 +1307,21 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
         a = g[0]; b = g[1]; c = g[2];
         g[0] = z; g[1] = z; g[2] = z; g[3] = z;
     }
+    // streaming stores: the four gradient arrays are read once, by the
+    // preprocess backward
     float* m = g_m2d + (size_t)i * m2d_stride;
-    m[0] = a.x;
-    m[1] = a.y;
-    for (int k = 2; k < m2d_stride; k++) m[k] = 0.f;
+    gs::st_stream(&m[0], a.x);
+    gs::st_stream(&m[1], a.y);
+    for (int k = 2; k < m2d_stride; k++) gs::st_stream(&m[k], 0.f);
     if (g_m2d_abs != nullptr) {
-        g_m2d_abs[3 * (size_t)i] = a.z; g_m2d_abs[3 * (size_t)i + 1] = a.w; g_m2d_abs[3 * (size_t)i + 2] = 0.f;
+        gs::st_stream(&g_m2d_abs[3 * (size_t)i], a.z);
+        gs::st_stream(&g_m2d_abs[3 * (size_t)i + 1], a.w);
+        gs::st_stream(&g_m2d_abs[3 * (size_t)i + 2], 0.f);
     }
-    g_con[i] = b;
-    g_col[3 * (size_t)i] = c.x; g_col[3 * (size_t)i + 1] = c.y; g_col[3 * (size_t)i + 2] = c.z;
+    gs::st_stream(&g_con[i], b);
+    gs::st_stream(&g_col[3 * (size_t)i], c.x);
+    gs::st_stream(&g_col[3 * (size_t)i + 1], c.y);
+    gs::st_stream(&g_col[3 * (size_t)i + 2], c.z);
 }
 
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(SW) void ssim_bwd_kernel(int H, int W, const float*
                 d += v[0];
                 d += img1[oo] * 2.0f * v[1];
                 d += img2[oo] * v[2];
-                dL_dimg1[oo] = d;
+                gs::st_stream(&dL_dimg1[oo], d);   // streaming store: written once, not re-read here
             }
         }
     }

@@ -230,11 +230,17 @@ class _RasterizeGaussians(torch.autograd.Function):
         ctx.shapes = (tuple(dc.shape) if _given(dc) else None, tuple(sh.shape) if _given(sh) else None)
         ctx.save_for_backward(radii, geom, binning, img)
         ctx.mark_non_differentiable(radii, amc)
+        # radii and the max-count output take no gradient: not zero-filled
+        ctx.set_materialize_grads(False)
         return color, radii, amc
 
     @staticmethod
     def backward(ctx, grad_out_color, *_):
         radii, geom, binning, img = ctx.saved_tensors
+        if grad_out_color is None:
+            rs = ctx.raster_settings
+            grad_out_color = torch.zeros((3, int(rs.image_height), int(rs.image_width)), device=radii.device,
+                                         dtype=torch.float32)
         (g_m2d, g_col, g_op, g_m3d, g_cov, g_dc, g_sh, g_sc, g_rot) = _backward(
             ctx.raster_settings, ctx.x, radii, geom, ctx.R, binning, img, grad_out_color)
         x = ctx.x

@@ -150,6 +150,8 @@ class _PreprocessGaussians(torch.autograd.Function):
     def forward(ctx, means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
         num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = _preprocess_forward_raw(
             means3D, scales, rotations, sh, opacities, raster_settings)
+        # radii and depths take no gradient; unused outputs are not zero-filled
+        ctx.set_materialize_grads(False)
         ctx.raster_settings = raster_settings
         ctx.cuda_args = cuda_args
         ctx.num_rendered = num_rendered
@@ -287,8 +289,9 @@ class _RenderGaussians(torch.autograd.Function):
         if timing:
             cuda_args["stats_collector"]["forward_render_time"] = ms
         dev = means2D.device
-        out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
-        out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
+        # the geometry maps (render_geo off: zeros) share one zero fill
+        maps = torch.zeros((6, H, W), device=dev, dtype=torch.float32)
+        out_all_map, out_plane_depth = maps[:5], maps[5:]
         ctx.raster_settings = rs
         ctx.cuda_args = cuda_args
         ctx.num_rendered = R

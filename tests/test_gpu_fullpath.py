@@ -317,3 +317,30 @@ def test_render_depth_needs_scales_and_rotations(gpu):
         ras.render_depth(means3D=to_dev(scene["means3D"]), means2D=None, opacities=to_dev(scene["opacities"]),
                          culling=torch.zeros(10, dtype=torch.bool, device="cuda"), dc=to_dev(dc), shs=to_dev(rest),
                          cov3D_precomp=cov)
+
+
+def test_repeated_backward_of_one_forward(gpu):
+    """GaussianRasterizer.forward differentiated twice (retain_graph): the
+    second backward gives the first one's gradients."""
+    scene, cam = synth.small_scene(2000, seed=19, W=128, H=96, log_mu=-1.9)
+    rs = settings_for(cam, bg=(0.1, 0.1, 0.1))
+    dc, rest = _split_sh(scene)
+    leaves = {k: to_dev(v).requires_grad_() for k, v in
+              dict(means3D=scene["means3D"], opacities=scene["opacities"], scales=scene["scales"],
+                   rotations=scene["rotations"], dc=dc, rest=rest).items()}
+    means2D = torch.zeros_like(leaves["means3D"], requires_grad=True)
+    culling = torch.zeros(2000, dtype=torch.bool, device="cuda")
+    color, radii, amc = GaussianRasterizer(rs)(means3D=leaves["means3D"], means2D=means2D,
+                                               opacities=leaves["opacities"], culling=culling, dc=leaves["dc"],
+                                               shs=leaves["rest"], scales=leaves["scales"],
+                                               rotations=leaves["rotations"], flag_max_count=True)
+    loss = (color * torch.randn_like(color)).sum()
+    loss.backward(retain_graph=True)
+    first = {k: v.grad.detach().clone() for k, v in leaves.items()}
+    first_m2d = means2D.grad.detach().clone()
+    for v in list(leaves.values()) + [means2D]:
+        v.grad = None
+    loss.backward()
+    for k, v in leaves.items():
+        assert rel_l2(np_(v.grad), np_(first[k])) < 1e-5, k
+    assert rel_l2(np_(means2D.grad), np_(first_m2d)) < 1e-5

@@ -328,3 +328,45 @@ def test_valu_rate_probe_runs_and_writes_nothing():
     torch.cuda.synchronize()
     assert float(y.item()) == -7.0
     assert _lib.load().gs_diag_math(5, 1, None, None, None) != 0
+
+
+def _split_forward(scene, cam, bg):
+    from blitzgs_amd import rasterizer as R
+    rs = settings_for(cam, bg=bg)
+    params = {k: to_dev(scene[k]).requires_grad_(True) for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+    ras = R.GaussianRasterizer(rs)
+    cuda_args = {"avoid_pixel_all2all": False}
+    means2D, rgb, conic_opacity, radii, depths = ras.preprocess_gaussians(
+        params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], cuda_args)
+    P = means2D.shape[0]
+    means2D_abs = torch.zeros((P, 3), device="cuda", requires_grad=True)
+    all_map = torch.zeros((P, 5), device="cuda")
+    color = ras.render_gaussians(means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, None, None,
+                                 cuda_args)[0]
+    return params, color
+
+
+def test_autograd_interleaved_and_repeated_backward():
+    """Two cameras' forwards before either backward (each keeps its own
+    buffers), then one graph differentiated twice (retain_graph): the second
+    backward starts from cleared accumulators and repeats the first."""
+    bg = (0.1, 0.2, 0.3)
+    sA, cA = synth.small_scene(3000, seed=12, W=200, H=150, extent=1.2)
+    sB, cB = synth.small_scene(2500, seed=13, W=160, H=120, extent=1.0)
+    pA, colA = _split_forward(sA, cA, bg)
+    pB, colB = _split_forward(sB, cB, bg)
+    (colB * to_dev(sB["dL_dimage"])).sum().backward()
+    lossA = (colA * to_dev(sA["dL_dimage"])).sum()
+    lossA.backward(retain_graph=True)
+    gA1 = {k: p.grad.detach().clone() for k, p in pA.items()}
+    for p in pA.values():
+        p.grad = None
+    lossA.backward()
+    names = {"means3D": "dL_dmeans3D", "scales": "dL_dscales", "rotations": "dL_drotations", "sh": "dL_dsh",
+             "opacities": "dL_dopacity"}
+    for scene, cam, params in ((sA, cA, pA), (sB, cB, pB)):
+        _, _, _, _, pb = _grad_chain(scene, cam, bg, scene["dL_dimage"])
+        for k, n in names.items():
+            assert rel_l2(np_(params[k].grad), pb[n]) < 1e-3, (k, rel_l2(np_(params[k].grad), pb[n]))
+    for k in names:
+        assert rel_l2(np_(pA[k].grad), np_(gA1[k])) < 1e-5, k

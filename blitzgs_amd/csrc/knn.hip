@@ -6,7 +6,7 @@
 // reference's pruning is conservative, so its output is the exact 3-NN
 // statistic; it scans every box for every point (O(P^2/1024) box tests).
 //
-// Here: a uniform grid of about two points per cell is built with a counting
+// Here: a uniform grid of about three points per cell is built with a counting
 // sort (bbox reduce, cell histogram, device-wide scan, scatter), and every
 // point searches the cell shells around its own cell until the third-best
 // squared distance is below the distance to the unsearched region (computed
@@ -355,8 +355,10 @@ extern "C" int gs_knn_meandist3(int P, const float* points, float* out, void* wo
         if (ext[k] < 1e-12) ext[k] = 1e-12;
         vol *= ext[k];
     }
-    // about two points per cell, at most 1024 cells per axis and max_cells(P) in total
-    double h = cbrt(vol / ((double)P / 2.0 + 1.0));
+    // about three points per cell (measured: 2 -> 3 per cell is -11 % on a ground
+    // plane with dense clusters, -3.5 % on uniform points; 1 or >= 4 are slower),
+    // at most 1024 cells per axis and max_cells(P) in total
+    double h = cbrt(vol / ((double)P / 3.0 + 1.0));
     size_t NC = 0;
     for (int iter = 0; iter < 200; iter++) {
         NC = 1;

@@ -163,40 +163,59 @@ const T* at(const void* base, size_t off) { return reinterpret_cast<const T*>(st
 
 // compute_locally (null: every tile) -> local tile numbering and the
 // bounding box of the local tiles (meta[5..8] = x0, y0, x1, y1, exclusive
-// ends; empty box if none); clears the per-tile counters
+// ends; empty box if none); clears the per-tile counters.  One block of 16
+// waves; each wave owns a contiguous run of 64-tile rounds: it counts its
+// local tiles (ballots), one barrier publishes the 16 counts, and a second
+// walk numbers the tiles in order with coalesced loads and stores.
 __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, const uint8_t* __restrict__ cl,
                                                         int* __restrict__ loc_map, int* __restrict__ tile_of_local,
                                                         uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta)
 {
-    __shared__ uint32_t s_wave[32];
+    __shared__ uint32_t s_cnt[16];
     __shared__ uint32_t s_box[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (threadIdx.x == 0) { s_box[0] = 0xffffffffu; s_box[1] = 0xffffffffu; s_box[2] = 0u; s_box[3] = 0u; }
+    const int rounds = (T + 63) / 64;
+    const int per = (rounds + 15) / 16;
+    const int r0 = min(rounds, w * per), r1 = min(rounds, r0 + per);
+    uint32_t cnt = 0;
+    for (int r = r0; r < r1; r++) {
+        const int t = r * 64 + lane;
+        cnt += (uint32_t)__builtin_popcountll(gs::ballot(t < T && (cl == nullptr || cl[t])));
+    }
+    if (lane == 0) s_cnt[w] = cnt;
     __syncthreads();
+    uint32_t base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t c = s_cnt[i];
+        base += i < w ? c : 0u;
+        tot += c;
+    }
     uint32_t bx0 = 0xffffffffu, by0 = 0xffffffffu, bx1 = 0u, by1 = 0u;
-    uint32_t base = 0;
-    for (int t0 = 0; t0 < T; t0 += 1024) {
-        const int t = t0 + threadIdx.x;
-        const uint32_t f = (t < T && (cl == nullptr || cl[t])) ? 1u : 0u;
-        uint32_t tot;
-        const uint32_t pre = gs::block_excl_scan_1024(f, s_wave, &tot);
+    for (int r = r0; r < r1; r++) {
+        const int t = r * 64 + lane;
+        const bool f = t < T && (cl == nullptr || cl[t]);
+        const uint64_t m = gs::ballot(f);
+        const uint32_t l = base + (uint32_t)gs::rank_below(m);
         if (t < T) {
-            loc_map[t] = f ? (int)(base + pre) : -1;
-            if (f) {
-                tile_of_local[base + pre] = t;
-                const uint32_t tx = (uint32_t)t % gx, ty = (uint32_t)t / gx;
-                bx0 = min(bx0, tx); by0 = min(by0, ty);
-                bx1 = max(bx1, tx + 1); by1 = max(by1, ty + 1);
-            }
+            loc_map[t] = f ? (int)l : -1;
             tile_count[t] = 0;
         }
-        base += tot;
+        if (f) {
+            tile_of_local[l] = t;
+            const uint32_t tx = (uint32_t)t % gx, ty = (uint32_t)t / gx;
+            bx0 = min(bx0, tx); by0 = min(by0, ty);
+            bx1 = max(bx1, tx + 1); by1 = max(by1, ty + 1);
+        }
+        base += (uint32_t)__builtin_popcountll(m);
     }
     atomicMin(&s_box[0], bx0); atomicMin(&s_box[1], by0);
     atomicMax(&s_box[2], bx1); atomicMax(&s_box[3], by1);
     __syncthreads();
     if (threadIdx.x == 0) {
-        meta[0] = base;
-        const bool any = base > 0;
+        meta[0] = tot;
+        const bool any = tot > 0;
         meta[5] = any ? s_box[0] : 0u; meta[6] = any ? s_box[1] : 0u;
         meta[7] = any ? s_box[2] : 0u; meta[8] = any ? s_box[3] : 0u;
     }

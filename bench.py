@@ -761,8 +761,9 @@ def run_ply(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding of this path is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards by "
+              "Gaussians for preprocess and by tile rows for render, with an all-to-all between them, which is "
+              "not built here", file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)

@@ -523,6 +523,12 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
 
 // ------------------------------------------------------------- scatter
 
+// per-Gaussian int32 accumulators of the blend (null: not used by the mode),
+// zeroed by the scatter, which visits every Gaussian once
+struct ZeroOut {
+    int32_t* p[4];
+};
+
 // Re-walks the chunk (each wave its run, as in the count) and appends
 // (depth bits << 32 | compact index) to the chunk's reserved slice of each
 // tile bucket (LDS cursors).  Compact indices follow Gaussian id order, so
@@ -537,7 +543,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     const uint32_t* __restrict__ hist, const uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
     const uint32_t* __restrict__ wbase, uint64_t* __restrict__ sortkey, int* __restrict__ cidx_of,
     uint32_t* __restrict__ cid2id, float4* __restrict__ rec, float4* __restrict__ gacc,
-    const float2* __restrict__ rects)
+    const float2* __restrict__ rects, ZeroOut Z)
 {
     // dynamic LDS: per wave 64 staged records, then min(T, LDS_TILES) cursors
     extern __shared__ uint4 s_dyn[];
@@ -600,7 +606,12 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
         const uint32_t cidx = first + (uint32_t)rank;
         next += (uint32_t)nl;
         uint32_t dbits = 0;
-        if (i < i1) cidx_of[i] = cnt > 0 ? (int)cidx : -1;
+        if (i < i1) {
+            cidx_of[i] = cnt > 0 ? (int)cidx : -1;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (Z.p[q] != nullptr) Z.p[q][i] = 0;
+        }
         if (cnt > 0) {
             dbits = gs::f2u(dep);
             const gs::CullPrep cp = gs::cull_prepare(xy.x, xy.y, co.x, co.y, co.z, co.w);
@@ -1659,21 +1670,16 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
                        tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
     GS_LAUNCH_CHECK("ranges_kernel");
-    if (P > 0) {
-        // per-Gaussian accumulators start at zero
+    // per-Gaussian accumulators start at zero: inside the scatter when there
+    // are instances, else with a fill kernel each
+    ZeroOut Z{{mode == BLEND_SPLIT ? O.out_observe : nullptr, reinterpret_cast<int32_t*>(O.accum_max_count),
+                mode == BLEND_SIMP ? reinterpret_cast<int32_t*>(O.accum_weights) : nullptr,
+                mode == BLEND_SIMP ? O.accum_weights_count : nullptr}};
+    if (P > 0 && R == 0) {
         const dim3 zg(gs_div_up((size_t)P, 256));
-        int32_t* zero_these[3] = {mode == BLEND_SPLIT ? O.out_observe : nullptr,
-                                  reinterpret_cast<int32_t*>(O.accum_max_count),
-                                  mode == BLEND_SIMP ? reinterpret_cast<int32_t*>(O.accum_weights) : nullptr};
-        for (int32_t* z : zero_these) {
-            if (z == nullptr) continue; {
-                GS_TIMED("zero_i32_kernel", stream, hipLaunchKernelGGL(zero_i32_kernel, zg, dim3(256), 0, stream, P, z));
-            }
-            GS_LAUNCH_CHECK("zero_i32_kernel");
-        }
-        if (mode == BLEND_SIMP) {
-            GS_TIMED("zero_i32_kernel", stream,
-                     hipLaunchKernelGGL(zero_i32_kernel, zg, dim3(256), 0, stream, P, O.accum_weights_count));
+        for (int32_t* z : Z.p) {
+            if (z == nullptr) continue;
+            GS_TIMED("zero_i32_kernel", stream, hipLaunchKernelGGL(zero_i32_kernel, zg, dim3(256), 0, stream, P, z));
             GS_LAUNCH_CHECK("zero_i32_kernel");
         }
     }
@@ -1687,14 +1693,14 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
                                         hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
                                         at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
                                         at<float4>(geom, g.rec), at<float4>(geom, g.gacc),
-                                        reinterpret_cast<const float2*>(rects)));
+                                        reinterpret_cast<const float2*>(rects), Z));
         } else {
             GS_TIMED("scatter_kernel", stream,
                      hipLaunchKernelGGL(scatter_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
                                         stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
                                         hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
                                         at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
-                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc), nullptr));
+                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc), nullptr, Z));
         }
         GS_LAUNCH_CHECK("scatter_kernel");
         const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};

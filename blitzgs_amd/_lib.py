@@ -61,7 +61,7 @@ _SIGS = {
                                         _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_render_full_count": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, C.POINTER(_i64), _c]),
     "gs_render_full_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
-    "gs_render_full_depth": (_i, [_i, _i64, _i, _i] + [_c] * 20 + [_c]),
+    "gs_render_full_depth": (_i, [_i, _i64, _i, _i] + [_c] * 21 + [_c]),
     "gs_render_full_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward_full": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i, _c,
                                          _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
@@ -114,6 +114,18 @@ def check(rc, what):
     if rc != 0:
         msg = load().gs_last_error().decode(errors="replace")
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def debug_sync(debug, what):
+    """The reference's debug mode (CHECK_CUDA, _f/cuda_rasterizer/auxiliary.h:186-193):
+    wait for the device after a call and raise RuntimeError if it failed."""
+    if not debug:
+        return
+    import torch
+    try:
+        torch.cuda.synchronize()
+    except RuntimeError as e:
+        raise RuntimeError(f"{what}: {e}") from e
 
 
 def ptr(t):

@@ -38,7 +38,8 @@ class _RS:
 def preprocess_gaussians(means3D, scales, rotations, sh, opacity, scale_modifier, viewmatrix, projmatrix, tan_fovx,
                          tan_fovy, image_height, image_width, degree, campos, prefiltered, debug, args=None):
     rs = _RS(scale_modifier=scale_modifier, viewmatrix=viewmatrix, projmatrix=projmatrix, tanfovx=tan_fovx,
-             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos)
+             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos,
+             debug=debug)
     return _r._preprocess_forward_raw(means3D, scales, rotations, sh, opacity, rs)
 
 
@@ -46,7 +47,8 @@ def preprocess_gaussians_backward(radii, cov3D, clamped, means3D, scales, rotati
                                   projmatrix, tan_fovx, tan_fovy, image_height, image_width, degree, campos,
                                   dL_dmeans2D, dL_dconic_opacity, dL_dcolors, R, debug, args=None):
     rs = _RS(scale_modifier=scale_modifier, viewmatrix=viewmatrix, projmatrix=projmatrix, tanfovx=tan_fovx,
-             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos)
+             tanfovy=tan_fovy, image_height=image_height, image_width=image_width, sh_degree=degree, campos=campos,
+             debug=debug)
     return _r._preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
                                        dL_dconic_opacity, dL_dcolors)
 
@@ -58,7 +60,8 @@ def render_gaussians(background, image_height, image_width, means2D, depths, rad
     timing = _r._want_timing(args)
     H, W = int(image_height), int(image_width)
     (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
-     ms) = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing)
+     ms) = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing,
+                                  bool(debug))
     if timing:
         args["stats_collector"]["forward_render_time"] = ms
     dev = means2D.device
@@ -76,7 +79,7 @@ def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, al
     timing = _r._want_timing(args)
     dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _r._render_backward_raw(
         background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, geomBuffer, binningBuffer, imageBuffer,
-        dL_dout_color.contiguous(), 3, timing)
+        dL_dout_color.contiguous(), 3, timing, bool(debug))
     if timing:
         args["stats_collector"]["backward_render_time"] = ms
     dL_dall_map = torch.zeros((means2D.size(0), 5), device=means2D.device, dtype=torch.float32)

@@ -11,12 +11,27 @@ from blitzgs_amd.fullpath import (_RasterizeGaussians, rasterize_gaussians, rast
 from blitzgs_amd.rasterizer import (GaussianRasterizationSettings, GaussianRasterizer, _PreprocessGaussians,
                                     _RenderGaussians, preprocess_gaussians, render_gaussians)
 
-_SPLIT_C = _C
+try:
+    import diff_gaussian_rasterization_r as _split_package
+    _SPLIT_C = _split_package._C
+except ImportError:
+    _SPLIT_C = None
+
+# render ops must come from the _r package (a missing one is an error, not a
+# fallback); every other op comes from this package first
+_SPLIT_ONLY = ("render_gaussians", "render_gaussians_backward")
 
 
 def _get_split_op_backend(op_name):
-    if hasattr(_C, op_name):
-        return _C
+    """The module that provides split op `op_name` (_f __init__.py:24-46)."""
+    if op_name in _SPLIT_ONLY:
+        if _SPLIT_C is None or not hasattr(_SPLIT_C, op_name):
+            raise AttributeError(f"Missing split backend op '{op_name}': the diff_gaussian_rasterization_r "
+                                 "drop-in must be importable for the render ops")
+        return _SPLIT_C
+    for backend in (_C, _SPLIT_C):
+        if backend is not None and hasattr(backend, op_name):
+            return backend
     raise AttributeError(f"No backend provides split op '{op_name}'")
 
 

@@ -159,6 +159,7 @@ def _forward(rs, x, culling, flag_max_count, simp, depth=False):
                                        ptr(rws), ptr(binning), ptr(img), ptr(color), ptr(d["out_pts"]),
                                        ptr(d["depth"]), ptr(d["accum_alpha"]), ptr(d["gidx"]),
                                        ptr(d["discriminants"]), s), "gs_render_full_depth")
+        _lib.debug_sync(getattr(rs, "debug", False), "rasterize_gaussians_depth")
         return color, radii, d, None, None, geom, binning, img, R
     check(lib.gs_render_full_forward(P, R, W, H, ptr(x["bg"]), ptr(g["means2D"]), ptr(g["depths"]), ptr(radii),
                                      ptr(g["rects"]), ptr(g["conic"]), ptr(colors), ptr(rws), ptr(binning), ptr(img),
@@ -166,6 +167,7 @@ def _forward(rs, x, culling, flag_max_count, simp, depth=False):
                                      s), "gs_render_full_forward")
     if not (flag_max_count or simp):
         amc.zero_()
+    _lib.debug_sync(getattr(rs, "debug", False), "rasterize_gaussians")
     return color, radii, amc, aw, awc, geom, binning, img, R
 
 
@@ -205,6 +207,7 @@ def _backward(rs, x, radii, geom, R, binning, img, grad_out_color):
             ptr(g["cov3D"]), ptr(g["clamped"]), ptr(dL_dmeans2D), ptr(dL_dco), ptr(dL_dcolors), ptr(dL_dmeans3D),
             ptr(dL_dcov3D), ptr(dL_ddc), ptr(dL_dsh), ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dopacity), s),
             "gs_preprocess_backward_full")
+        _lib.debug_sync(getattr(rs, "debug", False), "rasterize_gaussians_backward")
     return dL_dmeans2D, dL_dcolors, dL_dopacity, dL_dmeans3D, dL_dcov3D, dL_ddc, dL_dsh, dL_dscales, dL_drotations
 
 

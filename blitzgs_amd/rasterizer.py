@@ -109,6 +109,7 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs):
             int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii), ptr(cov3D),
             ptr(conic_opacity), ptr(rgb), ptr(clamped), _stream(dev))
         check(rc, "gs_preprocess_forward")
+        _lib.debug_sync(getattr(rs, "debug", False), "gs_preprocess_forward")
     return 0, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped
 
 
@@ -142,6 +143,7 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
             ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
             ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
         check(rc, "gs_preprocess_backward")
+        _lib.debug_sync(getattr(rs, "debug", False), "gs_preprocess_backward")
     return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity
 
 
@@ -195,7 +197,8 @@ def _tile_mask(cl, H, W, device):
     return cl.reshape(-1).to(torch.uint8).contiguous()
 
 
-def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False):
+def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False,
+                        debug=False):
     """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
     geomBuffer, binningBuffer, imgBuffer, render_ms)."""
     _require_device(means2D, "means2D")
@@ -232,6 +235,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     check(lib.gs_render_forward(P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity),
                                 ptr(rgb), ptr(cl), ptr(geom), ptr(binning), ptr(img), ptr(color), ptr(n_render),
                                 ptr(n_consider), ptr(n_contrib), ptr(out_observe), stream), "gs_render_forward")
+    _lib.debug_sync(debug, "gs_render_forward")
     ms = None
     if timing:
         ev1.record()
@@ -241,7 +245,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
 
 
 def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img, dL_dpixels,
-                         m2d_stride=2, timing=False):
+                         m2d_stride=2, timing=False, debug=False):
     dev = means2D.device
     P = means2D.size(0)
     lib = _lib.load()
@@ -263,6 +267,7 @@ def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_local
                                  ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D), m2d_stride,
                                  ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors), _stream(dev)),
           "gs_render_backward")
+    _lib.debug_sync(debug, "gs_render_backward")
     ms = None
     if timing:
         ev1.record()
@@ -285,7 +290,8 @@ class _RenderGaussians(torch.autograd.Function):
         H, W = int(rs.image_height), int(rs.image_width)
         timing = _want_timing(cuda_args)
         (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
-         ms) = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing)
+         ms) = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing,
+                                   bool(rs.debug))
         if timing:
             cuda_args["stats_collector"]["forward_render_time"] = ms
         dev = means2D.device
@@ -312,7 +318,7 @@ class _RenderGaussians(torch.autograd.Function):
         timing = _want_timing(ctx.cuda_args)
         dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
             rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
-            grad_color.contiguous(), 2, timing)
+            grad_color.contiguous(), 2, timing, bool(rs.debug))
         if timing:
             ctx.cuda_args["stats_collector"]["backward_render_time"] = ms
         dL_dall_map = None

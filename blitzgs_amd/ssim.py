@@ -62,33 +62,40 @@ def fusedssim_backward(C1, C2, img1, img2, dL_dmap, dm_dmu1, dm_dsigma1_sq, dm_d
     return g
 
 
+# the loss window's half width: "valid" drops this many pixels on every side
+_BORDER = 5
+_SSIM_C1 = 0.01 ** 2
+_SSIM_C2 = 0.03 ** 2
+
+
+def _interior(t):
+    return t[..., _BORDER:t.shape[-2] - _BORDER, _BORDER:t.shape[-1] - _BORDER]
+
+
 class FusedSSIMMap(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, C1, C2, img1, img2, padding="same", train=True):
-        ssim_map, dm_dmu1, dm_dsigma1_sq, dm_dsigma12 = fusedssim(C1, C2, img1, img2, train)
-        if padding == "valid":
-            ssim_map = ssim_map[:, :, 5:-5, 5:-5]
-        ctx.save_for_backward(img1.detach(), img2, dm_dmu1, dm_dsigma1_sq, dm_dsigma12)
-        ctx.C1 = C1
-        ctx.C2 = C2
-        ctx.padding = padding
-        return ssim_map
+    """Autograd node of the SSIM map (fused_ssim/__init__.py:8-35): the
+    gradient flows to img1 only; "valid" returns the map without its 5-pixel
+    border, whose gradient is zero."""
 
     @staticmethod
-    def backward(ctx, opt_grad):
+    def forward(ctx, C1, C2, img1, img2, padding="same", train=True):
+        full_map, *partials = fusedssim(C1, C2, img1, img2, train)
+        ctx.consts = (C1, C2)
+        ctx.valid = padding == "valid"
+        ctx.save_for_backward(img1.detach(), img2, *partials)
+        return _interior(full_map) if ctx.valid else full_map
+
+    @staticmethod
+    def backward(ctx, grad_map):
         img1, img2, dm_dmu1, dm_dsigma1_sq, dm_dsigma12 = ctx.saved_tensors
-        C1, C2, padding = ctx.C1, ctx.C2, ctx.padding
-        dL_dmap = opt_grad
-        if padding == "valid":
-            dL_dmap = torch.zeros_like(img1)
-            dL_dmap[:, :, 5:-5, 5:-5] = opt_grad
-        grad = fusedssim_backward(C1, C2, img1, img2, dL_dmap, dm_dmu1, dm_dsigma1_sq, dm_dsigma12)
-        return None, None, grad, None, None, None
+        if ctx.valid:
+            grad_map = torch.nn.functional.pad(grad_map, (_BORDER,) * 4)
+        dL_dimg1 = fusedssim_backward(*ctx.consts, img1, img2, grad_map, dm_dmu1, dm_dsigma1_sq, dm_dsigma12)
+        return None, None, dL_dimg1, None, None, None
 
 
 def fused_ssim(img1, img2, padding="same", train=True):
-    C1 = 0.01 ** 2
-    C2 = 0.03 ** 2
-    assert padding in allowed_padding
-    map = FusedSSIMMap.apply(C1, C2, img1, img2, padding, train)
-    return map.mean()
+    """Mean SSIM of img1 against img2 (fused_ssim/__init__.py:37-41)."""
+    if padding not in allowed_padding:
+        raise AssertionError(f"padding must be one of {allowed_padding}, got {padding!r}")
+    return FusedSSIMMap.apply(_SSIM_C1, _SSIM_C2, img1, img2, padding, train).mean()

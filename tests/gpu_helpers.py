@@ -88,3 +88,96 @@ def rel_l2(got, ref):
     ref = np.asarray(ref, np.float64)
     den = np.linalg.norm(ref)
     return float(np.linalg.norm(got - ref) / (den if den > 0 else 1.0))
+
+
+# ------------------------------------------------ full autograd step vs oracle
+
+PARAM_KEYS = ("means3D", "scales", "rotations", "sh", "opacities")
+GRAD_NAMES = {"means3D": "dL_dmeans3D", "scales": "dL_dscales", "rotations": "dL_drotations", "sh": "dL_dsh",
+              "opacities": "dL_dopacity"}
+
+
+def autograd_step(scene, cam, bg=(0.0, 0.0, 0.0), cl=None, ext=None, avoid=False, dL_dimage=None, loss_fn=None):
+    """One training step through the drop-in autograd API, in the order
+    gaussian_renderer uses it (preprocess_gaussians -> retain_grad on means2D ->
+    render_gaussians with a means2D_abs leaf -> backward).  cl / ext: the
+    compute_locally and extended_compute_locally tile masks (numpy, or None);
+    avoid: cuda_args["avoid_pixel_all2all"].  The backward takes dL/dimage
+    (dL_dimage) or the gradient of loss_fn(color).  Returns the forward
+    outputs, the seven gradients and the render's saved buffers."""
+    from blitzgs_amd.rasterizer import GaussianRasterizer
+    rs = settings_for(cam, bg=bg)
+    params = {k: to_dev(scene[k]).requires_grad_(True) for k in PARAM_KEYS}
+    ras = GaussianRasterizer(rs)
+    cuda_args = {"avoid_pixel_all2all": bool(avoid), "stats_collector": {}}
+    means2D, rgb, conic_opacity, radii, depths = ras.preprocess_gaussians(
+        params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], cuda_args)
+    means2D.retain_grad()
+    P = means2D.shape[0]
+    means2D_abs = torch.zeros((P, 3), device="cuda", requires_grad=True) + 0
+    means2D_abs.retain_grad()
+    all_map = torch.zeros((P, 5), device="cuda")
+    dcl = None if cl is None else to_dev(np.asarray(cl, np.uint8)).bool()
+    dext = None if ext is None else to_dev(np.asarray(ext, np.uint8)).bool()
+    color, n_render, n_consider, n_contrib, out_observe, _, _ = ras.render_gaussians(
+        means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, dcl, dext, cuda_args)
+    node = color.grad_fn
+    R = int(node.num_rendered)
+    geom, binning, img = node.saved_tensors[5:8]
+    views = buffer_views(R, int(cam["W"]), int(cam["H"]), binning, img)
+    if loss_fn is None:
+        torch.autograd.backward([color], [to_dev(dL_dimage)])
+    else:
+        loss_fn(color).backward()
+    torch.cuda.synchronize()
+    out = dict(R=R, color=color, n_render=n_render, n_consider=n_consider, n_contrib=n_contrib,
+               out_observe=out_observe, means2D=means2D, rgb=rgb, conic_opacity=conic_opacity, radii=radii,
+               depths=depths, dL_dmeans2D=means2D.grad, dL_dmeans2D_abs=means2D_abs.grad, stats=cuda_args,
+               **views)
+    for k in PARAM_KEYS:
+        out[GRAD_NAMES[k]] = params[k].grad
+    return out
+
+
+def oracle_step(scene, cam, bg=(0.0, 0.0, 0.0), cl_fwd=None, cl_bwd=None, dL_dimage=None, dL_dimage_fn=None):
+    """The CPU oracle's forward (tile mask cl_fwd) and backward (mask cl_bwd,
+    over the forward's lists and per-pixel state).  dL/dimage is given, or
+    computed from the oracle's image by dL_dimage_fn."""
+    from oracle import oracle as O
+    bgv = np.asarray(bg, np.float32)
+    pre, bn, rf = O.full_forward(cam, scene, bg=bgv, compute_locally=cl_fwd)
+    dLd = dL_dimage if dL_dimage_fn is None else dL_dimage_fn(rf["color"])
+    rb = O.render_bwd(cam["W"], cam["H"], bgv, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"],
+                      bn["point_list"], rf["final_T"], rf["n_contrib_px"], dLd, cl_bwd)
+    pb = O.preprocess_bwd(cam, scene["means3D"], scene["scales"], scene["rotations"], scene["sh"], pre["radii"],
+                          pre["cov3D"], pre["clamped"], rb["dL_dmeans2D"], rb["dL_dconic_opacity"], rb["dL_dcolors"])
+    return pre, bn, rf, rb, pb
+
+
+def check_step(g, pre, bn, rf, rb, pb, tol=1e-3, binning=True):
+    """The bar: preprocess outputs, binning arrays, image and per-pixel /
+    per-tile counters bit-exact; the seven gradients within tol relative L2."""
+    for k in ("means2D", "depths", "radii", "conic_opacity", "rgb"):
+        assert_bitexact(np_(g[k]), pre[k], k)
+    assert g["R"] == bn["R"], (g["R"], bn["R"])
+    if binning:
+        assert_bitexact(np_(g["point_list"]).view(np.uint32), bn["point_list"], "point_list")
+        assert_bitexact(np_(g["keys"]).view(np.uint64), bn["keys"], "point_list_keys")
+    assert_bitexact(np_(g["ranges"]).view(np.uint32), bn["ranges"], "ranges")
+    assert_bitexact(np_(g["color"]), rf["color"], "color")
+    assert_bitexact(np_(g["final_T"]), rf["final_T"], "final_T")
+    assert_bitexact(np_(g["n_contrib_px"]).view(np.uint32), rf["n_contrib_px"], "n_contrib (pixel)")
+    assert_bitexact(np_(g["out_observe"]), rf["out_observe"], "out_observe")
+    assert_bitexact(np_(g["n_render"]), rf["n_render"], "n_render")
+    assert_bitexact(np_(g["n_consider"]), rf["n_consider"], "n_consider")
+    assert_bitexact(np_(g["n_contrib"]), rf["n_contrib"], "n_contrib (tile)")
+    errs = {"dL_dmeans2D": rel_l2(np_(g["dL_dmeans2D"]), rb["dL_dmeans2D"][:, :2]),
+            "dL_dmeans2D_abs": rel_l2(np_(g["dL_dmeans2D_abs"]), rb["dL_dmeans2D_abs"])}
+    for k in PARAM_KEYS:
+        n = GRAD_NAMES[k]
+        errs[n] = rel_l2(np_(g[n]), pb[n])
+    bad = {k: v for k, v in errs.items() if not v < tol}
+    assert not bad, f"gradients above {tol} relative L2: {bad} (all: {errs})"
+    # the gradients are not trivially zero
+    assert np.linalg.norm(pb["dL_dsh"]) > 0 and np.linalg.norm(rb["dL_dmeans2D"]) > 0
+    return errs

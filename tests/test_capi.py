@@ -34,6 +34,52 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) <= set(_lib.exported_symbols())
 
 
+def _declarations():
+    """{name: (return type, [parameter types])} of every entry point in the header."""
+    src = open(os.path.join(ROOT, "include", "blitzgs_amd.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    src = re.sub(r"#[^\n]*", "", src)
+    out = {}
+    for m in re.finditer(r"([A-Za-z_][\w ]*?[\s\*]+)(gs_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", src):
+        ret, name, params = m.group(1).strip(), m.group(2), m.group(3).strip()
+        types = []
+        if params and params != "void":
+            for prm in params.split(","):
+                prm = " ".join(prm.split())
+                # drop the parameter name: the last identifier
+                types.append(re.sub(r"\s*\b\w+$", "", prm).strip() if not prm.endswith("*") else prm)
+        out[name] = (ret, types)
+    return out
+
+
+def _ctype_class(decl):
+    """The ctypes class a C parameter type must be bound with."""
+    if "*" in decl or decl == "gs_stream_t":
+        return "pointer"
+    base = decl.replace("const ", "").strip()
+    return {"int": C.c_int, "int32_t": C.c_int32, "int64_t": C.c_int64, "float": C.c_float,
+            "size_t": C.c_size_t}[base]
+
+
+def test_binding_signatures_match_the_header():
+    """Every argtypes entry of the ctypes binding has the arity and the kind
+    (pointer / int / int64 / float) of the header's declaration, so a call
+    with a missing or extra argument cannot pass silently."""
+    decls = _declarations()
+    assert len(decls) >= 30
+    for name, (res, args) in _lib._SIGS.items():
+        assert name in decls, name
+        ret, params = decls[name]
+        assert len(args) == len(params), (name, len(args), len(params))
+        for i, (a, p) in enumerate(zip(args, params)):
+            want = _ctype_class(p)
+            if want == "pointer":
+                assert a is C.c_void_p or a is C.c_char_p or hasattr(a, "_type_") and issubclass(a, C._Pointer), \
+                    (name, i, p, a)
+            else:
+                assert a is want, (name, i, p, a)
+
+
 def test_workspace_queries(lib):
     g = lib.gs_render_geom_bytes(6_000_000, 1600, 1066)
     assert g % 256 == 0 and g > 4 * 100 * 67

@@ -9,8 +9,10 @@ on size or against the oracle where it finishes in seconds:
   bit-identical, every other tile is empty;
 * config 4: distCUDA2 over all 10M points, checked bit for bit at 2048 sampled
   points against a brute force over all points (torch, the reference's
-  distance expression with separately rounded operations); fused_ssim on the
-  8 x 3 x 1080 x 1920 pair against the oracle on two of the images.
+  distance expression with separately rounded operations) and at every point
+  against the CPU oracle; fused_ssim on the 8 x 3 x 1080 x 1920 pair (map, the
+  three partial derivatives and the backward) against the oracle on two of
+  the images.
 """
 import numpy as np
 import pytest
@@ -104,12 +106,28 @@ def test_config4_knn_10m_sampled_bruteforce(gpu):
     _bitexact(out[idx], ref, "distCUDA2 at sampled points")
 
 
+def test_config4_knn_10m_vs_oracle(gpu):
+    # every one of the 10M outputs against the CPU oracle (exact 3-NN, the
+    # reference's distance expression): bit-exact
+    from blitzgs_amd.knn import distCUDA2
+    pts = synth.config4_points()
+    out = np_(distCUDA2(to_dev(pts)))
+    _bitexact(out, O.knn_meandist3(pts), "distCUDA2 over all 10M points")
+
+
 def test_config4_ssim_batch_vs_oracle(gpu):
-    from blitzgs_amd.ssim import fusedssim
+    from blitzgs_amd.ssim import fusedssim, fusedssim_backward
     a, b = synth.config4_images()
-    m, d1, d2, d3 = fusedssim(0.01 ** 2, 0.03 ** 2, to_dev(a), to_dev(b), True)
+    C1, C2 = 0.01 ** 2, 0.03 ** 2
+    da, db = to_dev(a), to_dev(b)
+    m, d1, d2, d3 = fusedssim(C1, C2, da, db, True)
+    dL = np.random.default_rng(44).standard_normal(a.shape).astype(np.float32)
+    g = fusedssim_backward(C1, C2, da, db, to_dev(dL), d1, d2, d3)
     for i in (0, 7):
         om, od1, od2, od3 = O.ssim_fwd(a[i:i + 1], b[i:i + 1])
         _bitexact(np_(m[i:i + 1]), om, f"ssim map image {i}")
         _bitexact(np_(d1[i:i + 1]), od1, f"dm_dmu1 image {i}")
+        _bitexact(np_(d2[i:i + 1]), od2, f"dm_dsigma1_sq image {i}")
         _bitexact(np_(d3[i:i + 1]), od3, f"dm_dsigma12 image {i}")
+        og = O.ssim_bwd(a[i:i + 1], b[i:i + 1], dL[i:i + 1], od1, od2, od3)
+        _bitexact(np_(g[i:i + 1]), og, f"dL_dimg1 image {i}")

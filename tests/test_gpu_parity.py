@@ -370,3 +370,64 @@ def test_autograd_interleaved_and_repeated_backward():
             assert rel_l2(np_(params[k].grad), pb[n]) < 1e-3, (k, rel_l2(np_(params[k].grad), pb[n]))
     for k in names:
         assert rel_l2(np_(pA[k].grad), np_(gA1[k])) < 1e-5, k
+
+
+def _dilate(m):
+    """A tile mask grown by one tile in every direction (a wider extended mask)."""
+    d = m.copy()
+    d[1:] |= m[:-1]
+    d[:-1] |= m[1:]
+    d[:, 1:] |= m[:, :-1]
+    d[:, :-1] |= m[:, 1:]
+    return d
+
+
+@pytest.mark.parametrize("avoid", [False, True])
+def test_masked_step_and_extended_mask_vs_oracle(avoid):
+    """The masked render through the autograd API, forward and backward
+    (render backward under compute_locally, backward.cu:354-355).  With
+    avoid_pixel_all2all the forward bins and blends the wider
+    extended_compute_locally and the backward differentiates only the
+    compute_locally tiles over the forward's lists (_f __init__.py:231)."""
+    from tests.gpu_helpers import autograd_step, check_step, oracle_step
+    scene, cam = synth.small_scene(8000, seed=91, W=331, H=203, extent=1.5, log_mu=-2.3)
+    gx, gy = (331 + 15) // 16, (203 + 15) // 16
+    rng = np.random.default_rng(17)
+    cl = (rng.random((gy, gx)) < 0.35).astype(np.uint8)
+    ext = _dilate(cl)
+    assert ext.sum() > cl.sum()
+    bg = (0.2, 0.4, 0.1)
+    g = autograd_step(scene, cam, bg=bg, cl=cl, ext=ext, avoid=avoid, dL_dimage=scene["dL_dimage"])
+    fwd_mask = ext if avoid else cl
+    pre, bn, rf, rb, pb = oracle_step(scene, cam, bg=bg, cl_fwd=fwd_mask, cl_bwd=cl, dL_dimage=scene["dL_dimage"])
+    check_step(g, pre, bn, rf, rb, pb)
+    if avoid:
+        # the extended-only tiles are rendered but give no gradient: the
+        # same step with dL/dimage zeroed outside compute_locally matches
+        pre2, bn2, rf2, rb2, pb2 = oracle_step(scene, cam, bg=bg, cl_fwd=ext, cl_bwd=ext,
+                                               dL_dimage=_masked_pixels(scene["dL_dimage"], cl))
+        for k in ("dL_dmeans3D", "dL_dsh"):
+            assert rel_l2(np_(g[k]), pb2[k]) < 1e-3, k
+
+
+def _masked_pixels(img, cl):
+    m = np.repeat(np.repeat(cl.astype(bool), 16, 0), 16, 1)[:img.shape[1], :img.shape[2]]
+    return np.where(m[None], img, 0).astype(np.float32)
+
+
+def test_masked_step_more_than_16384_local_tiles_vs_oracle():
+    """A masked image with more local tiles than the LDS histogram holds: the
+    mask numbering kernel and the global-atomics count / scatter path run
+    together, forward and backward, plain and extended masks."""
+    from tests.gpu_helpers import autograd_step, check_step, oracle_step
+    W, H = 2304, 2048                     # 144 x 128 = 18432 tiles
+    scene, cam = synth.small_scene(20000, seed=5, W=W, H=H, extent=1.6, log_mu=-3.6, log_sd=0.3)
+    gx, gy = 144, 128
+    rng = np.random.default_rng(23)
+    cl = (rng.random((gy, gx)) < 0.93).astype(np.uint8)
+    assert cl.sum() > 16384
+    ext = _dilate(cl)
+    g = autograd_step(scene, cam, cl=cl, ext=ext, avoid=True, dL_dimage=scene["dL_dimage"])
+    pre, bn, rf, rb, pb = oracle_step(scene, cam, cl_fwd=ext, cl_bwd=cl, dL_dimage=scene["dL_dimage"])
+    assert bn["R"] > 100_000
+    check_step(g, pre, bn, rf, rb, pb)

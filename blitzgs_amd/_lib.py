@@ -53,6 +53,7 @@ _SIGS = {
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
     "gs_knn_workspace_bytes": (_sz, [_i]),
     "gs_knn_meandist3": (_i, [_i, _c, _c, _c, _c]),
+    "gs_knn_meandist3_noalloc": (_i, [_i, _c, _c, _c]),
     "gs_ssim_forward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c]),
     "gs_ssim_backward": (_i, [_i, _i, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_adam_update": (_i, [_c, _c, _c, _c, _c, _f, _f, _f, _f, _i64, _i64, _c]),

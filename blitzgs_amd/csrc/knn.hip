@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "gs_device.h"
 #include "gs_host.h"
@@ -29,7 +30,7 @@ namespace {
 constexpr int RED_BLOCKS = 1024;
 constexpr int SCAN_BLOCK = 1024;
 
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KnnLayout {
     size_t partial, cell_of, count, start, blocksum, sorted, total;
@@ -37,11 +38,11 @@ struct KnnLayout {
 
 // upper bound on the grid's cell count (the host grid rule enlarges the cell
 // size until it holds, e.g. for flat or degenerate point sets)
-size_t max_cells(int P) { return 2 * (size_t)P + 1024; }
+constexpr size_t max_cells(int P) { return 2 * (size_t)P + 1024; }
 
-KnnLayout knn_layout(int P)
+constexpr KnnLayout knn_layout(int P)
 {
-    KnnLayout l;
+    KnnLayout l{};
     const size_t NCmax = max_cells(P);
     size_t o = 0;
     l.partial = o; o = align256(o + sizeof(float) * 6 * RED_BLOCKS);
@@ -319,12 +320,14 @@ __global__ __launch_bounds__(256) void knn_query_kernel(int P, Grid g, const uin
 
 extern "C" size_t gs_knn_workspace_bytes(int P) { return knn_layout(P < 0 ? 0 : P).total; }
 
-extern "C" int gs_knn_meandist3(int P, const float* points, float* out, void* workspace, hipStream_t stream)
+namespace {
+
+// grid build + query over the caller's (or the scratch) workspace of
+// knn_layout(P).total bytes; every workspace array is written before it is
+// read (the cell counters by a fill kernel), so its previous contents do not
+// matter
+int knn_impl(int P, const float* points, float* out, void* workspace, hipStream_t stream)
 {
-    gs::clear_error();
-    GS_REQUIRE(P >= 0, "P must be >= 0");
-    if (P == 0) return GS_OK;
-    GS_REQUIRE(workspace != nullptr, "workspace must be non-null (gs_knn_workspace_bytes)");
     const KnnLayout L = knn_layout(P);
     float* partial = at<float>(workspace, L.partial);
     uint32_t* cell_of = at<uint32_t>(workspace, L.cell_of);
@@ -407,4 +410,72 @@ extern "C" int gs_knn_meandist3(int P, const float* points, float* out, void* wo
     GS_LAUNCH_CHECK("knn_query_kernel");
     GS_HIP(hipStreamSynchronize(stream));
     return GS_OK;
+}
+
+}  // namespace
+
+extern "C" int gs_knn_meandist3(int P, const float* points, float* out, void* workspace, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0");
+    if (P == 0) return GS_OK;
+    GS_REQUIRE(workspace != nullptr, "workspace must be non-null (gs_knn_workspace_bytes)");
+    return knn_impl(P, points, out, workspace, stream);
+}
+
+// ---------------------------------------------------------- allocation-free
+//
+// gs_knn_meandist3_noalloc: the same computation with its workspace in a
+// file-scope device array instead of caller memory, for callers that cannot
+// allocate (graph capture, serving loops).  Each GPU the library runs on holds
+// its own copy of the array (KNN_SCRATCH_BYTES, about 38 MB) until the process
+// ends.  In host code `scratch` names a host-side stand-in, never the device
+// memory: the per-device address comes from hipGetSymbolAddress on the first
+// call on each device and only that address is passed to kernels and copies.
+
+constexpr int KNN_NOALLOC_MAX_P = 1 << 20;
+constexpr size_t KNN_SCRATCH_BYTES = knn_layout(KNN_NOALLOC_MAX_P).total;
+static_assert(KNN_SCRATCH_BYTES % 256 == 0, "scratch size");
+
+static __device__ __align__(256) unsigned char scratch[KNN_SCRATCH_BYTES];
+
+namespace {
+constexpr int KNN_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[KNN_MAX_DEVICES] = {};
+
+// the current device's copy of `scratch` (looked up once per device)
+int scratch_of_current_device(void** out)
+{
+    int dev = -1;
+    GS_HIP(hipGetDevice(&dev));
+    GS_REQUIRE(dev >= 0 && dev < KNN_MAX_DEVICES, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        GS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        GS_REQUIRE(p != nullptr, "no device address for the scratch array on device %d", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_knn_meandist3_noalloc(int P, const float* points, float* out, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0, "P must be >= 0");
+    GS_REQUIRE(P <= KNN_NOALLOC_MAX_P, "P = %d exceeds the allocation-free limit of %d points", P,
+               KNN_NOALLOC_MAX_P);
+    if (P == 0) return GS_OK;
+    if (stream != nullptr) {
+        int cur = -1, sdev = -1;
+        GS_HIP(hipGetDevice(&cur));
+        GS_HIP(hipStreamGetDevice(stream, &sdev));
+        GS_REQUIRE(sdev == cur, "stream belongs to device %d, the current device is %d", sdev, cur);
+    }
+    void* ws = nullptr;
+    if (int rc = scratch_of_current_device(&ws); rc != GS_OK) return rc;
+    return knn_impl(P, points, out, ws, stream);
 }

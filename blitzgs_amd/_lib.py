@@ -51,6 +51,7 @@ _SIGS = {
     "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
+    "gs_render_point_list": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c]),
     "gs_knn_workspace_bytes": (_sz, [_i]),
     "gs_knn_meandist3": (_i, [_i, _c, _c, _c, _c]),
     "gs_knn_meandist3_noalloc": (_i, [_i, _c, _c, _c]),

@@ -40,6 +40,7 @@ struct TimingState {
     bool on = false;
     std::vector<hipEvent_t> pool;
     std::vector<PendingMark> pending;
+    std::vector<PendingMark> open_stages;   // stages begun and not yet ended
     std::vector<std::string> names;
     std::vector<double> total_ms;
     std::vector<int> counts;
@@ -98,6 +99,28 @@ void timing_mark_end(hipStream_t stream)
     m.stop = take_event(t);
     if (m.stop) (void)hipEventRecord(m.stop, stream);
 }
+void timing_stage_begin(hipStream_t stream, const char* name)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    PendingMark m{name, take_event(t), nullptr};
+    if (m.start) (void)hipEventRecord(m.start, stream);
+    t.open_stages.push_back(m);
+}
+void timing_stage_end(hipStream_t stream, const char* name)
+{
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lk(t.mu);
+    for (size_t i = t.open_stages.size(); i-- > 0;) {
+        if (t.open_stages[i].name != name) continue;
+        PendingMark m = t.open_stages[i];
+        t.open_stages.erase(t.open_stages.begin() + (long)i);
+        m.stop = take_event(t);
+        if (m.stop) (void)hipEventRecord(m.stop, stream);
+        t.pending.push_back(m);
+        return;
+    }
+}
 }  // namespace gs
 
 extern "C" int gs_timing_enable(int on)
@@ -113,6 +136,9 @@ extern "C" int gs_timing_reset(void)
     TimingState& t = timing();
     std::lock_guard<std::mutex> lk(t.mu);
     drain(t);
+    for (auto& m : t.open_stages)
+        if (m.start) t.pool.push_back(m.start);
+    t.open_stages.clear();
     t.names.clear(); t.total_ms.clear(); t.counts.clear();
     return GS_OK;
 }
@@ -155,6 +181,7 @@ __global__ void diag_math_kernel(int op, int n, const float* __restrict__ x, flo
     float r;
     if (op == 0) r = gs::expf_full(v);
     else if (op == 1) r = gs::logf_full(v);
+    else if (op == 6) gs::blend_alpha(1.0f, v, gs::alpha_cut_power(1.0f), r);
     else r = (v <= 0.0f || v != v) ? gs::expf_nonpos(v) : gs::expf_full(v);
     y[i] = r;
 }
@@ -193,8 +220,9 @@ __global__ __launch_bounds__(256) void diag_valu_kernel(int iters, float a, floa
 extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t stream)
 {
     gs::clear_error();
-    GS_REQUIRE(op >= 0 && op <= 5,
-               "op must be 0 (exp), 1 (log), 2 (blend exp), 3 (wave sum of 12 values), 4 (copy) or 5 (VALU rate)");
+    GS_REQUIRE(op >= 0 && op <= 6,
+               "op must be 0 (exp), 1 (log), 2 (exact blend exp), 3 (wave sum of 12 values), 4 (copy), "
+               "5 (VALU rate) or 6 (the blend's falloff G)");
     GS_REQUIRE(n >= 0, "n must be >= 0");
     if (op == 5) {
         GS_REQUIRE(y != nullptr, "op 5 needs y (one float)");

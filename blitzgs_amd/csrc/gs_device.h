@@ -3,8 +3,9 @@
 // The library is compiled with -ffp-contract=off: a*b+c is never fused
 // implicitly, every fused multiply-add is an explicit __builtin_fmaf, and fp32
 // division and sqrt are correctly rounded (HIP's default).  Together with the
-// fixed operation order below this makes the per-Gaussian preprocess, the tile
-// keys and the forward blend bit-reproducible on a CPU.
+// fixed operation order below this makes the per-Gaussian preprocess and the
+// tile keys bit-reproducible on a CPU; the blend's falloff uses the hardware
+// exp2 (expf_fast), with the exact exp around each Gaussian's alpha cut-off.
 //
 // gs_expf / gs_logf are written from the mathematics:
 //   exp: Cody-Waite reduction x = k*ln2 + r, ln2 split into a 16-bit high part
@@ -74,6 +75,37 @@ __device__ __forceinline__ float expf_nonpos(float x)
     return (x != x) ? x : e;
 }
 
+// The blend's Gaussian falloff G = exp(power), power <= 0 or NaN: the
+// hardware exp2 (v_exp_f32) of power * log2(e).  Relative to the exact
+// expf_nonpos it is off by at most ~1e-5 for power >= -87 (the rounding of
+// the product, ~|power| * 6e-8, plus about one ulp); below that both are far
+// under 1/255.  NaN stays NaN.
+__device__ __forceinline__ float expf_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
+// The power at which opacity * exp(power) = 1/255, -log(255 * opacity), is
+// each Gaussian's alpha cut-off (computed once per Gaussian with logf_full,
+// below).  ALPHA_GUARD is the half-width of the window around it in which
+// blend_alpha evaluates G exactly: 3e-5 in power, i.e. a relative window of
+// 3e-5 in opacity * G, far above the fast exp's error there (power >= -6 for
+// opacity >= 1/255: <= ~5e-7) plus the cut-off's own rounding (~1e-6).
+constexpr float ALPHA_GUARD = 3e-5f;
+
+// alpha = min(0.99, opacity * G) of one (pixel, Gaussian) evaluation with the
+// fast exp; where power lies within ALPHA_GUARD of the Gaussian's cut-off
+// power (any lane of the wave), G is the exact expf_nonpos instead, so the
+// decision alpha >= 1/255 is the one the exact evaluation makes.  The window
+// test needs only power, not the exp, so the exp's latency overlaps it.  G is
+// returned too.
+__device__ __forceinline__ float blend_alpha(float opacity, float power, float cut_power, float& G)
+{
+    const bool near = __builtin_fabsf(power - cut_power) <= ALPHA_GUARD;
+    G = expf_fast(power);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(near) != 0, 0)) {
+        if (near) G = expf_nonpos(power);
+    }
+    return __builtin_fminf(0.99f, opacity * G);
+}
+
 __device__ __forceinline__ float logf_full(float x)
 {
     if (x != x) return x;
@@ -98,6 +130,10 @@ __device__ __forceinline__ float logf_full(float x)
 }
 
 // (int) cast with the reference's device semantics: truncate, saturate, NaN -> 0
+// the power at which opacity * exp(power) reaches 1/255 (blend_alpha's
+// window centre): NaN for a NaN opacity, +inf for opacity 0
+__device__ __forceinline__ float alpha_cut_power(float opacity) { return -logf_full(255.0f * opacity); }
+
 __device__ __forceinline__ int f2i_sat(float x)
 {
     if (x != x) return 0;

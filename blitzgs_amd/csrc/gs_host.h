@@ -16,6 +16,10 @@ void clear_error();
 bool timing_on();
 void timing_mark_begin(hipStream_t stream, const char* name);
 void timing_mark_end(hipStream_t stream);
+// A named stage spanning several launches (and entry points) on one stream:
+// its time runs from the begin mark to the end mark of the same name.
+void timing_stage_begin(hipStream_t stream, const char* name);
+void timing_stage_end(hipStream_t stream, const char* name);
 }  // namespace gs
 
 #define GS_TIMED(name, stream, launch)                                                 \

@@ -67,13 +67,14 @@ constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys pe
 constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
 constexpr int64_t SIDE_STREAM_MIN_R = 1 << 21;   // instances from which the size classes sort concurrently
 constexpr int BIG_SORT_THREADS = 1024;
+constexpr const char* BINNING_STAGE = "binning (wall)";   // per-kernel timing: the whole binning stage
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
 // record of 4 x float4 at its compact index:
 //   [0] mean x, mean y, conic a, conic b
 //   [1] conic c, opacity, red, green
 //   [2] blue, cull threshold, cull slopes -b/c and -b/a
-//   [3] Gaussian id bits, 0, 0, 0
+//   [3] Gaussian id bits, alpha cut-off power -log(255 opacity), 0, 0
 // so the blend gathers one aligned 64-byte segment per list entry.
 constexpr size_t REC_BYTES = 64;
 // Per-Gaussian gradient accumulator of the backward (16 floats, 11 used):
@@ -619,7 +620,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
             sp[0] = make_float4(xy.x, xy.y, co.x, co.y);
             sp[1] = make_float4(co.z, co.w, col.x, col.y);
             sp[2] = make_float4(col.z, cp.thresh, cp.nbc, cp.nba);
-            sp[3] = make_float4(__uint_as_float((uint32_t)i), 0.f, 0.f, 0.f);
+            sp[3] = make_float4(__uint_as_float((uint32_t)i), gs::alpha_cut_power(co.w), 0.f, 0.f);
             cid2id[cidx] = (uint32_t)i;
         }
         // the group's records and zeroed accumulators are one contiguous run:
@@ -692,30 +693,20 @@ __device__ __forceinline__ void bitonic(uint64_t* s, int n, int N)
     }
 }
 
-// sorted bucket -> Gaussian ids, tile|depth keys and the blend's compact list
-struct SortOut {
-    const uint32_t* cid2id;
-    uint32_t* point_list;
-    uint64_t* keys;
-    uint32_t* clist;
-};
-
-__device__ __forceinline__ void write_sorted(uint32_t tile, uint32_t start, int n, const uint64_t* src,
-                                             const SortOut& o, int nt)
+// A sorted bucket is written as the blend's compact list only (clist: compact
+// index per list position).  The reference's sorted Gaussian ids and
+// (tile << 32 | depth bits) keys are derived from it on request
+// (pointlist_kernel, gs_render_point_list).
+__device__ __forceinline__ void write_sorted(uint32_t start, int n, const uint64_t* src, uint32_t* __restrict__ clist,
+                                             int nt)
 {
-    for (int i = threadIdx.x; i < n; i += nt) {
-        const uint64_t k = src[i];
-        const uint32_t cx = (uint32_t)k;
-        o.clist[start + i] = cx;
-        o.point_list[start + i] = o.cid2id[cx];
-        o.keys[start + i] = ((uint64_t)tile << 32) | (k >> 32);
-    }
+    for (int i = threadIdx.x; i < n; i += nt) clist[start + i] = (uint32_t)src[i];
 }
 
-// ---- register-resident bitonic sort: each thread holds 8 consecutive keys
-// (position i = 8 t + r), so a compare-exchange between positions i and i ^ M
-// is in-thread for M < 8, between lanes of a wave for M < 512 (ds_swizzle /
-// permlane32 exchanges, no barrier) and through LDS only beyond that.
+// ---- register-resident bitonic sort (buckets of up to 512 keys, one wave):
+// each lane holds 8 consecutive keys (position i = 8 lane + r), so a
+// compare-exchange between positions i and i ^ M is in-lane for M < 8 and
+// between lanes (ds_swizzle / permlane32 exchanges, no barrier) up to M < 512.
 
 // value of v held by lane (lane ^ D) of this wave, 0 < D < 64 (all lanes active)
 template <int D>
@@ -745,10 +736,7 @@ struct TopBit<0> {
     static constexpr int value = 0;
 };
 
-// padded LDS slot of position i (one spare slot per 8 keys: conflict-free rows)
-__device__ __forceinline__ int sort_slot(int i) { return (i >> 3) * 9 + (i & 7); }
-
-// compare-exchanges (i, i ^ M), M < 8, inside each thread
+// compare-exchanges (i, i ^ M), M < 8, inside each lane
 template <int M>
 __device__ __forceinline__ void sort_stage_in(uint64_t (&k)[8])
 {
@@ -763,26 +751,16 @@ __device__ __forceinline__ void sort_stage_in(uint64_t (&k)[8])
     }
 }
 
-// compare-exchanges (i, i ^ M), M >= 8: the partner is register r ^ (M & 7) of
-// thread t ^ (M >> 3); the lower position keeps the minimum
-template <int NT, int M>
-__device__ __forceinline__ void sort_stage_cross(uint64_t (&k)[8], uint64_t* lds)
+// compare-exchanges (i, i ^ M), 8 <= M < 512: the partner is register
+// r ^ (M & 7) of lane l ^ (M >> 3); the lower position keeps the minimum
+template <int M>
+__device__ __forceinline__ void sort_stage_cross(uint64_t (&k)[8])
 {
     constexpr int DT = M >> 3, RX = M & 7;
     const bool lower = ((threadIdx.x >> TopBit<DT>::value) & 1u) == 0;
     uint64_t p[8];
-    if constexpr (DT < 64) {
 #pragma unroll
-        for (int r = 0; r < 8; r++) p[r] = lane_xor64<DT>(k[r ^ RX]);
-    } else {
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < 8; r++) lds[threadIdx.x * 9 + r] = k[r];
-        __syncthreads();
-        const int pt = (int)threadIdx.x ^ DT;
-#pragma unroll
-        for (int r = 0; r < 8; r++) p[r] = lds[pt * 9 + (r ^ RX)];
-    }
+    for (int r = 0; r < 8; r++) p[r] = lane_xor64<DT>(k[r ^ RX]);
 #pragma unroll
     for (int r = 0; r < 8; r++) {
         const uint64_t x = k[r], y = p[r];
@@ -791,86 +769,300 @@ __device__ __forceinline__ void sort_stage_cross(uint64_t (&k)[8], uint64_t* lds
 }
 
 // half-cleaners j = J, J/2, ..., 1
-template <int NT, int J>
-__device__ __forceinline__ void sort_cleaners(uint64_t (&k)[8], uint64_t* lds)
+template <int J>
+__device__ __forceinline__ void sort_cleaners(uint64_t (&k)[8])
 {
     if constexpr (J >= 8) {
-        sort_stage_cross<NT, J>(k, lds);
-        sort_cleaners<NT, J / 2>(k, lds);
+        sort_stage_cross<J>(k);
+        sort_cleaners<J / 2>(k);
     } else if constexpr (J >= 1) {
         sort_stage_in<J>(k);
-        sort_cleaners<NT, J / 2>(k, lds);
+        sort_cleaners<J / 2>(k);
     }
 }
 
-// merges of size K2, 2 K2, ..., 8 NT: a flip (i, i ^ (K2 - 1)) then the half-cleaners
-template <int NT, int K2>
-__device__ __forceinline__ void sort_merges(uint64_t (&k)[8], uint64_t* lds)
+// merges of size K2, 2 K2, ..., 512: a flip (i, i ^ (K2 - 1)) then the half-cleaners
+template <int K2>
+__device__ __forceinline__ void sort_merges(uint64_t (&k)[8])
 {
-    if constexpr (K2 <= 8 * NT) {
+    if constexpr (K2 <= 512) {
         if constexpr (K2 <= 8) sort_stage_in<K2 - 1>(k);
-        else sort_stage_cross<NT, K2 - 1>(k, lds);
-        sort_cleaners<NT, K2 / 4>(k, lds);
-        sort_merges<NT, K2 * 2>(k, lds);
+        else sort_stage_cross<K2 - 1>(k);
+        sort_cleaners<K2 / 4>(k);
+        sort_merges<K2 * 2>(k);
     }
 }
 
-// A bucket whose size lies in (8 NT / 2, 8 NT] (any size up to 512 for one
-// wave) is sorted by one block of NT threads: padded with all-ones keys, by
-// (depth bits, compact index) in registers.
-template <int NT, int LO, int CAP>
-__device__ __forceinline__ void tilesort_one(int l, const int* __restrict__ tile_of_local,
-                                             const uint32_t* __restrict__ tile_count,
-                                             const uint32_t* __restrict__ tile_start,
-                                             const uint64_t* __restrict__ sortkey, const SortOut& out,
-                                             uint64_t* lds)
+// Buckets of up to 512 keys: one wave per bucket, by (depth bits, compact
+// index), padded with all-ones keys; blocks walk the class's bucket list.
+__global__ __launch_bounds__(64) void tilesort_wave_kernel(const uint32_t* __restrict__ cls_count,
+                                                          const int* __restrict__ cls_list,
+                                                          const uint32_t* __restrict__ tile_count,
+                                                          const uint32_t* __restrict__ tile_start,
+                                                          const uint64_t* __restrict__ sortkey,
+                                                          uint32_t* __restrict__ clist)
 {
-    const int n = (int)tile_count[l];
-    const uint32_t start = tile_start[l];
+    const int nl = (int)*cls_count;
     const int t = threadIdx.x;
-    for (int i = t; i < CAP; i += NT) lds[sort_slot(i)] = i < n ? sortkey[start + i] : ~0ull;
-    __syncthreads();
-    uint64_t k[8];
+    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
+        const int l = cls_list[e];
+        const int n = (int)tile_count[l];
+        const uint32_t start = tile_start[l];
+        uint64_t k[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) k[r] = lds[t * 9 + r];
-    sort_merges<NT, 2>(k, lds);
-    __syncthreads();
+        for (int r = 0; r < 8; r++) {
+            const int i = 8 * t + r;
+            k[r] = i < n ? sortkey[start + i] : ~0ull;
+        }
+        sort_merges<2>(k);
 #pragma unroll
-    for (int r = 0; r < 8; r++) lds[t * 9 + r] = k[r];
-    __syncthreads();
-    const uint32_t tile = (uint32_t)tile_of_local[l];
-    for (int i = t; i < n; i += NT) {
-        const uint64_t key = lds[sort_slot(i)];
-        const uint32_t cx = (uint32_t)key;
-        out.clist[start + i] = cx;
-        out.point_list[start + i] = out.cid2id[cx];
-        out.keys[start + i] = ((uint64_t)tile << 32) | (key >> 32);
+        for (int r = 0; r < 8; r++) {
+            const int i = 8 * t + r;
+            if (i < n) clist[start + i] = (uint32_t)k[r];
+        }
     }
+}
+
+// ---- LDS radix sort of one bucket (least-significant digit first, 4-bit
+// digits; Merrill & Grimshaw's per-thread counter ranking):
+//   items = (depth bits, compact index); each thread owns K consecutive
+//   positions of the bucket (blocked), stored in LDS with one pad slot per K
+//   items so that the blocked reads are conflict-free.  Per digit:
+//     count  : every item adds 1 to its thread's counter for its digit
+//              (ds_add_rtn: the old value is the item's rank among the
+//              thread's earlier items of that digit); the counters form a
+//              digit-major (digit, thread) table,
+//     scan   : an exclusive scan of that table in digit-major order gives
+//              each (digit, thread) its first output position (raking: each
+//              thread scans 16 consecutive entries, then one block-wide scan
+//              of the 16-entry totals),
+//     scatter: every item goes to its (digit, thread) base + rank.
+//   Each pass is stable, so after the digits of the depth bits the bucket is
+//   ordered by depth, items of equal depth in input order.  Digits on which
+//   all keys agree are skipped.  Runs of equal depth (the reference orders
+//   them by Gaussian id, i.e. by compact index) are then sorted by compact
+//   index in place, one thread per run; a run longer than MAX_TIE_RUN sends
+//   the bucket to the 64-bit bitonic network in global memory instead.
+constexpr int RADIX_DIGITS = 16;
+constexpr int MAX_TIE_RUN = 32;
+
+template <int K>
+struct Log2 {
+    static constexpr int value = K <= 1 ? 0 : 1 + Log2<K / 2>::value;
+};
+
+template <int LK>
+__device__ __forceinline__ int rpad(int i) { return i + (i >> LK); }
+
+// inclusive scan over the 64 lanes of a wave (DPP: row_shr 1, 2, 4, 8 inside
+// each 16-lane row, then row_bcast 15 / 31 across rows); all lanes active
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v)
+{
+    v += dpp_u<0x111>(v);          // row_shr:1
+    v += dpp_u<0x112>(v);          // row_shr:2
+    v += dpp_u<0x114>(v);          // row_shr:4
+    v += dpp_u<0x118>(v);          // row_shr:8
+    v += dpp_u<0x142, 0xa>(v);     // row_bcast:15 into rows 1 and 3
+    v += dpp_u<0x143, 0xc>(v);     // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// exclusive scan of one value per thread over an NT-thread block (block
+// total in *total); s_tmp holds NT / 64 words
+template <int NT>
+__device__ __forceinline__ uint32_t radix_block_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint32_t x = wave_incl_scan_u32(v);
+    if (lane == 63) s_tmp[wid] = x;
+    __syncthreads();
+    uint32_t base = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) {
+        const uint32_t sv = s_tmp[w];
+        base += w < wid ? sv : 0u;
+        tot += sv;
+    }
+    *total = tot;
+    return base + x - v;
+}
+
+// The (digit, thread) counter table, flattened digit-major (f = digit * NT +
+// thread), is stored with its 16-byte chunks XOR-swizzled inside each
+// 256-byte row (word bits 2-5 ^= bits 4-7, a bijection): the per-item
+// atomics (one column, consecutive threads) and the raking reads (16
+// consecutive entries per thread, as 16-byte vectors) are then both free of
+// bank conflicts, with 32 or 64 four-byte banks.
+__device__ __forceinline__ int cnt_slot(int f) { return f ^ (((f >> 4) & 15) << 2); }
+
+template <int NT, int K>
+struct alignas(16) RadixLds {
+    uint2 items[NT * K + NT];
+    uint32_t cnt[RADIX_DIGITS * NT];
+    uint32_t misc[3 * (NT / 64) + 4];
+};
+
+template <int NT, int K>
+__device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist,
+                                  RadixLds<NT, K>& S)
+{
+    constexpr int LK = Log2<K>::value;
+    constexpr int CAP = NT * K;
+    constexpr int NW = NT / 64;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
+    // load (coalesced); padding items sort last and are never written out
+    uint32_t kor = 0u, kand = ~0u;
+    for (int i = t; i < CAP; i += NT) {
+        uint2 it = make_uint2(~0u, ~0u);
+        if (i < n) {
+            const uint64_t v = sortkey[start + i];
+            it = make_uint2((uint32_t)(v >> 32), (uint32_t)v);
+            kor |= it.x;
+            kand &= it.x;
+        }
+        S.items[rpad<LK>(i)] = it;
+    }
+    // which key bits vary over the bucket (digits that do not are skipped)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
+        kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
+    }
+    if (lane == 0) { S.misc[wid] = kor; S.misc[NW + wid] = kand; }
+    if (t == 0) S.misc[2 * NW] = 0u;   // long-tie-run flag
+    // this thread's raking segment of the counter table: four 16-byte chunks
+    auto seg = [&](int i) -> uint4* { return reinterpret_cast<uint4*>(&S.cnt[cnt_slot(RADIX_DIGITS * t + 4 * i)]); };
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) *seg(i) = z4;
+    __syncthreads();
+    uint32_t vor = 0u, vand = ~0u;
+#pragma unroll
+    for (int w = 0; w < NW; w++) { vor |= S.misc[w]; vand &= S.misc[NW + w]; }
+    const uint32_t vary = vor ^ vand;
+    uint32_t* s_tmp = S.misc + 2 * NW + 1;   // NW words for the block scan
+
+    uint32_t* cnt = S.cnt;
+    for (int shift = 0; shift < 32; shift += 4) {
+        if (((vary >> shift) & 15u) == 0u) continue;   // uniform over the block
+        uint32_t key[K], val[K], rk[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const uint2 it = S.items[rpad<LK>(t * K + k)];
+            key[k] = it.x;
+            val[k] = it.y;
+        }
+        // the table is all zero here (cleared before the first pass, and by
+        // every thread's column at the end of each pass)
+#pragma unroll
+        for (int k = 0; k < K; k++) rk[k] = atomicAdd(&cnt[cnt_slot((int)((key[k] >> shift) & 15u) * NT + t)], 1u);
+        __syncthreads();
+        {
+            uint4 q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = *seg(i);
+            uint32_t run = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t a = q[i].x, b = q[i].y, c = q[i].z, d = q[i].w;
+                q[i].x = run; run += a;
+                q[i].y = run; run += b;
+                q[i].z = run; run += c;
+                q[i].w = run; run += d;
+            }
+            uint32_t tot;
+            const uint32_t base = radix_block_scan<NT>(run, s_tmp, &tot);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                q[i].x += base; q[i].y += base; q[i].z += base; q[i].w += base;
+                *seg(i) = q[i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const uint32_t pos = cnt[cnt_slot((int)((key[k] >> shift) & 15u) * NT + t)] + rk[k];
+            S.items[rpad<LK>((int)pos)] = make_uint2(key[k], val[k]);
+        }
+        // only this thread reads its column (digit, t) in the scatter: clear
+        // it for the next pass
+#pragma unroll
+        for (int d = 0; d < RADIX_DIGITS; d++) cnt[cnt_slot(d * NT + t)] = 0u;
+        __syncthreads();
+    }
+
+    // runs of equal depth: order by compact index (one thread per run)
+#pragma unroll 1
+    for (int k = 0; k < K; k++) {
+        const int i = t * K + k;
+        if (i + 1 >= n) break;
+        const uint32_t key_i = S.items[rpad<LK>(i)].x;
+        if (S.items[rpad<LK>(i + 1)].x != key_i) continue;
+        if (i > 0 && S.items[rpad<LK>(i - 1)].x == key_i) continue;   // not the run's first item
+        int e = i + 2;
+        while (e < n && e - i <= MAX_TIE_RUN && S.items[rpad<LK>(e)].x == key_i) e++;
+        if (e - i > MAX_TIE_RUN) {
+            S.misc[2 * NW] = 1u;
+            continue;
+        }
+        for (int a = i + 1; a < e; a++) {
+            const uint32_t v = S.items[rpad<LK>(a)].y;
+            int b = a - 1;
+            while (b >= i && S.items[rpad<LK>(b)].y > v) {
+                S.items[rpad<LK>(b + 1)].y = S.items[rpad<LK>(b)].y;
+                b--;
+            }
+            S.items[rpad<LK>(b + 1)].y = v;
+        }
+    }
+    __syncthreads();
+    if (S.misc[2 * NW] != 0u) {
+        // a long run of equal depths: the full 64-bit sort in global memory
+        uint64_t* s = sortkey + start;
+        for (int i = t; i < n; i += NT) {
+            const uint2 it = S.items[rpad<LK>(i)];
+            s[i] = ((uint64_t)it.x << 32) | it.y;
+        }
+        __syncthreads();
+        int N = 1;
+        while (N < n) N <<= 1;
+        bitonic<NT>(s, n, N);
+        write_sorted(start, n, s, clist, NT);
+        return;
+    }
+    for (int i = t; i < n; i += NT) clist[start + i] = S.items[rpad<LK>(i)].y;
 }
 
 // One launch per size class; its blocks walk the class's list of buckets
 // (block b takes entries b, b + gridDim.x, ...).
-template <int NT, int LO>
-__global__ __launch_bounds__(NT) void tilesort_kernel(
-    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const int* __restrict__ tile_of_local,
-    const uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start,
-    const uint64_t* __restrict__ sortkey, SortOut out)
+template <int NT, int K>
+__global__ __launch_bounds__(NT) void tilesort_radix_kernel(const uint32_t* __restrict__ cls_count,
+                                                           const int* __restrict__ cls_list,
+                                                           const uint32_t* __restrict__ tile_count,
+                                                           const uint32_t* __restrict__ tile_start,
+                                                           uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist)
 {
-    constexpr int CAP = 8 * NT;
-    __shared__ uint64_t lds[NT * 9];
+    __shared__ RadixLds<NT, K> S;
     const int nl = (int)*cls_count;
     for (int e = blockIdx.x; e < nl; e += gridDim.x) {
-        if (e != (int)blockIdx.x) __syncthreads();   // the previous bucket's reads of lds are done
-        tilesort_one<NT, LO, CAP>(cls_list[e], tile_of_local, tile_count, tile_start, sortkey, out, lds);
+        if (e != (int)blockIdx.x) __syncthreads();   // the previous bucket's reads of LDS are done
+        const int l = cls_list[e];
+        radix_sort_bucket<NT, K>(tile_start[l], (int)tile_count[l], sortkey, clist, S);
     }
 }
 
-// Buckets larger than the biggest LDS class: the same network in global
-// memory, in place.
+// Buckets larger than the biggest LDS class: the 64-bit bitonic network in
+// global memory, in place.
 __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
-    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const int* __restrict__ tile_of_local,
-    const uint32_t* __restrict__ tile_count, const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey,
-    SortOut out)
+    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const uint32_t* __restrict__ tile_count,
+    const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist)
 {
     const int nl = (int)*cls_count;
     for (int e = blockIdx.x; e < nl; e += gridDim.x) {
@@ -882,7 +1074,25 @@ __global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
         int N = 1;
         while (N < n) N <<= 1;
         bitonic<BIG_SORT_THREADS>(s, n, N);
-        write_sorted((uint32_t)tile_of_local[l], start, n, s, out, BIG_SORT_THREADS);
+        write_sorted(start, n, s, clist, BIG_SORT_THREADS);
+    }
+}
+
+// The reference's sorted arrays from the compact list, on request: per
+// local tile, point_list[i] = Gaussian id and point_list_keys[i] =
+// (tile << 32) | depth bits of list position i.
+__global__ __launch_bounds__(256) void pointlist_kernel(const uint2* __restrict__ ranges,
+                                                        const uint32_t* __restrict__ clist,
+                                                        const uint32_t* __restrict__ cid2id,
+                                                        const float* __restrict__ depths,
+                                                        uint32_t* __restrict__ point_list, uint64_t* __restrict__ keys)
+{
+    const uint32_t tile = blockIdx.x;
+    const uint2 r = ranges[tile];
+    for (uint32_t i = r.x + threadIdx.x; i < r.y; i += 256) {
+        const uint32_t id = cid2id[clist[i]];
+        point_list[i] = id;
+        keys[i] = ((uint64_t)tile << 32) | (uint64_t)__float_as_uint(depths[id]);
     }
 }
 
@@ -915,15 +1125,17 @@ __device__ __forceinline__ bool block_to_tile(unsigned b, unsigned gx, unsigned 
 
 struct Rec {
     float4 q0, q1, q2;
-    uint32_t gid;   // Gaussian id (loaded only WITH_ID)
+    uint32_t gid;      // Gaussian id (loaded only WITH_ID)
+    float cut_power;   // alpha cut-off power of the blend's exact-exp window
 };
 
 template <bool WITH_ID>
 __device__ __forceinline__ Rec load_rec(const float4* __restrict__ rec, uint32_t cx)
 {
     const float4* r = rec + 4 * (size_t)cx;
-    Rec o{r[0], r[1], r[2], 0u};
-    if (WITH_ID) o.gid = __float_as_uint(r[3].x);
+    const float2 q3 = *reinterpret_cast<const float2*>(&r[3]);
+    Rec o{r[0], r[1], r[2], 0u, q3.y};
+    if (WITH_ID) o.gid = __float_as_uint(q3.x);
     return o;
 }
 
@@ -936,7 +1148,7 @@ __device__ __forceinline__ bool rec_may_touch(const Rec& r, float x0, float y0, 
 struct Stage {
     float4 a[64];   // x, y, -a/2, -b
     float4 b[64];   // -c/2, opacity, r, g
-    float4 c[64];   // blue, tag bits, position in the tile's list (bits), 0
+    float4 c[64];   // blue, tag bits, position in the tile's list (bits), alpha cut-off power
 };
 
 // stages entry k of the list; `tag` (Gaussian id in the forward, compact
@@ -945,7 +1157,7 @@ __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uin
 {
     st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
     st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
-    st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k), 0.f);
+    st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k), r.cut_power);
 }
 
 // Blend modes: the split path's render (observation counts and per-tile
@@ -1034,7 +1246,8 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
             const float dx = A.x - pxf, dy = A.y - pyf;
             const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-            const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
+            float G;
+            const float alpha = gs::blend_alpha(B.y, power, Cc.w, G);
             const float test_T = T_ * (1.0f - alpha);
             const bool use = !done && !(power > 0.0f) && !(alpha < alpha_min);
             const bool fin = use && test_T < 0.0001f;
@@ -1194,7 +1407,7 @@ __device__ void inv4_colmajor(const float* __restrict__ mf, float* __restrict__ 
 struct DepthStage {
     float4 a[64];    // x, y, -a/2, -b
     float4 b[64];    // -c/2, opacity, r, g
-    float4 c[64];    // blue, Gaussian id (bits), 0, 0
+    float4 c[64];    // blue, Gaussian id (bits), 0, alpha cut-off power
     float4 r0[64];   // rotation entries m0..m3 (glm column order)
     float4 r1[64];   // m4..m7
     float4 r2[64];   // m8, ray origin in the Gaussian's frame
@@ -1262,7 +1475,7 @@ __global__ __launch_bounds__(64) void render_depth_kernel(int W, int H, unsigned
             const int slot = gs::rank_below(km);
             st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
             st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
-            st.c[slot] = make_float4(r.q2.x, __uint_as_float(r.gid), 0.f, 0.f);
+            st.c[slot] = make_float4(r.q2.x, __uint_as_float(r.gid), 0.f, r.cut_power);
             const uint32_t g = r.gid;
             const float4 q = reinterpret_cast<const float4*>(D.rotations)[g];
             const float qr = q.x, qxx = q.y, qy_ = q.z, qz = q.w;
@@ -1293,7 +1506,8 @@ __global__ __launch_bounds__(64) void render_depth_kernel(int W, int H, unsigned
             const float dx = A.x - pxf, dy = A.y - pyf;
             const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
             if (power > 0.0f) continue;
-            const float alpha = __builtin_fminf(0.99f, B.y * gs::expf_nonpos(power));
+            float G;
+            const float alpha = gs::blend_alpha(B.y, power, Cc.w, G);
             if (alpha < alpha_min) continue;
             const float test_T = T_ * (1.0f - alpha);
             if (test_T < 0.0001f) { done = true; continue; }
@@ -1447,8 +1661,8 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             // selects on three factors instead of per-value zeroing.
             const float dx = A.x - pxf, dy = A.y - pyf;
             const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-            const float G0 = gs::expf_nonpos(power);
-            const float alpha = __builtin_fminf(0.99f, B.y * G0);
+            float G0;
+            const float alpha = gs::blend_alpha(B.y, power, Cc.w, G0);
             const bool valid = ci < last && !(power > 0.0f) && !(alpha < alpha_min);
             const float G = valid ? G0 : 0.f;
             const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
@@ -1537,6 +1751,26 @@ extern "C" int gs_render_buffer_views(int64_t R, int W, int H, void* binning, vo
     return GS_OK;
 }
 
+extern "C" int gs_render_point_list(int P, int64_t R, int W, int H, const float* depths, const void* geom,
+                                    void* binning, const void* img, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
+    if (R == 0) return GS_OK;
+    GS_REQUIRE(depths != nullptr && geom != nullptr && binning != nullptr && img != nullptr,
+               "depths and the forward's workspaces must be non-null");
+    const GeomLayout g = geom_layout(P, W, H);
+    const ImgLayout il = img_layout(W, H);
+    const BinLayout b = bin_layout(R);
+    GS_TIMED("pointlist_kernel", stream,
+             hipLaunchKernelGGL(pointlist_kernel, dim3((unsigned)g.T), dim3(256), 0, stream,
+                                at<const uint2>(img, il.ranges), at<const uint32_t>(binning, b.clist),
+                                at<const uint32_t>(geom, g.cid2id), depths, at<uint32_t>(binning, b.point_list),
+                                at<uint64_t>(binning, b.keys)));
+    GS_LAUNCH_CHECK("pointlist_kernel");
+    return GS_OK;
+}
+
 namespace {
 
 // Side streams for the bucket sort: the size classes sort disjoint buckets,
@@ -1596,6 +1830,10 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     uint32_t* tile_start = at<uint32_t>(geom, g.tile_start);
     uint32_t* cursor = at<uint32_t>(geom, g.cursor);
 
+    // the binning's wall time on the caller's stream: from here to the end of
+    // the sorts in the forward call (the R readback and the caller's
+    // allocation between the two calls included)
+    if (gs::timing_on()) gs::timing_stage_begin(stream, BINNING_STAGE);
     if (compute_locally == nullptr) {
         GS_TIMED("localmap_kernel", stream,
                  hipLaunchKernelGGL(localmap_all_kernel, dim3(gs_div_up((size_t)g.T, 256)), dim3(256), 0, stream, g.T,
@@ -1663,8 +1901,6 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     uint32_t* cursor = at<uint32_t>(geom, g.cursor);
     uint2* ranges = at<uint2>(img, il.ranges);
     uint64_t* sortkey = at<uint64_t>(binning, bl.sortkey);
-    uint32_t* point_list = at<uint32_t>(binning, bl.point_list);
-    uint64_t* keys = at<uint64_t>(binning, bl.keys);
 
     const unsigned T = (unsigned)g.T;
     GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
@@ -1703,7 +1939,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
                                         at<float4>(geom, g.rec), at<float4>(geom, g.gacc), nullptr, Z));
         }
         GS_LAUNCH_CHECK("scatter_kernel");
-        const SortOut sout{at<const uint32_t>(geom, g.cid2id), point_list, keys, at<uint32_t>(binning, bl.clist)};
+        uint32_t* clist = at<uint32_t>(binning, bl.clist);
         // one launch per size class over that class's bucket list; the grid is
         // bounded by how many buckets of the class R instances can fill and
         // by what fits on the chip at once
@@ -1714,7 +1950,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             return (unsigned)std::min<int64_t>(std::min<int64_t>((int64_t)T, fit), (int64_t)cap);
         };
         const unsigned gcs[SORT_CLASSES] = {grid_of(0, 8192), grid_of(512, 4096), grid_of(1024, 2048),
-                                            grid_of(2048, 1024), grid_of(4096, 512), grid_of(SORT_CAP_MAX, 256)};
+                                            grid_of(2048, 2048), grid_of(4096, 1024), grid_of(SORT_CAP_MAX, 256)};
         // side streams pay off once the sorts are long enough to hide the
         // fork / join (small scenes sort on the caller's stream)
         SideStreams* ss = nullptr;
@@ -1739,33 +1975,33 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             switch (c) {
             case 0:
                 GS_TIMED("tilesort_kernel_512", cs,
-                         hipLaunchKernelGGL((tilesort_kernel<64, 0>), dim3(gc), dim3(64), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                         hipLaunchKernelGGL(tilesort_wave_kernel, dim3(gc), dim3(64), 0, cs, ccc, cl, tile_count,
+                                            tile_start, sortkey, clist));
                 break;
             case 1:
                 GS_TIMED("tilesort_kernel_1k", cs,
-                         hipLaunchKernelGGL((tilesort_kernel<128, 512>), dim3(gc), dim3(128), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                         hipLaunchKernelGGL((tilesort_radix_kernel<128, 8>), dim3(gc), dim3(128), 0, cs, ccc, cl,
+                                            tile_count, tile_start, sortkey, clist));
                 break;
             case 2:
                 GS_TIMED("tilesort_kernel_2k", cs,
-                         hipLaunchKernelGGL((tilesort_kernel<256, 1024>), dim3(gc), dim3(256), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                         hipLaunchKernelGGL((tilesort_radix_kernel<256, 8>), dim3(gc), dim3(256), 0, cs, ccc, cl,
+                                            tile_count, tile_start, sortkey, clist));
                 break;
             case 3:
                 GS_TIMED("tilesort_kernel_4k", cs,
-                         hipLaunchKernelGGL((tilesort_kernel<512, 2048>), dim3(gc), dim3(512), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                         hipLaunchKernelGGL((tilesort_radix_kernel<256, 16>), dim3(gc), dim3(256), 0, cs, ccc, cl,
+                                            tile_count, tile_start, sortkey, clist));
                 break;
             case 4:
                 GS_TIMED("tilesort_kernel_8k", cs,
-                         hipLaunchKernelGGL((tilesort_kernel<1024, 4096>), dim3(gc), dim3(1024), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                         hipLaunchKernelGGL((tilesort_radix_kernel<512, 16>), dim3(gc), dim3(512), 0, cs, ccc, cl,
+                                            tile_count, tile_start, sortkey, clist));
                 break;
             default:
                 GS_TIMED("tilesort_big_kernel", cs,
                          hipLaunchKernelGGL(tilesort_big_kernel, dim3(gc), dim3(BIG_SORT_THREADS), 0, cs, ccc, cl,
-                                            tile_of_local, tile_count, tile_start, sortkey, sout));
+                                            tile_count, tile_start, sortkey, clist));
                 break;
             }
             GS_LAUNCH_CHECK("tilesort_kernel");
@@ -1775,6 +2011,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             }
         }
     }
+    if (gs::timing_on()) gs::timing_stage_end(stream, BINNING_STAGE);
     unsigned sgx, NS;
     const unsigned nblk = blend_grid(gx, gy, sgx, NS);
     O.final_T = at<float>(img, il.final_T);

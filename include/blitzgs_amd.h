@@ -139,12 +139,25 @@ int gs_render_backward(int P, int64_t R, int image_width, int image_height, cons
                        gs_stream_t stream);
 
 /* Views into the opaque buffers, for tests and tools:
- *   binning: point_list uint32 (R), point_list_keys uint64 (R)
+ *   binning: point_list uint32 (R), point_list_keys uint64 (R) -- written by
+ *            gs_render_point_list, not by the forward
  *   img    : ranges uint32 (T,2), final_T float (H,W), n_contrib uint32 (H,W),
  *            n_contrib2loss uint32 (H,W)                                    */
 int gs_render_buffer_views(int64_t R, int image_width, int image_height, void* binning, void* img,
                            uint32_t** point_list, uint64_t** point_list_keys, uint32_t** ranges,
                            float** final_T, uint32_t** n_contrib, uint32_t** n_contrib2loss);
+
+/* The reference's sorted instance arrays (the point_list and
+ * point_list_keys its binningBuffer holds after SortPairs,
+ * diff-gaussian-rasterization_r/cuda_rasterizer/rasterizer_impl.cu:643-652),
+ * written into `binning` on request: the forward itself keeps only the
+ * blend's compact list, so these 12 bytes per instance are spent only by
+ * callers that read them.  point_list[i] = Gaussian id, point_list_keys[i] =
+ * (tile << 32) | bits of depths[id].  geom / binning / img: a completed
+ * gs_render_forward or gs_render_full_forward (P, R, W, H as passed there);
+ * depths: the depths the forward was given. */
+int gs_render_point_list(int P, int64_t R, int image_width, int image_height, const float* depths,
+                         const void* geom, void* binning, const void* img, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * distCUDA2 (simple-knn/spatial.cu:15-26, simple_knn.cu:186-221):
@@ -399,9 +412,12 @@ int gs_ply_pack(int64_t P, int32_t n_tensors, const gs_ply_tensor* tensors, cons
 
 /* ------------------------------------------------------------------------ *
  * Diagnostics (no counterpart in the reference): evaluate the device exp / log
- * used by the kernels on n inputs (op 0 = exp, 1 = log, 2 = the blend's exp,
+ * used by the kernels on n inputs (op 0 = exp, 1 = log, 2 = the exact exp of
+ * the blend's guard,
  * 3 = the 12-value wave reduction on 12 x 64 inputs), so tests can compare them
- * bit for bit with the CPU; op 4 copies n floats (n % 4 == 0, 16-byte aligned),
+ * bit for bit with the CPU; op 6 evaluates the blend's falloff G = exp(x),
+ * x <= 0 (hardware exp2, exact within a window around the 1/255 alpha
+ * cut-off at opacity 1); op 4 copies n floats (n % 4 == 0, 16-byte aligned),
  * the known-size kernel that HBM byte counters are calibrated against; op 5
  * runs 8192 blocks of 256 threads, each wave issuing 32 * n fp32 FMAs (x unused,
  * y one float that is never written), the reference for the VALU issue rate.
@@ -414,7 +430,11 @@ int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
  * enabled, every kernel launch is bracketed by HIP events on its stream.
  * gs_timing_read synchronises on the recorded events and returns, per kernel
  * name (64-byte slots in `names`), the summed milliseconds and launch count;
- * the return value is the number of distinct kernels.
+ * the return value is the number of distinct kernels.  One entry is a stage,
+ * not a kernel: "binning (wall)", the render's binning from its first kernel
+ * (gs_render_forward_count / gs_render_full_count) to the end of the sorts
+ * (gs_render_forward / _full_forward / _full_depth), on the caller's stream,
+ * the R readback and the caller's work between the two calls included.
  * ------------------------------------------------------------------------ */
 int gs_timing_enable(int on);
 int gs_timing_reset(void);

@@ -40,14 +40,20 @@ def gpu_render_forward(rs, means2D, depths, radii, conic_opacity, rgb, compute_l
     out = rasterizer._render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb,
                                          None if compute_locally is None else to_dev(compute_locally))
     R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, _ = out
-    views = buffer_views(R, W, H, binning, img)
+    views = buffer_views(R, W, H, binning, img, means2D.shape[0], depths, geom)
     return dict(R=R, color=color, n_render=n_render, n_consider=n_consider, n_contrib=n_contrib,
                 out_observe=out_observe, geom=geom, binning=binning, img=img, **views)
 
 
-def buffer_views(R, W, H, binning, img):
-    """Copy the sorted ids/keys, ranges and per-pixel state out of the opaque buffers."""
+def buffer_views(R, W, H, binning, img, P=None, depths=None, geom=None):
+    """Copy the sorted ids/keys, ranges and per-pixel state out of the opaque
+    buffers; with P / depths / geom the sorted ids and keys are first written
+    from the forward's compact list (gs_render_point_list)."""
     lib = _lib.load()
+    if depths is not None:
+        _lib.check(lib.gs_render_point_list(int(P), R, W, H, _lib.ptr(depths.contiguous()), _lib.ptr(geom),
+                                            _lib.ptr(binning), _lib.ptr(img), _lib.stream_of()),
+                   "gs_render_point_list")
     pl, keys, rg, ft, nc, n2 = (C.c_void_p() for _ in range(6))
     _lib.check(lib.gs_render_buffer_views(R, W, H, _lib.ptr(binning), _lib.ptr(img), C.byref(pl), C.byref(keys),
                                           C.byref(rg), C.byref(ft), C.byref(nc), C.byref(n2)), "buffer_views")
@@ -81,6 +87,40 @@ def assert_bitexact(got, ref, name):
         i = bad[0]
         raise AssertionError(f"{name}: {bad.size} of {g.size} entries differ; first at flat index {i}: "
                              f"got {np.asarray(got).reshape(-1)[i]!r} ref {np.asarray(ref).reshape(-1)[i]!r}")
+
+
+# The blend evaluates G = exp(power) with the hardware exp2 (a few 1e-7
+# relative from the oracle's exact fp32 exp; the alpha >= 1/255 cut-off is
+# decided exactly), so its outputs carry the north_star's tolerance: RGB and
+# transmittance within 1e-4 max-abs of the oracle.  Its integer outputs (last
+# contributor, contributor counts, observations) are equal except where a
+# pixel's transmittance lands within ~1e-6 of a decision threshold (the
+# T < 1e-4 stop, the T > 0.5 observation): at most 1e-4 of the entries may
+# differ (and at least 3 are allowed).
+BLEND_ATOL = 1e-4
+
+
+def assert_close_abs(got, ref, name, atol=BLEND_ATOL):
+    g, r = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    assert g.shape == r.shape, (name, g.shape, r.shape)
+    if not g.size:
+        return
+    nan_g, nan_r = np.isnan(g), np.isnan(r)
+    assert (nan_g == nan_r).all(), f"{name}: NaN positions differ"
+    d = np.abs(np.where(nan_g, 0.0, g - r))
+    i = int(np.argmax(d))
+    assert d.flat[i] <= atol, (f"{name}: max-abs difference {d.flat[i]:.3g} > {atol} at flat index {i}: "
+                               f"got {g.flat[i]!r} ref {r.flat[i]!r}")
+
+
+def assert_counts_close(got, ref, name, frac=1e-4, min_allowed=3):
+    g = np.asarray(got).astype(np.int64).ravel()
+    r = np.asarray(ref).astype(np.int64).ravel()
+    assert g.shape == r.shape, (name, g.shape, r.shape)
+    bad = np.flatnonzero(g != r)
+    allowed = max(min_allowed, int(frac * g.size))
+    assert bad.size <= allowed, (f"{name}: {bad.size} of {g.size} entries differ (allowed {allowed}); first at "
+                                 f"{bad[:5].tolist()}: got {g[bad[:5]].tolist()} ref {r[bad[:5]].tolist()}")
 
 
 def rel_l2(got, ref):
@@ -124,7 +164,7 @@ def autograd_step(scene, cam, bg=(0.0, 0.0, 0.0), cl=None, ext=None, avoid=False
     node = color.grad_fn
     R = int(node.num_rendered)
     geom, binning, img = node.saved_tensors[5:8]
-    views = buffer_views(R, int(cam["W"]), int(cam["H"]), binning, img)
+    views = buffer_views(R, int(cam["W"]), int(cam["H"]), binning, img, P, depths, geom)
     if loss_fn is None:
         torch.autograd.backward([color], [to_dev(dL_dimage)])
     else:
@@ -155,8 +195,10 @@ def oracle_step(scene, cam, bg=(0.0, 0.0, 0.0), cl_fwd=None, cl_bwd=None, dL_dim
 
 
 def check_step(g, pre, bn, rf, rb, pb, tol=1e-3, binning=True):
-    """The bar: preprocess outputs, binning arrays, image and per-pixel /
-    per-tile counters bit-exact; the seven gradients within tol relative L2."""
+    """The bar: preprocess outputs and binning arrays bit-exact; image and
+    transmittance within 1e-4 max-abs, the per-pixel / per-tile / per-Gaussian
+    counts equal up to rare threshold cases (assert_counts_close); the seven
+    gradients within tol relative L2."""
     for k in ("means2D", "depths", "radii", "conic_opacity", "rgb"):
         assert_bitexact(np_(g[k]), pre[k], k)
     assert g["R"] == bn["R"], (g["R"], bn["R"])
@@ -164,13 +206,13 @@ def check_step(g, pre, bn, rf, rb, pb, tol=1e-3, binning=True):
         assert_bitexact(np_(g["point_list"]).view(np.uint32), bn["point_list"], "point_list")
         assert_bitexact(np_(g["keys"]).view(np.uint64), bn["keys"], "point_list_keys")
     assert_bitexact(np_(g["ranges"]).view(np.uint32), bn["ranges"], "ranges")
-    assert_bitexact(np_(g["color"]), rf["color"], "color")
-    assert_bitexact(np_(g["final_T"]), rf["final_T"], "final_T")
-    assert_bitexact(np_(g["n_contrib_px"]).view(np.uint32), rf["n_contrib_px"], "n_contrib (pixel)")
-    assert_bitexact(np_(g["out_observe"]), rf["out_observe"], "out_observe")
     assert_bitexact(np_(g["n_render"]), rf["n_render"], "n_render")
-    assert_bitexact(np_(g["n_consider"]), rf["n_consider"], "n_consider")
-    assert_bitexact(np_(g["n_contrib"]), rf["n_contrib"], "n_contrib (tile)")
+    assert_close_abs(np_(g["color"]), rf["color"], "color")
+    assert_close_abs(np_(g["final_T"]), rf["final_T"], "final_T")
+    assert_counts_close(np_(g["n_contrib_px"]).view(np.uint32), rf["n_contrib_px"], "n_contrib (pixel)")
+    assert_counts_close(np_(g["out_observe"]), rf["out_observe"], "out_observe")
+    assert_counts_close(np_(g["n_consider"]), rf["n_consider"], "n_consider")
+    assert_counts_close(np_(g["n_contrib"]), rf["n_contrib"], "n_contrib (tile)")
     errs = {"dL_dmeans2D": rel_l2(np_(g["dL_dmeans2D"]), rb["dL_dmeans2D"][:, :2]),
             "dL_dmeans2D_abs": rel_l2(np_(g["dL_dmeans2D_abs"]), rb["dL_dmeans2D_abs"])}
     for k in PARAM_KEYS:

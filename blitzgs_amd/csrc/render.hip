@@ -543,8 +543,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     const float* __restrict__ rgb, const int* __restrict__ loc_map, const uint32_t* __restrict__ meta,
     const uint32_t* __restrict__ hist, const uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
     const uint32_t* __restrict__ wbase, uint64_t* __restrict__ sortkey, int* __restrict__ cidx_of,
-    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, float4* __restrict__ gacc,
-    const float2* __restrict__ rects, ZeroOut Z)
+    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, const float2* __restrict__ rects, ZeroOut Z)
 {
     // dynamic LDS: per wave 64 staged records, then min(T, LDS_TILES) cursors
     extern __shared__ uint4 s_dyn[];
@@ -623,18 +622,13 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
             sp[3] = make_float4(__uint_as_float((uint32_t)i), gs::alpha_cut_power(co.w), 0.f, 0.f);
             cid2id[cidx] = (uint32_t)i;
         }
-        // the group's records and zeroed accumulators are one contiguous run:
-        // write them with consecutive 16-byte stores (wave-private staging, so
-        // a wave-level barrier suffices)
+        // the group's records are one contiguous run: write them with
+        // consecutive 16-byte stores (wave-private staging, so a wave-level
+        // barrier suffices)
         __builtin_amdgcn_wave_barrier();
         {
             float4* rdst = rec + 4 * (size_t)first;
-            float4* gdst = gacc + 4 * (size_t)first;
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int j = lane; j < 4 * nl; j += 64) {
-                rdst[j] = stage[j];
-                gdst[j] = z;
-            }
+            for (int j = lane; j < 4 * nl; j += 64) rdst[j] = stage[j];
         }
         __builtin_amdgcn_wave_barrier();
         const Expansion e = expansion_begin(cnt);
@@ -1553,36 +1547,76 @@ __global__ __launch_bounds__(64) void render_depth_kernel(int W, int H, unsigned
     }
 }
 
-// Writes the render backward's outputs for every Gaussian from its
-// accumulator (listed Gaussians, whose accumulator is then cleared for the
-// next backward) or zeros; one thread per Gaussian.
-__global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __restrict__ cidx_of,
-                                                           float4* __restrict__ gacc, int m2d_stride,
-                                                           float* __restrict__ g_m2d, float* __restrict__ g_m2d_abs,
-                                                           float4* __restrict__ g_con, float* __restrict__ g_col)
+// Clears the gradient accumulators of the listed Gaussians (meta[4] of them)
+// before a backward accumulates into them.
+__global__ __launch_bounds__(256) void zero_gacc_kernel(const uint32_t* __restrict__ meta, float4* __restrict__ gacc)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= P) return;
+    const size_t n4 = 4 * (size_t)meta[4];
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
+        gacc[i] = z;
+}
+
+// Writes the k-float rows (k = 2 or 3) of a wave's 64 consecutive Gaussians
+// as one contiguous run: the rows are staged in the wave's LDS slice and
+// leave as 16-byte streaming stores that fill whole cache lines.
+__device__ __forceinline__ void emit_rows(float* __restrict__ S, int lane, int k, float* __restrict__ out,
+                                          int base, float v0, float v1, float v2)
+{
+    S[lane * k] = v0;
+    S[lane * k + 1] = v1;
+    if (k == 3) S[lane * k + 2] = v2;
+    __builtin_amdgcn_wave_barrier();
+    float4* dst = reinterpret_cast<float4*>(out + (size_t)base * k);
+    const float4* src = reinterpret_cast<const float4*>(S);
+    for (int e = lane; e < 16 * k; e += 64) gs::st_stream(dst + e, src[e]);
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Writes the render backward's outputs for every Gaussian from its
+// accumulator (listed Gaussians) or zeros, one Gaussian per thread.  A wave
+// whose 64 Gaussians are all in range writes its rows through emit_rows when
+// the outputs are 16-byte aligned (vec); otherwise element by element.
+__global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __restrict__ cidx_of,
+                                                           const float4* __restrict__ gacc, int m2d_stride,
+                                                           float* __restrict__ g_m2d, float* __restrict__ g_m2d_abs,
+                                                           float4* __restrict__ g_con, float* __restrict__ g_col,
+                                                           bool vec)
+{
+    __shared__ __align__(16) float stage[4][64 * 3];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int base = (int)(blockIdx.x * 4 + w) * 64;
+    if (base >= P) return;                         // the whole wave leaves; no block barrier follows
+    const int i = base + lane;
+    const bool in = i < P;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    // a = dmean x, dmean y, |dmean x|, |dmean y|; b = dconic a, b, c, dopacity; c = drgb
     float4 a = z, b = z, c = z;
-    const int cx = cidx_of != nullptr ? cidx_of[i] : -1;
-    if (cx >= 0) {
-        float4* g = gacc + 4 * (size_t)cx;
-        a = g[0]; b = g[1]; c = g[2];
-        g[0] = z; g[1] = z; g[2] = z; g[3] = z;
+    if (in && cidx_of != nullptr) {
+        const int cx = cidx_of[i];
+        if (cx >= 0) {
+            const float4* g = gacc + 4 * (size_t)cx;
+            a = g[0]; b = g[1]; c = g[2];
+        }
     }
-    // streaming stores: the four gradient arrays are read once, by the
-    // preprocess backward
+    if (in) gs::st_stream(&g_con[i], b);
+    if (vec && base + 64 <= P) {
+        float* S = stage[w];
+        emit_rows(S, lane, m2d_stride, g_m2d, base, a.x, a.y, 0.f);
+        if (g_m2d_abs != nullptr) emit_rows(S, lane, 3, g_m2d_abs, base, a.z, a.w, 0.f);
+        emit_rows(S, lane, 3, g_col, base, c.x, c.y, c.z);
+        return;
+    }
+    if (!in) return;
     float* m = g_m2d + (size_t)i * m2d_stride;
     gs::st_stream(&m[0], a.x);
     gs::st_stream(&m[1], a.y);
-    for (int k = 2; k < m2d_stride; k++) gs::st_stream(&m[k], 0.f);
+    if (m2d_stride == 3) gs::st_stream(&m[2], 0.f);
     if (g_m2d_abs != nullptr) {
         gs::st_stream(&g_m2d_abs[3 * (size_t)i], a.z);
         gs::st_stream(&g_m2d_abs[3 * (size_t)i + 1], a.w);
         gs::st_stream(&g_m2d_abs[3 * (size_t)i + 2], 0.f);
     }
-    gs::st_stream(&g_con[i], b);
     gs::st_stream(&g_col[3 * (size_t)i], c.x);
     gs::st_stream(&g_col[3 * (size_t)i + 1], c.y);
     gs::st_stream(&g_col[3 * (size_t)i + 2], c.z);
@@ -1928,15 +1962,14 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
                                         stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
                                         hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
                                         at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
-                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc),
-                                        reinterpret_cast<const float2*>(rects), Z));
+                                        at<float4>(geom, g.rec), reinterpret_cast<const float2*>(rects), Z));
         } else {
             GS_TIMED("scatter_kernel", stream,
                      hipLaunchKernelGGL(scatter_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
                                         stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
                                         hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
                                         at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
-                                        at<float4>(geom, g.rec), at<float4>(geom, g.gacc), nullptr, Z));
+                                        at<float4>(geom, g.rec), nullptr, Z));
         }
         GS_LAUNCH_CHECK("scatter_kernel");
         uint32_t* clist = at<uint32_t>(binning, bl.clist);
@@ -2061,6 +2094,12 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
     const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
     float4* gacc = at<float4>(geom, g.gacc);
     if (R > 0) {
+        // the listed Gaussians' accumulators start at zero (every backward)
+        const unsigned zb = std::min<unsigned>(gs_div_up(4 * (size_t)P, 256), 2048u);
+        GS_TIMED("zero_gacc_kernel", stream,
+                 hipLaunchKernelGGL(zero_gacc_kernel, dim3(zb), dim3(256), 0, stream,
+                                    at<const uint32_t>(geom, g.meta), gacc));
+        GS_LAUNCH_CHECK("zero_gacc_kernel");
         unsigned sgx, NS;
         const unsigned nblk = blend_grid(gx, gy, sgx, NS);
         const uint2* rng = at<uint2>(img, il.ranges);
@@ -2084,7 +2123,8 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
              hipLaunchKernelGGL(unpack_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream, P,
                                 R > 0 ? at<const int>(geom, g.cidx_of) : nullptr, gacc, dL_dmeans2D_stride,
                                 dL_dmeans2D, dL_dmeans2D_abs, reinterpret_cast<float4*>(dL_dconic_opacity),
-                                dL_dcolors));
+                                dL_dcolors,
+                                (((uintptr_t)dL_dmeans2D | (uintptr_t)dL_dmeans2D_abs | (uintptr_t)dL_dcolors) & 15) == 0));
     GS_LAUNCH_CHECK("unpack_grads_kernel");
     return GS_OK;
 }

@@ -48,6 +48,7 @@ _SIGS = {
     "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _c]),
     "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
                                _c, _c]),
+    "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _c]),
     "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
@@ -63,6 +64,7 @@ _SIGS = {
                                         _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_render_full_count": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, C.POINTER(_i64), _c]),
     "gs_render_full_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_full_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 14 + [C.POINTER(_i64), _c]),
     "gs_render_full_depth": (_i, [_i, _i64, _i, _i] + [_c] * 21 + [_c]),
     "gs_render_full_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward_full": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i, _c,
@@ -161,3 +163,31 @@ def timing_read(max_entries=64):
         nm = names.raw[64 * i:64 * i + 64].split(b"\0", 1)[0].decode()
         out[nm] = (tot[i], cnt[i])
     return out
+
+
+class InstanceReserve:
+    """Per-device estimate of the next forward's instance count R: a slowly
+    decaying maximum of the recent counts.  The reserved capacity (10 % above
+    it) sizes the binning buffer before R is known, so that the forward is one
+    library call with no host round trip between the count and the
+    duplication; a forward with more instances is redone at the exact size."""
+
+    HEADROOM = 1.10
+    DECAY = 0.98
+    MIN_CAPACITY = 4096
+
+    def __init__(self):
+        self._est = {}
+
+    def capacity(self, dev):
+        e = self._est.get(dev)
+        return None if e is None else min(int(e * self.HEADROOM) + self.MIN_CAPACITY, 2 ** 32 - 1)
+
+    def update(self, dev, R):
+        self._est[dev] = max(int(R), int(self._est.get(dev, 0) * self.DECAY))
+
+    def reset(self):
+        self._est.clear()
+
+
+RESERVE = InstanceReserve()

@@ -143,14 +143,21 @@ struct BinLayout {
     size_t sortkey, point_list, keys, clist, total;
 };
 
+// The compact list comes first: it is the only array the blend, the backward
+// and the depth pass read.  The point list and its keys (written on request,
+// after the forward) follow it, and the forward's unsorted keys use their
+// space as scratch.  Nothing at or past an offset depends on R except through
+// that offset, so a buffer laid out for a capacity C >= R serves R: its
+// compact list is at the same place and the point list fits.
 BinLayout bin_layout(int64_t R)
 {
     BinLayout b;
     size_t o = 0;
-    b.sortkey = o; o = align256(o + sizeof(uint64_t) * (size_t)R);
-    b.point_list = o; o = align256(o + sizeof(uint32_t) * (size_t)R);
-    b.keys = o; o = align256(o + sizeof(uint64_t) * (size_t)R);
     b.clist = o; o = align256(o + sizeof(uint32_t) * (size_t)R);
+    b.point_list = o;
+    b.sortkey = o;                                   // 8R bytes inside point list + keys
+    o = align256(o + sizeof(uint32_t) * (size_t)R);
+    b.keys = o; o = align256(o + sizeof(uint64_t) * (size_t)R);
     b.total = o < 256 ? 256 : o;
     return b;
 }
@@ -456,10 +463,16 @@ __device__ __forceinline__ int sort_class(uint32_t n)
     return n <= 512u ? 0 : n <= 1024u ? 1 : n <= 2048u ? 2 : n <= 4096u ? 3 : n <= (uint32_t)SORT_CAP_MAX ? 4 : 5;
 }
 
+//
+// cap: the instance capacity of the caller's binning buffer.  When R exceeds
+// it, meta[9] is set and the class lists are left empty: the ranges, the
+// scatter and the sorts then do nothing (the caller redoes the forward with a
+// buffer for R).
 __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ meta, const uint32_t* __restrict__ tile_count,
                                                         uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
                                                         uint32_t* __restrict__ wcount, int NW, int T,
-                                                        uint32_t* __restrict__ cls_count, int* __restrict__ cls_list)
+                                                        uint32_t* __restrict__ cls_count, int* __restrict__ cls_list,
+                                                        uint64_t cap)
 {
     __shared__ uint32_t s_wave[32];
     __shared__ uint32_t s_cls[SORT_CLASSES];
@@ -495,15 +508,18 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
         base += tot;
     }
     __syncthreads();
-    if (threadIdx.x < SORT_CLASSES) cls_count[threadIdx.x] = s_cls[threadIdx.x];
+    const bool over = base > cap;
+    if (threadIdx.x < SORT_CLASSES) cls_count[threadIdx.x] = over ? 0u : s_cls[threadIdx.x];
     if (threadIdx.x == 0) {
         meta[2] = (uint32_t)(base & 0xffffffffu);
         meta[3] = (uint32_t)(base >> 32);
+        meta[9] = over ? 1u : 0u;
     }
 }
 
-// per tile: ranges, n_render; clears the per-tile blend statistics
-__global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restrict__ loc_map,
+// per tile: ranges, n_render; clears the per-tile blend statistics (all
+// ranges empty when R exceeded the caller's capacity)
+__global__ __launch_bounds__(256) void ranges_kernel(int T, const uint32_t* __restrict__ meta, const int* __restrict__ loc_map,
                                                      const uint32_t* __restrict__ tile_count,
                                                      const uint32_t* __restrict__ tile_start, uint2* __restrict__ ranges,
                                                      int32_t* __restrict__ n_render, int32_t* __restrict__ n_consider,
@@ -513,7 +529,7 @@ __global__ __launch_bounds__(256) void ranges_kernel(int T, const int* __restric
     if (t >= T) return;
     const int l = loc_map[t];
     uint32_t cnt = 0, s = 0;
-    if (l >= 0) { cnt = tile_count[l]; s = tile_start[l]; }
+    if (l >= 0 && meta[9] == 0u) { cnt = tile_count[l]; s = tile_start[l]; }
     ranges[t] = cnt ? make_uint2(s, s + cnt) : make_uint2(0u, 0u);
     if (n_render != nullptr) {   // the split path's per-tile statistics
         n_render[t] = (int32_t)cnt;
@@ -545,6 +561,7 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     const uint32_t* __restrict__ wbase, uint64_t* __restrict__ sortkey, int* __restrict__ cidx_of,
     uint32_t* __restrict__ cid2id, float4* __restrict__ rec, const float2* __restrict__ rects, ZeroOut Z)
 {
+    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: nothing to write
     // dynamic LDS: per wave 64 staged records, then min(T, LDS_TILES) cursors
     extern __shared__ uint4 s_dyn[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -980,11 +997,13 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
             }
         }
         __syncthreads();
+        // all K bases are read before the first item moves (the compiler
+        // cannot tell the item stores from the counter table, so interleaved
+        // reads would each wait for the previous store)
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const uint32_t pos = cnt[cnt_slot((int)((key[k] >> shift) & 15u) * NT + t)] + rk[k];
-            S.items[rpad<LK>((int)pos)] = make_uint2(key[k], val[k]);
-        }
+        for (int k = 0; k < K; k++) rk[k] += cnt[cnt_slot((int)((key[k] >> shift) & 15u) * NT + t)];
+#pragma unroll
+        for (int k = 0; k < K; k++) S.items[rpad<LK>((int)rk[k])] = make_uint2(key[k], val[k]);
         // only this thread reads its column (digit, t) in the scatter: clear
         // it for the next pass
 #pragma unroll
@@ -992,14 +1011,21 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
         __syncthreads();
     }
 
-    // runs of equal depth: order by compact index (one thread per run)
-#pragma unroll 1
+    // runs of equal depth: order by compact index (one thread per run); the
+    // thread's keys and its two neighbours' are read at once
+    uint32_t kn[K + 2];
+#pragma unroll
+    for (int j = 0; j < K + 2; j++) {
+        const int i = t * K - 1 + j;
+        kn[j] = (i >= 0 && i < n) ? S.items[rpad<LK>(i)].x : 0u;
+    }
+#pragma unroll
     for (int k = 0; k < K; k++) {
         const int i = t * K + k;
         if (i + 1 >= n) break;
-        const uint32_t key_i = S.items[rpad<LK>(i)].x;
-        if (S.items[rpad<LK>(i + 1)].x != key_i) continue;
-        if (i > 0 && S.items[rpad<LK>(i - 1)].x == key_i) continue;   // not the run's first item
+        const uint32_t key_i = kn[k + 1];
+        if (kn[k + 2] != key_i) continue;
+        if (i > 0 && kn[k] == key_i) continue;   // not the run's first item
         int e = i + 2;
         while (e < n && e - i <= MAX_TIE_RUN && S.items[rpad<LK>(e)].x == key_i) e++;
         if (e - i > MAX_TIE_RUN) {
@@ -1843,13 +1869,56 @@ int side_streams_for(hipStream_t stream, SideStreams*& out)
     return GS_OK;
 }
 
-// count + scan + R readback, shared by the split and the full-image path
+// Pinned host words for R, one slot per forward in flight: a reserved
+// forward copies R there and records the slot's event, and waits for that
+// event only after the rest of the forward is queued.
+struct Readback {
+    uint32_t* host = nullptr;
+    hipEvent_t ev = nullptr;
+    int dev = -1;
+    bool busy = false;
+};
+constexpr int READBACK_SLOTS = 64;
+std::mutex g_rb_mu;
+Readback g_rb[READBACK_SLOTS];
+
+int readback_acquire(Readback*& out)
+{
+    out = nullptr;
+    int dev = 0;
+    GS_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_rb_mu);
+    for (Readback& r : g_rb) {
+        if (r.busy || (r.dev >= 0 && r.dev != dev)) continue;
+        if (r.dev < 0) {
+            GS_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 2 * sizeof(uint32_t), hipHostMallocDefault));
+            GS_HIP(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
+            r.dev = dev;
+        }
+        r.busy = true;
+        out = &r;
+        return GS_OK;
+    }
+    gs::set_error("more than %d reserved forwards in flight", READBACK_SLOTS);
+    return GS_ERR_SIZE;
+}
+
+void readback_release(Readback* r)
+{
+    std::lock_guard<std::mutex> lk(g_rb_mu);
+    r->busy = false;
+}
+
+// count + scan + R readback, shared by the split and the full-image path.
+// Without a readback slot (rb null) R is copied back synchronously into
+// *num_rendered; with one, the copy into the slot and its event are only
+// queued, and cap is the caller's instance capacity (see tilescan_kernel).
 int render_count_impl(bool full, int P, int W, int H, const float* means2D, const int* radii,
                       const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
-                      int64_t* num_rendered, hipStream_t stream)
+                      int64_t* num_rendered, hipStream_t stream, uint64_t cap = ~0ull, Readback* rb = nullptr)
 {
     GS_REQUIRE(P >= 0 && W > 0 && H > 0, "invalid sizes P=%d W=%d H=%d", P, W, H);
-    GS_REQUIRE(geom != nullptr && num_rendered != nullptr, "geom and num_rendered must be non-null");
+    GS_REQUIRE(geom != nullptr && (num_rendered != nullptr || rb != nullptr), "geom and num_rendered must be non-null");
     GS_REQUIRE(!full || P == 0 || (rects != nullptr && conic_opacity != nullptr),
                "the full path needs rects and conic_opacity");
     GS_REQUIRE(((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0 && ((uintptr_t)conic_opacity & 15) == 0,
@@ -1897,8 +1966,13 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     GS_TIMED("tilescan_kernel", stream,
              hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
                                 at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
-                                at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list)));
+                                at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap));
     GS_LAUNCH_CHECK("tilescan_kernel");
+    if (rb != nullptr) {
+        GS_HIP(hipMemcpyAsync(rb->host, meta + 2, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+        GS_HIP(hipEventRecord(rb->ev, stream));
+        return GS_OK;
+    }
     uint32_t hR[2] = {0, 0};
     GS_HIP(hipMemcpyAsync(hR, meta + 2, sizeof(hR), hipMemcpyDeviceToHost, stream));
     GS_HIP(hipStreamSynchronize(stream));
@@ -1937,7 +2011,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     uint64_t* sortkey = at<uint64_t>(binning, bl.sortkey);
 
     const unsigned T = (unsigned)g.T;
-    GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, loc_map, tile_count,
+    GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, meta, loc_map, tile_count,
                        tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
     GS_LAUNCH_CHECK("ranges_kernel");
     // per-Gaussian accumulators start at zero: inside the scatter when there
@@ -2129,6 +2203,40 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
     return GS_OK;
 }
 
+// Queues the count, the scan and the rest of the forward (forward()) against
+// a binning buffer laid out for `cap` instances, and waits only for R, which
+// arrives while the scatter, sorts and blend still run.  R > cap: the scatter
+// and sorts did nothing (tilescan_kernel) and the caller redoes the forward
+// with a buffer for R.
+template <typename Fwd>
+int reserved_forward(bool full, int P, int64_t cap, int W, int H, const float* means2D, const int* radii,
+                     const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
+                     int64_t* num_rendered, hipStream_t stream, Fwd&& forward)
+{
+    GS_REQUIRE(cap > 0 && cap <= 0xffffffffll, "capacity must be in [1, 2^32 - 1] (got %lld)", (long long)cap);
+    GS_REQUIRE(num_rendered != nullptr, "num_rendered must be non-null");
+    Readback* rb = nullptr;
+    if (int rc = readback_acquire(rb); rc != GS_OK) return rc;
+    int rc = render_count_impl(full, P, W, H, means2D, radii, compute_locally, rects, conic_opacity, geom, nullptr,
+                               stream, (uint64_t)cap, rb);
+    if (rc == GS_OK) rc = forward();
+    // the slot's copy may be queued: wait for it before the slot is reused
+    const hipError_t e = hipEventSynchronize(rb->ev);
+    const uint64_t R = (uint64_t)rb->host[0] | ((uint64_t)rb->host[1] << 32);
+    readback_release(rb);
+    if (rc != GS_OK) return rc;
+    if (e != hipSuccess) {
+        gs::set_error("waiting for the instance count failed: %s", hipGetErrorString(e));
+        return GS_ERR_HIP;
+    }
+    if (R > 0xffffffffull) {
+        gs::set_error("number of tile instances %llu exceeds 2^32-1", (unsigned long long)R);
+        return GS_ERR_SIZE;
+    }
+    *num_rendered = (int64_t)R;
+    return GS_OK;
+}
+
 }  // namespace
 
 extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D, const int* radii,
@@ -2155,6 +2263,29 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
     O.n_contrib_tile = n_contrib;
     return render_forward_impl(BLEND_SPLIT, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
                                compute_locally, nullptr, geom, binning, img, O, n_render, stream);
+}
+
+extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H, const float* bg,
+                                          const float* means2D, const float* depths, const int* radii,
+                                          const float* conic_opacity, const float* rgb,
+                                          const uint8_t* compute_locally, void* geom, void* binning, void* img,
+                                          float* out_color, int32_t* n_render, int32_t* n_consider,
+                                          int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
+                                          hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.out_observe = out_observe;
+    O.n_consider = n_consider;
+    O.n_contrib_tile = n_contrib;
+    return reserved_forward(false, P, capacity, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom,
+                            num_rendered, stream, [&] {
+                                return render_forward_impl(BLEND_SPLIT, P, capacity, W, H, bg, means2D, depths, radii,
+                                                           conic_opacity, rgb, compute_locally, nullptr, geom, binning,
+                                                           img, O, n_render, stream);
+                            });
 }
 
 extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
@@ -2197,6 +2328,32 @@ extern "C" int gs_render_full_forward(int P, int64_t R, int W, int H, const floa
     O.accum_weights_count = accum_weights_count;
     return render_forward_impl(accum_weights != nullptr ? BLEND_SIMP : BLEND_FULL, P, R, W, H, bg, means2D, depths,
                                radii, conic_opacity, colors, nullptr, rects, geom, binning, img, O, nullptr, stream);
+}
+
+extern "C" int gs_render_full_forward_reserved(int P, int64_t capacity, int W, int H, const float* bg,
+                                               const float* means2D, const float* depths, const int* radii,
+                                               const float* rects, const float* conic_opacity, const float* colors,
+                                               void* geom, void* binning, void* img, float* out_color,
+                                               float* accum_max_count, float* accum_weights,
+                                               int32_t* accum_weights_count, int64_t* num_rendered, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(out_color != nullptr, "out_color must be non-null");
+    GS_REQUIRE((accum_weights == nullptr) == (accum_weights_count == nullptr),
+               "accum_weights and accum_weights_count go together");
+    GS_REQUIRE(accum_weights == nullptr || accum_max_count != nullptr, "render_simp needs accum_max_count");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.accum_max_count = accum_max_count;
+    O.accum_weights = accum_weights;
+    O.accum_weights_count = accum_weights_count;
+    return reserved_forward(true, P, capacity, W, H, means2D, radii, nullptr, rects, conic_opacity, geom,
+                            num_rendered, stream, [&] {
+                                return render_forward_impl(accum_weights != nullptr ? BLEND_SIMP : BLEND_FULL, P,
+                                                           capacity, W, H, bg, means2D, depths, radii, conic_opacity,
+                                                           colors, nullptr, rects, geom, binning, img, O, nullptr,
+                                                           stream);
+                            });
 }
 
 extern "C" int gs_render_full_depth(int P, int64_t R, int W, int H, const float* bg, const float* means2D,

@@ -139,14 +139,35 @@ def _forward(rs, x, culling, flag_max_count, simp, depth=False):
             ptr(g["conic"]), ptr(g["rgb"]), ptr(g["clamped"]), ptr(g["rects"]), ptr(g["tiles"]), s),
             "gs_preprocess_forward_full")
     rws = gl.render_ws(geom)
+    img = torch.empty(int(lib.gs_render_img_bytes(W, H)), dtype=torch.uint8, device=dev)
+    colors = x["colors_precomp"] if x["colors_precomp"] is not None else g["rgb"]
+    want_amc = flag_max_count or simp
+    cap = None if depth else _lib.RESERVE.capacity(dev)
+    if cap is not None:
+        # one call, no host round trip between the count and the duplication
+        binning = torch.empty(int(lib.gs_render_binning_bytes(cap)), dtype=torch.uint8, device=dev)
+        Rv = _lib.C.c_int64(0)
+        check(lib.gs_render_full_forward_reserved(
+            P, cap, W, H, ptr(x["bg"]), ptr(g["means2D"]), ptr(g["depths"]), ptr(radii), ptr(g["rects"]),
+            ptr(g["conic"]), ptr(colors), ptr(rws), ptr(binning), ptr(img), ptr(color),
+            ptr(amc) if want_amc else None, ptr(aw), ptr(awc), _lib.C.byref(Rv), s), "gs_render_full_forward_reserved")
+        _lib.RESERVE.update(dev, int(Rv.value))
+        if Rv.value <= cap:
+            R = int(Rv.value)
+            geom[:8].view(torch.int64).fill_(R)
+            if not want_amc:
+                amc.zero_()
+            _lib.debug_sync(getattr(rs, "debug", False), "rasterize_gaussians")
+            return color, radii, amc, aw, awc, geom, binning, img, R
+    # the exact path: first forward on the device, more instances than
+    # reserved, or the depth render
     R = _lib.C.c_int64(0)
     check(lib.gs_render_full_count(P, W, H, ptr(g["means2D"]), ptr(radii), ptr(g["rects"]), ptr(g["conic"]),
                                    ptr(rws), _lib.C.byref(R), s), "gs_render_full_count")
     R = int(R.value)
-    geom[:8].copy_(torch.tensor([R], dtype=torch.int64).view(torch.uint8), non_blocking=False)
+    _lib.RESERVE.update(dev, R)
+    geom[:8].view(torch.int64).fill_(R)
     binning = torch.empty(int(lib.gs_render_binning_bytes(R)), dtype=torch.uint8, device=dev)
-    img = torch.empty(int(lib.gs_render_img_bytes(W, H)), dtype=torch.uint8, device=dev)
-    colors = x["colors_precomp"] if x["colors_precomp"] is not None else g["rgb"]
     if depth:
         d = dict(out_pts=torch.empty((3, H, W), dtype=torch.float32, device=dev),
                  depth=torch.empty((1, H, W), dtype=torch.float32, device=dev),
@@ -163,9 +184,9 @@ def _forward(rs, x, culling, flag_max_count, simp, depth=False):
         return color, radii, d, None, None, geom, binning, img, R
     check(lib.gs_render_full_forward(P, R, W, H, ptr(x["bg"]), ptr(g["means2D"]), ptr(g["depths"]), ptr(radii),
                                      ptr(g["rects"]), ptr(g["conic"]), ptr(colors), ptr(rws), ptr(binning), ptr(img),
-                                     ptr(color), ptr(amc) if (flag_max_count or simp) else None, ptr(aw), ptr(awc),
+                                     ptr(color), ptr(amc) if want_amc else None, ptr(aw), ptr(awc),
                                      s), "gs_render_full_forward")
-    if not (flag_max_count or simp):
+    if not want_amc:
         amc.zero_()
     _lib.debug_sync(getattr(rs, "debug", False), "rasterize_gaussians")
     return color, radii, amc, aw, awc, geom, binning, img, R

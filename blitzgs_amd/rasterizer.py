@@ -200,7 +200,9 @@ def _tile_mask(cl, H, W, device):
 def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False,
                         debug=False):
     """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
-    geomBuffer, binningBuffer, imgBuffer, render_ms)."""
+    geomBuffer, binningBuffer, imgBuffer, render_ms).  The binning buffer may be
+    sized for more than num_rendered instances (_lib.InstanceReserve); render_ms
+    covers the whole render forward, the instance count included."""
     _require_device(means2D, "means2D")
     dev = means2D.device
     P = means2D.size(0)
@@ -217,24 +219,38 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     stream = _stream(dev)
     geom = torch.empty(lib.gs_render_geom_bytes(P, W, H), device=dev, dtype=torch.uint8)
     img = torch.empty(lib.gs_render_img_bytes(W, H), device=dev, dtype=torch.uint8)
-    # everything that does not depend on R is allocated before the count call,
-    # whose R readback synchronises the stream
     color = torch.empty((3, H, W), device=dev, dtype=torch.float32)
     n_render = torch.empty((T,), **i32)
     n_consider = torch.empty((T,), **i32)
     n_contrib = torch.empty((T,), **i32)
     out_observe = torch.empty((P,), **i32)
-    R = C.c_int64(0)
-    check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(R), stream),
-          "gs_render_forward_count")
-    R = int(R.value)
-    binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
+    outs = (ptr(color), ptr(n_render), ptr(n_consider), ptr(n_contrib), ptr(out_observe))
     if timing:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
-    check(lib.gs_render_forward(P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity),
-                                ptr(rgb), ptr(cl), ptr(geom), ptr(binning), ptr(img), ptr(color), ptr(n_render),
-                                ptr(n_consider), ptr(n_contrib), ptr(out_observe), stream), "gs_render_forward")
+    R = None
+    cap = _lib.RESERVE.capacity(dev)
+    if cap is not None:
+        # one call, no host round trip between the count and the duplication
+        binning = torch.empty(lib.gs_render_binning_bytes(cap), device=dev, dtype=torch.uint8)
+        Rv = C.c_int64(0)
+        check(lib.gs_render_forward_reserved(P, cap, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii),
+                                             ptr(conic_opacity), ptr(rgb), ptr(cl), ptr(geom), ptr(binning),
+                                             ptr(img), *outs, C.byref(Rv), stream), "gs_render_forward_reserved")
+        _lib.RESERVE.update(dev, int(Rv.value))
+        R = int(Rv.value) if Rv.value <= cap else None
+    if R is None:
+        # first forward on the device, or more instances than reserved: count,
+        # then size the binning buffer exactly
+        Rv = C.c_int64(0)
+        check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(Rv),
+                                          stream), "gs_render_forward_count")
+        R = int(Rv.value)
+        _lib.RESERVE.update(dev, R)
+        binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
+        check(lib.gs_render_forward(P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity),
+                                    ptr(rgb), ptr(cl), ptr(geom), ptr(binning), ptr(img), *outs, stream),
+              "gs_render_forward")
     _lib.debug_sync(debug, "gs_render_forward")
     ms = None
     if timing:

@@ -92,7 +92,9 @@ int gs_preprocess_backward(int P, int D, int K, const float* means3D, const floa
  * cuda_rasterizer/rasterizer_impl.cu:556-723, forward.cu:263-413).
  *
  *   geom    : gs_render_geom_bytes(P, W, H) bytes  (counts, offsets)
- *   binning : gs_render_binning_bytes(R) bytes     (sorted keys and ids)
+ *   binning : gs_render_binning_bytes(R) bytes     (the blend's sorted list;
+ *             the point list and its keys on request; a buffer sized for a
+ *             capacity >= R serves R)
  *   img     : gs_render_img_bytes(W, H) bytes      (tile ranges, per-pixel
  *             final transmittance and contributor counts)
  * compute_locally is a uint8 (ceil(H/16), ceil(W/16)) tile mask, or NULL
@@ -121,12 +123,30 @@ int gs_render_forward(int P, int64_t R, int image_width, int image_height, const
                       int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe,
                       gs_stream_t stream);
 
+/* The two calls above in one, without the host round trip between them: the
+ * count, the duplication, the sorts and the blend are all queued at once
+ * against a binning buffer of gs_render_binning_bytes(capacity) bytes, and
+ * the call waits only for R (copied back as soon as the count is done, while
+ * the rest still runs).  R is returned in *num_rendered.  If R > capacity the
+ * duplication, sorts and blend did nothing useful: the caller sizes a binning
+ * buffer for R and repeats the forward with gs_render_forward_count and
+ * gs_render_forward.  Same outputs and workspaces as those two calls; the
+ * forward of rasterize_points.cu:273-361, whose host reads R back
+ * (rasterizer_impl.cu:621) before it can size and launch the duplication. */
+int gs_render_forward_reserved(int P, int64_t capacity, int image_width, int image_height,
+                               const float* bg, const float* means2D, const float* depths,
+                               const int* radii, const float* conic_opacity, const float* rgb,
+                               const uint8_t* compute_locally, void* geom, void* binning, void* img,
+                               float* out_color, int32_t* n_render, int32_t* n_consider,
+                               int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
+                               gs_stream_t stream);
+
 /* Render backward.  Replaces RenderGaussiansBackwardCUDA
  * (diff-gaussian-rasterization_r/rasterize_points.cu:363-436; kernel
  * cuda_rasterizer/backward.cu:324-530).
  *   geom / binning / img: the forward's workspaces (geom also holds the
- *   gradient accumulators, cleared again on exit, so calls sharing one geom
- *   must not overlap).  means2D / conic_opacity / rgb: the forward's inputs
+ *   gradient accumulators, cleared at the start of each call, so calls
+ *   sharing one geom must not overlap).  means2D / conic_opacity / rgb: the forward's inputs
  *   (the kernels read the forward's packed copy of them in geom).
  *   dL_dpixels (3,H,W).  Outputs: dL_dmeans2D (row stride dL_dmeans2D_stride,
  *   2 or 3; the third column, when present, is zero), dL_dmeans2D_abs (P,3),
@@ -283,6 +303,15 @@ int gs_render_full_forward(int P, int64_t R, int image_width, int image_height, 
                            const float* conic_opacity, const float* colors, void* geom, void* binning,
                            void* img, float* out_color, float* accum_max_count, float* accum_weights,
                            int32_t* accum_weights_count, gs_stream_t stream);
+/* gs_render_full_count + gs_render_full_forward in one call with a reserved
+ * binning capacity, as gs_render_forward_reserved. */
+int gs_render_full_forward_reserved(int P, int64_t capacity, int image_width, int image_height,
+                                    const float* bg, const float* means2D, const float* depths,
+                                    const int* radii, const float* rects, const float* conic_opacity,
+                                    const float* colors, void* geom, void* binning, void* img,
+                                    float* out_color, float* accum_max_count, float* accum_weights,
+                                    int32_t* accum_weights_count, int64_t* num_rendered,
+                                    gs_stream_t stream);
 int gs_render_full_depth(int P, int64_t R, int image_width, int image_height, const float* bg,
                          const float* means2D, const float* depths, const int* radii, const float* rects,
                          const float* conic_opacity, const float* colors, const float* means3D,

@@ -456,10 +456,11 @@ def test_masked_step_more_than_16384_local_tiles_vs_oracle():
     check_step(g, pre, bn, rf, rb, pb)
 
 
-def test_forward_leaves_point_list_unwritten_until_requested():
-    """The forward keeps only the blend's compact list: the reference's sorted
-    ids and keys are written by gs_render_point_list when a caller asks (the
-    binning buffer's bytes for them stay as they were until then)."""
+def test_point_list_written_on_request():
+    """The forward keeps only the blend's compact list (its unsorted keys use
+    the point list's space as scratch): the blend is right without the
+    reference's sorted ids and keys, which gs_render_point_list writes when a
+    caller asks."""
     import ctypes as C
     scene, cam = synth.small_scene(5000, seed=8, W=240, H=176, extent=1.5, log_mu=-2.2)
     pre = _oracle_pre(scene, cam)
@@ -487,9 +488,6 @@ def test_forward_leaves_point_list_unwritten_until_requested():
                "forward")
     torch.cuda.synchronize()
     from tests.gpu_helpers import buffer_views
-    untouched = buffer_views(R, W, H, binning, img)
-    assert (untouched["point_list"].view(torch.uint8) == 0xAB).all()
-    assert (untouched["keys"].view(torch.uint8) == 0xAB).all()
     ob = O.binning(W, H, pre["means2D"], pre["depths"], pre["radii"])
     orf = O.render_fwd(W, H, np.zeros(3, np.float32), pre["means2D"], pre["conic_opacity"], pre["rgb"], ob["ranges"],
                        ob["point_list"])

@@ -190,6 +190,30 @@ __device__ __forceinline__ void load_sh_split(const float* __restrict__ dc, cons
     for (int i = 0; i < 3 * (NC - 1); i++) s[3 + i] = rest[i];
 }
 
+// 3D covariance (upper triangle) of Gaussian idx from its scale and
+// rotation: Sigma = M^T M with M = diag(mod * scale) R (reference
+// forward.cu:118-150).  The backward recomputes it with this same function
+// when the forward's copy was not kept.
+__device__ __forceinline__ void cov3d_of(const float* __restrict__ scales, const float* __restrict__ rotations, int idx,
+                                         float mod, float* c6)
+{
+    const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
+    float Rm[3][3];
+    quat_rows(q.x, q.y, q.z, q.w, Rm);
+    const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
+    float M[3][3];
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) M[i][j] = s[i] * Rm[i][j];
+    c6[0] = M[0][0] * M[0][0] + M[1][0] * M[1][0] + M[2][0] * M[2][0];
+    c6[1] = M[0][0] * M[0][1] + M[1][0] * M[1][1] + M[2][0] * M[2][1];
+    c6[2] = M[0][0] * M[0][2] + M[1][0] * M[1][2] + M[2][0] * M[2][2];
+    c6[3] = M[0][1] * M[0][1] + M[1][1] * M[1][1] + M[2][1] * M[2][1];
+    c6[4] = M[0][1] * M[0][2] + M[1][1] * M[1][2] + M[2][1] * M[2][2];
+    c6[5] = M[0][2] * M[0][2] + M[1][2] * M[1][2] + M[2][2] * M[2][2];
+}
+
 template <int DEG, bool FULL>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
@@ -227,21 +251,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 #pragma unroll
             for (int k = 0; k < 6; k++) c6[k] = F.cov3D_precomp[6 * (size_t)idx + k];
         } else {
-            const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
-            float Rm[3][3];
-            quat_rows(q.x, q.y, q.z, q.w, Rm);
-            const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
-            float M[3][3];
-#pragma unroll
-            for (int i = 0; i < 3; i++)
-#pragma unroll
-                for (int j = 0; j < 3; j++) M[i][j] = s[i] * Rm[i][j];
-            c6[0] = M[0][0] * M[0][0] + M[1][0] * M[1][0] + M[2][0] * M[2][0];
-            c6[1] = M[0][0] * M[0][1] + M[1][0] * M[1][1] + M[2][0] * M[2][1];
-            c6[2] = M[0][0] * M[0][2] + M[1][0] * M[1][2] + M[2][0] * M[2][2];
-            c6[3] = M[0][1] * M[0][1] + M[1][1] * M[1][1] + M[2][1] * M[2][1];
-            c6[4] = M[0][1] * M[0][2] + M[1][1] * M[1][2] + M[2][1] * M[2][2];
-            c6[5] = M[0][2] * M[0][2] + M[1][2] * M[1][2] + M[2][2] * M[2][2];
+            cov3d_of(scales, rotations, idx, mod, c6);
         }
 
         Ewa e;
@@ -312,10 +322,12 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     reinterpret_cast<float2*>(means2D)[idx] = make_float2(o_m2d[0], o_m2d[1]);
     depths[idx] = o_depth;
     radii[idx] = o_radius;
-    float2* c2 = reinterpret_cast<float2*>(cov3D + 6 * (size_t)idx);
-    c2[0] = make_float2(c6[0], c6[1]);
-    c2[1] = make_float2(c6[2], c6[3]);
-    c2[2] = make_float2(c6[4], c6[5]);
+    if (cov3D != nullptr) {   // (null: the caller keeps no copy; the backward recomputes it)
+        float2* c2 = reinterpret_cast<float2*>(cov3D + 6 * (size_t)idx);
+        c2[0] = make_float2(c6[0], c6[1]);
+        c2[1] = make_float2(c6[2], c6[3]);
+        c2[2] = make_float2(c6[4], c6[5]);
+    }
     reinterpret_cast<float4*>(conic_opacity)[idx] = make_float4(o_con[0], o_con[1], o_con[2], o_con[3]);
     rgb[3 * idx + 0] = o_rgb[0];
     rgb[3 * idx + 1] = o_rgb[1];
@@ -413,9 +425,10 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
     const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
-    float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
+    float* __restrict__ m3_row, float* __restrict__ sc_row, float* __restrict__ dL_drotations,
     float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row, const FullPreBwd& F)
 {
+    // m3_row / sc_row: this Gaussian's dL/dmeans3D and dL/dscales rows
     constexpr int NC = (DEG + 1) * (DEG + 1);
     const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
     dL_dopacity[idx] = gco.w;
@@ -430,10 +443,12 @@ __device__ __forceinline__ void preprocess_bwd_one(
     if (FULL && F.cov3D_precomp != nullptr) {
 #pragma unroll
         for (int k = 0; k < 6; k++) c6[k] = F.cov3D_precomp[6 * (size_t)idx + k];
-    } else {
+    } else if (cov3D != nullptr) {
         const float2* c2 = reinterpret_cast<const float2*>(cov3D + 6 * (size_t)idx);
         const float2 a = c2[0], b = c2[1], c = c2[2];
         c6[0] = a.x; c6[1] = a.y; c6[2] = b.x; c6[3] = b.y; c6[4] = c.x; c6[5] = c.y;
+    } else {
+        cov3d_of(scales, rotations, idx, mod, c6);   // the forward's value, recomputed
     }
 
     // ---- conic -> 2D covariance -> 3D covariance and mean (cov2D backward)
@@ -553,15 +568,15 @@ __device__ __forceinline__ void preprocess_bwd_one(
             for (int i = 3 * NC; i < 3 * K; i++) gsh_out[i] = 0.f;
         }
     }
-    dL_dmeans3D[3 * idx + 0] = gm[0];
-    dL_dmeans3D[3 * idx + 1] = gm[1];
-    dL_dmeans3D[3 * idx + 2] = gm[2];
+    m3_row[0] = gm[0];
+    m3_row[1] = gm[1];
+    m3_row[2] = gm[2];
 
     // ---- 3D covariance -> scale and (un-normalised) quaternion
     if (FULL && F.cov3D_precomp != nullptr) {
-        dL_dscales[3 * idx + 0] = 0.f;
-        dL_dscales[3 * idx + 1] = 0.f;
-        dL_dscales[3 * idx + 2] = 0.f;
+        sc_row[0] = 0.f;
+        sc_row[1] = 0.f;
+        sc_row[2] = 0.f;
         reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
         const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
@@ -585,7 +600,7 @@ __device__ __forceinline__ void preprocess_bwd_one(
                 G[i][j] = (2.0f * M[i][0]) * D[0][j] + (2.0f * M[i][1]) * D[1][j] + (2.0f * M[i][2]) * D[2][j];
 #pragma unroll
         for (int i = 0; i < 3; i++)
-            dL_dscales[3 * idx + i] = Rm[i][0] * G[i][0] + Rm[i][1] * G[i][1] + Rm[i][2] * G[i][2];
+            sc_row[i] = Rm[i][0] * G[i][0] + Rm[i][1] * G[i][1] + Rm[i][2] * G[i][2];
 #pragma unroll
         for (int i = 0; i < 3; i++)
 #pragma unroll
@@ -621,18 +636,22 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     const bool in = idx < P;
     const bool vis = in && radii[idx] > 0;
+    // this Gaussian's dL/dmeans3D and dL/dscales rows (stored directly: staging
+    // them in LDS for whole-line stores measured slower)
+    float* m3_row = dL_dmeans3D + 3 * (size_t)idx;
+    float* sc_row = dL_dscales + 3 * (size_t)idx;
     // staged rows hold SH gradients (the full path has none with precomputed
     // colours or without a rest array)
     const bool sh_rows = !FULL || (!F.colors_precomp && F.rest != nullptr);
     if (STAGED) s_vis[threadIdx.x] = (vis && sh_rows) ? 1 : 0;
     if (in && !vis) {
         dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
-        dL_dmeans3D[3 * idx + 0] = 0.f;
-        dL_dmeans3D[3 * idx + 1] = 0.f;
-        dL_dmeans3D[3 * idx + 2] = 0.f;
-        dL_dscales[3 * idx + 0] = 0.f;
-        dL_dscales[3 * idx + 1] = 0.f;
-        dL_dscales[3 * idx + 2] = 0.f;
+        m3_row[0] = 0.f;
+        m3_row[1] = 0.f;
+        m3_row[2] = 0.f;
+        sc_row[0] = 0.f;
+        sc_row[1] = 0.f;
+        sc_row[2] = 0.f;
         reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (FULL) {
             for (int k = 0; k < 6; k++) F.dL_dcov3D[6 * (size_t)idx + k] = 0.f;
@@ -657,7 +676,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     if (vis) preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
                                                     means3D, scales, rotations, sh, sh_vec16, cov3D, clamped,
                                                     dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb,
-                                                    dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity,
+                                                    m3_row, sc_row, dL_drotations, dL_dsh, dL_dopacity,
                                                     s_sh + threadIdx.x * SH_PITCH, F);
     if (STAGED && FULL) {
         // coalesced copy-out of this block's rows [blockIdx*256, +nrows): 3 DC floats, then 3M rest floats

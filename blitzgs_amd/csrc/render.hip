@@ -29,12 +29,13 @@
 //   3. scatter : each block re-walks its chunk, appends (depth bits, compact
 //                index) to its reserved slices (LDS cursors) and writes each
 //                listed Gaussian's 64-byte blend record at its compact index.
-//   4. sort    : one block per tile sorts its bucket by (depth bits, compact
-//                index) in registers (bitonic, five size classes, each class
-//                walking its own list of buckets, the classes side by side on
-//                side streams for large R) and writes the sorted Gaussian ids,
-//                the (tile << 32 | depth bits) keys and the compact list the
-//                blend walks.
+//   4. sort    : one block (or wave) per tile sorts its bucket by (depth
+//                bits, compact index) on chip -- a register bitonic network
+//                up to 512 keys, an LDS radix sort up to 8192, a bitonic
+//                network in global memory beyond -- in size classes, each
+//                class walking its own list of buckets, and writes the
+//                compact list the blend walks (the reference's sorted ids and
+//                keys are derived from it on request).
 // The compact index is increasing in Gaussian id, so each sorted bucket is
 // exactly the order of a stable sort of the reference's duplicated keys, and
 // the sorted arrays and the ranges are bit-identical to the reference
@@ -65,8 +66,6 @@ constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
 constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
-constexpr int64_t SIDE_STREAM_MIN_R = 1 << 21;   // instances from which the size classes sort concurrently
-constexpr int BIG_SORT_THREADS = 1024;
 constexpr const char* BINNING_STAGE = "binning (wall)";   // per-kernel timing: the whole binning stage
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
@@ -804,33 +803,22 @@ __device__ __forceinline__ void sort_merges(uint64_t (&k)[8])
     }
 }
 
-// Buckets of up to 512 keys: one wave per bucket, by (depth bits, compact
-// index), padded with all-ones keys; blocks walk the class's bucket list.
-__global__ __launch_bounds__(64) void tilesort_wave_kernel(const uint32_t* __restrict__ cls_count,
-                                                          const int* __restrict__ cls_list,
-                                                          const uint32_t* __restrict__ tile_count,
-                                                          const uint32_t* __restrict__ tile_start,
-                                                          const uint64_t* __restrict__ sortkey,
-                                                          uint32_t* __restrict__ clist)
+// A bucket of up to 512 keys sorted by one wave (lane = this thread's lane),
+// by (depth bits, compact index), padded with all-ones keys.
+__device__ __forceinline__ void wave_sort_bucket(uint32_t start, int n, const uint64_t* __restrict__ sortkey,
+                                                 uint32_t* __restrict__ clist, int lane)
 {
-    const int nl = (int)*cls_count;
-    const int t = threadIdx.x;
-    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
-        const int l = cls_list[e];
-        const int n = (int)tile_count[l];
-        const uint32_t start = tile_start[l];
-        uint64_t k[8];
+    uint64_t k[8];
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const int i = 8 * t + r;
-            k[r] = i < n ? sortkey[start + i] : ~0ull;
-        }
-        sort_merges<2>(k);
+    for (int r = 0; r < 8; r++) {
+        const int i = 8 * lane + r;
+        k[r] = i < n ? sortkey[start + i] : ~0ull;
+    }
+    sort_merges<2>(k);
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const int i = 8 * t + r;
-            if (i < n) clist[start + i] = (uint32_t)k[r];
-        }
+    for (int r = 0; r < 8; r++) {
+        const int i = 8 * lane + r;
+        if (i < n) clist[start + i] = (uint32_t)k[r];
     }
 }
 
@@ -1061,13 +1049,22 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
 }
 
 // One launch per size class; its blocks walk the class's list of buckets
-// (block b takes entries b, b + gridDim.x, ...).
-template <int NT, int K>
+// (block b takes entries b, b + gridDim.x, ...).  A launch also takes a
+// second list (xcount / xlist) when EXTRA says so, so that the smallest and
+// the largest buckets need no launches of their own:
+//   EXTRA_WAVE: buckets of up to 512 keys, one per wave (wave_sort_bucket);
+//   EXTRA_BIG : buckets of more than SORT_CAP_MAX keys, one per block (the
+//               64-bit bitonic network in global memory, in place).
+constexpr int EXTRA_NONE = 0, EXTRA_WAVE = 1, EXTRA_BIG = 2;
+
+template <int NT, int K, int EXTRA = EXTRA_NONE>
 __global__ __launch_bounds__(NT) void tilesort_radix_kernel(const uint32_t* __restrict__ cls_count,
                                                            const int* __restrict__ cls_list,
                                                            const uint32_t* __restrict__ tile_count,
                                                            const uint32_t* __restrict__ tile_start,
-                                                           uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist)
+                                                           uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist,
+                                                           const uint32_t* __restrict__ xcount,
+                                                           const int* __restrict__ xlist)
 {
     __shared__ RadixLds<NT, K> S;
     const int nl = (int)*cls_count;
@@ -1076,25 +1073,27 @@ __global__ __launch_bounds__(NT) void tilesort_radix_kernel(const uint32_t* __re
         const int l = cls_list[e];
         radix_sort_bucket<NT, K>(tile_start[l], (int)tile_count[l], sortkey, clist, S);
     }
-}
-
-// Buckets larger than the biggest LDS class: the 64-bit bitonic network in
-// global memory, in place.
-__global__ __launch_bounds__(BIG_SORT_THREADS) void tilesort_big_kernel(
-    const uint32_t* __restrict__ cls_count, const int* __restrict__ cls_list, const uint32_t* __restrict__ tile_count,
-    const uint32_t* __restrict__ tile_start, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist)
-{
-    const int nl = (int)*cls_count;
-    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
-        if (e != (int)blockIdx.x) __syncthreads();
-        const int l = cls_list[e];
-        const int n = (int)tile_count[l];
-        const uint32_t start = tile_start[l];
-        uint64_t* s = sortkey + start;
-        int N = 1;
-        while (N < n) N <<= 1;
-        bitonic<BIG_SORT_THREADS>(s, n, N);
-        write_sorted(start, n, s, clist, BIG_SORT_THREADS);
+    if constexpr (EXTRA == EXTRA_WAVE) {
+        // no block barrier from here on: every wave sorts its own buckets
+        constexpr int NW = NT / 64;
+        const int nx = (int)*xcount;
+        for (int e = blockIdx.x * NW + (int)(threadIdx.x >> 6); e < nx; e += gridDim.x * NW) {
+            const int l = xlist[e];
+            wave_sort_bucket(tile_start[l], (int)tile_count[l], sortkey, clist, threadIdx.x & 63);
+        }
+    } else if constexpr (EXTRA == EXTRA_BIG) {
+        const int nx = (int)*xcount;
+        for (int e = blockIdx.x; e < nx; e += gridDim.x) {
+            const int l = xlist[e];
+            const int n = (int)tile_count[l];
+            const uint32_t start = tile_start[l];
+            uint64_t* s = sortkey + start;
+            int N = 1;
+            while (N < n) N <<= 1;
+            __syncthreads();
+            bitonic<NT>(s, n, N);
+            write_sorted(start, n, s, clist, NT);
+        }
     }
 }
 
@@ -1838,37 +1837,6 @@ namespace {
 // latency-bound, so the classes run side by side (forked from and joined back
 // to the caller's stream with events).  Created once per device, at the
 // default priority, never destroyed.
-struct SideStreams {
-    std::mutex mu;
-    bool ready = false;
-    hipStream_t s[SORT_CLASSES];
-    hipEvent_t fork, join[SORT_CLASSES];
-};
-constexpr int MAX_DEVICES = 64;
-SideStreams g_side[MAX_DEVICES];
-
-// the side streams of the stream's device (null if it is not the current device)
-int side_streams_for(hipStream_t stream, SideStreams*& out)
-{
-    out = nullptr;
-    int cur = 0, sdev = -1;
-    GS_HIP(hipGetDevice(&cur));
-    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != cur || cur < 0 || cur >= MAX_DEVICES) {
-        (void)hipGetLastError();
-        return GS_OK;
-    }
-    SideStreams& ss = g_side[cur];
-    std::lock_guard<std::mutex> lk(ss.mu);
-    if (!ss.ready) {
-        for (int c = 0; c < SORT_CLASSES; c++) GS_HIP(hipStreamCreateWithFlags(&ss.s[c], hipStreamNonBlocking));
-        GS_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
-        for (int c = 0; c < SORT_CLASSES; c++) GS_HIP(hipEventCreateWithFlags(&ss.join[c], hipEventDisableTiming));
-        ss.ready = true;
-    }
-    out = &ss;
-    return GS_OK;
-}
-
 // Pinned host words for R, one slot per forward in flight: a reserved
 // forward copies R there and records the slot's event, and waits for that
 // event only after the rest of the forward is queued.
@@ -2047,75 +2015,47 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         }
         GS_LAUNCH_CHECK("scatter_kernel");
         uint32_t* clist = at<uint32_t>(binning, bl.clist);
-        // one launch per size class over that class's bucket list; the grid is
-        // bounded by how many buckets of the class R instances can fill and
-        // by what fits on the chip at once
+        // one launch per LDS size class over that class's bucket list, one
+        // after another on the caller's stream (run side by side on streams
+        // of their own they contend for the same CUs and add a fork and a
+        // join, which measured slower); the buckets of up to 512 keys ride
+        // with the 1024-key class, those above SORT_CAP_MAX with the 8192-key
+        // class.  The grid is bounded by how many buckets of the class R
+        // instances can fill and by what fits on the chip at once.
         const uint32_t* cc = at<const uint32_t>(geom, g.cls_count);
         const int* cls = at<const int>(geom, g.cls_list);
         auto grid_of = [&](int lo, int cap) {
             const int64_t fit = R / (int64_t)(lo + 1);
             return (unsigned)std::min<int64_t>(std::min<int64_t>((int64_t)T, fit), (int64_t)cap);
         };
-        const unsigned gcs[SORT_CLASSES] = {grid_of(0, 8192), grid_of(512, 4096), grid_of(1024, 2048),
-                                            grid_of(2048, 2048), grid_of(4096, 1024), grid_of(SORT_CAP_MAX, 256)};
-        // side streams pay off once the sorts are long enough to hide the
-        // fork / join (small scenes sort on the caller's stream)
-        SideStreams* ss = nullptr;
-        if (R >= SIDE_STREAM_MIN_R) {
-            if (int rc = side_streams_for(stream, ss); rc != GS_OK) return rc;
+        auto list = [&](int c) { return cls + (size_t)c * T; };
+        const unsigned g_wave = (grid_of(0, 8192) + 1) / 2;   // two waves per 128-thread block
+        const unsigned g1 = std::max(grid_of(512, 4096), g_wave);
+        const unsigned g2 = grid_of(1024, 2048), g3 = grid_of(2048, 2048);
+        const unsigned g4 = std::max(grid_of(4096, 1024), grid_of(SORT_CAP_MAX, 256));
+        if (g4 > 0) {
+            GS_TIMED("tilesort_kernel_8k", stream,
+                     hipLaunchKernelGGL((tilesort_radix_kernel<512, 16, EXTRA_BIG>), dim3(g4), dim3(512), 0, stream,
+                                        cc + 4, list(4), tile_count, tile_start, sortkey, clist, cc + 5, list(5)));
+            GS_LAUNCH_CHECK("tilesort_kernel_8k");
         }
-        std::unique_lock<std::mutex> lk;
-        if (ss != nullptr) {
-            lk = std::unique_lock<std::mutex>(ss->mu);
-            GS_HIP(hipEventRecord(ss->fork, stream));
+        if (g3 > 0) {
+            GS_TIMED("tilesort_kernel_4k", stream,
+                     hipLaunchKernelGGL((tilesort_radix_kernel<256, 16>), dim3(g3), dim3(256), 0, stream, cc + 3,
+                                        list(3), tile_count, tile_start, sortkey, clist, nullptr, nullptr));
+            GS_LAUNCH_CHECK("tilesort_kernel_4k");
         }
-        for (int c = SORT_CLASSES - 1; c >= 0; c--) {
-            const unsigned gc = gcs[c];
-            if (gc == 0) continue;
-            hipStream_t cs = stream;
-            if (ss != nullptr) {
-                cs = ss->s[c];
-                GS_HIP(hipStreamWaitEvent(cs, ss->fork, 0));
-            }
-            const uint32_t* ccc = cc + c;
-            const int* cl = cls + (size_t)c * T;
-            switch (c) {
-            case 0:
-                GS_TIMED("tilesort_kernel_512", cs,
-                         hipLaunchKernelGGL(tilesort_wave_kernel, dim3(gc), dim3(64), 0, cs, ccc, cl, tile_count,
-                                            tile_start, sortkey, clist));
-                break;
-            case 1:
-                GS_TIMED("tilesort_kernel_1k", cs,
-                         hipLaunchKernelGGL((tilesort_radix_kernel<128, 8>), dim3(gc), dim3(128), 0, cs, ccc, cl,
-                                            tile_count, tile_start, sortkey, clist));
-                break;
-            case 2:
-                GS_TIMED("tilesort_kernel_2k", cs,
-                         hipLaunchKernelGGL((tilesort_radix_kernel<256, 8>), dim3(gc), dim3(256), 0, cs, ccc, cl,
-                                            tile_count, tile_start, sortkey, clist));
-                break;
-            case 3:
-                GS_TIMED("tilesort_kernel_4k", cs,
-                         hipLaunchKernelGGL((tilesort_radix_kernel<256, 16>), dim3(gc), dim3(256), 0, cs, ccc, cl,
-                                            tile_count, tile_start, sortkey, clist));
-                break;
-            case 4:
-                GS_TIMED("tilesort_kernel_8k", cs,
-                         hipLaunchKernelGGL((tilesort_radix_kernel<512, 16>), dim3(gc), dim3(512), 0, cs, ccc, cl,
-                                            tile_count, tile_start, sortkey, clist));
-                break;
-            default:
-                GS_TIMED("tilesort_big_kernel", cs,
-                         hipLaunchKernelGGL(tilesort_big_kernel, dim3(gc), dim3(BIG_SORT_THREADS), 0, cs, ccc, cl,
-                                            tile_count, tile_start, sortkey, clist));
-                break;
-            }
-            GS_LAUNCH_CHECK("tilesort_kernel");
-            if (ss != nullptr) {
-                GS_HIP(hipEventRecord(ss->join[c], cs));
-                GS_HIP(hipStreamWaitEvent(stream, ss->join[c], 0));
-            }
+        if (g2 > 0) {
+            GS_TIMED("tilesort_kernel_2k", stream,
+                     hipLaunchKernelGGL((tilesort_radix_kernel<256, 8>), dim3(g2), dim3(256), 0, stream, cc + 2,
+                                        list(2), tile_count, tile_start, sortkey, clist, nullptr, nullptr));
+            GS_LAUNCH_CHECK("tilesort_kernel_2k");
+        }
+        if (g1 > 0) {
+            GS_TIMED("tilesort_kernel_1k", stream,
+                     hipLaunchKernelGGL((tilesort_radix_kernel<128, 8, EXTRA_WAVE>), dim3(g1), dim3(128), 0, stream,
+                                        cc + 1, list(1), tile_count, tile_start, sortkey, clist, cc + 0, list(0)));
+            GS_LAUNCH_CHECK("tilesort_kernel_1k");
         }
     }
     if (gs::timing_on()) gs::timing_stage_end(stream, BINNING_STAGE);

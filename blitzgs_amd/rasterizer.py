@@ -73,9 +73,11 @@ def preprocess_gaussians(means3D, scales, rotations, sh, opacities, raster_setti
     return _PreprocessGaussians.apply(means3D, scales, rotations, sh, opacities, raster_settings, cuda_args)
 
 
-def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs):
+def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_cov3D=True):
     """Direct call of the C ABI; returns the reference's 8-tuple
-    (num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped)."""
+    (num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped).
+    keep_cov3D False: cov3D is None (not written; the backward recomputes it
+    from scales and rotations)."""
     if means3D.ndimension() != 2 or means3D.size(1) != 3:
         raise RuntimeError("means3D must have dimensions (num_points, 3)")
     _require_device(means3D, "means3D")
@@ -87,7 +89,7 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs):
     means2D = torch.empty((P, 2), **f32)
     depths = torch.empty((P,), **f32)
     radii = torch.empty((P,), device=dev, dtype=torch.int32)
-    cov3D = torch.empty((P, 6), **f32)
+    cov3D = torch.empty((P, 6), **f32) if keep_cov3D else None
     conic_opacity = torch.empty((P, 4), **f32)
     rgb = torch.empty((P, 3), **f32)
     clamped = torch.empty((P, 3), device=dev, dtype=torch.bool)
@@ -106,7 +108,8 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs):
         rc = lib.gs_preprocess_forward(
             P, int(rs.sh_degree), sh.size(1), ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), ptr(opacities),
             float(rs.scale_modifier), ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy),
-            int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii), ptr(cov3D),
+            int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii),
+            ptr(cov3D) if cov3D is not None else None,
             ptr(conic_opacity), ptr(rgb), ptr(clamped), _stream(dev))
         check(rc, "gs_preprocess_forward")
         _lib.debug_sync(getattr(rs, "debug", False), "gs_preprocess_forward")
@@ -139,7 +142,8 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
         rc = lib.gs_preprocess_backward(
             P, int(rs.sh_degree), K, ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), float(rs.scale_modifier),
             ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height),
-            int(rs.image_width), ptr(radii.contiguous()), ptr(cov3D.contiguous()), ptr(clamped.contiguous()),
+            int(rs.image_width), ptr(radii.contiguous()), ptr(cov3D.contiguous()) if cov3D is not None else None,
+            ptr(clamped.contiguous()),
             ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
             ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
         check(rc, "gs_preprocess_backward")
@@ -150,8 +154,9 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
 class _PreprocessGaussians(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
+        # cov3D is internal to the pair: the backward recomputes it
         num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = _preprocess_forward_raw(
-            means3D, scales, rotations, sh, opacities, raster_settings)
+            means3D, scales, rotations, sh, opacities, raster_settings, keep_cov3D=False)
         # radii and depths take no gradient; unused outputs are not zero-filled
         ctx.set_materialize_grads(False)
         ctx.raster_settings = raster_settings

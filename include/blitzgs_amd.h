@@ -57,7 +57,8 @@ const char* gs_last_error(void);
  *   sh (P,K,3), opacities (P,1).  viewmatrix/projmatrix (4,4) and campos (3)
  *   are device tensors laid out as the reference's settings tensors.
  *   Outputs: means2D (P,2), depths (P), radii int32 (P), cov3D (P,6),
- *   conic_opacity (P,4), rgb (P,3), clamped uint8 (P,3).
+ *   conic_opacity (P,4), rgb (P,3), clamped uint8 (P,3).  cov3D may be
+ *   NULL (not written; gs_preprocess_backward then recomputes it).
  *   rotations and conic_opacity must be 16-byte aligned.
  * ------------------------------------------------------------------------ */
 int gs_preprocess_forward(int P, int D, int K, const float* means3D, const float* scales,
@@ -72,6 +73,8 @@ int gs_preprocess_forward(int P, int D, int K, const float* means3D, const float
  * cuda_rasterizer/backward.cu:146-276 and 348-400).
  *   dL_dmeans2D has row stride dL_dmeans2D_stride floats (2, or 3 for the
  *   reference's padded (P,3) layout); dL_dconic_opacity (P,4); dL_drgb (P,3).
+ *   cov3D: the forward's output, or NULL to recompute it from scales and
+ *   rotations (the same arithmetic as the forward's).
  *   Outputs: dL_dmeans3D (P,3), dL_dscales (P,3), dL_drotations (P,4),
  *   dL_dsh (P,K,3), dL_dopacity (P,1) = dL_dconic_opacity[:,3]. */
 int gs_preprocess_backward(int P, int D, int K, const float* means3D, const float* scales,

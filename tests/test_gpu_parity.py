@@ -220,6 +220,48 @@ def _grad_chain(scene, cam, bg, dLd):
     return pre, bn, rf, rb, pb
 
 
+def test_preprocess_backward_recomputed_cov3D_and_row_layouts():
+    """The preprocess backward without the forward's cov3D (recomputed from
+    scales and rotations by the forward's own code) equals the one with it,
+    bit for bit, also through the C ABI with dL/dmeans3D and dL/dscales at
+    4-byte (not 16-byte) aligned addresses and a partial last block
+    (P = 3000)."""
+    import ctypes as C
+    from blitzgs_amd import rasterizer as R
+    scene, cam = synth.small_scene(3000, seed=31, W=200, H=150, extent=1.2)
+    rs = settings_for(cam)
+    g = gpu_preprocess(scene, rs)
+    P = scene["means3D"].shape[0]
+    rng = np.random.default_rng(5)
+    dm2 = to_dev(rng.standard_normal((P, 2)).astype(np.float32))
+    dco = to_dev(rng.standard_normal((P, 4)).astype(np.float32))
+    drgb = to_dev(rng.standard_normal((P, 3)).astype(np.float32))
+    t = {k: to_dev(np.asarray(scene[k], np.float32)) for k in ["means3D", "scales", "rotations", "sh"]}
+    args = (t["means3D"], t["scales"], t["rotations"], t["sh"], rs, dm2, dco, drgb)
+    with_cov = R._preprocess_backward_raw(g["radii"], g["cov3D"], g["clamped"], *args)
+    without = R._preprocess_backward_raw(g["radii"], None, g["clamped"], *args)
+    for a, b, name in zip(with_cov, without, ["means3D", "scales", "rotations", "sh", "opacity"]):
+        assert torch.equal(a, b), name
+    assert (np_(g["radii"]) > 0).sum() > 500
+    # misaligned dL/dmeans3D and dL/dscales
+    lib = _lib.load()
+    buf_m, buf_s = torch.empty(3 * P + 1, device="cuda"), torch.empty(3 * P + 1, device="cuda")
+    dmean, dscale = buf_m[1:], buf_s[1:]
+    drot = torch.empty((P, 4), device="cuda")
+    dsh = torch.empty((P, 16, 3), device="cuda")
+    dop = torch.empty((P, 1), device="cuda")
+    p_ = _lib.ptr
+    _lib.check(lib.gs_preprocess_backward(
+        P, 3, 16, p_(t["means3D"]), p_(t["scales"]), p_(t["rotations"]), p_(t["sh"]), 1.0,
+        p_(rs.viewmatrix.contiguous()), p_(rs.projmatrix.contiguous()), p_(rs.campos.contiguous()), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height),
+        int(rs.image_width), p_(g["radii"]), None, p_(g["clamped"]), p_(dm2), 2, p_(dco), p_(drgb), p_(dmean),
+        p_(dscale), p_(drot), p_(dsh), p_(dop), _lib.stream_of()), "preprocess_backward")
+    torch.cuda.synchronize()
+    assert torch.equal(dmean.view(P, 3), with_cov[0])
+    assert torch.equal(dscale.view(P, 3), with_cov[1])
+    assert torch.equal(drot, with_cov[2]) and torch.equal(dsh, with_cov[3]) and torch.equal(dop, with_cov[4])
+
+
 @pytest.mark.parametrize("cfg", ["small", "config0"])
 def test_autograd_forward_backward_vs_oracle(cfg):
     from blitzgs_amd import rasterizer as R

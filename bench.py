@@ -43,22 +43,32 @@ STEP_METRIC = "rasterizer fwd+bwd ms/iter & Gaussians/s at 6M SH3 1600x1066; % H
 
 # algorithmic bytes per unit of work, per stage (the scope table's per-unit figures)
 def stage_bytes(P, P_vis, R, npx):
+    """Algorithmic HBM bytes per launch (per step for binning and other): P
+    Gaussians, P_vis of them visible (radius > 0; the listed ones, which touch
+    a tile, are counted as P_vis), R tile instances, npx pixels."""
     return {
-        "preprocess_fwd_kernel": 115 * P + 192 * P_vis,
-        "preprocess_bwd_kernel": 240 * P + 295 * P_vis,
-        "binning": 16 * P + 44 * R,
+        # reads means3D, scales, rotations, opacity (44 B) of all, SH (192 B) of the visible; writes means2D,
+        # depth, radius, conic+opacity, rgb, clamped (47 B) of all (cov3D is recomputed by the backward)
+        "preprocess_fwd_kernel": 91 * P + 192 * P_vis,
+        # writes the five gradients (236 B) and reads radius (4 B) of all; reads means3D, scales, rotations,
+        # clamped, the three incoming gradients and SH (271 B) of the visible
+        "preprocess_bwd_kernel": 240 * P + 271 * P_vis,
+        # count: radius + means2D of all (12 B); scatter: the same again, compact index and out_observe (8 B)
+        # of all, depth/conic/rgb (32 B) of the listed, their 64-byte record and id (68 B); per instance the
+        # key written and read back (16 B) and the compact list written (4 B)
+        "binning": 32 * P + 100 * P_vis + 20 * R,
         "render_fwd_kernel": 40 * R + 24 * npx,
         "render_bwd_kernel": 40 * R + 32 * npx,
-        # out_observe clear (4P) and the gradient unpack (1P flag + 48 P_vis read + 48 P_vis clear + 48 P written)
-        "other": 4 * P + P + 96 * P_vis + 48 * P,
+        # the accumulators cleared (64 B per listed), then the gradient unpack: compact index of all (4 B),
+        # accumulators of the listed (48 B), four gradient rows of all written (48 B)
+        "other": 64 * P_vis + 4 * P + 48 * P_vis + 48 * P,
     }
 
 
 BINNING_KERNELS = ("localmap_kernel", "count_kernel", "tilescan_kernel", "ranges_kernel", "scatter_kernel",
-                   "tilesort_kernel_512", "tilesort_kernel_1k", "tilesort_kernel_2k", "tilesort_kernel_4k",
-                   "tilesort_kernel_8k", "tilesort_big_kernel")
+                   "tilesort_kernel_1k", "tilesort_kernel_2k", "tilesort_kernel_4k", "tilesort_kernel_8k")
 # the library's stage mark around the whole binning on the caller's stream
-# (first binning kernel -> end of the sorts, R readback included)
+# (first binning kernel -> end of the sorts)
 BINNING_STAGE = "binning (wall)"
 STEP_STAGES = ("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel")
 
@@ -77,6 +87,10 @@ def parse():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the library's plain copy kernel on MIB MiB (5 launches): the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
+    ap.add_argument("--valu-probes", action="store_true",
+                    help="only run the blend kernels' VALU probes (gs_diag_math ops 7 and 8, one launch each at "
+                         "the iteration counts the bench times them at): the launches whose SQ_INSTS_VALU "
+                         "profiles/valu_probes.json records, then exit")
     return ap.parse_args()
 
 
@@ -174,20 +188,62 @@ def valu_peak(iters=2000, reps=5):
     return 8192 * 4 * 32 * iters / (best * 1e-3) / 1e9
 
 
+# the blend kernels' VALU probes: gs_diag_math op, kernel name, iterations
+VALU_PROBES = {"render_fwd_kernel": (7, "valu_probe_fwd_kernel", 24),
+               "render_bwd_kernel": (8, "valu_probe_bwd_kernel", 8)}
+
+
+def run_valu_probe(op, iters, reps=5):
+    """Best-of-`reps` time (ms) of one VALU probe launch."""
+    import torch
+    from blitzgs_amd import _lib
+    lib = _lib.load()
+    y = torch.zeros(1, device="cuda:0")
+    stream = _lib.stream_of(y.device)
+    _lib.check(lib.gs_diag_math(op, 1, None, _lib.ptr(y), stream), "gs_diag_math probe")
+    best = float("inf")
+    for _ in range(reps):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        _lib.check(lib.gs_diag_math(op, iters, None, _lib.ptr(y), stream), "gs_diag_math probe")
+        ev1.record()
+        torch.cuda.synchronize()
+        best = min(best, ev0.elapsed_time(ev1))
+    return best
+
+
+def valu_probes_only():
+    for name, (op, pname, iters) in VALU_PROBES.items():
+        ms = run_valu_probe(op, iters, reps=1)
+        log(f"[bench] {pname}: {iters} iterations, {ms:.3f} ms")
+
+
 def valu_of(name, avg_ms, config):
     """VALU issue rate of kernel `name` per launch: SQ_INSTS_VALU per launch
     (profiles/valu_config<N>.json, rocprofv3 --pmc) over its live launch time,
-    against the measured FMA issue rate."""
+    against the ceiling for its instruction mix: the issue rate of its VALU
+    probe (the same per-entry arithmetic with no memory traffic; instructions
+    per probe launch in profiles/valu_probes.json, the probe timed live)."""
     f = os.path.join(ROOT, "profiles", f"valu_config{config}.json")
     try:
         insts = json.load(open(f))[name]["SQ_INSTS_VALU"]
     except (OSError, ValueError, KeyError):
         return None
-    peak = valu_peak()
     achieved = insts / (avg_ms * 1e-3) / 1e9
-    return {"unit": "G wave-instructions/s", "insts_per_launch": int(insts), "achieved": round(achieved, 1),
-            "peak": round(peak, 1), "frac": round(achieved / peak, 4),
-            "peak_is": "measured fp32 FMA issue rate (gs_diag_math op 5)"}
+    out = {"unit": "G wave-instructions/s", "insts_per_launch": int(insts), "achieved": round(achieved, 1),
+           "fma_rate": round(valu_peak(), 1)}
+    if name in VALU_PROBES:
+        op, pname, iters = VALU_PROBES[name]
+        try:
+            pj = json.load(open(os.path.join(ROOT, "profiles", "valu_probes.json")))[pname]
+            assert int(pj["iters"]) == iters
+            peak = pj["SQ_INSTS_VALU"] / (run_valu_probe(op, iters) * 1e-3) / 1e9
+            out.update(peak=round(peak, 1), frac=round(achieved / peak, 4),
+                       peak_is=f"measured VALU issue rate of the kernel's own per-entry arithmetic "
+                               f"({pname}, gs_diag_math op {op}: no memory traffic, {iters} x 64 entries per wave)")
+        except (OSError, ValueError, KeyError, AssertionError):
+            pass
+    return out
 
 
 def roofline_of(name, alg_bytes, avg_ms, traffic=None):
@@ -290,13 +346,17 @@ def run_step(args):
             traffic = None
     roofline = roofline_of(dom, sb[dom], avg_launch.get(dom, float("nan")), traffic)
     if dom == "binning":
-        roofline["note"] = ("binning = tile count, scan, R readback, duplication and the per-tile LDS radix sort, "
-                            "timed as one stage on the caller's stream (wall clock, host round trip included)")
-    else:
-        roofline["note"] = ("HBM roofline of the kernel (algorithmic bytes / launch time); the blend kernels' limiter "
-                            "is VALU issue, not HBM: `valu` compares their VALU instruction issue rate with the "
-                            "measured ceiling")
+        roofline["note"] = ("binning = tile count, scan, duplication and the per-tile sorts, timed as one stage on "
+                            "the caller's stream (wall clock from the first binning kernel to the end of the sorts; "
+                            "the forward is queued in one call, so no host round trip falls inside)")
+    elif dom in VALU_PROBES:
+        roofline["limiter"] = "valu"
+        roofline["note"] = ("`bound` and `frac` are the HBM roofline (algorithmic bytes / launch time) the line format "
+                            "asks for; this blend kernel is limited by VALU issue, not HBM: `valu.frac` is its VALU "
+                            "instruction rate over that of its own per-entry arithmetic run with no memory traffic")
         roofline["valu"] = valu_of(dom, avg_launch.get(dom, float("nan")), args.config)
+    else:
+        roofline["note"] = "HBM roofline of the kernel (algorithmic bytes / launch time)"
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -778,6 +838,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.valu_probes:
+        valu_probes_only()
         return
     import torch
     from blitzgs_amd import _lib

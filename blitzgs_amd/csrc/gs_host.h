@@ -20,6 +20,8 @@ void timing_mark_end(hipStream_t stream);
 // its time runs from the begin mark to the end mark of the same name.
 void timing_stage_begin(hipStream_t stream, const char* name);
 void timing_stage_end(hipStream_t stream, const char* name);
+// The blend kernels' VALU probes (render.hip): which 0 forward, 1 backward.
+int render_valu_probe(int which, int iters, float* y, hipStream_t stream);
 }  // namespace gs
 
 #define GS_TIMED(name, stream, launch)                                                 \

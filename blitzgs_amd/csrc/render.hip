@@ -1170,6 +1170,45 @@ struct Stage {
     float4 c[64];   // blue, tag bits, position in the tile's list (bits), alpha cut-off power
 };
 
+// Per-pixel state of the forward blend, and the blend of one staged entry
+// (A, B, Cc as staged by stage_put) into it.  Branch-free: every lane
+// evaluates the entry and the state changes are selects.  Shared by the
+// forward kernels and the VALU probe (render_valu_probe), which therefore
+// issue the same instructions per entry.
+struct FwdPixel {
+    float T, C0, C1, C2;
+    uint32_t last, n2l;
+    bool done;
+};
+
+struct FwdStep {
+    bool upd, observe;
+    float wgt;
+};
+
+__device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, const float4& B, const float4& Cc,
+                                                  float pxf, float pyf)
+{
+    const float dx = A.x - pxf, dy = A.y - pyf;
+    const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
+    float G;
+    const float alpha = gs::blend_alpha(B.y, power, Cc.w, G);
+    const float test_T = p.T * (1.0f - alpha);
+    const bool use = !p.done && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+    const bool fin = use && test_T < 0.0001f;
+    const bool upd = use && !fin;
+    const bool observe = upd && p.T > 0.5f;
+    const float wgt = alpha * p.T;
+    p.C0 = upd ? __builtin_fmaf(B.z, wgt, p.C0) : p.C0;
+    p.C1 = upd ? __builtin_fmaf(B.w, wgt, p.C1) : p.C1;
+    p.C2 = upd ? __builtin_fmaf(Cc.x, wgt, p.C2) : p.C2;
+    p.T = upd ? test_T : p.T;
+    p.n2l += upd ? 1u : 0u;
+    p.last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : p.last;
+    p.done = p.done || fin;
+    return FwdStep{upd, observe, wgt};
+}
+
 // stages entry k of the list; `tag` (Gaussian id in the forward, compact
 // index in the backward) rides along in the blue slot's partner
 __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uint32_t tag, int k)
@@ -1230,12 +1269,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     const uint32_t* list = clist + range.x;
     const float pxf = (float)px, pyf = (float)py;
     const float qx0 = (float)qx, qy0 = (float)qy;
-    const float alpha_min = 1.0f / 255.0f;
-    float T_ = 1.0f, C0 = 0.f, C1 = 0.f, C2 = 0.f;
-    uint32_t last = 0, n2l = 0;
+    FwdPixel px_st{1.0f, 0.f, 0.f, 0.f, 0u, 0u, !inside};
     float wmax = 0.f;      // largest blend weight so far, and its Gaussian (full / simp)
     uint32_t imax = 0u;
-    bool done = !inside;
 
     // software pipeline: while a batch blends, the next batch's records and
     // the list entries of the batch after it are in flight
@@ -1245,7 +1281,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     if (lane < n) r_cur = load_rec<true>(rec, id_cur);
 
     for (int base = 0; base < n; base += 64) {
-        if (gs::ballot(!done) == 0) break;
+        if (gs::ballot(!px_st.done) == 0) break;
         const int k = base + lane;
         Rec r_nxt{};
         uint32_t id_nn = 0;
@@ -1259,27 +1295,13 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         const int cnt = (int)__builtin_popcountll(km);
         // T only decreases, so a batch that starts with no live pixel above
         // T = 0.5 cannot observe (split path): its entries skip the ballot
-        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(!done && T_ > 0.5f) != 0;
+        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(!px_st.done && px_st.T > 0.5f) != 0;
         // Branch-free blend of one staged entry: every lane evaluates it and
         // the state changes are selects, so no exec-mask bookkeeping.
         auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
-            const float dx = A.x - pxf, dy = A.y - pyf;
-            const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-            float G;
-            const float alpha = gs::blend_alpha(B.y, power, Cc.w, G);
-            const float test_T = T_ * (1.0f - alpha);
-            const bool use = !done && !(power > 0.0f) && !(alpha < alpha_min);
-            const bool fin = use && test_T < 0.0001f;
-            const bool upd = use && !fin;
-            const bool observe = upd && T_ > 0.5f;
-            const float wgt = alpha * T_;
-            C0 = upd ? __builtin_fmaf(B.z, wgt, C0) : C0;
-            C1 = upd ? __builtin_fmaf(B.w, wgt, C1) : C1;
-            C2 = upd ? __builtin_fmaf(Cc.x, wgt, C2) : C2;
-            T_ = upd ? test_T : T_;
-            n2l += upd ? 1u : 0u;
-            last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : last;
-            done = done || fin;
+            const FwdStep f = fwd_blend_step(px_st, A, B, Cc, pxf, pyf);
+            const bool upd = f.upd, observe = f.observe;
+            const float wgt = f.wgt;
             if (MODE == BLEND_SPLIT) {
                 if (!obs_batch) return;
                 const uint64_t m = gs::ballot(observe);
@@ -1308,10 +1330,10 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
         float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
         float4 A1, B1, D1;
         for (int j = 0; j < cnt; j += 2) {
-            if (gs::ballot(!done) == 0) break;
+            if (gs::ballot(!px_st.done) == 0) break;
             A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
             blend(A0, B0, D0);
-            if (j + 1 >= cnt || gs::ballot(!done) == 0) break;
+            if (j + 1 >= cnt || gs::ballot(!px_st.done) == 0) break;
             A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
             blend(A1, B1, D1);
         }
@@ -1322,21 +1344,21 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(
     }
 
     if (inside) {
-        O.final_T[pid] = T_;
-        O.n_contrib_px[pid] = last;
-        if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = n2l;
-        out_color[pid] = __builtin_fmaf(T_, bg[0], C0);
-        out_color[HW + pid] = __builtin_fmaf(T_, bg[1], C1);
-        out_color[2 * HW + pid] = __builtin_fmaf(T_, bg[2], C2);
+        O.final_T[pid] = px_st.T;
+        O.n_contrib_px[pid] = px_st.last;
+        if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = px_st.n2l;
+        out_color[pid] = __builtin_fmaf(px_st.T, bg[0], px_st.C0);
+        out_color[HW + pid] = __builtin_fmaf(px_st.T, bg[1], px_st.C1);
+        out_color[2 * HW + pid] = __builtin_fmaf(px_st.T, bg[2], px_st.C2);
     }
     if (MODE == BLEND_SPLIT) {
-        const int s_last = gs::wave_sum_i(inside ? (int)last : 0);
-        const int s_n2l = gs::wave_sum_i(inside ? (int)n2l : 0);
+        const int s_last = gs::wave_sum_i(inside ? (int)px_st.last : 0);
+        const int s_n2l = gs::wave_sum_i(inside ? (int)px_st.n2l : 0);
         if (lane == 0) {
             if (s_last) atomicAdd(&O.n_consider[tile], s_last);
             if (s_n2l) atomicAdd(&O.n_contrib_tile[tile], s_n2l);
         }
-    } else if (O.accum_max_count != nullptr && inside && last > 0) {
+    } else if (O.accum_max_count != nullptr && inside && px_st.last > 0) {
         atomicAdd(&O.accum_max_count[imax], 1.0f);
     }
 }
@@ -1647,6 +1669,76 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
     gs::st_stream(&g_col[3 * (size_t)i + 2], c.z);
 }
 
+// Per-pixel state and constants of the backward blend, and the backward of
+// one staged entry for one pixel: updates the state and returns whether the
+// pixel blends the entry, with its eleven gradient terms in vals (dmean x, y,
+// |dmean x|, |dmean y|, dconic a, b, c, dopacity, drgb; vals[11] = 0).
+// Shared by the backward kernels and the VALU probe (render_valu_probe).
+struct BwdPixel {
+    float T, acc0, acc1, acc2, lc0, lc1, lc2, last_alpha;
+};
+
+struct BwdConst {
+    float pxf, pyf, dp0, dp1, dp2, nT_bg, ddelx_dx, ddely_dy;
+    int last;
+};
+
+template <bool FULL>
+__device__ __forceinline__ bool bwd_blend_step(BwdPixel& p, const BwdConst& k, const float4& A, const float4& B,
+                                               const float4& Cc, float (&vals)[12])
+{
+    const int ci = __float_as_int(Cc.z);   // position in the tile's list
+    // Branch-free: every lane evaluates the entry; a lane whose pixel
+    // does not blend it (past its last contributor, power > 0, alpha <
+    // 1/255) gets zero gradient factors and unchanged state, through
+    // selects on three factors instead of per-value zeroing.
+    const float dx = A.x - k.pxf, dy = A.y - k.pyf;
+    const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
+    float G0;
+    const float alpha = gs::blend_alpha(B.y, power, Cc.w, G0);
+    const bool valid = ci < k.last && !(power > 0.0f) && !(alpha < (1.0f / 255.0f));
+    const float G = valid ? G0 : 0.f;
+    const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
+    p.T = p.T * inv_one_m;
+    const float dchannel_dcolor = valid ? alpha * p.T : 0.f;
+    // the reference's expressions, regrouped into fused multiply-adds
+    // (gradients carry a tolerance, not bit-exactness):
+    //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
+    //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
+    //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms);
+    // a lane that does not blend the entry updates acc with factor 0
+    const float la = valid ? p.last_alpha : 0.f;
+    p.acc0 = __builtin_fmaf(la, p.lc0 - p.acc0, p.acc0);
+    p.acc1 = __builtin_fmaf(la, p.lc1 - p.acc1, p.acc1);
+    p.acc2 = __builtin_fmaf(la, p.lc2 - p.acc2, p.acc2);
+    p.lc0 = valid ? B.z : p.lc0;
+    p.lc1 = valid ? B.w : p.lc1;
+    p.lc2 = valid ? Cc.x : p.lc2;
+    p.last_alpha = valid ? alpha : p.last_alpha;
+    float dL_dalpha = __builtin_fmaf(B.z - p.acc0, k.dp0, __builtin_fmaf(B.w - p.acc1, k.dp1, (Cc.x - p.acc2) * k.dp2));
+    const float gc0 = dchannel_dcolor * k.dp0;
+    const float gc1 = dchannel_dcolor * k.dp1;
+    const float gc2 = dchannel_dcolor * k.dp2;
+    dL_dalpha = valid ? __builtin_fmaf(dL_dalpha, p.T, inv_one_m * k.nT_bg) : 0.f;
+    const float dL_dG = B.y * dL_dalpha;
+    const float gdx = G * dx, gdy = G * dy;
+    const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
+    const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
+    const float gmx = (dL_dG * k.ddelx_dx) * dG_ddelx;
+    const float gmy = (dL_dG * k.ddely_dy) * dG_ddely;
+    const float h = -0.5f * dL_dG;
+    const float hgdx = h * gdx;
+    const bool clamped = FULL && B.y * G > 0.99f;
+    const float gca = clamped ? 0.f : hgdx * dx;
+    const float gcb = clamped ? 0.f : hgdx * dy;
+    const float gcc = clamped ? 0.f : (h * gdy) * dy;
+    const float gop = clamped ? 0.f : G * dL_dalpha;
+    vals[0] = gmx; vals[1] = gmy; vals[2] = __builtin_fabsf(gmx); vals[3] = __builtin_fabsf(gmy);
+    vals[4] = gca; vals[5] = gcb; vals[6] = gcc; vals[7] = gop;
+    vals[8] = gc0; vals[9] = gc1; vals[10] = gc2; vals[11] = 0.f;
+    return valid;
+}
+
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no
 // conic or opacity gradient from a pixel where opacity * G > 0.99 (the alpha
 // clamp is active); |dL/dmean2D| is accumulated but not written out.
@@ -1677,18 +1769,14 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     __shared__ Stage st;
 
     const uint32_t* list = clist + ranges[tile].x;
-    const float pxf = (float)px, pyf = (float)py;
     const float qx0 = (float)qx, qy0 = (float)qy;
-    const float alpha_min = 1.0f / 255.0f;
-    const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
     const float bg_dot = bg[0] * dp0 + bg[1] * dp1 + bg[2] * dp2;
-    const float nT_bg = -T_final * bg_dot;   // the background term of dL/dalpha, before 1/(1-alpha)
+    // nT_bg: the background term of dL/dalpha, before 1/(1-alpha)
+    const BwdConst kc{(float)px, (float)py, dp0, dp1, dp2, -T_final * bg_dot, 0.5f * (float)W, 0.5f * (float)H, last};
     // after the wave reduction this lane holds the total of gradient term
     // my_k (accumulator slot), or nothing (my_k < 0)
     const int my_k = gs::wave_sum12_index(lane);
-    float T_ = T_final;
-    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
-    float lc0 = 0.f, lc1 = 0.f, lc2 = 0.f, last_alpha = 0.f;
+    BwdPixel px_st{T_final, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
     // walk positions maxlast-1 .. 0 of the tile's list, back to front, with
     // the same software pipeline as the forward
@@ -1713,56 +1801,10 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             const float4 A = st.a[j];
             const float4 B = st.b[j];
             const float4 Cc = st.c[j];
-            const int ci = __float_as_int(Cc.z);   // position in the tile's list
-            // Branch-free: every lane evaluates the entry; a lane whose pixel
-            // does not blend it (past its last contributor, power > 0, alpha <
-            // 1/255) gets zero gradient factors and unchanged state, through
-            // selects on three factors instead of per-value zeroing.
-            const float dx = A.x - pxf, dy = A.y - pyf;
-            const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-            float G0;
-            const float alpha = gs::blend_alpha(B.y, power, Cc.w, G0);
-            const bool valid = ci < last && !(power > 0.0f) && !(alpha < alpha_min);
-            const float G = valid ? G0 : 0.f;
-            const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
-            T_ = T_ * inv_one_m;
-            const float dchannel_dcolor = valid ? alpha * T_ : 0.f;
-            // the reference's expressions, regrouped into fused multiply-adds
-            // (gradients carry a tolerance, not bit-exactness):
-            //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
-            //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
-            //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms);
-            // a lane that does not blend the entry updates acc with factor 0
-            const float la = valid ? last_alpha : 0.f;
-            acc0 = __builtin_fmaf(la, lc0 - acc0, acc0);
-            acc1 = __builtin_fmaf(la, lc1 - acc1, acc1);
-            acc2 = __builtin_fmaf(la, lc2 - acc2, acc2);
-            lc0 = valid ? B.z : lc0;
-            lc1 = valid ? B.w : lc1;
-            lc2 = valid ? Cc.x : lc2;
-            last_alpha = valid ? alpha : last_alpha;
-            float dL_dalpha = __builtin_fmaf(B.z - acc0, dp0, __builtin_fmaf(B.w - acc1, dp1, (Cc.x - acc2) * dp2));
-            const float gc0 = dchannel_dcolor * dp0;
-            const float gc1 = dchannel_dcolor * dp1;
-            const float gc2 = dchannel_dcolor * dp2;
-            dL_dalpha = valid ? __builtin_fmaf(dL_dalpha, T_, inv_one_m * nT_bg) : 0.f;
-            const float dL_dG = B.y * dL_dalpha;
-            const float gdx = G * dx, gdy = G * dy;
-            const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
-            const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
-            const float gmx = (dL_dG * ddelx_dx) * dG_ddelx;
-            const float gmy = (dL_dG * ddely_dy) * dG_ddely;
-            const float h = -0.5f * dL_dG;
-            const float hgdx = h * gdx;
-            const bool clamped = FULL && B.y * G > 0.99f;
-            const float gca = clamped ? 0.f : hgdx * dx;
-            const float gcb = clamped ? 0.f : hgdx * dy;
-            const float gcc = clamped ? 0.f : (h * gdy) * dy;
-            const float gop = clamped ? 0.f : G * dL_dalpha;
+            float vals[12];
+            const bool valid = bwd_blend_step<FULL>(px_st, kc, A, B, Cc, vals);
             if (gs::ballot(valid) == 0) continue;
             const uint32_t cx = __float_as_uint(Cc.y);
-            const float vals[12] = {gmx, gmy, __builtin_fabsf(gmx), __builtin_fabsf(gmy), gca, gcb, gcc, gop,
-                                    gc0, gc1, gc2, 0.f};
             const float tot = gs::wave_sum12(vals);
             // the eleven totals of one Gaussian land in one 64-byte accumulator
             if (my_k >= 0 && my_k < 11 && tot != 0.f) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
@@ -1772,6 +1814,78 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
         id_cur = id_nxt;
         id_nxt = id_nn;
     }
+}
+
+// ---- VALU probes: the blend kernels' per-entry arithmetic (fwd_blend_step;
+// bwd_blend_step + wave_sum12), on 64 entries staged in LDS once, with no
+// global memory traffic, in the blend kernels' 64-thread blocks.  Their VALU
+// instruction rate is the ceiling the blend kernels' rate is compared with.
+constexpr int VALU_PROBE_BLOCKS = 16384;
+
+__device__ __forceinline__ void probe_stage(Stage& st, int lane)
+{
+    // entries centred on the quadrant's pixels, wide and faint enough that
+    // every pixel blends every entry
+    const float mx = (float)(lane & 7) + 0.25f, my = (float)(lane >> 3) + 0.5f;
+    const float a = 0.02f + 0.0005f * (float)lane, b = 0.002f, c = 0.03f - 0.0003f * (float)lane;
+    const float op = 0.02f + 0.0004f * (float)lane;
+    st.a[lane] = make_float4(mx, my, -0.5f * a, -b);
+    st.b[lane] = make_float4(-0.5f * c, op, 0.3f, 0.6f);
+    st.c[lane] = make_float4(0.9f, __uint_as_float((uint32_t)lane), __int_as_float(lane), gs::alpha_cut_power(op));
+}
+
+template <int WHICH>
+__global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __restrict__ y)
+{
+    __shared__ Stage st;
+    const int lane = threadIdx.x;
+    probe_stage(st, lane);
+    __syncthreads();
+    const float pxf = (float)(lane & 7), pyf = (float)(lane >> 3);
+    float out = 0.f;
+    if (WHICH == 0) {
+        // the forward: the two-register-set loop of render_fwd_kernel, with
+        // the observe ballot of its split mode (counted, not stored)
+        int observed = 0;
+        for (int it = 0; it < iters; it++) {
+            FwdPixel p{1.0f, 0.f, 0.f, 0.f, 0u, 0u, false};
+            auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
+                const FwdStep f = fwd_blend_step(p, A, B, Cc, pxf, pyf);
+                const uint64_t m = gs::ballot(f.observe);
+                if (m != 0) observed += (int)__builtin_popcountll(m);
+            };
+            float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
+            float4 A1, B1, D1;
+            for (int j = 0; j < 64; j += 2) {
+                if (gs::ballot(!p.done) == 0) break;
+                A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
+                blend(A0, B0, D0);
+                if (j + 1 >= 64 || gs::ballot(!p.done) == 0) break;
+                A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
+                blend(A1, B1, D1);
+            }
+            out += p.C0 + p.C1 + p.C2 + p.T + (float)(p.last + p.n2l);
+        }
+        out += (float)observed;
+    } else {
+        // the backward: render_bwd_kernel's entry loop, the accumulator
+        // atomics replaced by a sum
+        const int my_k = gs::wave_sum12_index(lane);
+        const BwdConst kc{pxf, pyf, 0.3f, -0.2f, 0.1f, -0.05f, 800.f, 533.f, 64};
+        for (int it = 0; it < iters; it++) {
+            BwdPixel p{0.2f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 64; j++) {
+                const float4 A = st.a[j], B = st.b[j], Cc = st.c[j];
+                float vals[12];
+                const bool valid = bwd_blend_step<false>(p, kc, A, B, Cc, vals);
+                if (gs::ballot(valid) == 0) continue;
+                const float tot = gs::wave_sum12(vals);
+                if (my_k >= 0 && my_k < 11 && tot != 0.f) out += tot;
+            }
+            out += p.T;
+        }
+    }
+    if (out == 12345.0f) y[0] = out;   // keeps the work; never true for these inputs in practice
 }
 
 }  // namespace
@@ -2326,3 +2440,23 @@ extern "C" int gs_render_full_backward(int P, int64_t R, int W, int H, const flo
     return render_backward_impl(true, P, R, W, H, bg, means2D, conic_opacity, nullptr, geom, binning, img, dL_dpixels,
                                 dL_dmeans2D, 3, nullptr, dL_dconic_opacity, dL_dcolors, stream);
 }
+
+namespace gs {
+// The VALU probes (which 0: forward, 1: backward) over `iters` passes of 64
+// entries per wave, VALU_PROBE_BLOCKS waves.
+int render_valu_probe(int which, int iters, float* y, hipStream_t stream)
+{
+    GS_REQUIRE(which == 0 || which == 1, "which must be 0 (forward) or 1 (backward)");
+    GS_REQUIRE(iters >= 0 && y != nullptr, "iters must be >= 0 and y non-null");
+    if (iters == 0) return GS_OK;
+    if (which == 0) {
+        GS_TIMED("valu_probe_fwd_kernel", stream,
+                 hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(VALU_PROBE_BLOCKS), dim3(64), 0, stream, iters, y));
+    } else {
+        GS_TIMED("valu_probe_bwd_kernel", stream,
+                 hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(VALU_PROBE_BLOCKS), dim3(64), 0, stream, iters, y));
+    }
+    GS_LAUNCH_CHECK("valu_probe_kernel");
+    return GS_OK;
+}
+}  // namespace gs

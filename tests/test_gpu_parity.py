@@ -385,14 +385,16 @@ def test_wave_sum12_lane_layout():
     np.testing.assert_array_equal(np_(y), x.astype(np.float64).sum(1).astype(np.float32))
 
 
-def test_valu_rate_probe_runs_and_writes_nothing():
-    # the VALU issue-rate reference bench.py times: it runs, and its sentinel
-    # store is never taken
+@pytest.mark.parametrize("op,iters", [(5, 20), (7, 2), (8, 1)])
+def test_valu_rate_probe_runs_and_writes_nothing(op, iters):
+    # the VALU issue-rate references bench.py times (the FMA chains, the
+    # forward and backward blend probes): they run, and their sentinel store
+    # is not taken
     y = torch.full((1,), -7.0, device="cuda")
-    _lib.check(_lib.load().gs_diag_math(5, 20, None, _lib.ptr(y), None), "diag valu")
+    _lib.check(_lib.load().gs_diag_math(op, iters, None, _lib.ptr(y), None), "diag valu")
     torch.cuda.synchronize()
     assert float(y.item()) == -7.0
-    assert _lib.load().gs_diag_math(5, 1, None, None, None) != 0
+    assert _lib.load().gs_diag_math(op, 1, None, None, None) != 0
 
 
 def _split_forward(scene, cam, bg):

@@ -360,7 +360,9 @@ __device__ __forceinline__ float wave_sum(float v) { return bcast63(wave_sum_to_
 //            two lanes (row_shl) so one register carries all twelve totals.
 // 34 VALU operations instead of 12 separate full-wave reductions.  Lane L
 // returns the total of value wave_sum12_index(L) (-1: nothing).  All lanes
-// must be active.
+// must be active.  ABS23: values 2 and 3 are summed as absolute values (the
+// first level adds |a| + |b|, which costs nothing: source modifiers).
+template <bool ABS23 = false>
 __device__ __forceinline__ float wave_sum12(const float (&v)[12])
 {
     float s[6];
@@ -368,7 +370,8 @@ __device__ __forceinline__ float wave_sum12(const float (&v)[12])
     for (int i = 0; i < 6; i++) {
         const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * i]), __float_as_uint(v[2 * i + 1]),
                                                         false, false);
-        s[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+        s[i] = (ABS23 && i == 1) ? __builtin_fabsf(a) + __builtin_fabsf(b) : a + b;
     }
     float t[3];
 #pragma unroll

@@ -1199,9 +1199,11 @@ __device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, 
     const bool upd = use && !fin;
     const bool observe = upd && p.T > 0.5f;
     const float wgt = alpha * p.T;
-    p.C0 = upd ? __builtin_fmaf(B.z, wgt, p.C0) : p.C0;
-    p.C1 = upd ? __builtin_fmaf(B.w, wgt, p.C1) : p.C1;
-    p.C2 = upd ? __builtin_fmaf(Cc.x, wgt, p.C2) : p.C2;
+    // a pixel that does not take the entry adds colour * 0 (exactly its colour)
+    const float w = upd ? wgt : 0.f;
+    p.C0 = __builtin_fmaf(B.z, w, p.C0);
+    p.C1 = __builtin_fmaf(B.w, w, p.C1);
+    p.C2 = __builtin_fmaf(Cc.x, w, p.C2);
     p.T = upd ? test_T : p.T;
     p.n2l += upd ? 1u : 0u;
     p.last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : p.last;
@@ -1623,14 +1625,16 @@ __device__ __forceinline__ void emit_rows(float* __restrict__ S, int lane, int k
 }
 
 // Writes the render backward's outputs for every Gaussian from its
-// accumulator (listed Gaussians) or zeros, one Gaussian per thread.  A wave
-// whose 64 Gaussians are all in range writes its rows through emit_rows when
-// the outputs are 16-byte aligned (vec); otherwise element by element.
+// accumulator (listed Gaussians) or zeros, one Gaussian per thread, applying
+// the factors the blend leaves to the sums: dmean/dpixel (sx = W/2, sy = H/2)
+// to the mean terms, -1/2 to the conic terms.  A wave whose 64 Gaussians are
+// all in range writes its rows through emit_rows when the outputs are 16-byte
+// aligned (vec); otherwise element by element.
 __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __restrict__ cidx_of,
                                                            const float4* __restrict__ gacc, int m2d_stride,
                                                            float* __restrict__ g_m2d, float* __restrict__ g_m2d_abs,
                                                            float4* __restrict__ g_con, float* __restrict__ g_col,
-                                                           bool vec)
+                                                           bool vec, float sx, float sy)
 {
     __shared__ __align__(16) float stage[4][64 * 3];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -1646,6 +1650,8 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
         if (cx >= 0) {
             const float4* g = gacc + 4 * (size_t)cx;
             a = g[0]; b = g[1]; c = g[2];
+            a = make_float4(a.x * sx, a.y * sy, a.z * sx, a.w * sy);
+            b = make_float4(-0.5f * b.x, -0.5f * b.y, -0.5f * b.z, b.w);
         }
     }
     if (in) gs::st_stream(&g_con[i], b);
@@ -1681,7 +1687,7 @@ struct BwdPixel {
 };
 
 struct BwdConst {
-    float pxf, pyf, dp0, dp1, dp2, nT_bg, ddelx_dx, ddely_dy;
+    float pxf, pyf, dp0, dp1, dp2, nT_bg;
     int last;
 };
 
@@ -1726,16 +1732,18 @@ __device__ __forceinline__ bool bwd_blend_step(BwdPixel& p, const BwdConst& k, c
     const float gdx = G * dx, gdy = G * dy;
     const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
     const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
-    const float gmx = (dL_dG * k.ddelx_dx) * dG_ddelx;
-    const float gmy = (dL_dG * k.ddely_dy) * dG_ddely;
-    const float h = -0.5f * dL_dG;
-    const float hgdx = h * gdx;
+    // the constant factors dmean/dpixel (W/2, H/2) and the conic terms' -1/2
+    // are applied once to the sums (unpack_grads_kernel), not per entry
+    const float gmx = dL_dG * dG_ddelx;
+    const float gmy = dL_dG * dG_ddely;
+    const float hgdx = dL_dG * gdx;
     const bool clamped = FULL && B.y * G > 0.99f;
     const float gca = clamped ? 0.f : hgdx * dx;
     const float gcb = clamped ? 0.f : hgdx * dy;
-    const float gcc = clamped ? 0.f : (h * gdy) * dy;
+    const float gcc = clamped ? 0.f : (dL_dG * gdy) * dy;
     const float gop = clamped ? 0.f : G * dL_dalpha;
-    vals[0] = gmx; vals[1] = gmy; vals[2] = __builtin_fabsf(gmx); vals[3] = __builtin_fabsf(gmy);
+    // vals[2], vals[3]: |dmean| terms, made absolute by wave_sum12<true>
+    vals[0] = gmx; vals[1] = gmy; vals[2] = gmx; vals[3] = gmy;
     vals[4] = gca; vals[5] = gcb; vals[6] = gcc; vals[7] = gop;
     vals[8] = gc0; vals[9] = gc1; vals[10] = gc2; vals[11] = 0.f;
     return valid;
@@ -1774,7 +1782,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     const float qx0 = (float)qx, qy0 = (float)qy;
     const float bg_dot = bg[0] * dp0 + bg[1] * dp1 + bg[2] * dp2;
     // nT_bg: the background term of dL/dalpha, before 1/(1-alpha)
-    const BwdConst kc{(float)px, (float)py, dp0, dp1, dp2, -T_final * bg_dot, 0.5f * (float)W, 0.5f * (float)H, last};
+    const BwdConst kc{(float)px, (float)py, dp0, dp1, dp2, -T_final * bg_dot, last};
     // after the wave reduction this lane holds the total of gradient term
     // my_k (accumulator slot), or nothing (my_k < 0)
     const int my_k = gs::wave_sum12_index(lane);
@@ -1807,7 +1815,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             const bool valid = bwd_blend_step<FULL>(px_st, kc, A, B, Cc, vals);
             if (gs::ballot(valid) == 0) continue;
             const uint32_t cx = __float_as_uint(Cc.y);
-            const float tot = gs::wave_sum12(vals);
+            const float tot = gs::wave_sum12<true>(vals);
             // the eleven totals of one Gaussian land in one 64-byte accumulator
             if (my_k >= 0 && my_k < 11 && tot != 0.f) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
         }
@@ -1873,7 +1881,7 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
         // the backward: render_bwd_kernel's entry loop, the accumulator
         // atomics replaced by a sum
         const int my_k = gs::wave_sum12_index(lane);
-        const BwdConst kc{pxf, pyf, 0.3f, -0.2f, 0.1f, -0.05f, 800.f, 533.f, 64};
+        const BwdConst kc{pxf, pyf, 0.3f, -0.2f, 0.1f, -0.05f, 64};
         for (int it = 0; it < iters; it++) {
             BwdPixel p{0.2f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             for (int j = 0; j < 64; j++) {
@@ -1881,7 +1889,7 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
                 float vals[12];
                 const bool valid = bwd_blend_step<false>(p, kc, A, B, Cc, vals);
                 if (gs::ballot(valid) == 0) continue;
-                const float tot = gs::wave_sum12(vals);
+                const float tot = gs::wave_sum12<true>(vals);
                 if (my_k >= 0 && my_k < 11 && tot != 0.f) out += tot;
             }
             out += p.T;
@@ -2254,7 +2262,8 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                                 R > 0 ? at<const int>(geom, g.cidx_of) : nullptr, gacc, dL_dmeans2D_stride,
                                 dL_dmeans2D, dL_dmeans2D_abs, reinterpret_cast<float4*>(dL_dconic_opacity),
                                 dL_dcolors,
-                                (((uintptr_t)dL_dmeans2D | (uintptr_t)dL_dmeans2D_abs | (uintptr_t)dL_dcolors) & 15) == 0));
+                                (((uintptr_t)dL_dmeans2D | (uintptr_t)dL_dmeans2D_abs | (uintptr_t)dL_dcolors) & 15) == 0,
+                                0.5f * (float)W, 0.5f * (float)H));
     GS_LAUNCH_CHECK("unpack_grads_kernel");
     return GS_OK;
 }

@@ -65,7 +65,11 @@ def stage_bytes(P, P_vis, R, npx):
     }
 
 
-BINNING_KERNELS = ("localmap_kernel", "count_kernel", "tilescan_kernel", "ranges_kernel", "scatter_kernel",
+BINNING_KERNELS = ("localmap_kernel", "count_regions_kernel", "scan_regions_kernel", "ranges_kernel",
+                   "scatter_regions_kernel", "regionsort_kernel_1k", "regionsort_kernel_2k", "regionsort_kernel_4k",
+                   "regionsort_kernel_8k", "regionsort_kernel_12k", "regionsort_big_kernel",
+                   # the full-image path's per-tile binning
+                   "count_kernel", "tilescan_kernel", "scatter_kernel",
                    "tilesort_kernel_1k", "tilesort_kernel_2k", "tilesort_kernel_4k", "tilesort_kernel_8k")
 # the library's stage mark around the whole binning on the caller's stream
 # (first binning kernel -> end of the sorts)

@@ -66,6 +66,14 @@ constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
 constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
+// Regions of the split path: RS x RS-tile blocks (RS = 4, or 8 for very
+// large tile grids) tiling the local-tile box from its corner.
+constexpr int REGION_SIDE = 2;       // preferred region side (tiles)
+constexpr int MAX_REGIONS = 16384;   // regions of the full tile grid
+constexpr int LDS_REGIONS = 4096;    // region counters / cursors held in LDS by the count and the scatter
+constexpr int LDS_GRID = 12288;      // entries of the tile-count difference grid held in LDS
+constexpr int REGION_CLASSES = 5;    // region list size classes: <= 1k, 2k, 4k, 8k entries, larger
+constexpr int REGION_CAP = 8192;     // longest region list sorted on chip in one piece
 constexpr const char* BINNING_STAGE = "binning (wall)";   // per-kernel timing: the whole binning stage
 // Listed Gaussians (non-empty tile rect) are numbered densely, in Gaussian id
 // order ("compact index").  Per listed Gaussian the scatter writes a blend
@@ -84,16 +92,36 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct GeomLayout {
     int T, NC, CH, WS;
+    int RS, NR, G;                // region side (0: grid too large), regions and difference-grid entries of the full grid
     size_t cls_count, cls_list;   // per size class: number of local tiles, their local indices (T per class)
-    size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, wcount, cidx_of, cid2id, rec, gacc,
-        total;
+    size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, wcount, cidx_of, cid2id, rec, gacc;
+    // split path: per-region local-tile masks, list lengths, offsets and
+    // cursors, per-chunk region bases, per-class region lists and the
+    // per-tile count difference grid
+    size_t regmask, rcount, rstart, rcursor, rhist, rcls_count, rcls_list, grid;
+    size_t total;
 };
+
+// region side for a gx x gy tile grid: 4, or 8 when 4 would give more than
+// MAX_REGIONS regions; 0 when 8 does too
+inline int region_side(int gx, int gy)
+{
+    for (int rs = REGION_SIDE; rs <= 8; rs *= 2)
+        if ((long)((gx + rs - 1) / rs) * (long)((gy + rs - 1) / rs) <= MAX_REGIONS) return rs;
+    return 0;
+}
 
 GeomLayout geom_layout(int P, int W, int H)
 {
     GeomLayout g;
     const int gx = (W + 15) / 16, gy = (H + 15) / 16;
     g.T = gx * gy;
+    g.RS = region_side(gx, gy);
+    {
+        const int rs = g.RS > 0 ? g.RS : 8;
+        g.NR = ((gx + rs - 1) / rs) * ((gy + rs - 1) / rs);
+    }
+    g.G = (gx + 1) * (gy + 1);
     long nc = ((long)P + 2047) / 2048;
     if (nc < 1) nc = 1;
     if (nc > MAX_CHUNKS) nc = MAX_CHUNKS;
@@ -116,6 +144,14 @@ GeomLayout geom_layout(int P, int W, int H)
     g.cid2id = o; o = align256(o + sizeof(uint32_t) * (size_t)P);
     g.rec = o; o = align256(o + REC_BYTES * (size_t)P);
     g.gacc = o; o = align256(o + GACC_BYTES * (size_t)P);
+    g.regmask = o; o = align256(o + sizeof(uint64_t) * (size_t)g.NR);
+    g.rcount = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NR);
+    g.rstart = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NR);
+    g.rcursor = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NR);
+    g.rhist = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NC * (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS));
+    g.rcls_count = o; o = align256(o + sizeof(uint32_t) * REGION_CLASSES);
+    g.rcls_list = o; o = align256(o + sizeof(int) * (size_t)REGION_CLASSES * (size_t)g.NR);
+    g.grid = o; o = align256(o + sizeof(uint32_t) * (size_t)g.G);
     g.total = o;
     return g;
 }
@@ -168,16 +204,39 @@ const T* at(const void* base, size_t off) { return reinterpret_cast<const T*>(st
 
 // ---------------------------------------------------------------- scans
 
+// Per-call state of the split path's region binning, cleared by the local
+// tile map (null pointers: not used by the caller's path).  Thread i of n
+// clears entries i, i + n, ...
+struct ClearRegions {
+    uint64_t* regmask;   // per-region local-tile masks (null when every tile is local)
+    uint32_t* rcount;    // per-region list lengths
+    uint32_t* grid;      // per-tile count difference grid
+    int NR, G;
+    unsigned lrs;        // log2 of the region side
+
+    __device__ __forceinline__ void clear(int i, int n) const
+    {
+        for (int k = i; k < G && grid != nullptr; k += n) grid[k] = 0u;
+        for (int k = i; k < NR && rcount != nullptr; k += n) {
+            rcount[k] = 0u;
+            if (regmask != nullptr) regmask[k] = 0ull;
+        }
+    }
+};
+
 // compute_locally (null: every tile) -> local tile numbering and the
 // bounding box of the local tiles (meta[5..8] = x0, y0, x1, y1, exclusive
-// ends; empty box if none); clears the per-tile counters.  One block of 16
-// waves; each wave owns a contiguous run of 64-tile rounds: it counts its
-// local tiles (ballots), one barrier publishes the 16 counts, and a second
-// walk numbers the tiles in order with coalesced loads and stores.
+// ends; empty box if none); clears the per-tile counters and the region
+// state, then sets the regions' local-tile masks.  One block of 16 waves;
+// each wave owns a contiguous run of 64-tile rounds: it counts its local
+// tiles (ballots), one barrier publishes the 16 counts, and a second walk
+// numbers the tiles in order with coalesced loads and stores.
 __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, const uint8_t* __restrict__ cl,
                                                         int* __restrict__ loc_map, int* __restrict__ tile_of_local,
-                                                        uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta)
+                                                        uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta,
+                                                        ClearRegions CR)
 {
+    CR.clear(threadIdx.x, 1024);
     __shared__ uint32_t s_cnt[16];
     __shared__ uint32_t s_box[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -226,6 +285,18 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
         meta[5] = any ? s_box[0] : 0u; meta[6] = any ? s_box[1] : 0u;
         meta[7] = any ? s_box[2] : 0u; meta[8] = any ? s_box[3] : 0u;
     }
+    // local-tile mask of every region of the box (the cleared masks and the
+    // box are visible after the barrier above; every local tile lies in the box)
+    if (CR.regmask != nullptr && tot > 0) {
+        const unsigned rs = 1u << CR.lrs, nrx = (s_box[2] - s_box[0] + rs - 1) >> CR.lrs;
+        for (int t = threadIdx.x; t < T; t += 1024) {
+            if (!cl[t]) continue;
+            const unsigned ax = (unsigned)t % gx - s_box[0], ay = (unsigned)t / gx - s_box[1];
+            const unsigned r = (ay >> CR.lrs) * nrx + (ax >> CR.lrs);
+            atomicOr(reinterpret_cast<unsigned long long*>(&CR.regmask[r]),
+                     1ull << (((ay & (rs - 1)) << CR.lrs) + (ax & (rs - 1))));
+        }
+    }
 }
 
 // compute_locally null (every tile local): the identity numbering, the full
@@ -234,9 +305,10 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
 __global__ __launch_bounds__(256) void localmap_all_kernel(int T, unsigned gx, unsigned gy, int* __restrict__ loc_map,
                                                             int* __restrict__ tile_of_local,
                                                             uint32_t* __restrict__ tile_count,
-                                                            uint32_t* __restrict__ meta)
+                                                            uint32_t* __restrict__ meta, ClearRegions CR)
 {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    CR.clear(t, (int)(gridDim.x * blockDim.x));
     if (t < T) {
         loc_map[t] = t;
         tile_of_local[t] = t;
@@ -455,6 +527,195 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     }
 }
 
+// ---- split path: region binning
+//
+// The local-tile box is tiled by regions of RS x RS tiles from its corner
+// (region (rx, ry) = box-relative tiles [rx RS, rx RS + RS) x [ry RS, ...)).
+// A listed Gaussian enters the list of every region where its rect meets a
+// local tile; the lists are sorted per region on chip and filtered into the
+// region's tiles in order.
+
+struct RegionGrid {
+    unsigned bx0, by0, bw, bh, lrs, nrx, nry;
+};
+
+__device__ __forceinline__ RegionGrid region_grid(const uint32_t* __restrict__ meta, unsigned lrs)
+{
+    RegionGrid g;
+    g.bx0 = meta[5];
+    g.by0 = meta[6];
+    g.bw = meta[7] - meta[5];
+    g.bh = meta[8] - meta[6];
+    g.lrs = lrs;
+    const unsigned rs = 1u << lrs;
+    g.nrx = (g.bw + rs - 1) >> lrs;
+    g.nry = (g.bh + rs - 1) >> lrs;
+    return g;
+}
+
+// tile rect of a Gaussian with radius r and mean p (binning rule) clipped to
+// the local-tile box: [x0, x1) x [y0, y1); false when empty (not listed)
+__device__ __forceinline__ bool clip_rect(int r, float2 p, unsigned gx, unsigned gy, const TileBox& box, unsigned& x0,
+                                          unsigned& y0, unsigned& x1, unsigned& y1)
+{
+    x0 = y0 = x1 = y1 = 0;
+    if (r <= 0) return false;
+    gs::rect_int(p.x, p.y, r, gx, gy, x0, y0, x1, y1);
+    x0 = max(x0, box.x0); y0 = max(y0, box.y0);
+    x1 = min(x1, box.x1); y1 = min(y1, box.y1);
+    return x1 > x0 && y1 > y0;
+}
+
+// tiles of the box-relative rect [ax0, ax1) x [ay0, ay1) inside region
+// (rx, ry) as a mask over the region's tiles (bit y RS + x, RS <= 8); the
+// rect meets the region
+__device__ __forceinline__ uint64_t rect_bits_in_region(unsigned ax0, unsigned ay0, unsigned ax1, unsigned ay1,
+                                                        unsigned rx, unsigned ry, unsigned lrs)
+{
+    const unsigned rs = 1u << lrs;
+    const unsigned ox = rx << lrs, oy = ry << lrs;
+    const unsigned cx0 = max(ax0, ox) - ox, cx1 = min(ax1, ox + rs) - ox;
+    const unsigned cy0 = max(ay0, oy) - oy, cy1 = min(ay1, oy + rs) - oy;
+    const uint64_t row = ((1ull << (cx1 - cx0)) - 1ull) << cx0;
+    const uint64_t ones = rs == 8u ? 0x0101010101010101ull : rs == 4u ? 0x1111ull : 0x5ull;   // bit 0 of every row
+    const uint64_t rows = (ones >> ((rs - (cy1 - cy0)) << lrs)) << (cy0 << lrs);
+    return rows * row;
+}
+
+// tiles of the box-relative rect [ax0, ax1) x [ay0, ay1) in region (rx, ry),
+// which it meets, as masks over the region's tile columns (bits 0-7) and rows
+// (bits 8-15): tile (jx, jy) of the region is in the rect iff bits jx and
+// 8 + jy are both set
+__device__ __forceinline__ uint32_t region_mask(unsigned ax0, unsigned ay0, unsigned ax1, unsigned ay1, unsigned rx,
+                                                unsigned ry, unsigned lrs)
+{
+    const unsigned rs = 1u << lrs;
+    auto span = [&](unsigned a0, unsigned a1, unsigned o) {
+        const unsigned c0 = a0 > o ? a0 - o : 0u, c1 = min(a1 - o, rs);
+        return ((1u << c1) - 1u) & ~((1u << c0) - 1u);
+    };
+    return span(ax0, ax1, rx << lrs) | (span(ay0, ay1, ry << lrs) << 8);
+}
+
+// Wave-cooperative walk over the regions each lane's box-relative rect
+// [ax0, ax1) x [ay0, ay1) meets (all 64 lanes call it; in = false: no rect).
+// The wave walks the concatenated (lane, region) pairs 64 at a time, one pair
+// per lane per round however the rect sizes are spread, and calls
+// f(q, rx, ry, owner's rect, owner's pa, pb) for the pairs whose region list
+// the owner enters: the regions that hold a local tile of its rect (every
+// region it meets when all tiles are local).  pa / pb: per-lane payload
+// handed to f as the owner's.
+template <typename F>
+__device__ __forceinline__ void expand_regions(const RegionGrid& rg, bool all_local,
+                                               const uint64_t* __restrict__ regmask, bool in, unsigned ax0,
+                                               unsigned ay0, unsigned ax1, unsigned ay1, uint32_t pa, uint32_t pb,
+                                               F&& f)
+{
+    const int lane = threadIdx.x & 63;
+    unsigned rx0 = 0u, ry0 = 0u, w = 0u;
+    int cnt = 0;
+    if (in) {
+        rx0 = ax0 >> rg.lrs;
+        ry0 = ay0 >> rg.lrs;
+        w = ((ax1 - 1) >> rg.lrs) + 1 - rx0;
+        cnt = (int)(w * (((ay1 - 1) >> rg.lrs) + 1 - ry0));
+    }
+    const uint32_t px = ax0 | (ax1 << 16), py = ay0 | (ay1 << 16);
+    const Expansion e = expansion_begin(cnt);
+    for (int k0 = 0; k0 < e.total; k0 += 64) {
+        int owner;
+        unsigned rx, ry;
+        expansion_at(e, cnt, rx0, ry0, w, k0 + lane, owner, rx, ry);
+        const uint32_t opx = (uint32_t)__shfl((int)px, owner, 64), opy = (uint32_t)__shfl((int)py, owner, 64);
+        const uint32_t opa = (uint32_t)__shfl((int)pa, owner, 64), opb = (uint32_t)__shfl((int)pb, owner, 64);
+        if (k0 + lane < e.total) {
+            const unsigned oax0 = opx & 0xffffu, oax1 = opx >> 16, oay0 = opy & 0xffffu, oay1 = opy >> 16;
+            const unsigned q = ry * rg.nrx + rx;
+            if (all_local || (regmask[q] & rect_bits_in_region(oax0, oay0, oax1, oay1, rx, ry, rg.lrs)) != 0ull)
+                f(q, rx, ry, oax0, oay0, oax1, oay1, opa, opb);
+        }
+    }
+}
+
+// Split path, step 1 (count).  Per chunk of Gaussians (each wave a
+// contiguous run of it, as count_kernel): each wave's listed count; per
+// region, how many of the chunk's listed Gaussians enter its list (LDS
+// histogram; the chunk then reserves its slice of every region list with one
+// atomic per non-empty region and keeps the returned base in its histogram
+// row); and the per-tile instance counts as a difference grid over the box
+// (+1 at (x0, y0) and (x1, y1), -1 at (x1, y0) and (x0, y1) per rect; the
+// scan sums it in 2D).  Beyond LDS_REGIONS regions or LDS_GRID grid entries
+// the counters are global atomics.  Dynamic LDS: min(NR, LDS_REGIONS) +
+// min(G, LDS_GRID) words for the full tile grid.
+__global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
+    int P, int CH, int WS, unsigned gx, unsigned gy, unsigned lrs, const float2* __restrict__ means2D,
+    const int* __restrict__ radii, const uint32_t* __restrict__ meta, const uint64_t* __restrict__ regmask,
+    uint32_t* __restrict__ rhist, uint32_t* __restrict__ rcount, uint32_t* __restrict__ grid,
+    uint32_t* __restrict__ wcount)
+{
+    extern __shared__ uint4 s_dyn[];
+    const RegionGrid rg = region_grid(meta, lrs);
+    const int NRb = (int)(rg.nrx * rg.nry);
+    const bool lds_r = NRb <= LDS_REGIONS;
+    const unsigned gw = rg.bw + 1;
+    const int G = (int)(gw * (rg.bh + 1));
+    const bool lds_g = G <= LDS_GRID;
+    uint32_t* s_rh = reinterpret_cast<uint32_t*>(s_dyn);
+    uint32_t* s_grid = s_rh + (lds_r ? NRb : 0);
+    uint32_t* rc = lds_r ? s_rh : rcount;
+    uint32_t* gp = lds_g ? s_grid : grid;
+    const bool all_local = meta[0] == gx * gy;
+    const TileBox box = tile_box(meta);
+    const int c = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    {
+        const int nz = (lds_r ? NRb : 0) + (lds_g ? G : 0);
+        for (int i = threadIdx.x; i < nz; i += BIN_THREADS) s_rh[i] = 0u;
+        __syncthreads();
+    }
+    const int i1c = min(P, c * CH + CH);
+    const int ws = min(i1c, c * CH + wave * WS);
+    const int i1 = min(i1c, ws + WS);
+    uint32_t listed = 0;
+    int r_n;
+    float2 m_n;
+    load_rm(ws + lane, i1, radii, means2D, r_n, m_n);
+    for (int wb = ws; wb < i1; wb += 64) {
+        const int r = r_n;
+        const float2 m = m_n;
+        load_rm(wb + 64 + lane, i1, radii, means2D, r_n, m_n);
+        unsigned x0, y0, x1, y1;
+        const bool in = clip_rect(r, m, gx, gy, box, x0, y0, x1, y1);
+        listed += (uint32_t)__builtin_popcountll(gs::ballot(in));
+        const unsigned ax0 = x0 - rg.bx0, ax1 = x1 - rg.bx0, ay0 = y0 - rg.by0, ay1 = y1 - rg.by0;
+        if (in) {
+            atomicAdd(&gp[ay0 * gw + ax0], 1u);
+            atomicAdd(&gp[ay0 * gw + ax1], ~0u);
+            atomicAdd(&gp[ay1 * gw + ax0], ~0u);
+            atomicAdd(&gp[ay1 * gw + ax1], 1u);
+        }
+        expand_regions(rg, all_local, regmask, in, ax0, ay0, ax1, ay1, 0u, 0u,
+                       [&](unsigned q, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, uint32_t, uint32_t) {
+                           atomicAdd(&rc[q], 1u);
+                       });
+    }
+    if (lane == 0) wcount[(size_t)c * WAVES_PER_BIN + wave] = listed;
+    __syncthreads();
+    if (lds_r) {
+        uint32_t* row = rhist + (size_t)c * NRb;
+        for (int q = threadIdx.x; q < NRb; q += BIN_THREADS) {
+            const uint32_t v = s_rh[q];
+            row[q] = v ? atomicAdd(&rcount[q], v) : 0u;
+        }
+    }
+    if (lds_g) {
+        for (int i = threadIdx.x; i < G; i += BIN_THREADS) {
+            const uint32_t v = s_grid[i];
+            if (v) atomicAdd(&grid[i], v);
+        }
+    }
+}
+
 // exclusive scans: over local tiles -> tile_start, R -> meta[2..3]; over the
 // per-wave listed counts (in place) -> compact index bases, L -> meta[4]
 __device__ __forceinline__ int sort_class(uint32_t n)
@@ -667,6 +928,107 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
     }
 }
 
+// Split path, step 3 (scatter).  Re-walks the chunk (each wave its run, as
+// in the count) and appends the entry (depth bits, compact index, tile mask
+// over the region -- region_mask) to the chunk's reserved slice of each
+// region list it enters (LDS cursors; global cursors beyond LDS_REGIONS
+// regions).  Every Gaussian gets its compact index or -1 (cidx_of); listed
+// ones also get their blend record and id (cid2id) and their accumulators
+// zeroed, as in scatter_kernel.
+__global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
+    int P, int CH, int WS, unsigned gx, unsigned gy, unsigned lrs, const float2* __restrict__ means2D,
+    const float* __restrict__ depths, const int* __restrict__ radii, const float4* __restrict__ conic_opacity,
+    const float* __restrict__ rgb, const uint32_t* __restrict__ meta, const uint64_t* __restrict__ regmask,
+    const uint32_t* __restrict__ rhist, const uint32_t* __restrict__ rstart, uint32_t* __restrict__ rcursor,
+    const uint32_t* __restrict__ wbase, uint3* __restrict__ rent, int* __restrict__ cidx_of,
+    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, ZeroOut Z)
+{
+    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: nothing to write
+    // dynamic LDS: per wave 64 staged records, then min(NR, LDS_REGIONS) cursors
+    extern __shared__ uint4 s_dyn[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float4* stage = reinterpret_cast<float4*>(s_dyn) + wave * 256;
+    uint32_t* s_cur = reinterpret_cast<uint32_t*>(s_dyn + WAVES_PER_BIN * 256);
+    const RegionGrid rg = region_grid(meta, lrs);
+    const int NRb = (int)(rg.nrx * rg.nry);
+    const bool lds_r = NRb <= LDS_REGIONS;
+    uint32_t* cur = lds_r ? s_cur : rcursor;
+    const bool all_local = meta[0] == gx * gy;
+    const TileBox box = tile_box(meta);
+    const int c = blockIdx.x;
+    if (lds_r) {
+        const uint32_t* row = rhist + (size_t)c * NRb;
+        for (int q = threadIdx.x; q < NRb; q += BIN_THREADS) s_cur[q] = rstart[q] + row[q];
+        __syncthreads();
+    }
+    const int i1c = min(P, c * CH + CH);
+    const int ws = min(i1c, c * CH + wave * WS);
+    const int i1 = min(i1c, ws + WS);
+    uint32_t next = wbase[(size_t)c * WAVES_PER_BIN + wave];
+    // the next group's inputs are loaded while this group is written, as in
+    // scatter_kernel
+    int r_n;
+    float2 m_n;
+    float d_n = 0.f;
+    float4 co_n = make_float4(0.f, 0.f, 0.f, 0.f);
+    float3 c_n = make_float3(0.f, 0.f, 0.f);
+    auto load_next = [&](int in) {
+        load_rm(in, i1, radii, means2D, r_n, m_n);
+        if (in < i1) {
+            d_n = depths[in];
+            co_n = conic_opacity[in];
+            c_n = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
+        }
+    };
+    load_next(ws + lane);
+    for (int wb = ws; wb < i1; wb += 64) {
+        const int i = wb + lane;
+        const int r = r_n;
+        const float2 xy = m_n;
+        const float dep = d_n;
+        const float4 co = co_n;
+        const float3 col = c_n;
+        load_next(i + 64);
+        unsigned x0, y0, x1, y1;
+        const bool in = clip_rect(r, xy, gx, gy, box, x0, y0, x1, y1);
+        const uint64_t lm = gs::ballot(in);
+        const int nl = (int)__builtin_popcountll(lm);
+        const int rank = gs::rank_below(lm);
+        const uint32_t first = next;
+        const uint32_t cidx = first + (uint32_t)rank;
+        next += (uint32_t)nl;
+        if (i < i1) {
+            cidx_of[i] = in ? (int)cidx : -1;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (Z.p[q] != nullptr) Z.p[q][i] = 0;
+        }
+        if (in) {
+            const gs::CullPrep cp = gs::cull_prepare(xy.x, xy.y, co.x, co.y, co.z, co.w);
+            float4* sp = stage + 4 * rank;
+            sp[0] = make_float4(xy.x, xy.y, co.x, co.y);
+            sp[1] = make_float4(co.z, co.w, col.x, col.y);
+            sp[2] = make_float4(col.z, cp.thresh, cp.nbc, cp.nba);
+            sp[3] = make_float4(__uint_as_float((uint32_t)i), gs::alpha_cut_power(co.w), 0.f, 0.f);
+            cid2id[cidx] = (uint32_t)i;
+        }
+        expand_regions(rg, all_local, regmask, in, x0 - rg.bx0, y0 - rg.by0, x1 - rg.bx0, y1 - rg.by0, gs::f2u(dep),
+                       cidx,
+                       [&](unsigned q, unsigned rx, unsigned ry, unsigned ax0, unsigned ay0, unsigned ax1, unsigned ay1,
+                           uint32_t dbits, uint32_t ocidx) {
+                           rent[atomicAdd(&cur[q], 1u)] =
+                               make_uint3(dbits, ocidx, region_mask(ax0, ay0, ax1, ay1, rx, ry, lrs));
+                       });
+        // the group's records are one contiguous run (wave-private staging)
+        __builtin_amdgcn_wave_barrier();
+        {
+            float4* rdst = rec + 4 * (size_t)first;
+            for (int j = lane; j < 4 * nl; j += 64) rdst[j] = stage[j];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // ------------------------------------------------------- per-tile sort
 
 __device__ __forceinline__ void cswap(uint64_t* a, uint64_t* b)
@@ -850,8 +1212,11 @@ struct Log2 {
     static constexpr int value = K <= 1 ? 0 : 1 + Log2<K / 2>::value;
 };
 
-template <int LK>
-__device__ __forceinline__ int rpad(int i) { return i + (i >> LK); }
+// slot of item i: one pad slot after every K items, so that the K items of
+// thread t start at t (K + 1) and the blocked reads (consecutive threads at an
+// odd stride) are free of bank conflicts
+template <int K>
+__device__ __forceinline__ int rpad(int i) { return i + i / K; }
 
 // inclusive scan over the 64 lanes of a wave (DPP: row_shr 1, 2, 4, 8 inside
 // each 16-lane row, then row_bcast 15 / 31 across rows); all lanes active
@@ -907,27 +1272,51 @@ struct alignas(16) RadixLds {
     uint32_t misc[3 * (NT / 64) + 4];
 };
 
+// Loads a bucket's n keys into S.items (all-ones padding from n up to the
+// capacity NT K); kor / kand: OR and AND of the depth bits this thread loaded.
 template <int NT, int K>
-__device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist,
-                                  RadixLds<NT, K>& S)
+__device__ __forceinline__ void radix_load(uint32_t start, int n, const uint64_t* __restrict__ src,
+                                           RadixLds<NT, K>& S, uint32_t& kor, uint32_t& kand)
 {
-    constexpr int LK = Log2<K>::value;
-    constexpr int CAP = NT * K;
-    constexpr int NW = NT / 64;
-    const int t = threadIdx.x;
-    const int lane = t & 63, wid = t >> 6;
-    // load (coalesced); padding items sort last and are never written out
-    uint32_t kor = 0u, kand = ~0u;
-    for (int i = t; i < CAP; i += NT) {
-        uint2 it = make_uint2(~0u, ~0u);
+    kor = 0u;
+    kand = ~0u;
+    // all K loads are issued before the first is used
+    uint64_t v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = (int)threadIdx.x + k * NT;
+        v[k] = i < n ? src[start + i] : ~0ull;
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = (int)threadIdx.x + k * NT;
+        const uint2 it = make_uint2((uint32_t)(v[k] >> 32), (uint32_t)v[k]);
         if (i < n) {
-            const uint64_t v = sortkey[start + i];
-            it = make_uint2((uint32_t)(v >> 32), (uint32_t)v);
             kor |= it.x;
             kand &= it.x;
         }
-        S.items[rpad<LK>(i)] = it;
+        S.items[rpad<K>(i)] = it;
     }
+}
+
+// the compact index of an item whose second word is that index
+struct TieIdentity {
+    __device__ __forceinline__ uint32_t operator()(uint32_t y) const { return y; }
+};
+
+// Sorts the n items in S.items (padding above them, as radix_load leaves it)
+// by (depth bits, compact index), the compact index of an item being
+// tk(second word).  kor / kand: OR and AND of the depth bits of the items
+// this thread placed.  Returns true (block-uniform) when a run of equal
+// depths is longer than MAX_TIE_RUN: the items are then ordered by depth only
+// and the caller sorts the bucket another way.
+template <int NT, int K, typename TieKey = TieIdentity>
+__device__ __forceinline__ bool radix_sort_items(int n, RadixLds<NT, K>& S, uint32_t kor, uint32_t kand,
+                                                 TieKey tk = TieKey())
+{
+    constexpr int NW = NT / 64;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
     // which key bits vary over the bucket (digits that do not are skipped)
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -954,7 +1343,7 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
         uint32_t key[K], val[K], rk[K];
 #pragma unroll
         for (int k = 0; k < K; k++) {
-            const uint2 it = S.items[rpad<LK>(t * K + k)];
+            const uint2 it = S.items[rpad<K>(t * K + k)];
             key[k] = it.x;
             val[k] = it.y;
         }
@@ -991,7 +1380,7 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
 #pragma unroll
         for (int k = 0; k < K; k++) rk[k] += cnt[cnt_slot((int)((key[k] >> shift) & 15u) * NT + t)];
 #pragma unroll
-        for (int k = 0; k < K; k++) S.items[rpad<LK>((int)rk[k])] = make_uint2(key[k], val[k]);
+        for (int k = 0; k < K; k++) S.items[rpad<K>((int)rk[k])] = make_uint2(key[k], val[k]);
         // only this thread reads its column (digit, t) in the scatter: clear
         // it for the next pass
 #pragma unroll
@@ -1005,7 +1394,7 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
 #pragma unroll
     for (int j = 0; j < K + 2; j++) {
         const int i = t * K - 1 + j;
-        kn[j] = (i >= 0 && i < n) ? S.items[rpad<LK>(i)].x : 0u;
+        kn[j] = (i >= 0 && i < n) ? S.items[rpad<K>(i)].x : 0u;
     }
 #pragma unroll
     for (int k = 0; k < K; k++) {
@@ -1015,37 +1404,43 @@ __device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ 
         if (kn[k + 2] != key_i) continue;
         if (i > 0 && kn[k] == key_i) continue;   // not the run's first item
         int e = i + 2;
-        while (e < n && e - i <= MAX_TIE_RUN && S.items[rpad<LK>(e)].x == key_i) e++;
+        while (e < n && e - i <= MAX_TIE_RUN && S.items[rpad<K>(e)].x == key_i) e++;
         if (e - i > MAX_TIE_RUN) {
             S.misc[2 * NW] = 1u;
             continue;
         }
         for (int a = i + 1; a < e; a++) {
-            const uint32_t v = S.items[rpad<LK>(a)].y;
+            const uint32_t v = S.items[rpad<K>(a)].y;
+            const uint32_t kv = tk(v);
             int b = a - 1;
-            while (b >= i && S.items[rpad<LK>(b)].y > v) {
-                S.items[rpad<LK>(b + 1)].y = S.items[rpad<LK>(b)].y;
+            while (b >= i && tk(S.items[rpad<K>(b)].y) > kv) {
+                S.items[rpad<K>(b + 1)].y = S.items[rpad<K>(b)].y;
                 b--;
             }
-            S.items[rpad<LK>(b + 1)].y = v;
+            S.items[rpad<K>(b + 1)].y = v;
         }
     }
     __syncthreads();
-    if (S.misc[2 * NW] != 0u) {
+    return S.misc[2 * NW] != 0u;
+}
+
+template <int NT, int K>
+__device__ void radix_sort_bucket(uint32_t start, int n, uint64_t* __restrict__ sortkey, uint32_t* __restrict__ clist,
+                                  RadixLds<NT, K>& S)
+{
+    uint32_t kor, kand;
+    radix_load<NT, K>(start, n, sortkey, S, kor, kand);
+    if (radix_sort_items<NT, K>(n, S, kor, kand)) {
         // a long run of equal depths: the full 64-bit sort in global memory
+        // (the bucket there is still the unsorted input)
         uint64_t* s = sortkey + start;
-        for (int i = t; i < n; i += NT) {
-            const uint2 it = S.items[rpad<LK>(i)];
-            s[i] = ((uint64_t)it.x << 32) | it.y;
-        }
-        __syncthreads();
         int N = 1;
         while (N < n) N <<= 1;
         bitonic<NT>(s, n, N);
         write_sorted(start, n, s, clist, NT);
         return;
     }
-    for (int i = t; i < n; i += NT) clist[start + i] = S.items[rpad<LK>(i)].y;
+    for (int i = threadIdx.x; i < n; i += NT) clist[start + i] = S.items[rpad<K>(i)].y;
 }
 
 // One launch per size class; its blocks walk the class's list of buckets
@@ -1094,6 +1489,648 @@ __global__ __launch_bounds__(NT) void tilesort_radix_kernel(const uint32_t* __re
             bitonic<NT>(s, n, N);
             write_sorted(start, n, s, clist, NT);
         }
+    }
+}
+
+// size class of a region list of n entries
+__device__ __forceinline__ int region_class(uint32_t n)
+{
+    return n <= 1024u ? 0 : n <= 2048u ? 1 : n <= 4096u ? 2 : n <= (uint32_t)REGION_CAP ? 3 : 4;
+}
+
+// Split path, step 2 (scan), one block:
+//   - the per-wave listed counts -> compact index bases (in place), L -> meta[4];
+//   - the difference grid summed in 2D (rows, then columns; in LDS when it
+//     fits) -> each local tile's instance count (tile_count) and, by a scan in
+//     local order, its offset (tile_start) and R -> meta[2..3];
+//   - the region list lengths -> offsets (rstart, and rcursor for the global
+//     cursors) and per-class region lists; the total -> meta[10].
+// cap: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
+__global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict__ meta, unsigned gx, unsigned lrs,
+                                                            const int* __restrict__ tile_of_local,
+                                                            uint32_t* __restrict__ grid,
+                                                            uint32_t* __restrict__ tile_count,
+                                                            uint32_t* __restrict__ tile_start,
+                                                            uint32_t* __restrict__ wcount, int NW,
+                                                            const uint32_t* __restrict__ rcount,
+                                                            uint32_t* __restrict__ rstart,
+                                                            uint32_t* __restrict__ rcursor,
+                                                            uint32_t* __restrict__ rcls_count,
+                                                            int* __restrict__ rcls_list, int NR, uint64_t cap)
+{
+    __shared__ uint32_t s_grid[LDS_GRID];
+    __shared__ uint32_t s_wave[32];
+    __shared__ uint32_t s_cls[REGION_CLASSES];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    if (tid < REGION_CLASSES) s_cls[tid] = 0u;
+    {
+        uint32_t base = 0;
+        for (int w0 = 0; w0 < NW; w0 += 1024) {
+            const int wi = w0 + tid;
+            const uint32_t v = wi < NW ? wcount[wi] : 0u;
+            uint32_t tot;
+            const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
+            if (wi < NW) wcount[wi] = base + pre;
+            base += tot;
+        }
+        if (tid == 0) meta[4] = base;
+    }
+    const RegionGrid rg = region_grid(meta, lrs);
+    const unsigned gw = rg.bw + 1;
+    const int G = (int)(gw * (rg.bh + 1));
+    const bool lds_g = G <= LDS_GRID;
+    uint32_t* gp = lds_g ? s_grid : grid;
+    if (lds_g) {
+        for (int i = tid; i < G; i += 1024) s_grid[i] = grid[i];
+        __syncthreads();
+    }
+    // rows: one wave per row, 64 columns at a time
+    for (unsigned y = (unsigned)wid; y < rg.bh; y += 16) {
+        uint32_t carry = 0u;
+        for (unsigned x0 = 0; x0 < rg.bw; x0 += 64) {
+            const unsigned x = x0 + (unsigned)lane;
+            const uint32_t v = x < rg.bw ? gp[y * gw + x] : 0u;
+            const uint32_t sum = wave_incl_scan_u32(v) + carry;
+            if (x < rg.bw) gp[y * gw + x] = sum;
+            carry = (uint32_t)__builtin_amdgcn_readlane((int)sum, 63);
+        }
+    }
+    __syncthreads();
+    // columns: one thread per column, 8 rows per step
+    for (unsigned x = (unsigned)tid; x < rg.bw; x += 1024) {
+        uint32_t acc = 0u;
+        unsigned y = 0;
+        for (; y + 8 <= rg.bh; y += 8) {
+            uint32_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = gp[(y + k) * gw + x];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc += v[k];
+                gp[(y + k) * gw + x] = acc;
+            }
+        }
+        for (; y < rg.bh; y++) {
+            acc += gp[y * gw + x];
+            gp[y * gw + x] = acc;
+        }
+    }
+    __syncthreads();
+    // local tiles in order: counts, offsets, R
+    const int TL = (int)meta[0];
+    uint64_t base = 0;
+    for (int t0 = 0; t0 < TL; t0 += 1024) {
+        const int l = t0 + tid;
+        uint32_t v = 0u;
+        if (l < TL) {
+            const unsigned t = (unsigned)tile_of_local[l];
+            v = gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)];
+        }
+        uint32_t tot;
+        const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
+        if (l < TL) {
+            tile_count[l] = v;
+            tile_start[l] = (uint32_t)(base + pre);
+        }
+        base += tot;
+    }
+    // regions: offsets and size classes
+    const int NRb = (int)(rg.nrx * rg.nry);
+    uint64_t ebase = 0;
+    for (int r0 = 0; r0 < NRb; r0 += 1024) {
+        const int r = r0 + tid;
+        const uint32_t v = r < NRb ? rcount[r] : 0u;
+        uint32_t tot;
+        const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
+        if (r < NRb) {
+            rstart[r] = (uint32_t)(ebase + pre);
+            rcursor[r] = (uint32_t)(ebase + pre);
+            if (v > 0u) {
+                const int c = region_class(v);
+                rcls_list[(size_t)c * NR + atomicAdd(&s_cls[c], 1u)] = r;
+            }
+        }
+        ebase += tot;
+    }
+    __syncthreads();
+    const bool over = base > cap || ebase > cap;
+    if (tid < REGION_CLASSES) rcls_count[tid] = over ? 0u : s_cls[tid];
+    if (tid == 0) {
+        meta[2] = (uint32_t)(base & 0xffffffffu);
+        meta[3] = (uint32_t)(base >> 32);
+        meta[9] = over ? 1u : 0u;
+        meta[10] = (uint32_t)ebase;
+    }
+}
+
+// ---- split path: per-region sort and tile filter
+
+// the tiles of region r: origin and extent (clipped to the box)
+struct RegionTiles {
+    unsigned tx0, ty0, tw, th;
+};
+
+__device__ __forceinline__ RegionTiles region_tiles(const RegionGrid& rg, int r)
+{
+    const unsigned rx = (unsigned)r % rg.nrx, ry = (unsigned)r / rg.nrx;
+    const unsigned rs = 1u << rg.lrs;
+    RegionTiles t;
+    t.tx0 = rg.bx0 + (rx << rg.lrs);
+    t.ty0 = rg.by0 + (ry << rg.lrs);
+    t.tw = min(rs, rg.bw - (rx << rg.lrs));
+    t.th = min(rs, rg.bh - (ry << rg.lrs));
+    return t;
+}
+
+// where the filter writes: tile t's list is clist[tile_start[l], + tile_count[l])
+// for its local index l
+struct TileOut {
+    const int* loc_map;
+    const uint32_t* tile_start;
+    const uint32_t* tile_count;
+    uint32_t* clist;
+    unsigned gx, gy;
+};
+
+// Region lists hold 12-byte entries (uint3): depth bits, compact index and
+// the entry's tile mask over the region (region_mask), written with one store.
+
+// LDS of a region sort.  An item is (depth bits, slot | tile mask << 16): the
+// slot it was loaded into (its compact index is cidx[slot]) and its tile mask.
+template <int NT, int K>
+struct RegionLds {
+    RadixLds<NT, K> R;
+    uint32_t cidx[NT * K];
+    uint32_t tslot[64 * 2];        // per tile of the region: list start (~0u: not local) and end
+    uint32_t tab[(NT / 64) * 4];   // filter: per wave and tile of a pass, the wave's count, then its offset
+    uint32_t piece[4 * 2];         // filter: per tile of a pass, this call's output start (~0u: none) and length
+};
+
+// words the filter may stage output in: the item slots and the counter
+// table, which are free once every wave holds its items in registers
+template <int NT, int K>
+constexpr int stage_words() { return 2 * (NT * K + NT) + RADIX_DIGITS * NT; }
+
+// list start (~0u: the tile is outside the box or not local) and end of tile
+// j (row-major in the region, RS per row)
+__device__ __forceinline__ void tile_slot(unsigned j, unsigned lrs, const RegionTiles& rt, const TileOut& to,
+                                          bool all_local, uint32_t& b, uint32_t& e)
+{
+    b = ~0u;
+    e = 0u;
+    const unsigned rs = 1u << lrs, jx = j & (rs - 1), jy = j >> lrs;
+    if (jx < rt.tw && jy < rt.th) {
+        const unsigned tt = (rt.ty0 + jy) * to.gx + rt.tx0 + jx;
+        const int l = all_local ? (int)tt : to.loc_map[tt];
+        if (l >= 0) {
+            b = to.tile_start[l];
+            e = b + to.tile_count[l];
+        }
+    }
+}
+
+// Loads region list entries [start, start + n) (n <= NT K) into slots 0..n-1
+// (all-ones padding above); kor / kand: OR and AND of this thread's depths.
+template <int NT, int K>
+__device__ __forceinline__ void region_load(uint32_t start, int n, const uint3* __restrict__ rent,
+                                            RegionLds<NT, K>& L, uint32_t& kor, uint32_t& kand)
+{
+    kor = 0u;
+    kand = ~0u;
+    uint3 v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = (int)threadIdx.x + k * NT;
+        v[k] = i < n ? rent[start + i] : make_uint3(~0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = (int)threadIdx.x + k * NT;
+        uint2 it = make_uint2(~0u, ~0u);
+        if (i < n) {
+            it = make_uint2(v[k].x, (uint32_t)i | (v[k].z << 16));
+            kor |= it.x;
+            kand &= it.x;
+            L.cidx[i] = v[k].y;
+        }
+        L.R.items[rpad<K>(i)] = it;
+    }
+}
+
+// Bitonic sort of the n items in LDS by (depth bits, tk(second word)) -- the
+// way out when radix_sort_items finds a long run of equal depths; pairs
+// touching slots past n are skipped (those slots hold padding, which sorts last)
+template <int NT, int K, typename TieKey>
+__device__ void lds_bitonic_items(int n, RadixLds<NT, K>& S, TieKey tk)
+{
+    int N = 1;
+    while (N < n) N <<= 1;
+    auto cx = [&](int a, int b) {
+        const uint2 A = S.items[rpad<K>(a)], B = S.items[rpad<K>(b)];
+        if (B.x < A.x || (B.x == A.x && tk(B.y) < tk(A.y))) {
+            S.items[rpad<K>(a)] = B;
+            S.items[rpad<K>(b)] = A;
+        }
+    };
+    for (int k = 2; k <= N; k <<= 1) {
+        const int lh = __builtin_ctz((unsigned)k) - 1;
+        for (int p = threadIdx.x; p < (N >> 1); p += NT) {
+            const int blk = p >> lh, off = p & ((1 << lh) - 1);
+            const int a = (blk << (lh + 1)) + off;
+            const int b = a + k - 1 - 2 * off;
+            if (b < n) cx(a, b);
+        }
+        __syncthreads();
+        for (int j = k >> 2; j >= 1; j >>= 1) {
+            const int lj = __builtin_ctz((unsigned)j);
+            for (int p = threadIdx.x; p < (N >> 1); p += NT) {
+                const int blk = p >> lj, off = p & (j - 1);
+                const int a = (blk << (lj + 1)) + off;
+                if (a + j < n) cx(a, a + j);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// copies len words from LDS to global memory (all NT threads): 16-byte
+// stores once dst is aligned, single words at the ends
+template <int NT>
+__device__ __forceinline__ void copy_out(uint32_t* __restrict__ dst, const uint32_t* src, uint32_t len)
+{
+    const uint32_t mis = (uint32_t)(((uintptr_t)dst >> 2) & 3u);
+    const uint32_t head = min(len, (4u - mis) & 3u);
+    if (threadIdx.x < head) dst[threadIdx.x] = src[threadIdx.x];
+    const uint32_t nb = (len - head) >> 2;
+    uint4* d4 = reinterpret_cast<uint4*>(dst + head);
+    for (uint32_t i = threadIdx.x; i < nb; i += NT) {
+        const uint32_t o = head + 4u * i;
+        d4[i] = make_uint4(src[o], src[o + 1], src[o + 2], src[o + 3]);
+    }
+    const uint32_t t0 = head + 4u * nb;
+    if (threadIdx.x < len - t0) dst[t0 + threadIdx.x] = src[t0 + threadIdx.x];
+}
+
+// Filters the n sorted items into the region's local tiles, in order, four
+// tiles of a row at a time.  Wave w holds items [w c, w c + c) in registers
+// (c = n / (NT/64) rounded up to 64, at most 64 K), 64 per step.  Per pass:
+// each wave counts, per tile, its items whose mask holds the tile (one ballot
+// per step and tile); 4 threads turn the counts into each wave's offset in
+// each tile's piece; a second walk puts each wave's items there (ballot ranks
+// give consecutive positions), into LDS when the pass's pieces fit there, and
+// the pieces are then written out with 16-byte stores (each piece is one
+// contiguous run of the tile's list).  tb / te: this thread's tile slot
+// (threads below RS^2; tile_slot); s_tcur (optional): per-tile offsets
+// carried over from earlier calls for the same region, advanced by this call.
+template <int NT, int K>
+__device__ void filter_region(int n, RegionLds<NT, K>& L, const RegionTiles& rt, const TileOut& to, unsigned lrs,
+                              uint32_t tb, uint32_t te, uint32_t* s_tcur)
+{
+    constexpr int NW = NT / 64, SW = stage_words<NT, K>();
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int chunk = ((n + NW - 1) / NW + 63) & ~63;
+    const int i0 = wid * chunk, i1 = min(n, i0 + chunk);
+    const int steps = i1 > i0 ? (i1 - i0 + 63) >> 6 : 0;
+    const unsigned rs = 1u << lrs;
+    uint32_t pm[K], cx[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = i0 + 64 * k + lane;
+        pm[k] = 0u;
+        cx[k] = 0u;
+        if (i < i1) {
+            const uint32_t y = L.R.items[rpad<K>(i)].y;
+            pm[k] = y >> 16;
+            cx[k] = L.cidx[y & 0xffffu];
+        }
+    }
+    if (threadIdx.x < rs * rs) {
+        L.tslot[2 * threadIdx.x] = tb;
+        L.tslot[2 * threadIdx.x + 1] = te;
+    }
+    __syncthreads();   // every wave holds its items: item slots and counters are staging space
+    uint32_t* stage = reinterpret_cast<uint32_t*>(L.R.items);
+    // a row's tiles four at a time (RS = 8: two passes per row)
+    for (unsigned jy = 0; jy < rt.th; jy++) {
+        for (unsigned x0 = 0; x0 < rt.tw; x0 += 4) {
+            uint32_t cnt[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) cnt[q] = 0u;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                if (k < steps) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (x0 + (unsigned)q < rt.tw) {
+                            const uint32_t bits = (1u << (x0 + q)) | (1u << (8 + jy));
+                            cnt[q] += (uint32_t)__builtin_popcountll(gs::ballot((pm[k] & bits) == bits));
+                        }
+                    }
+                }
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) L.tab[wid * 4 + q] = cnt[q];
+            }
+            __syncthreads();
+            if (threadIdx.x < 4) {
+                const unsigned q = threadIdx.x, j = (jy << lrs) + x0 + q;
+                uint32_t b = ~0u, e = 0u;
+                if (x0 + q < rt.tw) {
+                    b = L.tslot[2 * j];
+                    e = L.tslot[2 * j + 1];
+                }
+                uint32_t run = 0u;
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    const uint32_t v = L.tab[w * 4 + q];
+                    L.tab[w * 4 + q] = run;
+                    run += v;
+                }
+                uint32_t gs0 = b;
+                if (b != ~0u && s_tcur != nullptr) gs0 += s_tcur[j];
+                // a piece that would overrun its list (never by construction) is not written
+                const bool ok = b != ~0u && gs0 + run <= e;
+                L.piece[2 * q] = ok ? gs0 : ~0u;
+                L.piece[2 * q + 1] = ok ? run : 0u;
+                if (ok && s_tcur != nullptr) s_tcur[j] += run;
+            }
+            __syncthreads();
+            uint32_t gq[4], so[4], pos[4];
+            uint32_t total = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                gq[q] = __builtin_amdgcn_readfirstlane(L.piece[2 * q]);
+                so[q] = total;
+                total += __builtin_amdgcn_readfirstlane(L.piece[2 * q + 1]);
+                pos[q] = __builtin_amdgcn_readfirstlane(L.tab[wid * 4 + q]);
+            }
+            const bool staged = total <= (uint32_t)SW;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                if (k < steps) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (gq[q] == ~0u) continue;
+                        const uint32_t bits = (1u << (x0 + q)) | (1u << (8 + jy));
+                        const bool hit = (pm[k] & bits) == bits;
+                        const uint64_t m = gs::ballot(hit);
+                        if (hit) {
+                            const uint32_t p = pos[q] + (uint32_t)gs::rank_below(m);
+                            if (staged) stage[so[q] + p] = cx[k];
+                            else to.clist[gq[q] + p] = cx[k];
+                        }
+                        pos[q] += (uint32_t)__builtin_popcountll(m);
+                    }
+                }
+            }
+            __syncthreads();
+            if (staged) {
+#pragma unroll 1
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t len = __builtin_amdgcn_readfirstlane(L.piece[2 * q + 1]);
+                    if (gq[q] != ~0u && len > 0u) copy_out<NT>(to.clist + gq[q], stage + so[q], len);
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Bitonic sort of n region entries in global memory by (depth bits, compact
+// index), in place (one block; pairs touching positions past n are skipped)
+template <int NT>
+__device__ void bitonic_entries(uint3* s, int n, int N)
+{
+    auto cx = [&](int a, int b) {
+        const uint3 A = s[a], B = s[b];
+        if (B.x < A.x || (B.x == A.x && B.y < A.y)) {
+            s[a] = B;
+            s[b] = A;
+        }
+    };
+    for (int k = 2; k <= N; k <<= 1) {
+        const int lh = __builtin_ctz((unsigned)k) - 1;
+        for (int p = threadIdx.x; p < (N >> 1); p += NT) {
+            const int blk = p >> lh, off = p & ((1 << lh) - 1);
+            const int a = (blk << (lh + 1)) + off;
+            const int b = a + k - 1 - 2 * off;
+            if (b < n) cx(a, b);
+        }
+        __syncthreads();
+        for (int j = k >> 2; j >= 1; j >>= 1) {
+            const int lj = __builtin_ctz((unsigned)j);
+            for (int p = threadIdx.x; p < (N >> 1); p += NT) {
+                const int blk = p >> lj, off = p & (j - 1);
+                const int a = (blk << (lj + 1)) + off;
+                if (a + j < n) cx(a, a + j);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Fallback filter over a region list sorted in global memory: one wave per tile.
+template <int NT>
+__device__ void filter_global(uint32_t start, int n, const uint3* __restrict__ rent, const RegionTiles& rt,
+                              const TileOut& to, bool all_local)
+{
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63;
+    const int ntile = (int)(rt.tw * rt.th);
+    for (int j = (int)(threadIdx.x >> 6); j < ntile; j += NW) {
+        const unsigned jx = (unsigned)j % rt.tw, jy = (unsigned)j / rt.tw;
+        const unsigned tt = (rt.ty0 + jy) * to.gx + rt.tx0 + jx;
+        const int l = all_local ? (int)tt : to.loc_map[tt];
+        if (l < 0) continue;
+        const uint32_t bits = (1u << jx) | (1u << (8 + jy));
+        const uint32_t base = to.tile_start[l], end = base + to.tile_count[l];
+        uint32_t cur = 0u;
+        for (int b = 0; b < n; b += 64) {
+            const int i = b + lane;
+            uint32_t m = 0u, cidx = 0u;
+            if (i < n) {
+                const uint3 v = rent[start + i];
+                cidx = v.y;
+                m = v.z;
+            }
+            const bool hit = (m & bits) == bits;
+            const uint64_t mb = gs::ballot(hit);
+            const uint32_t pos = base + cur + (uint32_t)gs::rank_below(mb);
+            if (hit && pos < end) to.clist[pos] = cidx;
+            cur += (uint32_t)__builtin_popcountll(mb);
+        }
+    }
+}
+
+// A region list longer than CAP = NT K: its entries are split into depth
+// ranges of at most CAP (digit = 12 bits of the depth from its highest varying
+// bit; range k = the digits whose exclusive prefix lies in [k CAP/2,
+// (k+1) CAP/2), so a range holds at most CAP/2 plus its last digit's count),
+// which are gathered, sorted and filtered one after another, the tile
+// positions carried over.  A digit holding more than CAP/2 entries or a list
+// of one depth: the whole list is sorted in global memory (bitonic, in place)
+// and filtered from there (filter_global).  s_big: 4096 digit prefixes, then
+// 64 tile positions.
+template <int NT, int K>
+__device__ void sort_filter_big(uint32_t start, int n, uint3* __restrict__ rent, RegionLds<NT, K>& L,
+                                uint32_t* s_big, const RegionGrid& rg, int r, const TileOut& to, bool all_local)
+{
+    constexpr int CAP = NT * K, C = CAP / 2, NW = NT / 64, NDIG = 4096;
+    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    RadixLds<NT, K>& S = L.R;
+    const RegionTiles rt = region_tiles(rg, r);
+    uint32_t* s_pre = s_big;
+    uint32_t* s_tcur = s_big + NDIG;
+    uint32_t* s_gather = S.misc + 3 * NW + 1;
+    uint32_t* s_max = S.misc + 3 * NW + 2;
+    uint32_t tb = ~0u, te = 0u;
+    if ((unsigned)t < (1u << (2 * rg.lrs))) tile_slot((unsigned)t, rg.lrs, rt, to, all_local, tb, te);
+    // passes over the list read 8 entries per thread at a time, all in flight
+    constexpr int U = 8;
+    auto pass = [&](auto&& f) {
+        for (int i0 = 0; i0 < n; i0 += U * NT) {
+            uint3 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + t + u * NT;
+                v[u] = i < n ? rent[start + i] : make_uint3(0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (i0 + t + u * NT < n) f(v[u]);
+        }
+    };
+    uint32_t kor = 0u, kand = ~0u;
+    pass([&](const uint3& v) {
+        kor |= v.x;
+        kand &= v.x;
+    });
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
+        kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
+    }
+    if (lane == 0) { S.misc[wid] = kor; S.misc[NW + wid] = kand; }
+    for (int i = t; i < NDIG; i += NT) s_pre[i] = 0u;
+    if (t < 64) s_tcur[t] = 0u;
+    if (t == 0) *s_max = 0u;
+    __syncthreads();
+    uint32_t vor = 0u, vand = ~0u;
+#pragma unroll
+    for (int w = 0; w < NW; w++) { vor |= S.misc[w]; vand &= S.misc[NW + w]; }
+    const uint32_t vary = vor ^ vand;
+    bool global_sort = vary == 0u;
+    unsigned shift = 0u;
+    if (!global_sort) {
+        const int hb = 31 - __builtin_clz(vary);
+        shift = hb >= 11 ? (unsigned)(hb - 11) : 0u;
+        pass([&](const uint3& v) { atomicAdd(&s_pre[(v.x >> shift) & (NDIG - 1)], 1u); });
+        __syncthreads();
+        // exclusive scan of the digit counts in place; the largest count
+        constexpr int PER = (NDIG + NT - 1) / NT;
+        uint32_t loc[PER];
+        uint32_t sum = 0u, mx = 0u;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int d = t * PER + j;
+            const uint32_t v = d < NDIG ? s_pre[d] : 0u;
+            loc[j] = v;
+            sum += v;
+            mx = max(mx, v);
+        }
+        uint32_t tot;
+        uint32_t run = radix_block_scan<NT>(sum, S.misc + 2 * NW + 1, &tot);
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int d = t * PER + j;
+            if (d < NDIG) s_pre[d] = run;
+            run += loc[j];
+        }
+        atomicMax(s_max, mx);
+        __syncthreads();
+        global_sort = *s_max > (uint32_t)(CAP - C);
+    }
+    if (!global_sort) {
+        auto tk = [&](uint32_t y) { return L.cidx[y & 0xffffu]; };
+        const int nr = (n + C - 1) / C;
+        for (int k = 0; k < nr; k++) {
+            for (int i = t; i < CAP; i += NT) S.items[rpad<K>(i)] = make_uint2(~0u, ~0u);
+            if (t == 0) *s_gather = 0u;
+            __syncthreads();
+            uint32_t gor = 0u, gand = ~0u;
+            pass([&](const uint3& v) {
+                if (s_pre[(v.x >> shift) & (NDIG - 1)] / (uint32_t)C == (uint32_t)k) {
+                    const uint32_t p = atomicAdd(s_gather, 1u);
+                    S.items[rpad<K>((int)p)] = make_uint2(v.x, p | (v.z << 16));
+                    L.cidx[p] = v.y;
+                    gor |= v.x;
+                    gand &= v.x;
+                }
+            });
+            __syncthreads();
+            const int m = (int)*s_gather;
+            if (radix_sort_items<NT, K>(m, S, gor, gand, tk)) lds_bitonic_items<NT, K>(m, S, tk);
+            filter_region<NT, K>(m, L, rt, to, rg.lrs, tb, te, s_tcur);
+        }
+    } else {
+        __syncthreads();
+        int N = 1;
+        while (N < n) N <<= 1;
+        bitonic_entries<NT>(rent + start, n, N);
+        filter_global<NT>(start, n, rent, rt, to, all_local);
+    }
+}
+
+// Split path, step 4: one launch per region size class; its blocks walk the
+// class's region list (block b takes entries b, b + gridDim.x, ...), sort each
+// region's list on chip (radix_sort_items; a long run of equal depths: a
+// bitonic network in LDS) and filter it into the region's tiles.
+template <int NT, int K>
+__global__ __launch_bounds__(NT) void regionsort_kernel(const uint32_t* __restrict__ cls_count,
+                                                        const int* __restrict__ cls_list,
+                                                        const uint32_t* __restrict__ rcount,
+                                                        const uint32_t* __restrict__ rstart,
+                                                        const uint3* __restrict__ rent,
+                                                        const uint32_t* __restrict__ meta, unsigned lrs, TileOut to)
+{
+    __shared__ RegionLds<NT, K> L;
+    const RegionGrid rg = region_grid(meta, lrs);
+    const bool all_local = meta[0] == to.gx * to.gy;
+    const int nl = (int)*cls_count;
+    auto tk = [&](uint32_t y) { return L.cidx[y & 0xffffu]; };
+    for (int e = blockIdx.x; e < nl; e += gridDim.x) {
+        if (e != (int)blockIdx.x) __syncthreads();   // the previous region's reads of LDS are done
+        const int r = cls_list[e];
+        const int n = (int)rcount[r];
+        const RegionTiles rt = region_tiles(rg, r);
+        uint32_t tb = ~0u, te = 0u;   // this thread's tile slot, loaded while the region sorts
+        if (threadIdx.x < (1u << (2 * lrs))) tile_slot(threadIdx.x, lrs, rt, to, all_local, tb, te);
+        uint32_t kor, kand;
+        region_load<NT, K>(rstart[r], n, rent, L, kor, kand);
+        if (radix_sort_items<NT, K>(n, L.R, kor, kand, tk)) lds_bitonic_items<NT, K>(n, L.R, tk);
+        filter_region<NT, K>(n, L, rt, to, lrs, tb, te, nullptr);
+    }
+}
+
+// the regions longer than NT K (sort_filter_big), one block each
+template <int NT, int K>
+__global__ __launch_bounds__(NT) void regionsort_big_kernel(const uint32_t* __restrict__ xcount,
+                                                            const int* __restrict__ xlist,
+                                                            const uint32_t* __restrict__ rcount,
+                                                            const uint32_t* __restrict__ rstart,
+                                                            uint3* __restrict__ rent,
+                                                            const uint32_t* __restrict__ meta, unsigned lrs, TileOut to)
+{
+    __shared__ RegionLds<NT, K> L;
+    __shared__ uint32_t s_big[4096 + 64];
+    const RegionGrid rg = region_grid(meta, lrs);
+    const bool all_local = meta[0] == to.gx * to.gy;
+    const int nx = (int)*xcount;
+    for (int e = blockIdx.x; e < nx; e += gridDim.x) {
+        if (e != (int)blockIdx.x) __syncthreads();
+        const int r = xlist[e];
+        sort_filter_big<NT, K>(rstart[r], (int)rcount[r], rent, L, s_big, rg, r, to, all_local);
     }
 }
 
@@ -1904,6 +2941,15 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
 
 namespace {
 size_t count_lds_bytes(int T) { return sizeof(uint32_t) * (size_t)(T < LDS_TILES ? T : LDS_TILES); }
+size_t count_regions_lds_bytes(const GeomLayout& g)
+{
+    return sizeof(uint32_t) * ((size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS) + (size_t)(g.G < LDS_GRID ? g.G : LDS_GRID));
+}
+size_t scatter_regions_lds_bytes(const GeomLayout& g)
+{
+    return sizeof(float4) * 256 * WAVES_PER_BIN + sizeof(uint32_t) * (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS);
+}
+unsigned region_lrs(const GeomLayout& g) { return g.RS == 8 ? 3u : g.RS == 4 ? 2u : 1u; }
 size_t scatter_lds_bytes(int T) { return sizeof(float4) * 256 * WAVES_PER_BIN + count_lds_bytes(T); }
 
 // grid of the blend kernels: whole supertiles per XCD
@@ -2028,38 +3074,62 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     // the binning's wall time on the caller's stream: from here to the end of
     // the sorts in the forward call (the R readback and the caller's
     // allocation between the two calls included)
+    // the split path bins through regions (count_regions / scan_regions /
+    // scatter_regions / regionsort); the full-image path through per-tile
+    // buckets (count / tilescan / scatter / tilesort)
+    const bool split = !full;
+    GS_REQUIRE(!split || g.RS > 0, "a %ux%u tile grid has more than %d regions of 8x8 tiles", gx, gy, MAX_REGIONS);
+    const unsigned lrs = region_lrs(g);
+    ClearRegions CR{nullptr, nullptr, nullptr, 0, 0, lrs};
+    if (split)
+        CR = ClearRegions{compute_locally != nullptr ? at<uint64_t>(geom, g.regmask) : nullptr,
+                          at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid), g.NR, g.G, lrs};
     if (gs::timing_on()) gs::timing_stage_begin(stream, BINNING_STAGE);
     if (compute_locally == nullptr) {
+        const size_t nclear = std::max<size_t>((size_t)g.T, split ? (size_t)std::max(g.G, g.NR) : 0);
         GS_TIMED("localmap_kernel", stream,
-                 hipLaunchKernelGGL(localmap_all_kernel, dim3(gs_div_up((size_t)g.T, 256)), dim3(256), 0, stream, g.T,
-                                    gx, gy, loc_map, tile_of_local, tile_count, meta));
+                 hipLaunchKernelGGL(localmap_all_kernel, dim3(gs_div_up(nclear, 256)), dim3(256), 0, stream, g.T,
+                                    gx, gy, loc_map, tile_of_local, tile_count, meta, CR));
     } else {
         GS_TIMED("localmap_kernel", stream,
                  hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, gx, compute_locally, loc_map,
-                                    tile_of_local, tile_count, meta));
+                                    tile_of_local, tile_count, meta, CR));
     }
     GS_LAUNCH_CHECK("localmap_kernel");
-    if (P > 0) {
-        const float2* m2 = reinterpret_cast<const float2*>(means2D);
-        if (full) {
-            GS_TIMED("count_kernel", stream,
-                     hipLaunchKernelGGL(count_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream,
-                                        P, g.CH, g.WS, gx, gy, m2, radii, loc_map, meta, hist, tile_count,
-                                        at<uint32_t>(geom, g.wcount), reinterpret_cast<const float2*>(rects),
-                                        reinterpret_cast<const float4*>(conic_opacity)));
-        } else {
-            GS_TIMED("count_kernel", stream,
-                     hipLaunchKernelGGL(count_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream,
-                                        P, g.CH, g.WS, gx, gy, m2, radii, loc_map, meta, hist, tile_count,
-                                        at<uint32_t>(geom, g.wcount), nullptr, nullptr));
+    if (split) {
+        if (P > 0) {
+            GS_TIMED("count_regions_kernel", stream,
+                     hipLaunchKernelGGL(count_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), count_regions_lds_bytes(g),
+                                        stream, P, g.CH, g.WS, gx, gy, lrs, reinterpret_cast<const float2*>(means2D),
+                                        radii, meta, at<const uint64_t>(geom, g.regmask), at<uint32_t>(geom, g.rhist),
+                                        at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid),
+                                        at<uint32_t>(geom, g.wcount)));
+            GS_LAUNCH_CHECK("count_regions_kernel");
         }
+        GS_TIMED("scan_regions_kernel", stream,
+                 hipLaunchKernelGGL(scan_regions_kernel, dim3(1), dim3(1024), 0, stream, meta, gx, lrs, tile_of_local,
+                                    at<uint32_t>(geom, g.grid), tile_count, tile_start, at<uint32_t>(geom, g.wcount),
+                                    P > 0 ? g.NC * WAVES_PER_BIN : 0, at<const uint32_t>(geom, g.rcount),
+                                    at<uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
+                                    at<uint32_t>(geom, g.rcls_count), at<int>(geom, g.rcls_list), g.NR, cap));
+        GS_LAUNCH_CHECK("scan_regions_kernel");
+    }
+    if (!split && P > 0) {
+        GS_TIMED("count_kernel", stream,
+                 hipLaunchKernelGGL(count_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), count_lds_bytes(g.T), stream, P,
+                                    g.CH, g.WS, gx, gy, reinterpret_cast<const float2*>(means2D), radii, loc_map,
+                                    meta, hist, tile_count, at<uint32_t>(geom, g.wcount),
+                                    reinterpret_cast<const float2*>(rects),
+                                    reinterpret_cast<const float4*>(conic_opacity)));
         GS_LAUNCH_CHECK("count_kernel");
     }
-    GS_TIMED("tilescan_kernel", stream,
-             hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
-                                at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
-                                at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap));
-    GS_LAUNCH_CHECK("tilescan_kernel");
+    if (!split) {
+        GS_TIMED("tilescan_kernel", stream,
+                 hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
+                                    at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
+                                    at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap));
+        GS_LAUNCH_CHECK("tilescan_kernel");
+    }
     if (rb != nullptr) {
         GS_HIP(hipMemcpyAsync(rb->host, meta + 2, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
         GS_HIP(hipEventRecord(rb->ev, stream));
@@ -2119,24 +3189,78 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             GS_LAUNCH_CHECK("zero_i32_kernel");
         }
     }
-    if (R > 0) {
+    if (R > 0 && !full) {
+        // split path: region lists, then per region a sort and the filter
+        // into its tiles.  One launch per region size class, largest first,
+        // one after another on the caller's stream; the grids are bounded by
+        // how many regions of the class the region entries (at most R) can
+        // fill and by what fits on the chip at once.
+        const unsigned lrs = region_lrs(g);
+        uint32_t* clist = at<uint32_t>(binning, bl.clist);
+        // region lists (12 bytes per entry, at most R entries) in the point
+        // list and key areas of the binning buffer (12 R bytes from point_list)
+        uint3* rent = at<uint3>(binning, bl.point_list);
+        GS_TIMED("scatter_regions_kernel", stream,
+                 hipLaunchKernelGGL(scatter_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), scatter_regions_lds_bytes(g),
+                                    stream, P, g.CH, g.WS, gx, gy, lrs, reinterpret_cast<const float2*>(means2D),
+                                    depths, radii, reinterpret_cast<const float4*>(conic_opacity), rgb, meta,
+                                    at<const uint64_t>(geom, g.regmask), at<const uint32_t>(geom, g.rhist),
+                                    at<const uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
+                                    at<const uint32_t>(geom, g.wcount), rent, at<int>(geom, g.cidx_of),
+                                    at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec), Z));
+        GS_LAUNCH_CHECK("scatter_regions_kernel");
+        const uint32_t* cc = at<const uint32_t>(geom, g.rcls_count);
+        const int* cls = at<const int>(geom, g.rcls_list);
+        const uint32_t* rcount = at<const uint32_t>(geom, g.rcount);
+        const uint32_t* rstart = at<const uint32_t>(geom, g.rstart);
+        const TileOut to{loc_map, tile_start, tile_count, clist, gx, gy};
+        auto grid_of = [&](int lo, int cap) {
+            const int64_t fit = R / (int64_t)(lo + 1);
+            return (unsigned)std::min<int64_t>(std::min<int64_t>((int64_t)g.NR, fit), (int64_t)cap);
+        };
+        auto list = [&](int c) { return cls + (size_t)c * g.NR; };
+        const unsigned g4 = grid_of(REGION_CAP, 256), g3 = grid_of(4096, 256), g2 = grid_of(2048, 512);
+        const unsigned g1 = grid_of(1024, 1024), g0 = grid_of(0, 2048);
+        if (g4 > 0) {
+            GS_TIMED("regionsort_big_kernel", stream,
+                     hipLaunchKernelGGL((regionsort_big_kernel<512, 16>), dim3(g4), dim3(512), 0, stream, cc + 4,
+                                        list(4), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_big_kernel");
+        }
+        if (g3 > 0) {
+            GS_TIMED("regionsort_kernel_8k", stream,
+                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, stream, cc + 3,
+                                        list(3), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_kernel_8k");
+        }
+        if (g2 > 0) {
+            GS_TIMED("regionsort_kernel_4k", stream,
+                     hipLaunchKernelGGL((regionsort_kernel<256, 16>), dim3(g2), dim3(256), 0, stream, cc + 2,
+                                        list(2), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_kernel_4k");
+        }
+        if (g1 > 0) {
+            GS_TIMED("regionsort_kernel_2k", stream,
+                     hipLaunchKernelGGL((regionsort_kernel<256, 8>), dim3(g1), dim3(256), 0, stream, cc + 1,
+                                        list(1), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_kernel_2k");
+        }
+        if (g0 > 0) {
+            GS_TIMED("regionsort_kernel_1k", stream,
+                     hipLaunchKernelGGL((regionsort_kernel<128, 8>), dim3(g0), dim3(128), 0, stream, cc + 0,
+                                        list(0), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_kernel_1k");
+        }
+    }
+    if (R > 0 && full) {
         const float2* m2 = reinterpret_cast<const float2*>(means2D);
         const float4* co = reinterpret_cast<const float4*>(conic_opacity);
-        if (full) {
-            GS_TIMED("scatter_kernel", stream,
-                     hipLaunchKernelGGL(scatter_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
-                                        stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
-                                        hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
-                                        at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
-                                        at<float4>(geom, g.rec), reinterpret_cast<const float2*>(rects), Z));
-        } else {
-            GS_TIMED("scatter_kernel", stream,
-                     hipLaunchKernelGGL(scatter_kernel<false>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T),
-                                        stream, P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta,
-                                        hist, tile_start, cursor, at<const uint32_t>(geom, g.wcount), sortkey,
-                                        at<int>(geom, g.cidx_of), at<uint32_t>(geom, g.cid2id),
-                                        at<float4>(geom, g.rec), nullptr, Z));
-        }
+        GS_TIMED("scatter_kernel", stream,
+                 hipLaunchKernelGGL(scatter_kernel<true>, dim3(g.NC), dim3(BIN_THREADS), scatter_lds_bytes(g.T), stream,
+                                    P, g.CH, g.WS, gx, gy, m2, depths, radii, co, rgb, loc_map, meta, hist, tile_start,
+                                    cursor, at<const uint32_t>(geom, g.wcount), sortkey, at<int>(geom, g.cidx_of),
+                                    at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec),
+                                    reinterpret_cast<const float2*>(rects), Z));
         GS_LAUNCH_CHECK("scatter_kernel");
         uint32_t* clist = at<uint32_t>(binning, bl.clist);
         // one launch per LDS size class over that class's bucket list, one

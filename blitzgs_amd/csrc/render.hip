@@ -72,6 +72,7 @@ constexpr int REGION_SIDE = 2;       // preferred region side (tiles)
 constexpr int MAX_REGIONS = 16384;   // regions of the full tile grid
 constexpr int LDS_REGIONS = 4096;    // region counters / cursors held in LDS by the count and the scatter
 constexpr int LDS_GRID = 12288;      // entries of the tile-count difference grid held in LDS
+constexpr int GRID_PARTS = 16;       // partial difference grids (chunk c adds into part c % GRID_PARTS)
 constexpr int REGION_CLASSES = 5;    // region list size classes: <= 1k, 2k, 4k, 8k entries, larger
 constexpr int REGION_CAP = 8192;     // longest region list sorted on chip in one piece
 constexpr const char* BINNING_STAGE = "binning (wall)";   // per-kernel timing: the whole binning stage
@@ -96,8 +97,8 @@ struct GeomLayout {
     size_t cls_count, cls_list;   // per size class: number of local tiles, their local indices (T per class)
     size_t loc_map, tile_of_local, meta, hist, tile_count, tile_start, cursor, wcount, cidx_of, cid2id, rec, gacc;
     // split path: per-region local-tile masks, list lengths, offsets and
-    // cursors, per-chunk region bases, per-class region lists and the
-    // per-tile count difference grid
+    // cursors, per-chunk region bases, per-class region lists and the partial
+    // per-tile count difference grids
     size_t regmask, rcount, rstart, rcursor, rhist, rcls_count, rcls_list, grid;
     size_t total;
 };
@@ -151,7 +152,7 @@ GeomLayout geom_layout(int P, int W, int H)
     g.rhist = o; o = align256(o + sizeof(uint32_t) * (size_t)g.NC * (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS));
     g.rcls_count = o; o = align256(o + sizeof(uint32_t) * REGION_CLASSES);
     g.rcls_list = o; o = align256(o + sizeof(int) * (size_t)REGION_CLASSES * (size_t)g.NR);
-    g.grid = o; o = align256(o + sizeof(uint32_t) * (size_t)g.G);
+    g.grid = o; o = align256(o + sizeof(uint32_t) * (size_t)GRID_PARTS * (size_t)g.G);
     g.total = o;
     return g;
 }
@@ -210,8 +211,8 @@ const T* at(const void* base, size_t off) { return reinterpret_cast<const T*>(st
 struct ClearRegions {
     uint64_t* regmask;   // per-region local-tile masks (null when every tile is local)
     uint32_t* rcount;    // per-region list lengths
-    uint32_t* grid;      // per-tile count difference grid
-    int NR, G;
+    uint32_t* grid;      // partial per-tile count difference grids
+    int NR, G;           // regions; entries of all partial grids
     unsigned lrs;        // log2 of the region side
 
     __device__ __forceinline__ void clear(int i, int n) const
@@ -527,6 +528,39 @@ __global__ __launch_bounds__(BIN_THREADS) void count_kernel(
     }
 }
 
+// inclusive scan over the 64 lanes of a wave (DPP: row_shr 1, 2, 4, 8 inside
+// each 16-lane row, then row_bcast 15 / 31 across rows); all lanes active
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v)
+{
+    v += dpp_u<0x111>(v);          // row_shr:1
+    v += dpp_u<0x112>(v);          // row_shr:2
+    v += dpp_u<0x114>(v);          // row_shr:4
+    v += dpp_u<0x118>(v);          // row_shr:8
+    v += dpp_u<0x142, 0xa>(v);     // row_bcast:15 into rows 1 and 3
+    v += dpp_u<0x143, 0xc>(v);     // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+
+// inclusive max over the 64 lanes of a wave, for values >= 0 (the DPP steps
+// read 0 past the row edges); all lanes active
+__device__ __forceinline__ uint32_t wave_incl_max_u32(uint32_t v)
+{
+    v = max(v, dpp_u<0x111>(v));
+    v = max(v, dpp_u<0x112>(v));
+    v = max(v, dpp_u<0x114>(v));
+    v = max(v, dpp_u<0x118>(v));
+    v = max(v, dpp_u<0x142, 0xa>(v));
+    v = max(v, dpp_u<0x143, 0xc>(v));
+    return v;
+}
+
 // ---- split path: region binning
 //
 // The local-tile box is tiled by regions of RS x RS tiles from its corner
@@ -597,43 +631,66 @@ __device__ __forceinline__ uint32_t region_mask(unsigned ax0, unsigned ay0, unsi
     return span(ax0, ax1, rx << lrs) | (span(ay0, ay1, ry << lrs) << 8);
 }
 
+// LDS a wave needs for expand_regions: per lane its staged data (two
+// uint4), then 64 segment marks
+constexpr int EXPAND_WORDS = 64 * 8 + 64;
+
 // Wave-cooperative walk over the regions each lane's box-relative rect
 // [ax0, ax1) x [ay0, ay1) meets (all 64 lanes call it; in = false: no rect).
 // The wave walks the concatenated (lane, region) pairs 64 at a time, one pair
 // per lane per round however the rect sizes are spread, and calls
-// f(q, rx, ry, owner's rect, owner's pa, pb) for the pairs whose region list
-// the owner enters: the regions that hold a local tile of its rect (every
-// region it meets when all tiles are local).  pa / pb: per-lane payload
-// handed to f as the owner's.
+// f(q, rx, ry, owner's rect, owner's pa, pb, lbits) for the pairs whose region
+// list the owner enters: the regions that hold a local tile of its rect
+// (every region it meets when all tiles are local; lbits: the rect's local
+// tiles in the region, rect_bits_in_region layout -- 0 when all are local).  pa / pb: per-lane payload
+// handed to f as the owner's.  The lanes' data are staged in the wave's LDS
+// (s, EXPAND_WORDS words); the owner of each position is found by marking the
+// segment starts of the round and a max-scan over the marks.
 template <typename F>
 __device__ __forceinline__ void expand_regions(const RegionGrid& rg, bool all_local,
                                                const uint64_t* __restrict__ regmask, bool in, unsigned ax0,
                                                unsigned ay0, unsigned ax1, unsigned ay1, uint32_t pa, uint32_t pb,
-                                               F&& f)
+                                               uint32_t* s, F&& f)
 {
     const int lane = threadIdx.x & 63;
+    uint4* s_own = reinterpret_cast<uint4*>(s);
+    uint32_t* s_mark = s + 64 * 8;
     unsigned rx0 = 0u, ry0 = 0u, w = 0u;
-    int cnt = 0;
+    uint32_t cnt = 0u;
     if (in) {
         rx0 = ax0 >> rg.lrs;
         ry0 = ay0 >> rg.lrs;
         w = ((ax1 - 1) >> rg.lrs) + 1 - rx0;
-        cnt = (int)(w * (((ay1 - 1) >> rg.lrs) + 1 - ry0));
+        cnt = w * (((ay1 - 1) >> rg.lrs) + 1 - ry0);
     }
-    const uint32_t px = ax0 | (ax1 << 16), py = ay0 | (ay1 << 16);
-    const Expansion e = expansion_begin(cnt);
-    for (int k0 = 0; k0 < e.total; k0 += 64) {
-        int owner;
-        unsigned rx, ry;
-        expansion_at(e, cnt, rx0, ry0, w, k0 + lane, owner, rx, ry);
-        const uint32_t opx = (uint32_t)__shfl((int)px, owner, 64), opy = (uint32_t)__shfl((int)py, owner, 64);
-        const uint32_t opa = (uint32_t)__shfl((int)pa, owner, 64), opb = (uint32_t)__shfl((int)pb, owner, 64);
-        if (k0 + lane < e.total) {
-            const unsigned oax0 = opx & 0xffffu, oax1 = opx >> 16, oay0 = opy & 0xffffu, oay1 = opy >> 16;
+    const uint32_t incl = wave_incl_scan_u32(cnt);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    if (total == 0u) return;
+    const uint32_t excl = incl - cnt;
+    s_own[2 * lane] = make_uint4(rx0 | (ry0 << 16), w, excl, ax0 | (ax1 << 16));
+    s_own[2 * lane + 1] = make_uint4(ay0 | (ay1 << 16), pa, pb, 0u);
+    for (uint32_t k0 = 0; k0 < total; k0 += 64) {
+        s_mark[lane] = 0u;
+        __builtin_amdgcn_wave_barrier();
+        if (cnt > 0u && excl >= k0 && excl < k0 + 64u) s_mark[excl - k0] = (uint32_t)lane + 1u;
+        // the lane whose segment holds position k0: the first with incl > k0
+        const uint32_t own0 = (uint32_t)__builtin_popcountll(gs::ballot(incl <= k0));
+        __builtin_amdgcn_wave_barrier();
+        uint32_t v = s_mark[lane];
+        if (lane == 0 && v == 0u) v = own0 + 1u;
+        const int owner = (int)wave_incl_max_u32(v) - 1;
+        const uint4 o0 = s_own[2 * owner], o1 = s_own[2 * owner + 1];
+        const uint32_t k = k0 + (uint32_t)lane;
+        if (k < total) {
+            const uint32_t local = k - o0.z, ow = o0.y;
+            const uint32_t qy = local / ow;
+            const unsigned rx = (o0.x & 0xffffu) + (local - qy * ow), ry = (o0.x >> 16) + qy;
+            const unsigned oax0 = o0.w & 0xffffu, oax1 = o0.w >> 16, oay0 = o1.x & 0xffffu, oay1 = o1.x >> 16;
             const unsigned q = ry * rg.nrx + rx;
-            if (all_local || (regmask[q] & rect_bits_in_region(oax0, oay0, oax1, oay1, rx, ry, rg.lrs)) != 0ull)
-                f(q, rx, ry, oax0, oay0, oax1, oay1, opa, opb);
+            const uint64_t lbits = all_local ? 0ull : regmask[q] & rect_bits_in_region(oax0, oay0, oax1, oay1, rx, ry, rg.lrs);
+            if (all_local || lbits != 0ull) f(q, rx, ry, oax0, oay0, oax1, oay1, o1.y, o1.z, lbits);
         }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -644,13 +701,15 @@ __device__ __forceinline__ void expand_regions(const RegionGrid& rg, bool all_lo
 // atomic per non-empty region and keeps the returned base in its histogram
 // row); and the per-tile instance counts as a difference grid over the box
 // (+1 at (x0, y0) and (x1, y1), -1 at (x1, y0) and (x0, y1) per rect; the
-// scan sums it in 2D).  Beyond LDS_REGIONS regions or LDS_GRID grid entries
-// the counters are global atomics.  Dynamic LDS: min(NR, LDS_REGIONS) +
+// scan sums it in 2D), added into partial grid c % GRID_PARTS so that the
+// chunks' additions do not all meet at the same addresses.  Beyond
+// LDS_REGIONS regions or LDS_GRID grid entries the counters are global
+// atomics.  Dynamic LDS: per wave EXPAND_WORDS, then min(NR, LDS_REGIONS) +
 // min(G, LDS_GRID) words for the full tile grid.
 __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
     int P, int CH, int WS, unsigned gx, unsigned gy, unsigned lrs, const float2* __restrict__ means2D,
     const int* __restrict__ radii, const uint32_t* __restrict__ meta, const uint64_t* __restrict__ regmask,
-    uint32_t* __restrict__ rhist, uint32_t* __restrict__ rcount, uint32_t* __restrict__ grid,
+    uint32_t* __restrict__ rhist, uint32_t* __restrict__ rcount, uint32_t* __restrict__ grid, int Gfull,
     uint32_t* __restrict__ wcount)
 {
     extern __shared__ uint4 s_dyn[];
@@ -660,13 +719,15 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
     const unsigned gw = rg.bw + 1;
     const int G = (int)(gw * (rg.bh + 1));
     const bool lds_g = G <= LDS_GRID;
-    uint32_t* s_rh = reinterpret_cast<uint32_t*>(s_dyn);
+    const int c = blockIdx.x;
+    uint32_t* s_exp = reinterpret_cast<uint32_t*>(s_dyn) + (threadIdx.x >> 6) * EXPAND_WORDS;
+    uint32_t* s_rh = reinterpret_cast<uint32_t*>(s_dyn) + WAVES_PER_BIN * EXPAND_WORDS;
     uint32_t* s_grid = s_rh + (lds_r ? NRb : 0);
     uint32_t* rc = lds_r ? s_rh : rcount;
-    uint32_t* gp = lds_g ? s_grid : grid;
+    uint32_t* part = grid + (size_t)(c % GRID_PARTS) * (size_t)Gfull;
+    uint32_t* gp = lds_g ? s_grid : part;
     const bool all_local = meta[0] == gx * gy;
     const TileBox box = tile_box(meta);
-    const int c = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     {
         const int nz = (lds_r ? NRb : 0) + (lds_g ? G : 0);
@@ -677,13 +738,17 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
     const int ws = min(i1c, c * CH + wave * WS);
     const int i1 = min(i1c, ws + WS);
     uint32_t listed = 0;
-    int r_n;
-    float2 m_n;
+    // the inputs of the next two groups are loaded while this group is counted
+    int r_n, r_nn;
+    float2 m_n, m_nn;
     load_rm(ws + lane, i1, radii, means2D, r_n, m_n);
+    load_rm(ws + 64 + lane, i1, radii, means2D, r_nn, m_nn);
     for (int wb = ws; wb < i1; wb += 64) {
         const int r = r_n;
         const float2 m = m_n;
-        load_rm(wb + 64 + lane, i1, radii, means2D, r_n, m_n);
+        r_n = r_nn;
+        m_n = m_nn;
+        load_rm(wb + 128 + lane, i1, radii, means2D, r_nn, m_nn);
         unsigned x0, y0, x1, y1;
         const bool in = clip_rect(r, m, gx, gy, box, x0, y0, x1, y1);
         listed += (uint32_t)__builtin_popcountll(gs::ballot(in));
@@ -694,24 +759,34 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
             atomicAdd(&gp[ay1 * gw + ax0], ~0u);
             atomicAdd(&gp[ay1 * gw + ax1], 1u);
         }
-        expand_regions(rg, all_local, regmask, in, ax0, ay0, ax1, ay1, 0u, 0u,
-                       [&](unsigned q, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, uint32_t, uint32_t) {
-                           atomicAdd(&rc[q], 1u);
-                       });
+        expand_regions(rg, all_local, regmask, in, ax0, ay0, ax1, ay1, 0u, 0u, s_exp,
+                       [&](unsigned q, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, uint32_t, uint32_t,
+                           uint64_t) { atomicAdd(&rc[q], 1u); });
     }
     if (lane == 0) wcount[(size_t)c * WAVES_PER_BIN + wave] = listed;
     __syncthreads();
     if (lds_r) {
         uint32_t* row = rhist + (size_t)c * NRb;
-        for (int q = threadIdx.x; q < NRb; q += BIN_THREADS) {
-            const uint32_t v = s_rh[q];
-            row[q] = v ? atomicAdd(&rcount[q], v) : 0u;
+        // the bases of up to four regions per thread are requested at once
+        for (int q0 = 0; q0 < NRb; q0 += 4 * BIN_THREADS) {
+            uint32_t b[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int q = q0 + u * BIN_THREADS + (int)threadIdx.x;
+                const uint32_t v = q < NRb ? s_rh[q] : 0u;
+                b[u] = v ? atomicAdd(&rcount[q], v) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int q = q0 + u * BIN_THREADS + (int)threadIdx.x;
+                if (q < NRb) row[q] = b[u];
+            }
         }
     }
     if (lds_g) {
         for (int i = threadIdx.x; i < G; i += BIN_THREADS) {
             const uint32_t v = s_grid[i];
-            if (v) atomicAdd(&grid[i], v);
+            if (v) atomicAdd(&part[i], v);
         }
     }
 }
@@ -948,7 +1023,8 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
     extern __shared__ uint4 s_dyn[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float4* stage = reinterpret_cast<float4*>(s_dyn) + wave * 256;
-    uint32_t* s_cur = reinterpret_cast<uint32_t*>(s_dyn + WAVES_PER_BIN * 256);
+    uint32_t* s_exp = reinterpret_cast<uint32_t*>(s_dyn + WAVES_PER_BIN * 256) + wave * EXPAND_WORDS;
+    uint32_t* s_cur = reinterpret_cast<uint32_t*>(s_dyn + WAVES_PER_BIN * 256) + WAVES_PER_BIN * EXPAND_WORDS;
     const RegionGrid rg = region_grid(meta, lrs);
     const int NRb = (int)(rg.nrx * rg.nry);
     const bool lds_r = NRb <= LDS_REGIONS;
@@ -965,30 +1041,37 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
     const int ws = min(i1c, c * CH + wave * WS);
     const int i1 = min(i1c, ws + WS);
     uint32_t next = wbase[(size_t)c * WAVES_PER_BIN + wave];
-    // the next group's inputs are loaded while this group is written, as in
-    // scatter_kernel
-    int r_n;
-    float2 m_n;
-    float d_n = 0.f;
-    float4 co_n = make_float4(0.f, 0.f, 0.f, 0.f);
-    float3 c_n = make_float3(0.f, 0.f, 0.f);
-    auto load_next = [&](int in) {
-        load_rm(in, i1, radii, means2D, r_n, m_n);
+    // the inputs of the next two groups are loaded while this group is written
+    struct In {
+        int r;
+        float2 m;
+        float d;
+        float4 co;
+        float3 c;
+    };
+    auto load_in = [&](int in, In& v) {
+        load_rm(in, i1, radii, means2D, v.r, v.m);
+        v.d = 0.f;
+        v.co = make_float4(0.f, 0.f, 0.f, 0.f);
+        v.c = make_float3(0.f, 0.f, 0.f);
         if (in < i1) {
-            d_n = depths[in];
-            co_n = conic_opacity[in];
-            c_n = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
+            v.d = depths[in];
+            v.co = conic_opacity[in];
+            v.c = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
         }
     };
-    load_next(ws + lane);
+    In nx1, nx2;
+    load_in(ws + lane, nx1);
+    load_in(ws + 64 + lane, nx2);
     for (int wb = ws; wb < i1; wb += 64) {
         const int i = wb + lane;
-        const int r = r_n;
-        const float2 xy = m_n;
-        const float dep = d_n;
-        const float4 co = co_n;
-        const float3 col = c_n;
-        load_next(i + 64);
+        const int r = nx1.r;
+        const float2 xy = nx1.m;
+        const float dep = nx1.d;
+        const float4 co = nx1.co;
+        const float3 col = nx1.c;
+        nx1 = nx2;
+        load_in(i + 128, nx2);
         unsigned x0, y0, x1, y1;
         const bool in = clip_rect(r, xy, gx, gy, box, x0, y0, x1, y1);
         const uint64_t lm = gs::ballot(in);
@@ -1013,9 +1096,9 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
             cid2id[cidx] = (uint32_t)i;
         }
         expand_regions(rg, all_local, regmask, in, x0 - rg.bx0, y0 - rg.by0, x1 - rg.bx0, y1 - rg.by0, gs::f2u(dep),
-                       cidx,
+                       cidx, s_exp,
                        [&](unsigned q, unsigned rx, unsigned ry, unsigned ax0, unsigned ay0, unsigned ax1, unsigned ay1,
-                           uint32_t dbits, uint32_t ocidx) {
+                           uint32_t dbits, uint32_t ocidx, uint64_t) {
                            rent[atomicAdd(&cur[q], 1u)] =
                                make_uint3(dbits, ocidx, region_mask(ax0, ay0, ax1, ay1, rx, ry, lrs));
                        });
@@ -1218,24 +1301,6 @@ struct Log2 {
 template <int K>
 __device__ __forceinline__ int rpad(int i) { return i + i / K; }
 
-// inclusive scan over the 64 lanes of a wave (DPP: row_shr 1, 2, 4, 8 inside
-// each 16-lane row, then row_bcast 15 / 31 across rows); all lanes active
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
-{
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
-}
-
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v)
-{
-    v += dpp_u<0x111>(v);          // row_shr:1
-    v += dpp_u<0x112>(v);          // row_shr:2
-    v += dpp_u<0x114>(v);          // row_shr:4
-    v += dpp_u<0x118>(v);          // row_shr:8
-    v += dpp_u<0x142, 0xa>(v);     // row_bcast:15 into rows 1 and 3
-    v += dpp_u<0x143, 0xc>(v);     // row_bcast:31 into rows 2 and 3
-    return v;
-}
 
 // exclusive scan of one value per thread over an NT-thread block (block
 // total in *total); s_tmp holds NT / 64 words
@@ -1498,17 +1563,46 @@ __device__ __forceinline__ int region_class(uint32_t n)
     return n <= 1024u ? 0 : n <= 2048u ? 1 : n <= 4096u ? 2 : n <= (uint32_t)REGION_CAP ? 3 : 4;
 }
 
+// Exclusive scan of N values over a 1024-thread block, each thread taking 8
+// consecutive values per round of 8192 (all 8 loads in flight, one block scan
+// per round): put(i, prefix, value) for every i < N; returns the total.
+template <typename Get, typename Put>
+__device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Get&& get, Put&& put)
+{
+    uint64_t base = 0;
+    for (int r0 = 0; r0 < N; r0 += 8192) {
+        const int i0 = r0 + (int)threadIdx.x * 8;
+        uint32_t v[8];
+        uint32_t sum = 0u;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            v[j] = i0 + j < N ? get(i0 + j) : 0u;
+            sum += v[j];
+        }
+        uint32_t tot;
+        uint32_t run = gs::block_excl_scan_1024(sum, s_wave, &tot);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (i0 + j < N) put(i0 + j, (uint32_t)(base + run), v[j]);
+            run += v[j];
+        }
+        base += tot;
+    }
+    return base;
+}
+
 // Split path, step 2 (scan), one block:
 //   - the per-wave listed counts -> compact index bases (in place), L -> meta[4];
-//   - the difference grid summed in 2D (rows, then columns; in LDS when it
-//     fits) -> each local tile's instance count (tile_count) and, by a scan in
-//     local order, its offset (tile_start) and R -> meta[2..3];
+//   - the difference grid (the sum of the partial grids) summed in 2D (rows,
+//     then columns; in LDS when it fits) -> each local tile's instance count
+//     (tile_count) and, by a scan in local order, its offset (tile_start) and
+//     R -> meta[2..3];
 //   - the region list lengths -> offsets (rstart, and rcursor for the global
 //     cursors) and per-class region lists; the total -> meta[10].
 // cap: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
 __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict__ meta, unsigned gx, unsigned lrs,
                                                             const int* __restrict__ tile_of_local,
-                                                            uint32_t* __restrict__ grid,
+                                                            uint32_t* __restrict__ grid, int Gfull,
                                                             uint32_t* __restrict__ tile_count,
                                                             uint32_t* __restrict__ tile_start,
                                                             uint32_t* __restrict__ wcount, int NW,
@@ -1524,26 +1618,26 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     if (tid < REGION_CLASSES) s_cls[tid] = 0u;
     {
-        uint32_t base = 0;
-        for (int w0 = 0; w0 < NW; w0 += 1024) {
-            const int wi = w0 + tid;
-            const uint32_t v = wi < NW ? wcount[wi] : 0u;
-            uint32_t tot;
-            const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
-            if (wi < NW) wcount[wi] = base + pre;
-            base += tot;
-        }
-        if (tid == 0) meta[4] = base;
+        const uint64_t L = block_scan_runs(
+            NW, s_wave, [&](int i) { return wcount[i]; }, [&](int i, uint32_t pre, uint32_t) { wcount[i] = pre; });
+        if (tid == 0) meta[4] = (uint32_t)L;
     }
     const RegionGrid rg = region_grid(meta, lrs);
     const unsigned gw = rg.bw + 1;
     const int G = (int)(gw * (rg.bh + 1));
     const bool lds_g = G <= LDS_GRID;
+    // the partial grids summed (into LDS, or into partial 0)
     uint32_t* gp = lds_g ? s_grid : grid;
-    if (lds_g) {
-        for (int i = tid; i < G; i += 1024) s_grid[i] = grid[i];
-        __syncthreads();
+    for (int i = tid; i < G; i += 1024) {
+        uint32_t v[GRID_PARTS];
+#pragma unroll
+        for (int k = 0; k < GRID_PARTS; k++) v[k] = grid[(size_t)k * Gfull + i];
+        uint32_t sum = 0u;
+#pragma unroll
+        for (int k = 0; k < GRID_PARTS; k++) sum += v[k];
+        gp[i] = sum;
     }
+    __syncthreads();
     // rows: one wave per row, 64 columns at a time
     for (unsigned y = (unsigned)wid; y < rg.bh; y += 16) {
         uint32_t carry = 0u;
@@ -1578,48 +1672,36 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     __syncthreads();
     // local tiles in order: counts, offsets, R
     const int TL = (int)meta[0];
-    uint64_t base = 0;
-    for (int t0 = 0; t0 < TL; t0 += 1024) {
-        const int l = t0 + tid;
-        uint32_t v = 0u;
-        if (l < TL) {
+    const uint64_t R = block_scan_runs(
+        TL, s_wave,
+        [&](int l) {
             const unsigned t = (unsigned)tile_of_local[l];
-            v = gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)];
-        }
-        uint32_t tot;
-        const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
-        if (l < TL) {
+            return gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)];
+        },
+        [&](int l, uint32_t pre, uint32_t v) {
             tile_count[l] = v;
-            tile_start[l] = (uint32_t)(base + pre);
-        }
-        base += tot;
-    }
+            tile_start[l] = pre;
+        });
     // regions: offsets and size classes
     const int NRb = (int)(rg.nrx * rg.nry);
-    uint64_t ebase = 0;
-    for (int r0 = 0; r0 < NRb; r0 += 1024) {
-        const int r = r0 + tid;
-        const uint32_t v = r < NRb ? rcount[r] : 0u;
-        uint32_t tot;
-        const uint32_t pre = gs::block_excl_scan_1024(v, s_wave, &tot);
-        if (r < NRb) {
-            rstart[r] = (uint32_t)(ebase + pre);
-            rcursor[r] = (uint32_t)(ebase + pre);
+    const uint64_t E = block_scan_runs(
+        NRb, s_wave, [&](int r) { return rcount[r]; },
+        [&](int r, uint32_t pre, uint32_t v) {
+            rstart[r] = pre;
+            rcursor[r] = pre;
             if (v > 0u) {
                 const int c = region_class(v);
                 rcls_list[(size_t)c * NR + atomicAdd(&s_cls[c], 1u)] = r;
             }
-        }
-        ebase += tot;
-    }
+        });
     __syncthreads();
-    const bool over = base > cap || ebase > cap;
+    const bool over = R > cap || E > cap;
     if (tid < REGION_CLASSES) rcls_count[tid] = over ? 0u : s_cls[tid];
     if (tid == 0) {
-        meta[2] = (uint32_t)(base & 0xffffffffu);
-        meta[3] = (uint32_t)(base >> 32);
+        meta[2] = (uint32_t)(R & 0xffffffffu);
+        meta[3] = (uint32_t)(R >> 32);
         meta[9] = over ? 1u : 0u;
-        meta[10] = (uint32_t)ebase;
+        meta[10] = (uint32_t)E;
     }
 }
 
@@ -2943,11 +3025,13 @@ namespace {
 size_t count_lds_bytes(int T) { return sizeof(uint32_t) * (size_t)(T < LDS_TILES ? T : LDS_TILES); }
 size_t count_regions_lds_bytes(const GeomLayout& g)
 {
-    return sizeof(uint32_t) * ((size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS) + (size_t)(g.G < LDS_GRID ? g.G : LDS_GRID));
+    return sizeof(uint32_t) * ((size_t)WAVES_PER_BIN * EXPAND_WORDS + (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS) +
+                               (size_t)(g.G < LDS_GRID ? g.G : LDS_GRID));
 }
 size_t scatter_regions_lds_bytes(const GeomLayout& g)
 {
-    return sizeof(float4) * 256 * WAVES_PER_BIN + sizeof(uint32_t) * (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS);
+    return sizeof(float4) * 256 * WAVES_PER_BIN +
+           sizeof(uint32_t) * ((size_t)WAVES_PER_BIN * EXPAND_WORDS + (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS));
 }
 unsigned region_lrs(const GeomLayout& g) { return g.RS == 8 ? 3u : g.RS == 4 ? 2u : 1u; }
 size_t scatter_lds_bytes(int T) { return sizeof(float4) * 256 * WAVES_PER_BIN + count_lds_bytes(T); }
@@ -3083,10 +3167,10 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     ClearRegions CR{nullptr, nullptr, nullptr, 0, 0, lrs};
     if (split)
         CR = ClearRegions{compute_locally != nullptr ? at<uint64_t>(geom, g.regmask) : nullptr,
-                          at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid), g.NR, g.G, lrs};
+                          at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid), g.NR, GRID_PARTS * g.G, lrs};
     if (gs::timing_on()) gs::timing_stage_begin(stream, BINNING_STAGE);
     if (compute_locally == nullptr) {
-        const size_t nclear = std::max<size_t>((size_t)g.T, split ? (size_t)std::max(g.G, g.NR) : 0);
+        const size_t nclear = std::max<size_t>((size_t)g.T, split ? (size_t)std::max(GRID_PARTS * g.G, g.NR) : 0);
         GS_TIMED("localmap_kernel", stream,
                  hipLaunchKernelGGL(localmap_all_kernel, dim3(gs_div_up(nclear, 256)), dim3(256), 0, stream, g.T,
                                     gx, gy, loc_map, tile_of_local, tile_count, meta, CR));
@@ -3102,14 +3186,15 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
                      hipLaunchKernelGGL(count_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), count_regions_lds_bytes(g),
                                         stream, P, g.CH, g.WS, gx, gy, lrs, reinterpret_cast<const float2*>(means2D),
                                         radii, meta, at<const uint64_t>(geom, g.regmask), at<uint32_t>(geom, g.rhist),
-                                        at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid),
+                                        at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid), g.G,
                                         at<uint32_t>(geom, g.wcount)));
             GS_LAUNCH_CHECK("count_regions_kernel");
         }
         GS_TIMED("scan_regions_kernel", stream,
                  hipLaunchKernelGGL(scan_regions_kernel, dim3(1), dim3(1024), 0, stream, meta, gx, lrs, tile_of_local,
-                                    at<uint32_t>(geom, g.grid), tile_count, tile_start, at<uint32_t>(geom, g.wcount),
-                                    P > 0 ? g.NC * WAVES_PER_BIN : 0, at<const uint32_t>(geom, g.rcount),
+                                    at<uint32_t>(geom, g.grid), g.G, tile_count, tile_start,
+                                    at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0,
+                                    at<const uint32_t>(geom, g.rcount),
                                     at<uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
                                     at<uint32_t>(geom, g.rcls_count), at<int>(geom, g.rcls_list), g.NR, cap));
         GS_LAUNCH_CHECK("scan_regions_kernel");
@@ -3173,8 +3258,9 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     uint64_t* sortkey = at<uint64_t>(binning, bl.sortkey);
 
     const unsigned T = (unsigned)g.T;
-    GS_TIMED("ranges_kernel", stream, hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, meta, loc_map, tile_count,
-                       tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
+    GS_TIMED("ranges_kernel", stream,
+             hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, meta, loc_map,
+                                tile_count, tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
     GS_LAUNCH_CHECK("ranges_kernel");
     // per-Gaussian accumulators start at zero: inside the scatter when there
     // are instances, else with a fill kernel each
@@ -3191,15 +3277,17 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     }
     if (R > 0 && !full) {
         // split path: region lists, then per region a sort and the filter
-        // into its tiles.  One launch per region size class, largest first,
-        // one after another on the caller's stream; the grids are bounded by
-        // how many regions of the class the region entries (at most R) can
-        // fill and by what fits on the chip at once.
+        // into its tiles.  One sort launch per region size class, largest
+        // first, one after another on the caller's stream; the grids are
+        // bounded by how many regions of the class the region entries (at
+        // most R) can fill and by what fits on the chip at once.
         const unsigned lrs = region_lrs(g);
         uint32_t* clist = at<uint32_t>(binning, bl.clist);
         // region lists (12 bytes per entry, at most R entries) in the point
         // list and key areas of the binning buffer (12 R bytes from point_list)
         uint3* rent = at<uint3>(binning, bl.point_list);
+        const uint32_t* rcount = at<const uint32_t>(geom, g.rcount);
+        const uint32_t* rstart = at<const uint32_t>(geom, g.rstart);
         GS_TIMED("scatter_regions_kernel", stream,
                  hipLaunchKernelGGL(scatter_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), scatter_regions_lds_bytes(g),
                                     stream, P, g.CH, g.WS, gx, gy, lrs, reinterpret_cast<const float2*>(means2D),
@@ -3211,8 +3299,6 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         GS_LAUNCH_CHECK("scatter_regions_kernel");
         const uint32_t* cc = at<const uint32_t>(geom, g.rcls_count);
         const int* cls = at<const int>(geom, g.rcls_list);
-        const uint32_t* rcount = at<const uint32_t>(geom, g.rcount);
-        const uint32_t* rstart = at<const uint32_t>(geom, g.rstart);
         const TileOut to{loc_map, tile_start, tile_count, clist, gx, gy};
         auto grid_of = [&](int lo, int cap) {
             const int64_t fit = R / (int64_t)(lo + 1);

@@ -66,7 +66,7 @@ def stage_bytes(P, P_vis, R, npx):
 
 
 BINNING_KERNELS = ("localmap_kernel", "count_regions_kernel", "scan_regions_kernel", "ranges_kernel",
-                   "scatter_regions_kernel", "regionsort_kernel_1k", "regionsort_kernel_2k", "regionsort_kernel_4k",
+                   "scatter_regions_kernel", "regionsort_small_kernel",
                    "regionsort_kernel_8k", "regionsort_kernel_12k", "regionsort_big_kernel",
                    # the full-image path's per-tile binning
                    "count_kernel", "tilescan_kernel", "scatter_kernel",

@@ -2164,10 +2164,29 @@ __device__ void sort_filter_big(uint32_t start, int n, uint3* __restrict__ rent,
     }
 }
 
+// One region: its list sorted on chip (radix_sort_items; a long run of equal
+// depths: a bitonic network in LDS) and filtered into its tiles.  The caller
+// separates consecutive regions with a barrier.
+template <int NT, int K>
+__device__ __forceinline__ void sort_filter_region(int r, const uint32_t* __restrict__ rcount,
+                                                   const uint32_t* __restrict__ rstart, const uint3* __restrict__ rent,
+                                                   RegionLds<NT, K>& L, const RegionGrid& rg, const TileOut& to,
+                                                   bool all_local)
+{
+    auto tk = [&](uint32_t y) { return L.cidx[y & 0xffffu]; };
+    const int n = (int)rcount[r];
+    const RegionTiles rt = region_tiles(rg, r);
+    uint32_t tb = ~0u, te = 0u;   // this thread's tile slot, loaded while the region sorts
+    if (threadIdx.x < (1u << (2 * rg.lrs))) tile_slot(threadIdx.x, rg.lrs, rt, to, all_local, tb, te);
+    uint32_t kor, kand;
+    region_load<NT, K>(rstart[r], n, rent, L, kor, kand);
+    if (radix_sort_items<NT, K>(n, L.R, kor, kand, tk)) lds_bitonic_items<NT, K>(n, L.R, tk);
+    filter_region<NT, K>(n, L, rt, to, rg.lrs, tb, te, nullptr);
+}
+
 // Split path, step 4: one launch per region size class; its blocks walk the
-// class's region list (block b takes entries b, b + gridDim.x, ...), sort each
-// region's list on chip (radix_sort_items; a long run of equal depths: a
-// bitonic network in LDS) and filter it into the region's tiles.
+// class's region list (block b takes entries b, b + gridDim.x, ...) and sort
+// and filter each region (sort_filter_region).
 template <int NT, int K>
 __global__ __launch_bounds__(NT) void regionsort_kernel(const uint32_t* __restrict__ cls_count,
                                                         const int* __restrict__ cls_list,
@@ -2180,18 +2199,37 @@ __global__ __launch_bounds__(NT) void regionsort_kernel(const uint32_t* __restri
     const RegionGrid rg = region_grid(meta, lrs);
     const bool all_local = meta[0] == to.gx * to.gy;
     const int nl = (int)*cls_count;
-    auto tk = [&](uint32_t y) { return L.cidx[y & 0xffffu]; };
     for (int e = blockIdx.x; e < nl; e += gridDim.x) {
         if (e != (int)blockIdx.x) __syncthreads();   // the previous region's reads of LDS are done
-        const int r = cls_list[e];
-        const int n = (int)rcount[r];
-        const RegionTiles rt = region_tiles(rg, r);
-        uint32_t tb = ~0u, te = 0u;   // this thread's tile slot, loaded while the region sorts
-        if (threadIdx.x < (1u << (2 * lrs))) tile_slot(threadIdx.x, lrs, rt, to, all_local, tb, te);
-        uint32_t kor, kand;
-        region_load<NT, K>(rstart[r], n, rent, L, kor, kand);
-        if (radix_sort_items<NT, K>(n, L.R, kor, kand, tk)) lds_bitonic_items<NT, K>(n, L.R, tk);
-        filter_region<NT, K>(n, L, rt, to, lrs, tb, te, nullptr);
+        sort_filter_region<NT, K>(cls_list[e], rcount, rstart, rent, L, rg, to, all_local);
+    }
+}
+
+// The regions of up to 4096 entries (size classes 0..2) in one launch of
+// 256-thread blocks: block b takes entries b, b + gridDim.x, ... of the class
+// lists concatenated largest class first; a list of up to 2048 entries is
+// sorted with 8 keys per thread, a longer one with 16 (the two layouts share
+// the block's LDS).
+__global__ __launch_bounds__(256, 2) void regionsort_small_kernel(const uint32_t* __restrict__ cls_count,
+                                                               const int* __restrict__ cls_list, int NR,
+                                                               const uint32_t* __restrict__ rcount,
+                                                               const uint32_t* __restrict__ rstart,
+                                                               const uint3* __restrict__ rent,
+                                                               const uint32_t* __restrict__ meta, unsigned lrs,
+                                                               TileOut to)
+{
+    static_assert(sizeof(RegionLds<256, 8>) <= sizeof(RegionLds<256, 16>), "shared layout");
+    __shared__ RegionLds<256, 16> L16;
+    RegionLds<256, 8>& L8 = *reinterpret_cast<RegionLds<256, 8>*>(&L16);
+    const RegionGrid rg = region_grid(meta, lrs);
+    const bool all_local = meta[0] == to.gx * to.gy;
+    const int n2 = (int)cls_count[2], n1 = (int)cls_count[1], n0 = (int)cls_count[0];
+    for (int e = blockIdx.x; e < n2 + n1 + n0; e += gridDim.x) {
+        if (e != (int)blockIdx.x) __syncthreads();   // the previous region's reads of LDS are done
+        const int r = e < n2 ? cls_list[2 * (size_t)NR + e]
+                             : e < n2 + n1 ? cls_list[(size_t)NR + (e - n2)] : cls_list[e - n2 - n1];
+        if (rcount[r] > 2048u) sort_filter_region<256, 16>(r, rcount, rstart, rent, L16, rg, to, all_local);
+        else sort_filter_region<256, 8>(r, rcount, rstart, rent, L8, rg, to, all_local);
     }
 }
 
@@ -3102,6 +3140,34 @@ struct Readback {
 };
 constexpr int READBACK_SLOTS = 64;
 std::mutex g_rb_mu;
+
+// A second stream per device for the region sorts of the largest lists, which
+// run beside those of the smaller ones (forked from and joined back to the
+// caller's stream with events): created once, at the default priority, never
+// destroyed.  g_side_mu is held from the fork to the join, so that forwards
+// queued from several host threads use the events one after another.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int MAX_DEVICES = 64;
+std::mutex g_side_mu;
+SideStream g_side[MAX_DEVICES];
+
+int side_stream(SideStream*& out)
+{
+    int dev = 0;
+    GS_HIP(hipGetDevice(&dev));
+    GS_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "device %d out of range", dev);
+    SideStream& ss = g_side[dev];
+    if (ss.s == nullptr) {
+        GS_HIP(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking));
+        GS_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
+        GS_HIP(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming));
+    }
+    out = &ss;
+    return GS_OK;
+}
 Readback g_rb[READBACK_SLOTS];
 
 int readback_acquire(Readback*& out)
@@ -3305,37 +3371,39 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             return (unsigned)std::min<int64_t>(std::min<int64_t>((int64_t)g.NR, fit), (int64_t)cap);
         };
         auto list = [&](int c) { return cls + (size_t)c * g.NR; };
-        const unsigned g4 = grid_of(REGION_CAP, 256), g3 = grid_of(4096, 256), g2 = grid_of(2048, 512);
-        const unsigned g1 = grid_of(1024, 1024), g0 = grid_of(0, 2048);
+        const unsigned g4 = grid_of(REGION_CAP, 256), g3 = grid_of(4096, 256), g0 = grid_of(0, 2048);
+        // the largest lists (one 512-thread block per region, one block per
+        // CU) on the side stream, beside the smaller ones on the caller's
+        std::lock_guard<std::mutex> side_lock(g_side_mu);
+        SideStream* ss = nullptr;
+        if (int rc = side_stream(ss); rc != GS_OK) return rc;
+        const bool side = g4 > 0 || g3 > 0;
+        if (side) {
+            GS_HIP(hipEventRecord(ss->fork, stream));
+            GS_HIP(hipStreamWaitEvent(ss->s, ss->fork, 0));
+        }
         if (g4 > 0) {
-            GS_TIMED("regionsort_big_kernel", stream,
-                     hipLaunchKernelGGL((regionsort_big_kernel<512, 16>), dim3(g4), dim3(512), 0, stream, cc + 4,
+            GS_TIMED("regionsort_big_kernel", ss->s,
+                     hipLaunchKernelGGL((regionsort_big_kernel<512, 16>), dim3(g4), dim3(512), 0, ss->s, cc + 4,
                                         list(4), rcount, rstart, rent, meta, lrs, to));
             GS_LAUNCH_CHECK("regionsort_big_kernel");
         }
         if (g3 > 0) {
-            GS_TIMED("regionsort_kernel_8k", stream,
-                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, stream, cc + 3,
+            GS_TIMED("regionsort_kernel_8k", ss->s,
+                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, ss->s, cc + 3,
                                         list(3), rcount, rstart, rent, meta, lrs, to));
             GS_LAUNCH_CHECK("regionsort_kernel_8k");
         }
-        if (g2 > 0) {
-            GS_TIMED("regionsort_kernel_4k", stream,
-                     hipLaunchKernelGGL((regionsort_kernel<256, 16>), dim3(g2), dim3(256), 0, stream, cc + 2,
-                                        list(2), rcount, rstart, rent, meta, lrs, to));
-            GS_LAUNCH_CHECK("regionsort_kernel_4k");
+        const unsigned gs = std::min<unsigned>(g0, 512u);
+        if (gs > 0) {
+            GS_TIMED("regionsort_small_kernel", stream,
+                     hipLaunchKernelGGL(regionsort_small_kernel, dim3(gs), dim3(256), 0, stream, cc, cls, g.NR, rcount,
+                                        rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_small_kernel");
         }
-        if (g1 > 0) {
-            GS_TIMED("regionsort_kernel_2k", stream,
-                     hipLaunchKernelGGL((regionsort_kernel<256, 8>), dim3(g1), dim3(256), 0, stream, cc + 1,
-                                        list(1), rcount, rstart, rent, meta, lrs, to));
-            GS_LAUNCH_CHECK("regionsort_kernel_2k");
-        }
-        if (g0 > 0) {
-            GS_TIMED("regionsort_kernel_1k", stream,
-                     hipLaunchKernelGGL((regionsort_kernel<128, 8>), dim3(g0), dim3(128), 0, stream, cc + 0,
-                                        list(0), rcount, rstart, rent, meta, lrs, to));
-            GS_LAUNCH_CHECK("regionsort_kernel_1k");
+        if (side) {
+            GS_HIP(hipEventRecord(ss->join, ss->s));
+            GS_HIP(hipStreamWaitEvent(stream, ss->join, 0));
         }
     }
     if (R > 0 && full) {

@@ -42,10 +42,21 @@ STEP_METRIC = "rasterizer fwd+bwd ms/iter & Gaussians/s at 6M SH3 1600x1066; % H
 
 
 # algorithmic bytes per unit of work, per stage (the scope table's per-unit figures)
-def stage_bytes(P, P_vis, R, npx):
+def stage_bytes(P, P_vis, R, npx, E=None):
     """Algorithmic HBM bytes per launch (per step for binning and other): P
     Gaussians, P_vis of them visible (radius > 0; the listed ones, which touch
-    a tile, are counted as P_vis), R tile instances, npx pixels."""
+    a tile, are counted as P_vis), R tile instances, npx pixels, E region-list
+    entries of the split path's binning (region_entries; None: the full-image
+    path's per-tile binning)."""
+    if E is None:
+        # count: radius + means2D of all (12 B); scatter: the same again, compact index and out_observe (8 B)
+        # of all, depth/conic/rgb (32 B) of the listed, their 64-byte record and id (68 B); per instance the
+        # key written and read back (16 B) and the compact list written (4 B)
+        binning = 32 * P + 100 * P_vis + 20 * R
+    else:
+        # count and scatter as above; per region-list entry 12 B written and read back, per instance the
+        # compact list written (4 B)
+        binning = 32 * P + 100 * P_vis + 24 * E + 4 * R
     return {
         # reads means3D, scales, rotations, opacity (44 B) of all, SH (192 B) of the visible; writes means2D,
         # depth, radius, conic+opacity, rgb, clamped (47 B) of all (cov3D is recomputed by the backward)
@@ -53,10 +64,7 @@ def stage_bytes(P, P_vis, R, npx):
         # writes the five gradients (236 B) and reads radius (4 B) of all; reads means3D, scales, rotations,
         # clamped, the three incoming gradients and SH (271 B) of the visible
         "preprocess_bwd_kernel": 240 * P + 271 * P_vis,
-        # count: radius + means2D of all (12 B); scatter: the same again, compact index and out_observe (8 B)
-        # of all, depth/conic/rgb (32 B) of the listed, their 64-byte record and id (68 B); per instance the
-        # key written and read back (16 B) and the compact list written (4 B)
-        "binning": 32 * P + 100 * P_vis + 20 * R,
+        "binning": binning,
         "render_fwd_kernel": 40 * R + 24 * npx,
         "render_bwd_kernel": 40 * R + 32 * npx,
         # the accumulators cleared (64 B per listed), then the gradient unpack: compact index of all (4 B),
@@ -67,7 +75,7 @@ def stage_bytes(P, P_vis, R, npx):
 
 BINNING_KERNELS = ("localmap_kernel", "count_regions_kernel", "scan_regions_kernel", "ranges_kernel",
                    "scatter_regions_kernel", "regionsort_small_kernel",
-                   "regionsort_kernel_8k", "regionsort_kernel_12k", "regionsort_big_kernel",
+                   "regionsort_kernel_8k", "regionsort_big_kernel",
                    # the full-image path's per-tile binning
                    "count_kernel", "tilescan_kernel", "scatter_kernel",
                    "tilesort_kernel_1k", "tilesort_kernel_2k", "tilesort_kernel_4k", "tilesort_kernel_8k")
@@ -75,6 +83,36 @@ BINNING_KERNELS = ("localmap_kernel", "count_regions_kernel", "scan_regions_kern
 # (first binning kernel -> end of the sorts)
 BINNING_STAGE = "binning (wall)"
 STEP_STAGES = ("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel")
+
+
+def region_entries(means2D, radii, W, H, cl=None):
+    """Entries of the split path's region lists: per listed Gaussian, the
+    RS x RS-tile regions (RS = 2, or 4 / 8 when 2 gives more than 16384
+    regions) that its tile rect, clipped to the box of the local tiles, meets,
+    regions tiling the box from its corner.  Exact when the local tiles fill
+    their box (no mask, or whole tile rows / columns), an upper bound
+    otherwise."""
+    import torch
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    rs = next((s for s in (2, 4, 8) if ((gx + s - 1) // s) * ((gy + s - 1) // s) <= 16384), 8)
+    bx0, by0, bx1, by1 = 0, 0, gx, gy
+    if cl is not None:
+        cols = torch.nonzero(cl.reshape(gy, gx).any(0)).flatten()
+        rows = torch.nonzero(cl.reshape(gy, gx).any(1)).flatten()
+        if cols.numel() == 0:
+            return 0
+        bx0, bx1, by0, by1 = int(cols[0]), int(cols[-1]) + 1, int(rows[0]), int(rows[-1]) + 1
+    r = radii.float()
+    m = means2D.detach().float()
+    tile = lambda v, n: torch.nan_to_num(torch.trunc(v / 16.0), nan=0.0).clamp(0, n).long()
+    x0 = tile(m[:, 0] - r, gx).clamp(bx0, bx1)
+    y0 = tile(m[:, 1] - r, gy).clamp(by0, by1)
+    x1 = tile(m[:, 0] + r + 15.0, gx).clamp(bx0, bx1)
+    y1 = tile(m[:, 1] + r + 15.0, gy).clamp(by0, by1)
+    ok = (radii > 0) & (x1 > x0) & (y1 > y0)
+    nx = torch.div(x1 - 1 - bx0, rs, rounding_mode="floor") - torch.div(x0 - bx0, rs, rounding_mode="floor") + 1
+    ny = torch.div(y1 - 1 - by0, rs, rounding_mode="floor") - torch.div(y0 - by0, rs, rounding_mode="floor") + 1
+    return int(torch.where(ok, nx * ny, torch.zeros_like(nx)).sum().item())
 
 
 def parse():
@@ -168,7 +206,21 @@ def timed(fn, steps, warmup):
     torch.cuda.synchronize()
     _lib.timing_enable(False)
     kt = _lib.timing_read()
-    return ms, kt, ev0.elapsed_time(ev1) / steps
+    ms_instr = ev0.elapsed_time(ev1) / steps
+    if BINNING_STAGE in kt:
+        # the binning's wall time again, with the stage marks alone (per-kernel
+        # events add a gap between the stage's launches)
+        _lib.timing_reset()
+        _lib.timing_enable(True, stages_only=True)
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        _lib.timing_enable(False)
+        ks = _lib.timing_read()
+        if BINNING_STAGE in ks:
+            kt[BINNING_STAGE + " with kernel events"] = kt[BINNING_STAGE]
+            kt[BINNING_STAGE] = ks[BINNING_STAGE]
+    return ms, kt, ms_instr
 
 
 def valu_peak(iters=2000, reps=5):
@@ -314,6 +366,7 @@ def run_step(args):
             loss = 0.8 * (color - target).abs().mean() + 0.2 * (1.0 - fused_ssim(color[None], target[None]))
             loss.backward()
         info["radii"] = radii
+        info["means2D"] = means2D
         info["n_render"] = n_render
         info["n_consider"] = n_consider
 
@@ -330,8 +383,9 @@ def run_step(args):
     stages["binning"] = per_kernel.get(BINNING_STAGE, binning_kernels_ms)
     avg_launch["binning"] = avg_launch.get(BINNING_STAGE, binning_kernels_ms)
     stages["other"] = sum(v for k, v in per_kernel.items()
-                          if k not in stages and k not in BINNING_KERNELS and k != BINNING_STAGE)
-    sb = stage_bytes(P, P_vis, R, W * H)
+                          if k not in stages and k not in BINNING_KERNELS and not k.startswith(BINNING_STAGE))
+    E_reg = region_entries(info["means2D"], info["radii"], W, H, cl)
+    sb = stage_bytes(P, P_vis, R, W * H, E_reg)
     stage_rows = {}
     for k, ms in stages.items():
         gbs = sb[k] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
@@ -369,12 +423,17 @@ def run_step(args):
     metric = STEP_METRIC if args.config == 2 else f"rasterizer fwd+bwd ms/iter & Gaussians/s, config {args.config}"
     out = header(args, metric, P / (ms_per_step * 1e-3), "Gaussians/s", ms_per_step, "f32",
                  f"config{args.config}: {P} Gaussians SH3, {W}x{H}, fwd+bwd",
-                 {"gaussians": P, "visible": P_vis, "instances": R, "image": [W, H], "tiles": T,
+                 {"gaussians": P, "visible": P_vis, "instances": R, "region_entries": E_reg, "image": [W, H],
+                  "tiles": T,
                   "local_tiles": int(cl.sum().item()) if cl is not None else T, "loss": loss_desc})
     out["stages_ms"] = stage_rows
     out["stages_note"] = ("per-kernel HIP-event times; `binning` is the wall time of the whole stage on the caller's "
-                          "stream (its kernels overlap on side streams; their summed times are binning_kernels_ms)")
+                          "stream, timed in a run with only the stage's two marks (its kernels overlap on a side "
+                          "stream; their summed times are binning_kernels_ms; binning_wall_with_kernel_events_ms is "
+                          "the same wall in the run with an event pair around every kernel)")
     out["binning_kernels_ms"] = round(binning_kernels_ms, 4)
+    if BINNING_STAGE + " with kernel events" in per_kernel:
+        out["binning_wall_with_kernel_events_ms"] = round(per_kernel[BINNING_STAGE + " with kernel events"], 4)
     out["ms_per_step_with_kernel_events"] = round(ms_instr, 4)
     out["render_fwd_evaluations"] = E
     out["hbm_copy_GBs"] = round(peak_copy, 1)

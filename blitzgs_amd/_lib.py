@@ -144,8 +144,12 @@ def stream_of(device=None):
     return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def timing_enable(on=True):
-    load().gs_timing_enable(1 if on else 0)
+def timing_enable(on=True, stages_only=False):
+    """on: time every kernel launch and the stages (stages_only: the stages
+    alone, without per-kernel events in the way); off: nothing."""
+    rc = load().gs_timing_enable((2 if stages_only else 1) if on else 0)
+    if rc != 0:
+        raise RuntimeError(f"gs_timing_enable failed ({rc})")
 
 
 def timing_reset():

@@ -37,7 +37,7 @@ struct PendingMark {
 };
 struct TimingState {
     std::mutex mu;
-    bool on = false;
+    int on = 0;   // 0 off, 1 every kernel and the stages, 2 the stages only
     std::vector<hipEvent_t> pool;
     std::vector<PendingMark> pending;
     std::vector<PendingMark> open_stages;   // stages begun and not yet ended
@@ -81,7 +81,8 @@ void drain(TimingState& t)
 }  // namespace
 
 namespace gs {
-bool timing_on() { return timing().on; }
+bool timing_on() { return timing().on != 0; }
+bool timing_kernels_on() { return timing().on == 1; }
 void timing_mark_begin(hipStream_t stream, const char* name)
 {
     TimingState& t = timing();
@@ -127,7 +128,11 @@ extern "C" int gs_timing_enable(int on)
 {
     TimingState& t = timing();
     std::lock_guard<std::mutex> lk(t.mu);
-    t.on = on != 0;
+    if (on < 0 || on > 2) {
+        gs::set_error("timing mode must be 0, 1 or 2 (got %d)", on);
+        return GS_ERR_ARG;
+    }
+    t.on = on;
     return GS_OK;
 }
 

@@ -10,10 +10,12 @@ namespace gs {
 void set_error(const char* fmt, ...);
 void clear_error();
 
-// Optional per-kernel timing (gs_timing_enable): when on, every launch made
+// Optional per-kernel timing (gs_timing_enable): in mode 1 every launch made
 // through GS_TIMED is bracketed by HIP events on its stream and the elapsed
-// times are accumulated per kernel name by gs_timing_read.
-bool timing_on();
+// times are accumulated per kernel name by gs_timing_read; stages (below) are
+// timed in modes 1 and 2.
+bool timing_on();          // mode 1 or 2: stage marks
+bool timing_kernels_on();  // mode 1: per-launch marks
 void timing_mark_begin(hipStream_t stream, const char* name);
 void timing_mark_end(hipStream_t stream);
 // A named stage spanning several launches (and entry points) on one stream:
@@ -26,7 +28,7 @@ int render_valu_probe(int which, int iters, float* y, hipStream_t stream);
 
 #define GS_TIMED(name, stream, launch)                                                 \
     do {                                                                               \
-        const bool gs_t_ = gs::timing_on();                                            \
+        const bool gs_t_ = gs::timing_kernels_on();                                    \
         if (gs_t_) gs::timing_mark_begin(stream, name);                                \
         launch;                                                                        \
         if (gs_t_) gs::timing_mark_end(stream);                                        \

@@ -66,7 +66,7 @@ constexpr int WAVES_PER_BIN = BIN_THREADS / 64;
 constexpr int MAX_CHUNKS = 512;
 constexpr int SORT_CAP_MAX = 8192;   // largest bucket sorted on chip (8 keys per thread, 1024 threads)
 constexpr int SORT_CLASSES = 6;      // bucket size classes: <= 512, 1k, 2k, 4k, 8k keys, larger
-// Regions of the split path: RS x RS-tile blocks (RS = 4, or 8 for very
+// Regions of the split path: RS x RS-tile blocks (RS = 2, or 4 / 8 for very
 // large tile grids) tiling the local-tile box from its corner.
 constexpr int REGION_SIDE = 2;       // preferred region side (tiles)
 constexpr int MAX_REGIONS = 16384;   // regions of the full tile grid
@@ -103,8 +103,8 @@ struct GeomLayout {
     size_t total;
 };
 
-// region side for a gx x gy tile grid: 4, or 8 when 4 would give more than
-// MAX_REGIONS regions; 0 when 8 does too
+// region side for a gx x gy tile grid: the smallest of REGION_SIDE, 4 and 8
+// that gives at most MAX_REGIONS regions; 0 when 8 does not
 inline int region_side(int gx, int gy)
 {
     for (int rs = REGION_SIDE; rs <= 8; rs *= 2)
@@ -802,12 +802,14 @@ __device__ __forceinline__ int sort_class(uint32_t n)
 // cap: the instance capacity of the caller's binning buffer.  When R exceeds
 // it, meta[9] is set and the class lists are left empty: the ranges, the
 // scatter and the sorts then do nothing (the caller redoes the forward with a
-// buffer for R).
+// buffer for R).  host_R (device address of mapped, coherent pinned host
+// memory, or null): R is also stored there, for the host to read once the
+// kernel is done.
 __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ meta, const uint32_t* __restrict__ tile_count,
                                                         uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
                                                         uint32_t* __restrict__ wcount, int NW, int T,
                                                         uint32_t* __restrict__ cls_count, int* __restrict__ cls_list,
-                                                        uint64_t cap)
+                                                        uint64_t cap, uint32_t* __restrict__ host_R)
 {
     __shared__ uint32_t s_wave[32];
     __shared__ uint32_t s_cls[SORT_CLASSES];
@@ -849,28 +851,43 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
         meta[2] = (uint32_t)(base & 0xffffffffu);
         meta[3] = (uint32_t)(base >> 32);
         meta[9] = over ? 1u : 0u;
+        if (host_R != nullptr) {
+            host_R[0] = (uint32_t)(base & 0xffffffffu);
+            host_R[1] = (uint32_t)(base >> 32);
+        }
     }
 }
 
 // per tile: ranges, n_render; clears the per-tile blend statistics (all
 // ranges empty when R exceeded the caller's capacity)
-__global__ __launch_bounds__(256) void ranges_kernel(int T, const uint32_t* __restrict__ meta, const int* __restrict__ loc_map,
-                                                     const uint32_t* __restrict__ tile_count,
-                                                     const uint32_t* __restrict__ tile_start, uint2* __restrict__ ranges,
-                                                     int32_t* __restrict__ n_render, int32_t* __restrict__ n_consider,
-                                                     int32_t* __restrict__ n_contrib)
+struct RangesOut {
+    int T;
+    const int* loc_map;
+    const uint32_t* tile_count;
+    const uint32_t* tile_start;
+    uint2* ranges;
+    int32_t* n_render;     // null: the full-image path (no per-tile statistics)
+    int32_t* n_consider;
+    int32_t* n_contrib;
+
+    __device__ __forceinline__ void tile(int t, bool over) const
+    {
+        const int l = loc_map[t];
+        uint32_t cnt = 0, s = 0;
+        if (l >= 0 && !over) { cnt = tile_count[l]; s = tile_start[l]; }
+        ranges[t] = cnt ? make_uint2(s, s + cnt) : make_uint2(0u, 0u);
+        if (n_render != nullptr) {
+            n_render[t] = (int32_t)cnt;
+            n_consider[t] = 0;
+            n_contrib[t] = 0;
+        }
+    }
+};
+
+__global__ __launch_bounds__(256) void ranges_kernel(const uint32_t* __restrict__ meta, RangesOut ro)
 {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const int l = loc_map[t];
-    uint32_t cnt = 0, s = 0;
-    if (l >= 0 && meta[9] == 0u) { cnt = tile_count[l]; s = tile_start[l]; }
-    ranges[t] = cnt ? make_uint2(s, s + cnt) : make_uint2(0u, 0u);
-    if (n_render != nullptr) {   // the split path's per-tile statistics
-        n_render[t] = (int32_t)cnt;
-        n_consider[t] = 0;
-        n_contrib[t] = 0;
-    }
+    if (t < ro.T) ro.tile(t, meta[9] != 0u);
 }
 
 // ------------------------------------------------------------- scatter
@@ -1009,16 +1026,19 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_kernel(
 // region list it enters (LDS cursors; global cursors beyond LDS_REGIONS
 // regions).  Every Gaussian gets its compact index or -1 (cidx_of); listed
 // ones also get their blend record and id (cid2id) and their accumulators
-// zeroed, as in scatter_kernel.
+// zeroed, as in scatter_kernel.  The blocks also write the tiles' ranges
+// (ranges_kernel's work; tiles t = block * 512 + thread, strided by the grid).
 __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
     int P, int CH, int WS, unsigned gx, unsigned gy, unsigned lrs, const float2* __restrict__ means2D,
     const float* __restrict__ depths, const int* __restrict__ radii, const float4* __restrict__ conic_opacity,
     const float* __restrict__ rgb, const uint32_t* __restrict__ meta, const uint64_t* __restrict__ regmask,
     const uint32_t* __restrict__ rhist, const uint32_t* __restrict__ rstart, uint32_t* __restrict__ rcursor,
     const uint32_t* __restrict__ wbase, uint3* __restrict__ rent, int* __restrict__ cidx_of,
-    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, ZeroOut Z)
+    uint32_t* __restrict__ cid2id, float4* __restrict__ rec, ZeroOut Z, RangesOut ro)
 {
-    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: nothing to write
+    const bool over = meta[9] != 0u;
+    for (int t = blockIdx.x * BIN_THREADS + threadIdx.x; t < ro.T; t += gridDim.x * BIN_THREADS) ro.tile(t, over);
+    if (over) return;   // R exceeded the caller's capacity: nothing to write
     // dynamic LDS: per wave 64 staged records, then min(NR, LDS_REGIONS) cursors
     extern __shared__ uint4 s_dyn[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1599,7 +1619,7 @@ __device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Get
 //     R -> meta[2..3];
 //   - the region list lengths -> offsets (rstart, and rcursor for the global
 //     cursors) and per-class region lists; the total -> meta[10].
-// cap: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
+// cap, host_R: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
 __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict__ meta, unsigned gx, unsigned lrs,
                                                             const int* __restrict__ tile_of_local,
                                                             uint32_t* __restrict__ grid, int Gfull,
@@ -1610,7 +1630,8 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
                                                             uint32_t* __restrict__ rstart,
                                                             uint32_t* __restrict__ rcursor,
                                                             uint32_t* __restrict__ rcls_count,
-                                                            int* __restrict__ rcls_list, int NR, uint64_t cap)
+                                                            int* __restrict__ rcls_list, int NR, uint64_t cap,
+                                                            uint32_t* __restrict__ host_R)
 {
     __shared__ uint32_t s_grid[LDS_GRID];
     __shared__ uint32_t s_wave[32];
@@ -1702,6 +1723,10 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
         meta[3] = (uint32_t)(R >> 32);
         meta[9] = over ? 1u : 0u;
         meta[10] = (uint32_t)E;
+        if (host_R != nullptr) {
+            host_R[0] = (uint32_t)(R & 0xffffffffu);
+            host_R[1] = (uint32_t)(R >> 32);
+        }
     }
 }
 
@@ -1854,7 +1879,7 @@ __device__ __forceinline__ void copy_out(uint32_t* __restrict__ dst, const uint3
 }
 
 // Filters the n sorted items into the region's local tiles, in order, four
-// tiles of a row at a time.  Wave w holds items [w c, w c + c) in registers
+// tiles at a time (row-major).  Wave w holds items [w c, w c + c) in registers
 // (c = n / (NT/64) rounded up to 64, at most 64 K), 64 per step.  Per pass:
 // each wave counts, per tile, its items whose mask holds the tile (one ballot
 // per step and tile); 4 threads turn the counts into each wave's offset in
@@ -1892,9 +1917,19 @@ __device__ void filter_region(int n, RegionLds<NT, K>& L, const RegionTiles& rt,
     }
     __syncthreads();   // every wave holds its items: item slots and counters are staging space
     uint32_t* stage = reinterpret_cast<uint32_t*>(L.R.items);
-    // a row's tiles four at a time (RS = 8: two passes per row)
-    for (unsigned jy = 0; jy < rt.th; jy++) {
-        for (unsigned x0 = 0; x0 < rt.tw; x0 += 4) {
+    // the region's tiles four at a time in row-major order (RS = 2: the whole
+    // region in one pass; RS = 4: a row per pass; RS = 8: half a row)
+    for (unsigned j0 = 0; j0 < rs * rs; j0 += 4) {
+        {
+            // tile j0 + q: column j & (RS - 1), row j >> lrs; bits: its mask test
+            uint32_t bits[4];
+            bool tin[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const unsigned j = j0 + (unsigned)q, jx = j & (rs - 1u), jy = j >> lrs;
+                tin[q] = jx < rt.tw && jy < rt.th;
+                bits[q] = (1u << jx) | (1u << (8 + jy));
+            }
             uint32_t cnt[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) cnt[q] = 0u;
@@ -1903,10 +1938,7 @@ __device__ void filter_region(int n, RegionLds<NT, K>& L, const RegionTiles& rt,
                 if (k < steps) {
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        if (x0 + (unsigned)q < rt.tw) {
-                            const uint32_t bits = (1u << (x0 + q)) | (1u << (8 + jy));
-                            cnt[q] += (uint32_t)__builtin_popcountll(gs::ballot((pm[k] & bits) == bits));
-                        }
+                        if (tin[q]) cnt[q] += (uint32_t)__builtin_popcountll(gs::ballot((pm[k] & bits[q]) == bits[q]));
                     }
                 }
             }
@@ -1916,9 +1948,9 @@ __device__ void filter_region(int n, RegionLds<NT, K>& L, const RegionTiles& rt,
             }
             __syncthreads();
             if (threadIdx.x < 4) {
-                const unsigned q = threadIdx.x, j = (jy << lrs) + x0 + q;
+                const unsigned q = threadIdx.x, j = j0 + q;
                 uint32_t b = ~0u, e = 0u;
-                if (x0 + q < rt.tw) {
+                if ((j & (rs - 1u)) < rt.tw && (j >> lrs) < rt.th) {
                     b = L.tslot[2 * j];
                     e = L.tslot[2 * j + 1];
                 }
@@ -1954,8 +1986,7 @@ __device__ void filter_region(int n, RegionLds<NT, K>& L, const RegionTiles& rt,
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         if (gq[q] == ~0u) continue;
-                        const uint32_t bits = (1u << (x0 + q)) | (1u << (8 + jy));
-                        const bool hit = (pm[k] & bits) == bits;
+                        const bool hit = (pm[k] & bits[q]) == bits[q];
                         const uint64_t m = gs::ballot(hit);
                         if (hit) {
                             const uint32_t p = pos[q] + (uint32_t)gs::rank_below(m);
@@ -3133,22 +3164,24 @@ namespace {
 // forward copies R there and records the slot's event, and waits for that
 // event only after the rest of the forward is queued.
 struct Readback {
-    uint32_t* host = nullptr;
+    uint32_t* host = nullptr;   // mapped, coherent pinned memory: the scan kernel stores R here
+    uint32_t* dev = nullptr;    // its device address
     hipEvent_t ev = nullptr;
-    int dev = -1;
+    int device = -1;
     bool busy = false;
 };
 constexpr int READBACK_SLOTS = 64;
 std::mutex g_rb_mu;
 
-// A second stream per device for the region sorts of the largest lists, which
-// run beside those of the smaller ones (forked from and joined back to the
-// caller's stream with events): created once, at the default priority, never
-// destroyed.  g_side_mu is held from the fork to the join, so that forwards
-// queued from several host threads use the events one after another.
+// Two more streams per device for the region sorts of the largest lists
+// (one per size class), which run beside those of the smaller ones (forked
+// from and joined back to the caller's stream with events): created once, at
+// the default priority, never destroyed.  g_side_mu is held from the fork to
+// the join, so that forwards queued from several host threads use the events
+// one after another.
 struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
+    hipStream_t s[2] = {nullptr, nullptr};
+    hipEvent_t fork = nullptr, join[2] = {nullptr, nullptr};
 };
 constexpr int MAX_DEVICES = 64;
 std::mutex g_side_mu;
@@ -3160,10 +3193,12 @@ int side_stream(SideStream*& out)
     GS_HIP(hipGetDevice(&dev));
     GS_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "device %d out of range", dev);
     SideStream& ss = g_side[dev];
-    if (ss.s == nullptr) {
-        GS_HIP(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking));
+    if (ss.fork == nullptr) {
+        for (int k = 0; k < 2; k++) {
+            GS_HIP(hipStreamCreateWithFlags(&ss.s[k], hipStreamNonBlocking));
+            GS_HIP(hipEventCreateWithFlags(&ss.join[k], hipEventDisableTiming));
+        }
         GS_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
-        GS_HIP(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming));
     }
     out = &ss;
     return GS_OK;
@@ -3177,11 +3212,13 @@ int readback_acquire(Readback*& out)
     GS_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_rb_mu);
     for (Readback& r : g_rb) {
-        if (r.busy || (r.dev >= 0 && r.dev != dev)) continue;
-        if (r.dev < 0) {
-            GS_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 2 * sizeof(uint32_t), hipHostMallocDefault));
+        if (r.busy || (r.device >= 0 && r.device != dev)) continue;
+        if (r.device < 0) {
+            GS_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 2 * sizeof(uint32_t),
+                                 hipHostMallocMapped | hipHostMallocCoherent));
+            GS_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&r.dev), r.host, 0));
             GS_HIP(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
-            r.dev = dev;
+            r.device = dev;
         }
         r.busy = true;
         out = &r;
@@ -3262,7 +3299,8 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
                                     at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0,
                                     at<const uint32_t>(geom, g.rcount),
                                     at<uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
-                                    at<uint32_t>(geom, g.rcls_count), at<int>(geom, g.rcls_list), g.NR, cap));
+                                    at<uint32_t>(geom, g.rcls_count), at<int>(geom, g.rcls_list), g.NR, cap,
+                                    rb != nullptr ? rb->dev : nullptr));
         GS_LAUNCH_CHECK("scan_regions_kernel");
     }
     if (!split && P > 0) {
@@ -3278,11 +3316,12 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
         GS_TIMED("tilescan_kernel", stream,
                  hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
                                     at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
-                                    at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap));
+                                    at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap,
+                                    rb != nullptr ? rb->dev : nullptr));
         GS_LAUNCH_CHECK("tilescan_kernel");
     }
     if (rb != nullptr) {
-        GS_HIP(hipMemcpyAsync(rb->host, meta + 2, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+        // the scan stored R into rb->host; the event marks the end of the scan
         GS_HIP(hipEventRecord(rb->ev, stream));
         return GS_OK;
     }
@@ -3324,10 +3363,12 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     uint64_t* sortkey = at<uint64_t>(binning, bl.sortkey);
 
     const unsigned T = (unsigned)g.T;
-    GS_TIMED("ranges_kernel", stream,
-             hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, g.T, meta, loc_map,
-                                tile_count, tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile));
-    GS_LAUNCH_CHECK("ranges_kernel");
+    const RangesOut ro{g.T, loc_map, tile_count, tile_start, ranges, n_render, O.n_consider, O.n_contrib_tile};
+    if (R == 0 || full) {   // the split path's scatter writes the ranges itself
+        GS_TIMED("ranges_kernel", stream,
+                 hipLaunchKernelGGL(ranges_kernel, dim3(gs_div_up(T, 256)), dim3(256), 0, stream, meta, ro));
+        GS_LAUNCH_CHECK("ranges_kernel");
+    }
     // per-Gaussian accumulators start at zero: inside the scatter when there
     // are instances, else with a fill kernel each
     ZeroOut Z{{mode == BLEND_SPLIT ? O.out_observe : nullptr, reinterpret_cast<int32_t*>(O.accum_max_count),
@@ -3361,7 +3402,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
                                     at<const uint64_t>(geom, g.regmask), at<const uint32_t>(geom, g.rhist),
                                     at<const uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
                                     at<const uint32_t>(geom, g.wcount), rent, at<int>(geom, g.cidx_of),
-                                    at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec), Z));
+                                    at<uint32_t>(geom, g.cid2id), at<float4>(geom, g.rec), Z, ro));
         GS_LAUNCH_CHECK("scatter_regions_kernel");
         const uint32_t* cc = at<const uint32_t>(geom, g.rcls_count);
         const int* cls = at<const int>(geom, g.rcls_list);
@@ -3373,26 +3414,27 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         auto list = [&](int c) { return cls + (size_t)c * g.NR; };
         const unsigned g4 = grid_of(REGION_CAP, 256), g3 = grid_of(4096, 256), g0 = grid_of(0, 2048);
         // the largest lists (one 512-thread block per region, one block per
-        // CU) on the side stream, beside the smaller ones on the caller's
+        // CU) on the side streams, one per class, beside the smaller ones on
+        // the caller's
         std::lock_guard<std::mutex> side_lock(g_side_mu);
         SideStream* ss = nullptr;
         if (int rc = side_stream(ss); rc != GS_OK) return rc;
-        const bool side = g4 > 0 || g3 > 0;
-        if (side) {
-            GS_HIP(hipEventRecord(ss->fork, stream));
-            GS_HIP(hipStreamWaitEvent(ss->s, ss->fork, 0));
-        }
+        if (g4 > 0 || g3 > 0) GS_HIP(hipEventRecord(ss->fork, stream));
         if (g4 > 0) {
-            GS_TIMED("regionsort_big_kernel", ss->s,
-                     hipLaunchKernelGGL((regionsort_big_kernel<512, 16>), dim3(g4), dim3(512), 0, ss->s, cc + 4,
+            GS_HIP(hipStreamWaitEvent(ss->s[0], ss->fork, 0));
+            GS_TIMED("regionsort_big_kernel", ss->s[0],
+                     hipLaunchKernelGGL((regionsort_big_kernel<512, 16>), dim3(g4), dim3(512), 0, ss->s[0], cc + 4,
                                         list(4), rcount, rstart, rent, meta, lrs, to));
             GS_LAUNCH_CHECK("regionsort_big_kernel");
+            GS_HIP(hipEventRecord(ss->join[0], ss->s[0]));
         }
         if (g3 > 0) {
-            GS_TIMED("regionsort_kernel_8k", ss->s,
-                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, ss->s, cc + 3,
+            GS_HIP(hipStreamWaitEvent(ss->s[1], ss->fork, 0));
+            GS_TIMED("regionsort_kernel_8k", ss->s[1],
+                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, ss->s[1], cc + 3,
                                         list(3), rcount, rstart, rent, meta, lrs, to));
             GS_LAUNCH_CHECK("regionsort_kernel_8k");
+            GS_HIP(hipEventRecord(ss->join[1], ss->s[1]));
         }
         const unsigned gs = std::min<unsigned>(g0, 512u);
         if (gs > 0) {
@@ -3401,10 +3443,8 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
                                         rstart, rent, meta, lrs, to));
             GS_LAUNCH_CHECK("regionsort_small_kernel");
         }
-        if (side) {
-            GS_HIP(hipEventRecord(ss->join, ss->s));
-            GS_HIP(hipStreamWaitEvent(stream, ss->join, 0));
-        }
+        if (g4 > 0) GS_HIP(hipStreamWaitEvent(stream, ss->join[0], 0));
+        if (g3 > 0) GS_HIP(hipStreamWaitEvent(stream, ss->join[1], 0));
     }
     if (R > 0 && full) {
         const float2* m2 = reinterpret_cast<const float2*>(means2D);

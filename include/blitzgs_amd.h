@@ -107,18 +107,24 @@ size_t gs_render_geom_bytes(int P, int image_width, int image_height);
 size_t gs_render_binning_bytes(int64_t R);
 size_t gs_render_img_bytes(int image_width, int image_height);
 
-/* Count the tile instances: per-tile counts and offsets go to `geom`; R is
- * copied to *num_rendered.  Synchronises `stream` (the reference reads R back
- * with cudaMemcpy at rasterizer_impl.cu:621). */
+/* Count the tile instances: per-tile counts and offsets (and, for the
+ * sorts, per-region list lengths and offsets over 2x2-tile regions) go to
+ * `geom`; R is copied to *num_rendered.  Synchronises `stream` (the
+ * reference reads R back with cudaMemcpy at rasterizer_impl.cu:621). */
 int gs_render_forward_count(int P, int image_width, int image_height, const float* means2D,
                             const int* radii, const uint8_t* compute_locally, void* geom,
                             int64_t* num_rendered, gs_stream_t stream);
 
 /* Duplicate, sort, range and blend.  Outputs: out_color (3,H,W),
  * n_render / n_consider / n_contrib int32 (tiles), out_observe int32 (P).
- * The sorted tile|depth keys and Gaussian ids stay in `binning`, the ranges
- * and per-pixel state in `img`, and a packed 64-byte copy of each listed
- * Gaussian's means2D / conic_opacity / rgb in `geom`, for gs_render_backward. */
+ * The per-tile sorted lists (compact Gaussian indices) stay in `binning`
+ * (gs_render_point_list turns them into the reference's point list and
+ * keys), the ranges and per-pixel state in `img`, and a packed 64-byte copy
+ * of each listed Gaussian's means2D / conic_opacity / rgb in `geom`, for
+ * gs_render_backward.  The sorts of the longest lists run on a second stream
+ * of the library's (one per device, default priority), forked from `stream`
+ * and joined back to it with events: work queued on `stream` afterwards sees
+ * every result. */
 int gs_render_forward(int P, int64_t R, int image_width, int image_height, const float* bg,
                       const float* means2D, const float* depths, const int* radii,
                       const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
@@ -462,9 +468,10 @@ int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Per-kernel timing (the counterpart of the reference's MyTimerOnGPU,
- * diff-gaussian-rasterization_r/cuda_rasterizer/timers.cu:11-79): when
- * enabled, every kernel launch is bracketed by HIP events on its stream.
- * gs_timing_read synchronises on the recorded events and returns, per kernel
+ * diff-gaussian-rasterization_r/cuda_rasterizer/timers.cu:11-79).  on = 1:
+ * every kernel launch is bracketed by HIP events on its stream, and so are
+ * the stages; on = 2: only the stages (so that their wall times carry no
+ * per-kernel event overhead); on = 0: off.  gs_timing_read synchronises on the recorded events and returns, per kernel
  * name (64-byte slots in `names`), the summed milliseconds and launch count;
  * the return value is the number of distinct kernels.  One entry is a stage,
  * not a kernel: "binning (wall)", the render's binning from its first kernel

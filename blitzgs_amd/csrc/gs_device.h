@@ -350,18 +350,26 @@ __device__ __forceinline__ float bcast63(float v) { return __int_as_float(__buil
 // with all 64 lanes active.
 __device__ __forceinline__ float wave_sum(float v) { return bcast63(wave_sum_to_lane63(v)); }
 
-// Twelve per-lane values summed over the wave at once (gfx950 lane swaps):
+// Twelve per-lane values summed over the wave at once (gfx950 lane swaps),
+// each level a transpose-add: two registers exchange halves of their lanes so
+// that one register carries the pairwise sums of both:
 //   level 1  v_permlane32_swap pairs (v0,v1),...: one register holds 32-lane
 //            partials of v[2i] in lanes 0-31 and of v[2i+1] in lanes 32-63;
-//   level 2  v_permlane16_swap pairs of those: each 16-lane row of a register
-//            holds 16 partials of one value (rows map to values 0,2,1,3);
-//   level 3  DPP row_shr 1,2,4,8 inside each row: lane 15 of the row has the
-//            total; the second and third registers are shifted down one and
-//            two lanes (row_shl) so one register carries all twelve totals.
-// 34 VALU operations instead of 12 separate full-wave reductions.  Lane L
-// returns the total of value wave_sum12_index(L) (-1: nothing).  All lanes
-// must be active.  ABS23: values 2 and 3 are summed as absolute values (the
-// first level adds |a| + |b|, which costs nothing: source modifiers).
+//   level 2  v_permlane16_swap pairs of those: each 16-lane row of register
+//            t[j] holds 16 partials of value 4j + m(row), m = 0,2,1,3;
+//   level 3  DPP row_ror:8 (lane c of a row <-> c ^ 8): t0 and t1 share a
+//            register, t0's values in lanes 0-7 of each row and t1's in lanes
+//            8-15 (8 partials); t2 is folded onto itself;
+//   level 4  DPP row_half_mirror (c <-> 7 - c inside each 8-lane half): that
+//            register and t2's share one, t2's values in lanes 4-7 of each
+//            half (4 partials);
+//   level 5, 6  DPP quad_perm xor 2, xor 1: every lane of an aligned group of
+//            four holds its value's total.
+// 27 VALU operations instead of 12 separate full-wave reductions.  Lane L
+// returns the total of value wave_sum12_index(L) (-1: a duplicate or
+// nothing).  All lanes must be active.  ABS23: values 2 and 3 are summed as
+// absolute values (the first level adds |a| + |b|, which costs nothing:
+// source modifiers).
 template <bool ABS23 = false>
 __device__ __forceinline__ float wave_sum12(const float (&v)[12])
 {
@@ -378,24 +386,28 @@ __device__ __forceinline__ float wave_sum12(const float (&v)[12])
     for (int j = 0; j < 3; j++) {
         const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[2 * j]), __float_as_uint(s[2 * j + 1]),
                                                         false, false);
-        float x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        x = x + dpp_f<0x111>(x);      // row_shr:1
-        x = x + dpp_f<0x112>(x);      // row_shr:2
-        x = x + dpp_f<0x114>(x);      // row_shr:4
-        x = x + dpp_f<0x118>(x);      // row_shr:8
-        t[j] = x;
+        t[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    const float t1 = dpp_f<0x101>(t[1]);   // row_shl:1 -> lane 14 of each row
-    const float t2 = dpp_f<0x102>(t[2]);   // row_shl:2 -> lane 13
-    const int sl = lane_id() & 15;
-    return sl == 15 ? t[0] : (sl == 14 ? t1 : t2);
+    const int c = lane_id() & 15;
+    // level 3: lanes c < 8 keep t0, c >= 8 t1; the partner c ^ 8 brings the other half
+    const bool lo8 = c < 8;
+    const float z = (lo8 ? t[0] : t[1]) + dpp_f<0x128>(lo8 ? t[1] : t[0]);   // row_ror:8
+    const float t2 = t[2] + dpp_f<0x128>(t[2]);
+    // level 4: lanes c % 8 < 4 keep z, the others t2; the partner 7 - c brings the rest
+    const bool lo4 = (c & 7) < 4;
+    float w = (lo4 ? z : t2) + dpp_f<0x141>(lo4 ? t2 : z);                    // row_half_mirror
+    w = w + dpp_f<0x4e>(w);                                                   // quad_perm [2,3,0,1]
+    w = w + dpp_f<0xb1>(w);                                                   // quad_perm [1,0,3,2]
+    return w;
 }
 
+// the value whose total lane `lane` holds after wave_sum12: lane 16 r + c
+// with c = 0 (t0), 4 (t2) or 8 (t1) of row r; -1 for the other lanes
 __device__ __forceinline__ int wave_sum12_index(int lane)
 {
-    const int q = lane >> 4, sl = lane & 15;
-    const int m = q == 0 ? 0 : (q == 1 ? 2 : (q == 2 ? 1 : 3));
-    return sl == 15 ? m : (sl == 14 ? 4 + m : (sl == 13 ? 8 + m : -1));
+    const int r = lane >> 4, c = lane & 15;
+    const int m = r == 0 ? 0 : (r == 1 ? 2 : (r == 2 ? 1 : 3));
+    return c == 0 ? m : (c == 4 ? 8 + m : (c == 8 ? 4 + m : -1));
 }
 
 __device__ __forceinline__ int wave_sum_i(int v)

@@ -3002,7 +3002,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             float vals[12];
             const bool valid = bwd_blend_step<FULL>(px_st, kc, A, B, Cc, vals);
             if (gs::ballot(valid) == 0) continue;
-            const uint32_t cx = __float_as_uint(Cc.y);
+            const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));   // one Gaussian per entry
             const float tot = gs::wave_sum12<true>(vals);
             // the eleven totals of one Gaussian land in one 64-byte accumulator
             if (my_k >= 0 && my_k < 11 && tot != 0.f) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);

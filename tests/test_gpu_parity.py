@@ -372,8 +372,9 @@ def test_quadrant_cull_keeps_results_exact_on_hard_cases():
 
 
 def test_wave_sum12_lane_layout():
-    # the backward's 12-value wave reduction (permlane32/16 swaps + DPP row
-    # scans) against a plain sum, with values that make any mis-routed lane visible
+    # the backward's 12-value wave reduction (permlane32/16 swaps, then DPP
+    # transpose-adds) against a plain sum, with values that make any mis-routed
+    # lane visible
     rng = np.random.default_rng(0)
     x = rng.integers(-1000, 1000, (12, 64)).astype(np.float32)
     x[7] = 1.0

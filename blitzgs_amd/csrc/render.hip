@@ -2879,28 +2879,50 @@ struct BwdConst {
     int last;
 };
 
-template <bool FULL>
-__device__ __forceinline__ bool bwd_blend_step(BwdPixel& p, const BwdConst& k, const float4& A, const float4& B,
-                                               const float4& Cc, float (&vals)[12])
+// One entry of the backward for this lane's pixel, in two parts: bwd_eval
+// decides whether the pixel blends the entry (the forward's exact alpha
+// expressions), and bwd_apply, which the caller skips when no lane of the
+// wave blends it (the state update is then the identity for every lane),
+// updates the pixel's state and yields the entry's twelve gradient terms.
+struct BwdEval {
+    float dx, dy, hadx, hcdy, nbdx, alpha, G0;
+    bool valid;
+};
+
+__device__ __forceinline__ BwdEval bwd_eval(const BwdConst& k, const float4& A, const float4& B, const float4& Cc)
 {
+    BwdEval e;
     const int ci = __float_as_int(Cc.z);   // position in the tile's list
-    // Branch-free: every lane evaluates the entry; a lane whose pixel
-    // does not blend it (past its last contributor, power > 0, alpha <
-    // 1/255) gets zero gradient factors and unchanged state, through
-    // selects on three factors instead of per-value zeroing.
-    const float dx = A.x - k.pxf, dy = A.y - k.pyf;
-    const float power = gs::power_of(A.z, A.w, B.x, dx, dy);
-    float G0;
-    const float alpha = gs::blend_alpha(B.y, power, Cc.w, G0);
-    const bool valid = ci < k.last && !(power > 0.0f) && !(alpha < (1.0f / 255.0f));
-    const float G = valid ? G0 : 0.f;
+    e.dx = A.x - k.pxf;
+    e.dy = A.y - k.pyf;
+    // gs::power_of's operations, with the products ha dx, hc dy, nb dx kept
+    // for the gradient
+    e.hadx = A.z * e.dx;
+    e.hcdy = B.x * e.dy;
+    e.nbdx = A.w * e.dx;
+    const float power = __builtin_fmaf(e.hadx, e.dx, __builtin_fmaf(e.hcdy, e.dy, e.nbdx * e.dy));
+    e.alpha = gs::blend_alpha(B.y, power, Cc.w, e.G0);
+    e.valid = ci < k.last && !(power > 0.0f) && !(e.alpha < (1.0f / 255.0f));
+    return e;
+}
+
+// Branch-free: every lane applies the entry; a lane whose pixel does not
+// blend it (past its last contributor, power > 0, alpha < 1/255) gets zero
+// gradient factors and unchanged state, through selects on three factors
+// instead of per-value zeroing.
+template <bool FULL>
+__device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const float4& A, const float4& B,
+                                          const float4& Cc, const BwdEval& e, float (&vals)[12])
+{
+    const bool valid = e.valid;
+    const float alpha = e.alpha, dx = e.dx, dy = e.dy;
+    const float G = valid ? e.G0 : 0.f;
     const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
     p.T = p.T * inv_one_m;
     const float dchannel_dcolor = valid ? alpha * p.T : 0.f;
     // the reference's expressions, regrouped into fused multiply-adds
     // (gradients carry a tolerance, not bit-exactness):
     //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
-    //   dG/ddelx = -gdx * a - gdy * b         -> gdx * (2 ha) + gdy * nb
     //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms);
     // a lane that does not blend the entry updates acc with factor 0
     const float la = valid ? p.last_alpha : 0.f;
@@ -2917,24 +2939,26 @@ __device__ __forceinline__ bool bwd_blend_step(BwdPixel& p, const BwdConst& k, c
     const float gc2 = dchannel_dcolor * k.dp2;
     dL_dalpha = valid ? __builtin_fmaf(dL_dalpha, p.T, inv_one_m * k.nT_bg) : 0.f;
     const float dL_dG = B.y * dL_dalpha;
-    const float gdx = G * dx, gdy = G * dy;
-    const float dG_ddelx = __builtin_fmaf(gdx, A.z + A.z, gdy * A.w);
-    const float dG_ddely = __builtin_fmaf(gdy, B.x + B.x, gdx * A.w);
+    // dG/ddelx = G (2 ha dx + nb dy), dG/ddely = G (2 hc dy + nb dx)
+    const float dpx = __builtin_fmaf(2.0f, e.hadx, A.w * dy);
+    const float dpy = __builtin_fmaf(2.0f, e.hcdy, e.nbdx);
+    const float wG = dL_dG * G;
     // the constant factors dmean/dpixel (W/2, H/2) and the conic terms' -1/2
     // are applied once to the sums (unpack_grads_kernel), not per entry
-    const float gmx = dL_dG * dG_ddelx;
-    const float gmy = dL_dG * dG_ddely;
-    const float hgdx = dL_dG * gdx;
+    const float gmx = wG * dpx;
+    const float gmy = wG * dpy;
+    const float wdx = wG * dx;
     const bool clamped = FULL && B.y * G > 0.99f;
-    const float gca = clamped ? 0.f : hgdx * dx;
-    const float gcb = clamped ? 0.f : hgdx * dy;
-    const float gcc = clamped ? 0.f : (dL_dG * gdy) * dy;
+    const float gca = clamped ? 0.f : wdx * dx;
+    const float gcb = clamped ? 0.f : wdx * dy;
+    const float gcc = clamped ? 0.f : (wG * dy) * dy;
     const float gop = clamped ? 0.f : G * dL_dalpha;
     // vals[2], vals[3]: |dmean| terms, made absolute by wave_sum12<true>
     vals[0] = gmx; vals[1] = gmy; vals[2] = gmx; vals[3] = gmy;
     vals[4] = gca; vals[5] = gcb; vals[6] = gcc; vals[7] = gop;
-    vals[8] = gc0; vals[9] = gc1; vals[10] = gc2; vals[11] = 0.f;
-    return valid;
+    // slot 11 is never read back: any register that is dead here fills it
+    // (no zero has to be materialised for it)
+    vals[8] = gc0; vals[9] = gc1; vals[10] = gc2; vals[11] = dx;
 }
 
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no
@@ -2999,13 +3023,14 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             const float4 A = st.a[j];
             const float4 B = st.b[j];
             const float4 Cc = st.c[j];
+            const BwdEval e = bwd_eval(kc, A, B, Cc);
+            if (gs::ballot(e.valid) == 0) continue;   // no lane blends the entry: nothing changes
             float vals[12];
-            const bool valid = bwd_blend_step<FULL>(px_st, kc, A, B, Cc, vals);
-            if (gs::ballot(valid) == 0) continue;
+            bwd_apply<FULL>(px_st, kc, A, B, Cc, e, vals);
             const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));   // one Gaussian per entry
             const float tot = gs::wave_sum12<true>(vals);
             // the eleven totals of one Gaussian land in one 64-byte accumulator
-            if (my_k >= 0 && my_k < 11 && tot != 0.f) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
+            if (my_k >= 0 && my_k < 11) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
         }
         __syncthreads();
         r_cur = r_nxt;
@@ -3015,7 +3040,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
 }
 
 // ---- VALU probes: the blend kernels' per-entry arithmetic (fwd_blend_step;
-// bwd_blend_step + wave_sum12), on 64 entries staged in LDS once, with no
+// bwd_eval + bwd_apply + wave_sum12), on 64 entries staged in LDS once, with no
 // global memory traffic, in the blend kernels' 64-thread blocks.  Their VALU
 // instruction rate is the ceiling the blend kernels' rate is compared with.
 constexpr int VALU_PROBE_BLOCKS = 16384;
@@ -3074,9 +3099,10 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
             BwdPixel p{0.2f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             for (int j = 0; j < 64; j++) {
                 const float4 A = st.a[j], B = st.b[j], Cc = st.c[j];
+                const BwdEval e = bwd_eval(kc, A, B, Cc);
+                if (gs::ballot(e.valid) == 0) continue;
                 float vals[12];
-                const bool valid = bwd_blend_step<false>(p, kc, A, B, Cc, vals);
-                if (gs::ballot(valid) == 0) continue;
+                bwd_apply<false>(p, kc, A, B, Cc, e, vals);
                 const float tot = gs::wave_sum12<true>(vals);
                 if (my_k >= 0 && my_k < 11 && tot != 0.f) out += tot;
             }

@@ -2351,6 +2351,23 @@ __device__ __forceinline__ bool rec_may_touch(const Rec& r, float x0, float y0, 
     return gs::may_touch_prepared(r.q2.y, r.q2.z, r.q2.w, r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, x0, y0, x1, y1);
 }
 
+// The pixel rectangle [x0, x1] x [y0, y1] spanned by the lanes set in m
+// (m != 0; lane 8 y + x is pixel (qx0 + x, qy0 + y) of the quadrant): the
+// staging cull of a batch tests against the pixels that can still take part
+// in it.  Scalar bit arithmetic on the wave-uniform mask.
+__device__ __forceinline__ void active_rect(uint64_t m, float qx0, float qy0, float& x0, float& y0, float& x1,
+                                            float& y1)
+{
+    uint32_t c = (uint32_t)m | (uint32_t)(m >> 32);   // columns: OR of the eight row bytes
+    c |= c >> 16;
+    c |= c >> 8;
+    c &= 0xffu;
+    x0 = qx0 + (float)__builtin_ctz(c);
+    x1 = qx0 + (float)(31 - __builtin_clz(c));
+    y0 = qy0 + (float)(__builtin_ctzll(m) >> 3);
+    y1 = qy0 + (float)((63 - __builtin_clzll(m)) >> 3);
+}
+
 // wave-private staging slots of one batch of 64 list entries
 struct Stage {
     float4 a[64];   // x, y, -a/2, -b
@@ -2473,14 +2490,19 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     if (lane < n) r_cur = load_rec<true>(rec, id_cur);
 
     for (int base = 0; base < n; base += 64) {
-        if (gs::ballot(!px_st.done) == 0) break;
+        const uint64_t live = gs::ballot(!px_st.done);
+        if (live == 0) break;
         const int k = base + lane;
         Rec r_nxt{};
         uint32_t id_nn = 0;
         if (k + 64 < n) r_nxt = load_rec<true>(rec, id_nxt);
         if (k + 128 < n) id_nn = list[k + 128];
-        // stage the batch, keeping only Gaussians that can reach this quadrant
-        const bool keep = k < n && rec_may_touch(r_cur, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
+        // stage the batch, keeping only Gaussians that can reach a pixel of
+        // the quadrant that is still blending (a finished pixel takes no
+        // further entry, so the others cannot change any output)
+        float cx0, cy0, cx1, cy1;
+        active_rect(live, qx0, qy0, cx0, cy0, cx1, cy1);
+        const bool keep = k < n && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
         const uint64_t km = gs::ballot(keep);
         if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
         __syncthreads();
@@ -2870,8 +2892,15 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
 // pixel blends the entry, with its eleven gradient terms in vals (dmean x, y,
 // |dmean x|, |dmean y|, dconic a, b, c, dopacity, drgb; vals[11] = 0).
 // Shared by the backward kernels and the VALU probe (render_valu_probe).
+// Per-pixel state of the backward walk.  The accumulated colour behind the
+// current entry and the last blended colour enter the gradient only through
+// their dot products with dL/dpixel, and the accumulation is linear, so the
+// state keeps those two dot products instead of the six channel values.
 struct BwdPixel {
-    float T, acc0, acc1, acc2, lc0, lc1, lc2, last_alpha;
+    float T;            // transmittance in front of the current entry
+    float acc_dp;       // (colour accumulated behind it) . dL/dpixel
+    float last_dp;      // (colour of the last blended entry) . dL/dpixel
+    float last_alpha;
 };
 
 struct BwdConst {
@@ -2920,20 +2949,19 @@ __device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const 
     const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
     p.T = p.T * inv_one_m;
     const float dchannel_dcolor = valid ? alpha * p.T : 0.f;
-    // the reference's expressions, regrouped into fused multiply-adds
-    // (gradients carry a tolerance, not bit-exactness):
-    //   acc = la * lc + (1 - la) * acc        -> acc + la * (lc - acc)
+    // the reference's expressions, regrouped into fused multiply-adds and
+    // taken in their dot products with dL/dpixel (gradients carry a
+    // tolerance, not bit-exactness):
+    //   acc = la * lc + (1 - la) * acc        -> acc.dp += la * (lc.dp - acc.dp)
+    //   dL/dalpha = sum_ch (c - acc) dp_ch    -> c.dp - acc.dp
     //   (ha = -a/2, nb = -b, hc = -c/2 are the staged conic terms);
     // a lane that does not blend the entry updates acc with factor 0
     const float la = valid ? p.last_alpha : 0.f;
-    p.acc0 = __builtin_fmaf(la, p.lc0 - p.acc0, p.acc0);
-    p.acc1 = __builtin_fmaf(la, p.lc1 - p.acc1, p.acc1);
-    p.acc2 = __builtin_fmaf(la, p.lc2 - p.acc2, p.acc2);
-    p.lc0 = valid ? B.z : p.lc0;
-    p.lc1 = valid ? B.w : p.lc1;
-    p.lc2 = valid ? Cc.x : p.lc2;
+    p.acc_dp = __builtin_fmaf(la, p.last_dp - p.acc_dp, p.acc_dp);
+    const float c_dp = __builtin_fmaf(B.z, k.dp0, __builtin_fmaf(B.w, k.dp1, Cc.x * k.dp2));
+    p.last_dp = valid ? c_dp : p.last_dp;
     p.last_alpha = valid ? alpha : p.last_alpha;
-    float dL_dalpha = __builtin_fmaf(B.z - p.acc0, k.dp0, __builtin_fmaf(B.w - p.acc1, k.dp1, (Cc.x - p.acc2) * k.dp2));
+    float dL_dalpha = c_dp - p.acc_dp;
     const float gc0 = dchannel_dcolor * k.dp0;
     const float gc1 = dchannel_dcolor * k.dp1;
     const float gc2 = dchannel_dcolor * k.dp2;
@@ -2998,7 +3026,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     // after the wave reduction this lane holds the total of gradient term
     // my_k (accumulator slot), or nothing (my_k < 0)
     const int my_k = gs::wave_sum12_index(lane);
-    BwdPixel px_st{T_final, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    BwdPixel px_st{T_final, 0.f, 0.f, 0.f};
 
     // walk positions maxlast-1 .. 0 of the tile's list, back to front, with
     // the same software pipeline as the forward
@@ -3013,8 +3041,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
         uint32_t id_nn = 0;
         if (k - 64 >= 0) r_nxt = load_rec<false>(rec, id_nxt);
         if (k - 128 >= 0) id_nn = list[k - 128];
-        // stage positions top-1, top-2, ... keeping only Gaussians that can reach this quadrant
-        const bool keep = k >= 0 && rec_may_touch(r_cur, qx0, qy0, qx0 + 7.0f, qy0 + 7.0f);
+        // stage positions top-1, top-2, ..., top-64, keeping only Gaussians
+        // that can reach a pixel whose last contributor lies past top-64
+        // (the other pixels blend no entry of this batch); that pixel set is
+        // never empty: it holds the pixels of the largest last contributor
+        float cx0, cy0, cx1, cy1;
+        active_rect(gs::ballot(last > max(top - 64, 0)), qx0, qy0, cx0, cy0, cx1, cy1);
+        const bool keep = k >= 0 && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
         const uint64_t km = gs::ballot(keep);
         if (keep) stage_put(st, gs::rank_below(km), r_cur, id_cur, k);
         __syncthreads();
@@ -3096,7 +3129,7 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
         const int my_k = gs::wave_sum12_index(lane);
         const BwdConst kc{pxf, pyf, 0.3f, -0.2f, 0.1f, -0.05f, 64};
         for (int it = 0; it < iters; it++) {
-            BwdPixel p{0.2f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            BwdPixel p{0.2f, 0.f, 0.f, 0.f};
             for (int j = 0; j < 64; j++) {
                 const float4 A = st.a[j], B = st.b[j], Cc = st.c[j];
                 const BwdEval e = bwd_eval(kc, A, B, Cc);

@@ -2944,11 +2944,15 @@ __device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const 
                                           const float4& Cc, const BwdEval& e, float (&vals)[12])
 {
     const bool valid = e.valid;
-    const float alpha = e.alpha, dx = e.dx, dy = e.dy;
+    const float dx = e.dx, dy = e.dy;
+    // a lane that does not blend the entry runs it with alpha = 0 and G = 0:
+    // T is unchanged (1 / (1 - 0) is exactly 1), and every gradient term
+    // carries a factor alpha (colour) or G (the others; dL/dalpha stays finite)
+    const float alpha = valid ? e.alpha : 0.f;
     const float G = valid ? e.G0 : 0.f;
-    const float inv_one_m = valid ? __builtin_amdgcn_rcpf(1.f - alpha) : 1.0f;   // 1 ulp; gradients only
+    const float inv_one_m = __builtin_amdgcn_rcpf(1.f - alpha);   // 1 ulp; gradients only
     p.T = p.T * inv_one_m;
-    const float dchannel_dcolor = valid ? alpha * p.T : 0.f;
+    const float dchannel_dcolor = alpha * p.T;
     // the reference's expressions, regrouped into fused multiply-adds and
     // taken in their dot products with dL/dpixel (gradients carry a
     // tolerance, not bit-exactness):
@@ -2965,7 +2969,7 @@ __device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const 
     const float gc0 = dchannel_dcolor * k.dp0;
     const float gc1 = dchannel_dcolor * k.dp1;
     const float gc2 = dchannel_dcolor * k.dp2;
-    dL_dalpha = valid ? __builtin_fmaf(dL_dalpha, p.T, inv_one_m * k.nT_bg) : 0.f;
+    dL_dalpha = __builtin_fmaf(dL_dalpha, p.T, inv_one_m * k.nT_bg);
     const float dL_dG = B.y * dL_dalpha;
     // dG/ddelx = G (2 ha dx + nb dy), dG/ddely = G (2 hc dy + nb dx)
     const float dpx = __builtin_fmaf(2.0f, e.hadx, A.w * dy);

@@ -100,6 +100,11 @@ def test_argument_errors_without_device(lib):
     assert rc != 0 and b"coefficients" in lib.gs_last_error()
     rc = lib.gs_diag_math(9, 1, None, None, None)
     assert rc != 0 and b"op" in lib.gs_last_error()
+    # timing modes: 0 off, 1 every kernel and the stages, 2 the stages only
+    rc = lib.gs_timing_enable(3)
+    assert rc != 0 and b"timing mode" in lib.gs_last_error()
+    for mode in (2, 1, 0):
+        assert lib.gs_timing_enable(mode) == 0
 
 
 def test_routing_argument_errors_without_device(lib):

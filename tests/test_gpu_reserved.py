@@ -109,6 +109,32 @@ def test_reserved_forward_without_instances():
     assert not out["obs"].any() and not out["n_render"].any()
 
 
+@pytest.mark.parametrize("reserved", [False, True])
+def test_binning_stage_timing_modes(reserved):
+    # mode 2 times the binning as one stage and nothing else; mode 1 also every
+    # kernel; the stage is closed once per forward, on both forward routes
+    scene, cam, pre, dev = _inputs(n=4000, seed=9)
+    W, H = cam["W"], cam["H"]
+    cap = 1 << 20 if reserved else None
+    ref = _forward(dev, W, H)
+    for mode_kernels in (False, True):
+        _lib.timing_reset()
+        _lib.timing_enable(True, stages_only=not mode_kernels)
+        try:
+            out = _forward(dev, W, H, cap)
+        finally:
+            _lib.timing_enable(False)
+        kt = _lib.timing_read()
+        assert kt["binning (wall)"][1] == 1 and kt["binning (wall)"][0] > 0.0
+        if mode_kernels:
+            assert {"count_regions_kernel", "scan_regions_kernel", "scatter_regions_kernel",
+                    "render_fwd_kernel"} <= set(kt)
+        else:
+            assert set(kt) == {"binning (wall)"}
+        assert out["R"] == ref["R"] and torch.equal(out["color"].view(torch.int32), ref["color"].view(torch.int32))
+    _lib.timing_reset()
+
+
 def test_operator_layer_reserves_after_first_forward():
     """The first forward on the device sizes the binning buffer exactly; the
     next ones reserve (from the largest recent count) and give the same

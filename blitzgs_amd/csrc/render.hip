@@ -798,18 +798,27 @@ __device__ __forceinline__ int sort_class(uint32_t n)
     return n <= 512u ? 0 : n <= 1024u ? 1 : n <= 2048u ? 2 : n <= 4096u ? 3 : n <= (uint32_t)SORT_CAP_MAX ? 4 : 5;
 }
 
+// The instance count as the host reads it back: one 64-bit word, so that a
+// single store publishes it -- bits 0-31 R (mod 2^32), bit 32 set when R does
+// not fit in 32 bits, bits 33-63 the caller's sequence number (31 bits), by
+// which the host tells this call's word from an earlier one.
+__host__ __device__ __forceinline__ uint64_t readback_word(uint64_t R, uint32_t seq)
+{
+    return (R & 0xffffffffull) | ((R >> 32) != 0 ? (1ull << 32) : 0ull) | ((uint64_t)(seq & 0x7fffffffu) << 33);
+}
+
 //
 // cap: the instance capacity of the caller's binning buffer.  When R exceeds
 // it, meta[9] is set and the class lists are left empty: the ranges, the
 // scatter and the sorts then do nothing (the caller redoes the forward with a
 // buffer for R).  host_R (device address of mapped, coherent pinned host
-// memory, or null): R is also stored there, for the host to read once the
-// kernel is done.
+// memory, or null): R is also stored there in one 8-byte store, tagged with
+// the caller's sequence number seq, for the host to poll (readback_word).
 __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ meta, const uint32_t* __restrict__ tile_count,
                                                         uint32_t* __restrict__ tile_start, uint32_t* __restrict__ cursor,
                                                         uint32_t* __restrict__ wcount, int NW, int T,
                                                         uint32_t* __restrict__ cls_count, int* __restrict__ cls_list,
-                                                        uint64_t cap, uint32_t* __restrict__ host_R)
+                                                        uint64_t cap, uint64_t* __restrict__ host_R, uint32_t seq)
 {
     __shared__ uint32_t s_wave[32];
     __shared__ uint32_t s_cls[SORT_CLASSES];
@@ -851,10 +860,7 @@ __global__ __launch_bounds__(1024) void tilescan_kernel(uint32_t* __restrict__ m
         meta[2] = (uint32_t)(base & 0xffffffffu);
         meta[3] = (uint32_t)(base >> 32);
         meta[9] = over ? 1u : 0u;
-        if (host_R != nullptr) {
-            host_R[0] = (uint32_t)(base & 0xffffffffu);
-            host_R[1] = (uint32_t)(base >> 32);
-        }
+        if (host_R != nullptr) *host_R = readback_word(base, seq);
     }
 }
 
@@ -1619,7 +1625,7 @@ __device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Get
 //     R -> meta[2..3];
 //   - the region list lengths -> offsets (rstart, and rcursor for the global
 //     cursors) and per-class region lists; the total -> meta[10].
-// cap, host_R: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
+// cap, host_R, seq: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
 __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict__ meta, unsigned gx, unsigned lrs,
                                                             const int* __restrict__ tile_of_local,
                                                             uint32_t* __restrict__ grid, int Gfull,
@@ -1631,7 +1637,7 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
                                                             uint32_t* __restrict__ rcursor,
                                                             uint32_t* __restrict__ rcls_count,
                                                             int* __restrict__ rcls_list, int NR, uint64_t cap,
-                                                            uint32_t* __restrict__ host_R)
+                                                            uint64_t* __restrict__ host_R, uint32_t seq)
 {
     __shared__ uint32_t s_grid[LDS_GRID];
     __shared__ uint32_t s_wave[32];
@@ -1723,10 +1729,7 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
         meta[3] = (uint32_t)(R >> 32);
         meta[9] = over ? 1u : 0u;
         meta[10] = (uint32_t)E;
-        if (host_R != nullptr) {
-            host_R[0] = (uint32_t)(R & 0xffffffffu);
-            host_R[1] = (uint32_t)(R >> 32);
-        }
+        if (host_R != nullptr) *host_R = readback_word(R, seq);
     }
 }
 
@@ -3226,10 +3229,14 @@ namespace {
 // Pinned host words for R, one slot per forward in flight: a reserved
 // forward copies R there and records the slot's event, and waits for that
 // event only after the rest of the forward is queued.
+// A reserved forward's slot for R: one word of mapped, coherent pinned host
+// memory that the scan kernel stores readback_word(R, seq) into and the host
+// polls, so that nothing is queued on the stream between the scan and the
+// scatter (an event there costs the stream a gap of several microseconds).
 struct Readback {
-    uint32_t* host = nullptr;   // mapped, coherent pinned memory: the scan kernel stores R here
-    uint32_t* dev = nullptr;    // its device address
-    hipEvent_t ev = nullptr;
+    uint64_t* host = nullptr;   // the word, host side
+    uint64_t* dev = nullptr;    // its device address
+    uint32_t seq = 0;           // this use's sequence number (31 bits, never 0)
     int device = -1;
     bool busy = false;
 };
@@ -3277,12 +3284,14 @@ int readback_acquire(Readback*& out)
     for (Readback& r : g_rb) {
         if (r.busy || (r.device >= 0 && r.device != dev)) continue;
         if (r.device < 0) {
-            GS_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 2 * sizeof(uint32_t),
+            GS_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), sizeof(uint64_t),
                                  hipHostMallocMapped | hipHostMallocCoherent));
             GS_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&r.dev), r.host, 0));
-            GS_HIP(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
+            __atomic_store_n(r.host, 0ull, __ATOMIC_RELEASE);   // sequence 0: never a use's
             r.device = dev;
         }
+        r.seq = (r.seq + 1u) & 0x7fffffffu;
+        if (r.seq == 0u) r.seq = 1u;
         r.busy = true;
         out = &r;
         return GS_OK;
@@ -3363,7 +3372,7 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
                                     at<const uint32_t>(geom, g.rcount),
                                     at<uint32_t>(geom, g.rstart), at<uint32_t>(geom, g.rcursor),
                                     at<uint32_t>(geom, g.rcls_count), at<int>(geom, g.rcls_list), g.NR, cap,
-                                    rb != nullptr ? rb->dev : nullptr));
+                                    rb != nullptr ? rb->dev : nullptr, rb != nullptr ? rb->seq : 0u));
         GS_LAUNCH_CHECK("scan_regions_kernel");
     }
     if (!split && P > 0) {
@@ -3380,14 +3389,10 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
                  hipLaunchKernelGGL(tilescan_kernel, dim3(1), dim3(1024), 0, stream, meta, tile_count, tile_start, cursor,
                                     at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0, g.T,
                                     at<uint32_t>(geom, g.cls_count), at<int>(geom, g.cls_list), cap,
-                                    rb != nullptr ? rb->dev : nullptr));
+                                    rb != nullptr ? rb->dev : nullptr, rb != nullptr ? rb->seq : 0u));
         GS_LAUNCH_CHECK("tilescan_kernel");
     }
-    if (rb != nullptr) {
-        // the scan stored R into rb->host; the event marks the end of the scan
-        GS_HIP(hipEventRecord(rb->ev, stream));
-        return GS_OK;
-    }
+    if (rb != nullptr) return GS_OK;   // the scan stores R into rb's word (reserved_forward polls it)
     uint32_t hR[2] = {0, 0};
     GS_HIP(hipMemcpyAsync(hR, meta + 2, sizeof(hR), hipMemcpyDeviceToHost, stream));
     GS_HIP(hipStreamSynchronize(stream));
@@ -3666,20 +3671,38 @@ int reserved_forward(bool full, int P, int64_t cap, int W, int H, const float* m
     int rc = render_count_impl(full, P, W, H, means2D, radii, compute_locally, rects, conic_opacity, geom, nullptr,
                                stream, (uint64_t)cap, rb);
     if (rc == GS_OK) rc = forward();
-    // the slot's copy may be queued: wait for it before the slot is reused
-    const hipError_t e = hipEventSynchronize(rb->ev);
-    const uint64_t R = (uint64_t)rb->host[0] | ((uint64_t)rb->host[1] << 32);
+    if (rc != GS_OK) {
+        // a scan already queued may still store into the slot: let it land first
+        (void)hipStreamSynchronize(stream);
+        readback_release(rb);
+        return rc;
+    }
+    // poll the slot's word for this use's sequence number; every 256 polls the
+    // stream is queried, and once it is idle (or failed) the word is final
+    uint64_t v = 0;
+    hipError_t e = hipSuccess;
+    for (uint32_t poll = 1;; poll++) {
+        v = __atomic_load_n(rb->host, __ATOMIC_ACQUIRE);
+        if ((uint32_t)(v >> 33) == rb->seq) break;
+        if ((poll & 255u) == 0u) {
+            const hipError_t q = hipStreamQuery(stream);
+            if (q == hipErrorNotReady) continue;
+            v = __atomic_load_n(rb->host, __ATOMIC_ACQUIRE);
+            if ((uint32_t)(v >> 33) != rb->seq) e = q != hipSuccess ? q : hipErrorUnknown;
+            break;
+        }
+        __builtin_ia32_pause();
+    }
     readback_release(rb);
-    if (rc != GS_OK) return rc;
     if (e != hipSuccess) {
         gs::set_error("waiting for the instance count failed: %s", hipGetErrorString(e));
         return GS_ERR_HIP;
     }
-    if (R > 0xffffffffull) {
-        gs::set_error("number of tile instances %llu exceeds 2^32-1", (unsigned long long)R);
+    if (v & (1ull << 32)) {
+        gs::set_error("number of tile instances exceeds 2^32-1");
         return GS_ERR_SIZE;
     }
-    *num_rendered = (int64_t)R;
+    *num_rendered = (int64_t)(v & 0xffffffffull);
     return GS_OK;
 }
 

@@ -2384,9 +2384,9 @@ struct Stage {
 // forward kernels and the VALU probe (render_valu_probe), which therefore
 // issue the same instructions per entry.
 struct FwdPixel {
-    float T, C0, C1, C2;
+    float T;   // transmittance; negated once the pixel has finished (its final value is |T|)
+    float C0, C1, C2;
     uint32_t last, n2l;
-    bool done;
 };
 
 struct FwdStep {
@@ -2402,7 +2402,7 @@ __device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, 
     float G;
     const float alpha = gs::blend_alpha(B.y, power, Cc.w, G);
     const float test_T = p.T * (1.0f - alpha);
-    const bool use = !p.done && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
+    const bool use = p.T > 0.0f && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
     const bool fin = use && test_T < 0.0001f;
     const bool upd = use && !fin;
     const bool observe = upd && p.T > 0.5f;
@@ -2412,10 +2412,11 @@ __device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, 
     p.C0 = __builtin_fmaf(B.z, w, p.C0);
     p.C1 = __builtin_fmaf(B.w, w, p.C1);
     p.C2 = __builtin_fmaf(Cc.x, w, p.C2);
-    p.T = upd ? test_T : p.T;
+    // a pixel finishes (the reference's T < 1e-4 stop) by negating T: the
+    // sign is the live test (one compare, no separate flag), |T| its value
+    p.T = upd ? test_T : (fin ? -p.T : p.T);
     p.n2l += upd ? 1u : 0u;
     p.last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : p.last;
-    p.done = p.done || fin;
     return FwdStep{upd, observe, wgt};
 }
 
@@ -2481,7 +2482,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     const uint32_t* list = clist + range.x;
     const float pxf = (float)px, pyf = (float)py;
     const float qx0 = (float)qx, qy0 = (float)qy;
-    FwdPixel px_st{1.0f, 0.f, 0.f, 0.f, 0u, 0u, !inside};
+    FwdPixel px_st{inside ? 1.0f : -1.0f, 0.f, 0.f, 0.f, 0u, 0u};
     float wmax = 0.f;      // largest blend weight so far, and its Gaussian (full / simp)
     uint32_t imax = 0u;
 
@@ -2493,7 +2494,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     if (lane < n) r_cur = load_rec<true>(rec, id_cur);
 
     for (int base = 0; base < n; base += 64) {
-        const uint64_t live = gs::ballot(!px_st.done);
+        const uint64_t live = gs::ballot(px_st.T > 0.0f);
         if (live == 0) break;
         const int k = base + lane;
         Rec r_nxt{};
@@ -2512,7 +2513,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         const int cnt = (int)__builtin_popcountll(km);
         // T only decreases, so a batch that starts with no live pixel above
         // T = 0.5 cannot observe (split path): its entries skip the ballot
-        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(!px_st.done && px_st.T > 0.5f) != 0;
+        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(px_st.T > 0.5f) != 0;
         // Branch-free blend of one staged entry: every lane evaluates it and
         // the state changes are selects, so no exec-mask bookkeeping.
         auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
@@ -2547,10 +2548,10 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
         float4 A1, B1, D1;
         for (int j = 0; j < cnt; j += 2) {
-            if (gs::ballot(!px_st.done) == 0) break;
+            if (gs::ballot(px_st.T > 0.0f) == 0) break;
             A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
             blend(A0, B0, D0);
-            if (j + 1 >= cnt || gs::ballot(!px_st.done) == 0) break;
+            if (j + 1 >= cnt) break;   // (the finished-pixel test runs once per pair)
             A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
             blend(A1, B1, D1);
         }
@@ -2561,12 +2562,13 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     }
 
     if (inside) {
-        O.final_T[pid] = px_st.T;
+        const float Tf = __builtin_fabsf(px_st.T);
+        O.final_T[pid] = Tf;
         O.n_contrib_px[pid] = px_st.last;
         if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = px_st.n2l;
-        out_color[pid] = __builtin_fmaf(px_st.T, bg[0], px_st.C0);
-        out_color[HW + pid] = __builtin_fmaf(px_st.T, bg[1], px_st.C1);
-        out_color[2 * HW + pid] = __builtin_fmaf(px_st.T, bg[2], px_st.C2);
+        out_color[pid] = __builtin_fmaf(Tf, bg[0], px_st.C0);
+        out_color[HW + pid] = __builtin_fmaf(Tf, bg[1], px_st.C1);
+        out_color[2 * HW + pid] = __builtin_fmaf(Tf, bg[2], px_st.C2);
     }
     if (MODE == BLEND_SPLIT) {
         const int s_last = gs::wave_sum_i(inside ? (int)px_st.last : 0);
@@ -3111,7 +3113,7 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
         // the observe ballot of its split mode (counted, not stored)
         int observed = 0;
         for (int it = 0; it < iters; it++) {
-            FwdPixel p{1.0f, 0.f, 0.f, 0.f, 0u, 0u, false};
+            FwdPixel p{1.0f, 0.f, 0.f, 0.f, 0u, 0u};
             auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
                 const FwdStep f = fwd_blend_step(p, A, B, Cc, pxf, pyf);
                 const uint64_t m = gs::ballot(f.observe);
@@ -3120,10 +3122,10 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
             float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
             float4 A1, B1, D1;
             for (int j = 0; j < 64; j += 2) {
-                if (gs::ballot(!p.done) == 0) break;
+                if (gs::ballot(p.T > 0.0f) == 0) break;
                 A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
                 blend(A0, B0, D0);
-                if (j + 1 >= 64 || gs::ballot(!p.done) == 0) break;
+                if (j + 1 >= 64 || gs::ballot(p.T > 0.0f) == 0) break;
                 A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
                 blend(A1, B1, D1);
             }

@@ -217,38 +217,71 @@ struct ClearRegions {
 
     __device__ __forceinline__ void clear(int i, int n) const
     {
+        clear_bulk(i, n);
+        clear_masks(i, n);
+    }
+    // the partial grids and the list lengths
+    __device__ __forceinline__ void clear_bulk(int i, int n) const
+    {
         for (int k = i; k < G && grid != nullptr; k += n) grid[k] = 0u;
-        for (int k = i; k < NR && rcount != nullptr; k += n) {
-            rcount[k] = 0u;
-            if (regmask != nullptr) regmask[k] = 0ull;
-        }
+        for (int k = i; k < NR && rcount != nullptr; k += n) rcount[k] = 0u;
+    }
+    // the local-tile masks
+    __device__ __forceinline__ void clear_masks(int i, int n) const
+    {
+        for (int k = i; k < NR && regmask != nullptr; k += n) regmask[k] = 0ull;
     }
 };
 
 // compute_locally (null: every tile) -> local tile numbering and the
 // bounding box of the local tiles (meta[5..8] = x0, y0, x1, y1, exclusive
 // ends; empty box if none); clears the per-tile counters and the region
-// state, then sets the regions' local-tile masks.  One block of 16 waves;
-// each wave owns a contiguous run of 64-tile rounds: it counts its local
-// tiles (ballots), one barrier publishes the 16 counts, and a second walk
-// numbers the tiles in order with coalesced loads and stores.
+// state, then sets the regions' local-tile masks.  Block 0 (16 waves) does
+// the numbering: each wave owns a contiguous run of 64-tile rounds, counts
+// its local tiles (ballots), one barrier publishes the 16 counts, and a
+// second walk numbers the tiles in order with coalesced loads and stores.
+// The other blocks clear the partial count grids and list lengths, which
+// block 0 does not touch (alone it took ~70 us for a 256 x 171-tile grid).
 __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, const uint8_t* __restrict__ cl,
                                                         int* __restrict__ loc_map, int* __restrict__ tile_of_local,
                                                         uint32_t* __restrict__ tile_count, uint32_t* __restrict__ meta,
-                                                        ClearRegions CR)
+                                                        ClearRegions CR, int lds_rounds)
 {
-    CR.clear(threadIdx.x, 1024);
+    if (gridDim.x == 1) {
+        CR.clear_bulk(threadIdx.x, 1024);
+    } else if (blockIdx.x > 0) {
+        CR.clear_bulk((int)((blockIdx.x - 1) * 1024 + threadIdx.x), (int)((gridDim.x - 1) * 1024));
+        return;
+    }
+    CR.clear_masks(threadIdx.x, 1024);
+    // dynamic LDS: the mask as one 64-bit word per 64-tile round, when the
+    // grid has at most lds_rounds rounds (else the mask is re-read from memory)
+    extern __shared__ uint64_t s_bits[];
     __shared__ uint32_t s_cnt[16];
     __shared__ uint32_t s_box[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (threadIdx.x == 0) { s_box[0] = 0xffffffffu; s_box[1] = 0xffffffffu; s_box[2] = 0u; s_box[3] = 0u; }
     const int rounds = (T + 63) / 64;
+    const bool in_lds = rounds <= lds_rounds;
     const int per = (rounds + 15) / 16;
     const int r0 = min(rounds, w * per), r1 = min(rounds, r0 + per);
+    auto flag = [&](int t) { return t < T && cl[t] != 0; };
+    // pass 1: the wave's local-tile count; the mask bytes of eight rounds are
+    // loaded at once (unconditionally, at clamped indices, then masked)
     uint32_t cnt = 0;
-    for (int r = r0; r < r1; r++) {
-        const int t = r * 64 + lane;
-        cnt += (uint32_t)__builtin_popcountll(gs::ballot(t < T && (cl == nullptr || cl[t])));
+    for (int rb = r0; rb < r1; rb += 8) {
+        uint8_t byte[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) byte[k] = cl[min((rb + k) * 64 + lane, T - 1)];
+        bool f[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) f[k] = rb + k < r1 && (rb + k) * 64 + lane < T && byte[k] != 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint64_t m = gs::ballot(f[k]);
+            cnt += (uint32_t)__builtin_popcountll(m);
+            if (in_lds && lane == 0 && rb + k < r1) s_bits[rb + k] = m;
+        }
     }
     if (lane == 0) s_cnt[w] = cnt;
     __syncthreads();
@@ -259,11 +292,15 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
         base += i < w ? c : 0u;
         tot += c;
     }
+    // pass 2: number the tiles in order; the lane's tile (tx, ty) advances by
+    // 64 tiles a round without a division
     uint32_t bx0 = 0xffffffffu, by0 = 0xffffffffu, bx1 = 0u, by1 = 0u;
+    const uint32_t step_x = 64u % gx, step_y = 64u / gx;
+    uint32_t tx = (uint32_t)(r0 * 64 + lane) % gx, ty = (uint32_t)(r0 * 64 + lane) / gx;
     for (int r = r0; r < r1; r++) {
         const int t = r * 64 + lane;
-        const bool f = t < T && (cl == nullptr || cl[t]);
-        const uint64_t m = gs::ballot(f);
+        const uint64_t m = in_lds ? s_bits[r] : gs::ballot(flag(t));
+        const bool f = (m >> lane) & 1ull;
         const uint32_t l = base + (uint32_t)gs::rank_below(m);
         if (t < T) {
             loc_map[t] = f ? (int)l : -1;
@@ -271,11 +308,13 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
         }
         if (f) {
             tile_of_local[l] = t;
-            const uint32_t tx = (uint32_t)t % gx, ty = (uint32_t)t / gx;
             bx0 = min(bx0, tx); by0 = min(by0, ty);
             bx1 = max(bx1, tx + 1); by1 = max(by1, ty + 1);
         }
         base += (uint32_t)__builtin_popcountll(m);
+        tx += step_x;
+        ty += step_y;
+        if (tx >= gx) { tx -= gx; ty++; }
     }
     atomicMin(&s_box[0], bx0); atomicMin(&s_box[1], by0);
     atomicMax(&s_box[2], bx1); atomicMax(&s_box[3], by1);
@@ -290,19 +329,18 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
     // box are visible after the barrier above; every local tile lies in the box)
     if (CR.regmask != nullptr && tot > 0) {
         const unsigned rs = 1u << CR.lrs, nrx = (s_box[2] - s_box[0] + rs - 1) >> CR.lrs;
-        for (int t = threadIdx.x; t < T; t += 1024) {
-            if (!cl[t]) continue;
-            const unsigned ax = (unsigned)t % gx - s_box[0], ay = (unsigned)t / gx - s_box[1];
+        const uint32_t sx = 1024u % gx, sy = 1024u / gx;
+        uint32_t px = threadIdx.x % gx, py = threadIdx.x / gx;   // (px, py): tile t
+        for (int t = threadIdx.x; t < T; t += 1024, px += sx, py += sy) {
+            if (px >= gx) { px -= gx; py++; }
+            if (!(in_lds ? (bool)((s_bits[t >> 6] >> (t & 63)) & 1ull) : flag(t))) continue;
+            const unsigned ax = px - s_box[0], ay = py - s_box[1];
             const unsigned r = (ay >> CR.lrs) * nrx + (ax >> CR.lrs);
             atomicOr(reinterpret_cast<unsigned long long*>(&CR.regmask[r]),
                      1ull << (((ay & (rs - 1)) << CR.lrs) + (ax & (rs - 1))));
         }
     }
 }
-
-// compute_locally null (every tile local): the identity numbering, the full
-// box and cleared counters, spread over many blocks (the single-block scan
-// above is bound by its own instruction fetch, ~17 us at 1.8 KB of code)
 __global__ __launch_bounds__(256) void localmap_all_kernel(int T, unsigned gx, unsigned gy, int* __restrict__ loc_map,
                                                             int* __restrict__ tile_of_local,
                                                             uint32_t* __restrict__ tile_count,
@@ -3352,9 +3390,16 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
                  hipLaunchKernelGGL(localmap_all_kernel, dim3(gs_div_up(nclear, 256)), dim3(256), 0, stream, g.T,
                                     gx, gy, loc_map, tile_of_local, tile_count, meta, CR));
     } else {
+        // block 0 numbers the tiles, the others clear the region state (about
+        // 4 words per thread)
+        const size_t nbulk = split ? (size_t)std::max(GRID_PARTS * g.G, g.NR) : 0;
+        const unsigned nb = 1u + (unsigned)std::min<size_t>(gs_div_up(nbulk, 4096), 1024);
+        // the tile mask held in LDS as bits: one 64-bit word per 64-tile round, up to 64 KB
+        const int rounds = (g.T + 63) / 64, lds_rounds = 8192;
+        const size_t lds = rounds <= lds_rounds ? sizeof(uint64_t) * (size_t)rounds : 0;
         GS_TIMED("localmap_kernel", stream,
-                 hipLaunchKernelGGL(localmap_kernel, dim3(1), dim3(1024), 0, stream, g.T, gx, compute_locally, loc_map,
-                                    tile_of_local, tile_count, meta, CR));
+                 hipLaunchKernelGGL(localmap_kernel, dim3(nb), dim3(1024), lds, stream, g.T, gx, compute_locally,
+                                    loc_map, tile_of_local, tile_count, meta, CR, lds_rounds));
     }
     GS_LAUNCH_CHECK("localmap_kernel");
     if (split) {

@@ -326,8 +326,10 @@ __global__ __launch_bounds__(1024) void localmap_kernel(int T, unsigned gx, cons
         meta[7] = any ? s_box[2] : 0u; meta[8] = any ? s_box[3] : 0u;
     }
     // local-tile mask of every region of the box (the cleared masks and the
-    // box are visible after the barrier above; every local tile lies in the box)
-    if (CR.regmask != nullptr && tot > 0) {
+    // box are visible after the barrier above; every local tile lies in the
+    // box), needed only when the local tiles do not fill their box
+    const bool box_full = tot == (s_box[2] - s_box[0]) * (s_box[3] - s_box[1]);
+    if (CR.regmask != nullptr && tot > 0 && !box_full) {
         const unsigned rs = 1u << CR.lrs, nrx = (s_box[2] - s_box[0] + rs - 1) >> CR.lrs;
         const uint32_t sx = 1024u % gx, sy = 1024u / gx;
         uint32_t px = threadIdx.x % gx, py = threadIdx.x / gx;   // (px, py): tile t
@@ -679,7 +681,7 @@ constexpr int EXPAND_WORDS = 64 * 8 + 64;
 // per lane per round however the rect sizes are spread, and calls
 // f(q, rx, ry, owner's rect, owner's pa, pb, lbits) for the pairs whose region
 // list the owner enters: the regions that hold a local tile of its rect
-// (every region it meets when all tiles are local; lbits: the rect's local
+// (every region it meets when every tile of the box is local; lbits: the rect's local
 // tiles in the region, rect_bits_in_region layout -- 0 when all are local).  pa / pb: per-lane payload
 // handed to f as the owner's.  The lanes' data are staged in the wave's LDS
 // (s, EXPAND_WORDS words); the owner of each position is found by marking the
@@ -764,7 +766,9 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
     uint32_t* rc = lds_r ? s_rh : rcount;
     uint32_t* part = grid + (size_t)(c % GRID_PARTS) * (size_t)Gfull;
     uint32_t* gp = lds_g ? s_grid : part;
-    const bool all_local = meta[0] == gx * gy;
+    // every tile of the local box is local (no mask, or a mask that fills its box):
+    // each region a rect meets holds a local tile of it, and no mask test is needed
+    const bool all_local = meta[0] == (meta[7] - meta[5]) * (meta[8] - meta[6]);
     const TileBox box = tile_box(meta);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     {
@@ -1093,7 +1097,9 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
     const int NRb = (int)(rg.nrx * rg.nry);
     const bool lds_r = NRb <= LDS_REGIONS;
     uint32_t* cur = lds_r ? s_cur : rcursor;
-    const bool all_local = meta[0] == gx * gy;
+    // every tile of the local box is local (no mask, or a mask that fills its box):
+    // each region a rect meets holds a local tile of it, and no mask test is needed
+    const bool all_local = meta[0] == (meta[7] - meta[5]) * (meta[8] - meta[6]);
     const TileBox box = tile_box(meta);
     const int c = blockIdx.x;
     if (lds_r) {

@@ -613,6 +613,15 @@ struct RegionGrid {
     unsigned bx0, by0, bw, bh, lrs, nrx, nry;
 };
 
+// LDS words of count_regions_kernel's region counters: min(NR, LDS_REGIONS)
+// of the full grid, plus the extra row and column of a region difference grid
+__host__ __device__ __forceinline__ int count_region_words(unsigned gx, unsigned gy, unsigned lrs)
+{
+    const unsigned rs = 1u << lrs, nx = (gx + rs - 1) >> lrs, ny = (gy + rs - 1) >> lrs;
+    const int nr = (int)(nx * ny);
+    return (nr < LDS_REGIONS ? nr : LDS_REGIONS) + (int)(nx + ny + 1);
+}
+
 __device__ __forceinline__ RegionGrid region_grid(const uint32_t* __restrict__ meta, unsigned lrs)
 {
     RegionGrid g;
@@ -734,6 +743,33 @@ __device__ __forceinline__ void expand_regions(const RegionGrid& rg, bool all_lo
     }
 }
 
+// In-place 2D inclusive prefix sum of the w x h grid g (row stride w) in LDS
+// by an NT-thread block: rows one wave each, 64 columns at a time (DPP scan),
+// then columns one thread each.  Barriers before and after are the caller's.
+template <int NT>
+__device__ __forceinline__ void lds_prefix_2d(uint32_t* g, unsigned w, unsigned h)
+{
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    for (unsigned y = (unsigned)wid; y < h; y += NT / 64) {
+        uint32_t carry = 0u;
+        for (unsigned x0 = 0; x0 < w; x0 += 64) {
+            const unsigned x = x0 + (unsigned)lane;
+            const uint32_t v = x < w ? g[y * w + x] : 0u;
+            const uint32_t sum = wave_incl_scan_u32(v) + carry;
+            if (x < w) g[y * w + x] = sum;
+            carry = (uint32_t)__builtin_amdgcn_readlane((int)sum, 63);
+        }
+    }
+    __syncthreads();
+    for (unsigned x = threadIdx.x; x < w; x += NT) {
+        uint32_t acc = 0u;
+        for (unsigned y = 0; y < h; y++) {
+            acc += g[y * w + x];
+            g[y * w + x] = acc;
+        }
+    }
+}
+
 // Split path, step 1 (count).  Per chunk of Gaussians (each wave a
 // contiguous run of it, as count_kernel): each wave's listed count; per
 // region, how many of the chunk's listed Gaussians enter its list (LDS
@@ -760,20 +796,24 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
     const int G = (int)(gw * (rg.bh + 1));
     const bool lds_g = G <= LDS_GRID;
     const int c = blockIdx.x;
-    uint32_t* s_exp = reinterpret_cast<uint32_t*>(s_dyn) + (threadIdx.x >> 6) * EXPAND_WORDS;
-    uint32_t* s_rh = reinterpret_cast<uint32_t*>(s_dyn) + WAVES_PER_BIN * EXPAND_WORDS;
-    uint32_t* s_grid = s_rh + (lds_r ? NRb : 0);
-    uint32_t* rc = lds_r ? s_rh : rcount;
-    uint32_t* part = grid + (size_t)(c % GRID_PARTS) * (size_t)Gfull;
-    uint32_t* gp = lds_g ? s_grid : part;
     // every tile of the local box is local (no mask, or a mask that fills its box):
     // each region a rect meets holds a local tile of it, and no mask test is needed
     const bool all_local = meta[0] == (meta[7] - meta[5]) * (meta[8] - meta[6]);
+    // then the chunk's region counts come from a difference grid over the box's
+    // regions too ((nrx + 1) x (nry + 1) entries, in the region words)
+    const unsigned rgw = rg.nrx + 1;
+    const bool rdiff = all_local && lds_r;
+    uint32_t* s_exp = reinterpret_cast<uint32_t*>(s_dyn) + (threadIdx.x >> 6) * EXPAND_WORDS;
+    uint32_t* s_rh = reinterpret_cast<uint32_t*>(s_dyn) + WAVES_PER_BIN * EXPAND_WORDS;
+    uint32_t* s_grid = s_rh + (lds_r ? count_region_words(gx, gy, lrs) : 0);
+    uint32_t* rc = lds_r ? s_rh : rcount;
+    uint32_t* part = grid + (size_t)(c % GRID_PARTS) * (size_t)Gfull;
+    uint32_t* gp = lds_g ? s_grid : part;
     const TileBox box = tile_box(meta);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     {
-        const int nz = (lds_r ? NRb : 0) + (lds_g ? G : 0);
-        for (int i = threadIdx.x; i < nz; i += BIN_THREADS) s_rh[i] = 0u;
+        for (int i = threadIdx.x; lds_r && i < (rdiff ? (int)(rgw * (rg.nry + 1)) : NRb); i += BIN_THREADS) s_rh[i] = 0u;
+        for (int i = threadIdx.x; lds_g && i < G; i += BIN_THREADS) s_grid[i] = 0u;
         __syncthreads();
     }
     const int i1c = min(P, c * CH + CH);
@@ -800,13 +840,27 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
             atomicAdd(&gp[ay0 * gw + ax1], ~0u);
             atomicAdd(&gp[ay1 * gw + ax0], ~0u);
             atomicAdd(&gp[ay1 * gw + ax1], 1u);
+            if (rdiff) {
+                // the rect's regions [rx0, rx1] x [ry0, ry1], corners of the region difference grid
+                const unsigned rx0 = ax0 >> lrs, rx1 = ((ax1 - 1) >> lrs) + 1;
+                const unsigned ry0 = ay0 >> lrs, ry1 = ((ay1 - 1) >> lrs) + 1;
+                atomicAdd(&s_rh[ry0 * rgw + rx0], 1u);
+                atomicAdd(&s_rh[ry0 * rgw + rx1], ~0u);
+                atomicAdd(&s_rh[ry1 * rgw + rx0], ~0u);
+                atomicAdd(&s_rh[ry1 * rgw + rx1], 1u);
+            }
         }
-        expand_regions(rg, all_local, regmask, in, ax0, ay0, ax1, ay1, 0u, 0u, s_exp,
-                       [&](unsigned q, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, uint32_t, uint32_t,
-                           uint64_t) { atomicAdd(&rc[q], 1u); });
+        if (!rdiff)
+            expand_regions(rg, all_local, regmask, in, ax0, ay0, ax1, ay1, 0u, 0u, s_exp,
+                           [&](unsigned q, unsigned, unsigned, unsigned, unsigned, unsigned, unsigned, uint32_t,
+                               uint32_t, uint64_t) { atomicAdd(&rc[q], 1u); });
     }
     if (lane == 0) wcount[(size_t)c * WAVES_PER_BIN + wave] = listed;
     __syncthreads();
+    if (rdiff) {
+        lds_prefix_2d<BIN_THREADS>(s_rh, rgw, rg.nry + 1);
+        __syncthreads();
+    }
     if (lds_r) {
         uint32_t* row = rhist + (size_t)c * NRb;
         // the bases of up to four regions per thread are requested at once
@@ -815,7 +869,8 @@ __global__ __launch_bounds__(BIN_THREADS) void count_regions_kernel(
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int q = q0 + u * BIN_THREADS + (int)threadIdx.x;
-                const uint32_t v = q < NRb ? s_rh[q] : 0u;
+                uint32_t v = 0u;
+                if (q < NRb) v = rdiff ? s_rh[((unsigned)q / rg.nrx) * rgw + (unsigned)q % rg.nrx] : s_rh[q];
                 b[u] = v ? atomicAdd(&rcount[q], v) : 0u;
             }
 #pragma unroll
@@ -3204,9 +3259,9 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
 
 namespace {
 size_t count_lds_bytes(int T) { return sizeof(uint32_t) * (size_t)(T < LDS_TILES ? T : LDS_TILES); }
-size_t count_regions_lds_bytes(const GeomLayout& g)
+size_t count_regions_lds_bytes(const GeomLayout& g, unsigned gx, unsigned gy, unsigned lrs)
 {
-    return sizeof(uint32_t) * ((size_t)WAVES_PER_BIN * EXPAND_WORDS + (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS) +
+    return sizeof(uint32_t) * ((size_t)WAVES_PER_BIN * EXPAND_WORDS + (size_t)count_region_words(gx, gy, lrs) +
                                (size_t)(g.G < LDS_GRID ? g.G : LDS_GRID));
 }
 size_t scatter_regions_lds_bytes(const GeomLayout& g)
@@ -3411,7 +3466,7 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     if (split) {
         if (P > 0) {
             GS_TIMED("count_regions_kernel", stream,
-                     hipLaunchKernelGGL(count_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), count_regions_lds_bytes(g),
+                     hipLaunchKernelGGL(count_regions_kernel, dim3(g.NC), dim3(BIN_THREADS), count_regions_lds_bytes(g, gx, gy, lrs),
                                         stream, P, g.CH, g.WS, gx, gy, lrs, reinterpret_cast<const float2*>(means2D),
                                         radii, meta, at<const uint64_t>(geom, g.regmask), at<uint32_t>(geom, g.rhist),
                                         at<uint32_t>(geom, g.rcount), at<uint32_t>(geom, g.grid), g.G,

@@ -428,8 +428,8 @@ def run_step(args):
                   "local_tiles": int(cl.sum().item()) if cl is not None else T, "loss": loss_desc})
     out["stages_ms"] = stage_rows
     out["stages_note"] = ("per-kernel HIP-event times; `binning` is the wall time of the whole stage on the caller's "
-                          "stream, timed in a run with only the stage's two marks (its kernels overlap on a side "
-                          "stream; their summed times are binning_kernels_ms; binning_wall_with_kernel_events_ms is "
+                          "stream, timed in a run with only the stage's two marks (its kernels overlap on two side "
+                          "streams; their summed times are binning_kernels_ms; binning_wall_with_kernel_events_ms is "
                           "the same wall in the run with an event pair around every kernel)")
     out["binning_kernels_ms"] = round(binning_kernels_ms, 4)
     if BINNING_STAGE + " with kernel events" in per_kernel:

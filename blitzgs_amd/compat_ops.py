@@ -55,8 +55,6 @@ def preprocess_gaussians_backward(radii, cov3D, clamped, means3D, scales, rotati
 
 def render_gaussians(background, image_height, image_width, means2D, depths, radii, conic_opacity, rgb,
                      compute_locally, viewmatrix, campos, tan_fovx, tan_fovy, all_map, render_geo, debug, args=None):
-    if render_geo:
-        raise NotImplementedError("render_geo=True is not supported")
     timing = _r._want_timing(args)
     H, W = int(image_height), int(image_width)
     (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
@@ -65,24 +63,34 @@ def render_gaussians(background, image_height, image_width, means2D, depths, rad
     if timing:
         args["stats_collector"]["forward_render_time"] = ms
     dev = means2D.device
-    out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
-    out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
+    if render_geo:
+        out_all_map, out_plane_depth = _r._render_geo_forward_raw(means2D.size(0), H, W, tan_fovx, tan_fovy, all_map,
+                                                                  compute_locally, R, geom, binning, img,
+                                                                  bool(debug))
+    else:
+        out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
+        out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
     return R, color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth, geom, binning, img
 
 
 def render_gaussians_backward(background, tan_fovx, tan_fovy, all_map_pixels, all_maps, R, geomBuffer, binningBuffer,
                               imageBuffer, compute_locally, dL_dout_color, dL_dout_all_map, dL_dout_plane_depth,
                               means2D, conic_opacity, rgb, render_geo, debug, args=None):
-    if render_geo:
-        raise NotImplementedError("render_geo=True is not supported")
     H, W = int(dL_dout_color.size(1)), int(dL_dout_color.size(2))
     timing = _r._want_timing(args)
-    dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _r._render_backward_raw(
-        background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, geomBuffer, binningBuffer, imageBuffer,
-        dL_dout_color.contiguous(), 3, timing, bool(debug))
+    if render_geo:
+        (dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms,
+         dL_dall_map) = _r._render_backward_raw(
+            background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, geomBuffer, binningBuffer,
+            imageBuffer, dL_dout_color.contiguous(), 3, timing, bool(debug),
+            geo=(tan_fovx, tan_fovy, all_map_pixels, all_maps, dL_dout_all_map, dL_dout_plane_depth))
+    else:
+        dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _r._render_backward_raw(
+            background, int(R), H, W, means2D, conic_opacity, rgb, compute_locally, geomBuffer, binningBuffer,
+            imageBuffer, dL_dout_color.contiguous(), 3, timing, bool(debug))
+        dL_dall_map = torch.zeros((means2D.size(0), 5), device=means2D.device, dtype=torch.float32)
     if timing:
         args["stats_collector"]["backward_render_time"] = ms
-    dL_dall_map = torch.zeros((means2D.size(0), 5), device=means2D.device, dtype=torch.float32)
     return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, dL_dall_map
 
 

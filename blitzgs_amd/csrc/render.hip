@@ -2535,6 +2535,12 @@ __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uin
 // alpha * T and a count added to the Gaussian's accumulators, one atomic per
 // wave and Gaussian).
 constexpr int BLEND_SPLIT = 0, BLEND_FULL = 1, BLEND_SIMP = 2;
+// render_geo of the split path (reference _r forward.cu:381-384,407-412): a
+// second walk of the split render's lists that blends the five geometry
+// maps (all_map, P x 5) with the colour's weights and writes them and the
+// plane depth, and nothing else
+constexpr int BLEND_GEO = 4;
+constexpr int NUM_MAPS = 5;   // NUM_ALL_MAP (_r config.h:24)
 
 struct FwdOut {
     float* out_color;
@@ -2547,6 +2553,10 @@ struct FwdOut {
     float* accum_max_count;        // full (null: flag_max_count off), simp
     float* accum_weights;          // simp
     int32_t* accum_weights_count;  // simp
+    const float* all_map;          // geo: (P,5)
+    float* out_all_map;            // geo: (5,H,W)
+    float* out_plane_depth;        // geo: (H,W)
+    float focal_x, focal_y, cx, cy;   // geo: the plane depth's pixel rays
 };
 
 template <int MODE>
@@ -2568,13 +2578,20 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     float* __restrict__ out_color = O.out_color;
     if (cl != nullptr && !cl[tile]) {
         if (inside) {
-            out_color[pid] = 0.f; out_color[HW + pid] = 0.f; out_color[2 * HW + pid] = 0.f;
-            O.final_T[pid] = 0.f; O.n_contrib_px[pid] = 0;
-            if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = 0;
+            if constexpr (MODE == BLEND_GEO) {
+                for (int c = 0; c < NUM_MAPS; c++) O.out_all_map[c * HW + pid] = 0.f;
+                O.out_plane_depth[pid] = 0.f;
+            } else {
+                out_color[pid] = 0.f; out_color[HW + pid] = 0.f; out_color[2 * HW + pid] = 0.f;
+                O.final_T[pid] = 0.f; O.n_contrib_px[pid] = 0;
+                if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = 0;
+            }
         }
         return;
     }
     __shared__ Stage st;
+    __shared__ float st_map[MODE == BLEND_GEO ? NUM_MAPS * 64 : 1];   // geo: the staged entries' maps
+    [[maybe_unused]] float Mv[NUM_MAPS] = {0.f, 0.f, 0.f, 0.f, 0.f};
 
     const uint2 range = ranges[tile];
     const int n = (int)(range.y - range.x);
@@ -2608,6 +2625,13 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         const bool keep = k < n && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
         const uint64_t km = gs::ballot(keep);
         if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
+        if constexpr (MODE == BLEND_GEO) {
+            if (keep) {
+                const int slot = gs::rank_below(km);
+                const float* m = O.all_map + (size_t)NUM_MAPS * r_cur.gid;
+                for (int c = 0; c < NUM_MAPS; c++) st_map[c * 64 + slot] = m[c];
+            }
+        }
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
         // T only decreases, so a batch that starts with no live pixel above
@@ -2615,11 +2639,16 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(px_st.T > 0.5f) != 0;
         // Branch-free blend of one staged entry: every lane evaluates it and
         // the state changes are selects, so no exec-mask bookkeeping.
-        auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
+        auto blend = [&](const float4& A, const float4& B, const float4& Cc, [[maybe_unused]] int jj) {
             const FwdStep f = fwd_blend_step(px_st, A, B, Cc, pxf, pyf);
             const bool upd = f.upd, observe = f.observe;
             const float wgt = f.wgt;
-            if (MODE == BLEND_SPLIT) {
+            if constexpr (MODE == BLEND_GEO) {
+                // the colour's update rule: a pixel that does not take the
+                // entry adds map * 0
+                const float w = upd ? wgt : 0.f;
+                for (int c = 0; c < NUM_MAPS; c++) Mv[c] = __builtin_fmaf(st_map[c * 64 + jj], w, Mv[c]);
+            } else if constexpr (MODE == BLEND_SPLIT) {
                 if (!obs_batch) return;
                 const uint64_t m = gs::ballot(observe);
                 if (m != 0) {
@@ -2649,10 +2678,10 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         for (int j = 0; j < cnt; j += 2) {
             if (gs::ballot(px_st.T > 0.0f) == 0) break;
             A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
-            blend(A0, B0, D0);
+            blend(A0, B0, D0, j);
             if (j + 1 >= cnt) break;   // (the finished-pixel test runs once per pair)
             A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
-            blend(A1, B1, D1);
+            blend(A1, B1, D1, j + 1);
         }
         __syncthreads();
         r_cur = r_nxt;
@@ -2660,6 +2689,18 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         id_nxt = id_nn;
     }
 
+    if constexpr (MODE == BLEND_GEO) {
+        // plane depth (reference _r forward.cu:411): M4 / -(M0 rx + M1 ry + M2
+        // + 1e-8), the 1e-8 a double literal there: the sum in float, the rest
+        // in double
+        if (inside) {
+            for (int c = 0; c < NUM_MAPS; c++) O.out_all_map[c * HW + pid] = Mv[c];
+            const float rx = (pxf - O.cx) / O.focal_x, ry = (pyf - O.cy) / O.focal_y;
+            const float sdot = __builtin_fmaf(Mv[0], rx, Mv[1] * ry) + Mv[2];
+            O.out_plane_depth[pid] = (float)((double)Mv[4] / -((double)sdot + 1.0e-8));
+        }
+        return;
+    }
     if (inside) {
         const float Tf = __builtin_fabsf(px_st.T);
         O.final_T[pid] = Tf;
@@ -2991,6 +3032,20 @@ __global__ __launch_bounds__(256) void unpack_grads_kernel(int P, const int* __r
     gs::st_stream(&g_col[3 * (size_t)i + 2], c.z);
 }
 
+// render_geo: dL/dall_map (P,5) from accumulator slots 11..15 of the listed
+// Gaussians (cidx_of[i] >= 0), zeros for the others and when nothing was
+// listed (cidx_of null)
+__global__ __launch_bounds__(256) void unpack_map_grads_kernel(int P, const int* __restrict__ cidx_of,
+                                                               const float* __restrict__ gacc,
+                                                               float* __restrict__ g_map)
+{
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= P) return;
+    const int cx = cidx_of != nullptr ? cidx_of[i] : -1;
+    for (int c = 0; c < NUM_MAPS; c++)
+        g_map[(size_t)NUM_MAPS * i + c] = cx >= 0 ? gacc[(size_t)cx * 16 + 11 + c] : 0.f;
+}
+
 // Per-pixel state and constants of the backward blend, and the backward of
 // one staged entry for one pixel: updates the state and returns whether the
 // pixel blends the entry, with its eleven gradient terms in vals (dmean x, y,
@@ -3042,10 +3097,14 @@ __device__ __forceinline__ BwdEval bwd_eval(const BwdConst& k, const float4& A, 
 // Branch-free: every lane applies the entry; a lane whose pixel does not
 // blend it (past its last contributor, power > 0, alpha < 1/255) gets zero
 // gradient factors and unchanged state, through selects on three factors
-// instead of per-value zeroing.
-template <bool FULL>
-__device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const float4& A, const float4& B,
-                                          const float4& Cc, const BwdEval& e, float (&vals)[12])
+// instead of per-value zeroing.  GEO (render_geo): m_dp is the entry's five
+// maps dotted with the pixel's map gradients; the maps join the colour in
+// every dot product (the accumulation is the same linear rule for all eight
+// channels).  Returns alpha T, the factor of the colour and map gradients.
+template <bool FULL, bool GEO = false>
+__device__ __forceinline__ float bwd_apply(BwdPixel& p, const BwdConst& k, const float4& A, const float4& B,
+                                           const float4& Cc, const BwdEval& e, float (&vals)[12],
+                                           [[maybe_unused]] float m_dp = 0.f)
 {
     const bool valid = e.valid;
     const float dx = e.dx, dy = e.dy;
@@ -3066,7 +3125,8 @@ __device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const 
     // a lane that does not blend the entry updates acc with factor 0
     const float la = valid ? p.last_alpha : 0.f;
     p.acc_dp = __builtin_fmaf(la, p.last_dp - p.acc_dp, p.acc_dp);
-    const float c_dp = __builtin_fmaf(B.z, k.dp0, __builtin_fmaf(B.w, k.dp1, Cc.x * k.dp2));
+    float c_dp = __builtin_fmaf(B.z, k.dp0, __builtin_fmaf(B.w, k.dp1, Cc.x * k.dp2));
+    if constexpr (GEO) c_dp += m_dp;
     p.last_dp = valid ? c_dp : p.last_dp;
     p.last_alpha = valid ? alpha : p.last_alpha;
     float dL_dalpha = c_dp - p.acc_dp;
@@ -3095,17 +3155,30 @@ __device__ __forceinline__ void bwd_apply(BwdPixel& p, const BwdConst& k, const 
     // slot 11 is never read back: any register that is dead here fills it
     // (no zero has to be materialised for it)
     vals[8] = gc0; vals[9] = gc1; vals[10] = gc2; vals[11] = dx;
+    return dchannel_dcolor;
 }
+
+// render_geo's backward inputs (reference _r backward.cu:335-347)
+struct GeoBwd {
+    const float* all_map;     // (P,5)
+    const float* map_px;      // (5,H,W): the forward's out_all_map
+    const float* dL_dmaps;    // (5,H,W)
+    const float* dL_dplane;   // (H,W)
+    float fx, fy;             // focal lengths
+};
 
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no
 // conic or opacity gradient from a pixel where opacity * G > 0.99 (the alpha
 // clamp is active); |dL/dmean2D| is accumulated but not written out.
-template <bool FULL>
+// GEO: render_geo (reference _r backward.cu:393-405,427-432,476-490): the five
+// maps enter dL/dalpha beside the colour, and their gradients
+// alpha T dL/dmap go to accumulator slots 11..15.
+template <bool FULL, bool GEO = false>
 __global__ __launch_bounds__(64) void render_bwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
-    const float* __restrict__ dL_dpixels, float* __restrict__ gacc)
+    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G)
 {
     unsigned tile, quad, tx, ty;
     if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
@@ -3124,7 +3197,29 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     const int maxlast = gs::wave_max_i(last);
     if (maxlast == 0) return;
 
+    // render_geo: the pixel's map gradients, plus the plane depth's
+    // D = M4 / -(n . ray + 1e-8) through n = M0..2 and M4 (the ray as the
+    // reference's backward takes it: (x - W / 2) / fx in double)
+    [[maybe_unused]] float dm[NUM_MAPS] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (GEO) {
+        if (inside) {
+            for (int c = 0; c < NUM_MAPS; c++) dm[c] = G.dL_dmaps[c * HW + pid];
+            const float rx = (float)(((double)px - (double)W * 0.5) / (double)G.fx);
+            const float ry = (float)(((double)py - (double)H * 0.5) / (double)G.fy);
+            const float n0 = G.map_px[pid], n1 = G.map_px[HW + pid], n2 = G.map_px[2 * HW + pid];
+            const float distance = G.map_px[4 * HW + pid];
+            const float tmp = (float)((double)(n0 * rx + n1 * ry + n2) + 1.0e-8);
+            const float g = G.dL_dplane[pid];
+            const float q = distance / (tmp * tmp);
+            dm[4] += -g / tmp;
+            dm[0] += g * (q * rx);
+            dm[1] += g * (q * ry);
+            dm[2] += g * q;
+        }
+    }
+
     __shared__ Stage st;
+    __shared__ float st_map[GEO ? NUM_MAPS * 64 : 1];
 
     const uint32_t* list = clist + ranges[tile].x;
     const float qx0 = (float)qx, qy0 = (float)qy;
@@ -3141,13 +3236,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     uint32_t id_cur = maxlast - 1 - lane >= 0 ? list[maxlast - 1 - lane] : 0u;
     uint32_t id_nxt = maxlast - 65 - lane >= 0 ? list[maxlast - 65 - lane] : 0u;
     Rec r_cur{};
-    if (maxlast - 1 - lane >= 0) r_cur = load_rec<false>(rec, id_cur);
+    if (maxlast - 1 - lane >= 0) r_cur = load_rec<GEO>(rec, id_cur);
 
     for (int top = maxlast; top > 0; top -= 64) {
         const int k = top - 1 - lane;
         Rec r_nxt{};
         uint32_t id_nn = 0;
-        if (k - 64 >= 0) r_nxt = load_rec<false>(rec, id_nxt);
+        if (k - 64 >= 0) r_nxt = load_rec<GEO>(rec, id_nxt);
         if (k - 128 >= 0) id_nn = list[k - 128];
         // stage positions top-1, top-2, ..., top-64, keeping only Gaussians
         // that can reach a pixel whose last contributor lies past top-64
@@ -3158,6 +3253,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
         const bool keep = k >= 0 && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
         const uint64_t km = gs::ballot(keep);
         if (keep) stage_put(st, gs::rank_below(km), r_cur, id_cur, k);
+        if constexpr (GEO) {
+            if (keep) {
+                const int slot = gs::rank_below(km);
+                const float* m = G.all_map + (size_t)NUM_MAPS * r_cur.gid;
+                for (int c = 0; c < NUM_MAPS; c++) st_map[c * 64 + slot] = m[c];
+            }
+        }
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
         for (int j = 0; j < cnt; j++) {
@@ -3167,11 +3269,29 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
             const BwdEval e = bwd_eval(kc, A, B, Cc);
             if (gs::ballot(e.valid) == 0) continue;   // no lane blends the entry: nothing changes
             float vals[12];
-            bwd_apply<FULL>(px_st, kc, A, B, Cc, e, vals);
-            const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));   // one Gaussian per entry
-            const float tot = gs::wave_sum12<true>(vals);
-            // the eleven totals of one Gaussian land in one 64-byte accumulator
-            if (my_k >= 0 && my_k < 11) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
+            if constexpr (GEO) {
+                float mv[NUM_MAPS];
+                for (int c = 0; c < NUM_MAPS; c++) mv[c] = st_map[c * 64 + j];
+                float m_dp = mv[0] * dm[0];
+                for (int c = 1; c < NUM_MAPS; c++) m_dp = __builtin_fmaf(mv[c], dm[c], m_dp);
+                const float dcc = bwd_apply<FULL, true>(px_st, kc, A, B, Cc, e, vals, m_dp);
+                const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));
+                // slot 11: the first map's gradient; the other four in a
+                // second reduction, into slots 12..15
+                vals[11] = dcc * dm[0];
+                float v2[12] = {dcc * dm[1], dcc * dm[2], dcc * dm[3], dcc * dm[4], 0.f, 0.f,
+                                0.f,         0.f,         0.f,         0.f,         0.f, 0.f};
+                const float tot = gs::wave_sum12<true>(vals);
+                const float tot2 = gs::wave_sum12<false>(v2);
+                if (my_k >= 0) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
+                if (my_k >= 0 && my_k < 4) unsafeAtomicAdd(gacc + (size_t)cx * 16 + 12 + my_k, tot2);
+            } else {
+                bwd_apply<FULL>(px_st, kc, A, B, Cc, e, vals);
+                const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));   // one Gaussian per entry
+                const float tot = gs::wave_sum12<true>(vals);
+                // the eleven totals of one Gaussian land in one 64-byte accumulator
+                if (my_k >= 0 && my_k < 11) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
+            }
         }
         __syncthreads();
         r_cur = r_nxt;
@@ -3711,8 +3831,10 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
 int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                          const float* conic_opacity, const uint8_t* compute_locally, void* geom, const void* binning,
                          const void* img, const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
-                         float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
+                         float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream,
+                         const GeoBwd* geo = nullptr, float* dL_dall_map = nullptr)
 {
+    GS_REQUIRE(geo == nullptr || (!full && dL_dall_map != nullptr), "render_geo: split path, dL_dall_map non-null");
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
     GS_REQUIRE(dL_dmeans2D_stride == 2 || dL_dmeans2D_stride == 3, "dL_dmeans2D row stride must be 2 or 3");
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)dL_dconic_opacity & 15) == 0 &&
@@ -3741,12 +3863,20 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<true>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
-                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
+                                        GeoBwd{}));
+        } else if (geo != nullptr) {
+            GS_TIMED("render_bwd_geo_kernel", stream,
+                     hipLaunchKernelGGL((render_bwd_kernel<false, true>), dim3(nblk), dim3(64), 0, stream, W, H, gx,
+                                        gy, sgx, NS, rng, clist, recs, compute_locally, bg,
+                                        at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
+                                        reinterpret_cast<float*>(gacc), *geo));
         } else {
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<false>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
-                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc)));
+                                        at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
+                                        GeoBwd{}));
         }
         GS_LAUNCH_CHECK("render_bwd_kernel");
     }
@@ -3759,6 +3889,50 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                                 (((uintptr_t)dL_dmeans2D | (uintptr_t)dL_dmeans2D_abs | (uintptr_t)dL_dcolors) & 15) == 0,
                                 0.5f * (float)W, 0.5f * (float)H));
     GS_LAUNCH_CHECK("unpack_grads_kernel");
+    if (geo != nullptr) {
+        GS_TIMED("unpack_map_grads_kernel", stream,
+                 hipLaunchKernelGGL(unpack_map_grads_kernel, dim3(gs_div_up((size_t)P, 256)), dim3(256), 0, stream,
+                                    P, R > 0 ? at<const int>(geom, g.cidx_of) : nullptr,
+                                    reinterpret_cast<const float*>(gacc), dL_dall_map));
+        GS_LAUNCH_CHECK("unpack_map_grads_kernel");
+    }
+    return GS_OK;
+}
+
+// render_geo's maps (reference _r forward.cu:381-384,407-412): a second walk
+// of a completed split forward's lists (geom / binning / img, R as there).
+int render_geo_forward_impl(int P, int64_t R, int W, int H, float tan_fovx, float tan_fovy, const float* all_map,
+                            const uint8_t* compute_locally, const void* geom, const void* binning, const void* img,
+                            float* out_all_map, float* out_plane_depth, hipStream_t stream)
+{
+    GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
+    GS_REQUIRE(geom != nullptr && img != nullptr && (R == 0 || binning != nullptr),
+               "geom, binning and img must be the forward's workspaces");
+    GS_REQUIRE((P == 0 || all_map != nullptr) && out_all_map != nullptr && out_plane_depth != nullptr,
+               "all_map, out_all_map and out_plane_depth must be non-null");
+    GS_REQUIRE(tan_fovx > 0.f && tan_fovy > 0.f, "tan_fovx / tan_fovy must be positive");
+    const GeomLayout g = geom_layout(P, W, H);
+    const ImgLayout il = img_layout(W, H);
+    const BinLayout bl = bin_layout(R);
+    const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
+    FwdOut O{};
+    O.all_map = all_map;
+    O.out_all_map = out_all_map;
+    O.out_plane_depth = out_plane_depth;
+    // the render host's camera (rasterize_points.cu:325-326,339): focal
+    // lengths W / (2 tan_fovx), H / (2 tan_fovy) and centre (W / 2, H / 2), in float
+    O.focal_x = (float)W / (2.0f * tan_fovx);
+    O.focal_y = (float)H / (2.0f * tan_fovy);
+    O.cx = (float)W * 0.5f;
+    O.cy = (float)H * 0.5f;
+    unsigned sgx, NS;
+    const unsigned nblk = blend_grid(gx, gy, sgx, NS);
+    GS_TIMED("render_geo_kernel", stream,
+             hipLaunchKernelGGL(render_fwd_kernel<BLEND_GEO>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx, NS,
+                                at<const uint2>(img, il.ranges),
+                                R > 0 ? at<const uint32_t>(binning, bl.clist) : nullptr,
+                                at<const float4>(geom, g.rec), compute_locally, nullptr, O));
+    GS_LAUNCH_CHECK("render_geo_kernel");
     return GS_OK;
 }
 
@@ -3877,6 +4051,40 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
     return render_backward_impl(false, P, R, W, H, bg, means2D, conic_opacity, compute_locally, geom, binning, img,
                                 dL_dpixels, dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity,
                                 dL_dcolors, stream);
+}
+
+extern "C" int gs_render_geo_forward(int P, int64_t R, int W, int H, float tan_fovx, float tan_fovy,
+                                     const float* all_map, const uint8_t* compute_locally, const void* geom,
+                                     const void* binning, const void* img, float* out_all_map,
+                                     float* out_plane_depth, hipStream_t stream)
+{
+    gs::clear_error();
+    return render_geo_forward_impl(P, R, W, H, tan_fovx, tan_fovy, all_map, compute_locally, geom, binning, img,
+                                   out_all_map, out_plane_depth, stream);
+}
+
+extern "C" int gs_render_backward_geo(int P, int64_t R, int W, int H, const float* bg, float tan_fovx,
+                                      float tan_fovy, const float* all_map_pixels, const float* all_maps,
+                                      const float* means2D, const float* conic_opacity, const float* rgb,
+                                      const uint8_t* compute_locally, void* geom, const void* binning,
+                                      const void* img, const float* dL_dpixels, const float* dL_dout_all_map,
+                                      const float* dL_dout_plane_depth, float* dL_dmeans2D, int dL_dmeans2D_stride,
+                                      float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
+                                      float* dL_dall_map, hipStream_t stream)
+{
+    gs::clear_error();
+    (void)rgb;
+    GS_REQUIRE(dL_dmeans2D_abs != nullptr && dL_dall_map != nullptr, "dL_dmeans2D_abs and dL_dall_map must be non-null");
+    GS_REQUIRE(P == 0 || (all_map_pixels != nullptr && all_maps != nullptr && dL_dout_all_map != nullptr &&
+                          dL_dout_plane_depth != nullptr),
+               "all_map_pixels, all_maps, dL_dout_all_map and dL_dout_plane_depth must be non-null");
+    GS_REQUIRE(tan_fovx > 0.f && tan_fovy > 0.f, "tan_fovx / tan_fovy must be positive");
+    // the backward host's focal lengths (rasterizer_impl.cu:760-761)
+    const GeoBwd geo{all_maps, all_map_pixels, dL_dout_all_map, dL_dout_plane_depth, (float)W / (2.0f * tan_fovx),
+                     (float)H / (2.0f * tan_fovy)};
+    return render_backward_impl(false, P, R, W, H, bg, means2D, conic_opacity, compute_locally, geom, binning, img,
+                                dL_dpixels, dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity,
+                                dL_dcolors, stream, &geo, dL_dall_map);
 }
 
 extern "C" int gs_render_full_count(int P, int W, int H, const float* means2D, const int* radii, const float* rects,

@@ -265,8 +265,30 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     return R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms
 
 
+def _render_geo_forward_raw(P, H, W, tanfovx, tanfovy, all_maps, compute_locally, R, geom, binning, img,
+                            debug=False):
+    """render_geo's maps for a completed split forward of P Gaussians (R,
+    geom / binning / img as it returned them): out_all_map (5,H,W),
+    out_plane_depth (1,H,W)."""
+    dev = geom.device
+    lib = _lib.load()
+    cl = _tile_mask(compute_locally, H, W, dev)
+    if all_maps is None or tuple(all_maps.shape) != (P, 5):
+        raise RuntimeError(f"render_geo needs all_map of shape ({P}, 5)")
+    all_maps = _dev_f32(all_maps, dev)
+    maps = torch.empty((6, H, W), device=dev, dtype=torch.float32)
+    check(lib.gs_render_geo_forward(P, R, W, H, float(tanfovx), float(tanfovy), ptr(all_maps), ptr(cl), ptr(geom),
+                                    ptr(binning), ptr(img), ptr(maps[:5]), ptr(maps[5:]), _stream(dev)),
+          "gs_render_geo_forward")
+    _lib.debug_sync(debug, "gs_render_geo_forward")
+    return maps[:5], maps[5:]
+
+
 def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img, dL_dpixels,
-                         m2d_stride=2, timing=False, debug=False):
+                         m2d_stride=2, timing=False, debug=False, geo=None):
+    """geo (render_geo): (tanfovx, tanfovy, all_map_pixels, all_maps,
+    dL_dout_all_map, dL_dout_plane_depth); dL/dall_map (P,5) is then returned
+    after the timing, else None."""
     dev = means2D.device
     P = means2D.size(0)
     lib = _lib.load()
@@ -284,16 +306,38 @@ def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_local
     if timing:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
-    check(lib.gs_render_backward(P, R, W, H, ptr(bg), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
-                                 ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D), m2d_stride,
-                                 ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors), _stream(dev)),
-          "gs_render_backward")
+    dL_dall_map = None
+    if geo is None:
+        check(lib.gs_render_backward(P, R, W, H, ptr(bg), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
+                                     ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D),
+                                     m2d_stride, ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors),
+                                     _stream(dev)), "gs_render_backward")
+    else:
+        tanfovx, tanfovy, map_px, all_maps, dmaps, dplane = geo
+        if all_maps is None or tuple(all_maps.shape) != (P, 5):
+            raise RuntimeError(f"render_geo needs all_map of shape ({P}, 5)")
+        for name, t, n in (("all_map_pixels", map_px, 5), ("dL_dout_all_map", dmaps, 5),
+                           ("dL_dout_plane_depth", dplane, 1)):
+            if t is not None and t.numel() != n * H * W:
+                raise RuntimeError(f"{name} must hold {n}x{H}x{W} values, got {tuple(t.shape)}")
+        map_px, all_maps = _dev_f32(map_px, dev), _dev_f32(all_maps, dev)
+        dmaps = _dev_f32(dmaps, dev) if dmaps is not None else torch.zeros((5, H, W), **f32)
+        dplane = _dev_f32(dplane, dev) if dplane is not None else torch.zeros((1, H, W), **f32)
+        dL_dall_map = torch.empty((P, 5), **f32)
+        check(lib.gs_render_backward_geo(P, R, W, H, ptr(bg), float(tanfovx), float(tanfovy), ptr(map_px),
+                                         ptr(all_maps), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
+                                         ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dmaps),
+                                         ptr(dplane), ptr(dL_dmeans2D), m2d_stride, ptr(dL_dmeans2D_abs),
+                                         ptr(dL_dconic_opacity), ptr(dL_dcolors), ptr(dL_dall_map), _stream(dev)),
+              "gs_render_backward_geo")
     _lib.debug_sync(debug, "gs_render_backward")
     ms = None
     if timing:
         ev1.record()
         ev1.synchronize()
         ms = ev0.elapsed_time(ev1)
+    if geo is not None:
+        return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms, dL_dall_map
     return dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms
 
 
@@ -302,9 +346,10 @@ class _RenderGaussians(torch.autograd.Function):
     def forward(ctx, means2D, means2D_abs, conic_opacity, rgb, all_maps, depths, radii, compute_locally,
                 extended_compute_locally, raster_settings, cuda_args):
         rs = raster_settings
-        if getattr(rs, "render_geo", False):
-            raise NotImplementedError("render_geo=True (normal / plane-depth maps) is not supported")
-        # the backward reads only dL/dcolor: unused outputs need no zero-filled gradients
+        render_geo = bool(getattr(rs, "render_geo", False))
+        if render_geo and (all_maps is None or tuple(all_maps.shape) != (means2D.size(0), 5)):
+            raise RuntimeError("render_geo needs all_map of shape (P, 5)")
+        # absent output gradients stay None (no zero-filled tensors)
         ctx.set_materialize_grads(False)
         use_ext = isinstance(cuda_args, dict) and bool(cuda_args.get("avoid_pixel_all2all", False))
         cl = extended_compute_locally if use_ext else compute_locally
@@ -316,9 +361,15 @@ class _RenderGaussians(torch.autograd.Function):
         if timing:
             cuda_args["stats_collector"]["forward_render_time"] = ms
         dev = means2D.device
-        # the geometry maps (render_geo off: zeros) share one zero fill
-        maps = torch.zeros((6, H, W), device=dev, dtype=torch.float32)
-        out_all_map, out_plane_depth = maps[:5], maps[5:]
+        if render_geo:
+            # the five geometry maps and the plane depth (_r forward.cu:381-384,407-412)
+            out_all_map, out_plane_depth = _render_geo_forward_raw(means2D.size(0), H, W, rs.tanfovx, rs.tanfovy,
+                                                                   all_maps, cl, R, geom, binning, img,
+                                                                   bool(rs.debug))
+        else:
+            # render_geo off: both are zeros (one fill)
+            maps = torch.zeros((6, H, W), device=dev, dtype=torch.float32)
+            out_all_map, out_plane_depth = maps[:5], maps[5:]
         ctx.raster_settings = rs
         ctx.cuda_args = cuda_args
         ctx.num_rendered = R
@@ -337,14 +388,23 @@ class _RenderGaussians(torch.autograd.Function):
         if grad_color is None:
             grad_color = torch.zeros((3, H, W), device=means2D.device, dtype=torch.float32)
         timing = _want_timing(ctx.cuda_args)
-        dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
-            rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
-            grad_color.contiguous(), 2, timing, bool(rs.debug))
+        dL_dall_map = None
+        if getattr(rs, "render_geo", False):
+            (dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms,
+             dL_dall_map) = _render_backward_raw(
+                rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
+                grad_color.contiguous(), 2, timing, bool(rs.debug),
+                geo=(rs.tanfovx, rs.tanfovy, all_map_pixels, all_maps, grad_out_all_map, grad_out_plane_depth))
+        else:
+            dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
+                rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
+                grad_color.contiguous(), 2, timing, bool(rs.debug))
+            if ctx.needs_input_grad[4]:
+                dL_dall_map = torch.zeros_like(all_maps)
         if timing:
             ctx.cuda_args["stats_collector"]["backward_render_time"] = ms
-        dL_dall_map = None
-        if ctx.needs_input_grad[4]:
-            dL_dall_map = torch.zeros_like(all_maps)
+        if not ctx.needs_input_grad[4]:
+            dL_dall_map = None
         return (dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, dL_dall_map,
                 None, None, None, None, None, None)
 

@@ -167,6 +167,37 @@ int gs_render_backward(int P, int64_t R, int image_width, int image_height, cons
                        float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
                        gs_stream_t stream);
 
+/* render_geo of the render forward (rasterize_points.cu:273-361 with
+ * render_geo = true; kernel cuda_rasterizer/forward.cu:381-384,407-412):
+ * the five geometry maps all_map (P,5) blended with the colour's weights
+ * into out_all_map (5,H,W), and the plane depth out_plane_depth (H,W) =
+ * map4 / -(map0 rx + map1 ry + map2 + 1e-8) with the pixel ray
+ * (rx, ry) = ((x - W/2) / focal_x, (y - H/2) / focal_y), focal = W / (2 tan_fovx),
+ * H / (2 tan_fovy).  Runs after a completed gs_render_forward or
+ * gs_render_forward_reserved (same P, R, W, H, compute_locally and
+ * workspaces), as a second walk of its lists: the colour outputs are
+ * untouched.  Non-local tiles get zeros. */
+int gs_render_geo_forward(int P, int64_t R, int image_width, int image_height, float tan_fovx,
+                          float tan_fovy, const float* all_map, const uint8_t* compute_locally,
+                          const void* geom, const void* binning, const void* img, float* out_all_map,
+                          float* out_plane_depth, gs_stream_t stream);
+
+/* gs_render_backward with render_geo = true (RenderGaussiansBackwardCUDA,
+ * rasterize_points.cu:363-436; kernel backward.cu:393-405,427-432,476-490):
+ * the maps enter dL/dalpha beside the colour.  all_map_pixels: the
+ * forward's out_all_map; all_maps (P,5); dL_dout_all_map (5,H,W);
+ * dL_dout_plane_depth (H,W).  Writes dL_dall_map (P,5) as well as every
+ * output of gs_render_backward. */
+int gs_render_backward_geo(int P, int64_t R, int image_width, int image_height, const float* bg,
+                           float tan_fovx, float tan_fovy, const float* all_map_pixels,
+                           const float* all_maps, const float* means2D, const float* conic_opacity,
+                           const float* rgb, const uint8_t* compute_locally, void* geom,
+                           const void* binning, const void* img, const float* dL_dpixels,
+                           const float* dL_dout_all_map, const float* dL_dout_plane_depth,
+                           float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
+                           float* dL_dconic_opacity, float* dL_dcolors, float* dL_dall_map,
+                           gs_stream_t stream);
+
 /* Views into the opaque buffers, for tests and tools:
  *   binning: point_list uint32 (R), point_list_keys uint64 (R) -- written by
  *            gs_render_point_list, not by the forward

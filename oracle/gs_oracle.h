@@ -88,6 +88,39 @@ void o_render_bwd(int P, int W, int H, const float* bg,
                   float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
                   float* dL_dopacity, float* dL_dcolors);
 
+/* render_geo of the _r render (NUM_ALL_MAP = 5 channels, config.h:24). */
+#define O_NUM_MAPS 5
+
+/* The forward's geometry maps (_r forward.cu:381-384,407-412), by a walk of
+ * the same blend as o_render_fwd: out_all_map (5,H,W) = the all_map (P,5)
+ * channels blended with the colour's weights alpha T; out_plane_depth (H,W) =
+ * all_map[4] / -(n . ray + 1e-8), n = channels 0..2, ray = ((x - cx) / focal_x,
+ * (y - cy) / focal_y, 1).  Non-local tiles: zeros. */
+void o_render_geo_fwd(int W, int H, float focal_x, float focal_y, float cx, float cy,
+                      const float* means2D, const float* conic_opacity, const float* all_map,
+                      const uint8_t* compute_locally, const uint32_t* ranges, const uint32_t* point_list,
+                      float* out_all_map, float* out_plane_depth);
+
+/* The backward's render_geo inputs and output (_r backward.cu:335-347). */
+typedef struct {
+    float fx, fy;                  /* focal lengths W / (2 tan_fovx), H / (2 tan_fovy) */
+    const float* all_maps;         /* (P,5) */
+    const float* all_map_pixels;   /* (5,H,W): the forward's out_all_map */
+    const float* dL_dmaps;         /* (5,H,W) */
+    const float* dL_dplane;        /* (H,W) */
+    float* dL_dall_map;            /* (P,5), accumulated */
+} OGeoBwd;
+
+/* o_render_bwd with render_geo on (_r backward.cu:393-405,427-432,476-490). */
+void o_render_bwd_geo(int P, int W, int H, const float* bg,
+                      const float* means2D, const float* conic_opacity, const float* rgb,
+                      const uint8_t* compute_locally,
+                      const uint32_t* ranges, const uint32_t* point_list,
+                      const float* final_T, const uint32_t* n_contrib,
+                      const float* dL_dpixels,
+                      float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                      float* dL_dopacity, float* dL_dcolors, const OGeoBwd* geo);
+
 /* ---- full-image path (_f GaussianRasterizer.forward / render_simp) ---- */
 
 /* preprocessCUDA with the full path's arguments (_f forward.cu:165-284,

@@ -12,6 +12,8 @@
  *   getRect(float2,int)       cuda_rasterizer/auxiliary.h:66-76
  *   renderCUDA (forward)      cuda_rasterizer/forward.cu:263-413
  *   renderCUDA (backward)     cuda_rasterizer/backward.cu:324-530
+ *   render_geo maps (fwd)     cuda_rasterizer/forward.cu:381-384,407-412
+ *   render_geo maps (bwd)     cuda_rasterizer/backward.cu:393-405,427-432,476-490
  * The reference sorts with a stable LSD radix sort on bits [0, 32+msb); here a
  * stable merge sort on the full 64-bit key gives the same order (tile ids are
  * below 2^msb, checked in the tests, and depth bits are the low word).
@@ -222,6 +224,62 @@ void o_render_fwd(int P, int W, int H, const float* bg,
     }
 }
 
+/* plane depth of one pixel (_r forward.cu:411): all_map[4] / -(n . ray + 1e-8)
+ * with n = all_map[0..2], ray = (rx, ry, 1); the dot product in float
+ * (fma(n0, rx, n1 ry) + n2), the 1e-8 (a double literal), the negation and
+ * the division in double, stored as float */
+static inline float plane_depth(const float* M, float rx, float ry)
+{
+    const float s = fmaf(M[0], rx, M[1] * ry) + M[2];
+    return (float)((double)M[4] / -((double)s + 1.0e-8));
+}
+
+void o_render_geo_fwd(int W, int H, float focal_x, float focal_y, float cx, float cy,
+                      const float* means2D, const float* conic_opacity, const float* all_map,
+                      const uint8_t* compute_locally, const uint32_t* ranges, const uint32_t* point_list,
+                      float* out_all_map, float* out_plane_depth)
+{
+    const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const int T = gx * gy;
+    const size_t HW = (size_t)H * W;
+    const float alpha_min = 1.0f / 255.0f;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int t = 0; t < T; t++) {
+        const int tx = t % gx, ty = t / gx;
+        const int x0 = tx * OT, y0 = ty * OT;
+        const int x1 = x0 + OT < W ? x0 + OT : W, y1 = y0 + OT < H ? y0 + OT : H;
+        const int local = compute_locally[t] != 0;
+        const uint32_t rs = ranges[2 * t], re = ranges[2 * t + 1];
+        for (int y = y0; y < y1; y++)
+            for (int x = x0; x < x1; x++) {
+                const size_t pid = (size_t)y * W + x;
+                float M[O_NUM_MAPS] = { 0.f, 0.f, 0.f, 0.f, 0.f };
+                if (!local) {
+                    for (int c = 0; c < O_NUM_MAPS; c++) out_all_map[c * HW + pid] = 0.f;
+                    out_plane_depth[pid] = 0.f;
+                    continue;
+                }
+                const float px = (float)x, py = (float)y;
+                float T_ = 1.0f;
+                for (uint32_t k = rs; k < re; k++) {
+                    const uint32_t id = point_list[k];
+                    const float* co = conic_opacity + 4 * (size_t)id;
+                    const float power = o_power(means2D + 2 * (size_t)id, co, px, py);
+                    if (power > 0.0f) continue;
+                    const float alpha = o_fminf(0.99f, co[3] * o_expf(power));
+                    if (alpha < alpha_min) continue;
+                    const float test_T = T_ * (1.0f - alpha);
+                    if (test_T < 0.0001f) break;
+                    const float wgt = alpha * T_;
+                    for (int c = 0; c < O_NUM_MAPS; c++) M[c] = fmaf(all_map[O_NUM_MAPS * (size_t)id + c], wgt, M[c]);
+                    T_ = test_T;
+                }
+                for (int c = 0; c < O_NUM_MAPS; c++) out_all_map[c * HW + pid] = M[c];
+                out_plane_depth[pid] = plane_depth(M, (px - cx) / focal_x, (py - cy) / focal_y);
+            }
+    }
+}
+
 static inline void atomic_addf(float* p, float v)
 {
 #pragma omp atomic
@@ -238,9 +296,10 @@ static void render_bwd_impl(int full, int W, int H, const float* bg,
                             const float* final_T, const uint32_t* n_contrib,
                             const float* dL_dpixels,
                             float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
-                            float* dL_dopacity, float* dL_dcolors)
+                            float* dL_dopacity, float* dL_dcolors, const OGeoBwd* geo)
 {
     const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
+    const size_t HW = (size_t)H * W;
     const int T = gx * gy;
     const float alpha_min = 1.0f / 255.0f;
     const float ddelx_dx = 0.5f * (float)W, ddely_dy = 0.5f * (float)H;
@@ -261,6 +320,23 @@ static void render_bwd_impl(int full, int W, int H, const float* bg,
                 float dpix[3], accum[3] = { 0, 0, 0 }, last_color[3] = { 0, 0, 0 };
                 for (int c = 0; c < 3; c++) dpix[c] = dL_dpixels[(size_t)c * H * W + pid];
                 float last_alpha = 0.f;
+                /* render_geo (_r backward.cu:393-405): the maps' pixel
+                 * gradients, plus the plane depth's through n and distance */
+                float dmap[O_NUM_MAPS], accm[O_NUM_MAPS] = { 0, 0, 0, 0, 0 }, lastm[O_NUM_MAPS] = { 0, 0, 0, 0, 0 };
+                if (geo) {
+                    const float rx = (float)(((double)px - W * 0.5) / geo->fx);
+                    const float ry = (float)(((double)py - H * 0.5) / geo->fy);
+                    for (int c = 0; c < O_NUM_MAPS; c++) dmap[c] = geo->dL_dmaps[c * HW + pid];
+                    const float* mp = geo->all_map_pixels;
+                    const float n0 = mp[pid], n1 = mp[HW + pid], n2 = mp[2 * HW + pid];
+                    const float distance = mp[4 * HW + pid];
+                    const float tmp = (float)((double)(n0 * rx + n1 * ry + n2) + 1.0e-8);
+                    const float g = geo->dL_dplane[pid];
+                    dmap[O_NUM_MAPS - 1] += -g / tmp;
+                    dmap[0] += g * (distance / (tmp * tmp) * rx);
+                    dmap[1] += g * (distance / (tmp * tmp) * ry);
+                    dmap[2] += g * (distance / (tmp * tmp));
+                }
                 float bg_dot = 0.f;
                 for (int c = 0; c < 3; c++) bg_dot += bg[c] * dpix[c];
                 /* contributor index k-rs+1 runs from the back; skip >= last */
@@ -285,6 +361,15 @@ static void render_bwd_impl(int full, int W, int H, const float* bg,
                         last_color[c] = col;
                         dL_dalpha += (col - accum[c]) * dpix[c];
                         atomic_addf(&dL_dcolors[3 * (size_t)id + c], dchannel_dcolor * dpix[c]);
+                    }
+                    if (geo) {
+                        for (int c = 0; c < O_NUM_MAPS; c++) {
+                            const float m = geo->all_maps[O_NUM_MAPS * (size_t)id + c];
+                            accm[c] = last_alpha * lastm[c] + (1.f - last_alpha) * accm[c];
+                            lastm[c] = m;
+                            dL_dalpha += (m - accm[c]) * dmap[c];
+                            atomic_addf(&geo->dL_dall_map[O_NUM_MAPS * (size_t)id + c], dchannel_dcolor * dmap[c]);
+                        }
                     }
                     dL_dalpha *= T_;
                     last_alpha = alpha;
@@ -323,7 +408,21 @@ void o_render_bwd(int P, int W, int H, const float* bg,
 {
     (void)P;
     render_bwd_impl(0, W, H, bg, means2D, conic_opacity, rgb, compute_locally, ranges, point_list, final_T,
-                    n_contrib, dL_dpixels, dL_dmean2D, dL_dmean2D_abs, dL_dconic, dL_dopacity, dL_dcolors);
+                    n_contrib, dL_dpixels, dL_dmean2D, dL_dmean2D_abs, dL_dconic, dL_dopacity, dL_dcolors, NULL);
+}
+
+void o_render_bwd_geo(int P, int W, int H, const float* bg,
+                      const float* means2D, const float* conic_opacity, const float* rgb,
+                      const uint8_t* compute_locally,
+                      const uint32_t* ranges, const uint32_t* point_list,
+                      const float* final_T, const uint32_t* n_contrib,
+                      const float* dL_dpixels,
+                      float* dL_dmean2D, float* dL_dmean2D_abs, float* dL_dconic,
+                      float* dL_dopacity, float* dL_dcolors, const OGeoBwd* geo)
+{
+    (void)P;
+    render_bwd_impl(0, W, H, bg, means2D, conic_opacity, rgb, compute_locally, ranges, point_list, final_T,
+                    n_contrib, dL_dpixels, dL_dmean2D, dL_dmean2D_abs, dL_dconic, dL_dopacity, dL_dcolors, geo);
 }
 
 void o_render_bwd_full(int P, int W, int H, const float* bg,
@@ -335,7 +434,7 @@ void o_render_bwd_full(int P, int W, int H, const float* bg,
 {
     (void)P;
     render_bwd_impl(1, W, H, bg, means2D, conic_opacity, colors, NULL, ranges, point_list, final_T, n_contrib,
-                    dL_dpixels, dL_dmean2D, NULL, dL_dconic, dL_dopacity, dL_dcolors);
+                    dL_dpixels, dL_dmean2D, NULL, dL_dconic, dL_dopacity, dL_dcolors, NULL);
 }
 
 /* ---------------------------------------------------------------- full-image path

@@ -37,7 +37,8 @@ def lib():
         _lib.o_num_threads.restype = C.c_int
         for name in ["o_preprocess_fwd", "o_preprocess_bwd", "o_binning", "o_render_fwd",
                      "o_render_bwd", "o_knn_meandist3", "o_ssim_fwd", "o_ssim_bwd",
-                     "o_vec_expf", "o_vec_logf", "o_local2j_ids_bool", "o_local2j_ids_bool_rect"]:
+                     "o_vec_expf", "o_vec_logf", "o_local2j_ids_bool", "o_local2j_ids_bool_rect",
+                     "o_render_geo_fwd", "o_render_bwd_geo"]:
             getattr(_lib, name).restype = None
         del fp
     return _lib
@@ -192,6 +193,69 @@ def render_bwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, final_
                        _p(out["dL_dopacity"]), _p(out["dL_dcolors"]))
     dc = out["dL_dconic"]
     # rasterize_points.cu:425-433: repack (P,2,2) slots into [c00, c01, c11, opacity]
+    out["dL_dconic_opacity"] = np.stack([dc[:, 0], dc[:, 1], dc[:, 3], out["dL_dopacity"]], axis=1)
+    return out
+
+
+class OGeoBwd(C.Structure):
+    _fields_ = [("fx", C.c_float), ("fy", C.c_float), ("all_maps", C.c_void_p), ("all_map_pixels", C.c_void_p),
+                ("dL_dmaps", C.c_void_p), ("dL_dplane", C.c_void_p), ("dL_dall_map", C.c_void_p)]
+
+
+def focal(W, H, tanfovx, tanfovy):
+    """focal_x, focal_y as the render host computes them in float
+    (_r rasterize_points.cu:325-326): W / (2 tan_fovx), H / (2 tan_fovy)."""
+    fx = np.float32(W) / (np.float32(2.0) * np.float32(tanfovx))
+    fy = np.float32(H) / (np.float32(2.0) * np.float32(tanfovy))
+    return np.float32(fx), np.float32(fy)
+
+
+def render_geo_fwd(W, H, tanfovx, tanfovy, means2D, conic_opacity, all_map, ranges, point_list,
+                   compute_locally=None):
+    """render_geo's maps: out_all_map (5,H,W) and out_plane_depth (1,H,W)."""
+    means2D, conic_opacity, all_map = map(_f32, (means2D, conic_opacity, all_map))
+    assert all_map.shape == (means2D.shape[0], 5)
+    gx, gy = tile_grid(W, H)
+    if compute_locally is None:
+        compute_locally = np.ones(gx * gy, np.uint8)
+    cl = np.ascontiguousarray(compute_locally, dtype=np.uint8).reshape(-1)
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    fx, fy = focal(W, H, tanfovx, tanfovy)
+    out_all_map = np.empty((5, H, W), np.float32)
+    out_plane_depth = np.empty((1, H, W), np.float32)
+    # cx, cy = float(W * 0.5f), float(H * 0.5f) (rasterize_points.cu:339)
+    lib().o_render_geo_fwd(C.c_int(W), C.c_int(H), C.c_float(fx), C.c_float(fy), C.c_float(0.5 * W),
+                           C.c_float(0.5 * H), _p(means2D), _p(conic_opacity), _p(all_map), _p(cl), _p(ranges),
+                           _p(point_list), _p(out_all_map), _p(out_plane_depth))
+    return dict(out_all_map=out_all_map, out_plane_depth=out_plane_depth)
+
+
+def render_bwd_geo(W, H, tanfovx, tanfovy, bg, means2D, conic_opacity, rgb, all_maps, all_map_pixels, ranges,
+                   point_list, final_T, n_contrib_px, dL_dpixels, dL_dmaps, dL_dplane, compute_locally=None):
+    """render_bwd with render_geo on: also dL_dall_map (P,5)."""
+    means2D, conic_opacity, rgb, bg, final_T, dL_dpixels = map(
+        _f32, (means2D, conic_opacity, rgb, bg, final_T, dL_dpixels))
+    all_maps, all_map_pixels, dL_dmaps, dL_dplane = map(_f32, (all_maps, all_map_pixels, dL_dmaps, dL_dplane))
+    gx, gy = tile_grid(W, H)
+    if compute_locally is None:
+        compute_locally = np.ones(gx * gy, np.uint8)
+    cl = np.ascontiguousarray(compute_locally, dtype=np.uint8).reshape(-1)
+    ranges = np.ascontiguousarray(ranges, dtype=np.uint32)
+    point_list = np.ascontiguousarray(point_list, dtype=np.uint32)
+    n_contrib_px = np.ascontiguousarray(n_contrib_px, dtype=np.uint32)
+    P = means2D.shape[0]
+    fx, fy = focal(W, H, tanfovx, tanfovy)
+    out = dict(dL_dmeans2D=np.zeros((P, 3), np.float32), dL_dmeans2D_abs=np.zeros((P, 3), np.float32),
+               dL_dconic=np.zeros((P, 4), np.float32), dL_dopacity=np.zeros(P, np.float32),
+               dL_dcolors=np.zeros((P, 3), np.float32), dL_dall_map=np.zeros((P, 5), np.float32))
+    geo = OGeoBwd(fx, fy, all_maps.ctypes.data, all_map_pixels.ctypes.data, dL_dmaps.ctypes.data,
+                  dL_dplane.ctypes.data, out["dL_dall_map"].ctypes.data)
+    lib().o_render_bwd_geo(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity), _p(rgb),
+                           _p(cl), _p(ranges), _p(point_list), _p(final_T), _p(n_contrib_px), _p(dL_dpixels),
+                           _p(out["dL_dmeans2D"]), _p(out["dL_dmeans2D_abs"]), _p(out["dL_dconic"]),
+                           _p(out["dL_dopacity"]), _p(out["dL_dcolors"]), C.byref(geo))
+    dc = out["dL_dconic"]
     out["dL_dconic_opacity"] = np.stack([dc[:, 0], dc[:, 1], dc[:, 3], out["dL_dopacity"]], axis=1)
     return out
 

@@ -130,3 +130,35 @@ def test_routing_argument_errors_without_device(lib):
     assert rc != 0 and b"n_fields" in lib.gs_last_error()
     rc = lib.gs_move_rows(11, None, 10, None, 11, 1, f, 0, None)
     assert rc != 0 and b"source rows" in lib.gs_last_error()
+
+
+def test_render_geo_argument_errors_without_device(lib):
+    # render_geo entry points: argument checks come before any HIP call
+    nz = C.c_void_p(256)
+    rc = lib.gs_render_geo_forward(10, 5, 64, 64, C.c_float(0.5), C.c_float(0.5), None, None, nz, nz, nz, nz, nz,
+                                   None)
+    assert rc != 0 and b"all_map" in lib.gs_last_error()
+    rc = lib.gs_render_geo_forward(10, 5, 64, 64, C.c_float(0.0), C.c_float(0.5), nz, None, nz, nz, nz, nz, nz, None)
+    assert rc != 0 and b"tan_fov" in lib.gs_last_error()
+    rc = lib.gs_render_geo_forward(10, 5, 64, 64, C.c_float(0.5), C.c_float(0.5), nz, None, None, nz, nz, nz, nz,
+                                   None)
+    assert rc != 0 and b"workspaces" in lib.gs_last_error()
+    # backward: every map input is required, and dL_dall_map
+    args = [10, 5, 64, 64, nz, C.c_float(0.5), C.c_float(0.5), nz, nz, nz, nz, nz, None, nz, nz, nz, nz, nz, nz,
+            nz, 3, nz, nz, nz, nz, None]
+    bad = list(args)
+    bad[24] = None      # dL_dall_map
+    assert lib.gs_render_backward_geo(*bad) != 0 and b"dL_dall_map" in lib.gs_last_error()
+    bad = list(args)
+    bad[17] = None      # dL_dout_all_map
+    assert lib.gs_render_backward_geo(*bad) != 0 and b"dL_dout_all_map" in lib.gs_last_error()
+
+
+def test_render_geo_shape_checks_without_device(lib):
+    import torch
+    from blitzgs_amd import rasterizer
+    geom = torch.empty(16, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match=r"all_map of shape \(10, 5\)"):
+        rasterizer._render_geo_forward_raw(10, 32, 32, 0.5, 0.5, torch.zeros(10, 4), None, 0, geom, geom, geom)
+    with pytest.raises(RuntimeError, match=r"all_map of shape \(10, 5\)"):
+        rasterizer._render_geo_forward_raw(10, 32, 32, 0.5, 0.5, None, None, 0, geom, geom, geom)

@@ -164,3 +164,40 @@ def test_geo_autograd_and_raw_ops(gpu, monkeypatch):
     finally:
         for m in ("diff_gaussian_rasterization_f", "diff_gaussian_rasterization_r"):
             sys.modules.pop(m, None)
+
+
+def test_geo_config2_full_size_vs_oracle(gpu):
+    # the headline size (6M SH3 Gaussians, 1600x1066, > 8M instances): the maps'
+    # staging and the Gaussian ids the geometry passes read, at full list lengths
+    scene, cam = synth.config2()
+    W, H = cam["W"], cam["H"]
+    pre = O.preprocess_fwd(cam, scene["means3D"], scene["scales"], scene["rotations"], scene["sh"],
+                           scene["opacities"])
+    P = len(pre["radii"])
+    rng = np.random.default_rng(2)
+    all_map = rng.uniform(-1.0, 1.0, (P, 5)).astype(np.float32)
+    all_map[:, 2] = rng.uniform(-1.5, -0.5, P)
+    grads = dict(dpix=scene["dL_dimage"].astype(np.float32),
+                 dmaps=rng.normal(size=(5, H, W)).astype(np.float32),
+                 dplane=(0.1 * rng.normal(size=(1, H, W))).astype(np.float32))
+    cl = np.ones(O.tile_grid(W, H)[::-1], np.uint8)
+    bg = np.zeros(3, np.float32)
+    print(f"render_geo config 2: P={P} W={W} H={H}", flush=True)
+    rs = settings_for(cam, bg=bg)
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    f = gpu_render_forward(rs, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"], cl)
+    amap = to_dev(all_map)
+    maps, plane = rasterizer._render_geo_forward_raw(P, H, W, cam["tanfovx"], cam["tanfovy"], amap, to_dev(cl),
+                                                     f["R"], f["geom"], f["binning"], f["img"])
+    out = rasterizer._render_backward_raw(
+        rs.bg, f["R"], H, W, dev["means2D"], dev["conic_opacity"], dev["rgb"], to_dev(cl), f["geom"], f["binning"],
+        f["img"], to_dev(grads["dpix"]), 3,
+        geo=(cam["tanfovx"], cam["tanfovy"], maps, amap, to_dev(grads["dmaps"]), to_dev(grads["dplane"])))
+    bn, rf, geo, rb = _oracle(cam, pre, cl, all_map, bg, grads)
+    assert f["R"] == bn["R"] and f["R"] > 8_000_000
+    assert_close_abs(np_(maps), geo["out_all_map"], "out_all_map")
+    assert_plane_depth_close(np_(plane), geo["out_plane_depth"], geo["out_all_map"], cam, "out_plane_depth")
+    got = dict(zip(GRADS, out[:4] + (out[5],)))
+    errs = {k: rel_l2(np_(got[k]), rb[k]) for k in GRADS}
+    print("render_geo config 2 gradient errors:", errs)
+    assert max(errs.values()) < 1e-3, errs

@@ -178,24 +178,40 @@ def calibrate_copy(mib):
                       "launches": 5}), flush=True)
 
 
+STEP_TIMES = {}
+
+
+def step_times(fn, steps):
+    """`steps` calls of fn bracketed by synchronisation, a HIP event on the
+    current stream before every call and after the last: (median ms of the
+    per-call intervals, mean ms over the whole region)."""
+    import torch
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        evs[i].record()
+        fn()
+    evs[steps].record()
+    torch.cuda.synchronize()
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return float(np.median(per)), evs[0].elapsed_time(evs[steps]) / steps
+
+
 def timed(fn, steps, warmup):
     """Run fn warmup times, then two timed regions of `steps` calls, each
     bracketed by synchronisation: the first without instrumentation (the step
-    time), the second with the library's per-kernel HIP events recorded on the
-    launch stream around every kernel (the per-kernel durations).  Returns
-    (ms per step, per-kernel {name: (total ms, launches)}, instrumented ms per step)."""
+    time: the median of the per-call intervals; the mean over the region is
+    kept in STEP_TIMES), the second with the library's per-kernel HIP events
+    recorded on the launch stream around every kernel (the per-kernel
+    durations).  Returns (median ms per step, per-kernel {name: (total ms,
+    launches)}, instrumented ms per step)."""
     import torch
     from blitzgs_amd import _lib
     for _ in range(warmup):
         fn()
+    ms, ms_mean = step_times(fn, steps)
+    STEP_TIMES["median_ms"], STEP_TIMES["mean_ms"] = ms, ms_mean
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record()
-    for _ in range(steps):
-        fn()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
     _lib.timing_reset()
     _lib.timing_enable(True)
     torch.cuda.synchronize()
@@ -343,6 +359,10 @@ def run_step(args):
     ras = GaussianRasterizer(rs)
     means2D_abs = torch.zeros((P, 3), device=dev, requires_grad=True)
     all_map = torch.zeros((P, 5), device=dev)
+    # as gaussian_renderer passes them (its stats_collector makes every render
+    # forward and backward wait on an event for its timers), and without the
+    # collector (no host wait inside the step)
+    cuda_args_train = {"avoid_pixel_all2all": False, "stats_collector": {}}
     cuda_args = {"avoid_pixel_all2all": False}
     info = {}
     loss_desc = "dL/dimage ~ N(0,1)"
@@ -352,14 +372,14 @@ def run_step(args):
         target = tt(np.random.Generator(np.random.PCG64(101)).random((3, H, W), dtype=np.float32))
         loss_desc = "0.8 * L1 + 0.2 * (1 - fused_ssim) vs a seeded U[0,1] target (reference training loss)"
 
-    def step():
+    def step(ca=cuda_args):
         for p in params.values():
             p.grad = None
         means2D_abs.grad = None
         means2D, rgb, conic_opacity, radii, depths = ras.preprocess_gaussians(
-            params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], cuda_args)
+            params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], ca)
         color, n_render, n_consider, n_contrib, out_observe, _, _ = ras.render_gaussians(
-            means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, cl, cl, cuda_args)
+            means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, cl, cl, ca)
         if target is None:
             torch.autograd.backward([color], [dL_dimage])
         else:
@@ -371,10 +391,13 @@ def run_step(args):
         info["n_consider"] = n_consider
 
     ms_per_step, kt, ms_instr = timed(step, args.steps, args.warmup)
+    ms_mean = STEP_TIMES["mean_ms"]
+    ms_train, ms_train_mean = step_times(lambda: step(cuda_args_train), args.steps)
     P_vis = int((info["radii"] > 0).sum().item())
     R = int(info["n_render"].sum().item())
     E = int(info["n_consider"].sum().item())
-    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step ({ms_instr:.3f} with per-kernel events)")
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step median ({ms_mean:.3f} mean; {ms_instr:.3f} with "
+        f"per-kernel events; {ms_train:.3f} with cuda_args['stats_collector'])")
 
     per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
     avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
@@ -434,6 +457,13 @@ def run_step(args):
     out["binning_kernels_ms"] = round(binning_kernels_ms, 4)
     if BINNING_STAGE + " with kernel events" in per_kernel:
         out["binning_wall_with_kernel_events_ms"] = round(per_kernel[BINNING_STAGE + " with kernel events"], 4)
+    out["ms_per_step_note"] = ("median of the per-step intervals (HIP events between the steps) over the timed "
+                               "steps after the warm-up steps; ms_per_step_mean is the whole timed region / steps")
+    out["ms_per_step_mean"] = round(ms_mean, 4)
+    out["ms_per_step_with_stats_collector"] = {
+        "median": round(ms_train, 4), "mean": round(ms_train_mean, 4),
+        "note": "the same step with cuda_args['stats_collector'] set, as gaussian_renderer/__init__.py:216 passes "
+                "it: every render forward and backward then waits on the host for its timing event"}
     out["ms_per_step_with_kernel_events"] = round(ms_instr, 4)
     out["render_fwd_evaluations"] = E
     out["hbm_copy_GBs"] = round(peak_copy, 1)
@@ -454,17 +484,42 @@ def cpu_baseline_step(scene, cam, frac, cl):
     dLd = scene.get("dL_dimage")
     if dLd is None:
         dLd = np.random.default_rng(0).standard_normal((3, H, W)).astype(np.float32)
-    t0 = time.perf_counter()
-    pre, bn, rf = O.full_forward(cam, sub, bg=bg, compute_locally=clm)
-    rb = O.render_bwd(W, H, bg, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"], bn["point_list"],
-                      rf["final_T"], rf["n_contrib_px"], dLd, clm)
-    O.preprocess_bwd(cam, sub["means3D"], sub["scales"], sub["rotations"], sub["sh"], pre["radii"], pre["cov3D"],
-                     pre["clamped"], rb["dL_dmeans2D"], rb["dL_dconic_opacity"], rb["dL_dcolors"])
-    dt = time.perf_counter() - t0
-    log(f"[bench] cpu oracle fwd+bwd on {n} Gaussians: {dt:.2f}s")
+
+    def once():
+        t0 = time.perf_counter()
+        pre, bn, rf = O.full_forward(cam, sub, bg=bg, compute_locally=clm)
+        rb = O.render_bwd(W, H, bg, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"],
+                          bn["point_list"], rf["final_T"], rf["n_contrib_px"], dLd, clm)
+        O.preprocess_bwd(cam, sub["means3D"], sub["scales"], sub["rotations"], sub["sh"], pre["radii"],
+                         pre["cov3D"], pre["clamped"], rb["dL_dmeans2D"], rb["dL_dconic_opacity"], rb["dL_dcolors"])
+        return time.perf_counter() - t0
+
+    runs = cpu_runs(once)
+    dt = float(np.median(runs))
+    log(f"[bench] cpu oracle fwd+bwd on {n} Gaussians: {', '.join(f'{r:.2f}' for r in runs)} s")
     return {"value": round(n / dt, 1), "unit": "Gaussians/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"one fwd+bwd iteration of the CPU oracle on the first {n} of {P} Gaussians, "
-                      f"same camera ({W}x{H}); {dt * 1e3:.0f} ms"}
+            "cpu_model": cpu_model(),
+            "sample": f"CPU oracle fwd+bwd (fp32 C, OpenMP) on the first {n} of {P} Gaussians, same camera "
+                      f"({W}x{H}): 1 warm-up, then the median of {len(runs)} timed runs, {dt * 1e3:.0f} ms "
+                      f"(runs {', '.join(f'{r * 1e3:.0f}' for r in runs)} ms)"}
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_runs(once, timed_runs=3):
+    """The CPU baseline protocol: one warm-up call of once(), then
+    `timed_runs` timed calls; returns their durations (s)."""
+    once()
+    return [once() for _ in range(timed_runs)]
 
 
 # ------------------------------------------------------------------- knn
@@ -492,11 +547,17 @@ def run_knn(args):
         from oracle import oracle as O
         n = max(4, int(P * min(args.cpu_sample, 0.1)))
         sub = np.ascontiguousarray(pts_np[:n])
-        t1 = time.perf_counter()
-        O.knn_meandist3(sub)
-        dt = time.perf_counter() - t1
+
+        def once():
+            t1 = time.perf_counter()
+            O.knn_meandist3(sub)
+            return time.perf_counter() - t1
+        runs = cpu_runs(once)
+        dt = float(np.median(runs))
         cpu = {"value": round(n / dt, 1), "unit": "points/s", "cores": O.num_threads(), "kind": "port",
-               "sample": f"CPU oracle exact 3-NN (grid) on the first {n} of the {P} points; {dt * 1e3:.0f} ms"}
+               "cpu_model": cpu_model(),
+               "sample": f"CPU oracle exact 3-NN (grid) on the first {n} of the {P} points: 1 warm-up, then the "
+                         f"median of {len(runs)} timed runs, {dt * 1e3:.0f} ms"}
     out = header(args, "distCUDA2 points/s (exact 3-NN mean squared distance)", P / (ms * 1e-3), "points/s", ms,
                  "f32", f"config4: distCUDA2 over {P} points", {"points": P})
     out["stages_ms"] = {k: round(v, 4) for k, v in per_kernel.items()}
@@ -540,12 +601,18 @@ def run_ssim(args):
     if not args.no_cpu_baseline:
         from oracle import oracle as O
         x, y = np.ascontiguousarray(a[:1]), np.ascontiguousarray(b[:1])
-        t1 = time.perf_counter()
-        m, d1, d2, d3 = O.ssim_fwd(x, y)
-        O.ssim_bwd(x, y, np.full(x.shape, -1.0 / N, np.float32), d1, d2, d3)
-        dt = time.perf_counter() - t1
+
+        def once():
+            t1 = time.perf_counter()
+            m, d1, d2, d3 = O.ssim_fwd(x, y)
+            O.ssim_bwd(x, y, np.full(x.shape, -1.0 / N, np.float32), d1, d2, d3)
+            return time.perf_counter() - t1
+        runs = cpu_runs(once)
+        dt = float(np.median(runs))
         cpu = {"value": round(x.size / dt, 1), "unit": "pixels/s", "cores": O.num_threads(), "kind": "port",
-               "sample": f"CPU oracle SSIM fwd+bwd on image 1 of {B} (3x{H}x{W}); {dt * 1e3:.0f} ms"}
+               "cpu_model": cpu_model(),
+               "sample": f"CPU oracle SSIM fwd+bwd on image 1 of {B} (3x{H}x{W}): 1 warm-up, then the median of "
+                         f"{len(runs)} timed runs, {dt * 1e3:.0f} ms"}
     out = header(args, "fused_ssim fwd+bwd pixels/s", N / (ms * 1e-3), "pixels/s", ms, "f32",
                  f"config4: fused_ssim fwd+bwd, {B}x{C}x{H}x{W}", {"shape": [B, C, H, W]})
     out["stages_ms"] = rows

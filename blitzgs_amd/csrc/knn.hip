@@ -427,11 +427,16 @@ extern "C" int gs_knn_meandist3(int P, const float* points, float* out, void* wo
 //
 // gs_knn_meandist3_noalloc: the same computation with its workspace in a
 // file-scope device array instead of caller memory, for callers that cannot
-// allocate (graph capture, serving loops).  Each GPU the library runs on holds
-// its own copy of the array (KNN_SCRATCH_BYTES, about 38 MB) until the process
-// ends.  In host code `scratch` names a host-side stand-in, never the device
-// memory: the per-device address comes from hipGetSymbolAddress on the first
-// call on each device and only that address is passed to kernels and copies.
+// allocate (serving loops, harnesses that forbid hipMalloc).  It cannot be
+// captured into a HIP graph: like gs_knn_meandist3 it reads the bounding box
+// back to the host mid-call and synchronises the stream.  Each GPU the library
+// runs on holds its own copy of the array (KNN_SCRATCH_BYTES, about 38 MB)
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// never the device memory: the per-device address comes from
+// hipGetSymbolAddress on the first call on each device and only that address
+// is passed to kernels and copies.  A per-device lock is held for the whole
+// call, which ends with a synchronisation of its stream, so calls from several
+// host threads on one GPU run one after another instead of sharing the array.
 
 constexpr int KNN_NOALLOC_MAX_P = 1 << 20;
 constexpr size_t KNN_SCRATCH_BYTES = knn_layout(KNN_NOALLOC_MAX_P).total;
@@ -443,6 +448,7 @@ namespace {
 constexpr int KNN_MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[KNN_MAX_DEVICES] = {};
+std::mutex g_call_mu[KNN_MAX_DEVICES];   // one call at a time per device's scratch
 
 // the current device's copy of `scratch` (looked up once per device)
 int scratch_of_current_device(void** out)
@@ -477,5 +483,8 @@ extern "C" int gs_knn_meandist3_noalloc(int P, const float* points, float* out, 
     }
     void* ws = nullptr;
     if (int rc = scratch_of_current_device(&ws); rc != GS_OK) return rc;
+    int dev = -1;
+    GS_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_call_mu[dev]);
     return knn_impl(P, points, out, ws, stream);
 }

@@ -228,15 +228,16 @@ size_t gs_knn_workspace_bytes(int P);
 int gs_knn_meandist3(int P, const float* points, float* out, void* workspace, gs_stream_t stream);
 
 /* Allocation-free distCUDA2.  No counterpart in the reference: for callers
- * that cannot allocate device memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  Same result as
- * gs_knn_meandist3, with the workspace in a device array inside the library
- * (about 38 MB, held on every GPU the library runs on until the process
- * ends) instead of a caller buffer; allocates nothing.  P <= 1048576 (larger
- * P: error, use gs_knn_meandist3).  `stream` must belong to the current
- * device.  All calls on one GPU share that GPU's array: calls that overlap in
- * time on one GPU (other host threads, other streams) race.  Synchronises
- * `stream`. */
+ * that cannot allocate device memory (tight serving loops, harnesses that
+ * forbid hipMalloc).  Same result as gs_knn_meandist3, with the workspace in
+ * a device array inside the library (about 38 MB, held on every GPU the
+ * library runs on until the process ends) instead of a caller buffer;
+ * allocates nothing.  Not for HIP graph capture: it reads the points'
+ * bounding box back to the host mid-call and synchronises `stream`.
+ * P <= 1048576 (larger P: error, use gs_knn_meandist3).  `stream` must belong
+ * to the current device.  All calls on one GPU share that GPU's array; a
+ * per-device lock held for the whole call (which returns after its kernels
+ * finish) makes calls from several host threads run one after another. */
 int gs_knn_meandist3_noalloc(int P, const float* points, float* out, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *

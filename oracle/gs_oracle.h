@@ -73,7 +73,19 @@ void o_render_fwd(int P, int W, int H, const float* bg,
                   const uint32_t* ranges, const uint32_t* point_list,
                   float* out_color, float* final_T, uint32_t* n_contrib,
                   uint32_t* n_contrib2loss, int32_t* out_observe,
-                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile);
+                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile,
+                  int32_t* obs_near, uint8_t* stop_near);
+
+/* Decision margins of o_render_fwd (test infrastructure: they say which
+ * integer outputs a blend whose exp differs from o_expf by a relative
+ * O_EXP_REL may change).  Along each pixel's walk a first-order bound on the
+ * relative error of T is carried: every blended entry adds
+ * O_EXP_REL * alpha / (1 - alpha) (the factor (1 - alpha)'s error) plus two
+ * fp32 roundings.  obs_near (P, or NULL): per Gaussian, the number of blends
+ * whose T > 0.5 test had |T - 0.5| <= 0.5 * bound.  stop_near (H*W, or NULL):
+ * 1 where some alpha-passing entry had |test_T - 1e-4| <= 1e-4 * bound. */
+#define O_EXP_REL 4e-6f
+void o_set_blend_margin_model(float exp_delta, float bound_rel);
 
 /* Render backward (_r/cuda_rasterizer/backward.cu:324-530).  dL_dmean2D and
  * dL_dmean2D_abs are (P,3); dL_dconic is (P,4) in the reference's float4

@@ -156,13 +156,33 @@ static inline float o_power(const float* xy, const float* co, float px, float py
     return fmaf(ha * dx, dx, fmaf(hc * dy, dy, (nb * dx) * dy));
 }
 
+/* Margin model of o_render_fwd's decision bounds (test hook): exp_delta != 0
+ * multiplies each evaluated exp by 1 +- exp_delta (sign from a hash of the
+ * Gaussian and the pixel), to emulate a blend whose exp differs slightly;
+ * bound_rel is the relative exp error the margins assume (O_EXP_REL). */
+static float g_exp_delta = 0.0f, g_bound_rel = O_EXP_REL;
+
+void o_set_blend_margin_model(float exp_delta, float bound_rel)
+{
+    g_exp_delta = exp_delta;
+    g_bound_rel = bound_rel;
+}
+
+static inline float perturb_sign(uint32_t id, size_t pid)
+{
+    uint32_t h = id * 0x9E3779B1u ^ (uint32_t)pid * 0x85EBCA77u;
+    h ^= h >> 15; h *= 0x2C1B3C6Du; h ^= h >> 12;
+    return (h & 1u) ? 1.0f : -1.0f;
+}
+
 void o_render_fwd(int P, int W, int H, const float* bg,
                   const float* means2D, const float* conic_opacity, const float* rgb,
                   const uint8_t* compute_locally,
                   const uint32_t* ranges, const uint32_t* point_list,
                   float* out_color, float* final_T, uint32_t* n_contrib,
                   uint32_t* n_contrib2loss, int32_t* out_observe,
-                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile)
+                  int32_t* n_render, int32_t* n_consider, int32_t* n_contrib_tile,
+                  int32_t* obs_near, uint8_t* stop_near)
 {
     (void)P;
     const int gx = (W + OT - 1) / OT, gy = (H + OT - 1) / OT;
@@ -181,6 +201,7 @@ void o_render_fwd(int P, int W, int H, const float* bg,
                     const size_t pid = (size_t)y * W + x;
                     for (int c = 0; c < 3; c++) out_color[(size_t)c * H * W + pid] = 0.f;
                     final_T[pid] = 0.f; n_contrib[pid] = 0; n_contrib2loss[pid] = 0;
+                    if (stop_near) stop_near[pid] = 0;
                 }
             continue;
         }
@@ -189,17 +210,26 @@ void o_render_fwd(int P, int W, int H, const float* bg,
         for (int y = y0; y < y1; y++)
             for (int x = x0; x < x1; x++) {
                 const float px = (float)x, py = (float)y;
+                const size_t pid = (size_t)y * W + x;
                 float T_ = 1.0f, C[3] = { 0.f, 0.f, 0.f };
                 uint32_t contributor = 0, last = 0, n2l = 0;
+                double bound = 0.0;  /* relative error bound of T_ (decision margins only) */
+                int snear = 0;
                 for (uint32_t k = rs; k < re; k++) {
                     contributor++;
                     const uint32_t id = point_list[k];
                     const float* co = conic_opacity + 4 * (size_t)id;
                     const float power = o_power(means2D + 2 * (size_t)id, co, px, py);
                     if (power > 0.0f) continue;
-                    const float alpha = o_fminf(0.99f, co[3] * o_expf(power));
+                    const float G = o_expf(power);
+                    float alpha = o_fminf(0.99f, co[3] * G);
                     if (alpha < alpha_min) continue;
+                    /* test hook: the blend (not the exact alpha >= 1/255 cut) with a perturbed exp */
+                    if (g_exp_delta != 0.0f)
+                        alpha = o_fminf(0.99f, co[3] * (G * (1.0f + g_exp_delta * perturb_sign(id, pid))));
                     const float test_T = T_ * (1.0f - alpha);
+                    const double bound_next = bound + (double)g_bound_rel * alpha / (1.0 - alpha) + 2.4e-7;
+                    if (fabs((double)test_T - 1e-4) <= 1e-4 * bound_next) snear = 1;
                     if (test_T < 0.0001f) break;
                     n2l++;
                     const float wgt = alpha * T_;
@@ -208,10 +238,15 @@ void o_render_fwd(int P, int W, int H, const float* bg,
 #pragma omp atomic
                         out_observe[id]++;
                     }
+                    if (obs_near && fabs((double)T_ - 0.5) <= 0.5 * bound) {
+#pragma omp atomic
+                        obs_near[id]++;
+                    }
                     T_ = test_T;
+                    bound = bound_next;
                     last = contributor;
                 }
-                const size_t pid = (size_t)y * W + x;
+                if (stop_near) stop_near[pid] = (uint8_t)snear;
                 final_T[pid] = T_;
                 n_contrib[pid] = last;
                 n_contrib2loss[pid] = n2l;

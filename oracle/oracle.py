@@ -152,6 +152,9 @@ def binning(W, H, means2D, depths, radii, compute_locally=None):
 
 
 def render_fwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, compute_locally=None):
+    """Render forward with the per-tile statistics; also the decision margins
+    (obs_near per Gaussian, stop_near per pixel) that bound which integer
+    outputs a blend with a slightly different exp may change."""
     means2D, conic_opacity, rgb, bg = map(_f32, (means2D, conic_opacity, rgb, bg))
     gx, gy = tile_grid(W, H)
     if compute_locally is None:
@@ -164,12 +167,24 @@ def render_fwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, comput
     out = dict(color=np.empty((3, H, W), np.float32), final_T=np.empty((H, W), np.float32),
                n_contrib_px=np.empty((H, W), np.uint32), n_contrib2loss_px=np.empty((H, W), np.uint32),
                out_observe=np.zeros(P, np.int32), n_render=np.empty(T, np.int32),
-               n_consider=np.empty(T, np.int32), n_contrib=np.empty(T, np.int32))
+               n_consider=np.empty(T, np.int32), n_contrib=np.empty(T, np.int32),
+               obs_near=np.zeros(P, np.int32), stop_near=np.empty((H, W), np.uint8))
     lib().o_render_fwd(C.c_int(P), C.c_int(W), C.c_int(H), _p(bg), _p(means2D), _p(conic_opacity), _p(rgb),
                        _p(cl), _p(ranges), _p(point_list), _p(out["color"]), _p(out["final_T"]),
                        _p(out["n_contrib_px"]), _p(out["n_contrib2loss_px"]), _p(out["out_observe"]),
-                       _p(out["n_render"]), _p(out["n_consider"]), _p(out["n_contrib"]))
+                       _p(out["n_render"]), _p(out["n_consider"]), _p(out["n_contrib"]),
+                       _p(out["obs_near"]), _p(out["stop_near"]))
     return out
+
+
+def set_blend_margin_model(exp_delta=0.0, bound_rel=4e-6):
+    """Test hook of render_fwd: perturb every evaluated exp by a relative
+    +-exp_delta, and set the relative exp error its decision margins assume
+    (default: O_EXP_REL = 4e-6).  set_blend_margin_model() restores both."""
+    f = lib().o_set_blend_margin_model
+    f.restype = None
+    f.argtypes = [C.c_float, C.c_float]
+    f(float(exp_delta), float(bound_rel))
 
 
 def render_bwd(W, H, bg, means2D, conic_opacity, rgb, ranges, point_list, final_T, n_contrib_px,

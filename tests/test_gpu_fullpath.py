@@ -234,6 +234,67 @@ def test_config1_full_path_forward_vs_oracle(gpu):
     _check_forward(got, pre, bn, rf)
 
 
+def _tile_buckets_scene(specs, seed, n_bg=1500):
+    """A 256x256 scene (camera at (0, 0, -4) looking down +z, FoV 60, R = I)
+    whose tiles (tx, ty, n, ties) each receive n Gaussians projected onto the
+    tile centre with a small isotropic precomputed covariance (the tile test
+    keeps only that tile); with ties, half of them lie on the plane z = 0
+    (view depth exactly 4.0: one run of equal depths), the rest at depths in
+    [3, 7].  n_bg small Gaussians fill the lower half of the image."""
+    import math
+    rng = np.random.default_rng(seed)
+    W = H = 256
+    fov = math.radians(60.0)
+    cam = synth.make_camera(np.eye(3), (0.0, 0.0, -4.0), W, H, fov, fov)
+    tx_, ty_ = float(cam["tanfovx"]), float(cam["tanfovy"])
+    pts = []
+    for tx, ty, n, ties in specs:
+        zw = rng.uniform(-1.0, 3.0, n)
+        if ties:
+            zw[: n // 2] = 0.0
+        zv = zw + 4.0
+        px, py = 16 * tx + 8.0, 16 * ty + 8.0
+        x = ((2 * px + 1) / W - 1) * tx_ * zv
+        y = ((2 * py + 1) / H - 1) * ty_ * zv
+        pts.append(np.stack([x, y, zw], 1))
+    zb = rng.uniform(-1.0, 1.0, n_bg)
+    pyb = rng.uniform(140.0, 250.0, n_bg)
+    pxb = rng.uniform(4.0, 252.0, n_bg)
+    pts.append(np.stack([((2 * pxb + 1) / W - 1) * tx_ * (zb + 4), ((2 * pyb + 1) / H - 1) * ty_ * (zb + 4), zb], 1))
+    means = np.concatenate(pts)
+    P = means.shape[0]
+    order = rng.permutation(P)
+    means = means[order].astype(np.float32)
+    scene = synth._finish(rng, means, -4.0, 0.3, 1.0, 0.5, P)
+    var = np.float32(0.004 ** 2)
+    cov = np.zeros((P, 6), np.float32)
+    cov[:, 0] = cov[:, 3] = cov[:, 5] = var
+    cols = rng.random((P, 3)).astype(np.float32)
+    return scene, cam, cov, cols
+
+
+def test_full_path_tile_sort_classes_and_tie_runs(gpu):
+    # one tile per sort class of the full-image path's per-tile sort: <= 512
+    # keys (per-wave register network), 1k, 2k, 4k and 8k (LDS radix sort),
+    # > 8192 (EXTRA_BIG: bitonic network in global memory); the radix classes
+    # also with a run of more than 32 equal depths (the fallback to the full
+    # 64-bit sort in global memory); ties order by ascending id everywhere
+    specs = [(1, 1, 300, True), (3, 1, 700, False), (5, 1, 700, True), (7, 1, 1500, False), (9, 1, 1500, True),
+             (11, 1, 3000, False), (13, 1, 3000, True), (1, 3, 6000, False), (3, 3, 6000, True),
+             (5, 3, 9000, False), (7, 3, 9000, True)]
+    scene, cam, cov, cols = _tile_buckets_scene(specs, 51)
+    got = _run(scene, cam, colors_precomp=cols, cov3D_precomp=cov)
+    pre, bn, rf = _oracle(scene, cam, colors_precomp=cols, cov3D_precomp=cov)
+    _check_forward(got, pre, bn, rf)
+    n = np.diff(bn["ranges"].reshape(16, 16, 2), axis=2)[..., 0]
+    for tx, ty, cnt, ties in specs:
+        assert n[ty, tx] == cnt, (tx, ty, n[ty, tx], cnt)
+        ids = bn["point_list"][bn["ranges"][ty * 16 + tx, 0]:bn["ranges"][ty * 16 + tx, 1]]
+        d = pre["depths"][ids]
+        run = np.diff(np.flatnonzero(np.diff(np.r_[-1.0, d, -1.0]) != 0)).max()
+        assert (run > 32) == ties, (tx, ty, run)
+
+
 # ------------------------------------------------------------------ render_depth
 
 def _depth_gpu(scene, cam, bg=(0.0, 0.0, 0.0), culling=None, colors_precomp=None, deg=3):

@@ -20,7 +20,7 @@ import torch
 
 from blitzgs_amd import synth
 from oracle import oracle as O
-from tests.gpu_helpers import (assert_close_abs, assert_counts_close, gpu_preprocess, gpu_render_forward, np_,
+from tests.gpu_helpers import (assert_blend_counts, assert_close_abs, gpu_preprocess, gpu_render_forward, np_,
                                settings_for, to_dev)
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +48,10 @@ def test_config1_forward_vs_oracle(gpu):
     _bitexact(np_(out["ranges"]).view(np.uint32), bn["ranges"], "ranges")
     assert_close_abs(np_(out["color"]), rf["color"], "color")
     assert_close_abs(np_(out["final_T"]), rf["final_T"], "final_T")
-    assert_counts_close(np_(out["out_observe"]), rf["out_observe"], "out_observe")
+    assert_blend_counts(dict(n_contrib_px=np_(out["n_contrib_px"]).view(np.uint32),
+                             n_contrib2loss_px=np_(out["n_contrib2loss_px"]).view(np.uint32),
+                             out_observe=np_(out["out_observe"]), n_consider=np_(out["n_consider"]),
+                             n_contrib=np_(out["n_contrib"])), rf, "config 1 forward")
 
 
 def test_config3_share_matches_full_image(gpu):

@@ -64,20 +64,23 @@ def assert_plane_depth_close(got, ref, ref_maps, cam, name):
     assert bad.size == 0, (name, bad.size, float(np.abs(g - r)[ok].max()))
 
 
-def _oracle(cam, pre, cl, all_map, bg, grads):
+def _oracle(cam, pre, cl, all_map, bg, grads, cl_bwd=None):
+    """Forward (binning, colour, maps) over the tiles of cl; backward over
+    those of cl_bwd (default cl), as avoid_pixel_all2all splits them."""
     W, H = cam["W"], cam["H"]
+    cl_bwd = cl if cl_bwd is None else cl_bwd
     bn = O.binning(W, H, pre["means2D"], pre["depths"], pre["radii"], cl)
     rf = O.render_fwd(W, H, bg, pre["means2D"], pre["conic_opacity"], pre["rgb"], bn["ranges"], bn["point_list"], cl)
     geo = O.render_geo_fwd(W, H, cam["tanfovx"], cam["tanfovy"], pre["means2D"], pre["conic_opacity"], all_map,
                            bn["ranges"], bn["point_list"], cl)
     rb = O.render_bwd_geo(W, H, cam["tanfovx"], cam["tanfovy"], bg, pre["means2D"], pre["conic_opacity"], pre["rgb"],
                           all_map, geo["out_all_map"], bn["ranges"], bn["point_list"], rf["final_T"],
-                          rf["n_contrib_px"], grads["dpix"], grads["dmaps"], grads["dplane"], cl)
+                          rf["n_contrib_px"], grads["dpix"], grads["dmaps"], grads["dplane"], cl_bwd)
     return bn, rf, geo, rb
 
 
 @pytest.mark.parametrize("masked", [False, True])
-def test_geo_forward_bitexact_and_backward_vs_oracle(gpu, masked):
+def test_geo_forward_within_tolerance_and_backward_vs_oracle(gpu, masked):
     scene, cam, pre, cl, all_map, grads = _case(17 + masked, masked)
     bg = np.array([0.2, 0.5, 0.1], np.float32)
     W, H = cam["W"], cam["H"]
@@ -161,6 +164,58 @@ def test_geo_autograd_and_raw_ops(gpu, monkeypatch):
         for got, k in zip(g, GRADS):
             e = rel_l2(np_(got), rb[k])
             assert e < 1e-3, (k, e)
+    finally:
+        for m in ("diff_gaussian_rasterization_f", "diff_gaussian_rasterization_r"):
+            sys.modules.pop(m, None)
+
+
+def test_geo_autograd_avoid_pixel_all2all(gpu, monkeypatch):
+    # avoid_pixel_all2all: the forward (colour, maps, plane depth) renders the
+    # tiles of extended_compute_locally, the backward differentiates only those
+    # of compute_locally (a narrower block of tile rows inside them)
+    monkeypatch.syspath_prepend(DROPIN)
+    for m in ("diff_gaussian_rasterization_f", "diff_gaussian_rasterization_r"):
+        sys.modules.pop(m, None)
+    R_pkg = importlib.import_module("diff_gaussian_rasterization_r")
+    try:
+        scene, cam, pre, _, all_map, grads = _case(31, False, P=3500, W=176, H=160)
+        bg = np.array([0.3, 0.1, 0.2], np.float32)
+        W, H = cam["W"], cam["H"]
+        P = len(all_map)
+        gx, gy = O.tile_grid(W, H)
+        cl = np.zeros((gy, gx), np.uint8)
+        cl[3:6] = 1
+        ext = np.zeros((gy, gx), np.uint8)
+        ext[2:8] = 1
+        print(f"render_geo avoid_pixel_all2all: P={P} W={W} H={H}", flush=True)
+        rs = R_pkg.GaussianRasterizationSettings(**dict(settings_for(cam, bg=bg)._asdict(), render_geo=True))
+        ras = R_pkg.GaussianRasterizer(raster_settings=rs)
+        leaf = {k: to_dev(pre[k]).requires_grad_(True) for k in ["means2D", "conic_opacity", "rgb"]}
+        m2_abs = torch.zeros((P, 3), device="cuda", requires_grad=True)
+        amap = to_dev(all_map).requires_grad_(True)
+        color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth = ras.render_gaussians(
+            leaf["means2D"], m2_abs, leaf["conic_opacity"], leaf["rgb"], amap, to_dev(pre["depths"]),
+            to_dev(pre["radii"]), to_dev(cl).bool(), to_dev(ext).bool(),
+            {"stats_collector": {}, "avoid_pixel_all2all": True})
+        loss = ((color * to_dev(grads["dpix"])).sum() + (out_all_map * to_dev(grads["dmaps"])).sum()
+                + (out_plane_depth * to_dev(grads["dplane"])).sum())
+        loss.backward()
+        bn, rf, geo, rb = _oracle(cam, pre, ext, all_map, bg, grads, cl_bwd=cl)
+        assert_close_abs(np_(color), rf["color"], "color (extended rows)")
+        assert np_(color)[:, 2 * 16:3 * 16].any()                       # an extended-only row is rendered
+        assert_close_abs(np_(out_all_map), geo["out_all_map"], "out_all_map (extended rows)")
+        assert_plane_depth_close(np_(out_plane_depth), geo["out_plane_depth"], geo["out_all_map"], cam,
+                                 "out_plane_depth (extended rows)")
+        # the backward over compute_locally differs from one over the extended mask
+        rb_ext = _oracle(cam, pre, ext, all_map, bg, grads)[3]
+        assert rel_l2(rb_ext["dL_dall_map"], rb["dL_dall_map"]) > 1e-2
+        for got, ref, nm in ((leaf["means2D"].grad, rb["dL_dmeans2D"][:, :2], "means2D"),
+                             (m2_abs.grad, rb["dL_dmeans2D_abs"], "means2D_abs"),
+                             (leaf["conic_opacity"].grad, rb["dL_dconic_opacity"], "conic_opacity"),
+                             (leaf["rgb"].grad, rb["dL_dcolors"], "rgb"),
+                             (amap.grad, rb["dL_dall_map"], "all_map")):
+            e = rel_l2(np_(got), ref)
+            assert e < 1e-3, (nm, e)
     finally:
         for m in ("diff_gaussian_rasterization_f", "diff_gaussian_rasterization_r"):
             sys.modules.pop(m, None)

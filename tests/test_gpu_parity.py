@@ -14,7 +14,7 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-from tests.gpu_helpers import (assert_bitexact, assert_close_abs, assert_counts_close, gpu_preprocess,
+from tests.gpu_helpers import (assert_bitexact, assert_blend_counts, assert_close_abs, gpu_preprocess,
                                gpu_render_forward, np_, rel_l2, settings_for, to_dev)
 
 
@@ -110,11 +110,10 @@ def _check_binning_and_render(cam, pre, bg, cl=None):
     assert_bitexact(np_(g["n_render"]), orf["n_render"], "n_render")
     assert_close_abs(np_(g["color"]), orf["color"], "color")
     assert_close_abs(np_(g["final_T"]), orf["final_T"], "final_T")
-    assert_counts_close(np_(g["n_contrib_px"]).view(np.uint32), orf["n_contrib_px"], "n_contrib (pixel)")
-    assert_counts_close(np_(g["n_contrib2loss_px"]).view(np.uint32), orf["n_contrib2loss_px"], "n_contrib2loss")
-    assert_counts_close(np_(g["out_observe"]), orf["out_observe"], "out_observe")
-    assert_counts_close(np_(g["n_consider"]), orf["n_consider"], "n_consider")
-    assert_counts_close(np_(g["n_contrib"]), orf["n_contrib"], "n_contrib (tile)")
+    assert_blend_counts(dict(n_contrib_px=np_(g["n_contrib_px"]).view(np.uint32),
+                             n_contrib2loss_px=np_(g["n_contrib2loss_px"]).view(np.uint32),
+                             out_observe=np_(g["out_observe"]), n_consider=np_(g["n_consider"]),
+                             n_contrib=np_(g["n_contrib"])), orf)
     return g, ob, orf
 
 
@@ -184,6 +183,85 @@ def test_binning_large_bucket_and_global_mode():
     pre = dict(means2D=means2D, depths=depths, radii=radii, conic_opacity=conic, rgb=rgb)
     g, ob, _ = _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
     assert (np.diff(ob["ranges"], axis=1) > 4096).any()
+
+
+def _big_region_branch(depths):
+    """Which branch sort_filter_big takes for a region list longer than 8192
+    entries with these depths: "global" (bitonic network in global memory +
+    per-tile filter) when every depth is equal or one 12-bit digit (from the
+    highest bit on which the depths differ) holds more than 4096 entries,
+    else "split" (depth ranges sorted on chip)."""
+    b = np.asarray(depths, np.float32).view(np.uint32).astype(np.uint64)
+    vary = int(np.bitwise_or.reduce(b)) ^ int(np.bitwise_and.reduce(b))
+    if vary == 0:
+        return "global", len(b)
+    shift = max(vary.bit_length() - 1 - 11, 0)
+    mx = int(np.bincount(((b >> np.uint64(shift)) & np.uint64(4095)).astype(np.int64), minlength=4096).max())
+    return ("global" if mx > 4096 else "split"), mx
+
+
+def _one_big_region_scene(n_big, big_depths, seed):
+    """A 256x128 image (16x8 tiles, 8x4 regions of 2x2 tiles) whose region
+    (3, 1) -- tiles x 6..7, y 2..3 -- receives n_big Gaussians (rects of 1..4
+    tiles inside the region, so the filter splits each entry over its tiles),
+    and 3000 others confined to tile columns 0..4, interleaved in id order."""
+    rng = np.random.default_rng(seed)
+    W, H = 256, 128
+    nb = 3000
+    big = np.stack([rng.uniform(109, 115, n_big), rng.uniform(45, 51, n_big)], 1)
+    other = np.stack([rng.uniform(0, 60, nb), rng.uniform(0, H, nb)], 1)
+    P = n_big + nb
+    order = rng.permutation(P)
+    means2D = np.concatenate([big, other])[order].astype(np.float32)
+    radii = np.concatenate([rng.integers(1, 13, n_big), rng.integers(1, 17, nb)])[order].astype(np.int32)
+    depths = np.concatenate([np.asarray(big_depths, np.float32), rng.uniform(0.5, 50, nb)])[order].astype(np.float32)
+    conic = np.tile(np.array([[0.3, 0.0, 0.3, 0.02]], np.float32), (P, 1))
+    rgb = rng.random((P, 3)).astype(np.float32)
+    cam = dict(W=W, H=H, tanfovx=1.0, tanfovy=1.0, viewmatrix=np.eye(4, dtype=np.float32),
+               projmatrix=np.eye(4, dtype=np.float32), campos=np.zeros(3, np.float32))
+    in_big = np.zeros(P, bool)
+    in_big[np.argsort(order)[:n_big]] = True
+    return cam, dict(means2D=means2D, depths=depths, radii=radii, conic_opacity=conic, rgb=rgb), in_big
+
+
+def test_split_big_region_single_depth_global_sort():
+    # 10,000 entries of one region at one depth: sort_filter_big finds no
+    # varying depth bit and sorts the list in global memory by (depth, compact
+    # index), i.e. ascending id, then filters it per tile (filter_global)
+    n = 10000
+    cam, pre, in_big = _one_big_region_scene(n, np.full(n, 6.5, np.float32), 41)
+    assert _big_region_branch(pre["depths"][in_big]) == ("global", n)
+    g, ob, _ = _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
+    rg = ob["ranges"].reshape(8, 16, 2)
+    counts = (rg[2:4, 6:8, 1] - rg[2:4, 6:8, 0]).astype(np.int64)
+    assert counts.min() > 2000 and counts.sum() > n      # entries spread over all four tiles, some over several
+
+
+def test_split_big_region_crowded_digit_global_sort():
+    # 9,000 entries of one region: 8,500 distinct depths in [4.0, 4.01] and 500
+    # spread over [0.5, 90]; the 12-bit digit under the highest varying bit
+    # lumps the 8,500 together (> 4096), so the list is sorted in global memory
+    rng = np.random.default_rng(43)
+    d = np.concatenate([rng.uniform(4.0, 4.01, 8500), rng.uniform(0.5, 90.0, 500)]).astype(np.float32)
+    d = d[rng.permutation(d.size)]
+    assert np.unique(d[:8500]).size > 4096 or np.unique(d).size > 4096
+    cam, pre, in_big = _one_big_region_scene(d.size, d, 44)
+    branch, mx = _big_region_branch(pre["depths"][in_big])
+    assert branch == "global" and mx > 4096, (branch, mx)
+    assert np.unique(pre["depths"][in_big]).size > 4096
+    _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
+
+
+def test_split_big_region_depth_ranges_on_chip():
+    # the same region with 12,000 well-spread depths takes the on-chip branch
+    # (depth ranges of at most 4096 entries sorted one after another, tile
+    # positions carried over) -- the complement of the two tests above
+    rng = np.random.default_rng(45)
+    d = rng.uniform(0.5, 90.0, 12000).astype(np.float32)
+    d[:200] = d[0]                                       # a tie run inside one range
+    cam, pre, in_big = _one_big_region_scene(d.size, d, 46)
+    assert _big_region_branch(pre["depths"][in_big])[0] == "split"
+    _check_binning_and_render(cam, pre, (0.0, 0.0, 0.0))
 
 
 def test_sub_image_share_matches_full_image():
@@ -286,7 +364,7 @@ def test_autograd_forward_backward_vs_oracle(cfg):
     color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth = ras.render_gaussians(
         means2D, means2D_abs, conic_opacity, rgb, all_map, depths, radii, None, None, cuda_args)
     assert_close_abs(np_(color), rf["color"], "color")
-    assert_counts_close(np_(out_observe), rf["out_observe"], "out_observe")
+    assert_blend_counts(dict(out_observe=np_(out_observe), n_consider=np_(n_consider), n_contrib=np_(n_contrib)), rf)
     assert set(cuda_args["stats_collector"]) >= {"forward_render_time"}
     (color * to_dev(dLd)).sum().backward()
     assert "backward_render_time" in cuda_args["stats_collector"]

@@ -60,3 +60,44 @@ def test_noalloc_knn_limits(gpu):
     # three points: the missing neighbours keep FLT_MAX, as in the reference
     p3 = torch.as_tensor(np.eye(3, dtype=np.float32), device="cuda")
     assert np.array_equal(_noalloc(p3).view(np.uint32), _with_workspace(p3).view(np.uint32))
+
+
+def test_noalloc_knn_from_two_host_threads(gpu):
+    # two host threads, each on a stream of its own, call the entry point at
+    # the same time on different inputs: the per-device lock runs the calls
+    # one after another, so every result equals the workspace entry point's
+    import threading
+    rng = np.random.default_rng(12)
+    inputs = [torch.as_tensor(rng.uniform(-2.0, 2.0, (n, 3)).astype(np.float32), device="cuda")
+              for n in (300_000, 200_003)]
+    refs = [_with_workspace(d) for d in inputs]
+    lib = _lib.load()
+    results, errors = [[], []], []
+
+    def worker(k):
+        try:
+            s = torch.cuda.Stream()
+            d = inputs[k]
+            with torch.cuda.stream(s):
+                for _ in range(4):
+                    out = torch.full((d.shape[0],), float("nan"), device="cuda")
+                    rc = lib.gs_knn_meandist3_noalloc(d.shape[0], _lib.ptr(d), _lib.ptr(out),
+                                                      C.c_void_p(s.cuda_stream))
+                    if rc != 0:
+                        errors.append(lib.gs_last_error())
+                        return
+                    results[k].append(out.cpu().numpy())
+        except Exception as e:   # reported below
+            errors.append(repr(e))
+
+    torch.cuda.synchronize()
+    threads = [threading.Thread(target=worker, args=(k,)) for k in (0, 1)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    for k in (0, 1):
+        assert len(results[k]) == 4
+        for got in results[k]:
+            assert np.array_equal(got.view(np.uint32), refs[k].view(np.uint32)), k

@@ -290,6 +290,16 @@ __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u,
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// the writelane intrinsic (v_writelane_b32), which this compiler has no
+// builtin for: (value, lane, old)
+__device__ int gs_llvm_writelane(int x, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
+
+// v with lane `lane` (wave-uniform) replaced by the wave-uniform value x
+__device__ __forceinline__ uint32_t write_lane(uint32_t v, uint32_t x, int lane)
+{
+    return (uint32_t)gs_llvm_writelane((int)x, lane, (int)v);
+}
+
 // number of set bits of m below this lane
 __device__ __forceinline__ int rank_below(uint64_t m)
 {

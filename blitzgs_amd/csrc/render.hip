@@ -91,6 +91,12 @@ constexpr size_t GACC_BYTES = 64;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Blend blocks are grouped into supertiles of SUPER x SUPER tiles, supertile s
+// on XCD s % 8 (block_to_tile); an XCD's tiles, in supertile order, number at
+// most sched_cap of them.
+constexpr unsigned SUPER = 8;
+__host__ __device__ __forceinline__ unsigned sched_cap(unsigned NS) { return ((NS + 7u) / 8u) * SUPER * SUPER; }
+
 struct GeomLayout {
     int T, NC, CH, WS;
     int RS, NR, G;                // region side (0: grid too large), regions and difference-grid entries of the full grid
@@ -100,6 +106,7 @@ struct GeomLayout {
     // cursors, per-chunk region bases, per-class region lists and the partial
     // per-tile count difference grids
     size_t regmask, rcount, rstart, rcursor, rhist, rcls_count, rcls_list, grid;
+    size_t qwork, sched, scnt;   // split path: per-quadrant work (forward), backward block order
     size_t total;
 };
 
@@ -153,6 +160,12 @@ GeomLayout geom_layout(int P, int W, int H)
     g.rcls_count = o; o = align256(o + sizeof(uint32_t) * REGION_CLASSES);
     g.rcls_list = o; o = align256(o + sizeof(int) * (size_t)REGION_CLASSES * (size_t)g.NR);
     g.grid = o; o = align256(o + sizeof(uint32_t) * (size_t)GRID_PARTS * (size_t)g.G);
+    {
+        const unsigned NS = (unsigned)(((gx + SUPER - 1) / SUPER) * ((gy + SUPER - 1) / SUPER));
+        g.qwork = o; o = align256(o + sizeof(uint32_t) * 4 * (size_t)g.T);
+        g.sched = o; o = align256(o + sizeof(uint32_t) * 8 * (size_t)sched_cap(NS));
+        g.scnt = o; o = align256(o + sizeof(uint32_t) * 8);
+    }
     g.total = o;
     return g;
 }
@@ -1166,37 +1179,42 @@ __global__ __launch_bounds__(BIN_THREADS) void scatter_regions_kernel(
     const int ws = min(i1c, c * CH + wave * WS);
     const int i1 = min(i1c, ws + WS);
     uint32_t next = wbase[(size_t)c * WAVES_PER_BIN + wave];
-    // the inputs of the next two groups are loaded while this group is written
-    struct In {
-        int r;
-        float2 m;
+    // Radius and mean of the group after next, and depth, conic and colour of
+    // the next group -- the latter only for Gaussians with a radius (the
+    // others are not listed and their lines need not be fetched) -- are loaded
+    // while this group is written.
+    struct Ext {
         float d;
         float4 co;
         float3 c;
     };
-    auto load_in = [&](int in, In& v) {
-        load_rm(in, i1, radii, means2D, v.r, v.m);
+    auto load_ext = [&](int in, int r, Ext& v) {
         v.d = 0.f;
         v.co = make_float4(0.f, 0.f, 0.f, 0.f);
         v.c = make_float3(0.f, 0.f, 0.f);
-        if (in < i1) {
+        if (in < i1 && r > 0) {
             v.d = depths[in];
             v.co = conic_opacity[in];
             v.c = make_float3(rgb[3 * (size_t)in], rgb[3 * (size_t)in + 1], rgb[3 * (size_t)in + 2]);
         }
     };
-    In nx1, nx2;
-    load_in(ws + lane, nx1);
-    load_in(ws + 64 + lane, nx2);
+    int r0, r1;
+    float2 m0, m1;
+    Ext e0;
+    load_rm(ws + lane, i1, radii, means2D, r0, m0);
+    load_rm(ws + 64 + lane, i1, radii, means2D, r1, m1);
+    load_ext(ws + lane, r0, e0);
     for (int wb = ws; wb < i1; wb += 64) {
         const int i = wb + lane;
-        const int r = nx1.r;
-        const float2 xy = nx1.m;
-        const float dep = nx1.d;
-        const float4 co = nx1.co;
-        const float3 col = nx1.c;
-        nx1 = nx2;
-        load_in(i + 128, nx2);
+        const int r = r0;
+        const float2 xy = m0;
+        const float dep = e0.d;
+        const float4 co = e0.co;
+        const float3 col = e0.c;
+        r0 = r1;
+        m0 = m1;
+        load_rm(i + 128, i1, radii, means2D, r1, m1);
+        load_ext(i + 64, r0, e0);
         unsigned x0, y0, x1, y1;
         const bool in = clip_rect(r, xy, gx, gy, box, x0, y0, x1, y1);
         const uint64_t lm = gs::ballot(in);
@@ -2413,7 +2431,6 @@ __global__ __launch_bounds__(256) void pointlist_kernel(const uint2* __restrict_
 // an XCD's blocks walk its supertiles in order, four quadrant waves per tile,
 // so the waves resident on one XCD cover a compact patch of the image and
 // share the records of the Gaussians overlapping it in that XCD's L2.
-constexpr unsigned SUPER = 8;
 constexpr unsigned BLOCKS_PER_SUPER = SUPER * SUPER * 4;
 
 __device__ __forceinline__ bool block_to_tile(unsigned b, unsigned gx, unsigned gy, unsigned sgx, unsigned NS,
@@ -2550,6 +2567,7 @@ struct FwdOut {
     int32_t* out_observe;          // split
     int32_t* n_consider;           // split
     int32_t* n_contrib_tile;       // split
+    uint32_t* qwork;               // split: per quadrant (4 tile + quad) the largest last contributor
     float* accum_max_count;        // full (null: flag_max_count off), simp
     float* accum_weights;          // simp
     int32_t* accum_weights_count;  // simp
@@ -2587,6 +2605,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
                 if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = 0;
             }
         }
+        if (MODE == BLEND_SPLIT && lane == 0) O.qwork[4 * tile + quad] = 0u;
         return;
     }
     __shared__ Stage st;
@@ -2634,14 +2653,15 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         }
         __syncthreads();
         const int cnt = (int)__builtin_popcountll(km);
-        // T only decreases, so a batch that starts with no live pixel above
-        // T = 0.5 cannot observe (split path): its entries skip the ballot
-        const bool obs_batch = MODE == BLEND_SPLIT && gs::ballot(px_st.T > 0.5f) != 0;
         // Branch-free blend of one staged entry: every lane evaluates it and
-        // the state changes are selects, so no exec-mask bookkeeping.
-        auto blend = [&](const float4& A, const float4& B, const float4& Cc, [[maybe_unused]] int jj) {
+        // the state changes are selects, so no exec-mask bookkeeping.  OBS
+        // (split path): lane jj of obs_cnt takes the number of pixels that
+        // observe entry jj (T > 0.5 when they blend it), added to the
+        // Gaussian's out_observe after the batch, one atomic per entry.
+        auto blend = [&](auto OBS, const float4& A, const float4& B, const float4& Cc, [[maybe_unused]] int jj,
+                         [[maybe_unused]] uint32_t& obs_cnt) {
             const FwdStep f = fwd_blend_step(px_st, A, B, Cc, pxf, pyf);
-            const bool upd = f.upd, observe = f.observe;
+            const bool upd = f.upd;
             const float wgt = f.wgt;
             if constexpr (MODE == BLEND_GEO) {
                 // the colour's update rule: a pixel that does not take the
@@ -2649,11 +2669,9 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
                 const float w = upd ? wgt : 0.f;
                 for (int c = 0; c < NUM_MAPS; c++) Mv[c] = __builtin_fmaf(st_map[c * 64 + jj], w, Mv[c]);
             } else if constexpr (MODE == BLEND_SPLIT) {
-                if (!obs_batch) return;
-                const uint64_t m = gs::ballot(observe);
-                if (m != 0) {
-                    const int first = (int)__builtin_ctzll(m);
-                    if (lane == first) atomicAdd(&O.out_observe[__float_as_uint(Cc.y)], (int)__builtin_popcountll(m));
+                if constexpr (decltype(OBS)::value) {
+                    const uint32_t m = (uint32_t)__builtin_popcountll(gs::ballot(f.observe));
+                    obs_cnt = gs::write_lane(obs_cnt, m, jj);
                 }
             } else {
                 const bool better = upd && wmax < wgt;
@@ -2673,16 +2691,28 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         };
         // two register sets in turn: the next entry's LDS reads are issued
         // before this entry's arithmetic
-        float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
-        float4 A1, B1, D1;
-        for (int j = 0; j < cnt; j += 2) {
-            if (gs::ballot(px_st.T > 0.0f) == 0) break;
-            A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
-            blend(A0, B0, D0, j);
-            if (j + 1 >= cnt) break;   // (the finished-pixel test runs once per pair)
-            A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
-            blend(A1, B1, D1, j + 1);
-        }
+        auto blend_batch = [&](auto OBS) {
+            uint32_t obs_cnt = 0u;
+            float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
+            float4 A1, B1, D1;
+            for (int j = 0; j < cnt; j += 2) {
+                if (gs::ballot(px_st.T > 0.0f) == 0) break;
+                A1 = st.a[(j + 1) & 63]; B1 = st.b[(j + 1) & 63]; D1 = st.c[(j + 1) & 63];
+                blend(OBS, A0, B0, D0, j, obs_cnt);
+                if (j + 1 >= cnt) break;   // (the finished-pixel test runs once per pair)
+                A0 = st.a[(j + 2) & 63]; B0 = st.b[(j + 2) & 63]; D0 = st.c[(j + 2) & 63];
+                blend(OBS, A1, B1, D1, j + 1, obs_cnt);
+            }
+            if constexpr (decltype(OBS)::value) {
+                if (obs_cnt != 0u) atomicAdd(&O.out_observe[__float_as_uint(st.c[lane].y)], (int)obs_cnt);
+            }
+        };
+        // T only decreases, so a batch that starts with no live pixel above
+        // T = 0.5 cannot observe (split path): it runs without the counts
+        if (MODE == BLEND_SPLIT && gs::ballot(px_st.T > 0.5f) != 0)
+            blend_batch(std::integral_constant<bool, MODE == BLEND_SPLIT>{});
+        else
+            blend_batch(std::false_type{});
         __syncthreads();
         r_cur = r_nxt;
         id_cur = id_nxt;
@@ -2713,9 +2743,11 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     if (MODE == BLEND_SPLIT) {
         const int s_last = gs::wave_sum_i(inside ? (int)px_st.last : 0);
         const int s_n2l = gs::wave_sum_i(inside ? (int)px_st.n2l : 0);
+        const int m_last = gs::wave_max_i(inside ? (int)px_st.last : 0);
         if (lane == 0) {
             if (s_last) atomicAdd(&O.n_consider[tile], s_last);
             if (s_n2l) atomicAdd(&O.n_contrib_tile[tile], s_n2l);
+            O.qwork[4 * tile + quad] = (uint32_t)m_last;   // the backward's work for this wave
         }
     } else if (O.accum_max_count != nullptr && inside && px_st.last > 0) {
         atomicAdd(&O.accum_max_count[imax], 1.0f);
@@ -2954,12 +2986,26 @@ __global__ __launch_bounds__(64) void render_depth_kernel(int W, int H, unsigned
 }
 
 // Clears the gradient accumulators of the listed Gaussians (meta[4] of them)
-// before a backward accumulates into them.
-__global__ __launch_bounds__(256) void zero_gacc_kernel(const uint32_t* __restrict__ meta, float4* __restrict__ gacc)
+// before a backward accumulates into them (blocks nsched and up), beside the
+// backward's block order (blocks 0 .. nsched - 1, bwd_schedule_block; nsched
+// is 8, or 0 without a schedule).
+__device__ void bwd_schedule_block(unsigned x, unsigned gx, unsigned gy, unsigned sgx, unsigned NS,
+                                   const uint32_t* __restrict__ qwork, uint32_t* __restrict__ sched,
+                                   uint32_t* __restrict__ scnt);
+
+__global__ __launch_bounds__(1024) void zero_gacc_kernel(const uint32_t* __restrict__ meta, float4* __restrict__ gacc,
+                                                         unsigned nsched, unsigned gx, unsigned gy, unsigned sgx,
+                                                         unsigned NS, const uint32_t* __restrict__ qwork,
+                                                         uint32_t* __restrict__ sched, uint32_t* __restrict__ scnt)
 {
+    if (blockIdx.x < nsched) {
+        bwd_schedule_block(blockIdx.x, gx, gy, sgx, NS, qwork, sched, scnt);
+        return;
+    }
     const size_t n4 = 4 * (size_t)meta[4];
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x)
+    for (size_t i = (size_t)(blockIdx.x - nsched) * blockDim.x + threadIdx.x; i < n4;
+         i += (size_t)(gridDim.x - nsched) * blockDim.x)
         gacc[i] = z;
 }
 
@@ -3167,6 +3213,61 @@ struct GeoBwd {
     float fx, fy;             // focal lengths
 };
 
+// The backward's block order: per XCD (one block each), the tiles of its
+// supertiles (supertile s on XCD s % 8, as block_to_tile) with any work,
+// heaviest first -- a tile's work is the largest last contributor of its four
+// quadrants, which the forward recorded (qwork; the backward walks each
+// quadrant's list from that position to 0).  Waves are dispatched in block
+// order, so the long ones start first and the short ones fill in at the end
+// instead of a long one starting last.  A counting sort on min(work, 4095),
+// descending; ties in any order (the order only changes the schedule).
+// (one 1024-thread block per XCD x, inside zero_gacc_kernel)
+__device__ void bwd_schedule_block(unsigned x, unsigned gx, unsigned gy, unsigned sgx, unsigned NS,
+                                   const uint32_t* __restrict__ qwork, uint32_t* __restrict__ sched,
+                                   uint32_t* __restrict__ scnt)
+{
+    constexpr int NB = 4096;
+    __shared__ uint32_t hist[NB];
+    __shared__ uint32_t s_wave[32];
+    const unsigned cap = sched_cap(NS);
+    for (int i = threadIdx.x; i < NB; i += 1024) hist[i] = 0u;
+    __syncthreads();
+    // i-th tile of the XCD in supertile order -> tile index, or -1
+    auto tile_of = [&](unsigned i) -> int {
+        const unsigned st = (i / (SUPER * SUPER)) * 8u + x, t = i % (SUPER * SUPER);
+        if (st >= NS) return -1;
+        const unsigned tx = (st % sgx) * SUPER + t % SUPER, ty = (st / sgx) * SUPER + t / SUPER;
+        return tx < gx && ty < gy ? (int)(ty * gx + tx) : -1;
+    };
+    auto bucket_of = [&](int tile) -> int {
+        const uint4 q = reinterpret_cast<const uint4*>(qwork)[tile];
+        const uint32_t w = max(max(q.x, q.y), max(q.z, q.w));
+        return w == 0u ? -1 : NB - 1 - (int)min(w, (uint32_t)(NB - 1));
+    };
+    for (unsigned i = threadIdx.x; i < cap; i += 1024) {
+        const int t = tile_of(i);
+        const int b = t >= 0 ? bucket_of(t) : -1;
+        if (b >= 0) atomicAdd(&hist[b], 1u);
+    }
+    __syncthreads();
+    // exclusive scan of the buckets, four per thread
+    uint32_t v[4], sum = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; j++) { v[j] = hist[4 * threadIdx.x + j]; sum += v[j]; }
+    uint32_t tot;
+    uint32_t run = gs::block_excl_scan_1024(sum, s_wave, &tot);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; j++) { hist[4 * threadIdx.x + j] = run; run += v[j]; }
+    __syncthreads();
+    for (unsigned i = threadIdx.x; i < cap; i += 1024) {
+        const int t = tile_of(i);
+        const int b = t >= 0 ? bucket_of(t) : -1;
+        if (b >= 0) sched[(size_t)x * cap + atomicAdd(&hist[b], 1u)] = (uint32_t)t;
+    }
+    if (threadIdx.x == 0) scnt[x] = tot;
+}
+
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no
 // conic or opacity gradient from a pixel where opacity * G > 0.99 (the alpha
 // clamp is active); |dL/dmean2D| is accumulated but not written out.
@@ -3178,10 +3279,22 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
-    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G)
+    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G,
+    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt)
 {
     unsigned tile, quad, tx, ty;
-    if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
+    if (sched != nullptr) {
+        // bwd_schedule_kernel's order: XCD b % 8 takes its tiles heaviest first,
+        // four quadrant waves per tile
+        const unsigned xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3, i = slot >> 2;
+        if (i >= scnt[xcd]) return;
+        quad = slot & 3u;
+        tile = sched[(size_t)xcd * sched_cap(NS) + i];
+        tx = tile % gx;
+        ty = tile / gx;
+    } else if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) {
+        return;
+    }
     if (cl != nullptr && !cl[tile]) return;
     const int lane = threadIdx.x;
     const int qx = (int)tx * 16 + (int)(quad & 1u) * 8, qy = (int)ty * 16 + (int)(quad >> 1) * 8;
@@ -3485,11 +3598,15 @@ int side_stream(SideStream*& out)
     GS_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "device %d out of range", dev);
     SideStream& ss = g_side[dev];
     if (ss.fork == nullptr) {
+        // the events order work of one device: a device-scope release is
+        // enough (a system-scope one writes the L2s back to memory at every
+        // record)
+        constexpr unsigned ev_flags = hipEventDisableTiming | hipEventDisableSystemFence;
         for (int k = 0; k < 2; k++) {
             GS_HIP(hipStreamCreateWithFlags(&ss.s[k], hipStreamNonBlocking));
-            GS_HIP(hipEventCreateWithFlags(&ss.join[k], hipEventDisableTiming));
+            GS_HIP(hipEventCreateWithFlags(&ss.join[k], ev_flags));
         }
-        GS_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
+        GS_HIP(hipEventCreateWithFlags(&ss.fork, ev_flags));
     }
     out = &ss;
     return GS_OK;
@@ -3802,6 +3919,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     O.final_T = at<float>(img, il.final_T);
     O.n_contrib_px = at<uint32_t>(img, il.n_contrib);
     O.n_contrib2loss_px = at<uint32_t>(img, il.n_contrib2loss);
+    O.qwork = at<uint32_t>(geom, g.qwork);
     const uint32_t* clist = at<const uint32_t>(binning, bl.clist);
     const float4* recs = at<const float4>(geom, g.rec);
     if (mode == BLEND_SPLIT) {
@@ -3848,35 +3966,42 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
     const unsigned gx = (unsigned)((W + 15) / 16), gy = (unsigned)((H + 15) / 16);
     float4* gacc = at<float4>(geom, g.gacc);
     if (R > 0) {
-        // the listed Gaussians' accumulators start at zero (every backward)
-        const unsigned zb = std::min<unsigned>(gs_div_up(4 * (size_t)P, 256), 2048u);
-        GS_TIMED("zero_gacc_kernel", stream,
-                 hipLaunchKernelGGL(zero_gacc_kernel, dim3(zb), dim3(256), 0, stream,
-                                    at<const uint32_t>(geom, g.meta), gacc));
-        GS_LAUNCH_CHECK("zero_gacc_kernel");
         unsigned sgx, NS;
         const unsigned nblk = blend_grid(gx, gy, sgx, NS);
         const uint2* rng = at<uint2>(img, il.ranges);
         const uint32_t* clist = at<const uint32_t>(binning, bl.clist);
         const float4* recs = at<const float4>(geom, g.rec);
+        // the split path's waves heaviest first (the forward recorded each
+        // quadrant's work): the order is computed by eight blocks of the
+        // kernel that clears the listed Gaussians' accumulators (every
+        // backward starts from zero)
+        uint32_t* sched = full ? nullptr : at<uint32_t>(geom, g.sched);
+        uint32_t* scnt = full ? nullptr : at<uint32_t>(geom, g.scnt);
+        const unsigned nsched = full ? 0u : 8u;
+        const unsigned zb = std::min<unsigned>(gs_div_up(4 * (size_t)P, 1024), 512u) + nsched;
+        GS_TIMED("zero_gacc_kernel", stream,
+                 hipLaunchKernelGGL(zero_gacc_kernel, dim3(zb), dim3(1024), 0, stream,
+                                    at<const uint32_t>(geom, g.meta), gacc, nsched, gx, gy, sgx, NS,
+                                    at<const uint32_t>(geom, g.qwork), sched, scnt));
+        GS_LAUNCH_CHECK("zero_gacc_kernel");
         if (full) {
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<true>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}));
+                                        GeoBwd{}, nullptr, nullptr));
         } else if (geo != nullptr) {
             GS_TIMED("render_bwd_geo_kernel", stream,
                      hipLaunchKernelGGL((render_bwd_kernel<false, true>), dim3(nblk), dim3(64), 0, stream, W, H, gx,
                                         gy, sgx, NS, rng, clist, recs, compute_locally, bg,
                                         at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
-                                        reinterpret_cast<float*>(gacc), *geo));
+                                        reinterpret_cast<float*>(gacc), *geo, sched, scnt));
         } else {
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<false>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}));
+                                        GeoBwd{}, sched, scnt));
         }
         GS_LAUNCH_CHECK("render_bwd_kernel");
     }

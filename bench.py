@@ -18,7 +18,10 @@ all-to-all, config 3's 8M Gaussians split over four tile-row ranks.
 `--workload full`: the full-image path (GaussianRasterizer.forward + backward,
 and render_simp) on a config's scene.  `--workload ply`: the trained-scene PLY
 layer (records <-> parameter tensors) at config 2's size, plus one file
-save + load timed end to end.
+save + load timed end to end.  `--workload geo`: the render forward with
+render_geo (the five geometry maps and the plane depth) at a config's size,
+fused into the colour's walk of the lists, against the colour-only forward and
+a second walk.
 
 Prints ONE JSON line.  For the step, `value` is Gaussians/s = P / step time.
 `roofline` describes the dominant kernel, timed live with HIP events on the
@@ -120,7 +123,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route", "full", "ply"], default="step")
+    ap.add_argument("--workload", choices=["step", "knn", "ssim", "adam", "route", "full", "ply", "geo"],
+                    default="step")
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
@@ -959,6 +963,63 @@ def run_ply(args):
     print(json.dumps(out), flush=True)
 
 
+# ------------------------------------------------------------------ render_geo
+
+def run_geo(args):
+    """render_geo's forward (the _r render's five geometry maps and plane
+    depth) at a config's size: the colour-only render forward, the fused
+    forward (maps in the colour's walk of the lists) and the colour forward
+    followed by a second walk for the maps, each from the preprocess outputs
+    (binning included)."""
+    import torch
+    from blitzgs_amd import rasterizer as R
+    from blitzgs_amd import synth
+    gen = {0: synth.config0, 1: synth.config1, 2: synth.config2, 3: synth.config3}[args.config]
+    scene, cam = gen()
+    P = scene["means3D"].shape[0]
+    W, H = cam["W"], cam["H"]
+    dev = torch.device("cuda:0")
+    tt = lambda a: torch.as_tensor(np.ascontiguousarray(a), device=dev)
+    rs = R.GaussianRasterizationSettings(
+        image_height=H, image_width=W, tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"], bg=torch.zeros(3, device=dev),
+        scale_modifier=1.0, viewmatrix=tt(cam["viewmatrix"]), projmatrix=tt(cam["projmatrix"]), sh_degree=3,
+        campos=tt(cam["campos"]), prefiltered=False, debug=False)
+    pre = R._preprocess_forward_raw(tt(scene["means3D"]), tt(scene["scales"]), tt(scene["rotations"]),
+                                    tt(scene["sh"]), tt(scene["opacities"]), rs)
+    _, means2D, depths, radii, _, conic_opacity, rgb, _ = pre
+    rng = np.random.default_rng(7)
+    all_map = rng.uniform(-1.0, 1.0, (P, 5)).astype(np.float32)
+    all_map[:, 2] = rng.uniform(-1.5, -0.5, P)
+    amap = tt(all_map)
+    cl = tt(scene["compute_locally"]).bool() if "compute_locally" in scene else None
+    args_fwd = (rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl)
+    geo = (cam["tanfovx"], cam["tanfovy"], amap)
+
+    def two_walks():
+        out = R._render_forward_raw(*args_fwd)
+        R._render_geo_forward_raw(P, H, W, cam["tanfovx"], cam["tanfovy"], amap, cl, out[0], out[6], out[7], out[8])
+
+    res = {}
+    for name, fn in (("colour_only", lambda: R._render_forward_raw(*args_fwd)),
+                     ("fused", lambda: R._render_forward_raw(*args_fwd, geo=geo)),
+                     ("two_walks", two_walks)):
+        ms, kt, _ = timed(fn, args.steps, args.warmup)
+        per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
+        res[name] = {"ms_per_forward": round(ms, 4),
+                     "blend_kernels_ms": {k: round(v, 4) for k, v in per_kernel.items()
+                                          if k in ("render_fwd_kernel", "render_fwd_geo_kernel", "render_geo_kernel")}}
+        log(f"[bench] render_geo {name}: {ms:.3f} ms per forward")
+    out = header(args, f"render_geo forward ms (colour + 5 maps + plane depth), config {args.config}",
+                 1e3 / res["fused"]["ms_per_forward"], "forwards/s", res["fused"]["ms_per_forward"], "f32",
+                 f"config{args.config}: {P} Gaussians, {W}x{H}, render forward with render_geo",
+                 {"gaussians": P, "image": [W, H]})
+    out["higher_is_better"] = True
+    out["variants"] = res
+    out["roofline"] = None
+    out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -979,7 +1040,7 @@ def main():
         sys.exit(1)
     _lib.load()
     {"step": run_step, "knn": run_knn, "ssim": run_ssim, "adam": run_adam, "route": run_route,
-     "full": run_full, "ply": run_ply}[args.workload](args)
+     "full": run_full, "ply": run_ply, "geo": run_geo}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -51,6 +51,9 @@ _SIGS = {
     "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _c]),
     "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
     "gs_render_geo_forward": (_i, [_i, _i64, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_forward_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [_f, _f, _c, _c, _c, _c]),
+    "gs_render_forward_reserved_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _f, _f, _c, _c,
+                                                                             _c, _c]),
     "gs_render_backward_geo": (_i, [_i, _i64, _i, _i, _c, _f, _f] + [_c] * 13 + [_i, _c, _c, _c, _c, _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),

@@ -57,16 +57,16 @@ def render_gaussians(background, image_height, image_width, means2D, depths, rad
                      compute_locally, viewmatrix, campos, tan_fovx, tan_fovy, all_map, render_geo, debug, args=None):
     timing = _r._want_timing(args)
     H, W = int(image_height), int(image_width)
-    (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
-     ms) = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing,
-                                  bool(debug))
+    # render_geo: the maps in the colour's walk of the lists
+    geo = (tan_fovx, tan_fovy, all_map) if render_geo else None
+    res = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing,
+                                 bool(debug), geo=geo)
+    R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms = res[:10]
     if timing:
         args["stats_collector"]["forward_render_time"] = ms
     dev = means2D.device
     if render_geo:
-        out_all_map, out_plane_depth = _r._render_geo_forward_raw(means2D.size(0), H, W, tan_fovx, tan_fovy, all_map,
-                                                                  compute_locally, R, geom, binning, img,
-                                                                  bool(debug))
+        out_all_map, out_plane_depth = res[10:]
     else:
         out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
         out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)

@@ -2557,6 +2557,11 @@ constexpr int BLEND_SPLIT = 0, BLEND_FULL = 1, BLEND_SIMP = 2;
 // maps (all_map, P x 5) with the colour's weights and writes them and the
 // plane depth, and nothing else
 constexpr int BLEND_GEO = 4;
+// the split path's render and render_geo's maps in one walk: the colour
+// outputs and statistics of BLEND_SPLIT, the maps and plane depth of BLEND_GEO
+constexpr int BLEND_SPLIT_GEO = 5;
+__host__ __device__ constexpr bool is_split(int mode) { return mode == BLEND_SPLIT || mode == BLEND_SPLIT_GEO; }
+__host__ __device__ constexpr bool is_geo(int mode) { return mode == BLEND_GEO || mode == BLEND_SPLIT_GEO; }
 constexpr int NUM_MAPS = 5;   // NUM_ALL_MAP (_r config.h:24)
 
 struct FwdOut {
@@ -2579,8 +2584,9 @@ struct FwdOut {
 
 template <int MODE>
 // (at most 80 VGPRs, so that six waves fit per SIMD: measured 3 % faster than
-// the 84 the compiler picks unbounded; eight waves force spills)
-__global__ __launch_bounds__(64, 6) void render_fwd_kernel(
+// the 84 the compiler picks unbounded; eight waves force spills; the fused
+// render_geo walk carries five more accumulators: five waves, no spills)
+__global__ __launch_bounds__(64, MODE == BLEND_SPLIT_GEO ? 5 : 6) void render_fwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, FwdOut O)
@@ -2596,20 +2602,21 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
     float* __restrict__ out_color = O.out_color;
     if (cl != nullptr && !cl[tile]) {
         if (inside) {
-            if constexpr (MODE == BLEND_GEO) {
+            if constexpr (is_geo(MODE)) {
                 for (int c = 0; c < NUM_MAPS; c++) O.out_all_map[c * HW + pid] = 0.f;
                 O.out_plane_depth[pid] = 0.f;
-            } else {
+            }
+            if constexpr (MODE != BLEND_GEO) {
                 out_color[pid] = 0.f; out_color[HW + pid] = 0.f; out_color[2 * HW + pid] = 0.f;
                 O.final_T[pid] = 0.f; O.n_contrib_px[pid] = 0;
-                if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = 0;
+                if (is_split(MODE)) O.n_contrib2loss_px[pid] = 0;
             }
         }
-        if (MODE == BLEND_SPLIT && lane == 0) O.qwork[4 * tile + quad] = 0u;
+        if (is_split(MODE) && lane == 0) O.qwork[4 * tile + quad] = 0u;
         return;
     }
     __shared__ Stage st;
-    __shared__ float st_map[MODE == BLEND_GEO ? NUM_MAPS * 64 : 1];   // geo: the staged entries' maps
+    __shared__ float st_map[is_geo(MODE) ? NUM_MAPS * 64 : 1];   // geo: the staged entries' maps
     [[maybe_unused]] float Mv[NUM_MAPS] = {0.f, 0.f, 0.f, 0.f, 0.f};
 
     const uint2 range = ranges[tile];
@@ -2644,7 +2651,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         const bool keep = k < n && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
         const uint64_t km = gs::ballot(keep);
         if (keep) stage_put(st, gs::rank_below(km), r_cur, r_cur.gid, k);
-        if constexpr (MODE == BLEND_GEO) {
+        if constexpr (is_geo(MODE)) {
             if (keep) {
                 const int slot = gs::rank_below(km);
                 const float* m = O.all_map + (size_t)NUM_MAPS * r_cur.gid;
@@ -2663,12 +2670,14 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
             const FwdStep f = fwd_blend_step(px_st, A, B, Cc, pxf, pyf);
             const bool upd = f.upd;
             const float wgt = f.wgt;
-            if constexpr (MODE == BLEND_GEO) {
+            if constexpr (is_geo(MODE)) {
                 // the colour's update rule: a pixel that does not take the
                 // entry adds map * 0
                 const float w = upd ? wgt : 0.f;
                 for (int c = 0; c < NUM_MAPS; c++) Mv[c] = __builtin_fmaf(st_map[c * 64 + jj], w, Mv[c]);
-            } else if constexpr (MODE == BLEND_SPLIT) {
+            }
+            if constexpr (MODE == BLEND_GEO) {
+            } else if constexpr (is_split(MODE)) {
                 if constexpr (decltype(OBS)::value) {
                     const uint32_t m = (uint32_t)__builtin_popcountll(gs::ballot(f.observe));
                     obs_cnt = gs::write_lane(obs_cnt, m, jj);
@@ -2709,8 +2718,8 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         };
         // T only decreases, so a batch that starts with no live pixel above
         // T = 0.5 cannot observe (split path): it runs without the counts
-        if (MODE == BLEND_SPLIT && gs::ballot(px_st.T > 0.5f) != 0)
-            blend_batch(std::integral_constant<bool, MODE == BLEND_SPLIT>{});
+        if (is_split(MODE) && gs::ballot(px_st.T > 0.5f) != 0)
+            blend_batch(std::integral_constant<bool, is_split(MODE)>{});
         else
             blend_batch(std::false_type{});
         __syncthreads();
@@ -2719,7 +2728,7 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
         id_nxt = id_nn;
     }
 
-    if constexpr (MODE == BLEND_GEO) {
+    if constexpr (is_geo(MODE)) {
         // plane depth (reference _r forward.cu:411): M4 / -(M0 rx + M1 ry + M2
         // + 1e-8), the 1e-8 a double literal there: the sum in float, the rest
         // in double
@@ -2729,18 +2738,18 @@ __global__ __launch_bounds__(64, 6) void render_fwd_kernel(
             const float sdot = __builtin_fmaf(Mv[0], rx, Mv[1] * ry) + Mv[2];
             O.out_plane_depth[pid] = (float)((double)Mv[4] / -((double)sdot + 1.0e-8));
         }
-        return;
+        if constexpr (MODE == BLEND_GEO) return;
     }
     if (inside) {
         const float Tf = __builtin_fabsf(px_st.T);
         O.final_T[pid] = Tf;
         O.n_contrib_px[pid] = px_st.last;
-        if (MODE == BLEND_SPLIT) O.n_contrib2loss_px[pid] = px_st.n2l;
+        if (is_split(MODE)) O.n_contrib2loss_px[pid] = px_st.n2l;
         out_color[pid] = __builtin_fmaf(Tf, bg[0], px_st.C0);
         out_color[HW + pid] = __builtin_fmaf(Tf, bg[1], px_st.C1);
         out_color[2 * HW + pid] = __builtin_fmaf(Tf, bg[2], px_st.C2);
     }
-    if (MODE == BLEND_SPLIT) {
+    if (is_split(MODE)) {
         const int s_last = gs::wave_sum_i(inside ? (int)px_st.last : 0);
         const int s_n2l = gs::wave_sum_i(inside ? (int)px_st.n2l : 0);
         const int m_last = gs::wave_max_i(inside ? (int)px_st.last : 0);
@@ -3759,7 +3768,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0,
                "conic_opacity must be 16-byte and means2D / rects 8-byte aligned");
-    const bool full = mode != BLEND_SPLIT;
+    const bool full = !is_split(mode);
     GS_REQUIRE(!full || P == 0 || rects != nullptr, "the full path needs rects");
     const GeomLayout g = geom_layout(P, W, H);
     const ImgLayout il = img_layout(W, H);
@@ -3784,7 +3793,7 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
     }
     // per-Gaussian accumulators start at zero: inside the scatter when there
     // are instances, else with a fill kernel each
-    ZeroOut Z{{mode == BLEND_SPLIT ? O.out_observe : nullptr, reinterpret_cast<int32_t*>(O.accum_max_count),
+    ZeroOut Z{{is_split(mode) ? O.out_observe : nullptr, reinterpret_cast<int32_t*>(O.accum_max_count),
                 mode == BLEND_SIMP ? reinterpret_cast<int32_t*>(O.accum_weights) : nullptr,
                 mode == BLEND_SIMP ? O.accum_weights_count : nullptr}};
     if (P > 0 && R == 0) {
@@ -3926,6 +3935,10 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         GS_TIMED("render_fwd_kernel", stream,
                  hipLaunchKernelGGL(render_fwd_kernel<BLEND_SPLIT>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                     NS, ranges, clist, recs, compute_locally, bg, O));
+    } else if (mode == BLEND_SPLIT_GEO) {
+        GS_TIMED("render_fwd_geo_kernel", stream,
+                 hipLaunchKernelGGL(render_fwd_kernel<BLEND_SPLIT_GEO>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy,
+                                    sgx, NS, ranges, clist, recs, compute_locally, bg, O));
     } else if (mode == BLEND_FULL) {
         GS_TIMED("render_fwd_kernel", stream,
                  hipLaunchKernelGGL(render_fwd_kernel<BLEND_FULL>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
@@ -4161,6 +4174,74 @@ extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H,
                                 return render_forward_impl(BLEND_SPLIT, P, capacity, W, H, bg, means2D, depths, radii,
                                                            conic_opacity, rgb, compute_locally, nullptr, geom, binning,
                                                            img, O, n_render, stream);
+                            });
+}
+
+namespace {
+// render_geo's inputs and outputs on a FwdOut; the render host's camera
+// (rasterize_points.cu:325-326,339): focal lengths W / (2 tan_fovx),
+// H / (2 tan_fovy) and centre (W / 2, H / 2), in float
+int set_geo(FwdOut& O, int P, int W, int H, float tan_fovx, float tan_fovy, const float* all_map, float* out_all_map,
+            float* out_plane_depth)
+{
+    GS_REQUIRE((P == 0 || all_map != nullptr) && out_all_map != nullptr && out_plane_depth != nullptr,
+               "all_map, out_all_map and out_plane_depth must be non-null");
+    GS_REQUIRE(tan_fovx > 0.f && tan_fovy > 0.f, "tan_fovx / tan_fovy must be positive");
+    O.all_map = all_map;
+    O.out_all_map = out_all_map;
+    O.out_plane_depth = out_plane_depth;
+    O.focal_x = (float)W / (2.0f * tan_fovx);
+    O.focal_y = (float)H / (2.0f * tan_fovy);
+    O.cx = (float)W * 0.5f;
+    O.cy = (float)H * 0.5f;
+    return GS_OK;
+}
+}  // namespace
+
+extern "C" int gs_render_forward_geo(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
+                                     const float* depths, const int* radii, const float* conic_opacity,
+                                     const float* rgb, const uint8_t* compute_locally, void* geom, void* binning,
+                                     void* img, float* out_color, int32_t* n_render, int32_t* n_consider,
+                                     int32_t* n_contrib, int32_t* out_observe, float tan_fovx, float tan_fovy,
+                                     const float* all_map, float* out_all_map, float* out_plane_depth,
+                                     hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.out_observe = out_observe;
+    O.n_consider = n_consider;
+    O.n_contrib_tile = n_contrib;
+    if (int rc = set_geo(O, P, W, H, tan_fovx, tan_fovy, all_map, out_all_map, out_plane_depth); rc != GS_OK)
+        return rc;
+    return render_forward_impl(BLEND_SPLIT_GEO, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
+                               compute_locally, nullptr, geom, binning, img, O, n_render, stream);
+}
+
+extern "C" int gs_render_forward_reserved_geo(int P, int64_t capacity, int W, int H, const float* bg,
+                                              const float* means2D, const float* depths, const int* radii,
+                                              const float* conic_opacity, const float* rgb,
+                                              const uint8_t* compute_locally, void* geom, void* binning, void* img,
+                                              float* out_color, int32_t* n_render, int32_t* n_consider,
+                                              int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
+                                              float tan_fovx, float tan_fovy, const float* all_map,
+                                              float* out_all_map, float* out_plane_depth, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
+    FwdOut O{};
+    O.out_color = out_color;
+    O.out_observe = out_observe;
+    O.n_consider = n_consider;
+    O.n_contrib_tile = n_contrib;
+    if (int rc = set_geo(O, P, W, H, tan_fovx, tan_fovy, all_map, out_all_map, out_plane_depth); rc != GS_OK)
+        return rc;
+    return reserved_forward(false, P, capacity, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom,
+                            num_rendered, stream, [&] {
+                                return render_forward_impl(BLEND_SPLIT_GEO, P, capacity, W, H, bg, means2D, depths,
+                                                           radii, conic_opacity, rgb, compute_locally, nullptr, geom,
+                                                           binning, img, O, n_render, stream);
                             });
 }
 

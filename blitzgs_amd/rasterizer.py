@@ -203,11 +203,13 @@ def _tile_mask(cl, H, W, device):
 
 
 def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False,
-                        debug=False):
+                        debug=False, geo=None):
     """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
     geomBuffer, binningBuffer, imgBuffer, render_ms).  The binning buffer may be
     sized for more than num_rendered instances (_lib.InstanceReserve); render_ms
-    covers the whole render forward, the instance count included."""
+    covers the whole render forward, the instance count included.
+    geo = (tanfovx, tanfovy, all_maps (P,5)): render_geo in the same walk of the
+    lists; then out_all_map (5,H,W) and out_plane_depth (1,H,W) follow."""
     _require_device(means2D, "means2D")
     dev = means2D.device
     P = means2D.size(0)
@@ -230,6 +232,14 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     n_contrib = torch.empty((T,), **i32)
     out_observe = torch.empty((P,), **i32)
     outs = (ptr(color), ptr(n_render), ptr(n_consider), ptr(n_contrib), ptr(out_observe))
+    maps = None
+    if geo is not None:
+        tanfovx, tanfovy, all_maps = geo
+        if all_maps is None or tuple(all_maps.shape) != (P, 5):
+            raise RuntimeError(f"render_geo needs all_map of shape ({P}, 5)")
+        all_maps = _dev_f32(all_maps, dev)
+        maps = torch.empty((6, H, W), device=dev, dtype=torch.float32)
+        geo_args = (float(tanfovx), float(tanfovy), ptr(all_maps), ptr(maps[:5]), ptr(maps[5:]))
     if timing:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
@@ -239,9 +249,12 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         # one call, no host round trip between the count and the duplication
         binning = torch.empty(lib.gs_render_binning_bytes(cap), device=dev, dtype=torch.uint8)
         Rv = C.c_int64(0)
-        check(lib.gs_render_forward_reserved(P, cap, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii),
-                                             ptr(conic_opacity), ptr(rgb), ptr(cl), ptr(geom), ptr(binning),
-                                             ptr(img), *outs, C.byref(Rv), stream), "gs_render_forward_reserved")
+        args = (P, cap, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
+                ptr(geom), ptr(binning), ptr(img), *outs, C.byref(Rv))
+        if maps is None:
+            check(lib.gs_render_forward_reserved(*args, stream), "gs_render_forward_reserved")
+        else:
+            check(lib.gs_render_forward_reserved_geo(*args, *geo_args, stream), "gs_render_forward_reserved_geo")
         _lib.RESERVE.update(dev, int(Rv.value))
         R = int(Rv.value) if Rv.value <= cap else None
     if R is None:
@@ -253,23 +266,29 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         R = int(Rv.value)
         _lib.RESERVE.update(dev, R)
         binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
-        check(lib.gs_render_forward(P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity),
-                                    ptr(rgb), ptr(cl), ptr(geom), ptr(binning), ptr(img), *outs, stream),
-              "gs_render_forward")
+        args = (P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
+                ptr(geom), ptr(binning), ptr(img), *outs)
+        if maps is None:
+            check(lib.gs_render_forward(*args, stream), "gs_render_forward")
+        else:
+            check(lib.gs_render_forward_geo(*args, *geo_args, stream), "gs_render_forward_geo")
     _lib.debug_sync(debug, "gs_render_forward")
     ms = None
     if timing:
         ev1.record()
         ev1.synchronize()
         ms = ev0.elapsed_time(ev1)
+    if maps is not None:
+        return R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms, maps[:5], maps[5:]
     return R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms
 
 
 def _render_geo_forward_raw(P, H, W, tanfovx, tanfovy, all_maps, compute_locally, R, geom, binning, img,
                             debug=False):
     """render_geo's maps for a completed split forward of P Gaussians (R,
-    geom / binning / img as it returned them): out_all_map (5,H,W),
-    out_plane_depth (1,H,W)."""
+    geom / binning / img as it returned them), by a second walk of its lists:
+    out_all_map (5,H,W), out_plane_depth (1,H,W).  (The operators render the
+    maps in the forward's own walk: _render_forward_raw(geo=...).)"""
     dev = geom.device
     lib = _lib.load()
     cl = _tile_mask(compute_locally, H, W, dev)
@@ -355,17 +374,17 @@ class _RenderGaussians(torch.autograd.Function):
         cl = extended_compute_locally if use_ext else compute_locally
         H, W = int(rs.image_height), int(rs.image_width)
         timing = _want_timing(cuda_args)
-        (R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img,
-         ms) = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing,
-                                   bool(rs.debug))
+        dev = means2D.device
+        # render_geo: the five geometry maps and the plane depth in the colour's
+        # walk of the lists (_r forward.cu:381-384,407-412)
+        geo = (rs.tanfovx, rs.tanfovy, all_maps) if render_geo else None
+        res = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing,
+                                  bool(rs.debug), geo=geo)
+        R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms = res[:10]
         if timing:
             cuda_args["stats_collector"]["forward_render_time"] = ms
-        dev = means2D.device
         if render_geo:
-            # the five geometry maps and the plane depth (_r forward.cu:381-384,407-412)
-            out_all_map, out_plane_depth = _render_geo_forward_raw(means2D.size(0), H, W, rs.tanfovx, rs.tanfovy,
-                                                                   all_maps, cl, R, geom, binning, img,
-                                                                   bool(rs.debug))
+            out_all_map, out_plane_depth = res[10:]
         else:
             # render_geo off: both are zeros (one fill)
             maps = torch.zeros((6, H, W), device=dev, dtype=torch.float32)

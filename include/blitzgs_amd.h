@@ -182,6 +182,30 @@ int gs_render_geo_forward(int P, int64_t R, int image_width, int image_height, f
                           const void* geom, const void* binning, const void* img, float* out_all_map,
                           float* out_plane_depth, gs_stream_t stream);
 
+/* gs_render_forward / gs_render_forward_reserved with render_geo = true
+ * (RenderGaussiansCUDA, diff-gaussian-rasterization_r/rasterize_points.cu:
+ * 273-361; kernel cuda_rasterizer/forward.cu:381-384,407-412): every output
+ * of those calls, and in the same walk of the sorted lists the five
+ * geometry maps out_all_map (5,H,W) -- all_map (P,5) blended with the
+ * colour's weights -- and out_plane_depth (H,W) = all_map[4] /
+ * -(n . ray + 1e-8), n = maps 0..2, ray = ((x - W/2) / fx, (y - H/2) / fy, 1),
+ * fx = W / (2 tan_fovx), fy = H / (2 tan_fovy).  Non-local tiles get zeros. */
+int gs_render_forward_geo(int P, int64_t R, int image_width, int image_height, const float* bg,
+                          const float* means2D, const float* depths, const int* radii,
+                          const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
+                          void* geom, void* binning, void* img, float* out_color, int32_t* n_render,
+                          int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe, float tan_fovx,
+                          float tan_fovy, const float* all_map, float* out_all_map, float* out_plane_depth,
+                          gs_stream_t stream);
+int gs_render_forward_reserved_geo(int P, int64_t capacity, int image_width, int image_height,
+                                   const float* bg, const float* means2D, const float* depths,
+                                   const int* radii, const float* conic_opacity, const float* rgb,
+                                   const uint8_t* compute_locally, void* geom, void* binning, void* img,
+                                   float* out_color, int32_t* n_render, int32_t* n_consider,
+                                   int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
+                                   float tan_fovx, float tan_fovy, const float* all_map,
+                                   float* out_all_map, float* out_plane_depth, gs_stream_t stream);
+
 /* gs_render_backward with render_geo = true (RenderGaussiansBackwardCUDA,
  * rasterize_points.cu:363-436; kernel backward.cu:393-405,427-432,476-490):
  * the maps enter dL/dalpha beside the colour.  all_map_pixels: the

@@ -7,7 +7,10 @@ blend weights, and the blend evaluates exp with the hardware exp2 away from
 the alpha cut-off); out_plane_depth within that bound carried through its
 formula; every gradient, dL/dall_map included, within 1e-3 relative L2;
 through the C ABI (unmasked and with a compute_locally mask), the autograd
-operator with a loss on all three outputs, and the drop-in's raw _C ops."""
+operator with a loss on all three outputs, and the drop-in's raw _C ops.  The
+operators render the maps in the colour's own walk of the lists (the fused
+forward); it is checked bit for bit against the plain forward (every colour
+output) followed by the second walk (gs_render_geo_forward: the maps)."""
 import os
 import sys
 import importlib
@@ -18,8 +21,8 @@ import torch
 
 from blitzgs_amd import rasterizer, synth
 from oracle import oracle as O
-from tests.gpu_helpers import (BLEND_ATOL, assert_close_abs, gpu_render_forward, np_, rel_l2, settings_for,
-                               to_dev)
+from tests.gpu_helpers import (BLEND_ATOL, assert_bitexact, assert_close_abs, buffer_views, gpu_render_forward, np_,
+                               rel_l2, settings_for, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -110,6 +113,46 @@ def test_geo_forward_within_tolerance_and_backward_vs_oracle(gpu, masked):
     # the plane depth's gradient reaches the maps: without it dL/dall_map changes
     assert rel_l2(np_(got["dL_dall_map"]), _oracle(cam, pre, cl, all_map, bg,
                                                     dict(grads, dplane=0 * grads["dplane"]))[3]["dL_dall_map"]) > 1e-2
+
+
+def _fused_vs_two_walks(cam, pre, cl, all_map, bg):
+    """The fused forward (colour and maps in one walk) against the plain
+    forward followed by the second walk: every colour output, statistic and
+    buffer, and the maps and plane depth, bit for bit."""
+    import torch
+    W, H = cam["W"], cam["H"]
+    P = len(all_map)
+    rs = settings_for(cam, bg=bg)
+    dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
+    amap = to_dev(all_map)
+    args = (rs.bg, H, W, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"], to_dev(cl))
+    plain = rasterizer._render_forward_raw(*args)
+    R = plain[0]
+    maps2, plane2 = rasterizer._render_geo_forward_raw(P, H, W, cam["tanfovx"], cam["tanfovy"], amap, to_dev(cl), R,
+                                                       plain[6], plain[7], plain[8])
+    fused = rasterizer._render_forward_raw(*args, geo=(cam["tanfovx"], cam["tanfovy"], amap))
+    torch.cuda.synchronize()
+    assert fused[0] == R
+    for k, name in ((1, "color"), (2, "n_render"), (3, "n_consider"), (4, "n_contrib"), (5, "out_observe")):
+        assert_bitexact(np_(fused[k]), np_(plain[k]), name)
+    vf = buffer_views(R, W, H, fused[7], fused[8], P, dev["depths"], fused[6])
+    vp = buffer_views(R, W, H, plain[7], plain[8], P, dev["depths"], plain[6])
+    for k in ("point_list", "keys", "ranges", "final_T", "n_contrib_px", "n_contrib2loss_px"):
+        assert_bitexact(np_(vf[k]), np_(vp[k]), k)
+    assert_bitexact(np_(fused[10]), np_(maps2), "out_all_map")
+    assert_bitexact(np_(fused[11]), np_(plane2), "out_plane_depth")
+    return fused
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_geo_fused_forward_equals_plain_forward_and_second_walk(gpu, masked):
+    scene, cam, pre, cl, all_map, grads = _case(23 + masked, masked)
+    bg = np.array([0.3, 0.2, 0.1], np.float32)
+    print(f"render_geo fused forward: P={len(all_map)} W={cam['W']} H={cam['H']} masked={masked}", flush=True)
+    fused = _fused_vs_two_walks(cam, pre, cl, all_map, bg)
+    _, _, geo, _ = _oracle(cam, pre, cl, all_map, bg, grads)
+    assert_close_abs(np_(fused[10]), geo["out_all_map"], "out_all_map")
+    assert_plane_depth_close(np_(fused[11]), geo["out_plane_depth"], geo["out_all_map"], cam, "out_plane_depth")
 
 
 def test_geo_autograd_and_raw_ops(gpu, monkeypatch):
@@ -238,6 +281,7 @@ def test_geo_config2_full_size_vs_oracle(gpu):
     cl = np.ones(O.tile_grid(W, H)[::-1], np.uint8)
     bg = np.zeros(3, np.float32)
     print(f"render_geo config 2: P={P} W={W} H={H}", flush=True)
+    _fused_vs_two_walks(cam, pre, cl, all_map, bg)
     rs = settings_for(cam, bg=bg)
     dev = {k: to_dev(pre[k]) for k in ["means2D", "depths", "radii", "conic_opacity", "rgb"]}
     f = gpu_render_forward(rs, dev["means2D"], dev["depths"], dev["radii"], dev["conic_opacity"], dev["rgb"], cl)

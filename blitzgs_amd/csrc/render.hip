@@ -1707,19 +1707,24 @@ __device__ __forceinline__ int region_class(uint32_t n)
 }
 
 // Exclusive scan of N values over a 1024-thread block, each thread taking 8
-// consecutive values per round of 8192 (all 8 loads in flight, one block scan
-// per round): put(i, prefix, value) for every i < N; returns the total.
-template <typename Get, typename Put>
-__device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Get&& get, Put&& put)
+// consecutive values per round of 8192 (one block scan per round):
+// put(i, prefix, value) for every i < N; returns the total.  A value is
+// value(i, fetch(i)): the 8 fetches of a thread (global loads) are all issued
+// before the first value is formed (they read index min(i, N - 1), so that
+// none is conditional), and value may then read LDS.
+template <typename Fetch, typename Value, typename Put>
+__device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Fetch&& fetch, Value&& value, Put&& put)
 {
     uint64_t base = 0;
     for (int r0 = 0; r0 < N; r0 += 8192) {
         const int i0 = r0 + (int)threadIdx.x * 8;
-        uint32_t v[8];
+        uint32_t f[8], v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) f[j] = fetch(min(i0 + j, N - 1));
         uint32_t sum = 0u;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            v[j] = i0 + j < N ? get(i0 + j) : 0u;
+            v[j] = i0 + j < N ? value(i0 + j, f[j]) : 0u;
             sum += v[j];
         }
         uint32_t tot;
@@ -1734,15 +1739,18 @@ __device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Get
     return base;
 }
 
-// Split path, step 2 (scan), one block:
-//   - the per-wave listed counts -> compact index bases (in place), L -> meta[4];
-//   - the difference grid (the sum of the partial grids) summed in 2D (rows,
-//     then columns; in LDS when it fits) -> each local tile's instance count
-//     (tile_count) and, by a scan in local order, its offset (tile_start) and
-//     R -> meta[2..3];
-//   - the region list lengths -> offsets (rstart, and rcursor for the global
-//     cursors) and per-class region lists; the total -> meta[10].
-// cap, host_R, seq: as tilescan_kernel (R > cap: meta[9] set, class lists empty).
+// Split path, step 2 (scan): three blocks, independent of one another.
+//   block 0: the difference grid (the sum of the partial grids) summed in 2D
+//     (rows, then columns; in LDS when it fits) -> each local tile's instance
+//     count (tile_count) and, by a scan in local order, its offset
+//     (tile_start) and R -> meta[2..3]; meta[9] = R > cap (then nothing
+//     further is written: the scatter and the sorts check it); R stored
+//     for the host (host_R, seq: as tilescan_kernel);
+//   block 1: the per-wave listed counts -> compact index bases (in place),
+//     L -> meta[4];
+//   block 2: the region list lengths -> offsets (rstart, and rcursor for the
+//     global cursors) and per-class region lists; the total E -> meta[10]
+//     (E <= R: a region entry stands for one or more instances).
 __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict__ meta, unsigned gx, unsigned lrs,
                                                             const int* __restrict__ tile_of_local,
                                                             uint32_t* __restrict__ grid, int Gfull,
@@ -1760,26 +1768,60 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     __shared__ uint32_t s_wave[32];
     __shared__ uint32_t s_cls[REGION_CLASSES];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    if (tid < REGION_CLASSES) s_cls[tid] = 0u;
-    {
-        const uint64_t L = block_scan_runs(
-            NW, s_wave, [&](int i) { return wcount[i]; }, [&](int i, uint32_t pre, uint32_t) { wcount[i] = pre; });
-        if (tid == 0) meta[4] = (uint32_t)L;
-    }
     const RegionGrid rg = region_grid(meta, lrs);
+    if (blockIdx.x == 1) {
+        const uint64_t L = block_scan_runs(
+            NW, s_wave, [&](int i) { return wcount[i]; }, [&](int, uint32_t f) { return f; },
+            [&](int i, uint32_t pre, uint32_t) { wcount[i] = pre; });
+        if (tid == 0) meta[4] = (uint32_t)L;
+        return;
+    }
+    if (blockIdx.x == 2) {
+        // regions: offsets and size classes
+        if (tid < REGION_CLASSES) s_cls[tid] = 0u;
+        __syncthreads();
+        const int NRb = (int)(rg.nrx * rg.nry);
+        const uint64_t E = block_scan_runs(
+            NRb, s_wave, [&](int r) { return rcount[r]; }, [&](int, uint32_t f) { return f; },
+            [&](int r, uint32_t pre, uint32_t v) {
+                rstart[r] = pre;
+                rcursor[r] = pre;
+                if (v > 0u) {
+                    const int c = region_class(v);
+                    rcls_list[(size_t)c * NR + atomicAdd(&s_cls[c], 1u)] = r;
+                }
+            });
+        __syncthreads();
+        if (tid < REGION_CLASSES) rcls_count[tid] = s_cls[tid];
+        if (tid == 0) meta[10] = (uint32_t)E;
+        return;
+    }
     const unsigned gw = rg.bw + 1;
     const int G = (int)(gw * (rg.bh + 1));
     const bool lds_g = G <= LDS_GRID;
-    // the partial grids summed (into LDS, or into partial 0)
+    // the local tiles' indices, read while the grid is summed
+    const int TL = (int)meta[0];
+    uint32_t t_pre[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) t_pre[j] = TL > 0 ? (uint32_t)tile_of_local[min(tid * 8 + j, TL - 1)] : 0u;
+    // the partial grids summed (into LDS, or into partial 0): four entries per
+    // thread at a time, all 64 of their loads in flight
     uint32_t* gp = lds_g ? s_grid : grid;
-    for (int i = tid; i < G; i += 1024) {
-        uint32_t v[GRID_PARTS];
+    constexpr int EP = 4;
+    for (int i0 = tid; i0 < G; i0 += 1024 * EP) {
+        uint32_t v[EP][GRID_PARTS];
 #pragma unroll
-        for (int k = 0; k < GRID_PARTS; k++) v[k] = grid[(size_t)k * Gfull + i];
-        uint32_t sum = 0u;
+        for (int e = 0; e < EP; e++)
 #pragma unroll
-        for (int k = 0; k < GRID_PARTS; k++) sum += v[k];
-        gp[i] = sum;
+            for (int k = 0; k < GRID_PARTS; k++)
+                v[e][k] = i0 + e * 1024 < G ? grid[(size_t)k * Gfull + i0 + e * 1024] : 0u;
+#pragma unroll
+        for (int e = 0; e < EP; e++) {
+            uint32_t sum = 0u;
+#pragma unroll
+            for (int k = 0; k < GRID_PARTS; k++) sum += v[e][k];
+            if (i0 + e * 1024 < G) gp[i0 + e * 1024] = sum;
+        }
     }
     __syncthreads();
     // rows: one wave per row, 64 columns at a time
@@ -1814,38 +1856,21 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
         }
     }
     __syncthreads();
-    // local tiles in order: counts, offsets, R
-    const int TL = (int)meta[0];
+    // local tiles in order: counts, offsets, R (the first 8192 tiles' indices
+    // were read above)
     const uint64_t R = block_scan_runs(
         TL, s_wave,
-        [&](int l) {
-            const unsigned t = (unsigned)tile_of_local[l];
-            return gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)];
-        },
+        [&](int l) { return l < 8192 ? t_pre[l & 7] : (uint32_t)tile_of_local[l]; },
+        [&](int, uint32_t t) { return gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)]; },
         [&](int l, uint32_t pre, uint32_t v) {
             tile_count[l] = v;
             tile_start[l] = pre;
         });
-    // regions: offsets and size classes
-    const int NRb = (int)(rg.nrx * rg.nry);
-    const uint64_t E = block_scan_runs(
-        NRb, s_wave, [&](int r) { return rcount[r]; },
-        [&](int r, uint32_t pre, uint32_t v) {
-            rstart[r] = pre;
-            rcursor[r] = pre;
-            if (v > 0u) {
-                const int c = region_class(v);
-                rcls_list[(size_t)c * NR + atomicAdd(&s_cls[c], 1u)] = r;
-            }
-        });
-    __syncthreads();
-    const bool over = R > cap || E > cap;
-    if (tid < REGION_CLASSES) rcls_count[tid] = over ? 0u : s_cls[tid];
     if (tid == 0) {
+        const bool over = R > cap;
         meta[2] = (uint32_t)(R & 0xffffffffu);
         meta[3] = (uint32_t)(R >> 32);
         meta[9] = over ? 1u : 0u;
-        meta[10] = (uint32_t)E;
         if (host_R != nullptr) *host_R = readback_word(R, seq);
     }
 }
@@ -2349,6 +2374,7 @@ __global__ __launch_bounds__(NT) void regionsort_kernel(const uint32_t* __restri
     __shared__ RegionLds<NT, K> L;
     const RegionGrid rg = region_grid(meta, lrs);
     const bool all_local = meta[0] == to.gx * to.gy;
+    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: the lists were not written
     const int nl = (int)*cls_count;
     for (int e = blockIdx.x; e < nl; e += gridDim.x) {
         if (e != (int)blockIdx.x) __syncthreads();   // the previous region's reads of LDS are done
@@ -2374,6 +2400,7 @@ __global__ __launch_bounds__(256, 2) void regionsort_small_kernel(const uint32_t
     RegionLds<256, 8>& L8 = *reinterpret_cast<RegionLds<256, 8>*>(&L16);
     const RegionGrid rg = region_grid(meta, lrs);
     const bool all_local = meta[0] == to.gx * to.gy;
+    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: the lists were not written
     const int n2 = (int)cls_count[2], n1 = (int)cls_count[1], n0 = (int)cls_count[0];
     for (int e = blockIdx.x; e < n2 + n1 + n0; e += gridDim.x) {
         if (e != (int)blockIdx.x) __syncthreads();   // the previous region's reads of LDS are done
@@ -2397,6 +2424,7 @@ __global__ __launch_bounds__(NT) void regionsort_big_kernel(const uint32_t* __re
     __shared__ uint32_t s_big[4096 + 64];
     const RegionGrid rg = region_grid(meta, lrs);
     const bool all_local = meta[0] == to.gx * to.gy;
+    if (meta[9] != 0u) return;   // R exceeded the caller's capacity: the lists were not written
     const int nx = (int)*xcount;
     for (int e = blockIdx.x; e < nx; e += gridDim.x) {
         if (e != (int)blockIdx.x) __syncthreads();
@@ -3720,7 +3748,7 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
             GS_LAUNCH_CHECK("count_regions_kernel");
         }
         GS_TIMED("scan_regions_kernel", stream,
-                 hipLaunchKernelGGL(scan_regions_kernel, dim3(1), dim3(1024), 0, stream, meta, gx, lrs, tile_of_local,
+                 hipLaunchKernelGGL(scan_regions_kernel, dim3(3), dim3(1024), 0, stream, meta, gx, lrs, tile_of_local,
                                     at<uint32_t>(geom, g.grid), g.G, tile_count, tile_start,
                                     at<uint32_t>(geom, g.wcount), P > 0 ? g.NC * WAVES_PER_BIN : 0,
                                     at<const uint32_t>(geom, g.rcount),
@@ -3835,13 +3863,22 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         };
         auto list = [&](int c) { return cls + (size_t)c * g.NR; };
         const unsigned g4 = grid_of(REGION_CAP, 256), g3 = grid_of(4096, 256), g0 = grid_of(0, 2048);
-        // the largest lists (one 512-thread block per region, one block per
-        // CU) on the side streams, one per class, beside the smaller ones on
-        // the caller's
+        const unsigned gs = std::min<unsigned>(g0, 512u);
+        // The lists of 4097..8192 entries (one 512-thread block per region,
+        // one block per CU) sort on the caller's stream: they end last, so the
+        // joins of the side streams -- the longer lists (sort_filter_big) on
+        // the first, the lists of up to 4096 entries on the second -- are
+        // already complete when the caller's stream reaches them.
         std::lock_guard<std::mutex> side_lock(g_side_mu);
         SideStream* ss = nullptr;
         if (int rc = side_stream(ss); rc != GS_OK) return rc;
-        if (g4 > 0 || g3 > 0) GS_HIP(hipEventRecord(ss->fork, stream));
+        if (g4 > 0 || gs > 0) GS_HIP(hipEventRecord(ss->fork, stream));
+        if (g3 > 0) {
+            GS_TIMED("regionsort_kernel_8k", stream,
+                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, stream, cc + 3,
+                                        list(3), rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_kernel_8k");
+        }
         if (g4 > 0) {
             GS_HIP(hipStreamWaitEvent(ss->s[0], ss->fork, 0));
             GS_TIMED("regionsort_big_kernel", ss->s[0],
@@ -3850,23 +3887,16 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
             GS_LAUNCH_CHECK("regionsort_big_kernel");
             GS_HIP(hipEventRecord(ss->join[0], ss->s[0]));
         }
-        if (g3 > 0) {
+        if (gs > 0) {
             GS_HIP(hipStreamWaitEvent(ss->s[1], ss->fork, 0));
-            GS_TIMED("regionsort_kernel_8k", ss->s[1],
-                     hipLaunchKernelGGL((regionsort_kernel<512, 16>), dim3(g3), dim3(512), 0, ss->s[1], cc + 3,
-                                        list(3), rcount, rstart, rent, meta, lrs, to));
-            GS_LAUNCH_CHECK("regionsort_kernel_8k");
+            GS_TIMED("regionsort_small_kernel", ss->s[1],
+                     hipLaunchKernelGGL(regionsort_small_kernel, dim3(gs), dim3(256), 0, ss->s[1], cc, cls, g.NR,
+                                        rcount, rstart, rent, meta, lrs, to));
+            GS_LAUNCH_CHECK("regionsort_small_kernel");
             GS_HIP(hipEventRecord(ss->join[1], ss->s[1]));
         }
-        const unsigned gs = std::min<unsigned>(g0, 512u);
-        if (gs > 0) {
-            GS_TIMED("regionsort_small_kernel", stream,
-                     hipLaunchKernelGGL(regionsort_small_kernel, dim3(gs), dim3(256), 0, stream, cc, cls, g.NR, rcount,
-                                        rstart, rent, meta, lrs, to));
-            GS_LAUNCH_CHECK("regionsort_small_kernel");
-        }
         if (g4 > 0) GS_HIP(hipStreamWaitEvent(stream, ss->join[0], 0));
-        if (g3 > 0) GS_HIP(hipStreamWaitEvent(stream, ss->join[1], 0));
+        if (gs > 0) GS_HIP(hipStreamWaitEvent(stream, ss->join[1], 0));
     }
     if (R > 0 && full) {
         const float2* m2 = reinterpret_cast<const float2*>(means2D);

@@ -42,6 +42,11 @@ _SIGS = {
                                    _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward": (_i, [_i, _i, _i, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
                                     _c, _c, _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_preprocess_record_bytes": (_i64, [_i]),
+    "gs_preprocess_forward_rec": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
+                                       _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_preprocess_backward_rec": (_i, [_i, _i, _i, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
+                                        _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_render_geom_bytes": (_sz, [_i, _i, _i]),
     "gs_render_binning_bytes": (_sz, [_i64]),
     "gs_render_img_bytes": (_sz, [_i, _i]),

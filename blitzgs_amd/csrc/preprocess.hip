@@ -190,17 +190,15 @@ __device__ __forceinline__ void load_sh_split(const float* __restrict__ dc, cons
     for (int i = 0; i < 3 * (NC - 1); i++) s[3 + i] = rest[i];
 }
 
-// 3D covariance (upper triangle) of Gaussian idx from its scale and
-// rotation: Sigma = M^T M with M = diag(mod * scale) R (reference
-// forward.cu:118-150).  The backward recomputes it with this same function
-// when the forward's copy was not kept.
-__device__ __forceinline__ void cov3d_of(const float* __restrict__ scales, const float* __restrict__ rotations, int idx,
-                                         float mod, float* c6)
+// 3D covariance (upper triangle) from a Gaussian's scale s (before the
+// modifier) and rotation quaternion q: Sigma = M^T M with
+// M = diag(mod * scale) R (reference forward.cu:118-150).  The backward
+// recomputes it with this same function when the forward's copy was not kept.
+__device__ __forceinline__ void cov3d_from(const float* s_raw, float4 q, float mod, float* c6)
 {
-    const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
     float Rm[3][3];
     quat_rows(q.x, q.y, q.z, q.w, Rm);
-    const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
+    const float s[3] = {mod * s_raw[0], mod * s_raw[1], mod * s_raw[2]};
     float M[3][3];
 #pragma unroll
     for (int i = 0; i < 3; i++)
@@ -214,6 +212,24 @@ __device__ __forceinline__ void cov3d_of(const float* __restrict__ scales, const
     c6[5] = M[0][2] * M[0][2] + M[1][2] * M[1][2] + M[2][2] * M[2][2];
 }
 
+// The preprocess backward's per-Gaussian record (gs_preprocess_forward_rec):
+// the inputs the backward reads for a visible Gaussian, packed by the forward
+// into 48 bytes so that the backward reads them as three 16-byte loads from a
+// dense run instead of gathering 12-, 12-, 16- and 3-byte rows of the input
+// arrays (a wave's visible Gaussians, about one in five at the benchmark's
+// scene, touch nearly every cache line of those arrays).  Per wave of 64
+// Gaussians [64w, 64w+64): mask[w] = the ballot of the visible ones, and
+// records 64w .. 64w + popcount(mask[w]) - 1 hold them in index order.
+//   r0 = (mean x, y, z, scale 0), r1 = (scale 1, scale 2, clamp bits, index),
+//   r2 = rotation quaternion as given (not normalised).
+struct BwdRec {
+    float4* rec;
+    uint64_t* mask;
+};
+
+inline size_t bwdrec_mask_bytes(int P) { return (((size_t)gs_div_up((size_t)P, 64) * 8 + 255) / 256) * 256; }
+inline size_t bwdrec_bytes(int P) { return bwdrec_mask_bytes(P) + (size_t)gs_div_up((size_t)P, 64) * 64 * 48; }
+
 template <int DEG, bool FULL>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
@@ -221,7 +237,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
     const float* __restrict__ sh, int sh_vec16, const float* __restrict__ opacities,
     float* __restrict__ means2D, float* __restrict__ depths, int* __restrict__ radii, float* __restrict__ cov3D,
-    float* __restrict__ conic_opacity, float* __restrict__ rgb, uint8_t* __restrict__ clamped, FullPre F)
+    float* __restrict__ conic_opacity, float* __restrict__ rgb, uint8_t* __restrict__ clamped, FullPre F,
+    BwdRec rec)
 {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= P) return;
@@ -232,6 +249,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float mx = means3D[3 * idx], my = means3D[3 * idx + 1], mz = means3D[3 * idx + 2];
     float o_m2d[2] = {0.f, 0.f}, o_depth = 0.f, o_con[4] = {0.f, 0.f, 0.f, 0.f}, o_rgb[3] = {0.f, 0.f, 0.f};
     float c6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float s_raw[3] = {0.f, 0.f, 0.f};
+    float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
     int o_radius = 0;
     bool o_clamp[3] = {false, false, false};
     float o_ex = 0.f, o_ey = 0.f;
@@ -251,7 +270,9 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 #pragma unroll
             for (int k = 0; k < 6; k++) c6[k] = F.cov3D_precomp[6 * (size_t)idx + k];
         } else {
-            cov3d_of(scales, rotations, idx, mod, c6);
+            q = reinterpret_cast<const float4*>(rotations)[idx];
+            s_raw[0] = scales[3 * idx]; s_raw[1] = scales[3 * idx + 1]; s_raw[2] = scales[3 * idx + 2];
+            cov3d_from(s_raw, q, mod, c6);
         }
 
         Ewa e;
@@ -332,9 +353,26 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     rgb[3 * idx + 0] = o_rgb[0];
     rgb[3 * idx + 1] = o_rgb[1];
     rgb[3 * idx + 2] = o_rgb[2];
-    clamped[3 * idx + 0] = o_clamp[0];
-    clamped[3 * idx + 1] = o_clamp[1];
-    clamped[3 * idx + 2] = o_clamp[2];
+    if (clamped != nullptr) {   // (null: the records hold the flags for the backward)
+        clamped[3 * idx + 0] = o_clamp[0];
+        clamped[3 * idx + 1] = o_clamp[1];
+        clamped[3 * idx + 2] = o_clamp[2];
+    }
+
+    if (rec.rec != nullptr) {   // (split path only)
+        const bool vis = o_radius > 0;
+        const uint64_t m = __ballot(vis);
+        const int lane = threadIdx.x & 63;
+        if (vis) {
+            const int rank = __popcll(m & ((1ull << lane) - 1ull));
+            float4* r = rec.rec + 3 * (size_t)((idx & ~63) + rank);
+            const uint32_t cbits = (o_clamp[0] ? 1u : 0u) | (o_clamp[1] ? 2u : 0u) | (o_clamp[2] ? 4u : 0u);
+            r[0] = make_float4(mx, my, mz, s_raw[0]);
+            r[1] = make_float4(s_raw[1], s_raw[2], __uint_as_float(cbits), __int_as_float(idx));
+            r[2] = q;
+        }
+        if (lane == 0) rec.mask[idx >> 6] = m;   // lane 0 is the wave's lowest index, always < P here
+    }
 }
 
 // dnormvdv (reference auxiliary.h:126-136)
@@ -417,13 +455,40 @@ struct FullPreBwd {
     float* dL_dcov3D;                // P x 6
 };
 
-template <int DEG, bool STAGED, bool FULL>
+// Where preprocess_bwd_one reads a Gaussian's mean, scale (before the
+// modifier), rotation and clamp flags: the input arrays, row idx ...
+struct ArraySrc {
+    const float* __restrict__ means3D;
+    const float* __restrict__ scales;
+    const float* __restrict__ rotations;
+    const uint8_t* __restrict__ clamped;
+    __device__ float3 mean(int idx) const
+    {
+        return make_float3(means3D[3 * idx], means3D[3 * idx + 1], means3D[3 * idx + 2]);
+    }
+    __device__ void scale(int idx, float* s) const
+    {
+        s[0] = scales[3 * idx]; s[1] = scales[3 * idx + 1]; s[2] = scales[3 * idx + 2];
+    }
+    __device__ float4 rot(int idx) const { return reinterpret_cast<const float4*>(rotations)[idx]; }
+    __device__ bool clamp(int idx, int ch) const { return clamped[3 * idx + ch] != 0; }
+};
+
+// ... or the forward's record of it (BwdRec)
+struct RecSrc {
+    float4 r0, r1, r2;
+    __device__ float3 mean(int) const { return make_float3(r0.x, r0.y, r0.z); }
+    __device__ void scale(int, float* s) const { s[0] = r0.w; s[1] = r1.x; s[2] = r1.y; }
+    __device__ float4 rot(int) const { return r2; }
+    __device__ bool clamp(int, int ch) const { return ((__float_as_uint(r1.z) >> ch) & 1u) != 0; }
+};
+
+template <int DEG, bool STAGED, bool FULL, class Src>
 __device__ __forceinline__ void preprocess_bwd_one(
     int idx, int K, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
-    const float* __restrict__ means3D, const float* __restrict__ scales, const float* __restrict__ rotations,
-    const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
-    const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
+    const Src& src, const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
+    const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ m3_row, float* __restrict__ sc_row, float* __restrict__ dL_drotations,
     float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row, const FullPreBwd& F)
@@ -436,7 +501,8 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const bool vec16 = sh_vec16 != 0;
     Cam cam;
     load_cam(cam, view, proj, campos);
-    const float mx = means3D[3 * idx], my = means3D[3 * idx + 1], mz = means3D[3 * idx + 2];
+    const float3 mean = src.mean(idx);
+    const float mx = mean.x, my = mean.y, mz = mean.z;
     const float* V = cam.v;
     const float* PM = cam.p;
     float c6[6];
@@ -448,7 +514,9 @@ __device__ __forceinline__ void preprocess_bwd_one(
         const float2 a = c2[0], b = c2[1], c = c2[2];
         c6[0] = a.x; c6[1] = a.y; c6[2] = b.x; c6[3] = b.y; c6[4] = c.x; c6[5] = c.y;
     } else {
-        cov3d_of(scales, rotations, idx, mod, c6);   // the forward's value, recomputed
+        float sr[3];
+        src.scale(idx, sr);
+        cov3d_from(sr, src.rot(idx), mod, c6);   // the forward's value, recomputed
     }
 
     // ---- conic -> 2D covariance -> 3D covariance and mean (cov2D backward)
@@ -531,7 +599,7 @@ __device__ __forceinline__ void preprocess_bwd_one(
         const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
         float g[3];
 #pragma unroll
-        for (int ch = 0; ch < 3; ch++) g[ch] = clamped[3 * idx + ch] ? 0.0f : dL_drgb[3 * idx + ch];
+        for (int ch = 0; ch < 3; ch++) g[ch] = src.clamp(idx, ch) ? 0.0f : dL_drgb[3 * idx + ch];
         float gsh[3 * NC], dx[3], dy[3], dz[3];
         sh_backward<DEG>(x, y, z, s, g, gsh, dx, dy, dz);
         const float dL_ddir[3] = {dx[0] * g[0] + dx[1] * g[1] + dx[2] * g[2],
@@ -579,11 +647,13 @@ __device__ __forceinline__ void preprocess_bwd_one(
         sc_row[2] = 0.f;
         reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
-        const float4 q = reinterpret_cast<const float4*>(rotations)[idx];
+        const float4 q = src.rot(idx);
         const float r = q.x, x = q.y, y = q.z, z = q.w;
         float Rm[3][3];
         quat_rows(r, x, y, z, Rm);
-        const float s[3] = {mod * scales[3 * idx], mod * scales[3 * idx + 1], mod * scales[3 * idx + 2]};
+        float sr[3];
+        src.scale(idx, sr);
+        const float s[3] = {mod * sr[0], mod * sr[1], mod * sr[2]};
         float M[3][3];
 #pragma unroll
         for (int i = 0; i < 3; i++)
@@ -620,7 +690,10 @@ __device__ __forceinline__ void preprocess_bwd_one(
 // such whole-line writes: the 12-byte per-Gaussian rows are stored normally.)
 constexpr int SH_PITCH = 49;
 
-template <int DEG, bool STAGED, bool FULL>
+// REC: the visible Gaussians' inputs come from the forward's records (BwdRec;
+// lane l of a wave takes the wave's l-th record) and visibility from their
+// masks; radii, means3D, scales, rotations and clamped are not read.
+template <int DEG, bool STAGED, bool FULL, bool REC = false>
 __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     int P, int K, int W, int H, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
@@ -629,13 +702,17 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const uint8_t* __restrict__ clamped, const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
-    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, FullPreBwd F)
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, FullPreBwd F, const float4* __restrict__ rec,
+    const uint64_t* __restrict__ rec_mask)
 {
     __shared__ float s_sh[STAGED ? 256 * SH_PITCH : 1];
     __shared__ uint8_t s_vis[256];
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63, wbase = idx & ~63;
     const bool in = idx < P;
-    const bool vis = in && radii[idx] > 0;
+    uint64_t vmask = 0;
+    if (REC && wbase < P) vmask = rec_mask[wbase >> 6];
+    const bool vis = REC ? ((vmask >> lane) & 1ull) != 0 : (in && radii[idx] > 0);
     // this Gaussian's dL/dmeans3D and dL/dscales rows (stored directly: staging
     // them in LDS for whole-line stores measured slower)
     float* m3_row = dL_dmeans3D + 3 * (size_t)idx;
@@ -673,11 +750,26 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         float* o = F.dL_drest + (size_t)idx * F.M * 3;
         for (int i = 0; i < 3 * F.M; i++) o[i] = 0.f;
     }
-    if (vis) preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
-                                                    means3D, scales, rotations, sh, sh_vec16, cov3D, clamped,
-                                                    dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb,
-                                                    m3_row, sc_row, dL_drotations, dL_dsh, dL_dopacity,
-                                                    s_sh + threadIdx.x * SH_PITCH, F);
+    if (REC) {
+        if (lane < __popcll(vmask)) {
+            const float4* r = rec + 3 * (size_t)(wbase + lane);
+            const RecSrc src{r[0], r[1], r[2]};
+            const int id = __float_as_int(src.r1.w);
+            // a record names a Gaussian of its own wave (a buffer from another
+            // call could name any index: such records are skipped)
+            if ((unsigned)(id - wbase) < 64u && id < P)
+                preprocess_bwd_one<DEG, STAGED, FULL>(id, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src,
+                                                      sh, sh_vec16, cov3D, dL_dmeans2D, m2d_stride,
+                                                      dL_dconic_opacity, dL_drgb, dL_dmeans3D + 3 * (size_t)id,
+                                                      dL_dscales + 3 * (size_t)id, dL_drotations, dL_dsh,
+                                                      dL_dopacity, s_sh + (id - (int)blockIdx.x * 256) * SH_PITCH, F);
+        }
+    } else if (vis) {
+        preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
+                                              ArraySrc{means3D, scales, rotations, clamped}, sh, sh_vec16, cov3D,
+                                              dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb, m3_row, sc_row,
+                                              dL_drotations, dL_dsh, dL_dopacity, s_sh + threadIdx.x * SH_PITCH, F);
+    }
     if (STAGED && FULL) {
         // coalesced copy-out of this block's rows [blockIdx*256, +nrows): 3 DC floats, then 3M rest floats
         __syncthreads();
@@ -714,12 +806,12 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
 
 }  // namespace
 
-extern "C" int gs_preprocess_forward(
+static int preprocess_forward_impl(
     int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
     const float* sh, const float* opacities, float scale_modifier, const float* viewmatrix,
     const float* projmatrix, const float* campos, float tanfovx, float tanfovy, int image_height,
     int image_width, float* means2D, float* depths, int* radii, float* cov3D, float* conic_opacity,
-    float* rgb, uint8_t* clamped, hipStream_t stream)
+    float* rgb, uint8_t* clamped, void* bwd_records, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
@@ -730,7 +822,13 @@ extern "C" int gs_preprocess_forward(
     GS_REQUIRE(image_width > 0 && image_height > 0, "image size must be positive");
     GS_REQUIRE(((uintptr_t)rotations & 15) == 0 && ((uintptr_t)conic_opacity & 15) == 0,
                "rotations and conic_opacity must be 16-byte aligned");
+    GS_REQUIRE(((uintptr_t)bwd_records & 255) == 0, "bwd_records must be 256-byte aligned");
     const int sh_vec16 = ((K & 3) == 0 && ((uintptr_t)sh & 15) == 0) ? 1 : 0;
+    BwdRec rec{};
+    if (bwd_records != nullptr) {
+        rec.mask = static_cast<uint64_t*>(bwd_records);
+        rec.rec = reinterpret_cast<float4*>(static_cast<char*>(bwd_records) + bwdrec_mask_bytes(P));
+    }
     const float fy = (float)image_height / (2.0f * tanfovy);
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
@@ -738,7 +836,7 @@ extern "C" int gs_preprocess_forward(
     GS_TIMED("preprocess_fwd_kernel", stream, hipLaunchKernelGGL((preprocess_fwd_kernel<DEG, false>), grid, block, 0, stream, P, K, image_width,        \
                        image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
                        campos, means3D, scales, rotations, sh, sh_vec16, opacities, means2D, depths, radii, \
-                       cov3D, conic_opacity, rgb, clamped, FullPre{}))
+                       cov3D, conic_opacity, rgb, clamped, FullPre{}, rec))
     switch (D) {
         case 0: GS_PRE_FWD(0); break;
         case 1: GS_PRE_FWD(1); break;
@@ -750,13 +848,43 @@ extern "C" int gs_preprocess_forward(
     return GS_OK;
 }
 
-extern "C" int gs_preprocess_backward(
+extern "C" int gs_preprocess_forward(
+    int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
+    const float* sh, const float* opacities, float scale_modifier, const float* viewmatrix,
+    const float* projmatrix, const float* campos, float tanfovx, float tanfovy, int image_height,
+    int image_width, float* means2D, float* depths, int* radii, float* cov3D, float* conic_opacity,
+    float* rgb, uint8_t* clamped, hipStream_t stream)
+{
+    return preprocess_forward_impl(P, D, K, means3D, scales, rotations, sh, opacities, scale_modifier, viewmatrix,
+                                   projmatrix, campos, tanfovx, tanfovy, image_height, image_width, means2D, depths,
+                                   radii, cov3D, conic_opacity, rgb, clamped, nullptr, stream);
+}
+
+extern "C" int64_t gs_preprocess_record_bytes(int P) { return P <= 0 ? 0 : (int64_t)bwdrec_bytes(P); }
+
+extern "C" int gs_preprocess_forward_rec(
+    int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
+    const float* sh, const float* opacities, float scale_modifier, const float* viewmatrix,
+    const float* projmatrix, const float* campos, float tanfovx, float tanfovy, int image_height,
+    int image_width, float* means2D, float* depths, int* radii, float* cov3D, float* conic_opacity,
+    float* rgb, uint8_t* clamped, void* bwd_records, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P <= 0 || bwd_records != nullptr, "bwd_records must hold gs_preprocess_record_bytes(P) bytes");
+    GS_REQUIRE(P <= 0 || (means2D && depths && radii && conic_opacity && rgb), "null output");
+    return preprocess_forward_impl(P, D, K, means3D, scales, rotations, sh, opacities, scale_modifier, viewmatrix,
+                                   projmatrix, campos, tanfovx, tanfovy, image_height, image_width, means2D, depths,
+                                   radii, cov3D, conic_opacity, rgb, clamped, bwd_records, stream);
+}
+
+static int preprocess_backward_impl(
     int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
     const float* sh, float scale_modifier, const float* viewmatrix, const float* projmatrix,
     const float* campos, float tanfovx, float tanfovy, int image_height, int image_width,
     const int* radii, const float* cov3D, const uint8_t* clamped, const float* dL_dmeans2D,
     int dL_dmeans2D_stride, const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
-    float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, hipStream_t stream)
+    float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, const void* bwd_records,
+    hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
@@ -770,20 +898,27 @@ extern "C" int gs_preprocess_backward(
                "rotations, dL_dconic_opacity and dL_drotations must be 16-byte aligned");
     const int sh_vec16 = ((K & 3) == 0 && ((uintptr_t)sh & 15) == 0 && ((uintptr_t)dL_dsh & 15) == 0) ? 1 : 0;
     const bool staged = K == 16 && ((uintptr_t)dL_dsh & 15) == 0;
+    GS_REQUIRE(((uintptr_t)bwd_records & 255) == 0, "bwd_records must be 256-byte aligned");
+    const uint64_t* rmask = static_cast<const uint64_t*>(bwd_records);
+    const float4* rrec = bwd_records == nullptr ? nullptr
+        : reinterpret_cast<const float4*>(static_cast<const char*>(bwd_records) + bwdrec_mask_bytes(P));
     const float fy = (float)image_height / (2.0f * tanfovy);
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+#define GS_PRE_BWD_K(DEG, ST, RC)                                                                        \
+    GS_TIMED("preprocess_bwd_kernel", stream,                                                            \
+             hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, ST, false, RC>), grid, block, 0, stream, P, K,   \
+                                image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,      \
+                                viewmatrix, projmatrix, campos, means3D, scales, rotations, sh, sh_vec16, \
+                                radii, cov3D, clamped, dL_dmeans2D, dL_dmeans2D_stride,                   \
+                                dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales, dL_drotations,       \
+                                dL_dsh, dL_dopacity, FullPreBwd{}, rrec, rmask))
 #define GS_PRE_BWD(DEG)                                                                                  \
-    if (staged) GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, true, false>), grid, block, 0, stream, P, K, image_width,             \
-                       image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
-                       campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
-                       dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
-                       dL_drotations, dL_dsh, dL_dopacity, FullPreBwd{}));                                 \
-    else GS_TIMED("preprocess_bwd_kernel", stream, hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false, false>), grid, block, 0, stream, P, K, image_width,             \
-                       image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix,      \
-                       campos, means3D, scales, rotations, sh, sh_vec16, radii, cov3D, clamped, dL_dmeans2D, \
-                       dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales,           \
-                       dL_drotations, dL_dsh, dL_dopacity, FullPreBwd{}))
+    if (rrec != nullptr) {                                                                               \
+        if (staged) GS_PRE_BWD_K(DEG, true, true); else GS_PRE_BWD_K(DEG, false, true);                  \
+    } else {                                                                                             \
+        if (staged) GS_PRE_BWD_K(DEG, true, false); else GS_PRE_BWD_K(DEG, false, false);                \
+    }
     switch (D) {
         case 0: GS_PRE_BWD(0); break;
         case 1: GS_PRE_BWD(1); break;
@@ -791,8 +926,38 @@ extern "C" int gs_preprocess_backward(
         default: GS_PRE_BWD(3); break;
     }
 #undef GS_PRE_BWD
+#undef GS_PRE_BWD_K
     GS_LAUNCH_CHECK("preprocess_bwd_kernel");
     return GS_OK;
+}
+
+extern "C" int gs_preprocess_backward(
+    int P, int D, int K, const float* means3D, const float* scales, const float* rotations,
+    const float* sh, float scale_modifier, const float* viewmatrix, const float* projmatrix,
+    const float* campos, float tanfovx, float tanfovy, int image_height, int image_width,
+    const int* radii, const float* cov3D, const uint8_t* clamped, const float* dL_dmeans2D,
+    int dL_dmeans2D_stride, const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
+    float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, hipStream_t stream)
+{
+    return preprocess_backward_impl(P, D, K, means3D, scales, rotations, sh, scale_modifier, viewmatrix, projmatrix,
+                                    campos, tanfovx, tanfovy, image_height, image_width, radii, cov3D, clamped,
+                                    dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,
+                                    dL_dscales, dL_drotations, dL_dsh, dL_dopacity, nullptr, stream);
+}
+
+extern "C" int gs_preprocess_backward_rec(
+    int P, int D, int K, const void* bwd_records, const float* sh, float scale_modifier,
+    const float* viewmatrix, const float* projmatrix, const float* campos, float tanfovx, float tanfovy,
+    int image_height, int image_width, const float* cov3D, const float* dL_dmeans2D, int dL_dmeans2D_stride,
+    const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D, float* dL_dscales,
+    float* dL_drotations, float* dL_dsh, float* dL_dopacity, hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P <= 0 || bwd_records != nullptr, "bwd_records must be the records gs_preprocess_forward_rec wrote");
+    return preprocess_backward_impl(P, D, K, nullptr, nullptr, nullptr, sh, scale_modifier, viewmatrix, projmatrix,
+                                    campos, tanfovx, tanfovy, image_height, image_width, nullptr, cov3D, nullptr,
+                                    dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,
+                                    dL_dscales, dL_drotations, dL_dsh, dL_dopacity, bwd_records, stream);
 }
 
 extern "C" int gs_preprocess_forward_full(
@@ -827,7 +992,7 @@ extern "C" int gs_preprocess_forward_full(
              hipLaunchKernelGGL((preprocess_fwd_kernel<DEG, true>), grid, block, 0, stream, P, 0, image_width, \
                                 image_height, tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, \
                                 campos, means3D, scales, rotations, nullptr, 0, opacities, means2D, depths,     \
-                                radii, cov3D, conic_opacity, rgb, clamped, F))
+                                radii, cov3D, conic_opacity, rgb, clamped, F, BwdRec{}))
     switch (D) {
         case 0: GS_PRE_FWD_FULL(0); break;
         case 1: GS_PRE_FWD_FULL(1); break;
@@ -877,14 +1042,14 @@ extern "C" int gs_preprocess_backward_full(
                                     image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
                                     viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
                                     cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
-                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F));                         \
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr));                         \
     else                                                                                                         \
         GS_TIMED("preprocess_bwd_full_kernel", stream,                                                           \
                  hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false, true>), grid, block, 0, stream, P, 0,       \
                                     image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
                                     viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
                                     cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
-                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F))
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr))
     switch (D) {
         case 0: GS_PRE_BWD_FULL(0); break;
         case 1: GS_PRE_BWD_FULL(1); break;

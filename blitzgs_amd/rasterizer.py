@@ -73,11 +73,14 @@ def preprocess_gaussians(means3D, scales, rotations, sh, opacities, raster_setti
     return _PreprocessGaussians.apply(means3D, scales, rotations, sh, opacities, raster_settings, cuda_args)
 
 
-def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_cov3D=True):
+def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_cov3D=True, records=False,
+                            keep_clamped=True):
     """Direct call of the C ABI; returns the reference's 8-tuple
     (num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped).
     keep_cov3D False: cov3D is None (not written; the backward recomputes it
-    from scales and rotations)."""
+    from scales and rotations).  records True: a 9th element, the backward's
+    record buffer (gs_preprocess_forward_rec), follows; with records,
+    keep_clamped False leaves clamped None (the records hold the flags)."""
     if means3D.ndimension() != 2 or means3D.size(1) != 3:
         raise RuntimeError("means3D must have dimensions (num_points, 3)")
     _require_device(means3D, "means3D")
@@ -92,7 +95,7 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_
     cov3D = torch.empty((P, 6), **f32) if keep_cov3D else None
     conic_opacity = torch.empty((P, 4), **f32)
     rgb = torch.empty((P, 3), **f32)
-    clamped = torch.empty((P, 3), device=dev, dtype=torch.bool)
+    clamped = torch.empty((P, 3), device=dev, dtype=torch.bool) if keep_clamped or not records else None
     if P != 0:
         if sh.size(0) == 0:
             raise RuntimeError("sh must be provided (precomputed colours are not supported by the split path)")
@@ -105,19 +108,30 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_
         proj = _dev_f32(rs.projmatrix, dev)
         campos = _dev_f32(rs.campos, dev)
         lib = _lib.load()
-        rc = lib.gs_preprocess_forward(
-            P, int(rs.sh_degree), sh.size(1), ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), ptr(opacities),
-            float(rs.scale_modifier), ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy),
-            int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii),
-            ptr(cov3D) if cov3D is not None else None,
-            ptr(conic_opacity), ptr(rgb), ptr(clamped), _stream(dev))
-        check(rc, "gs_preprocess_forward")
+        args = (P, int(rs.sh_degree), sh.size(1), ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), ptr(opacities),
+                float(rs.scale_modifier), ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy),
+                int(rs.image_height), int(rs.image_width), ptr(means2D), ptr(depths), ptr(radii),
+                ptr(cov3D) if cov3D is not None else None, ptr(conic_opacity), ptr(rgb),
+                ptr(clamped) if clamped is not None else None)
+        if records:
+            # torch's caching allocator hands out 512-byte aligned blocks
+            rec = torch.empty(lib.gs_preprocess_record_bytes(P), device=dev, dtype=torch.uint8)
+            rc = lib.gs_preprocess_forward_rec(*args, ptr(rec), _stream(dev))
+            check(rc, "gs_preprocess_forward_rec")
+        else:
+            rc = lib.gs_preprocess_forward(*args, _stream(dev))
+            check(rc, "gs_preprocess_forward")
         _lib.debug_sync(getattr(rs, "debug", False), "gs_preprocess_forward")
-    return 0, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped
+    out = (0, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped)
+    if records:
+        return out + (rec if P != 0 else torch.empty(0, device=dev, dtype=torch.uint8),)
+    return out
 
 
 def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
-                             dL_dconic_opacity, dL_drgb):
+                             dL_dconic_opacity, dL_drgb, records=None):
+    """records: the forward's record buffer (_preprocess_forward_raw with
+    records=True); then radii, clamped, scales and rotations are not read."""
     dev = means3D.device
     P = means3D.size(0)
     K = sh.size(1) if sh.ndimension() == 3 else 1
@@ -139,14 +153,24 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
         proj = _dev_f32(rs.projmatrix, dev)
         campos = _dev_f32(rs.campos, dev)
         lib = _lib.load()
-        rc = lib.gs_preprocess_backward(
-            P, int(rs.sh_degree), K, ptr(means3D), ptr(scales), ptr(rotations), ptr(sh), float(rs.scale_modifier),
-            ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height),
-            int(rs.image_width), ptr(radii.contiguous()), ptr(cov3D.contiguous()) if cov3D is not None else None,
-            ptr(clamped.contiguous()),
-            ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
-            ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
-        check(rc, "gs_preprocess_backward")
+        cov = ptr(cov3D.contiguous()) if cov3D is not None else None
+        if records is not None:
+            if records.numel() != lib.gs_preprocess_record_bytes(P):
+                raise RuntimeError("records must be the preprocess forward's record buffer for these Gaussians")
+            rc = lib.gs_preprocess_backward_rec(
+                P, int(rs.sh_degree), K, ptr(records), ptr(sh), float(rs.scale_modifier), ptr(view), ptr(proj),
+                ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height), int(rs.image_width), cov,
+                ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
+                ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
+            check(rc, "gs_preprocess_backward_rec")
+        else:
+            rc = lib.gs_preprocess_backward(
+                P, int(rs.sh_degree), K, ptr(means3D), ptr(scales), ptr(rotations), ptr(sh),
+                float(rs.scale_modifier), ptr(view), ptr(proj), ptr(campos), float(rs.tanfovx), float(rs.tanfovy),
+                int(rs.image_height), int(rs.image_width), ptr(radii.contiguous()), cov, ptr(clamped.contiguous()),
+                ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
+                ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
+            check(rc, "gs_preprocess_backward")
         _lib.debug_sync(getattr(rs, "debug", False), "gs_preprocess_backward")
     return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity
 
@@ -154,23 +178,26 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
 class _PreprocessGaussians(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
-        # cov3D is internal to the pair: the backward recomputes it
-        num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = _preprocess_forward_raw(
-            means3D, scales, rotations, sh, opacities, raster_settings, keep_cov3D=False)
+        # cov3D is internal to the pair: the backward recomputes it from the
+        # records, the visible Gaussians' inputs packed by the forward
+        num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped, records = _preprocess_forward_raw(
+            means3D, scales, rotations, sh, opacities, raster_settings, keep_cov3D=False, records=True,
+            keep_clamped=False)
         # radii and depths take no gradient; unused outputs are not zero-filled
         ctx.set_materialize_grads(False)
         ctx.raster_settings = raster_settings
         ctx.cuda_args = cuda_args
         ctx.num_rendered = num_rendered
         ctx.save_for_backward(means3D, scales, rotations, sh, means2D, depths, radii, cov3D, conic_opacity, rgb,
-                              clamped)
+                              clamped, records)
         ctx.mark_non_differentiable(radii, depths)
         return means2D, rgb, conic_opacity, radii, depths
 
     @staticmethod
     def backward(ctx, grad_means2D, grad_rgb, grad_conic_opacity, grad_radii, grad_depths):
         rs = ctx.raster_settings
-        means3D, scales, rotations, sh, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped = ctx.saved_tensors
+        (means3D, scales, rotations, sh, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped,
+         records) = ctx.saved_tensors
         if grad_means2D is None:
             grad_means2D = torch.zeros_like(means2D)
         if grad_rgb is None:
@@ -178,7 +205,8 @@ class _PreprocessGaussians(torch.autograd.Function):
         if grad_conic_opacity is None:
             grad_conic_opacity = torch.zeros_like(conic_opacity)
         dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity = _preprocess_backward_raw(
-            radii, cov3D, clamped, means3D, scales, rotations, sh, rs, grad_means2D, grad_conic_opacity, grad_rgb)
+            radii, cov3D, clamped, means3D, scales, rotations, sh, rs, grad_means2D, grad_conic_opacity, grad_rgb,
+            records=records)
         return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity, None, None
 
 

@@ -87,6 +87,36 @@ int gs_preprocess_backward(int P, int D, int K, const float* means3D, const floa
                            float* dL_dscales, float* dL_drotations, float* dL_dsh,
                            float* dL_dopacity, gs_stream_t stream);
 
+/* Preprocess forward and backward through a record buffer: the forward packs
+ * each visible Gaussian's mean, scale, rotation and clamp flags into 48 bytes
+ * (with a 64-bit visibility mask per 64 Gaussians) and the backward reads
+ * those instead of means3D, scales, rotations, radii and clamped, which it
+ * does not take.  The counterpart of the reference's geomBuffer, which its
+ * forward fills for its backward (rasterizer_impl.cu:982-1067 writes it,
+ * 1069-1129 reads it); outputs are bit-identical to gs_preprocess_forward /
+ * gs_preprocess_backward on the same inputs.
+ *   bwd_records: gs_preprocess_record_bytes(P) bytes, 256-byte aligned,
+ *   written by gs_preprocess_forward_rec and read by gs_preprocess_backward_rec
+ *   of the same P (records naming a Gaussian outside their own group of 64
+ *   are skipped).  clamped may be NULL here (not written: the records hold
+ *   the flags). */
+int64_t gs_preprocess_record_bytes(int P);
+int gs_preprocess_forward_rec(int P, int D, int K, const float* means3D, const float* scales,
+                              const float* rotations, const float* sh, const float* opacities,
+                              float scale_modifier, const float* viewmatrix, const float* projmatrix,
+                              const float* campos, float tanfovx, float tanfovy, int image_height,
+                              int image_width, float* means2D, float* depths, int* radii, float* cov3D,
+                              float* conic_opacity, float* rgb, uint8_t* clamped, void* bwd_records,
+                              gs_stream_t stream);
+int gs_preprocess_backward_rec(int P, int D, int K, const void* bwd_records, const float* sh,
+                               float scale_modifier, const float* viewmatrix, const float* projmatrix,
+                               const float* campos, float tanfovx, float tanfovy, int image_height,
+                               int image_width, const float* cov3D, const float* dL_dmeans2D,
+                               int dL_dmeans2D_stride, const float* dL_dconic_opacity,
+                               const float* dL_drgb, float* dL_dmeans3D, float* dL_dscales,
+                               float* dL_drotations, float* dL_dsh, float* dL_dopacity,
+                               gs_stream_t stream);
+
 /* ------------------------------------------------------------------------ *
  * Render forward, in two calls because the size of the instance buffers
  * (R = number of Gaussian/tile instances) is known only after counting.

@@ -340,6 +340,54 @@ def test_preprocess_backward_recomputed_cov3D_and_row_layouts():
     assert torch.equal(drot, with_cov[2]) and torch.equal(dsh, with_cov[3]) and torch.equal(dop, with_cov[4])
 
 
+@pytest.mark.parametrize("P,D,K,extent,keep_cov", [(3000, 3, 16, 6.0, False), (4097, 3, 16, 1.2, True),
+                                                   (777, 2, 9, 6.0, False), (64, 0, 1, 6.0, False),
+                                                   (130, 1, 16, 40.0, False)])
+def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
+    """gs_preprocess_forward_rec / gs_preprocess_backward_rec (the backward
+    reads the forward's packed records of the visible Gaussians instead of
+    means3D, scales, rotations, radii and clamped) give the same outputs as
+    gs_preprocess_forward / gs_preprocess_backward, bit for bit: partly visible
+    scenes (extent 6 puts Gaussians behind the near plane and outside the
+    frustum; 40 leaves few visible), partial last waves and blocks, the staged
+    (K = 16) and unstaged dL/dsh layouts, SH degrees 0-3, with and without the
+    forward's cov3D.  The record forward leaves clamped unwritten (the records
+    hold the flags); some colours are forced below zero so that flags are set."""
+    from blitzgs_amd import rasterizer as R
+    scene, cam = synth.small_scene(P, seed=40 + D, W=200, H=150, extent=extent)
+    scene["sh"][::5, 0, 1] = -4.0
+    rs = settings_for(cam, sh_degree=D)
+    t = {k: to_dev(np.asarray(scene[k], np.float32)) for k in ["means3D", "scales", "rotations", "opacities"]}
+    t["sh"] = to_dev(np.ascontiguousarray(np.asarray(scene["sh"], np.float32)[:, :K]))
+    fwd_args = (t["means3D"], t["scales"], t["rotations"], t["sh"], t["opacities"], rs)
+    a = R._preprocess_forward_raw(*fwd_args, keep_cov3D=keep_cov)
+    b = R._preprocess_forward_raw(*fwd_args, keep_cov3D=keep_cov, records=True, keep_clamped=False)
+    names = ["num_rendered", "means2D", "depths", "radii", "cov3D", "conic_opacity", "rgb"]
+    for x, y, name in zip(a[1:7], b[1:7], names[1:]):
+        assert (x is None and y is None) or torch.equal(x, y), name
+    assert b[7] is None
+    radii = np_(a[3])
+    n_vis = int((radii > 0).sum())
+    assert 0 < n_vis < P or extent == 1.2, n_vis
+    assert n_vis < 50 or np_(a[7])[radii > 0].any()          # clamp flags among the visible
+    rng = np.random.default_rng(P)
+    dm2 = to_dev(rng.standard_normal((P, 2)).astype(np.float32))
+    dco = to_dev(rng.standard_normal((P, 4)).astype(np.float32))
+    drgb = to_dev(rng.standard_normal((P, 3)).astype(np.float32))
+    _, _, _, radii_t, cov3D, _, _, clamped = a
+    args = (t["means3D"], t["scales"], t["rotations"], t["sh"], rs, dm2, dco, drgb)
+    ref = R._preprocess_backward_raw(radii_t, cov3D, clamped, *args)
+    # the record path reads neither the input arrays nor radii / clamped:
+    # garbage in them changes nothing
+    junk = {k: torch.full_like(v, float("nan")) for k, v in t.items()}
+    got = R._preprocess_backward_raw(torch.zeros_like(radii_t), cov3D, torch.ones_like(clamped), junk["means3D"],
+                                     junk["scales"], junk["rotations"], t["sh"], rs, dm2, dco, drgb, records=b[8])
+    for x, y, name in zip(ref, got, ["means3D", "scales", "rotations", "sh", "opacity"]):
+        assert torch.equal(x, y), name
+    with pytest.raises(RuntimeError, match="record buffer"):
+        R._preprocess_backward_raw(radii_t, cov3D, clamped, *args, records=b[8][:-256])
+
+
 @pytest.mark.parametrize("cfg", ["small", "config0"])
 def test_autograd_forward_backward_vs_oracle(cfg):
     from blitzgs_amd import rasterizer as R

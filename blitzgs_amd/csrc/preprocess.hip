@@ -490,13 +490,14 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const Src& src, const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
     const float* __restrict__ dL_dmeans2D, int m2d_stride,
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
-    float* __restrict__ m3_row, float* __restrict__ sc_row, float* __restrict__ dL_drotations,
-    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, float* s_row, const FullPreBwd& F)
+    float* __restrict__ m3_row, float* __restrict__ sc_row, float4* __restrict__ rot_row,
+    float* __restrict__ dL_dsh, float* __restrict__ op_row, float* s_row, const FullPreBwd& F)
 {
-    // m3_row / sc_row: this Gaussian's dL/dmeans3D and dL/dscales rows
+    // m3_row / sc_row / rot_row / op_row: where this Gaussian's dL/dmeans3D,
+    // dL/dscales, dL/drotations and dL/dopacity go
     constexpr int NC = (DEG + 1) * (DEG + 1);
     const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
-    dL_dopacity[idx] = gco.w;
+    *op_row = gco.w;
     float* gsh_out = FULL ? nullptr : dL_dsh + (size_t)idx * K * 3;
     const bool vec16 = sh_vec16 != 0;
     Cam cam;
@@ -645,7 +646,7 @@ __device__ __forceinline__ void preprocess_bwd_one(
         sc_row[0] = 0.f;
         sc_row[1] = 0.f;
         sc_row[2] = 0.f;
-        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        *rot_row = make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
         const float4 q = src.rot(idx);
         const float r = q.x, x = q.y, y = q.z, z = q.w;
@@ -679,7 +680,7 @@ __device__ __forceinline__ void preprocess_bwd_one(
         const float q1 = 2 * y * (G[1][0] + G[0][1]) + 2 * z * (G[2][0] + G[0][2]) + 2 * r * (G[1][2] - G[2][1]) - 4 * x * (G[2][2] + G[1][1]);
         const float q2 = 2 * x * (G[1][0] + G[0][1]) + 2 * r * (G[2][0] - G[0][2]) + 2 * z * (G[1][2] + G[2][1]) - 4 * y * (G[2][2] + G[0][0]);
         const float q3 = 2 * r * (G[0][1] - G[1][0]) + 2 * x * (G[2][0] + G[0][2]) + 2 * y * (G[1][2] + G[2][1]) - 4 * z * (G[1][1] + G[0][0]);
-        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(q0, q1, q2, q3);
+        *rot_row = make_float4(q0, q1, q2, q3);
     }
 }
 
@@ -713,8 +714,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     uint64_t vmask = 0;
     if (REC && wbase < P) vmask = rec_mask[wbase >> 6];
     const bool vis = REC ? ((vmask >> lane) & 1ull) != 0 : (in && radii[idx] > 0);
-    // this Gaussian's dL/dmeans3D and dL/dscales rows (stored directly: staging
-    // them in LDS for whole-line stores measured slower)
+    // this Gaussian's dL/dmeans3D and dL/dscales rows
     float* m3_row = dL_dmeans3D + 3 * (size_t)idx;
     float* sc_row = dL_dscales + 3 * (size_t)idx;
     // staged rows hold SH gradients (the full path has none with precomputed
@@ -722,14 +722,16 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const bool sh_rows = !FULL || (!F.colors_precomp && F.rest != nullptr);
     if (STAGED) s_vis[threadIdx.x] = (vis && sh_rows) ? 1 : 0;
     if (in && !vis) {
-        dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
-        m3_row[0] = 0.f;
-        m3_row[1] = 0.f;
-        m3_row[2] = 0.f;
-        sc_row[0] = 0.f;
-        sc_row[1] = 0.f;
-        sc_row[2] = 0.f;
-        reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!REC) {   // (REC: written with the visible rows below)
+            dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
+            m3_row[0] = 0.f;
+            m3_row[1] = 0.f;
+            m3_row[2] = 0.f;
+            sc_row[0] = 0.f;
+            sc_row[1] = 0.f;
+            sc_row[2] = 0.f;
+            reinterpret_cast<float4*>(dL_drotations)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         if (FULL) {
             for (int k = 0; k < 6; k++) F.dL_dcov3D[6 * (size_t)idx + k] = 0.f;
         } else if (!STAGED) {
@@ -751,6 +753,13 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         for (int i = 0; i < 3 * F.M; i++) o[i] = 0.f;
     }
     if (REC) {
+        // lane l computes the wave's l-th visible Gaussian; its dL/dmeans3D,
+        // dL/dscales and dL/drotations come back to that Gaussian's own lane
+        // (ds_bpermute), which writes them with the zero rows of the invisible
+        // ones: every row of the wave's run leaves in the same few store
+        // instructions, so no cache line is written back half-filled
+        float m3[3] = {0.f, 0.f, 0.f}, sc[3] = {0.f, 0.f, 0.f}, op = 0.f;
+        float4 rot = make_float4(0.f, 0.f, 0.f, 0.f);
         if (lane < __popcll(vmask)) {
             const float4* r = rec + 3 * (size_t)(wbase + lane);
             const RecSrc src{r[0], r[1], r[2]};
@@ -760,15 +769,34 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
             if ((unsigned)(id - wbase) < 64u && id < P)
                 preprocess_bwd_one<DEG, STAGED, FULL>(id, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src,
                                                       sh, sh_vec16, cov3D, dL_dmeans2D, m2d_stride,
-                                                      dL_dconic_opacity, dL_drgb, dL_dmeans3D + 3 * (size_t)id,
-                                                      dL_dscales + 3 * (size_t)id, dL_drotations, dL_dsh,
-                                                      dL_dopacity, s_sh + (id - (int)blockIdx.x * 256) * SH_PITCH, F);
+                                                      dL_dconic_opacity, dL_drgb, m3, sc, &rot, dL_dsh, &op,
+                                                      s_sh + (id - (int)blockIdx.x * 256) * SH_PITCH, F);
+        }
+        const int from = 4 * __popcll(vmask & ((1ull << lane) - 1ull));   // this row's computing lane, x4
+        const auto take = [&](float v) {
+            const float x = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(v)));
+            return vis ? x : 0.f;
+        };
+        const float o_m0 = take(m3[0]), o_m1 = take(m3[1]), o_m2 = take(m3[2]);
+        const float o_s0 = take(sc[0]), o_s1 = take(sc[1]), o_s2 = take(sc[2]);
+        const float4 o_r = make_float4(take(rot.x), take(rot.y), take(rot.z), take(rot.w));
+        if (in) {
+            // dL/dopacity is dL/dconic_opacity.w for every Gaussian
+            dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
+            m3_row[0] = o_m0;
+            m3_row[1] = o_m1;
+            m3_row[2] = o_m2;
+            sc_row[0] = o_s0;
+            sc_row[1] = o_s1;
+            sc_row[2] = o_s2;
+            reinterpret_cast<float4*>(dL_drotations)[idx] = o_r;
         }
     } else if (vis) {
         preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
                                               ArraySrc{means3D, scales, rotations, clamped}, sh, sh_vec16, cov3D,
                                               dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb, m3_row, sc_row,
-                                              dL_drotations, dL_dsh, dL_dopacity, s_sh + threadIdx.x * SH_PITCH, F);
+                                              reinterpret_cast<float4*>(dL_drotations) + idx, dL_dsh,
+                                              dL_dopacity + idx, s_sh + threadIdx.x * SH_PITCH, F);
     }
     if (STAGED && FULL) {
         // coalesced copy-out of this block's rows [blockIdx*256, +nrows): 3 DC floats, then 3M rest floats

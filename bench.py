@@ -62,11 +62,12 @@ def stage_bytes(P, P_vis, R, npx, E=None):
         binning = 32 * P + 100 * P_vis + 24 * E + 4 * R
     return {
         # reads means3D, scales, rotations, opacity (44 B) of all, SH (192 B) of the visible; writes means2D,
-        # depth, radius, conic+opacity, rgb, clamped (47 B) of all (cov3D is recomputed by the backward)
-        "preprocess_fwd_kernel": 91 * P + 192 * P_vis,
-        # writes the five gradients (236 B) and reads radius (4 B) of all; reads means3D, scales, rotations,
-        # clamped, the three incoming gradients and SH (271 B) of the visible
-        "preprocess_bwd_kernel": 240 * P + 271 * P_vis,
+        # depth, radius, conic+opacity, rgb (44 B) of all, the backward's 48-byte record of the visible and a
+        # 64-bit mask per 64 Gaussians (cov3D is recomputed by the backward, the records hold the clamp flags)
+        "preprocess_fwd_kernel": 88 * P + P // 8 + 240 * P_vis,
+        # writes the five gradients (236 B) and reads dL/dopacity (4 B) of all and the masks; reads the record,
+        # the rest of dL/dconic_opacity, dL/dmeans2D, dL/drgb and SH (272 B) of the visible
+        "preprocess_bwd_kernel": 240 * P + P // 8 + 272 * P_vis,
         "binning": binning,
         "render_fwd_kernel": 40 * R + 24 * npx,
         "render_bwd_kernel": 40 * R + 32 * npx,

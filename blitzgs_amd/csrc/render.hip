@@ -3305,25 +3305,151 @@ __device__ void bwd_schedule_block(unsigned x, unsigned gx, unsigned gy, unsigne
     if (threadIdx.x == 0) scnt[x] = tot;
 }
 
+// The split path's backward over a 16x8 half tile (half 0: pixel rows 0-7,
+// 1: rows 8-15) in one wave, two pixels per lane: lane l takes the pixels
+// (x0 + l % 8, y) and (x0 + 8 + l % 8, y), y = y0 + l / 8.  Each staged
+// entry is evaluated for both pixels and their twelve terms enter one wave
+// reduction (the |dmean| terms as |a| + |b| per lane), so the reduction and
+// the atomics are paid once per two pixels.  It pays when the Gaussians are
+// wide enough that an entry the wave admits usually touches both 8x8 halves
+// of the 16x8 footprint: the blocks take it when a Gaussian has
+// TWO_PX_MIN_INSTANCES tile instances or more on average (two_px_lanes).
+// Measured: config 1 (R / L = 55) 0.402 -> 0.366 ms, config 2 (R / L = 7.2)
+// 0.651 -> 0.727 ms; a model of the two walks' admitted entries puts the
+// break-even at R / L ~ 24 on both scene families.
+constexpr uint64_t TWO_PX_MIN_INSTANCES = 24;
+
+__device__ __forceinline__ bool two_px_lanes(const uint32_t* __restrict__ meta)
+{
+    const uint64_t R = (uint64_t)meta[2] | ((uint64_t)meta[3] << 32), L = meta[4];
+    return R >= TWO_PX_MIN_INSTANCES * L;
+}
+
+__device__ __forceinline__ void bwd_half_tile(int W, int H, unsigned gx, unsigned tile, unsigned half,
+                                              const uint2* __restrict__ ranges, const uint32_t* __restrict__ clist,
+                                              const float4* __restrict__ rec, const float* __restrict__ bg,
+                                              const float* __restrict__ final_T,
+                                              const uint32_t* __restrict__ n_contrib_px,
+                                              const float* __restrict__ dL_dpixels, float* __restrict__ gacc,
+                                              Stage& st)
+{
+    const unsigned tx = tile % gx, ty = tile / gx;
+    const int lane = threadIdx.x;
+    const int qx = (int)tx * 16, qy = (int)ty * 16 + (int)half * 8;
+    const int pxa = qx + (lane & 7), pxb = pxa + 8, py = qy + (lane >> 3);
+    const bool ina = pxa < W && py < H, inb = pxb < W && py < H;
+    const size_t pida = (size_t)py * W + pxa, pidb = pida + 8;
+    const size_t HW = (size_t)H * W;
+    const float Tfa = ina ? final_T[pida] : 0.f, Tfb = inb ? final_T[pidb] : 0.f;
+    const int lasta = ina ? (int)n_contrib_px[pida] : 0, lastb = inb ? (int)n_contrib_px[pidb] : 0;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f;
+    if (ina) { a0 = dL_dpixels[pida]; a1 = dL_dpixels[HW + pida]; a2 = dL_dpixels[2 * HW + pida]; }
+    if (inb) { b0 = dL_dpixels[pidb]; b1 = dL_dpixels[HW + pidb]; b2 = dL_dpixels[2 * HW + pidb]; }
+    const int maxlast = gs::wave_max_i(max(lasta, lastb));
+    if (maxlast == 0) return;
+
+    const uint32_t* list = clist + ranges[tile].x;
+    const float qx0 = (float)qx, qy0 = (float)qy;
+    const float bga = bg[0] * a0 + bg[1] * a1 + bg[2] * a2, bgb = bg[0] * b0 + bg[1] * b1 + bg[2] * b2;
+    const BwdConst ka{(float)pxa, (float)py, a0, a1, a2, -Tfa * bga, lasta};
+    const BwdConst kb{(float)pxb, (float)py, b0, b1, b2, -Tfb * bgb, lastb};
+    const int my_k = gs::wave_sum12_index(lane);
+    BwdPixel pa{Tfa, 0.f, 0.f, 0.f}, pb{Tfb, 0.f, 0.f, 0.f};
+
+    // the same walk and software pipeline as the 8x8 quadrant waves
+    uint32_t id_cur = maxlast - 1 - lane >= 0 ? list[maxlast - 1 - lane] : 0u;
+    uint32_t id_nxt = maxlast - 65 - lane >= 0 ? list[maxlast - 65 - lane] : 0u;
+    Rec r_cur{};
+    if (maxlast - 1 - lane >= 0) r_cur = load_rec<false>(rec, id_cur);
+
+    for (int top = maxlast; top > 0; top -= 64) {
+        const int k = top - 1 - lane;
+        Rec r_nxt{};
+        uint32_t id_nn = 0;
+        if (k - 64 >= 0) r_nxt = load_rec<false>(rec, id_nxt);
+        if (k - 128 >= 0) id_nn = list[k - 128];
+        // the staging cull tests the rectangle of both halves' pixels whose
+        // last contributor lies past top - 64 (one of the two sets is not empty)
+        const int thr = max(top - 64, 0);
+        const uint64_t ma = gs::ballot(lasta > thr), mb = gs::ballot(lastb > thr);
+        float cx0 = 3.0e38f, cy0 = 3.0e38f, cx1 = -3.0e38f, cy1 = -3.0e38f;
+        if (ma != 0) active_rect(ma, qx0, qy0, cx0, cy0, cx1, cy1);
+        if (mb != 0) {
+            float x0, y0, x1, y1;
+            active_rect(mb, qx0 + 8.f, qy0, x0, y0, x1, y1);
+            cx0 = __builtin_fminf(cx0, x0);
+            cy0 = __builtin_fminf(cy0, y0);
+            cx1 = __builtin_fmaxf(cx1, x1);
+            cy1 = __builtin_fmaxf(cy1, y1);
+        }
+        const bool keep = k >= 0 && rec_may_touch(r_cur, cx0, cy0, cx1, cy1);
+        const uint64_t km = gs::ballot(keep);
+        if (keep) stage_put(st, gs::rank_below(km), r_cur, id_cur, k);
+        __syncthreads();
+        const int cnt = (int)__builtin_popcountll(km);
+        for (int j = 0; j < cnt; j++) {
+            const float4 A = st.a[j];
+            const float4 B = st.b[j];
+            const float4 Cc = st.c[j];
+            const BwdEval ea = bwd_eval(ka, A, B, Cc);
+            const BwdEval eb = bwd_eval(kb, A, B, Cc);
+            if (gs::ballot(ea.valid || eb.valid) == 0) continue;
+            float va[12], vb[12], v[12];
+            bwd_apply<false>(pa, ka, A, B, Cc, ea, va);
+            bwd_apply<false>(pb, kb, A, B, Cc, eb, vb);
+#pragma unroll
+            for (int q = 0; q < 11; q++) v[q] = va[q] + vb[q];
+            v[2] = __builtin_fabsf(va[2]) + __builtin_fabsf(vb[2]);
+            v[3] = __builtin_fabsf(va[3]) + __builtin_fabsf(vb[3]);
+            v[11] = va[11];   // never read back
+            const uint32_t cx = __builtin_amdgcn_readfirstlane(__float_as_uint(Cc.y));
+            const float tot = gs::wave_sum12<true>(v);
+            if (my_k >= 0 && my_k < 11) unsafeAtomicAdd(gacc + (size_t)cx * 16 + my_k, tot);
+        }
+        __syncthreads();
+        r_cur = r_nxt;
+        id_cur = id_nxt;
+        id_nxt = id_nn;
+    }
+}
+
 // FULL: the full-image path's rule (reference _f backward.cu:560-566): no
 // conic or opacity gradient from a pixel where opacity * G > 0.99 (the alpha
 // clamp is active); |dL/dmean2D| is accumulated but not written out.
 // GEO: render_geo (reference _r backward.cu:393-405,427-432,476-490): the five
 // maps enter dL/dalpha beside the colour, and their gradients
 // alpha T dL/dmap go to accumulator slots 11..15.
+// The split path without render_geo (!FULL && !GEO) walks 16x8 half tiles
+// instead of quadrants when the scene's Gaussians are wide (two_px_lanes,
+// from the forward's counts in meta; block-uniform).  Occupancy: six waves
+// per SIMD (80 VGPRs) except with render_geo's map terms.
 template <bool FULL, bool GEO = false>
-__global__ __launch_bounds__(64) void render_bwd_kernel(
+__global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
     const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G,
-    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt)
+    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt, const uint32_t* __restrict__ meta)
 {
+    __shared__ Stage st;
     unsigned tile, quad, tx, ty;
     if (sched != nullptr) {
         // bwd_schedule_kernel's order: XCD b % 8 takes its tiles heaviest first,
-        // four quadrant waves per tile
-        const unsigned xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3, i = slot >> 2;
+        // four quadrant waves per tile (or two half-tile waves: the grid's
+        // other half of the blocks then has nothing to do)
+        const unsigned xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+        if constexpr (!FULL && !GEO) {
+            if (two_px_lanes(meta)) {
+                const unsigned i = slot >> 1;
+                if (i >= scnt[xcd]) return;
+                const unsigned t = sched[(size_t)xcd * sched_cap(NS) + i];
+                if (cl != nullptr && !cl[t]) return;
+                bwd_half_tile(W, H, gx, t, slot & 1u, ranges, clist, rec, bg, final_T, n_contrib_px, dL_dpixels,
+                              gacc, st);
+                return;
+            }
+        }
+        const unsigned i = slot >> 2;
         if (i >= scnt[xcd]) return;
         quad = slot & 3u;
         tile = sched[(size_t)xcd * sched_cap(NS) + i];
@@ -3368,7 +3494,6 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(
         }
     }
 
-    __shared__ Stage st;
     __shared__ float st_map[GEO ? NUM_MAPS * 64 : 1];
 
     const uint32_t* list = clist + ranges[tile].x;
@@ -4032,19 +4157,19 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                      hipLaunchKernelGGL(render_bwd_kernel<true>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}, nullptr, nullptr));
+                                        GeoBwd{}, nullptr, nullptr, nullptr));
         } else if (geo != nullptr) {
             GS_TIMED("render_bwd_geo_kernel", stream,
                      hipLaunchKernelGGL((render_bwd_kernel<false, true>), dim3(nblk), dim3(64), 0, stream, W, H, gx,
                                         gy, sgx, NS, rng, clist, recs, compute_locally, bg,
                                         at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
-                                        reinterpret_cast<float*>(gacc), *geo, sched, scnt));
+                                        reinterpret_cast<float*>(gacc), *geo, sched, scnt, nullptr));
         } else {
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<false>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}, sched, scnt));
+                                        GeoBwd{}, sched, scnt, at<const uint32_t>(geom, g.meta)));
         }
         GS_LAUNCH_CHECK("render_bwd_kernel");
     }

@@ -47,8 +47,13 @@ def _cuda_args(avoid):
             "avoid_pixel_all2all": avoid, "stats_collector": {}}
 
 
-def _scene():
-    scene, cam = synth.small_scene(7000, seed=64, W=287, H=213, extent=1.4, log_mu=-2.4)
+def _scene(wide=False):
+    # wide: Gaussians with ~67 tile instances each, for which the backward
+    # walks 16x8 half tiles, two pixels per lane
+    if wide:
+        scene, cam = synth.small_scene(2500, seed=64, W=287, H=213, extent=1.4, log_mu=-1.2)
+    else:
+        scene, cam = synth.small_scene(7000, seed=64, W=287, H=213, extent=1.4, log_mu=-2.4)
     gx, gy = (287 + 15) // 16, (213 + 15) // 16
     cl = np.zeros((gy, gx), np.uint8)
     cl[3:9, :] = 1                                   # a tile-row block, as the strategy builds
@@ -57,10 +62,10 @@ def _scene():
     return scene, cam, cl, ext
 
 
-@pytest.mark.parametrize("avoid", [False, True])
-def test_gaussian_renderer_call_sequence(f_pkg, avoid):
+@pytest.mark.parametrize("avoid,wide", [(False, False), (True, False), (True, True)])
+def test_gaussian_renderer_call_sequence(f_pkg, avoid, wide):
     F = f_pkg
-    scene, cam, cl_np, ext_np = _scene()
+    scene, cam, cl_np, ext_np = _scene(wide)
     bg = (0.1, 0.3, 0.2)
     t = lambda a: to_dev(np.asarray(a, np.float32))
     raster_settings = F.GaussianRasterizationSettings(

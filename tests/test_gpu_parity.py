@@ -388,17 +388,26 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
         R._preprocess_backward_raw(radii_t, cov3D, clamped, *args, records=b[8][:-256])
 
 
-@pytest.mark.parametrize("cfg", ["small", "config0"])
+@pytest.mark.parametrize("cfg", ["small", "config0", "wide"])
 def test_autograd_forward_backward_vs_oracle(cfg):
+    """The autograd pair against the oracle's chain.  "wide": Gaussians with
+    more than 24 tile instances each on average, for which the backward walks
+    16x8 half tiles with two pixels per lane instead of 8x8 quadrants (the
+    200x150 image leaves partial tiles on both edges)."""
     from blitzgs_amd import rasterizer as R
     if cfg == "small":
         scene, cam = synth.small_scene(3000, seed=12, W=200, H=150, extent=1.2)
         bg = (0.3, 0.2, 0.1)
+    elif cfg == "wide":
+        scene, cam = synth.small_scene(2500, seed=91, W=200, H=150, extent=1.2, log_mu=-1.2)
+        bg = (0.1, 0.2, 0.3)
     else:
         scene, cam = synth.config0()
         bg = (0.0, 0.0, 0.0)
     dLd = scene["dL_dimage"]
     pre, bn, rf, rb, pb = _grad_chain(scene, cam, bg, dLd)
+    n_inst, n_listed = len(bn["point_list"]), int((pre["radii"] > 0).sum())
+    assert (n_inst >= 24 * n_listed) == (cfg == "wide"), (n_inst, n_listed)
     rs = settings_for(cam, bg=bg)
     params = {k: to_dev(scene[k]).requires_grad_(True) for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
     ras = R.GaussianRasterizer(rs)

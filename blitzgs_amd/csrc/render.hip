@@ -2611,10 +2611,12 @@ struct FwdOut {
 };
 
 template <int MODE>
-// (at most 80 VGPRs, so that six waves fit per SIMD: measured 3 % faster than
-// the 84 the compiler picks unbounded; eight waves force spills; the fused
-// render_geo walk carries five more accumulators: five waves, no spills)
-__global__ __launch_bounds__(64, MODE == BLEND_SPLIT_GEO ? 5 : 6) void render_fwd_kernel(
+// (Waves per SIMD.  The split path's walk: seven (72 VGPRs; one 8-byte value
+// spilled around the loop, none inside it): measured 2.5 % faster than six,
+// and six was 3 % faster than the 84 VGPRs the compiler picks unbounded;
+// eight force spills inside the loop and were slower.  The other paths: six;
+// the fused render_geo walk carries five more accumulators: five, no spills.)
+__global__ __launch_bounds__(64, MODE == BLEND_SPLIT ? 7 : (MODE == BLEND_SPLIT_GEO ? 5 : 6)) void render_fwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, FwdOut O)

@@ -267,7 +267,11 @@ def valu_peak(iters=2000, reps=5):
 
 # the blend kernels' VALU probes: gs_diag_math op, kernel name, iterations
 VALU_PROBES = {"render_fwd_kernel": (7, "valu_probe_fwd_kernel", 24),
-               "render_bwd_kernel": (8, "valu_probe_bwd_kernel", 8)}
+               "render_bwd_kernel": (8, "valu_probe_bwd_kernel", 8),
+               # the backward's 16x8 half-tile walk (two pixels per lane), which the kernel takes when the
+               # Gaussians average 24 or more tile instances (R >= 24 L)
+               "render_bwd_kernel_half_tiles": (9, "valu_probe_bwd2_kernel", 8)}
+TWO_PX_MIN_INSTANCES = 24
 
 
 def run_valu_probe(op, iters, reps=5):
@@ -295,7 +299,7 @@ def valu_probes_only():
         log(f"[bench] {pname}: {iters} iterations, {ms:.3f} ms")
 
 
-def valu_of(name, avg_ms, config):
+def valu_of(name, avg_ms, config, probe=None):
     """VALU issue rate of kernel `name` per launch: SQ_INSTS_VALU per launch
     (profiles/valu_config<N>.json, rocprofv3 --pmc) over its live launch time,
     against the ceiling for its instruction mix: the issue rate of its VALU
@@ -309,8 +313,9 @@ def valu_of(name, avg_ms, config):
     achieved = insts / (avg_ms * 1e-3) / 1e9
     out = {"unit": "G wave-instructions/s", "insts_per_launch": int(insts), "achieved": round(achieved, 1),
            "fma_rate": round(valu_peak(), 1)}
-    if name in VALU_PROBES:
-        op, pname, iters = VALU_PROBES[name]
+    probe = probe or name
+    if probe in VALU_PROBES:
+        op, pname, iters = VALU_PROBES[probe]
         try:
             pj = json.load(open(os.path.join(ROOT, "profiles", "valu_probes.json")))[pname]
             assert int(pj["iters"]) == iters
@@ -440,7 +445,10 @@ def run_step(args):
         roofline["note"] = ("`bound` and `frac` are the HBM roofline (algorithmic bytes / launch time) the line format "
                             "asks for; this blend kernel is limited by VALU issue, not HBM: `valu.frac` is its VALU "
                             "instruction rate over that of its own per-entry arithmetic run with no memory traffic")
-        roofline["valu"] = valu_of(dom, avg_launch.get(dom, float("nan")), args.config)
+        # the backward's walk: 16x8 half tiles when R >= 24 L (L: the listed Gaussians, here those with a radius)
+        half = dom == "render_bwd_kernel" and R >= TWO_PX_MIN_INSTANCES * P_vis
+        roofline["valu"] = valu_of(dom, avg_launch.get(dom, float("nan")), args.config,
+                                   "render_bwd_kernel_half_tiles" if half else None)
     else:
         roofline["note"] = "HBM roofline of the kernel (algorithmic bytes / launch time)"
 

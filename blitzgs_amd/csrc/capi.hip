@@ -225,11 +225,12 @@ __global__ __launch_bounds__(256) void diag_valu_kernel(int iters, float a, floa
 extern "C" int gs_diag_math(int op, int n, const float* x, float* y, hipStream_t stream)
 {
     gs::clear_error();
-    GS_REQUIRE(op >= 0 && op <= 8,
+    GS_REQUIRE(op >= 0 && op <= 9,
                "op must be 0 (exp), 1 (log), 2 (exact blend exp), 3 (wave sum of 12 values), 4 (copy), "
-               "5 (VALU rate), 6 (the blend's falloff G), 7 or 8 (forward / backward blend VALU probe)");
+               "5 (VALU rate), 6 (the blend's falloff G), 7, 8 or 9 (forward / backward / half-tile backward "
+               "blend VALU probe)");
     GS_REQUIRE(n >= 0, "n must be >= 0");
-    if (op == 7 || op == 8) return gs::render_valu_probe(op - 7, n, y, stream);
+    if (op >= 7 && op <= 9) return gs::render_valu_probe(op - 7, n, y, stream);
     if (op == 5) {
         GS_REQUIRE(y != nullptr, "op 5 needs y (one float)");
         if (n == 0) return GS_OK;

@@ -3628,6 +3628,33 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
             out += p.C0 + p.C1 + p.C2 + p.T + (float)(p.last + p.n2l);
         }
         out += (float)observed;
+    } else if (WHICH == 2) {
+        // the backward's half-tile walk (bwd_half_tile): two pixels per lane
+        // (here at one position, so that both blend every entry), one
+        // reduction per entry, the atomics replaced by a sum
+        const int my_k = gs::wave_sum12_index(lane);
+        const BwdConst ka{pxf, pyf, 0.3f, -0.2f, 0.1f, -0.05f, 64};
+        const BwdConst kb{pxf, pyf, -0.1f, 0.25f, 0.2f, -0.04f, 64};
+        for (int it = 0; it < iters; it++) {
+            BwdPixel pa{0.2f, 0.f, 0.f, 0.f}, pb{0.25f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 64; j++) {
+                const float4 A = st.a[j], B = st.b[j], Cc = st.c[j];
+                const BwdEval ea = bwd_eval(ka, A, B, Cc);
+                const BwdEval eb = bwd_eval(kb, A, B, Cc);
+                if (gs::ballot(ea.valid || eb.valid) == 0) continue;
+                float va[12], vb[12], v[12];
+                bwd_apply<false>(pa, ka, A, B, Cc, ea, va);
+                bwd_apply<false>(pb, kb, A, B, Cc, eb, vb);
+#pragma unroll
+                for (int q = 0; q < 11; q++) v[q] = va[q] + vb[q];
+                v[2] = __builtin_fabsf(va[2]) + __builtin_fabsf(vb[2]);
+                v[3] = __builtin_fabsf(va[3]) + __builtin_fabsf(vb[3]);
+                v[11] = va[11];
+                const float tot = gs::wave_sum12<true>(v);
+                if (my_k >= 0 && my_k < 11 && tot != 0.f) out += tot;
+            }
+            out += pa.T + pb.T;
+        }
     } else {
         // the backward: render_bwd_kernel's entry loop, the accumulator
         // atomics replaced by a sum
@@ -4540,15 +4567,18 @@ namespace gs {
 // entries per wave, VALU_PROBE_BLOCKS waves.
 int render_valu_probe(int which, int iters, float* y, hipStream_t stream)
 {
-    GS_REQUIRE(which == 0 || which == 1, "which must be 0 (forward) or 1 (backward)");
+    GS_REQUIRE(which >= 0 && which <= 2, "which must be 0 (forward), 1 (backward) or 2 (backward, half tiles)");
     GS_REQUIRE(iters >= 0 && y != nullptr, "iters must be >= 0 and y non-null");
     if (iters == 0) return GS_OK;
     if (which == 0) {
         GS_TIMED("valu_probe_fwd_kernel", stream,
                  hipLaunchKernelGGL(valu_probe_kernel<0>, dim3(VALU_PROBE_BLOCKS), dim3(64), 0, stream, iters, y));
-    } else {
+    } else if (which == 1) {
         GS_TIMED("valu_probe_bwd_kernel", stream,
                  hipLaunchKernelGGL(valu_probe_kernel<1>, dim3(VALU_PROBE_BLOCKS), dim3(64), 0, stream, iters, y));
+    } else {
+        GS_TIMED("valu_probe_bwd2_kernel", stream,
+                 hipLaunchKernelGGL(valu_probe_kernel<2>, dim3(VALU_PROBE_BLOCKS), dim3(64), 0, stream, iters, y));
     }
     GS_LAUNCH_CHECK("valu_probe_kernel");
     return GS_OK;

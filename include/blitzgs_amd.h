@@ -545,10 +545,12 @@ int gs_ply_pack(int64_t P, int32_t n_tensors, const gs_ply_tensor* tensors, cons
  * the known-size kernel that HBM byte counters are calibrated against; op 5
  * runs 8192 blocks of 256 threads, each wave issuing 32 * n fp32 FMAs (x unused,
  * y one float that is never written), the reference for the VALU issue rate;
- * ops 7 and 8 run the forward / backward blend kernels' per-entry arithmetic
- * (the same device functions) n times over 64 entries staged in LDS, in
- * 16384 waves with no global memory traffic (x unused, y one float that is
- * never written): the VALU issue rate of the blend's own instruction mix.
+ * ops 7, 8 and 9 run the forward / backward (8x8 quadrant walk) / backward
+ * (16x8 half-tile walk, two pixels per lane) blend kernels' per-entry
+ * arithmetic (the same device functions) n times over 64 entries staged in
+ * LDS, in 16384 waves with no global memory traffic (x unused, y one float
+ * that is never written): the VALU issue rate of the blend's own instruction
+ * mix.
  * ------------------------------------------------------------------------ */
 int gs_diag_math(int op, int n, const float* x, float* y, gs_stream_t stream);
 

@@ -98,7 +98,7 @@ def test_argument_errors_without_device(lib):
     rc = lib.gs_preprocess_forward(10, 3, 9, *([None] * 5), C.c_float(1.0), None, None, None, C.c_float(1.0),
                                    C.c_float(1.0), 10, 10, *([None] * 7), None)
     assert rc != 0 and b"coefficients" in lib.gs_last_error()
-    rc = lib.gs_diag_math(9, 1, None, None, None)
+    rc = lib.gs_diag_math(10, 1, None, None, None)
     assert rc != 0 and b"op" in lib.gs_last_error()
     # timing modes: 0 off, 1 every kernel and the stages, 2 the stages only
     rc = lib.gs_timing_enable(3)

@@ -48,6 +48,18 @@ def test_device_math_bitexact():
     assert_bitexact(np_(y), O.vec_logf(xl), "log")
 
 
+def test_valu_probes_run_and_write_nothing():
+    """The blend kernels' VALU probes (gs_diag_math ops 7, 8 and 9: forward,
+    quadrant backward, half-tile backward) run, and the float they could
+    write stays untouched (the work is kept alive by a test that never
+    holds)."""
+    y = torch.zeros(1, device="cuda")
+    for op in (7, 8, 9):
+        _lib.check(_lib.load().gs_diag_math(op, 1, None, _lib.ptr(y), None), f"probe op {op}")
+    torch.cuda.synchronize()
+    assert float(y[0]) == 0.0
+
+
 def test_blend_falloff_exp_bound_and_guard():
     """The blend's G (op 6, opacity 1): within 2e-5 relative of exp(x) in
     double over [-87, 0], and bit-equal to the oracle's exact exp for every x

@@ -3258,19 +3258,24 @@ struct GeoBwd {
 // quadrants, which the forward recorded (qwork; the backward walks each
 // quadrant's list from that position to 0).  Waves are dispatched in block
 // order, so the long ones start first and the short ones fill in at the end
-// instead of a long one starting last.  A counting sort on min(work, 4095),
-// descending; ties in any order (the order only changes the schedule).
+// instead of a long one starting last.  The order is by work class (two per
+// octave of the work, heaviest first) and, inside a class, the supertile
+// order, so that the tiles walked at the same time on an XCD are mostly
+// neighbours and share the records they read in its L2: an exact sort on the
+// work scattered them and raised the kernel's HBM reads at config 2 from 0.30
+// to 0.51 GB at the same speed; one class per octave reads 0.21 GB but was 2 %
+// slower.  A stable counting sort: per round of 1024 tiles, each wave ranks its
+// tiles of a class by a ballot, then the waves' counts are scanned in order.
 // (one 1024-thread block per XCD x, inside zero_gacc_kernel)
 __device__ void bwd_schedule_block(unsigned x, unsigned gx, unsigned gy, unsigned sgx, unsigned NS,
                                    const uint32_t* __restrict__ qwork, uint32_t* __restrict__ sched,
                                    uint32_t* __restrict__ scnt)
 {
-    constexpr int NB = 4096;
-    __shared__ uint32_t hist[NB];
-    __shared__ uint32_t s_wave[32];
+    constexpr int NB = 32;   // work classes, two per octave, heaviest first
+    __shared__ uint32_t s_base[NB];
+    __shared__ uint32_t s_wcnt[16][NB];
     const unsigned cap = sched_cap(NS);
-    for (int i = threadIdx.x; i < NB; i += 1024) hist[i] = 0u;
-    __syncthreads();
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     // i-th tile of the XCD in supertile order -> tile index, or -1
     auto tile_of = [&](unsigned i) -> int {
         const unsigned st = (i / (SUPER * SUPER)) * 8u + x, t = i % (SUPER * SUPER);
@@ -3278,33 +3283,57 @@ __device__ void bwd_schedule_block(unsigned x, unsigned gx, unsigned gy, unsigne
         const unsigned tx = (st % sgx) * SUPER + t % SUPER, ty = (st / sgx) * SUPER + t / SUPER;
         return tx < gx && ty < gy ? (int)(ty * gx + tx) : -1;
     };
-    auto bucket_of = [&](int tile) -> int {
+    auto class_of = [&](int tile) -> int {
         const uint4 q = reinterpret_cast<const uint4*>(qwork)[tile];
-        const uint32_t w = max(max(q.x, q.y), max(q.z, q.w));
-        return w == 0u ? -1 : NB - 1 - (int)min(w, (uint32_t)(NB - 1));
+        const uint32_t w = min(max(max(q.x, q.y), max(q.z, q.w)), 0xffffu);
+        if (w == 0u) return -1;
+        const int lg = 31 - __builtin_clz(w);
+        const int c = 2 * lg + (lg > 0 ? (int)((w >> (lg - 1)) & 1u) : 0);
+        return NB - 1 - c;
     };
-    for (unsigned i = threadIdx.x; i < cap; i += 1024) {
-        const int t = tile_of(i);
-        const int b = t >= 0 ? bucket_of(t) : -1;
-        if (b >= 0) atomicAdd(&hist[b], 1u);
-    }
-    __syncthreads();
-    // exclusive scan of the buckets, four per thread
-    uint32_t v[4], sum = 0u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) { v[j] = hist[4 * threadIdx.x + j]; sum += v[j]; }
-    uint32_t tot;
-    uint32_t run = gs::block_excl_scan_1024(sum, s_wave, &tot);
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; j++) { hist[4 * threadIdx.x + j] = run; run += v[j]; }
+    if (threadIdx.x < NB) s_base[threadIdx.x] = 0u;
     __syncthreads();
     for (unsigned i = threadIdx.x; i < cap; i += 1024) {
         const int t = tile_of(i);
-        const int b = t >= 0 ? bucket_of(t) : -1;
-        if (b >= 0) sched[(size_t)x * cap + atomicAdd(&hist[b], 1u)] = (uint32_t)t;
+        const int c = t >= 0 ? class_of(t) : -1;
+        if (c >= 0) atomicAdd(&s_base[c], 1u);
     }
-    if (threadIdx.x == 0) scnt[x] = tot;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0u;
+        for (int c = 0; c < NB; c++) {
+            const uint32_t v = s_base[c];
+            s_base[c] = run;
+            run += v;
+        }
+        scnt[x] = run;
+    }
+    __syncthreads();
+    // in each class, the tiles in supertile order (neighbours stay together)
+    for (unsigned r0 = 0; r0 < cap; r0 += 1024) {
+        const unsigned i = r0 + threadIdx.x;
+        const int t = i < cap ? tile_of(i) : -1;
+        const int cls = t >= 0 ? class_of(t) : -1;
+        uint32_t rank = 0u;
+        for (int c = 0; c < NB; c++) {
+            const uint64_t m = gs::ballot(cls == c);
+            if (cls == c) rank = (uint32_t)gs::rank_below(m);
+            if (lane == 0) s_wcnt[wid][c] = (uint32_t)__builtin_popcountll(m);
+        }
+        __syncthreads();
+        if (cls >= 0) {
+            uint32_t off = s_base[cls];
+            for (int w = 0; w < wid; w++) off += s_wcnt[w][cls];
+            sched[(size_t)x * cap + off + rank] = (uint32_t)t;
+        }
+        __syncthreads();
+        if (threadIdx.x < NB) {
+            uint32_t tot = 0u;
+            for (int w = 0; w < 16; w++) tot += s_wcnt[w][threadIdx.x];
+            s_base[threadIdx.x] += tot;
+        }
+        __syncthreads();
+    }
 }
 
 // The split path's backward over a 16x8 half tile (half 0: pixel rows 0-7,

@@ -46,7 +46,7 @@ _SIGS = {
     "gs_preprocess_forward_rec": (_i, [_i, _i, _i, _c, _c, _c, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
                                        _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward_rec": (_i, [_i, _i, _i, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
-                                        _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _c]),
+                                        _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _i, _c]),
     "gs_render_geom_bytes": (_sz, [_i, _i, _i]),
     "gs_render_binning_bytes": (_sz, [_i64]),
     "gs_render_img_bytes": (_sz, [_i, _i]),
@@ -54,12 +54,14 @@ _SIGS = {
     "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
                                _c, _c]),
     "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _c]),
-    "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c]),
+    "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c,
+                                _i64, _c]),
     "gs_render_geo_forward": (_i, [_i, _i64, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_render_forward_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [_f, _f, _c, _c, _c, _c]),
     "gs_render_forward_reserved_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _f, _f, _c, _c,
                                                                              _c, _c]),
-    "gs_render_backward_geo": (_i, [_i, _i64, _i, _i, _c, _f, _f] + [_c] * 13 + [_i, _c, _c, _c, _c, _c]),
+    "gs_render_backward_geo": (_i, [_i, _i64, _i, _i, _c, _f, _f] + [_c] * 13 + [_i, _c, _c, _c, _c, _c, _i64,
+                                                                               _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
                                     C.POINTER(_c), C.POINTER(_c), C.POINTER(_c)]),
     "gs_render_point_list": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c]),

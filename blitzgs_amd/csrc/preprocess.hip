@@ -704,7 +704,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
     float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
     float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, FullPreBwd F, const float4* __restrict__ rec,
-    const uint64_t* __restrict__ rec_mask)
+    const uint64_t* __restrict__ rec_mask, int zeroed)
 {
     __shared__ float s_sh[STAGED ? 256 * SH_PITCH : 1];
     __shared__ uint8_t s_vis[256];
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         }
         if (FULL) {
             for (int k = 0; k < 6; k++) F.dL_dcov3D[6 * (size_t)idx + k] = 0.f;
-        } else if (!STAGED) {
+        } else if (!STAGED && !zeroed) {
             float* gsh_out = dL_dsh + (size_t)idx * K * 3;
             if (sh_vec16) {
                 float4* o4 = reinterpret_cast<float4*>(gsh_out);
@@ -826,6 +826,8 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
             if (s_vis[r]) {
                 const float* src = s_sh + r * SH_PITCH + col;
                 v = make_float4(src[0], src[1], src[2], src[3]);
+            } else if (zeroed) {
+                continue;   // (the row already holds zeros)
             }
             gs::st_stream(&dst[c], v);
         }
@@ -912,7 +914,7 @@ static int preprocess_backward_impl(
     const int* radii, const float* cov3D, const uint8_t* clamped, const float* dL_dmeans2D,
     int dL_dmeans2D_stride, const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
     float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, const void* bwd_records,
-    hipStream_t stream)
+    hipStream_t stream, int zeroed = 0)
 {
     gs::clear_error();
     GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
@@ -940,7 +942,7 @@ static int preprocess_backward_impl(
                                 viewmatrix, projmatrix, campos, means3D, scales, rotations, sh, sh_vec16, \
                                 radii, cov3D, clamped, dL_dmeans2D, dL_dmeans2D_stride,                   \
                                 dL_dconic_opacity, dL_drgb, dL_dmeans3D, dL_dscales, dL_drotations,       \
-                                dL_dsh, dL_dopacity, FullPreBwd{}, rrec, rmask))
+                                dL_dsh, dL_dopacity, FullPreBwd{}, rrec, rmask, zeroed))
 #define GS_PRE_BWD(DEG)                                                                                  \
     if (rrec != nullptr) {                                                                               \
         if (staged) GS_PRE_BWD_K(DEG, true, true); else GS_PRE_BWD_K(DEG, false, true);                  \
@@ -978,14 +980,15 @@ extern "C" int gs_preprocess_backward_rec(
     const float* viewmatrix, const float* projmatrix, const float* campos, float tanfovx, float tanfovy,
     int image_height, int image_width, const float* cov3D, const float* dL_dmeans2D, int dL_dmeans2D_stride,
     const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D, float* dL_dscales,
-    float* dL_drotations, float* dL_dsh, float* dL_dopacity, hipStream_t stream)
+    float* dL_drotations, float* dL_dsh, float* dL_dopacity, int outputs_zeroed, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(P <= 0 || bwd_records != nullptr, "bwd_records must be the records gs_preprocess_forward_rec wrote");
     return preprocess_backward_impl(P, D, K, nullptr, nullptr, nullptr, sh, scale_modifier, viewmatrix, projmatrix,
                                     campos, tanfovx, tanfovy, image_height, image_width, nullptr, cov3D, nullptr,
                                     dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,
-                                    dL_dscales, dL_drotations, dL_dsh, dL_dopacity, bwd_records, stream);
+                                    dL_dscales, dL_drotations, dL_dsh, dL_dopacity, bwd_records, stream,
+                                    outputs_zeroed != 0 ? 1 : 0);
 }
 
 extern "C" int gs_preprocess_forward_full(
@@ -1070,14 +1073,14 @@ extern "C" int gs_preprocess_backward_full(
                                     image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
                                     viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
                                     cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
-                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr));                         \
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr, 0));                         \
     else                                                                                                         \
         GS_TIMED("preprocess_bwd_full_kernel", stream,                                                           \
                  hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, false, true>), grid, block, 0, stream, P, 0,       \
                                     image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,          \
                                     viewmatrix, projmatrix, campos, means3D, scales, rotations, nullptr, 0, radii, \
                                     cov3D, clamped, dL_dmeans2D, 3, dL_dconic_opacity, dL_dcolors, dL_dmeans3D,    \
-                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr))
+                                    dL_dscales, dL_drotations, nullptr, dL_dopacity, F, nullptr, nullptr, 0))
     switch (D) {
         case 0: GS_PRE_BWD_FULL(0); break;
         case 1: GS_PRE_BWD_FULL(1); break;

@@ -3454,15 +3454,15 @@ __device__ __forceinline__ void bwd_half_tile(int W, int H, unsigned gx, unsigne
 // instead of quadrants when the scene's Gaussians are wide (two_px_lanes,
 // from the forward's counts in meta; block-uniform).  Occupancy: six waves
 // per SIMD (80 VGPRs) except with render_geo's map terms.
-template <bool FULL, bool GEO = false>
-__global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
+template <bool FULL, bool GEO>
+__device__ __forceinline__ void render_bwd_body(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
-    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G,
-    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt, const uint32_t* __restrict__ meta)
+    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, const GeoBwd& G,
+    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt, const uint32_t* __restrict__ meta,
+    Stage& st)
 {
-    __shared__ Stage st;
     unsigned tile, quad, tx, ty;
     if (sched != nullptr) {
         // bwd_schedule_kernel's order: XCD b % 8 takes its tiles heaviest first,
@@ -3604,6 +3604,48 @@ __global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
         id_cur = id_nxt;
         id_nxt = id_nn;
     }
+}
+
+// A caller's buffer that the backward clears while it runs (clear16: 16-byte
+// words; none when 0): each block, after its walk, writes zeros over its
+// share with streaming stores.  The blend is VALU-bound and leaves HBM
+// bandwidth unused, so the clearing costs it little; the buffer is an output
+// of a later kernel that then writes only its non-zero rows (the preprocess
+// backward's dL/dsh).  The stores come after the walk: on this target vmcnt
+// also counts stores, so stores issued first would hold up the walk's loads.
+struct ClearBuf {
+    float4* p;
+    size_t n16;
+};
+
+__device__ __forceinline__ void clear_share(const ClearBuf& c)
+{
+    if (c.n16 == 0) return;
+    const size_t share = (c.n16 + gridDim.x - 1) / gridDim.x;
+    const size_t b0 = (size_t)blockIdx.x * share, b1 = min(c.n16, b0 + share);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (size_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) gs::st_stream(&c.p[i], z);
+}
+
+template <bool FULL, bool GEO = false>
+__global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
+    int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
+    const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
+    const float* __restrict__ bg, const float* __restrict__ final_T, const uint32_t* __restrict__ n_contrib_px,
+    const float* __restrict__ dL_dpixels, float* __restrict__ gacc, GeoBwd G,
+    const uint32_t* __restrict__ sched, const uint32_t* __restrict__ scnt, const uint32_t* __restrict__ meta,
+    ClearBuf clr)
+{
+    __shared__ Stage st;
+    render_bwd_body<FULL, GEO>(W, H, gx, gy, sgx, NS, ranges, clist, rec, cl, bg, final_T, n_contrib_px, dL_dpixels,
+                               gacc, G, sched, scnt, meta, st);
+    clear_share(clr);
+}
+
+// the clearing when no backward kernel runs (no instances)
+__global__ __launch_bounds__(256) void clear_kernel(ClearBuf clr)
+{
+    clear_share(clr);
 }
 
 // ---- VALU probes: the blend kernels' per-entry arithmetic (fwd_blend_step;
@@ -4176,7 +4218,8 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                          const float* conic_opacity, const uint8_t* compute_locally, void* geom, const void* binning,
                          const void* img, const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
                          float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream,
-                         const GeoBwd* geo = nullptr, float* dL_dall_map = nullptr)
+                         const GeoBwd* geo = nullptr, float* dL_dall_map = nullptr, void* clear_dst = nullptr,
+                         int64_t clear_bytes = 0)
 {
     GS_REQUIRE(geo == nullptr || (!full && dL_dall_map != nullptr), "render_geo: split path, dL_dall_map non-null");
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
@@ -4185,7 +4228,19 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                ((uintptr_t)means2D & 7) == 0,
                "conic_opacity / dL_dconic_opacity must be 16-byte and means2D 8-byte aligned");
     GS_REQUIRE(geom != nullptr, "geom must be the forward's geometry workspace");
-    if (P == 0) return GS_OK;
+    GS_REQUIRE(clear_bytes >= 0 && (clear_bytes & 15) == 0 && ((uintptr_t)clear_dst & 15) == 0 &&
+                   (clear_bytes == 0 || clear_dst != nullptr),
+               "clear_dst and clear_bytes must be 16-byte aligned (clear_bytes=%lld)", (long long)clear_bytes);
+    const ClearBuf clr{static_cast<float4*>(clear_dst), (size_t)clear_bytes / 16};
+    if (P == 0) {
+        if (clr.n16 != 0) {
+            GS_TIMED("clear_kernel", stream,
+                     hipLaunchKernelGGL(clear_kernel, dim3((unsigned)std::min<size_t>(gs_div_up(clr.n16, 256), 4096)),
+                                        dim3(256), 0, stream, clr));
+            GS_LAUNCH_CHECK("clear_kernel");
+        }
+        return GS_OK;
+    }
     const GeomLayout g = geom_layout(P, W, H);
     const ImgLayout il = img_layout(W, H);
     const BinLayout bl = bin_layout(R);
@@ -4215,21 +4270,26 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                      hipLaunchKernelGGL(render_bwd_kernel<true>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}, nullptr, nullptr, nullptr));
+                                        GeoBwd{}, nullptr, nullptr, nullptr, ClearBuf{nullptr, 0}));
         } else if (geo != nullptr) {
             GS_TIMED("render_bwd_geo_kernel", stream,
                      hipLaunchKernelGGL((render_bwd_kernel<false, true>), dim3(nblk), dim3(64), 0, stream, W, H, gx,
                                         gy, sgx, NS, rng, clist, recs, compute_locally, bg,
                                         at<float>(img, il.final_T), at<uint32_t>(img, il.n_contrib), dL_dpixels,
-                                        reinterpret_cast<float*>(gacc), *geo, sched, scnt, nullptr));
+                                        reinterpret_cast<float*>(gacc), *geo, sched, scnt, nullptr, clr));
         } else {
             GS_TIMED("render_bwd_kernel", stream,
                      hipLaunchKernelGGL(render_bwd_kernel<false>, dim3(nblk), dim3(64), 0, stream, W, H, gx, gy, sgx,
                                         NS, rng, clist, recs, compute_locally, bg, at<float>(img, il.final_T),
                                         at<uint32_t>(img, il.n_contrib), dL_dpixels, reinterpret_cast<float*>(gacc),
-                                        GeoBwd{}, sched, scnt, at<const uint32_t>(geom, g.meta)));
+                                        GeoBwd{}, sched, scnt, at<const uint32_t>(geom, g.meta), clr));
         }
         GS_LAUNCH_CHECK("render_bwd_kernel");
+    } else if (clr.n16 != 0) {
+        GS_TIMED("clear_kernel", stream,
+                 hipLaunchKernelGGL(clear_kernel, dim3((unsigned)std::min<size_t>(gs_div_up(clr.n16, 256), 4096)),
+                                    dim3(256), 0, stream, clr));
+        GS_LAUNCH_CHECK("clear_kernel");
     }
     // without instances the forward wrote no flags: every output is zero
     GS_TIMED("unpack_grads_kernel", stream,
@@ -4462,14 +4522,15 @@ extern "C" int gs_render_backward(int P, int64_t R, int W, int H, const float* b
                                   const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
                                   void* geom, const void* binning, const void* img, const float* dL_dpixels,
                                   float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
-                                  float* dL_dconic_opacity, float* dL_dcolors, hipStream_t stream)
+                                  float* dL_dconic_opacity, float* dL_dcolors, void* clear_dst, int64_t clear_bytes,
+                                  hipStream_t stream)
 {
     gs::clear_error();
     (void)rgb;
     GS_REQUIRE(dL_dmeans2D_abs != nullptr, "dL_dmeans2D_abs must be non-null");
     return render_backward_impl(false, P, R, W, H, bg, means2D, conic_opacity, compute_locally, geom, binning, img,
                                 dL_dpixels, dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity,
-                                dL_dcolors, stream);
+                                dL_dcolors, stream, nullptr, nullptr, clear_dst, clear_bytes);
 }
 
 extern "C" int gs_render_geo_forward(int P, int64_t R, int W, int H, float tan_fovx, float tan_fovy,
@@ -4489,7 +4550,7 @@ extern "C" int gs_render_backward_geo(int P, int64_t R, int W, int H, const floa
                                       const void* img, const float* dL_dpixels, const float* dL_dout_all_map,
                                       const float* dL_dout_plane_depth, float* dL_dmeans2D, int dL_dmeans2D_stride,
                                       float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
-                                      float* dL_dall_map, hipStream_t stream)
+                                      float* dL_dall_map, void* clear_dst, int64_t clear_bytes, hipStream_t stream)
 {
     gs::clear_error();
     (void)rgb;
@@ -4503,7 +4564,7 @@ extern "C" int gs_render_backward_geo(int P, int64_t R, int W, int H, const floa
                      (float)H / (2.0f * tan_fovy)};
     return render_backward_impl(false, P, R, W, H, bg, means2D, conic_opacity, compute_locally, geom, binning, img,
                                 dL_dpixels, dL_dmeans2D, dL_dmeans2D_stride, dL_dmeans2D_abs, dL_dconic_opacity,
-                                dL_dcolors, stream, &geo, dL_dall_map);
+                                dL_dcolors, stream, &geo, dL_dall_map, clear_dst, clear_bytes);
 }
 
 extern "C" int gs_render_full_count(int P, int W, int H, const float* means2D, const int* radii, const float* rects,

@@ -14,7 +14,13 @@ gfx950) through its C ABI.  Differences that do not change results:
     [:, :2] slice after the render backward are not materialised: the C ABI
     takes a row stride;
   * dL/dall_map (all zeros when render_geo is off) is returned only when the
-    all_map input requires a gradient.
+    all_map input requires a gradient;
+  * the preprocess backward's dL/dsh (zero for the invisible Gaussians; the
+    reference allocates it with torch::zeros) is allocated by the preprocess
+    forward and cleared by the render backward of a render that read this
+    call's means2D, while its VALU-bound blend runs (gs_render_backward's
+    clear_dst); the preprocess backward then writes only the visible
+    Gaussians' rows.
 """
 import ctypes as C
 from typing import NamedTuple
@@ -129,9 +135,12 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_
 
 
 def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
-                             dL_dconic_opacity, dL_drgb, records=None):
+                             dL_dconic_opacity, dL_drgb, records=None, zeroed=None):
     """records: the forward's record buffer (_preprocess_forward_raw with
-    records=True); then radii, clamped, scales and rotations are not read."""
+    records=True); then radii, clamped, scales and rotations are not read.
+    zeroed (with records): a (P,K,3) dL/dsh output tensor that already holds
+    zeros on the current stream; only the visible Gaussians' rows are written
+    into it."""
     dev = means3D.device
     P = means3D.size(0)
     K = sh.size(1) if sh.ndimension() == 3 else 1
@@ -139,7 +148,12 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
     dL_dmeans3D = torch.empty((P, 3), **f32)
     dL_dscales = torch.empty((P, 3), **f32)
     dL_drotations = torch.empty((P, 4), **f32)
-    dL_dsh = torch.empty((P, K, 3), **f32)
+    if zeroed is not None:
+        if records is None or tuple(zeroed.shape) != (P, K, 3):
+            raise RuntimeError(f"a zeroed dL/dsh needs the record path and shape ({P}, {K}, 3)")
+        dL_dsh = zeroed
+    else:
+        dL_dsh = torch.empty((P, K, 3), **f32)
     dL_dopacity = torch.empty((P, 1), **f32)
     if P != 0:
         means3D = _dev_f32(means3D, dev)
@@ -161,7 +175,8 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
                 P, int(rs.sh_degree), K, ptr(records), ptr(sh), float(rs.scale_modifier), ptr(view), ptr(proj),
                 ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height), int(rs.image_width), cov,
                 ptr(dL_dmeans2D), dL_dmeans2D.size(1), ptr(dL_dconic_opacity), ptr(dL_drgb), ptr(dL_dmeans3D),
-                ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), _stream(dev))
+                ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity), 1 if zeroed is not None else 0,
+                _stream(dev))
             check(rc, "gs_preprocess_backward_rec")
         else:
             rc = lib.gs_preprocess_backward(
@@ -175,6 +190,39 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
     return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity
 
 
+class _ZeroedGrads:
+    """The preprocess backward's dL/dsh, allocated by its forward.  The first
+    render backward of a render that read that call's means2D claims it and
+    clears it while it runs (claim(), then cleared() with an event after the
+    call); take() hands it to the preprocess backward, which waits for that
+    event, or gives None when no render backward cleared it (the preprocess
+    backward then writes every row itself).  Once taken it cannot be claimed
+    again, so a later render backward never clears a returned gradient."""
+
+    def __init__(self, P, K, dev):
+        self.dev = dev
+        self.dL_dsh = torch.empty((P, K, 3), device=dev, dtype=torch.float32)
+        self.event = None
+        self.claimed = False
+
+    def claim(self):
+        if self.claimed or self.dL_dsh is None:
+            return None
+        self.claimed = True
+        return self.dL_dsh
+
+    def cleared(self):
+        self.event = torch.cuda.Event()
+        self.event.record(torch.cuda.current_stream(self.dev))
+
+    def take(self):
+        t, self.dL_dsh = self.dL_dsh, None
+        if t is None or self.event is None:
+            return None
+        torch.cuda.current_stream(self.dev).wait_event(self.event)
+        return t
+
+
 class _PreprocessGaussians(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means3D, scales, rotations, sh, opacities, raster_settings, cuda_args):
@@ -183,6 +231,12 @@ class _PreprocessGaussians(torch.autograd.Function):
         num_rendered, means2D, depths, radii, cov3D, conic_opacity, rgb, clamped, records = _preprocess_forward_raw(
             means3D, scales, rotations, sh, opacities, raster_settings, keep_cov3D=False, records=True,
             keep_clamped=False)
+        # the backward's outputs, cleared on a side stream while the render runs
+        ctx.zeroed = None
+        P = means2D.size(0)
+        if P != 0 and ctx.needs_input_grad[3] and sh.size(1) * 12 % 16 == 0:
+            ctx.zeroed = _ZeroedGrads(P, sh.size(1), means2D.device)
+            means2D._gs_zeroed = ctx.zeroed
         # radii and depths take no gradient; unused outputs are not zero-filled
         ctx.set_materialize_grads(False)
         ctx.raster_settings = raster_settings
@@ -204,9 +258,10 @@ class _PreprocessGaussians(torch.autograd.Function):
             grad_rgb = torch.zeros_like(rgb)
         if grad_conic_opacity is None:
             grad_conic_opacity = torch.zeros_like(conic_opacity)
+        zeroed = ctx.zeroed.take() if ctx.zeroed is not None else None
         dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity = _preprocess_backward_raw(
             radii, cov3D, clamped, means3D, scales, rotations, sh, rs, grad_means2D, grad_conic_opacity, grad_rgb,
-            records=records)
+            records=records, zeroed=zeroed)
         return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity, None, None
 
 
@@ -332,10 +387,11 @@ def _render_geo_forward_raw(P, H, W, tanfovx, tanfovy, all_maps, compute_locally
 
 
 def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img, dL_dpixels,
-                         m2d_stride=2, timing=False, debug=False, geo=None):
+                         m2d_stride=2, timing=False, debug=False, geo=None, clear=None):
     """geo (render_geo): (tanfovx, tanfovy, all_map_pixels, all_maps,
     dL_dout_all_map, dL_dout_plane_depth); dL/dall_map (P,5) is then returned
-    after the timing, else None."""
+    after the timing, else None.  clear: a float32 tensor (16-byte multiple)
+    that the call fills with zeros while its blend runs."""
     dev = means2D.device
     P = means2D.size(0)
     lib = _lib.load()
@@ -354,11 +410,12 @@ def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_local
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
     dL_dall_map = None
+    clr = (ptr(clear), clear.numel() * 4) if clear is not None else (None, 0)
     if geo is None:
         check(lib.gs_render_backward(P, R, W, H, ptr(bg), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
                                      ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dL_dmeans2D),
                                      m2d_stride, ptr(dL_dmeans2D_abs), ptr(dL_dconic_opacity), ptr(dL_dcolors),
-                                     _stream(dev)), "gs_render_backward")
+                                     *clr, _stream(dev)), "gs_render_backward")
     else:
         tanfovx, tanfovy, map_px, all_maps, dmaps, dplane = geo
         if all_maps is None or tuple(all_maps.shape) != (P, 5):
@@ -375,7 +432,8 @@ def _render_backward_raw(bg, R, H, W, means2D, conic_opacity, rgb, compute_local
                                          ptr(all_maps), ptr(means2D), ptr(conic_opacity), ptr(rgb), ptr(cl),
                                          ptr(geom), ptr(binning), ptr(img), ptr(dL_dpixels), ptr(dmaps),
                                          ptr(dplane), ptr(dL_dmeans2D), m2d_stride, ptr(dL_dmeans2D_abs),
-                                         ptr(dL_dconic_opacity), ptr(dL_dcolors), ptr(dL_dall_map), _stream(dev)),
+                                         ptr(dL_dconic_opacity), ptr(dL_dcolors), ptr(dL_dall_map), *clr,
+                                         _stream(dev)),
               "gs_render_backward_geo")
     _lib.debug_sync(debug, "gs_render_backward")
     ms = None
@@ -408,6 +466,9 @@ class _RenderGaussians(torch.autograd.Function):
         geo = (rs.tanfovx, rs.tanfovy, all_maps) if render_geo else None
         res = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing,
                                   bool(rs.debug), geo=geo)
+        # the preprocess backward's dL/dsh, which this render's backward clears
+        zg = getattr(means2D, "_gs_zeroed", None)
+        ctx.zeroed = zg if isinstance(zg, _ZeroedGrads) else None
         R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms = res[:10]
         if timing:
             cuda_args["stats_collector"]["forward_render_time"] = ms
@@ -436,18 +497,24 @@ class _RenderGaussians(torch.autograd.Function):
             grad_color = torch.zeros((3, H, W), device=means2D.device, dtype=torch.float32)
         timing = _want_timing(ctx.cuda_args)
         dL_dall_map = None
+        # the preprocess backward's dL/dsh, cleared by this call while it runs
+        zg = getattr(ctx, "zeroed", None)
+        clear = zg.claim() if zg is not None else None
         if getattr(rs, "render_geo", False):
             (dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms,
              dL_dall_map) = _render_backward_raw(
                 rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
                 grad_color.contiguous(), 2, timing, bool(rs.debug),
-                geo=(rs.tanfovx, rs.tanfovy, all_map_pixels, all_maps, grad_out_all_map, grad_out_plane_depth))
+                geo=(rs.tanfovx, rs.tanfovy, all_map_pixels, all_maps, grad_out_all_map, grad_out_plane_depth),
+                clear=clear)
         else:
             dL_dmeans2D, dL_dmeans2D_abs, dL_dconic_opacity, dL_dcolors, ms = _render_backward_raw(
                 rs.bg, ctx.num_rendered, H, W, means2D, conic_opacity, rgb, compute_locally, geom, binning, img,
-                grad_color.contiguous(), 2, timing, bool(rs.debug))
+                grad_color.contiguous(), 2, timing, bool(rs.debug), clear=clear)
             if ctx.needs_input_grad[4]:
                 dL_dall_map = torch.zeros_like(all_maps)
+        if clear is not None:
+            zg.cleared()
         if timing:
             ctx.cuda_args["stats_collector"]["backward_render_time"] = ms
         if not ctx.needs_input_grad[4]:

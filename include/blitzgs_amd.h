@@ -99,7 +99,12 @@ int gs_preprocess_backward(int P, int D, int K, const float* means3D, const floa
  *   written by gs_preprocess_forward_rec and read by gs_preprocess_backward_rec
  *   of the same P (records naming a Gaussian outside their own group of 64
  *   are skipped).  clamped may be NULL here (not written: the records hold
- *   the flags). */
+ *   the flags).
+ *   outputs_zeroed (backward): nonzero when dL_dsh already holds zeros (the
+ *   render backward cleared it while it ran: gs_render_backward's clear_dst):
+ *   only the visible Gaussians' dL_dsh rows are written then (every other
+ *   output is written whole either way; the reference allocates them all
+ *   with torch::zeros, rasterize_points.cu:960-966). */
 int64_t gs_preprocess_record_bytes(int P);
 int gs_preprocess_forward_rec(int P, int D, int K, const float* means3D, const float* scales,
                               const float* rotations, const float* sh, const float* opacities,
@@ -115,7 +120,7 @@ int gs_preprocess_backward_rec(int P, int D, int K, const void* bwd_records, con
                                int dL_dmeans2D_stride, const float* dL_dconic_opacity,
                                const float* dL_drgb, float* dL_dmeans3D, float* dL_dscales,
                                float* dL_drotations, float* dL_dsh, float* dL_dopacity,
-                               gs_stream_t stream);
+                               int outputs_zeroed, gs_stream_t stream);
 
 /* ------------------------------------------------------------------------ *
  * Render forward, in two calls because the size of the instance buffers
@@ -189,13 +194,20 @@ int gs_render_forward_reserved(int P, int64_t capacity, int image_width, int ima
  *   (the kernels read the forward's packed copy of them in geom).
  *   dL_dpixels (3,H,W).  Outputs: dL_dmeans2D (row stride dL_dmeans2D_stride,
  *   2 or 3; the third column, when present, is zero), dL_dmeans2D_abs (P,3),
- *   dL_dconic_opacity (P,4) = [c00, c01, c11, opacity], dL_dcolors (P,3). */
+ *   dL_dconic_opacity (P,4) = [c00, c01, c11, opacity], dL_dcolors (P,3).
+ *   clear_dst / clear_bytes: NULL / 0, or a caller buffer (16-byte aligned,
+ *   clear_bytes a multiple of 16) that the call fills with zeros while its
+ *   blend runs -- the blend is VALU-bound and leaves HBM bandwidth unused --
+ *   e.g. the preprocess backward's dL_dsh, which that call then writes only
+ *   at the visible rows (gs_preprocess_backward_rec's outputs_zeroed).  No
+ *   counterpart in the reference (it allocates that output with
+ *   torch::zeros before its preprocess backward). */
 int gs_render_backward(int P, int64_t R, int image_width, int image_height, const float* bg,
                        const float* means2D, const float* conic_opacity, const float* rgb,
                        const uint8_t* compute_locally, void* geom, const void* binning, const void* img,
                        const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
                        float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
-                       gs_stream_t stream);
+                       void* clear_dst, int64_t clear_bytes, gs_stream_t stream);
 
 /* render_geo of the render forward (rasterize_points.cu:273-361 with
  * render_geo = true; kernel cuda_rasterizer/forward.cu:381-384,407-412):
@@ -250,7 +262,7 @@ int gs_render_backward_geo(int P, int64_t R, int image_width, int image_height, 
                            const float* dL_dout_all_map, const float* dL_dout_plane_depth,
                            float* dL_dmeans2D, int dL_dmeans2D_stride, float* dL_dmeans2D_abs,
                            float* dL_dconic_opacity, float* dL_dcolors, float* dL_dall_map,
-                           gs_stream_t stream);
+                           void* clear_dst, int64_t clear_bytes, gs_stream_t stream);
 
 /* Views into the opaque buffers, for tests and tools:
  *   binning: point_list uint32 (R), point_list_keys uint64 (R) -- written by

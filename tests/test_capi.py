@@ -145,7 +145,7 @@ def test_render_geo_argument_errors_without_device(lib):
     assert rc != 0 and b"workspaces" in lib.gs_last_error()
     # backward: every map input is required, and dL_dall_map
     args = [10, 5, 64, 64, nz, C.c_float(0.5), C.c_float(0.5), nz, nz, nz, nz, nz, None, nz, nz, nz, nz, nz, nz,
-            nz, 3, nz, nz, nz, nz, None]
+            nz, 3, nz, nz, nz, nz, None, 0, None]
     bad = list(args)
     bad[24] = None      # dL_dall_map
     assert lib.gs_render_backward_geo(*bad) != 0 and b"dL_dall_map" in lib.gs_last_error()

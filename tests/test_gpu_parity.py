@@ -396,8 +396,78 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
                                      junk["scales"], junk["rotations"], t["sh"], rs, dm2, dco, drgb, records=b[8])
     for x, y, name in zip(ref, got, ["means3D", "scales", "rotations", "sh", "opacity"]):
         assert torch.equal(x, y), name
+    # outputs cleared beforehand (the autograd pair clears them on a side
+    # stream while the render runs): only the visible rows are written
+    zeroed = torch.zeros_like(ref[3])
+    got_z = R._preprocess_backward_raw(torch.zeros_like(radii_t), cov3D, torch.ones_like(clamped), junk["means3D"],
+                                       junk["scales"], junk["rotations"], t["sh"], rs, dm2, dco, drgb, records=b[8],
+                                       zeroed=zeroed)
+    for x, y, name in zip(ref, got_z, ["means3D", "scales", "rotations", "sh", "opacity"]):
+        assert torch.equal(x, y), ("zeroed", name)
+    assert got_z[3] is zeroed
     with pytest.raises(RuntimeError, match="record buffer"):
         R._preprocess_backward_raw(radii_t, cov3D, clamped, *args, records=b[8][:-256])
+
+
+def test_autograd_clears_preprocess_grads_beside_the_render(monkeypatch):
+    """The render backward clears the preprocess backward's dL/dsh while its
+    blend runs, and the preprocess backward writes only the visible rows into
+    it; without a render in between the preprocess backward writes every row.
+    Gradients equal those of a run without the clearing (float atomics in the
+    render backward: within 1e-6), and the clearing happens once: a second render backward (retain_graph) leaves the returned
+    gradient alone."""
+    from blitzgs_amd import rasterizer as R
+    scene, cam = synth.small_scene(3000, seed=14, W=200, H=150, extent=1.5)
+    rs = settings_for(cam)
+    seen = []
+    real = R._preprocess_backward_raw
+
+    def spy(*a, **kw):
+        seen.append(kw.get("zeroed") is not None)
+        return real(*a, **kw)
+
+    monkeypatch.setattr(R, "_preprocess_backward_raw", spy)
+
+    def grads(render=True):
+        params = {k: to_dev(np.asarray(scene[k], np.float32)).requires_grad_(True)
+                  for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+        ras = R.GaussianRasterizer(rs)
+        args = {"avoid_pixel_all2all": False}
+        means2D, rgb, conic, radii, depths = ras.preprocess_gaussians(
+            params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], args)
+        if render:
+            P = means2D.shape[0]
+            color, *_ = ras.render_gaussians(means2D, torch.zeros((P, 3), device="cuda", requires_grad=True), conic,
+                                             rgb, torch.zeros((P, 5), device="cuda"), depths, radii, None, None, args)
+            torch.autograd.backward([color], [to_dev(scene["dL_dimage"])])
+        else:
+            torch.autograd.backward([means2D, rgb], [torch.ones_like(means2D), torch.ones_like(rgb)])
+        return [params[k].grad for k in ["means3D", "scales", "rotations", "sh", "opacities"]]
+
+    a = grads()
+    monkeypatch.setattr(R._ZeroedGrads, "claim", lambda self: None)
+    b = grads()
+    assert seen == [True, False]
+    for x, y in zip(a, b):
+        assert rel_l2(np_(x), np_(y)) < 1e-6
+    monkeypatch.undo()
+    c = grads(render=False)
+    assert np.isfinite(np_(c[3])).all()
+    # the render backward twice: the second does not clear the returned dL/dsh
+    params = {k: to_dev(np.asarray(scene[k], np.float32)).requires_grad_(True)
+              for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+    ras = R.GaussianRasterizer(rs)
+    args = {"avoid_pixel_all2all": False}
+    means2D, rgb, conic, radii, depths = ras.preprocess_gaussians(
+        params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], args)
+    P = means2D.shape[0]
+    color, *_ = ras.render_gaussians(means2D, torch.zeros((P, 3), device="cuda", requires_grad=True), conic, rgb,
+                                     torch.zeros((P, 5), device="cuda"), depths, radii, None, None, args)
+    dL = to_dev(scene["dL_dimage"])
+    torch.autograd.backward([color], [dL], retain_graph=True)
+    g1 = params["sh"].grad.clone()
+    torch.autograd.backward([color], [dL])
+    assert rel_l2(np_(params["sh"].grad), 2.0 * np_(g1)) < 1e-6
 
 
 @pytest.mark.parametrize("cfg", ["small", "config0", "wide"])

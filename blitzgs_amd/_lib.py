@@ -50,16 +50,16 @@ _SIGS = {
     "gs_render_geom_bytes": (_sz, [_i, _i, _i]),
     "gs_render_binning_bytes": (_sz, [_i64]),
     "gs_render_img_bytes": (_sz, [_i, _i]),
-    "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _c]),
+    "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _i, _c]),
     "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
-                               _c, _c]),
-    "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _c]),
+                               _c, _i, _c]),
+    "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _i, _c]),
     "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c,
                                 _i64, _c]),
     "gs_render_geo_forward": (_i, [_i, _i64, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),
-    "gs_render_forward_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [_f, _f, _c, _c, _c, _c]),
+    "gs_render_forward_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [_f, _f, _c, _c, _c, _i, _c]),
     "gs_render_forward_reserved_geo": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _f, _f, _c, _c,
-                                                                             _c, _c]),
+                                                                             _c, _i, _c]),
     "gs_render_backward_geo": (_i, [_i, _i64, _i, _i, _c, _f, _f] + [_c] * 13 + [_i, _c, _c, _c, _c, _c, _i64,
                                                                                _c]),
     "gs_render_buffer_views": (_i, [_i64, _i, _i, _c, _c, C.POINTER(_c), C.POINTER(_c), C.POINTER(_c),
@@ -194,16 +194,30 @@ class InstanceReserve:
 
     def __init__(self):
         self._est = {}
+        self._per_gaussian = {}
 
     def capacity(self, dev):
         e = self._est.get(dev)
         return None if e is None else min(int(e * self.HEADROOM) + self.MIN_CAPACITY, 2 ** 32 - 1)
 
-    def update(self, dev, R):
+    def update(self, dev, R, P=None):
         self._est[dev] = max(int(R), int(self._est.get(dev, 0) * self.DECAY))
+        if P:
+            self._per_gaussian[dev] = R / P
+
+    # Region side of the split path's binning: 4x4-tile regions when the last
+    # forward on the device had this many or more tile instances per Gaussian
+    # (large Gaussians: fewer region entries, lists still short enough to
+    # sort on chip), else the default.  The choice never changes a result.
+    REGION4_MIN_INSTANCES = 12.0
+
+    def region_side(self, dev):
+        r = self._per_gaussian.get(dev)
+        return 4 if r is not None and r >= self.REGION4_MIN_INSTANCES else 0
 
     def reset(self):
         self._est.clear()
+        self._per_gaussian.clear()
 
 
 RESERVE = InstanceReserve()

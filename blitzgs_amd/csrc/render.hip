@@ -3764,7 +3764,17 @@ size_t scatter_regions_lds_bytes(const GeomLayout& g)
     return sizeof(float4) * 256 * WAVES_PER_BIN +
            sizeof(uint32_t) * ((size_t)WAVES_PER_BIN * EXPAND_WORDS + (size_t)(g.NR < LDS_REGIONS ? g.NR : LDS_REGIONS));
 }
-unsigned region_lrs(const GeomLayout& g) { return g.RS == 8 ? 3u : g.RS == 4 ? 2u : 1u; }
+// log2 of the region side: the caller's side (0: the smallest the grid
+// allows, g.RS), never below g.RS -- the layout's region arrays are sized for
+// g.RS, so any larger side fits them.  The results do not depend on it; the
+// cost does: larger regions give fewer, longer lists to sort, which pays when
+// each Gaussian covers many tiles.
+unsigned region_lrs(const GeomLayout& g, int side)
+{
+    const int rs = std::max(g.RS, side);
+    return rs >= 8 ? 3u : rs == 4 ? 2u : 1u;
+}
+
 size_t scatter_lds_bytes(int T) { return sizeof(float4) * 256 * WAVES_PER_BIN + count_lds_bytes(T); }
 
 // grid of the blend kernels: whole supertiles per XCD
@@ -3912,7 +3922,8 @@ void readback_release(Readback* r)
 // queued, and cap is the caller's instance capacity (see tilescan_kernel).
 int render_count_impl(bool full, int P, int W, int H, const float* means2D, const int* radii,
                       const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
-                      int64_t* num_rendered, hipStream_t stream, uint64_t cap = ~0ull, Readback* rb = nullptr)
+                      int64_t* num_rendered, hipStream_t stream, uint64_t cap = ~0ull, Readback* rb = nullptr,
+                      int region_side = 0)
 {
     GS_REQUIRE(P >= 0 && W > 0 && H > 0, "invalid sizes P=%d W=%d H=%d", P, W, H);
     GS_REQUIRE(geom != nullptr && (num_rendered != nullptr || rb != nullptr), "geom and num_rendered must be non-null");
@@ -3938,7 +3949,9 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     // buckets (count / tilescan / scatter / tilesort)
     const bool split = !full;
     GS_REQUIRE(!split || g.RS > 0, "a %ux%u tile grid has more than %d regions of 8x8 tiles", gx, gy, MAX_REGIONS);
-    const unsigned lrs = region_lrs(g);
+    GS_REQUIRE(region_side == 0 || region_side == 2 || region_side == 4 || region_side == 8,
+               "region_side must be 0, 2, 4 or 8 (got %d)", region_side);
+    const unsigned lrs = region_lrs(g, region_side);
     ClearRegions CR{nullptr, nullptr, nullptr, 0, 0, lrs};
     if (split)
         CR = ClearRegions{compute_locally != nullptr ? at<uint64_t>(geom, g.regmask) : nullptr,
@@ -4016,7 +4029,7 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
 int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                         const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
                         const uint8_t* compute_locally, const float* rects, void* geom, void* binning, void* img,
-                        FwdOut O, int32_t* n_render, hipStream_t stream, const DepthIO* depth_io = nullptr)
+                        FwdOut O, int32_t* n_render, hipStream_t stream, const DepthIO* depth_io = nullptr, int region_side = 0)
 {
     GS_REQUIRE(P >= 0 && W > 0 && H > 0 && R >= 0, "invalid sizes P=%d W=%d H=%d R=%lld", P, W, H, (long long)R);
     GS_REQUIRE(((uintptr_t)conic_opacity & 15) == 0 && ((uintptr_t)means2D & 7) == 0 && ((uintptr_t)rects & 7) == 0,
@@ -4063,7 +4076,9 @@ int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* b
         // first, one after another on the caller's stream; the grids are
         // bounded by how many regions of the class the region entries (at
         // most R) can fill and by what fits on the chip at once.
-        const unsigned lrs = region_lrs(g);
+        GS_REQUIRE(region_side == 0 || region_side == 2 || region_side == 4 || region_side == 8,
+                   "region_side must be 0, 2, 4 or 8 (got %d)", region_side);
+        const unsigned lrs = region_lrs(g, region_side);
         uint32_t* clist = at<uint32_t>(binning, bl.clist);
         // region lists (12 bytes per entry, at most R entries) in the point
         // list and key areas of the binning buffer (12 R bytes from point_list)
@@ -4355,14 +4370,14 @@ int render_geo_forward_impl(int P, int64_t R, int W, int H, float tan_fovx, floa
 template <typename Fwd>
 int reserved_forward(bool full, int P, int64_t cap, int W, int H, const float* means2D, const int* radii,
                      const uint8_t* compute_locally, const float* rects, const float* conic_opacity, void* geom,
-                     int64_t* num_rendered, hipStream_t stream, Fwd&& forward)
+                     int64_t* num_rendered, hipStream_t stream, int region_side, Fwd&& forward)
 {
     GS_REQUIRE(cap > 0 && cap <= 0xffffffffll, "capacity must be in [1, 2^32 - 1] (got %lld)", (long long)cap);
     GS_REQUIRE(num_rendered != nullptr, "num_rendered must be non-null");
     Readback* rb = nullptr;
     if (int rc = readback_acquire(rb); rc != GS_OK) return rc;
     int rc = render_count_impl(full, P, W, H, means2D, radii, compute_locally, rects, conic_opacity, geom, nullptr,
-                               stream, (uint64_t)cap, rb);
+                               stream, (uint64_t)cap, rb, region_side);
     if (rc == GS_OK) rc = forward();
     if (rc != GS_OK) {
         // a scan already queued may still store into the slot: let it land first
@@ -4403,18 +4418,18 @@ int reserved_forward(bool full, int P, int64_t cap, int W, int H, const float* m
 
 extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D, const int* radii,
                                        const uint8_t* compute_locally, void* geom, int64_t* num_rendered,
-                                       hipStream_t stream)
+                                       int region_side, hipStream_t stream)
 {
     gs::clear_error();
     return render_count_impl(false, P, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom, num_rendered,
-                             stream);
+                             stream, ~0ull, nullptr, region_side);
 }
 
 extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                                  const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
                                  const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                  float* out_color, int32_t* n_render, int32_t* n_consider, int32_t* n_contrib,
-                                 int32_t* out_observe, hipStream_t stream)
+                                 int32_t* out_observe, int region_side, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4424,7 +4439,8 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
     O.n_consider = n_consider;
     O.n_contrib_tile = n_contrib;
     return render_forward_impl(BLEND_SPLIT, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
-                               compute_locally, nullptr, geom, binning, img, O, n_render, stream);
+                               compute_locally, nullptr, geom, binning, img, O, n_render, stream, nullptr,
+                               region_side);
 }
 
 extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H, const float* bg,
@@ -4433,7 +4449,7 @@ extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H,
                                           const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                           float* out_color, int32_t* n_render, int32_t* n_consider,
                                           int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
-                                          hipStream_t stream)
+                                          int region_side, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4443,10 +4459,10 @@ extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H,
     O.n_consider = n_consider;
     O.n_contrib_tile = n_contrib;
     return reserved_forward(false, P, capacity, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom,
-                            num_rendered, stream, [&] {
+                            num_rendered, stream, region_side, [&] {
                                 return render_forward_impl(BLEND_SPLIT, P, capacity, W, H, bg, means2D, depths, radii,
                                                            conic_opacity, rgb, compute_locally, nullptr, geom, binning,
-                                                           img, O, n_render, stream);
+                                                           img, O, n_render, stream, nullptr, region_side);
                             });
 }
 
@@ -4477,7 +4493,7 @@ extern "C" int gs_render_forward_geo(int P, int64_t R, int W, int H, const float
                                      void* img, float* out_color, int32_t* n_render, int32_t* n_consider,
                                      int32_t* n_contrib, int32_t* out_observe, float tan_fovx, float tan_fovy,
                                      const float* all_map, float* out_all_map, float* out_plane_depth,
-                                     hipStream_t stream)
+                                     int region_side, hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4489,7 +4505,8 @@ extern "C" int gs_render_forward_geo(int P, int64_t R, int W, int H, const float
     if (int rc = set_geo(O, P, W, H, tan_fovx, tan_fovy, all_map, out_all_map, out_plane_depth); rc != GS_OK)
         return rc;
     return render_forward_impl(BLEND_SPLIT_GEO, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
-                               compute_locally, nullptr, geom, binning, img, O, n_render, stream);
+                               compute_locally, nullptr, geom, binning, img, O, n_render, stream, nullptr,
+                               region_side);
 }
 
 extern "C" int gs_render_forward_reserved_geo(int P, int64_t capacity, int W, int H, const float* bg,
@@ -4499,7 +4516,8 @@ extern "C" int gs_render_forward_reserved_geo(int P, int64_t capacity, int W, in
                                               float* out_color, int32_t* n_render, int32_t* n_consider,
                                               int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
                                               float tan_fovx, float tan_fovy, const float* all_map,
-                                              float* out_all_map, float* out_plane_depth, hipStream_t stream)
+                                              float* out_all_map, float* out_plane_depth, int region_side,
+                                              hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4511,10 +4529,10 @@ extern "C" int gs_render_forward_reserved_geo(int P, int64_t capacity, int W, in
     if (int rc = set_geo(O, P, W, H, tan_fovx, tan_fovy, all_map, out_all_map, out_plane_depth); rc != GS_OK)
         return rc;
     return reserved_forward(false, P, capacity, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom,
-                            num_rendered, stream, [&] {
+                            num_rendered, stream, region_side, [&] {
                                 return render_forward_impl(BLEND_SPLIT_GEO, P, capacity, W, H, bg, means2D, depths,
                                                            radii, conic_opacity, rgb, compute_locally, nullptr, geom,
-                                                           binning, img, O, n_render, stream);
+                                                           binning, img, O, n_render, stream, nullptr, region_side);
                             });
 }
 
@@ -4613,7 +4631,7 @@ extern "C" int gs_render_full_forward_reserved(int P, int64_t capacity, int W, i
     O.accum_weights = accum_weights;
     O.accum_weights_count = accum_weights_count;
     return reserved_forward(true, P, capacity, W, H, means2D, radii, nullptr, rects, conic_opacity, geom,
-                            num_rendered, stream, [&] {
+                            num_rendered, stream, 0, [&] {
                                 return render_forward_impl(accum_weights != nullptr ? BLEND_SIMP : BLEND_FULL, P,
                                                            capacity, W, H, bg, means2D, depths, radii, conic_opacity,
                                                            colors, nullptr, rects, geom, binning, img, O, nullptr,

@@ -286,13 +286,15 @@ def _tile_mask(cl, H, W, device):
 
 
 def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False,
-                        debug=False, geo=None):
+                        debug=False, geo=None, region_side=None):
     """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
     geomBuffer, binningBuffer, imgBuffer, render_ms).  The binning buffer may be
     sized for more than num_rendered instances (_lib.InstanceReserve); render_ms
     covers the whole render forward, the instance count included.
     geo = (tanfovx, tanfovy, all_maps (P,5)): render_geo in the same walk of the
-    lists; then out_all_map (5,H,W) and out_plane_depth (1,H,W) follow."""
+    lists; then out_all_map (5,H,W) and out_plane_depth (1,H,W) follow.
+    region_side: the binning's region side (0, 2, 4, 8; None: chosen from the
+    device's last forward, _lib.InstanceReserve.region_side)."""
     _require_device(means2D, "means2D")
     dev = means2D.device
     P = means2D.size(0)
@@ -328,6 +330,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         ev0.record()
     R = None
     cap = _lib.RESERVE.capacity(dev)
+    rside = _lib.RESERVE.region_side(dev) if region_side is None else int(region_side)
     if cap is not None:
         # one call, no host round trip between the count and the duplication
         binning = torch.empty(lib.gs_render_binning_bytes(cap), device=dev, dtype=torch.uint8)
@@ -335,26 +338,27 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         args = (P, cap, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
                 ptr(geom), ptr(binning), ptr(img), *outs, C.byref(Rv))
         if maps is None:
-            check(lib.gs_render_forward_reserved(*args, stream), "gs_render_forward_reserved")
+            check(lib.gs_render_forward_reserved(*args, rside, stream), "gs_render_forward_reserved")
         else:
-            check(lib.gs_render_forward_reserved_geo(*args, *geo_args, stream), "gs_render_forward_reserved_geo")
-        _lib.RESERVE.update(dev, int(Rv.value))
+            check(lib.gs_render_forward_reserved_geo(*args, *geo_args, rside, stream),
+                  "gs_render_forward_reserved_geo")
+        _lib.RESERVE.update(dev, int(Rv.value), P)
         R = int(Rv.value) if Rv.value <= cap else None
     if R is None:
         # first forward on the device, or more instances than reserved: count,
         # then size the binning buffer exactly
         Rv = C.c_int64(0)
         check(lib.gs_render_forward_count(P, W, H, ptr(means2D), ptr(radii), ptr(cl), ptr(geom), C.byref(Rv),
-                                          stream), "gs_render_forward_count")
+                                          rside, stream), "gs_render_forward_count")
         R = int(Rv.value)
-        _lib.RESERVE.update(dev, R)
+        _lib.RESERVE.update(dev, R, P)
         binning = torch.empty(lib.gs_render_binning_bytes(R), device=dev, dtype=torch.uint8)
         args = (P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
                 ptr(geom), ptr(binning), ptr(img), *outs)
         if maps is None:
-            check(lib.gs_render_forward(*args, stream), "gs_render_forward")
+            check(lib.gs_render_forward(*args, rside, stream), "gs_render_forward")
         else:
-            check(lib.gs_render_forward_geo(*args, *geo_args, stream), "gs_render_forward_geo")
+            check(lib.gs_render_forward_geo(*args, *geo_args, rside, stream), "gs_render_forward_geo")
     _lib.debug_sync(debug, "gs_render_forward")
     ms = None
     if timing:

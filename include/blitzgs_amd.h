@@ -137,6 +137,12 @@ int gs_preprocess_backward_rec(int P, int D, int K, const void* bwd_records, con
  *             final transmittance and contributor counts)
  * compute_locally is a uint8 (ceil(H/16), ceil(W/16)) tile mask, or NULL
  * when every tile is local.
+ * region_side: 0, 2, 4 or 8 -- the side, in tiles, of the square regions the
+ * split path bins through (0: the smallest the tile grid allows; a side below
+ * that is raised to it).  Every output is the same for every side; larger
+ * regions suit Gaussians that each cover many tiles (fewer region entries,
+ * longer lists to sort).  A count call and the forward call after it take
+ * the same value.
  * ------------------------------------------------------------------------ */
 size_t gs_render_geom_bytes(int P, int image_width, int image_height);
 size_t gs_render_binning_bytes(int64_t R);
@@ -148,7 +154,7 @@ size_t gs_render_img_bytes(int image_width, int image_height);
  * reference reads R back with cudaMemcpy at rasterizer_impl.cu:621). */
 int gs_render_forward_count(int P, int image_width, int image_height, const float* means2D,
                             const int* radii, const uint8_t* compute_locally, void* geom,
-                            int64_t* num_rendered, gs_stream_t stream);
+                            int64_t* num_rendered, int region_side, gs_stream_t stream);
 
 /* Duplicate, sort, range and blend.  Outputs: out_color (3,H,W),
  * n_render / n_consider / n_contrib int32 (tiles), out_observe int32 (P).
@@ -165,7 +171,7 @@ int gs_render_forward(int P, int64_t R, int image_width, int image_height, const
                       const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
                       void* geom, void* binning, void* img, float* out_color, int32_t* n_render,
                       int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe,
-                      gs_stream_t stream);
+                      int region_side, gs_stream_t stream);
 
 /* The two calls above in one, without the host round trip between them: the
  * count, the duplication, the sorts and the blend are all queued at once
@@ -183,7 +189,7 @@ int gs_render_forward_reserved(int P, int64_t capacity, int image_width, int ima
                                const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                float* out_color, int32_t* n_render, int32_t* n_consider,
                                int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
-                               gs_stream_t stream);
+                               int region_side, gs_stream_t stream);
 
 /* Render backward.  Replaces RenderGaussiansBackwardCUDA
  * (diff-gaussian-rasterization_r/rasterize_points.cu:363-436; kernel
@@ -238,7 +244,7 @@ int gs_render_forward_geo(int P, int64_t R, int image_width, int image_height, c
                           void* geom, void* binning, void* img, float* out_color, int32_t* n_render,
                           int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe, float tan_fovx,
                           float tan_fovy, const float* all_map, float* out_all_map, float* out_plane_depth,
-                          gs_stream_t stream);
+                          int region_side, gs_stream_t stream);
 int gs_render_forward_reserved_geo(int P, int64_t capacity, int image_width, int image_height,
                                    const float* bg, const float* means2D, const float* depths,
                                    const int* radii, const float* conic_opacity, const float* rgb,
@@ -246,7 +252,8 @@ int gs_render_forward_reserved_geo(int P, int64_t capacity, int image_width, int
                                    float* out_color, int32_t* n_render, int32_t* n_consider,
                                    int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
                                    float tan_fovx, float tan_fovy, const float* all_map,
-                                   float* out_all_map, float* out_plane_depth, gs_stream_t stream);
+                                   float* out_all_map, float* out_plane_depth, int region_side,
+                                   gs_stream_t stream);
 
 /* gs_render_backward with render_geo = true (RenderGaussiansBackwardCUDA,
  * rasterize_points.cu:363-436; kernel backward.cu:393-405,427-432,476-490):

@@ -162,3 +162,27 @@ def test_render_geo_shape_checks_without_device(lib):
         rasterizer._render_geo_forward_raw(10, 32, 32, 0.5, 0.5, torch.zeros(10, 4), None, 0, geom, geom, geom)
     with pytest.raises(RuntimeError, match=r"all_map of shape \(10, 5\)"):
         rasterizer._render_geo_forward_raw(10, 32, 32, 0.5, 0.5, None, None, 0, geom, geom, geom)
+
+
+def test_region_side_checked_without_device(lib):
+    """The split render's region side must be 0, 2, 4 or 8; checked before any HIP call."""
+    nz = C.c_void_p(256)
+    R = C.c_int64(0)
+    rc = lib.gs_render_forward_count(10, 64, 64, nz, nz, None, nz, C.byref(R), 3, None)
+    assert rc != 0 and b"region_side" in lib.gs_last_error()
+
+
+def test_region_side_choice_follows_instances_per_gaussian():
+    """InstanceReserve.region_side: 4x4-tile regions after a forward with many
+    tile instances per Gaussian, the default otherwise (and without history)."""
+    from blitzgs_amd._lib import InstanceReserve
+    r = InstanceReserve()
+    assert r.region_side("cuda:0") == 0
+    r.update("cuda:0", 27_000_000, 1_000_000)     # config 1's shape: 27 per Gaussian
+    assert r.region_side("cuda:0") == 4
+    r.update("cuda:0", 8_000_000, 6_000_000)      # config 2's shape: 1.3 per Gaussian
+    assert r.region_side("cuda:0") == 0
+    r.update("cuda:0", 5)                          # no P: the choice is kept
+    assert r.region_side("cuda:0") == 0
+    r.reset()
+    assert r.region_side("cuda:0") == 0

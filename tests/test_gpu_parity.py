@@ -409,6 +409,46 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
         R._preprocess_backward_raw(radii_t, cov3D, clamped, *args, records=b[8][:-256])
 
 
+@pytest.mark.parametrize("case", ["wide", "small", "masked", "ragged"])
+def test_region_sides_give_identical_results(case):
+    """Every output of the split forward -- image, per-tile and per-pixel
+    counters, out_observe, ranges, the sorted ids and keys -- is the same for
+    region sides 2 (default), 4 and 8, through both forward routes; the
+    default side is checked against the oracle elsewhere."""
+    from blitzgs_amd import rasterizer as R
+    from tests.gpu_helpers import buffer_views
+    W, H, cl = 200, 150, None
+    if case == "wide":
+        scene, cam = synth.small_scene(2500, seed=91, W=W, H=H, extent=1.2, log_mu=-1.2)
+    elif case == "small":
+        scene, cam = synth.small_scene(3000, seed=12, W=W, H=H, extent=1.2)
+    elif case == "masked":
+        scene, cam = synth.small_scene(4000, seed=33, W=W, H=H, extent=1.2, log_mu=-1.8)
+        cl = torch.as_tensor(np.random.default_rng(5).random(((H + 15) // 16, (W + 15) // 16)) < 0.5, device="cuda")
+    else:
+        W, H = 333, 177
+        scene, cam = synth.small_scene(3500, seed=34, W=W, H=H, extent=1.3, log_mu=-1.6)
+    rs = settings_for(cam, bg=(0.2, 0.1, 0.3))
+    pre = gpu_preprocess(scene, rs)
+    args = (rs.bg, H, W, pre["means2D"], pre["depths"], pre["radii"], pre["conic_opacity"], pre["rgb"], cl)
+    outs = {}
+    for side in (2, 4, 8):
+        for reserved in (False, True):
+            if not reserved:
+                _lib.RESERVE.reset()
+            o = R._render_forward_raw(*args, region_side=side)
+            Rn, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, _ = o
+            v = buffer_views(Rn, W, H, binning, img, pre["means2D"].shape[0], pre["depths"], geom)
+            outs[(side, reserved)] = dict(R=Rn, color=color, n_render=n_render, n_consider=n_consider,
+                                         n_contrib=n_contrib, out_observe=out_observe, **v)
+    ref = outs[(2, False)]
+    for key, o in outs.items():
+        assert o["R"] == ref["R"] > 0, key
+        for k in ref:
+            if k != "R":
+                assert torch.equal(o[k], ref[k]), (case, key, k)
+
+
 def test_autograd_clears_preprocess_grads_beside_the_render(monkeypatch):
     """The render backward clears the preprocess backward's dL/dsh while its
     blend runs, and the preprocess backward writes only the visible rows into
@@ -736,7 +776,7 @@ def test_point_list_written_on_request():
     img = torch.empty(lib.gs_render_img_bytes(W, H), device="cuda", dtype=torch.uint8)
     R = C.c_int64(0)
     _lib.check(lib.gs_render_forward_count(P, W, H, _lib.ptr(dev["means2D"]), _lib.ptr(dev["radii"]), None,
-                                           _lib.ptr(geom), C.byref(R), s), "count")
+                                           _lib.ptr(geom), C.byref(R), 0, s), "count")
     R = int(R.value)
     binning = torch.full((lib.gs_render_binning_bytes(R),), 0xAB, device="cuda", dtype=torch.uint8)
     color = torch.empty((3, H, W), device="cuda")
@@ -746,7 +786,8 @@ def test_point_list_written_on_request():
     _lib.check(lib.gs_render_forward(P, R, W, H, _lib.ptr(bg), _lib.ptr(dev["means2D"]), _lib.ptr(dev["depths"]),
                                      _lib.ptr(dev["radii"]), _lib.ptr(dev["conic_opacity"]), _lib.ptr(dev["rgb"]),
                                      None, _lib.ptr(geom), _lib.ptr(binning), _lib.ptr(img), _lib.ptr(color),
-                                     _lib.ptr(n_render), _lib.ptr(n_consider), _lib.ptr(n_contrib), _lib.ptr(obs), s),
+                                     _lib.ptr(n_render), _lib.ptr(n_consider), _lib.ptr(n_contrib), _lib.ptr(obs), 0,
+                                     s),
                "forward")
     torch.cuda.synchronize()
     from tests.gpu_helpers import buffer_views

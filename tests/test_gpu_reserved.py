@@ -46,14 +46,14 @@ def _forward(dev, W, H, capacity=None, cl=None):
     R = C.c_int64(-1)
     if capacity is None:
         _lib.check(lib.gs_render_forward_count(P, W, H, _lib.ptr(dev["means2D"]), _lib.ptr(dev["radii"]), clp,
-                                               _lib.ptr(geom), C.byref(R), s), "count")
+                                               _lib.ptr(geom), C.byref(R), 0, s), "count")
         binning = torch.empty(lib.gs_render_binning_bytes(R.value), device="cuda", dtype=torch.uint8)
-        _lib.check(lib.gs_render_forward(P, R.value, W, H, *args, _lib.ptr(binning), _lib.ptr(img), *outs, s),
+        _lib.check(lib.gs_render_forward(P, R.value, W, H, *args, _lib.ptr(binning), _lib.ptr(img), *outs, 0, s),
                    "forward")
     else:
         binning = torch.empty(lib.gs_render_binning_bytes(capacity), device="cuda", dtype=torch.uint8)
         _lib.check(lib.gs_render_forward_reserved(P, capacity, W, H, *args, _lib.ptr(binning), _lib.ptr(img),
-                                                  *outs, C.byref(R), s), "forward_reserved")
+                                                  *outs, C.byref(R), 0, s), "forward_reserved")
     torch.cuda.synchronize()
     return dict(R=int(R.value), color=color, n_render=n_render, n_consider=n_consider, n_contrib=n_contrib,
                 obs=obs, geom=geom, binning=binning, img=img)

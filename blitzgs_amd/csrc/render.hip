@@ -2519,7 +2519,7 @@ __device__ __forceinline__ void active_rect(uint64_t m, float qx0, float qy0, fl
 struct Stage {
     float4 a[64];   // x, y, -a/2, -b
     float4 b[64];   // -c/2, opacity, r, g
-    float4 c[64];   // blue, tag bits, position in the tile's list (bits), alpha cut-off power
+    float4 c[64];   // blue, tag bits, 1-based position in the tile's list (bits), alpha cut-off power
 };
 
 // Per-pixel state of the forward blend, and the blend of one staged entry
@@ -2560,17 +2560,19 @@ __device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, 
     // sign is the live test (one compare, no separate flag), |T| its value
     p.T = upd ? test_T : (fin ? -p.T : p.T);
     p.n2l += upd ? 1u : 0u;
-    p.last = upd ? (uint32_t)__float_as_int(Cc.z) + 1u : p.last;
+    p.last = upd ? (uint32_t)__float_as_int(Cc.z) : p.last;   // (staged 1-based)
     return FwdStep{upd, observe, wgt};
 }
 
 // stages entry k of the list; `tag` (Gaussian id in the forward, compact
-// index in the backward) rides along in the blue slot's partner
+// index in the backward) rides along in the blue slot's partner, and the
+// entry's 1-based position k + 1 (the value a pixel's last contributor takes)
+// in the next slot
 __device__ __forceinline__ void stage_put(Stage& st, int slot, const Rec& r, uint32_t tag, int k)
 {
     st.a[slot] = make_float4(r.q0.x, r.q0.y, -0.5f * r.q0.z, -r.q0.w);
     st.b[slot] = make_float4(-0.5f * r.q1.x, r.q1.y, r.q1.z, r.q1.w);
-    st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k), r.cut_power);
+    st.c[slot] = make_float4(r.q2.x, __uint_as_float(tag), __int_as_float(k + 1), r.cut_power);
 }
 
 // Blend modes: the split path's render (observation counts and per-tile
@@ -3165,7 +3167,7 @@ struct BwdEval {
 __device__ __forceinline__ BwdEval bwd_eval(const BwdConst& k, const float4& A, const float4& B, const float4& Cc)
 {
     BwdEval e;
-    const int ci = __float_as_int(Cc.z);   // position in the tile's list
+    const int ci1 = __float_as_int(Cc.z);   // 1-based position in the tile's list
     e.dx = A.x - k.pxf;
     e.dy = A.y - k.pyf;
     // gs::power_of's operations, with the products ha dx, hc dy, nb dx kept
@@ -3175,7 +3177,7 @@ __device__ __forceinline__ BwdEval bwd_eval(const BwdConst& k, const float4& A, 
     e.nbdx = A.w * e.dx;
     const float power = __builtin_fmaf(e.hadx, e.dx, __builtin_fmaf(e.hcdy, e.dy, e.nbdx * e.dy));
     e.alpha = gs::blend_alpha(B.y, power, Cc.w, e.G0);
-    e.valid = ci < k.last && !(power > 0.0f) && !(e.alpha < (1.0f / 255.0f));
+    e.valid = ci1 <= k.last && !(power > 0.0f) && !(e.alpha < (1.0f / 255.0f));
     return e;
 }
 
@@ -3663,7 +3665,7 @@ __device__ __forceinline__ void probe_stage(Stage& st, int lane)
     const float op = 0.02f + 0.0004f * (float)lane;
     st.a[lane] = make_float4(mx, my, -0.5f * a, -b);
     st.b[lane] = make_float4(-0.5f * c, op, 0.3f, 0.6f);
-    st.c[lane] = make_float4(0.9f, __uint_as_float((uint32_t)lane), __int_as_float(lane), gs::alpha_cut_power(op));
+    st.c[lane] = make_float4(0.9f, __uint_as_float((uint32_t)lane), __int_as_float(lane + 1), gs::alpha_cut_power(op));
 }
 
 template <int WHICH>

@@ -65,12 +65,15 @@ def stage_bytes(P, P_vis, R, npx, E=None):
         # depth, radius, conic+opacity, rgb (44 B) of all, the backward's 48-byte record of the visible and a
         # 64-bit mask per 64 Gaussians (cov3D is recomputed by the backward, the records hold the clamp flags)
         "preprocess_fwd_kernel": 88 * P + P // 8 + 240 * P_vis,
-        # writes the five gradients (236 B) and reads dL/dopacity (4 B) of all and the masks; reads the record,
-        # the rest of dL/dconic_opacity, dL/dmeans2D, dL/drgb and SH (272 B) of the visible
-        "preprocess_bwd_kernel": 240 * P + P // 8 + 272 * P_vis,
+        # writes dL/dmeans3D, dL/dscales, dL/drotations, dL/dopacity (44 B) and reads dL/dopacity (4 B) of all
+        # and the masks; reads the record, the rest of dL/dconic_opacity, dL/dmeans2D, dL/drgb and SH (272 B)
+        # and writes the dL/dsh row (192 B) of the visible (the render backward cleared dL/dsh)
+        "preprocess_bwd_kernel": 48 * P + P // 8 + 464 * P_vis,
         "binning": binning,
         "render_fwd_kernel": 40 * R + 24 * npx,
-        "render_bwd_kernel": 40 * R + 32 * npx,
+        # the blend's reads and writes, and the zeros of dL/dsh (192 B of every Gaussian) that it clears for
+        # the preprocess backward while its VALU-bound walk runs
+        "render_bwd_kernel": 40 * R + 32 * npx + 192 * P,
         # the accumulators cleared (64 B per listed), then the gradient unpack: compact index of all (4 B),
         # accumulators of the listed (48 B), four gradient rows of all written (48 B)
         "other": 64 * P_vis + 4 * P + 48 * P_vis + 48 * P,
@@ -87,18 +90,22 @@ BINNING_KERNELS = ("localmap_kernel", "count_regions_kernel", "scan_regions_kern
 # (first binning kernel -> end of the sorts)
 BINNING_STAGE = "binning (wall)"
 STEP_STAGES = ("preprocess_fwd_kernel", "render_fwd_kernel", "render_bwd_kernel", "preprocess_bwd_kernel")
+# kernels timed under the name of the stage they implement (the preprocess
+# backward's packed form, taken when the render backward has cleared dL/dsh)
+STAGE_OF_KERNEL = {"preprocess_bwd_packed_kernel": "preprocess_bwd_kernel"}
 
 
-def region_entries(means2D, radii, W, H, cl=None):
+def region_entries(means2D, radii, W, H, cl=None, side=0):
     """Entries of the split path's region lists: per listed Gaussian, the
-    RS x RS-tile regions (RS = 2, or 4 / 8 when 2 gives more than 16384
-    regions) that its tile rect, clipped to the box of the local tiles, meets,
-    regions tiling the box from its corner.  Exact when the local tiles fill
-    their box (no mask, or whole tile rows / columns), an upper bound
-    otherwise."""
+    RS x RS-tile regions that its tile rect, clipped to the box of the local
+    tiles, meets, regions tiling the box from its corner; RS is the larger of
+    `side` (the forward's region_side argument) and the smallest of 2, 4, 8
+    that gives at most 16384 regions.  Exact when the local tiles fill their
+    box (no mask, or whole tile rows / columns), an upper bound otherwise."""
     import torch
     gx, gy = (W + 15) // 16, (H + 15) // 16
     rs = next((s for s in (2, 4, 8) if ((gx + s - 1) // s) * ((gy + s - 1) // s) <= 16384), 8)
+    rs = max(rs, side)
     bx0, by0, bx1, by1 = 0, 0, gx, gy
     if cl is not None:
         cols = torch.nonzero(cl.reshape(gy, gx).any(0)).flatten()
@@ -346,7 +353,7 @@ def header(args, metric, value, unit, ms, dtype, workload, extra_cfg):
 
 def run_step(args):
     import torch
-    from blitzgs_amd import synth
+    from blitzgs_amd import _lib, synth
     from blitzgs_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
     dev = torch.device("cuda:0")
     peak_copy = copy_peak()
@@ -409,6 +416,11 @@ def run_step(args):
     log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step median ({ms_mean:.3f} mean; {ms_instr:.3f} with "
         f"per-kernel events; {ms_train:.3f} with cuda_args['stats_collector'])")
 
+    for k, stage in STAGE_OF_KERNEL.items():
+        if k in kt:
+            t, n = kt.pop(k)
+            t0, n0 = kt.get(stage, (0.0, 0))
+            kt[stage] = (t0 + t, n0 + n)
     per_kernel = {k: v[0] / max(1, args.steps) for k, v in kt.items()}
     avg_launch = {k: v[0] / max(1, v[1]) for k, v in kt.items()}
     stages = {k: per_kernel.get(k, 0.0) for k in STEP_STAGES}
@@ -417,7 +429,7 @@ def run_step(args):
     avg_launch["binning"] = avg_launch.get(BINNING_STAGE, binning_kernels_ms)
     stages["other"] = sum(v for k, v in per_kernel.items()
                           if k not in stages and k not in BINNING_KERNELS and not k.startswith(BINNING_STAGE))
-    E_reg = region_entries(info["means2D"], info["radii"], W, H, cl)
+    E_reg = region_entries(info["means2D"], info["radii"], W, H, cl, side=_lib.RESERVE.region_side(dev))
     sb = stage_bytes(P, P_vis, R, W * H, E_reg)
     stage_rows = {}
     for k, ms in stages.items():
@@ -748,7 +760,10 @@ def run_full(args):
     R = fullpath._forward(rs, x, culling, True, False)[-1]
     sb = stage_bytes(P, P_vis, R, W * H)
     sb["preprocess_fwd_full_kernel"] = sb["preprocess_fwd_kernel"]
-    sb["preprocess_bwd_full_kernel"] = sb["preprocess_bwd_kernel"]
+    # the full-image path clears no dL/dsh in the render backward: its preprocess backward writes the SH
+    # gradients of every Gaussian (zeros for the invisible ones)
+    sb["preprocess_bwd_full_kernel"] = sb["preprocess_bwd_kernel"] + 192 * (P - P_vis)
+    sb["render_bwd_kernel"] -= 192 * P
     dom = max((k for k in sb if k in per_kernel), key=lambda k: per_kernel[k])
     roofline = roofline_of(dom, sb[dom], avg_launch[dom])
     roofline["note"] = ("the blend kernels are VALU-bound (per-pixel exp and gradient arithmetic plus a 64-lane "

@@ -506,6 +506,60 @@ __device__ __forceinline__ void preprocess_bwd_one(
     const float mx = mean.x, my = mean.y, mz = mean.z;
     const float* V = cam.v;
     const float* PM = cam.p;
+
+    // ---- SH backward first (the full path: only with SH colours and a rest
+    // array): its 48 coefficients and gradients are dead before the
+    // covariance backward starts; the mean term dm joins gm below, in the
+    // same order as before
+    const bool sh_grads = !FULL || (!F.colors_precomp && F.rest != nullptr);
+    float dm[3] = {0.f, 0.f, 0.f};
+    if (sh_grads) {
+        float s[3 * NC];
+        if (FULL)
+            load_sh_split<NC>(F.dc + 3 * (size_t)idx, F.rest + (size_t)idx * F.M * 3, s);
+        else
+            load_sh<NC>(sh + (size_t)idx * K * 3, vec16, s);
+        const float dir_orig[3] = {mx - cam.c[0], my - cam.c[1], mz - cam.c[2]};
+        const float len = __builtin_sqrtf(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]);
+        const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
+        float g[3];
+#pragma unroll
+        for (int ch = 0; ch < 3; ch++) g[ch] = src.clamp(idx, ch) ? 0.0f : dL_drgb[3 * idx + ch];
+        float gsh[3 * NC], dx[3], dy[3], dz[3];
+        sh_backward<DEG>(x, y, z, s, g, gsh, dx, dy, dz);
+        const float dL_ddir[3] = {dx[0] * g[0] + dx[1] * g[1] + dx[2] * g[2],
+                                  dy[0] * g[0] + dy[1] * g[1] + dy[2] * g[2],
+                                  dz[0] * g[0] + dz[1] * g[1] + dz[2] * g[2]};
+        dnormvdv3(dir_orig, dL_ddir, dm);
+        // dL/dsh: the first NC coefficients, zeros after
+        if (FULL && !STAGED) {
+            F.dL_ddc[3 * (size_t)idx + 0] = gsh[0];
+            F.dL_ddc[3 * (size_t)idx + 1] = gsh[1];
+            F.dL_ddc[3 * (size_t)idx + 2] = gsh[2];
+            float* o = F.dL_drest + (size_t)idx * F.M * 3;
+#pragma unroll
+            for (int i = 0; i < 3 * (NC - 1); i++) o[i] = gsh[3 + i];
+            for (int i = 3 * (NC - 1); i < 3 * F.M; i++) o[i] = 0.f;
+        } else if (STAGED) {
+#pragma unroll
+            for (int i = 0; i < 48; i++) s_row[i] = i < 3 * NC ? gsh[i] : 0.f;
+        } else if (vec16) {
+            float4* o4 = reinterpret_cast<float4*>(gsh_out);
+#pragma unroll
+            for (int i = 0; i < (3 * NC + 3) / 4; i++) {
+                float v[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[k] = (4 * i + k < 3 * NC) ? gsh[4 * i + k] : 0.f;
+                o4[i] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+            for (int i = (3 * NC + 3) / 4; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 3 * NC; i++) gsh_out[i] = gsh[i];
+            for (int i = 3 * NC; i < 3 * K; i++) gsh_out[i] = 0.f;
+        }
+    }
+
     float c6[6];
     if (FULL && F.cov3D_precomp != nullptr) {
 #pragma unroll
@@ -588,54 +642,10 @@ __device__ __forceinline__ void preprocess_bwd_one(
         gm[2] += (PM[8] * m_w - PM[11] * mul1) * gx + (PM[9] * m_w - PM[11] * mul2) * gy;
     }
 
-    // ---- SH backward (the full path: only with SH colours and a rest array)
-    if (!FULL || (!F.colors_precomp && F.rest != nullptr)) {
-        float s[3 * NC];
-        if (FULL)
-            load_sh_split<NC>(F.dc + 3 * (size_t)idx, F.rest + (size_t)idx * F.M * 3, s);
-        else
-            load_sh<NC>(sh + (size_t)idx * K * 3, vec16, s);
-        const float dir_orig[3] = {mx - cam.c[0], my - cam.c[1], mz - cam.c[2]};
-        const float len = __builtin_sqrtf(dir_orig[0] * dir_orig[0] + dir_orig[1] * dir_orig[1] + dir_orig[2] * dir_orig[2]);
-        const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
-        float g[3];
-#pragma unroll
-        for (int ch = 0; ch < 3; ch++) g[ch] = src.clamp(idx, ch) ? 0.0f : dL_drgb[3 * idx + ch];
-        float gsh[3 * NC], dx[3], dy[3], dz[3];
-        sh_backward<DEG>(x, y, z, s, g, gsh, dx, dy, dz);
-        const float dL_ddir[3] = {dx[0] * g[0] + dx[1] * g[1] + dx[2] * g[2],
-                                  dy[0] * g[0] + dy[1] * g[1] + dy[2] * g[2],
-                                  dz[0] * g[0] + dz[1] * g[1] + dz[2] * g[2]};
-        float dm[3];
-        dnormvdv3(dir_orig, dL_ddir, dm);
-        gm[0] += dm[0]; gm[1] += dm[1]; gm[2] += dm[2];
-        // dL/dsh: the first NC coefficients, zeros after
-        if (FULL && !STAGED) {
-            F.dL_ddc[3 * (size_t)idx + 0] = gsh[0];
-            F.dL_ddc[3 * (size_t)idx + 1] = gsh[1];
-            F.dL_ddc[3 * (size_t)idx + 2] = gsh[2];
-            float* o = F.dL_drest + (size_t)idx * F.M * 3;
-#pragma unroll
-            for (int i = 0; i < 3 * (NC - 1); i++) o[i] = gsh[3 + i];
-            for (int i = 3 * (NC - 1); i < 3 * F.M; i++) o[i] = 0.f;
-        } else if (STAGED) {
-#pragma unroll
-            for (int i = 0; i < 48; i++) s_row[i] = i < 3 * NC ? gsh[i] : 0.f;
-        } else if (vec16) {
-            float4* o4 = reinterpret_cast<float4*>(gsh_out);
-#pragma unroll
-            for (int i = 0; i < (3 * NC + 3) / 4; i++) {
-                float v[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) v[k] = (4 * i + k < 3 * NC) ? gsh[4 * i + k] : 0.f;
-                o4[i] = make_float4(v[0], v[1], v[2], v[3]);
-            }
-            for (int i = (3 * NC + 3) / 4; i < 3 * K / 4; i++) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 3 * NC; i++) gsh_out[i] = gsh[i];
-            for (int i = 3 * NC; i < 3 * K; i++) gsh_out[i] = 0.f;
-        }
+    if (sh_grads) {
+        gm[0] += dm[0];
+        gm[1] += dm[1];
+        gm[2] += dm[2];
     }
     m3_row[0] = gm[0];
     m3_row[1] = gm[1];
@@ -834,6 +844,119 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     }
 }
 
+// The record path when dL/dsh arrives cleared (outputs_zeroed) and its rows
+// are 16-byte vectors: a one-wave block takes PACK_RUNS consecutive
+// 64-Gaussian runs and packs their visible Gaussians onto its lanes (item i
+// of the runs' concatenated records on lane i mod 64, round i / 64), so the
+// per-Gaussian arithmetic runs on nearly full waves instead of on the one
+// lane in five that a run's visible Gaussians occupy at the benchmark's
+// scene.  A round's dL/dsh rows are staged in LDS (pitch SH_PITCH) and leave
+// as streaming 16-byte stores, twelve lanes to a 192-byte row (whole 64-byte
+// segments); the Gaussians' dL/dmeans3D, dL/dscales and dL/drotations go to
+// LDS slots at their rows, from which each run's 64 rows (zeros for the
+// invisible ones) leave in the same coalesced stores as in
+// preprocess_bwd_kernel.  Bit-identical to preprocess_bwd_kernel's record
+// path: the same preprocess_bwd_one per Gaussian.  Two runs per block: with
+// four (expected 49 items per round at one Gaussian in five visible) the
+// larger LDS slots leave fewer blocks per CU and scenes where half the
+// Gaussians are visible take two rounds per block; two is as fast at the
+// first and keeps the second at the unpacked kernel's speed.
+constexpr int PACK_RUNS = 2;
+
+template <int DEG>
+__global__ __launch_bounds__(64) void preprocess_bwd_packed_kernel(
+    int P, int K, float tanfovx, float tanfovy, float fx, float fy, float mod, const float* __restrict__ view,
+    const float* __restrict__ proj, const float* __restrict__ campos, const float* __restrict__ sh,
+    const float* __restrict__ cov3D, const float* __restrict__ dL_dmeans2D, int m2d_stride,
+    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb, float* __restrict__ dL_dmeans3D,
+    float* __restrict__ dL_dscales, float* __restrict__ dL_drotations, float* __restrict__ dL_dsh,
+    float* __restrict__ dL_dopacity, const float4* __restrict__ rec, const uint64_t* __restrict__ rec_mask)
+{
+    constexpr int NC = (DEG + 1) * (DEG + 1);
+    constexpr int CH = (3 * NC + 3) / 4;             // 16-byte chunks of a row that can be nonzero
+    __shared__ float s_sh[64 * SH_PITCH];            // one round's dL/dsh rows
+    __shared__ int s_id[64];                         // their Gaussians (-1: none)
+    __shared__ float4 s_rot[PACK_RUNS * 64];         // per row of the runs: dL/drotations,
+    __shared__ float s_ms[PACK_RUNS * 64 * 6];       // dL/dmeans3D and dL/dscales
+    const int lane = threadIdx.x;
+    const int run0 = (int)blockIdx.x * PACK_RUNS;    // first 64-run of this block
+    const int nruns = (P + 63) >> 6;
+    uint64_t m[PACK_RUNS];
+    int pre[PACK_RUNS + 1];
+    pre[0] = 0;
+#pragma unroll
+    for (int j = 0; j < PACK_RUNS; j++) {
+        m[j] = run0 + j < nruns ? rec_mask[run0 + j] : 0ull;
+        pre[j + 1] = pre[j] + __popcll(m[j]);
+    }
+    const int n = pre[PACK_RUNS];
+    const size_t row_floats = 3 * (size_t)K;
+    for (int i = lane; i < ((n + 63) & ~63); i += 64) {
+        int id = -1;
+        if (i < n) {
+            int j = 0, pj = 0;   // the run of item i and the items before it (selects, no indexed registers)
+#pragma unroll
+            for (int t = 1; t < PACK_RUNS; t++) {
+                const bool past = i >= pre[t];
+                j = past ? t : j;
+                pj = past ? pre[t] : pj;
+            }
+            const int wbase = (run0 + j) * 64;
+            const float4* r = rec + 3 * (size_t)(wbase + i - pj);
+            const RecSrc src{r[0], r[1], r[2]};
+            const int g = __float_as_int(src.r1.w);
+            // a record names a Gaussian of its own run (a buffer from another
+            // call could name any index: such records are skipped)
+            if ((unsigned)(g - wbase) < 64u && g < P) {
+                id = g;
+                const int row = j * 64 + (g - wbase);
+                float* ms = s_ms + row * 6;
+                float op;
+                preprocess_bwd_one<DEG, true, false>(g, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src,
+                                                     sh, 1, cov3D, dL_dmeans2D, m2d_stride, dL_dconic_opacity,
+                                                     dL_drgb, ms, ms + 3, &s_rot[row], dL_dsh, &op,
+                                                     s_sh + lane * SH_PITCH, FullPreBwd{});
+            }
+        }
+        s_id[lane] = id;
+        __syncthreads();
+        // the round's rows: lane c takes chunk c % CH of row c / CH
+        for (int c = lane; c < 64 * CH; c += 64) {
+            const int r = c / CH, col = (c - r * CH) * 4;
+            const int g = s_id[r];
+            if (g < 0) continue;
+            const float* src = s_sh + r * SH_PITCH + col;
+            gs::st_stream(reinterpret_cast<float4*>(dL_dsh + (size_t)g * row_floats + col),
+                          make_float4(src[0], src[1], src[2], src[3]));
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < PACK_RUNS; j++) {
+        const int idx = (run0 + j) * 64 + lane;
+        if (idx >= P) break;
+        const bool vis = ((m[j] >> lane) & 1ull) != 0;
+        float a[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (vis) {
+            const float* ms = s_ms + (j * 64 + lane) * 6;
+#pragma unroll
+            for (int k = 0; k < 6; k++) a[k] = ms[k];
+            c = s_rot[j * 64 + lane];
+        }
+        dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
+        float* m3 = dL_dmeans3D + 3 * (size_t)idx;
+        float* sc = dL_dscales + 3 * (size_t)idx;
+        m3[0] = a[0];
+        m3[1] = a[1];
+        m3[2] = a[2];
+        sc[0] = a[3];
+        sc[1] = a[4];
+        sc[2] = a[5];
+        reinterpret_cast<float4*>(dL_drotations)[idx] = c;
+    }
+}
+
 }  // namespace
 
 static int preprocess_forward_impl(
@@ -935,7 +1058,25 @@ static int preprocess_backward_impl(
     const float fy = (float)image_height / (2.0f * tanfovy);
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
-#define GS_PRE_BWD_K(DEG, ST, RC)                                                                        \
+    if (rrec != nullptr && zeroed && sh_vec16) {
+        const dim3 pgrid(gs_div_up((size_t)P, 64 * PACK_RUNS)), pblock(64);
+#define GS_PRE_BWD_P(DEG)                                                                                    \
+    GS_TIMED("preprocess_bwd_packed_kernel", stream,                                                         \
+             hipLaunchKernelGGL((preprocess_bwd_packed_kernel<DEG>), pgrid, pblock, 0, stream, P, K, tanfovx, \
+                                tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, campos, sh, cov3D,   \
+                                dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,     \
+                                dL_dscales, dL_drotations, dL_dsh, dL_dopacity, rrec, rmask))
+        switch (D) {
+            case 0: GS_PRE_BWD_P(0); break;
+            case 1: GS_PRE_BWD_P(1); break;
+            case 2: GS_PRE_BWD_P(2); break;
+            default: GS_PRE_BWD_P(3); break;
+        }
+#undef GS_PRE_BWD_P
+        GS_LAUNCH_CHECK("preprocess_bwd_packed_kernel");
+        return GS_OK;
+    }
+#define GS_PRE_BWD_K(DEG, ST, RC)                                                                      \
     GS_TIMED("preprocess_bwd_kernel", stream,                                                            \
              hipLaunchKernelGGL((preprocess_bwd_kernel<DEG, ST, false, RC>), grid, block, 0, stream, P, K,   \
                                 image_width, image_height, tanfovx, tanfovy, fx, fy, scale_modifier,      \

@@ -20,10 +20,10 @@ def bench():
     return mod
 
 
-def _enumerate(m, r, W, H, rows=None):
+def _enumerate(m, r, W, H, rows=None, side=2):
     """Pairs (Gaussian, region) by brute force: the tile rect of each Gaussian
     (the binning rule: trunc((mean -/+ radius (+15)) / 16) clamped to the grid),
-    clipped to the local rows, and every 2x2 region of the box it meets."""
+    clipped to the local rows, and every side x side region of the box it meets."""
     gx, gy = (W + 15) // 16, (H + 15) // 16
     by0, by1 = (0, gy) if rows is None else rows
     n = 0
@@ -33,13 +33,13 @@ def _enumerate(m, r, W, H, rows=None):
         t = lambda v, hi: min(max(int(np.trunc(v / 16.0)), 0), hi)
         x0, x1 = t(x - rad, gx), t(x + rad + 15.0, gx)
         y0, y1 = max(t(y - rad, gy), by0), min(t(y + rad + 15.0, gy), by1)
-        regions = {(tx // 2, (ty - by0) // 2) for tx in range(x0, x1) for ty in range(y0, y1)}
+        regions = {(tx // side, (ty - by0) // side) for tx in range(x0, x1) for ty in range(y0, y1)}
         n += len(regions)
     return n
 
 
-@pytest.mark.parametrize("rows", [None, (3, 9)])
-def test_region_entries_match_enumeration(bench, rows):
+@pytest.mark.parametrize("rows,side", [(None, 0), ((3, 9), 0), (None, 4), ((3, 9), 8)])
+def test_region_entries_match_enumeration(bench, rows, side):
     rng = np.random.default_rng(5)
     W, H = 300, 230
     P = 3000
@@ -53,6 +53,6 @@ def test_region_entries_match_enumeration(bench, rows):
         mask = np.zeros((gy, gx), bool)
         mask[rows[0]:rows[1]] = True
         cl = torch.from_numpy(mask.reshape(-1))
-    got = bench.region_entries(torch.from_numpy(m), torch.from_numpy(r), W, H, cl)
-    assert got == _enumerate(m, r, W, H, rows)
+    got = bench.region_entries(torch.from_numpy(m), torch.from_numpy(r), W, H, cl, side=side)
+    assert got == _enumerate(m, r, W, H, rows, max(side, 2))
     assert got > 1000

@@ -129,7 +129,7 @@ GeomLayout geom_layout(int P, int W, int H)
         const int rs = g.RS > 0 ? g.RS : 8;
         g.NR = ((gx + rs - 1) / rs) * ((gy + rs - 1) / rs);
     }
-    g.G = (gx + 1) * (gy + 1);
+    g.G = ((gx + 1) * (gy + 1) + 3) & ~3;   // a multiple of four cells: the scan reads the partials as 16-byte vectors
     long nc = ((long)P + 2047) / 2048;
     if (nc < 1) nc = 1;
     if (nc > MAX_CHUNKS) nc = MAX_CHUNKS;
@@ -1709,9 +1709,10 @@ __device__ __forceinline__ int region_class(uint32_t n)
 // Exclusive scan of N values over a 1024-thread block, each thread taking 8
 // consecutive values per round of 8192 (one block scan per round):
 // put(i, prefix, value) for every i < N; returns the total.  A value is
-// value(i, fetch(i)): the 8 fetches of a thread (global loads) are all issued
-// before the first value is formed (they read index min(i, N - 1), so that
-// none is conditional), and value may then read LDS.
+// value(i, fetch(i, j)), j the value's place among the thread's 8 (i = 8 tid
+// + j in the first round, unless clamped): the 8 fetches of a thread (global
+// loads) are all issued before the first value is formed (they read index
+// min(i, N - 1), so that none is conditional), and value may then read LDS.
 template <typename Fetch, typename Value, typename Put>
 __device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Fetch&& fetch, Value&& value, Put&& put)
 {
@@ -1720,7 +1721,7 @@ __device__ __forceinline__ uint64_t block_scan_runs(int N, uint32_t* s_wave, Fet
         const int i0 = r0 + (int)threadIdx.x * 8;
         uint32_t f[8], v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) f[j] = fetch(min(i0 + j, N - 1));
+        for (int j = 0; j < 8; j++) f[j] = fetch(min(i0 + j, N - 1), j);
         uint32_t sum = 0u;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -1771,7 +1772,7 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     const RegionGrid rg = region_grid(meta, lrs);
     if (blockIdx.x == 1) {
         const uint64_t L = block_scan_runs(
-            NW, s_wave, [&](int i) { return wcount[i]; }, [&](int, uint32_t f) { return f; },
+            NW, s_wave, [&](int i, int) { return wcount[i]; }, [&](int, uint32_t f) { return f; },
             [&](int i, uint32_t pre, uint32_t) { wcount[i] = pre; });
         if (tid == 0) meta[4] = (uint32_t)L;
         return;
@@ -1782,7 +1783,7 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
         __syncthreads();
         const int NRb = (int)(rg.nrx * rg.nry);
         const uint64_t E = block_scan_runs(
-            NRb, s_wave, [&](int r) { return rcount[r]; }, [&](int, uint32_t f) { return f; },
+            NRb, s_wave, [&](int r, int) { return rcount[r]; }, [&](int, uint32_t f) { return f; },
             [&](int r, uint32_t pre, uint32_t v) {
                 rstart[r] = pre;
                 rcursor[r] = pre;
@@ -1804,24 +1805,27 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     uint32_t t_pre[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) t_pre[j] = TL > 0 ? (uint32_t)tile_of_local[min(tid * 8 + j, TL - 1)] : 0u;
-    // the partial grids summed (into LDS, or into partial 0): four entries per
-    // thread at a time, all 64 of their loads in flight
+    // the partial grids summed (into LDS, or into partial 0): four
+    // consecutive cells per thread, one 16-byte load per partial (Gfull, the
+    // partials' stride, is a multiple of four cells and at least G rounded up
+    // to four), all 16 loads in flight
     uint32_t* gp = lds_g ? s_grid : grid;
-    constexpr int EP = 4;
-    for (int i0 = tid; i0 < G; i0 += 1024 * EP) {
-        uint32_t v[EP][GRID_PARTS];
+    for (int i0 = tid * 4; i0 < G; i0 += 4096) {
+        uint4 v[GRID_PARTS];
 #pragma unroll
-        for (int e = 0; e < EP; e++)
+        for (int k = 0; k < GRID_PARTS; k++) v[k] = *reinterpret_cast<const uint4*>(grid + (size_t)k * Gfull + i0);
+        uint4 sum = v[0];
 #pragma unroll
-            for (int k = 0; k < GRID_PARTS; k++)
-                v[e][k] = i0 + e * 1024 < G ? grid[(size_t)k * Gfull + i0 + e * 1024] : 0u;
-#pragma unroll
-        for (int e = 0; e < EP; e++) {
-            uint32_t sum = 0u;
-#pragma unroll
-            for (int k = 0; k < GRID_PARTS; k++) sum += v[e][k];
-            if (i0 + e * 1024 < G) gp[i0 + e * 1024] = sum;
+        for (int k = 1; k < GRID_PARTS; k++) {
+            sum.x += v[k].x;
+            sum.y += v[k].y;
+            sum.z += v[k].z;
+            sum.w += v[k].w;
         }
+        const uint32_t sv[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if (i0 + c < G) gp[i0 + c] = sv[c];
     }
     __syncthreads();
     // rows: one wave per row, 64 columns at a time
@@ -1860,7 +1864,7 @@ __global__ __launch_bounds__(1024) void scan_regions_kernel(uint32_t* __restrict
     // were read above)
     const uint64_t R = block_scan_runs(
         TL, s_wave,
-        [&](int l) { return l < 8192 ? t_pre[l & 7] : (uint32_t)tile_of_local[l]; },
+        [&](int l, int j) { return l < 8192 ? t_pre[j] : (uint32_t)tile_of_local[l]; },
         [&](int, uint32_t t) { return gp[(t / gx - rg.by0) * gw + (t % gx - rg.bx0)]; },
         [&](int l, uint32_t pre, uint32_t v) {
             tile_count[l] = v;

@@ -52,8 +52,8 @@ _SIGS = {
     "gs_render_img_bytes": (_sz, [_i, _i]),
     "gs_render_forward_count": (_i, [_i, _i, _i, _c, _c, _c, _c, C.POINTER(_i64), _i, _c]),
     "gs_render_forward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c,
-                               _c, _i, _c]),
-    "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _i, _c]),
+                               _c, _i, _c, _i64, _c]),
+    "gs_render_forward_reserved": (_i, [_i, _i64, _i, _i] + [_c] * 15 + [C.POINTER(_i64), _i, _c, _i64, _c]),
     "gs_render_backward": (_i, [_i, _i64, _i, _i, _c, _c, _c, _c, _c, _c, _c, _c, _c, _c, _i, _c, _c, _c, _c,
                                 _i64, _c]),
     "gs_render_geo_forward": (_i, [_i, _i64, _i, _i, _f, _f, _c, _c, _c, _c, _c, _c, _c, _c]),

@@ -59,17 +59,20 @@ def render_gaussians(background, image_height, image_width, means2D, depths, rad
     H, W = int(image_height), int(image_width)
     # render_geo: the maps in the colour's walk of the lists
     geo = (tan_fovx, tan_fovy, all_map) if render_geo else None
+    # render_geo off: the zero maps and plane depth are cleared by the blend
+    zmaps = None
+    if not render_geo:
+        zmaps = torch.empty(((6 * H * W + 3) // 4) * 4, device=means2D.device, dtype=torch.float32)
     res = _r._render_forward_raw(background, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing,
-                                 bool(debug), geo=geo)
+                                 bool(debug), geo=geo, clear=zmaps)
     R, color, n_render, n_consider, n_contrib, out_observe, geom, binning, img, ms = res[:10]
     if timing:
         args["stats_collector"]["forward_render_time"] = ms
-    dev = means2D.device
     if render_geo:
         out_all_map, out_plane_depth = res[10:]
     else:
-        out_all_map = torch.zeros((5, H, W), device=dev, dtype=torch.float32)
-        out_plane_depth = torch.zeros((1, H, W), device=dev, dtype=torch.float32)
+        maps = zmaps[:6 * H * W].view(6, H, W)
+        out_all_map, out_plane_depth = maps[:5], maps[5:]
     return R, color, n_render, n_consider, n_contrib, out_observe, out_all_map, out_plane_depth, geom, binning, img
 
 

@@ -2538,7 +2538,8 @@ struct FwdPixel {
 };
 
 struct FwdStep {
-    bool upd, observe;
+    bool upd;
+    uint64_t observe;   // the wave's pixels that observe the entry (ballot)
     float wgt;
 };
 
@@ -2553,7 +2554,12 @@ __device__ __forceinline__ FwdStep fwd_blend_step(FwdPixel& p, const float4& A, 
     const bool use = p.T > 0.0f && !(power > 0.0f) && !(alpha < 1.0f / 255.0f);
     const bool fin = use && test_T < 0.0001f;
     const bool upd = use && !fin;
-    const bool observe = upd && p.T > 0.5f;
+    // observed: taken (upd) with T > 0.5.  Then T (1 - alpha) >= 0.5 (1 - 0.99)
+    // > 1e-4, so the pixel does not finish and the test is T > 0.5 && power
+    // <= 0 && alpha >= 1/255: a ballot of each compare (scalar masks, no
+    // vector select to re-form a predicate)
+    const uint64_t observe =
+        gs::ballot(p.T > 0.5f) & gs::ballot(!(power > 0.0f)) & gs::ballot(!(alpha < 1.0f / 255.0f));
     const float wgt = alpha * p.T;
     // a pixel that does not take the entry adds colour * 0 (exactly its colour)
     const float w = upd ? wgt : 0.f;
@@ -2598,6 +2604,35 @@ __host__ __device__ constexpr bool is_split(int mode) { return mode == BLEND_SPL
 __host__ __device__ constexpr bool is_geo(int mode) { return mode == BLEND_GEO || mode == BLEND_SPLIT_GEO; }
 constexpr int NUM_MAPS = 5;   // NUM_ALL_MAP (_r config.h:24)
 
+// A caller's buffer that a blend kernel clears while it runs (n16: 16-byte
+// words; none when 0): each block, after its walk, writes zeros over its
+// share with streaming stores.  The blend kernels are VALU-bound and leave
+// HBM bandwidth unused, so the clearing costs them little; the buffer is an
+// output of a later step that then writes only its non-zero part (the
+// preprocess backward's dL/dsh, cleared by the render backward) or stays
+// zero (the render forward's geometry maps when render_geo is off).  The
+// stores come after the walk: on this target vmcnt also counts stores, so
+// stores issued first would hold up the walk's loads.
+struct ClearBuf {
+    float4* p;
+    size_t n16;
+};
+
+__device__ __forceinline__ void clear_share(const ClearBuf& c)
+{
+    if (c.n16 == 0) return;
+    const size_t share = (c.n16 + gridDim.x - 1) / gridDim.x;
+    const size_t b0 = (size_t)blockIdx.x * share, b1 = min(c.n16, b0 + share);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (size_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) gs::st_stream(&c.p[i], z);
+}
+
+// clears its buffer when the block leaves, by whichever return
+struct ClearAtExit {
+    const ClearBuf& c;
+    __device__ ~ClearAtExit() { clear_share(c); }
+};
+
 struct FwdOut {
     float* out_color;
     float* final_T;
@@ -2614,6 +2649,7 @@ struct FwdOut {
     float* out_all_map;            // geo: (5,H,W)
     float* out_plane_depth;        // geo: (H,W)
     float focal_x, focal_y, cx, cy;   // geo: the plane depth's pixel rays
+    ClearBuf clr;                  // split: a caller's buffer cleared after the walks (none: n16 == 0)
 };
 
 template <int MODE>
@@ -2627,6 +2663,7 @@ __global__ __launch_bounds__(64, MODE == BLEND_SPLIT ? 7 : (MODE == BLEND_SPLIT_
     const uint32_t* __restrict__ clist, const float4* __restrict__ rec, const uint8_t* __restrict__ cl,
     const float* __restrict__ bg, FwdOut O)
 {
+    [[maybe_unused]] const ClearAtExit clear_at_exit{O.clr};
     unsigned tile, quad, tx, ty;
     if (!block_to_tile(blockIdx.x, gx, gy, sgx, NS, tile, quad, tx, ty)) return;
     const int lane = threadIdx.x;
@@ -2715,7 +2752,7 @@ __global__ __launch_bounds__(64, MODE == BLEND_SPLIT ? 7 : (MODE == BLEND_SPLIT_
             if constexpr (MODE == BLEND_GEO) {
             } else if constexpr (is_split(MODE)) {
                 if constexpr (decltype(OBS)::value) {
-                    const uint32_t m = (uint32_t)__builtin_popcountll(gs::ballot(f.observe));
+                    const uint32_t m = (uint32_t)__builtin_popcountll(f.observe);
                     obs_cnt = gs::write_lane(obs_cnt, m, jj);
                 }
             } else {
@@ -3612,27 +3649,6 @@ __device__ __forceinline__ void render_bwd_body(
     }
 }
 
-// A caller's buffer that the backward clears while it runs (clear16: 16-byte
-// words; none when 0): each block, after its walk, writes zeros over its
-// share with streaming stores.  The blend is VALU-bound and leaves HBM
-// bandwidth unused, so the clearing costs it little; the buffer is an output
-// of a later kernel that then writes only its non-zero rows (the preprocess
-// backward's dL/dsh).  The stores come after the walk: on this target vmcnt
-// also counts stores, so stores issued first would hold up the walk's loads.
-struct ClearBuf {
-    float4* p;
-    size_t n16;
-};
-
-__device__ __forceinline__ void clear_share(const ClearBuf& c)
-{
-    if (c.n16 == 0) return;
-    const size_t share = (c.n16 + gridDim.x - 1) / gridDim.x;
-    const size_t b0 = (size_t)blockIdx.x * share, b1 = min(c.n16, b0 + share);
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (size_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) gs::st_stream(&c.p[i], z);
-}
-
 template <bool FULL, bool GEO = false>
 __global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
     int W, int H, unsigned gx, unsigned gy, unsigned sgx, unsigned NS, const uint2* __restrict__ ranges,
@@ -3648,7 +3664,7 @@ __global__ __launch_bounds__(64, GEO ? 5 : 6) void render_bwd_kernel(
     clear_share(clr);
 }
 
-// the clearing when no backward kernel runs (no instances)
+// the clearing when no blend kernel runs
 __global__ __launch_bounds__(256) void clear_kernel(ClearBuf clr)
 {
     clear_share(clr);
@@ -3689,7 +3705,7 @@ __global__ __launch_bounds__(64) void valu_probe_kernel(int iters, float* __rest
             FwdPixel p{1.0f, 0.f, 0.f, 0.f, 0u, 0u};
             auto blend = [&](const float4& A, const float4& B, const float4& Cc) {
                 const FwdStep f = fwd_blend_step(p, A, B, Cc, pxf, pyf);
-                const uint64_t m = gs::ballot(f.observe);
+                const uint64_t m = f.observe;
                 if (m != 0) observed += (int)__builtin_popcountll(m);
             };
             float4 A0 = st.a[0], B0 = st.b[0], D0 = st.c[0];
@@ -4031,6 +4047,16 @@ int render_count_impl(bool full, int P, int W, int H, const float* means2D, cons
     return GS_OK;
 }
 
+// a caller's buffer for a blend kernel to clear: 16-byte aligned, a
+// multiple of 16 bytes (none: 0 bytes)
+int clear_buf(void* dst, int64_t bytes, ClearBuf& out)
+{
+    GS_REQUIRE(bytes >= 0 && (bytes & 15) == 0 && ((uintptr_t)dst & 15) == 0 && (bytes == 0 || dst != nullptr),
+               "clear_dst and clear_bytes must be 16-byte aligned (clear_bytes=%lld)", (long long)bytes);
+    out = ClearBuf{static_cast<float4*>(dst), (size_t)bytes / 16};
+    return GS_OK;
+}
+
 // duplicate + sort + ranges + blend, shared by the split and the full-image path
 int render_forward_impl(int mode, int P, int64_t R, int W, int H, const float* bg, const float* means2D,
                         const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
@@ -4249,10 +4275,8 @@ int render_backward_impl(bool full, int P, int64_t R, int W, int H, const float*
                ((uintptr_t)means2D & 7) == 0,
                "conic_opacity / dL_dconic_opacity must be 16-byte and means2D 8-byte aligned");
     GS_REQUIRE(geom != nullptr, "geom must be the forward's geometry workspace");
-    GS_REQUIRE(clear_bytes >= 0 && (clear_bytes & 15) == 0 && ((uintptr_t)clear_dst & 15) == 0 &&
-                   (clear_bytes == 0 || clear_dst != nullptr),
-               "clear_dst and clear_bytes must be 16-byte aligned (clear_bytes=%lld)", (long long)clear_bytes);
-    const ClearBuf clr{static_cast<float4*>(clear_dst), (size_t)clear_bytes / 16};
+    ClearBuf clr{};
+    if (int rc = clear_buf(clear_dst, clear_bytes, clr); rc != GS_OK) return rc;
     if (P == 0) {
         if (clr.n16 != 0) {
             GS_TIMED("clear_kernel", stream,
@@ -4435,7 +4459,8 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
                                  const float* depths, const int* radii, const float* conic_opacity, const float* rgb,
                                  const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                  float* out_color, int32_t* n_render, int32_t* n_consider, int32_t* n_contrib,
-                                 int32_t* out_observe, int region_side, hipStream_t stream)
+                                 int32_t* out_observe, int region_side, void* clear_dst, int64_t clear_bytes,
+                                 hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4444,6 +4469,7 @@ extern "C" int gs_render_forward(int P, int64_t R, int W, int H, const float* bg
     O.out_observe = out_observe;
     O.n_consider = n_consider;
     O.n_contrib_tile = n_contrib;
+    if (int rc = clear_buf(clear_dst, clear_bytes, O.clr); rc != GS_OK) return rc;
     return render_forward_impl(BLEND_SPLIT, P, R, W, H, bg, means2D, depths, radii, conic_opacity, rgb,
                                compute_locally, nullptr, geom, binning, img, O, n_render, stream, nullptr,
                                region_side);
@@ -4455,7 +4481,8 @@ extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H,
                                           const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                           float* out_color, int32_t* n_render, int32_t* n_consider,
                                           int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
-                                          int region_side, hipStream_t stream)
+                                          int region_side, void* clear_dst, int64_t clear_bytes,
+                                          hipStream_t stream)
 {
     gs::clear_error();
     GS_REQUIRE(n_render && n_consider && n_contrib && out_observe && out_color, "null output");
@@ -4464,6 +4491,7 @@ extern "C" int gs_render_forward_reserved(int P, int64_t capacity, int W, int H,
     O.out_observe = out_observe;
     O.n_consider = n_consider;
     O.n_contrib_tile = n_contrib;
+    if (int rc = clear_buf(clear_dst, clear_bytes, O.clr); rc != GS_OK) return rc;
     return reserved_forward(false, P, capacity, W, H, means2D, radii, compute_locally, nullptr, nullptr, geom,
                             num_rendered, stream, region_side, [&] {
                                 return render_forward_impl(BLEND_SPLIT, P, capacity, W, H, bg, means2D, depths, radii,

@@ -286,7 +286,7 @@ def _tile_mask(cl, H, W, device):
 
 
 def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, compute_locally, timing=False,
-                        debug=False, geo=None, region_side=None):
+                        debug=False, geo=None, region_side=None, clear=None):
     """Returns (num_rendered, color, n_render, n_consider, n_contrib, out_observe,
     geomBuffer, binningBuffer, imgBuffer, render_ms).  The binning buffer may be
     sized for more than num_rendered instances (_lib.InstanceReserve); render_ms
@@ -294,7 +294,9 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
     geo = (tanfovx, tanfovy, all_maps (P,5)): render_geo in the same walk of the
     lists; then out_all_map (5,H,W) and out_plane_depth (1,H,W) follow.
     region_side: the binning's region side (0, 2, 4, 8; None: chosen from the
-    device's last forward, _lib.InstanceReserve.region_side)."""
+    device's last forward, _lib.InstanceReserve.region_side).
+    clear (without geo): a float32 device tensor, 16-byte aligned and a
+    multiple of 16 bytes, that the blend fills with zeros while it runs."""
     _require_device(means2D, "means2D")
     dev = means2D.device
     P = means2D.size(0)
@@ -325,6 +327,10 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         all_maps = _dev_f32(all_maps, dev)
         maps = torch.empty((6, H, W), device=dev, dtype=torch.float32)
         geo_args = (float(tanfovx), float(tanfovy), ptr(all_maps), ptr(maps[:5]), ptr(maps[5:]))
+    elif clear is not None:
+        if clear.device != dev or clear.dtype != torch.float32 or not clear.is_contiguous():
+            raise RuntimeError("clear must be a contiguous float32 tensor on the render's device")
+    clear_args = (ptr(clear), C.c_int64(clear.numel() * 4)) if clear is not None and maps is None else (None, 0)
     if timing:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
@@ -338,7 +344,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         args = (P, cap, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
                 ptr(geom), ptr(binning), ptr(img), *outs, C.byref(Rv))
         if maps is None:
-            check(lib.gs_render_forward_reserved(*args, rside, stream), "gs_render_forward_reserved")
+            check(lib.gs_render_forward_reserved(*args, rside, *clear_args, stream), "gs_render_forward_reserved")
         else:
             check(lib.gs_render_forward_reserved_geo(*args, *geo_args, rside, stream),
                   "gs_render_forward_reserved_geo")
@@ -356,7 +362,7 @@ def _render_forward_raw(bg, H, W, means2D, depths, radii, conic_opacity, rgb, co
         args = (P, R, W, H, ptr(bg), ptr(means2D), ptr(depths), ptr(radii), ptr(conic_opacity), ptr(rgb), ptr(cl),
                 ptr(geom), ptr(binning), ptr(img), *outs)
         if maps is None:
-            check(lib.gs_render_forward(*args, rside, stream), "gs_render_forward")
+            check(lib.gs_render_forward(*args, rside, *clear_args, stream), "gs_render_forward")
         else:
             check(lib.gs_render_forward_geo(*args, *geo_args, rside, stream), "gs_render_forward_geo")
     _lib.debug_sync(debug, "gs_render_forward")
@@ -468,8 +474,15 @@ class _RenderGaussians(torch.autograd.Function):
         # render_geo: the five geometry maps and the plane depth in the colour's
         # walk of the lists (_r forward.cu:381-384,407-412)
         geo = (rs.tanfovx, rs.tanfovy, all_maps) if render_geo else None
+        # render_geo off: the maps and the plane depth are zeros, cleared by
+        # the blend while it runs (no fill of their own); the buffer is
+        # rounded up to whole 16-byte words
+        zmaps = None
+        if not render_geo:
+            n = 6 * H * W
+            zmaps = torch.empty(((n + 3) // 4) * 4, device=means2D.device, dtype=torch.float32)
         res = _render_forward_raw(rs.bg, H, W, means2D, depths, radii, conic_opacity, rgb, cl, timing,
-                                  bool(rs.debug), geo=geo)
+                                  bool(rs.debug), geo=geo, clear=zmaps)
         # the preprocess backward's dL/dsh, which this render's backward clears
         zg = getattr(means2D, "_gs_zeroed", None)
         ctx.zeroed = zg if isinstance(zg, _ZeroedGrads) else None
@@ -479,8 +492,7 @@ class _RenderGaussians(torch.autograd.Function):
         if render_geo:
             out_all_map, out_plane_depth = res[10:]
         else:
-            # render_geo off: both are zeros (one fill)
-            maps = torch.zeros((6, H, W), device=dev, dtype=torch.float32)
+            maps = zmaps[:6 * H * W].view(6, H, W)
             out_all_map, out_plane_depth = maps[:5], maps[5:]
         ctx.raster_settings = rs
         ctx.cuda_args = cuda_args

@@ -165,13 +165,18 @@ int gs_render_forward_count(int P, int image_width, int image_height, const floa
  * gs_render_backward.  The sorts of the longest lists run on a second stream
  * of the library's (one per device, default priority), forked from `stream`
  * and joined back to it with events: work queued on `stream` afterwards sees
- * every result. */
+ * every result.  clear_dst / clear_bytes: NULL / 0, or a caller buffer
+ * (16-byte aligned, clear_bytes a multiple of 16) that the call fills with
+ * zeros while its blend runs -- the blend is VALU-bound and leaves HBM
+ * bandwidth unused -- e.g. the zero geometry maps the render returns when
+ * render_geo is off.  No counterpart in the reference (it allocates those
+ * outputs with torch::full(..., 0.0) before its forward). */
 int gs_render_forward(int P, int64_t R, int image_width, int image_height, const float* bg,
                       const float* means2D, const float* depths, const int* radii,
                       const float* conic_opacity, const float* rgb, const uint8_t* compute_locally,
                       void* geom, void* binning, void* img, float* out_color, int32_t* n_render,
                       int32_t* n_consider, int32_t* n_contrib, int32_t* out_observe,
-                      int region_side, gs_stream_t stream);
+                      int region_side, void* clear_dst, int64_t clear_bytes, gs_stream_t stream);
 
 /* The two calls above in one, without the host round trip between them: the
  * count, the duplication, the sorts and the blend are all queued at once
@@ -182,14 +187,17 @@ int gs_render_forward(int P, int64_t R, int image_width, int image_height, const
  * buffer for R and repeats the forward with gs_render_forward_count and
  * gs_render_forward.  Same outputs and workspaces as those two calls; the
  * forward of rasterize_points.cu:273-361, whose host reads R back
- * (rasterizer_impl.cu:621) before it can size and launch the duplication. */
+ * (rasterizer_impl.cu:621) before it can size and launch the duplication.
+ * clear_dst / clear_bytes as gs_render_forward (cleared whether or not R
+ * fits the capacity). */
 int gs_render_forward_reserved(int P, int64_t capacity, int image_width, int image_height,
                                const float* bg, const float* means2D, const float* depths,
                                const int* radii, const float* conic_opacity, const float* rgb,
                                const uint8_t* compute_locally, void* geom, void* binning, void* img,
                                float* out_color, int32_t* n_render, int32_t* n_consider,
                                int32_t* n_contrib, int32_t* out_observe, int64_t* num_rendered,
-                               int region_side, gs_stream_t stream);
+                               int region_side, void* clear_dst, int64_t clear_bytes,
+                               gs_stream_t stream);
 
 /* Render backward.  Replaces RenderGaussiansBackwardCUDA
  * (diff-gaussian-rasterization_r/rasterize_points.cu:363-436; kernel

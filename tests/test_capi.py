@@ -172,6 +172,20 @@ def test_region_side_checked_without_device(lib):
     assert rc != 0 and b"region_side" in lib.gs_last_error()
 
 
+def test_forward_clear_buffer_checked_without_device(lib):
+    """The split forward's clear buffer (a caller buffer the blend zeroes):
+    16-byte aligned and a whole number of 16-byte words, or none; checked
+    before any HIP call, on both forward routes."""
+    nz = C.c_void_p(256)
+    R = C.c_int64(0)
+    base = [10, 5, 64, 64] + [nz] * 5 + [nz, None] + [nz] * 3 + [nz] * 5
+    for dst, nbytes in ((C.c_void_p(264), 32), (nz, 20), (None, 16), (nz, -16)):
+        rc = lib.gs_render_forward(*base, 0, dst, C.c_int64(nbytes), None)
+        assert rc != 0 and b"clear_dst" in lib.gs_last_error(), (dst, nbytes)
+        rc = lib.gs_render_forward_reserved(*base, C.byref(R), 0, dst, C.c_int64(nbytes), None)
+        assert rc != 0 and b"clear_dst" in lib.gs_last_error(), (dst, nbytes)
+
+
 def test_region_side_choice_follows_instances_per_gaussian():
     """InstanceReserve.region_side: 4x4-tile regions after a forward with many
     tile instances per Gaussian, the default otherwise (and without history)."""

@@ -354,7 +354,8 @@ def test_preprocess_backward_recomputed_cov3D_and_row_layouts():
 
 @pytest.mark.parametrize("P,D,K,extent,keep_cov", [(3000, 3, 16, 6.0, False), (4097, 3, 16, 1.2, True),
                                                    (777, 2, 9, 6.0, False), (64, 0, 1, 6.0, False),
-                                                   (130, 1, 16, 40.0, False)])
+                                                   (130, 1, 16, 40.0, False), (779, 2, 16, 1.5, False),
+                                                   (197, 0, 16, 6.0, True)])
 def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
     """gs_preprocess_forward_rec / gs_preprocess_backward_rec (the backward
     reads the forward's packed records of the visible Gaussians instead of
@@ -363,7 +364,9 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
     scenes (extent 6 puts Gaussians behind the near plane and outside the
     frustum; 40 leaves few visible), partial last waves and blocks, the staged
     (K = 16) and unstaged dL/dsh layouts, SH degrees 0-3, with and without the
-    forward's cov3D.  The record forward leaves clamped unwritten (the records
+    forward's cov3D.  With dL/dsh cleared beforehand and 16-byte rows (K a
+    multiple of 4) the packed kernel runs: degrees 0-3, one and several
+    rounds per block (extent 1.2 / 1.5: most Gaussians visible), partial runs.  The record forward leaves clamped unwritten (the records
     hold the flags); some colours are forced below zero so that flags are set."""
     from blitzgs_amd import rasterizer as R
     scene, cam = synth.small_scene(P, seed=40 + D, W=200, H=150, extent=extent)
@@ -380,7 +383,7 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
     assert b[7] is None
     radii = np_(a[3])
     n_vis = int((radii > 0).sum())
-    assert 0 < n_vis < P or extent == 1.2, n_vis
+    assert 0 < n_vis < P or extent <= 1.5, n_vis
     assert n_vis < 50 or np_(a[7])[radii > 0].any()          # clamp flags among the visible
     rng = np.random.default_rng(P)
     dm2 = to_dev(rng.standard_normal((P, 2)).astype(np.float32))
@@ -787,7 +790,7 @@ def test_point_list_written_on_request():
                                      _lib.ptr(dev["radii"]), _lib.ptr(dev["conic_opacity"]), _lib.ptr(dev["rgb"]),
                                      None, _lib.ptr(geom), _lib.ptr(binning), _lib.ptr(img), _lib.ptr(color),
                                      _lib.ptr(n_render), _lib.ptr(n_consider), _lib.ptr(n_contrib), _lib.ptr(obs), 0,
-                                     s),
+                                     None, 0, s),
                "forward")
     torch.cuda.synchronize()
     from tests.gpu_helpers import buffer_views

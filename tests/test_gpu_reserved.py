@@ -27,8 +27,10 @@ def _inputs(n=6000, seed=21, W=272, H=208):
     return scene, cam, pre, dev
 
 
-def _forward(dev, W, H, capacity=None, cl=None):
-    """capacity None: the exact two-call forward; else the reserved call."""
+def _forward(dev, W, H, capacity=None, cl=None, clear_floats=0):
+    """capacity None: the exact two-call forward; else the reserved call.
+    clear_floats: a NaN-filled buffer of that many floats (a multiple of 4)
+    for the blend to clear, returned as "clear"."""
     lib = _lib.load()
     P = dev["means2D"].shape[0]
     T = ((W + 15) // 16) * ((H + 15) // 16)
@@ -43,20 +45,22 @@ def _forward(dev, W, H, capacity=None, cl=None):
     args = (_lib.ptr(bg), _lib.ptr(dev["means2D"]), _lib.ptr(dev["depths"]), _lib.ptr(dev["radii"]),
             _lib.ptr(dev["conic_opacity"]), _lib.ptr(dev["rgb"]), clp, _lib.ptr(geom))
     outs = (_lib.ptr(color), _lib.ptr(n_render), _lib.ptr(n_consider), _lib.ptr(n_contrib), _lib.ptr(obs))
+    clear = torch.full((clear_floats,), float("nan"), device="cuda") if clear_floats else None
+    clr = (_lib.ptr(clear), C.c_int64(4 * clear_floats))
     R = C.c_int64(-1)
     if capacity is None:
         _lib.check(lib.gs_render_forward_count(P, W, H, _lib.ptr(dev["means2D"]), _lib.ptr(dev["radii"]), clp,
                                                _lib.ptr(geom), C.byref(R), 0, s), "count")
         binning = torch.empty(lib.gs_render_binning_bytes(R.value), device="cuda", dtype=torch.uint8)
-        _lib.check(lib.gs_render_forward(P, R.value, W, H, *args, _lib.ptr(binning), _lib.ptr(img), *outs, 0, s),
-                   "forward")
+        _lib.check(lib.gs_render_forward(P, R.value, W, H, *args, _lib.ptr(binning), _lib.ptr(img), *outs, 0, *clr,
+                                         s), "forward")
     else:
         binning = torch.empty(lib.gs_render_binning_bytes(capacity), device="cuda", dtype=torch.uint8)
         _lib.check(lib.gs_render_forward_reserved(P, capacity, W, H, *args, _lib.ptr(binning), _lib.ptr(img),
-                                                  *outs, C.byref(R), 0, s), "forward_reserved")
+                                                  *outs, C.byref(R), 0, *clr, s), "forward_reserved")
     torch.cuda.synchronize()
     return dict(R=int(R.value), color=color, n_render=n_render, n_consider=n_consider, n_contrib=n_contrib,
-                obs=obs, geom=geom, binning=binning, img=img)
+                obs=obs, geom=geom, binning=binning, img=img, clear=clear)
 
 
 def _same(a, b, W, H, P, depths):
@@ -92,6 +96,15 @@ def test_reserved_forward_matches_two_calls(masked):
     small = _forward(dev, W, H, 1, cl)
     assert small["R"] == R
     _same(_forward(dev, W, H, None, cl), ref, W, H, P, dev["depths"])
+    # a caller buffer cleared by the blend (the zero maps of render_geo off),
+    # on both routes, fitting or not, larger than one block's share; results
+    # unchanged
+    nclr = 4 * ((6 * W * H + 3) // 4)
+    for cap in (None, R, 1):
+        out = _forward(dev, W, H, cap, cl, clear_floats=nclr)
+        assert out["R"] == R and not out["clear"].isnan().any() and not out["clear"].any(), cap
+        if cap != 1:
+            _same(out, ref, W, H, P, dev["depths"])
     # and against the oracle
     ob = O.binning(W, H, pre["means2D"], pre["depths"], pre["radii"], None if cl is None else np_(cl).reshape(
         (H + 15) // 16, (W + 15) // 16))
@@ -102,8 +115,9 @@ def test_reserved_forward_without_instances():
     scene, cam, pre, dev = _inputs(n=500, seed=5)
     W, H = cam["W"], cam["H"]
     dev["radii"] = torch.zeros_like(dev["radii"])
-    out = _forward(dev, W, H, 4096)
+    out = _forward(dev, W, H, 4096, clear_floats=4 * 1000)
     assert out["R"] == 0
+    assert not out["clear"].isnan().any() and not out["clear"].any()
     bg = np.array([0.1, 0.2, 0.3], np.float32)
     assert_close_abs(np_(out["color"]), np.broadcast_to(bg[:, None, None], (3, H, W)), "background", 0.0)
     assert not out["obs"].any() and not out["n_render"].any()

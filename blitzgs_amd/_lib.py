@@ -47,6 +47,9 @@ _SIGS = {
                                        _c, _c, _c, _c, _c, _c, _c, _c, _c]),
     "gs_preprocess_backward_rec": (_i, [_i, _i, _i, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
                                         _c, _c, _i, _c, _c, _c, _c, _c, _c, _c, _i, _c]),
+    "gs_preprocess_backward_rec_acc": (_i, [_i, _i, _i, _c, _c, _f, _c, _c, _c, _f, _f, _i, _i,
+                                            _c, _c, _c, _c, _c, _c, _c, _c, _c]),
+    "gs_render_accumulators": (_i, [_c, _i, _i, _i, _i64, C.POINTER(_c), C.POINTER(_c)]),
     "gs_render_geom_bytes": (_sz, [_i, _i, _i]),
     "gs_render_binning_bytes": (_sz, [_i64]),
     "gs_render_img_bytes": (_sz, [_i, _i]),

@@ -483,20 +483,41 @@ struct RecSrc {
     __device__ bool clamp(int, int ch) const { return ((__float_as_uint(r1.z) >> ch) & 1u) != 0; }
 };
 
-template <int DEG, bool STAGED, bool FULL, class Src>
+// Where preprocess_bwd_one reads a Gaussian's incoming gradients: the dense
+// (P, k) arrays the render backward returned (dL/dmeans2D with a row stride,
+// dL/dconic_opacity, dL/drgb) ...
+struct DenseGrads {
+    const float* __restrict__ m2d;
+    int m2d_stride;
+    const float* __restrict__ conic_op;
+    const float* __restrict__ rgb_;
+    __device__ float4 conic(int idx) const { return reinterpret_cast<const float4*>(conic_op)[idx]; }
+    __device__ float mean2d(int idx, int c) const { return m2d[(size_t)idx * m2d_stride + c]; }
+    __device__ float rgb(int idx, int ch) const { return rgb_[3 * idx + ch]; }
+};
+
+// ... or values the caller already holds (the render backward's accumulator
+// row of the Gaussian, turned into those gradients)
+struct HeldGrads {
+    float4 co;
+    float m[2], c[3];
+    __device__ float4 conic(int) const { return co; }
+    __device__ float mean2d(int, int k) const { return m[k]; }
+    __device__ float rgb(int, int ch) const { return c[ch]; }
+};
+
+template <int DEG, bool STAGED, bool FULL, class Src, class Grads>
 __device__ __forceinline__ void preprocess_bwd_one(
     int idx, int K, float tanfovx, float tanfovy, float fx, float fy, float mod,
     const float* __restrict__ view, const float* __restrict__ proj, const float* __restrict__ campos,
     const Src& src, const float* __restrict__ sh, int sh_vec16, const float* __restrict__ cov3D,
-    const float* __restrict__ dL_dmeans2D, int m2d_stride,
-    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb,
-    float* __restrict__ m3_row, float* __restrict__ sc_row, float4* __restrict__ rot_row,
+    const Grads& gr, float* __restrict__ m3_row, float* __restrict__ sc_row, float4* __restrict__ rot_row,
     float* __restrict__ dL_dsh, float* __restrict__ op_row, float* s_row, const FullPreBwd& F)
 {
     // m3_row / sc_row / rot_row / op_row: where this Gaussian's dL/dmeans3D,
     // dL/dscales, dL/drotations and dL/dopacity go
     constexpr int NC = (DEG + 1) * (DEG + 1);
-    const float4 gco = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx];
+    const float4 gco = gr.conic(idx);
     *op_row = gco.w;
     float* gsh_out = FULL ? nullptr : dL_dsh + (size_t)idx * K * 3;
     const bool vec16 = sh_vec16 != 0;
@@ -524,7 +545,7 @@ __device__ __forceinline__ void preprocess_bwd_one(
         const float x = dir_orig[0] / len, y = dir_orig[1] / len, z = dir_orig[2] / len;
         float g[3];
 #pragma unroll
-        for (int ch = 0; ch < 3; ch++) g[ch] = src.clamp(idx, ch) ? 0.0f : dL_drgb[3 * idx + ch];
+        for (int ch = 0; ch < 3; ch++) g[ch] = src.clamp(idx, ch) ? 0.0f : gr.rgb(idx, ch);
         float gsh[3 * NC], dx[3], dy[3], dz[3];
         sh_backward<DEG>(x, y, z, s, g, gsh, dx, dy, dz);
         const float dL_ddir[3] = {dx[0] * g[0] + dx[1] * g[1] + dx[2] * g[2],
@@ -635,8 +656,8 @@ __device__ __forceinline__ void preprocess_bwd_one(
         const float m_w = 1.0f / (xform_w(PM, mx, my, mz) + 0.0000001f);
         const float mul1 = (PM[0] * mx + PM[4] * my + PM[8] * mz + PM[12]) * m_w * m_w;
         const float mul2 = (PM[1] * mx + PM[5] * my + PM[9] * mz + PM[13]) * m_w * m_w;
-        const float gx = dL_dmeans2D[(size_t)idx * m2d_stride + 0];
-        const float gy = dL_dmeans2D[(size_t)idx * m2d_stride + 1];
+        const float gx = gr.mean2d(idx, 0);
+        const float gy = gr.mean2d(idx, 1);
         gm[0] += (PM[0] * m_w - PM[3] * mul1) * gx + (PM[1] * m_w - PM[3] * mul2) * gy;
         gm[1] += (PM[4] * m_w - PM[7] * mul1) * gx + (PM[5] * m_w - PM[7] * mul2) * gy;
         gm[2] += (PM[8] * m_w - PM[11] * mul1) * gx + (PM[9] * m_w - PM[11] * mul2) * gy;
@@ -778,8 +799,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
             // call could name any index: such records are skipped)
             if ((unsigned)(id - wbase) < 64u && id < P)
                 preprocess_bwd_one<DEG, STAGED, FULL>(id, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src,
-                                                      sh, sh_vec16, cov3D, dL_dmeans2D, m2d_stride,
-                                                      dL_dconic_opacity, dL_drgb, m3, sc, &rot, dL_dsh, &op,
+                                                      sh, sh_vec16, cov3D,
+                                                      DenseGrads{dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb},
+                                                      m3, sc, &rot, dL_dsh, &op,
                                                       s_sh + (id - (int)blockIdx.x * 256) * SH_PITCH, F);
         }
         const int from = 4 * __popcll(vmask & ((1ull << lane) - 1ull));   // this row's computing lane, x4
@@ -804,7 +826,8 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     } else if (vis) {
         preprocess_bwd_one<DEG, STAGED, FULL>(idx, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
                                               ArraySrc{means3D, scales, rotations, clamped}, sh, sh_vec16, cov3D,
-                                              dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb, m3_row, sc_row,
+                                              DenseGrads{dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb},
+                                              m3_row, sc_row,
                                               reinterpret_cast<float4*>(dL_drotations) + idx, dL_dsh,
                                               dL_dopacity + idx, s_sh + threadIdx.x * SH_PITCH, F);
     }
@@ -863,14 +886,44 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
 // first and keeps the second at the unpacked kernel's speed.
 constexpr int PACK_RUNS = 2;
 
-template <int DEG>
+// The render backward's per-Gaussian accumulators (the listed Gaussians'
+// 64-byte rows, cidx_of: a Gaussian's row or -1; cidx_of null: no row) and
+// the factors its unpack applies (dmean/dpixel sx = W/2, sy = H/2; -1/2 on
+// the conic terms): the incoming gradients of the preprocess backward when
+// they are exactly that render backward's outputs.
+struct AccIn {
+    const float4* __restrict__ gacc;
+    const int* __restrict__ cidx_of;
+    float sx, sy;
+    // unpack_grads_kernel's expressions, so the values are those it wrote
+    __device__ HeldGrads of(int id) const
+    {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a, c = a;
+        const int cx = cidx_of != nullptr ? cidx_of[id] : -1;
+        if (cx >= 0) {
+            const float4* g = gacc + 4 * (size_t)cx;
+            a = g[0];
+            b = g[1];
+            c = g[2];
+            a = make_float4(a.x * sx, a.y * sy, a.z * sx, a.w * sy);
+            b = make_float4(-0.5f * b.x, -0.5f * b.y, -0.5f * b.z, b.w);
+        }
+        return HeldGrads{b, {a.x, a.y}, {c.x, c.y, c.z}};
+    }
+};
+
+// ACC: the incoming gradients from the render backward's accumulators (acc)
+// instead of the dense arrays; an invisible Gaussian's dL/dopacity is then
+// zero (the render listed it nowhere), so dL/dconic_opacity is not read.
+template <int DEG, bool ACC>
 __global__ __launch_bounds__(64) void preprocess_bwd_packed_kernel(
     int P, int K, float tanfovx, float tanfovy, float fx, float fy, float mod, const float* __restrict__ view,
     const float* __restrict__ proj, const float* __restrict__ campos, const float* __restrict__ sh,
     const float* __restrict__ cov3D, const float* __restrict__ dL_dmeans2D, int m2d_stride,
-    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb, float* __restrict__ dL_dmeans3D,
-    float* __restrict__ dL_dscales, float* __restrict__ dL_drotations, float* __restrict__ dL_dsh,
-    float* __restrict__ dL_dopacity, const float4* __restrict__ rec, const uint64_t* __restrict__ rec_mask)
+    const float* __restrict__ dL_dconic_opacity, const float* __restrict__ dL_drgb, AccIn acc,
+    float* __restrict__ dL_dmeans3D, float* __restrict__ dL_dscales, float* __restrict__ dL_drotations,
+    float* __restrict__ dL_dsh, float* __restrict__ dL_dopacity, const float4* __restrict__ rec,
+    const uint64_t* __restrict__ rec_mask)
 {
     constexpr int NC = (DEG + 1) * (DEG + 1);
     constexpr int CH = (3 * NC + 3) / 4;             // 16-byte chunks of a row that can be nonzero
@@ -878,6 +931,7 @@ __global__ __launch_bounds__(64) void preprocess_bwd_packed_kernel(
     __shared__ int s_id[64];                         // their Gaussians (-1: none)
     __shared__ float4 s_rot[PACK_RUNS * 64];         // per row of the runs: dL/drotations,
     __shared__ float s_ms[PACK_RUNS * 64 * 6];       // dL/dmeans3D and dL/dscales
+    __shared__ float s_op[ACC ? PACK_RUNS * 64 : 1]; // (ACC) and dL/dopacity
     const int lane = threadIdx.x;
     const int run0 = (int)blockIdx.x * PACK_RUNS;    // first 64-run of this block
     const int nruns = (P + 63) >> 6;
@@ -912,10 +966,17 @@ __global__ __launch_bounds__(64) void preprocess_bwd_packed_kernel(
                 const int row = j * 64 + (g - wbase);
                 float* ms = s_ms + row * 6;
                 float op;
-                preprocess_bwd_one<DEG, true, false>(g, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src,
-                                                     sh, 1, cov3D, dL_dmeans2D, m2d_stride, dL_dconic_opacity,
-                                                     dL_drgb, ms, ms + 3, &s_rot[row], dL_dsh, &op,
-                                                     s_sh + lane * SH_PITCH, FullPreBwd{});
+                if constexpr (ACC) {
+                    preprocess_bwd_one<DEG, true, false>(g, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos,
+                                                         src, sh, 1, cov3D, acc.of(g), ms, ms + 3, &s_rot[row],
+                                                         dL_dsh, &op, s_sh + lane * SH_PITCH, FullPreBwd{});
+                    s_op[row] = op;
+                } else {
+                    preprocess_bwd_one<DEG, true, false>(
+                        g, K, tanfovx, tanfovy, fx, fy, mod, view, proj, campos, src, sh, 1, cov3D,
+                        DenseGrads{dL_dmeans2D, m2d_stride, dL_dconic_opacity, dL_drgb}, ms, ms + 3, &s_rot[row],
+                        dL_dsh, &op, s_sh + lane * SH_PITCH, FullPreBwd{});
+                }
             }
         }
         s_id[lane] = id;
@@ -944,7 +1005,10 @@ __global__ __launch_bounds__(64) void preprocess_bwd_packed_kernel(
             for (int k = 0; k < 6; k++) a[k] = ms[k];
             c = s_rot[j * 64 + lane];
         }
-        dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
+        if constexpr (ACC)
+            dL_dopacity[idx] = vis ? s_op[j * 64 + lane] : 0.f;
+        else
+            dL_dopacity[idx] = reinterpret_cast<const float4*>(dL_dconic_opacity)[idx].w;
         float* m3 = dL_dmeans3D + 3 * (size_t)idx;
         float* sc = dL_dscales + 3 * (size_t)idx;
         m3[0] = a[0];
@@ -1037,7 +1101,7 @@ static int preprocess_backward_impl(
     const int* radii, const float* cov3D, const uint8_t* clamped, const float* dL_dmeans2D,
     int dL_dmeans2D_stride, const float* dL_dconic_opacity, const float* dL_drgb, float* dL_dmeans3D,
     float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity, const void* bwd_records,
-    hipStream_t stream, int zeroed = 0)
+    hipStream_t stream, int zeroed = 0, const AccIn* acc = nullptr)
 {
     gs::clear_error();
     GS_REQUIRE(P >= 0, "P must be >= 0 (got %d)", P);
@@ -1058,20 +1122,26 @@ static int preprocess_backward_impl(
     const float fy = (float)image_height / (2.0f * tanfovy);
     const float fx = (float)image_width / (2.0f * tanfovx);
     const dim3 grid(gs_div_up((size_t)P, 256)), block(256);
+    GS_REQUIRE(acc == nullptr || (rrec != nullptr && zeroed && sh_vec16),
+               "the accumulator inputs need the records, cleared dL_dsh and 16-byte SH rows");
     if (rrec != nullptr && zeroed && sh_vec16) {
         const dim3 pgrid(gs_div_up((size_t)P, 64 * PACK_RUNS)), pblock(64);
-#define GS_PRE_BWD_P(DEG)                                                                                    \
+        const AccIn ai = acc != nullptr ? *acc : AccIn{};
+#define GS_PRE_BWD_P(DEG, ACC)                                                                               \
     GS_TIMED("preprocess_bwd_packed_kernel", stream,                                                         \
-             hipLaunchKernelGGL((preprocess_bwd_packed_kernel<DEG>), pgrid, pblock, 0, stream, P, K, tanfovx, \
-                                tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, campos, sh, cov3D,   \
-                                dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,     \
-                                dL_dscales, dL_drotations, dL_dsh, dL_dopacity, rrec, rmask))
+             hipLaunchKernelGGL((preprocess_bwd_packed_kernel<DEG, ACC>), pgrid, pblock, 0, stream, P, K,     \
+                                tanfovx, tanfovy, fx, fy, scale_modifier, viewmatrix, projmatrix, campos, sh, \
+                                cov3D, dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, ai,       \
+                                dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity, rrec, rmask))
+#define GS_PRE_BWD_PA(DEG) \
+    if (acc != nullptr) GS_PRE_BWD_P(DEG, true); else GS_PRE_BWD_P(DEG, false);
         switch (D) {
-            case 0: GS_PRE_BWD_P(0); break;
-            case 1: GS_PRE_BWD_P(1); break;
-            case 2: GS_PRE_BWD_P(2); break;
-            default: GS_PRE_BWD_P(3); break;
+            case 0: GS_PRE_BWD_PA(0); break;
+            case 1: GS_PRE_BWD_PA(1); break;
+            case 2: GS_PRE_BWD_PA(2); break;
+            default: GS_PRE_BWD_PA(3); break;
         }
+#undef GS_PRE_BWD_PA
 #undef GS_PRE_BWD_P
         GS_LAUNCH_CHECK("preprocess_bwd_packed_kernel");
         return GS_OK;
@@ -1130,6 +1200,25 @@ extern "C" int gs_preprocess_backward_rec(
                                     dL_dmeans2D, dL_dmeans2D_stride, dL_dconic_opacity, dL_drgb, dL_dmeans3D,
                                     dL_dscales, dL_drotations, dL_dsh, dL_dopacity, bwd_records, stream,
                                     outputs_zeroed != 0 ? 1 : 0);
+}
+
+extern "C" int gs_preprocess_backward_rec_acc(
+    int P, int D, int K, const void* bwd_records, const float* sh, float scale_modifier,
+    const float* viewmatrix, const float* projmatrix, const float* campos, float tanfovx, float tanfovy,
+    int image_height, int image_width, const float* cov3D, const void* render_acc, const int* render_cidx_of,
+    float* dL_dmeans3D, float* dL_dscales, float* dL_drotations, float* dL_dsh, float* dL_dopacity,
+    hipStream_t stream)
+{
+    gs::clear_error();
+    GS_REQUIRE(P <= 0 || bwd_records != nullptr, "bwd_records must be the records gs_preprocess_forward_rec wrote");
+    GS_REQUIRE(P <= 0 || (render_acc != nullptr && ((uintptr_t)render_acc & 15) == 0),
+               "render_acc must be the render's accumulators (gs_render_accumulators)");
+    const AccIn acc{static_cast<const float4*>(render_acc), render_cidx_of, 0.5f * (float)image_width,
+                    0.5f * (float)image_height};
+    return preprocess_backward_impl(P, D, K, nullptr, nullptr, nullptr, sh, scale_modifier, viewmatrix, projmatrix,
+                                    campos, tanfovx, tanfovy, image_height, image_width, nullptr, cov3D, nullptr,
+                                    nullptr, 2, nullptr, nullptr, dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh,
+                                    dL_dopacity, bwd_records, stream, 1, &acc);
 }
 
 extern "C" int gs_preprocess_forward_full(

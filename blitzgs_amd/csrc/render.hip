@@ -4446,6 +4446,18 @@ int reserved_forward(bool full, int P, int64_t cap, int W, int H, const float* m
 
 }  // namespace
 
+extern "C" int gs_render_accumulators(const void* geom, int P, int W, int H, int64_t R, const void** acc,
+                                      const int** cidx_of)
+{
+    gs::clear_error();
+    GS_REQUIRE(geom != nullptr && acc != nullptr && cidx_of != nullptr && P >= 0 && W > 0 && H > 0 && R >= 0,
+               "invalid arguments");
+    const GeomLayout g = geom_layout(P, W, H);
+    *acc = static_cast<const char*>(geom) + g.gacc;
+    *cidx_of = R > 0 ? reinterpret_cast<const int*>(static_cast<const char*>(geom) + g.cidx_of) : nullptr;
+    return GS_OK;
+}
+
 extern "C" int gs_render_forward_count(int P, int W, int H, const float* means2D, const int* radii,
                                        const uint8_t* compute_locally, void* geom, int64_t* num_rendered,
                                        int region_side, hipStream_t stream)

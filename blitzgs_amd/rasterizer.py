@@ -135,12 +135,15 @@ def _preprocess_forward_raw(means3D, scales, rotations, sh, opacities, rs, keep_
 
 
 def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, sh, rs, dL_dmeans2D,
-                             dL_dconic_opacity, dL_drgb, records=None, zeroed=None):
+                             dL_dconic_opacity, dL_drgb, records=None, zeroed=None, acc=None):
     """records: the forward's record buffer (_preprocess_forward_raw with
     records=True); then radii, clamped, scales and rotations are not read.
     zeroed (with records): a (P,K,3) dL/dsh output tensor that already holds
     zeros on the current stream; only the visible Gaussians' rows are written
-    into it."""
+    into it.  acc (with zeroed; (geom, R, W, H) of a split render whose
+    backward returned exactly dL_dmeans2D, dL_dconic_opacity and dL_drgb):
+    its accumulators are read instead of those dense arrays (the same
+    values)."""
     dev = means3D.device
     P = means3D.size(0)
     K = sh.size(1) if sh.ndimension() == 3 else 1
@@ -168,7 +171,20 @@ def _preprocess_backward_raw(radii, cov3D, clamped, means3D, scales, rotations, 
         campos = _dev_f32(rs.campos, dev)
         lib = _lib.load()
         cov = ptr(cov3D.contiguous()) if cov3D is not None else None
-        if records is not None:
+        if records is not None and zeroed is not None and acc is not None and K % 4 == 0:
+            if records.numel() != lib.gs_preprocess_record_bytes(P):
+                raise RuntimeError("records must be the preprocess forward's record buffer for these Gaussians")
+            geom, R, W, H = acc
+            pa, pc = C.c_void_p(), C.c_void_p()
+            check(lib.gs_render_accumulators(ptr(geom), P, W, H, R, C.byref(pa), C.byref(pc)),
+                  "gs_render_accumulators")
+            rc = lib.gs_preprocess_backward_rec_acc(
+                P, int(rs.sh_degree), K, ptr(records), ptr(sh), float(rs.scale_modifier), ptr(view), ptr(proj),
+                ptr(campos), float(rs.tanfovx), float(rs.tanfovy), int(rs.image_height), int(rs.image_width), cov,
+                pa, pc, ptr(dL_dmeans3D), ptr(dL_dscales), ptr(dL_drotations), ptr(dL_dsh), ptr(dL_dopacity),
+                _stream(dev))
+            check(rc, "gs_preprocess_backward_rec_acc")
+        elif records is not None:
             if records.numel() != lib.gs_preprocess_record_bytes(P):
                 raise RuntimeError("records must be the preprocess forward's record buffer for these Gaussians")
             rc = lib.gs_preprocess_backward_rec(
@@ -222,6 +238,27 @@ class _ZeroedGrads:
         torch.cuda.current_stream(self.dev).wait_event(self.event)
         return t
 
+    # The same render backward also offers its accumulators: the preprocess
+    # backward reads them instead of the dense gradients when the gradients it
+    # receives are exactly the tensors that backward returned (no other
+    # contribution summed in, nothing changed in place; holding them here also
+    # keeps autograd from summing into them in place).
+    acc = None
+
+    def offer(self, geom, R, W, H, grads):
+        self.acc = (geom, int(R), int(W), int(H), grads, tuple(g._version for g in grads))
+
+    def take_acc(self, grads):
+        a, self.acc = self.acc, None
+        if a is None:
+            return None
+        geom, R, W, H, mine, versions = a
+        for g, m, v in zip(grads, mine, versions):
+            if g is None or g.data_ptr() != m.data_ptr() or g.shape != m.shape or g.stride() != m.stride() or \
+                    g.dtype != m.dtype or m._version != v:
+                return None
+        return geom, R, W, H
+
 
 class _PreprocessGaussians(torch.autograd.Function):
     @staticmethod
@@ -259,9 +296,14 @@ class _PreprocessGaussians(torch.autograd.Function):
         if grad_conic_opacity is None:
             grad_conic_opacity = torch.zeros_like(conic_opacity)
         zeroed = ctx.zeroed.take() if ctx.zeroed is not None else None
+        acc = None
+        if zeroed is not None:
+            acc = ctx.zeroed.take_acc((grad_means2D, grad_rgb, grad_conic_opacity))
+            if acc is not None and (acc[2], acc[3]) != (int(rs.image_width), int(rs.image_height)):
+                acc = None
         dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity = _preprocess_backward_raw(
             radii, cov3D, clamped, means3D, scales, rotations, sh, rs, grad_means2D, grad_conic_opacity, grad_rgb,
-            records=records, zeroed=zeroed)
+            records=records, zeroed=zeroed, acc=acc)
         return dL_dmeans3D, dL_dscales, dL_drotations, dL_dsh, dL_dopacity, None, None
 
 
@@ -531,6 +573,8 @@ class _RenderGaussians(torch.autograd.Function):
                 dL_dall_map = torch.zeros_like(all_maps)
         if clear is not None:
             zg.cleared()
+            # the same call's accumulators, for the preprocess backward
+            zg.offer(geom, ctx.num_rendered, W, H, (dL_dmeans2D, dL_dcolors, dL_dconic_opacity))
         if timing:
             ctx.cuda_args["stats_collector"]["backward_render_time"] = ms
         if not ctx.needs_input_grad[4]:

@@ -122,6 +122,26 @@ int gs_preprocess_backward_rec(int P, int D, int K, const void* bwd_records, con
                                float* dL_drotations, float* dL_dsh, float* dL_dopacity,
                                int outputs_zeroed, gs_stream_t stream);
 
+/* gs_preprocess_backward_rec with outputs_zeroed = 1 whose incoming
+ * gradients are exactly what a split render backward returned: instead of
+ * the dense dL_dmeans2D / dL_dconic_opacity / dL_drgb it reads that render's
+ * per-Gaussian accumulators (render_acc, render_cidx_of: gs_render_accumulators
+ * of the render's geom, after its gs_render_backward and before any other
+ * call on that geom) and applies the same factors as the render backward's
+ * outputs (dmean/dpixel W/2, H/2; -1/2 on the conic terms), so the gradients
+ * are bit-identical; an invisible Gaussian's dL_dopacity is zero (the render
+ * listed it nowhere).  Needs 16-byte SH rows (K a multiple of 4, sh and
+ * dL_dsh 16-byte aligned) and dL_dsh cleared.  No counterpart in the
+ * reference: it saves the dense arrays' gathers (one visible Gaussian in
+ * five at the benchmark's scene touches nearly every line of them). */
+int gs_preprocess_backward_rec_acc(int P, int D, int K, const void* bwd_records, const float* sh,
+                                   float scale_modifier, const float* viewmatrix, const float* projmatrix,
+                                   const float* campos, float tanfovx, float tanfovy, int image_height,
+                                   int image_width, const float* cov3D, const void* render_acc,
+                                   const int* render_cidx_of, float* dL_dmeans3D, float* dL_dscales,
+                                   float* dL_drotations, float* dL_dsh, float* dL_dopacity,
+                                   gs_stream_t stream);
+
 /* ------------------------------------------------------------------------ *
  * Render forward, in two calls because the size of the instance buffers
  * (R = number of Gaussian/tile instances) is known only after counting.
@@ -222,6 +242,15 @@ int gs_render_backward(int P, int64_t R, int image_width, int image_height, cons
                        const float* dL_dpixels, float* dL_dmeans2D, int dL_dmeans2D_stride,
                        float* dL_dmeans2D_abs, float* dL_dconic_opacity, float* dL_dcolors,
                        void* clear_dst, int64_t clear_bytes, gs_stream_t stream);
+
+/* Device addresses of a split render's per-Gaussian gradient accumulators
+ * in its geom (64 bytes per listed Gaussian) and of the Gaussians'
+ * accumulator rows (cidx_of: int per Gaussian, -1 when not listed; NULL when
+ * R == 0), as gs_render_backward leaves them: the input of
+ * gs_preprocess_backward_rec_acc.  No device work.  No counterpart in the
+ * reference. */
+int gs_render_accumulators(const void* geom, int P, int image_width, int image_height, int64_t R,
+                           const void** acc, const int** cidx_of);
 
 /* render_geo of the render forward (rasterize_points.cu:273-361 with
  * render_geo = true; kernel cuda_rasterizer/forward.cu:381-384,407-412):

@@ -412,6 +412,82 @@ def test_preprocess_records_equal_array_path(P, D, K, extent, keep_cov):
         R._preprocess_backward_raw(radii_t, cov3D, clamped, *args, records=b[8][:-256])
 
 
+@pytest.mark.parametrize("extra", ["none", "summed", "hook_in_place", "geo"])
+def test_preprocess_backward_reads_render_accumulators(monkeypatch, extra):
+    """The preprocess backward reads the render backward's accumulators
+    instead of the dense dL/dmeans2D, dL/dconic_opacity and dL/drgb when it
+    receives exactly the tensors that backward returned; bit-identical
+    gradients.  Another contribution to rgb's gradient (summed by autograd),
+    a hook that changes the gradient in place, or render_geo's backward: the
+    dense arrays are read whenever the received gradients are not the render
+    backward's own (here: summed, hook), and the gradients still equal the
+    dense path's."""
+    from blitzgs_amd import rasterizer as R
+    scene, cam = synth.small_scene(3000, seed=16, W=200, H=150, extent=1.5)
+    rs = settings_for(cam)
+    if extra == "geo":
+        from blitzgs_amd.dropin import diff_gaussian_rasterization_r as R_pkg
+        rs = R_pkg.GaussianRasterizationSettings(**dict(rs._asdict(), render_geo=True))
+    seen = []
+    real = R._preprocess_backward_raw
+
+    def spy(*a, **kw):
+        seen.append(kw.get("acc") is not None)
+        return real(*a, **kw)
+
+    monkeypatch.setattr(R, "_preprocess_backward_raw", spy)
+
+    def grads():
+        params = {k: to_dev(np.asarray(scene[k], np.float32)).requires_grad_(True)
+                  for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+        ras = R.GaussianRasterizer(rs)
+        args = {"avoid_pixel_all2all": False}
+        means2D, rgb, conic, radii, depths = ras.preprocess_gaussians(
+            params["means3D"], params["scales"], params["rotations"], params["sh"], params["opacities"], args)
+        if extra == "hook_in_place":
+            rgb.register_hook(lambda g: g.mul_(2.0))
+        P = means2D.shape[0]
+        amap = to_dev(np.random.default_rng(3).uniform(-1, 1, (P, 5)).astype(np.float32))
+        color, *rest = ras.render_gaussians(means2D, torch.zeros((P, 3), device="cuda", requires_grad=True), conic,
+                                            rgb, amap, depths, radii, None, None, args)
+        loss = (color * to_dev(scene["dL_dimage"])).sum()
+        if extra == "summed":
+            loss = loss + 0.5 * rgb.sum()
+        if extra == "geo":
+            loss = loss + rest[4].sum() + rest[5].sum()
+        loss.backward()
+        return [params[k].grad for k in ["means3D", "scales", "rotations", "sh", "opacities"]]
+
+    a = grads()
+    monkeypatch.setattr(R._ZeroedGrads, "take_acc", lambda self, g: None)
+    b = grads()
+    assert seen == [extra in ("none", "geo"), False], seen
+    # two runs: the render backward's float atomics may sum in another order
+    for x, y, name in zip(a, b, ["means3D", "scales", "rotations", "sh", "opacities"]):
+        assert rel_l2(np_(x), np_(y)) < 1e-6, (extra, name)
+    if extra != "none":
+        return
+    # one render backward, both readings of its outputs: bit-identical
+    monkeypatch.undo()
+    t = {k: to_dev(np.asarray(scene[k], np.float32)) for k in ["means3D", "scales", "rotations", "sh", "opacities"]}
+    pre = R._preprocess_forward_raw(t["means3D"], t["scales"], t["rotations"], t["sh"], t["opacities"], rs,
+                                    keep_cov3D=False, records=True, keep_clamped=False)
+    _, m2d, depths, radii, _, conic, rgb, _, records = pre
+    W, H = int(rs.image_width), int(rs.image_height)
+    f = R._render_forward_raw(rs.bg, H, W, m2d, depths, radii, conic, rgb, None)
+    Rn, geom, binning, img = f[0], f[6], f[7], f[8]
+    gm2d, _, gco, gcol, _ = R._render_backward_raw(rs.bg, Rn, H, W, m2d, conic, rgb, None, geom, binning, img,
+                                                   to_dev(scene["dL_dimage"]), 2, False, False)
+    P, K = m2d.shape[0], t["sh"].shape[1]
+    args = (radii, None, None, t["means3D"], t["scales"], t["rotations"], t["sh"], rs, gm2d, gco, gcol)
+    zd = torch.zeros((P, K, 3), device="cuda")
+    dense = R._preprocess_backward_raw(*args, records=records, zeroed=zd)
+    za = torch.zeros((P, K, 3), device="cuda")
+    viaacc = R._preprocess_backward_raw(*args, records=records, zeroed=za, acc=(geom, Rn, W, H))
+    for x, y, name in zip(dense, viaacc, ["means3D", "scales", "rotations", "sh", "opacity"]):
+        assert torch.equal(x, y), ("accumulators", name)
+
+
 @pytest.mark.parametrize("case", ["wide", "small", "masked", "ragged"])
 def test_region_sides_give_identical_results(case):
     """Every output of the split forward -- image, per-tile and per-pixel
